@@ -1,0 +1,337 @@
+"""ferry_amd -- MI355X-native per-GPU sparse KV miss-stream executor.
+
+Python mirror of the C-ABI in include/ferry_amd.h, loaded with ctypes.  The
+compute path is libferry_amd.so (hand-written gfx950 HIP kernels); there is no
+CPU fallback: importing this package without the built library raises.
+
+torch supplies device memory and streams only.  It is imported before the
+library so that one HIP runtime serves both.
+
+Reference interfaces mirrored (clearleo126/ferry, paths relative to its tree):
+  Executor.fetch_step      run_miss_workload mode C / exec_step C engine
+                           (src/workloads/kv_exec.cuh:188-292,
+                           src/runtime/wla_multigpu.cuh:2527-2604)
+  Executor.sparse_decode   attn_kernel / wla_attn_kernel (real attention here)
+  queue_selftest           bench_queue (src/benches/bench_queue.cu:62-123)
+  SelGen / refgen_selections  replay_miss_stream (src/workloads/missstream.cuh:104)
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import torch  # noqa: F401  (HIP runtime + device memory; load before the library)
+
+__all__ = [
+    "FerryError", "Executor", "SelGen", "queue_selftest", "refgen_selections",
+    "ctx_uniform", "lib", "LIB_PATH", "F32", "F16", "BF16", "FP8", "LRU_STEP", "LRU_SERIAL",
+    "ASSIGN_SPREAD", "ASSIGN_AFFINITY", "MISS_DTYPE",
+]
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libferry_amd.so")
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"{LIB_PATH} is not built: run `make -C ferry_amd` "
+                      "(or __graft_entry__.build()); there is no fallback path")
+lib = C.CDLL(LIB_PATH)
+
+F32, F16, BF16, FP8 = 0, 1, 2, 3
+LRU_STEP, LRU_SERIAL = 0, 1
+ASSIGN_SPREAD, ASSIGN_AFFINITY = 0, 1
+ESIZE = {F32: 4, F16: 2, BF16: 2, FP8: 1}
+MISS_DTYPE = np.dtype([("block", "<u4"), ("slot", "<u4"), ("evicted", "<u4"), ("set", "<u4")])
+
+_ERRORS = {-1: "EINVAL", -2: "EHIP", -3: "ERANGE", -4: "ECAPACITY", -5: "ENOMEM",
+           -6: "ESPIN", -7: "ESTATE"}
+
+
+class FerryError(RuntimeError):
+    def __init__(self, code, where):
+        self.code = code
+        msg = lib.ferry_last_error().decode()
+        super().__init__(f"{where}: {_ERRORS.get(code, code)} ({code}) {msg}")
+
+
+class Config(C.Structure):
+    _fields_ = [
+        ("n_req", C.c_int32), ("group", C.c_int32), ("n_layers", C.c_int32),
+        ("kv_heads", C.c_int32), ("q_heads", C.c_int32), ("head_dim", C.c_int32),
+        ("block_tokens", C.c_int32), ("k", C.c_int32), ("slots_per_set", C.c_int32),
+        ("max_blocks", C.c_int32), ("dtype", C.c_int32), ("lru_mode", C.c_int32),
+        ("host_blocks", C.c_uint64), ("host_seed", C.c_uint64), ("value_std", C.c_float),
+        ("fetch_workers", C.c_int32), ("steal", C.c_int32), ("assign", C.c_int32),
+    ]
+
+
+class Stats(C.Structure):
+    _fields_ = [
+        ("steps", C.c_uint64), ("selections", C.c_uint64), ("misses", C.c_uint64),
+        ("fetched_bytes", C.c_uint64), ("steals", C.c_uint64), ("stolen", C.c_uint64),
+        ("last_misses", C.c_uint64), ("device_error", C.c_int32), ("pad", C.c_int32),
+    ]
+
+
+class SelGenConfig(C.Structure):
+    _fields_ = [
+        ("n_req", C.c_int32), ("group", C.c_int32), ("n_layers", C.c_int32),
+        ("kv_heads", C.c_int32), ("k", C.c_int32), ("dist", C.c_int32),
+        ("zipf_s", C.c_double), ("reuse", C.c_double), ("prefix_blocks", C.c_int32),
+        ("pad", C.c_int32), ("seed", C.c_uint64),
+    ]
+
+
+_vp = C.c_void_p
+_i32 = C.c_int32
+_PROTOS = {
+    "ferry_last_error": (C.c_char_p, []),
+    "ferry_version": (C.c_char_p, []),
+    "ferry_ctx_create": (C.c_int, [C.POINTER(Config), C.c_int, C.POINTER(_vp)]),
+    "ferry_ctx_destroy": (C.c_int, [_vp]),
+    "ferry_ctx_config": (C.c_int, [_vp, C.POINTER(Config)]),
+    "ferry_ctx_sizes": (C.c_int, [_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                                  C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "ferry_hosttier_fill": (C.c_int, [_vp, _vp]),
+    "ferry_hosttier_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),
+    "ferry_pool_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),
+    "ferry_sets_reset": (C.c_int, [_vp, _vp]),
+    "ferry_sets_state": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "ferry_fetch_step": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ferry_bookkeep_step": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ferry_missq_push": (C.c_int, [_vp, _vp, C.c_uint32, _vp]),
+    "ferry_missq_drain": (C.c_int, [_vp, _vp]),
+    "ferry_sparse_decode": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "ferry_stats_get": (C.c_int, [_vp, C.POINTER(Stats)]),
+    "ferry_stats_reset": (C.c_int, [_vp]),
+    "ferry_queue_selftest": (C.c_int, [C.c_int, C.c_uint64, C.c_uint64, C.c_int, C.c_int,
+                                       C.c_int, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                       C.POINTER(C.c_float)]),
+    "ferry_selgen_create": (C.c_int, [C.POINTER(SelGenConfig), _vp, C.POINTER(_vp)]),
+    "ferry_selgen_destroy": (C.c_int, [_vp]),
+    "ferry_selgen_max_blocks": (C.c_int, [_vp, C.POINTER(_i32)]),
+    "ferry_selgen_step": (C.c_int, [_vp, _i32, _vp]),
+    "ferry_ctx_uniform": (C.c_int, [C.c_uint64, _i32, _i32, _i32, _vp]),
+    "ferry_refgen_selections": (C.c_int, [_i32, _i32, _i32, _i32, C.c_uint64, _vp]),
+}
+for _name, (_res, _args) in _PROTOS.items():
+    _f = getattr(lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+
+def _check(rc, where):
+    if rc != 0:
+        raise FerryError(rc, where)
+
+
+def _ptr(t):
+    """Device/host pointer of a tensor or ndarray (None -> NULL)."""
+    if t is None:
+        return None
+    if isinstance(t, torch.Tensor):
+        return t.data_ptr()
+    return t.ctypes.data
+
+
+def _stream(stream):
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return getattr(stream, "cuda_stream", stream)
+
+
+class Executor:
+    """One executor (HBM slot pool + LRU sets + miss ring + pinned host tier)."""
+
+    def __init__(self, n_req, n_layers, kv_heads, k, slots_per_set, max_blocks,
+                 q_heads=None, group=1, head_dim=128, block_tokens=16, dtype=F16,
+                 lru_mode=LRU_STEP, host_blocks=1 << 16, host_seed=7, value_std=0.5,
+                 fetch_workers=0, steal=1, assign=ASSIGN_SPREAD, device=0):
+        cfg = Config(n_req, group, n_layers, kv_heads, q_heads or kv_heads, head_dim,
+                     block_tokens, k, slots_per_set, max_blocks, dtype, lru_mode,
+                     host_blocks, host_seed, value_std, fetch_workers, steal, assign)
+        self.device = device
+        torch.cuda.set_device(device)
+        h = _vp()
+        _check(lib.ferry_ctx_create(C.byref(cfg), device, C.byref(h)), "ferry_ctx_create")
+        self._h = h
+        full = Config()
+        _check(lib.ferry_ctx_config(h, C.byref(full)), "ferry_ctx_config")
+        self.cfg = full
+        ns, ms, bb, ps = C.c_uint32(), C.c_uint32(), C.c_uint64(), C.c_uint64()
+        _check(lib.ferry_ctx_sizes(h, C.byref(ns), C.byref(ms), C.byref(bb), C.byref(ps)),
+               "ferry_ctx_sizes")
+        self.n_sets, self.max_sel = ns.value, ms.value
+        self.block_bytes, self.pool_slots = bb.value, ps.value
+        self.sel_shape = (n_req, n_layers, kv_heads, k)
+
+    def close(self):
+        h, self._h = getattr(self, "_h", None), None
+        if h and lib is not None:
+            lib.ferry_ctx_destroy(h)
+
+    def __del__(self):
+        self.close()
+
+    # ---- buffers --------------------------------------------------------
+    def alloc_step_buffers(self):
+        dev = torch.device("cuda", self.device)
+        return dict(
+            slots=torch.empty(self.sel_shape, dtype=torch.int32, device=dev),
+            miss_count=torch.empty(self.n_sets, dtype=torch.int32, device=dev),
+            misses=torch.empty((self.n_sets, self.max_sel, 4), dtype=torch.int32, device=dev),
+            miss_flag=torch.empty(self.sel_shape, dtype=torch.uint8, device=dev),
+        )
+
+    # ---- path -------------------------------------------------------------
+    def hosttier_fill(self, stream=None):
+        _check(lib.ferry_hosttier_fill(self._h, _stream(stream)), "ferry_hosttier_fill")
+
+    def fetch_step(self, sel, bufs, stream=None, flags=True):
+        _check(lib.ferry_fetch_step(self._h, _ptr(sel), _ptr(bufs["slots"]),
+                                    _ptr(bufs["miss_count"]), _ptr(bufs["misses"]),
+                                    _ptr(bufs["miss_flag"]) if flags else None,
+                                    _stream(stream)), "ferry_fetch_step")
+
+    def bookkeep_step(self, sel, bufs, stream=None, flags=True):
+        _check(lib.ferry_bookkeep_step(self._h, _ptr(sel), _ptr(bufs["slots"]),
+                                       _ptr(bufs["miss_count"]), _ptr(bufs["misses"]),
+                                       _ptr(bufs["miss_flag"]) if flags else None,
+                                       _stream(stream)), "ferry_bookkeep_step")
+
+    def missq_push(self, misses, n, stream=None):
+        _check(lib.ferry_missq_push(self._h, _ptr(misses), n, _stream(stream)), "ferry_missq_push")
+
+    def missq_drain(self, stream=None):
+        _check(lib.ferry_missq_drain(self._h, _stream(stream)), "ferry_missq_drain")
+
+    def sparse_decode(self, q, slots, out, stream=None):
+        _check(lib.ferry_sparse_decode(self._h, _ptr(q), _ptr(slots), _ptr(out), _stream(stream)),
+               "ferry_sparse_decode")
+
+    def sets_reset(self, stream=None):
+        _check(lib.ferry_sets_reset(self._h, _stream(stream)), "ferry_sets_reset")
+
+    # ---- inspection (synchronous) ---------------------------------------
+    def stats(self):
+        s = Stats()
+        _check(lib.ferry_stats_get(self._h, C.byref(s)), "ferry_stats_get")
+        return {f: getattr(s, f) for f, _ in Stats._fields_ if f != "pad"}
+
+    def stats_reset(self):
+        _check(lib.ferry_stats_reset(self._h), "ferry_stats_reset")
+
+    def sets_state(self):
+        cap = self.cfg.slots_per_set
+        fill = np.zeros(self.n_sets, np.uint32)
+        ord_ = np.zeros((self.n_sets, cap), np.uint32)
+        tag = np.zeros((self.n_sets, cap), np.uint32)
+        _check(lib.ferry_sets_state(self._h, fill.ctypes.data, ord_.ctypes.data, tag.ctypes.data),
+               "ferry_sets_state")
+        return fill, ord_, tag
+
+    def hosttier_array(self):
+        """numpy view of the pinned host tier (bytes) and fp8 scales (or None)."""
+        b, s = _vp(), _vp()
+        _check(lib.ferry_hosttier_view(self._h, C.byref(b), C.byref(s)), "ferry_hosttier_view")
+        n = self.cfg.host_blocks * self.block_bytes
+        arr = np.ctypeslib.as_array(C.cast(b, C.POINTER(C.c_uint8)), shape=(n,))
+        sc = None
+        if s.value:
+            sc = np.ctypeslib.as_array(C.cast(s, C.POINTER(C.c_float)),
+                                       shape=(self.cfg.host_blocks * 2,))
+        return arr, sc
+
+    def pool_ptrs(self):
+        p, s = _vp(), _vp()
+        _check(lib.ferry_pool_view(self._h, C.byref(p), C.byref(s)), "ferry_pool_view")
+        return p.value, s.value
+
+    def pool_slots_bytes(self, slot_ids):
+        """Copy the given pool slots (global ids) to host: [n, block_bytes] uint8."""
+        p, _ = self.pool_ptrs()
+        return _gather_d2h(p, self.block_bytes, slot_ids)
+
+    def pool_slot_scales(self, slot_ids):
+        """fp8 scales (k, v) of the given pool slots, or None."""
+        _, s = self.pool_ptrs()
+        if not s:
+            return None
+        return _gather_d2h(s, 8, slot_ids).view(np.float32).reshape(-1, 2)
+
+
+_hip = None
+
+
+def _gather_d2h(base, row_bytes, ids):
+    """rows base[ids[i] * row_bytes : +row_bytes] of device memory -> host array."""
+    global _hip
+    if _hip is None:
+        _hip = C.CDLL("libamdhip64.so.7")  # the runtime already loaded with torch
+        _hip.hipMemcpy.restype = C.c_int
+        _hip.hipMemcpy.argtypes = [_vp, _vp, C.c_size_t, C.c_int]
+        _hip.hipDeviceSynchronize.restype = C.c_int
+    ids = np.asarray(ids, np.int64).reshape(-1)
+    out = np.zeros((ids.size, row_bytes), np.uint8)
+    if _hip.hipDeviceSynchronize() != 0:
+        raise RuntimeError("hipDeviceSynchronize failed")
+    order = np.argsort(ids, kind="stable")
+    i = 0
+    while i < ids.size:  # copy runs of consecutive ids in one call
+        j = i + 1
+        while j < ids.size and ids[order[j]] == ids[order[j - 1]] + 1 and \
+                order[j] == order[j - 1] + 1:
+            j += 1
+        rc = _hip.hipMemcpy(out[order[i]:].ctypes.data, base + int(ids[order[i]]) * row_bytes,
+                            (j - i) * row_bytes, 2)
+        if rc != 0:
+            raise RuntimeError(f"hipMemcpy D2H failed ({rc})")
+        i = j
+    return out
+
+
+class SelGen:
+    """Synthetic top-k selection stream (host).  Steps must be drawn in order."""
+
+    def __init__(self, n_req, n_layers, kv_heads, k, ctx_blocks, dist=1, zipf_s=1.1,
+                 reuse=0.66, group=1, prefix_blocks=0, seed=1):
+        self.cfg = SelGenConfig(n_req, group, n_layers, kv_heads, k, dist, zipf_s, reuse,
+                                prefix_blocks, 0, seed)
+        ctx = np.ascontiguousarray(ctx_blocks, np.int32)
+        h = _vp()
+        _check(lib.ferry_selgen_create(C.byref(self.cfg), ctx.ctypes.data, C.byref(h)),
+               "ferry_selgen_create")
+        self._h = h
+        mb = _i32()
+        _check(lib.ferry_selgen_max_blocks(h, C.byref(mb)), "ferry_selgen_max_blocks")
+        self.max_blocks = mb.value
+        self.shape = (n_req, n_layers, kv_heads, k)
+
+    def step(self, step):
+        out = np.zeros(self.shape, np.uint32)
+        _check(lib.ferry_selgen_step(self._h, step, out.ctypes.data), "ferry_selgen_step")
+        return out
+
+    def __del__(self):
+        h, self._h = getattr(self, "_h", None), None
+        if h and lib is not None:
+            lib.ferry_selgen_destroy(h)
+
+
+def ctx_uniform(seed, n_req, lo, hi):
+    out = np.zeros(n_req, np.int32)
+    _check(lib.ferry_ctx_uniform(seed, n_req, lo, hi, out.ctypes.data), "ferry_ctx_uniform")
+    return out
+
+
+def refgen_selections(R, L, S, sel, seed=42):
+    """replay_miss_stream's selections, (r, s, l, k) order -> array [R, S, L, sel]."""
+    out = np.zeros((R, S, L, sel), np.uint32)
+    _check(lib.ferry_refgen_selections(R, L, S, sel, seed, out.ctypes.data),
+           "ferry_refgen_selections")
+    return out
+
+
+def queue_selftest(capacity=1 << 20, n_tasks=1 << 22, producers=512, consumers=512, mode=1,
+                   device=0):
+    """Exactly-once run of the device MPMC ring.  Returns (popped, dups, ms)."""
+    p, d, ms = C.c_uint64(), C.c_uint64(), C.c_float()
+    _check(lib.ferry_queue_selftest(device, capacity, n_tasks, producers, consumers, mode,
+                                    C.byref(p), C.byref(d), C.byref(ms)), "ferry_queue_selftest")
+    return p.value, d.value, ms.value

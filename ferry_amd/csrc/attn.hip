@@ -1,0 +1,253 @@
+// attn.hip -- block-sparse decode attention over the selected pool slots.
+//
+// out[r,l,hq] = softmax(q K^T / sqrt(D)) V over every token of the k blocks
+// selected for (r, l, kv head of hq).  The reference has no attention (an FMA
+// proxy at src/workloads/kv_exec.cuh:30-37); this is textbook attention with
+// the per-step top-k block selection of tools/capture_miss_trace.py:139-159.
+//
+// Work decomposition (HBM-bound, ~1-8 flop/byte): one workgroup per
+// (request, layer, kv head); its four wavefronts take every fourth selected
+// block.  A block is K[T][D] then V[T][D].  Each 16-byte load instruction of a
+// wavefront covers one contiguous KiB of the tile, so lane l holds the
+// EPV-element dim chunk (l % LPT) of token (l / LPT) + ld * TPL.  The q.K dot
+// product is reduced over the LPT lanes of a row with DPP row ops (no LDS);
+// every row of lanes then runs its own online softmax over the tokens it
+// holds, and rows, then wavefronts, are merged at the end.  Q heads of one kv
+// head (GQA group G) share every K/V load.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ferry_amd {
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int CTRL>
+__device__ inline float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+constexpr int kQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+
+// Sum over groups of N consecutive lanes; every lane of the group gets the
+// total.  Mirror/half-mirror pairings partition a row like xor 8 / xor 4 do.
+template <int N>
+__device__ inline float group_sum(float v) {
+  if constexpr (N >= 32) v += __shfl_xor(v, 16);
+  if constexpr (N >= 16) v += dpp<kRowMirror>(v);
+  if constexpr (N >= 8) v += dpp<kRowHalfMirror>(v);
+  if constexpr (N >= 4) v += dpp<kQuadXor2>(v);
+  if constexpr (N >= 2) v += dpp<kQuadXor1>(v);
+  return v;
+}
+
+__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Decode the EPV elements of one 16-byte word to float.  fp8 E4M3 is widened
+// through binary16 (same mantissa, exponent bias 15 instead of 7), which
+// leaves a factor 2^-8 that the caller folds into the block scale.
+template <int DT>
+__device__ inline void decode(const u32x4& w, float* f) {
+  if constexpr (DT == FERRY_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __builtin_bit_cast(float, w[i]);
+  } else if constexpr (DT == FERRY_F16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFFu));
+      f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+    }
+  } else if constexpr (DT == FERRY_BF16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __builtin_bit_cast(float, w[i] << 16);
+      f[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xFFFF0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t v = (w[i] >> (8 * b)) & 0xFFu;
+        const uint16_t h = (uint16_t)(((v & 0x80u) << 8) | ((v & 0x7Fu) << 7));
+        f[4 * i + b] = (float)__builtin_bit_cast(_Float16, h);
+      }
+    }
+  }
+}
+
+struct Softmax {
+  float m, l;
+};
+
+}  // namespace
+
+template <int DT, int G>
+__global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q,
+                                              const uint32_t* __restrict__ slots,
+                                              const uint8_t* __restrict__ pool,
+                                              const float* __restrict__ pool_scales,
+                                              float* __restrict__ out, float qscale,
+                                              int* __restrict__ err) {
+  constexpr int ES = DT == FERRY_F32 ? 4 : (DT == FERRY_FP8_E4M3 ? 1 : 2);
+  constexpr int D = 128, T = 16;
+  constexpr int EPV = 16 / ES;   // elements per 16-byte word
+  constexpr int LPT = D / EPV;   // lanes per token row
+  constexpr int TPL = 64 / LPT;  // tokens per load instruction
+  constexpr int NLD = T / TPL;   // load instructions per K (or V) tile
+  constexpr uint32_t TILE_WORDS = T * D * ES / 16;
+  constexpr float kNeg = -1.0e30f;
+
+  __shared__ float red[4][G][LPT][EPV + 2];
+
+  const int row = blockIdx.x;  // (r * L + l) * Hkv + h
+  const int h = row % g.Hkv;
+  const int rl = row / g.Hkv;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int dg = lane % LPT;
+
+  float qv[G][EPV];
+#pragma unroll
+  for (int gq = 0; gq < G; ++gq) {
+    const float* qp = q + ((size_t)rl * g.Hq + (size_t)h * G + gq) * D + dg * EPV;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) qv[gq][e] = qp[e] * qscale;
+  }
+  Softmax sm[G];
+  float acc[G][EPV];
+#pragma unroll
+  for (int gq = 0; gq < G; ++gq) {
+    sm[gq].m = kNeg;
+    sm[gq].l = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[gq][e] = 0.0f;
+  }
+
+  const uint32_t* sl = slots + (size_t)row * g.k;
+  const int k = g.k;
+  for (int j = wave; j < k; j += 4) {
+    uint64_t slot = sl[j];
+    if (slot >= g.pool_slots) {  // never read outside the pool
+      set_error(err, FERRY_ERANGE);
+      slot = 0;
+    }
+    const u32x4* kp = reinterpret_cast<const u32x4*>(pool + slot * g.bb);
+    const u32x4* vp = kp + TILE_WORDS;
+    u32x4 kr[NLD], vr[NLD];
+#pragma unroll
+    for (int ld = 0; ld < NLD; ++ld) kr[ld] = kp[ld * 64 + lane];
+#pragma unroll
+    for (int ld = 0; ld < NLD; ++ld) vr[ld] = vp[ld * 64 + lane];
+    float ks = 1.0f, vs = 1.0f;
+    if constexpr (DT == FERRY_FP8_E4M3) {
+      ks = pool_scales[2 * slot] * 256.0f;
+      vs = pool_scales[2 * slot + 1] * 256.0f;
+    }
+    float kf[NLD][EPV];
+#pragma unroll
+    for (int ld = 0; ld < NLD; ++ld) decode<DT>(kr[ld], kf[ld]);
+    float s[G][NLD];
+#pragma unroll
+    for (int gq = 0; gq < G; ++gq)
+#pragma unroll
+      for (int ld = 0; ld < NLD; ++ld) {
+        float a = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) a = __builtin_fmaf(qv[gq][e], kf[ld][e], a);
+        s[gq][ld] = group_sum<LPT>(a) * ks;
+      }
+    float vf[NLD][EPV];
+#pragma unroll
+    for (int ld = 0; ld < NLD; ++ld) decode<DT>(vr[ld], vf[ld]);
+#pragma unroll
+    for (int gq = 0; gq < G; ++gq) {
+      float mb = s[gq][0];
+#pragma unroll
+      for (int ld = 1; ld < NLD; ++ld) mb = fmaxf(mb, s[gq][ld]);
+      const float mn = fmaxf(sm[gq].m, mb);
+      const float alpha = exp2_fast(sm[gq].m - mn);
+      float p[NLD], psum = 0.0f;
+#pragma unroll
+      for (int ld = 0; ld < NLD; ++ld) {
+        p[ld] = exp2_fast(s[gq][ld] - mn);
+        psum += p[ld];
+      }
+      sm[gq].l = sm[gq].l * alpha + psum;
+      sm[gq].m = mn;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) {
+        float a = acc[gq][e] * alpha;
+#pragma unroll
+        for (int ld = 0; ld < NLD; ++ld) a = __builtin_fmaf(p[ld] * vs, vf[ld][e], a);
+        acc[gq][e] = a;
+      }
+    }
+  }
+
+  // merge the TPL rows of the wavefront (lanes with the same dim chunk)
+#pragma unroll
+  for (int off = LPT; off < 64; off <<= 1) {
+#pragma unroll
+    for (int gq = 0; gq < G; ++gq) {
+      const float om = __shfl_xor(sm[gq].m, off);
+      const float ol = __shfl_xor(sm[gq].l, off);
+      const float mn = fmaxf(sm[gq].m, om);
+      const float a1 = exp2_fast(sm[gq].m - mn), a2 = exp2_fast(om - mn);
+      sm[gq].l = sm[gq].l * a1 + ol * a2;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) {
+        const float oa = __shfl_xor(acc[gq][e], off);
+        acc[gq][e] = acc[gq][e] * a1 + oa * a2;
+      }
+      sm[gq].m = mn;
+    }
+  }
+  if (lane < LPT) {
+#pragma unroll
+    for (int gq = 0; gq < G; ++gq) {
+      red[wave][gq][lane][0] = sm[gq].m;
+      red[wave][gq][lane][1] = sm[gq].l;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) red[wave][gq][lane][2 + e] = acc[gq][e];
+    }
+  }
+  __syncthreads();
+  // merge the four wavefronts and write out
+  for (int t = threadIdx.x; t < G * LPT; t += blockDim.x) {
+    const int gq = t / LPT, c = t % LPT;
+    float m = red[0][gq][c][0];
+    for (int w = 1; w < 4; ++w) m = fmaxf(m, red[w][gq][c][0]);
+    float l = 0.0f, o[EPV];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) o[e] = 0.0f;
+    for (int w = 0; w < 4; ++w) {
+      const float a = exp2_fast(red[w][gq][c][0] - m);
+      l += red[w][gq][c][1] * a;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) o[e] += red[w][gq][c][2 + e] * a;
+    }
+    const float inv = 1.0f / l;
+    float* op = out + ((size_t)rl * g.Hq + (size_t)h * G + gq) * D + c * EPV;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) op[e] = o[e] * inv;
+  }
+}
+
+#define FERRY_ATTN_INST(DT, G)                                                              \
+  template __global__ void k_attn<DT, G>(Geo, const float*, const uint32_t*, const uint8_t*, \
+                                         const float*, float*, float, int*);
+#define FERRY_ATTN_INST_G(DT) \
+  FERRY_ATTN_INST(DT, 1)      \
+  FERRY_ATTN_INST(DT, 2)      \
+  FERRY_ATTN_INST(DT, 4)      \
+  FERRY_ATTN_INST(DT, 8)
+FERRY_ATTN_INST_G(FERRY_F32)
+FERRY_ATTN_INST_G(FERRY_F16)
+FERRY_ATTN_INST_G(FERRY_BF16)
+FERRY_ATTN_INST_G(FERRY_FP8_E4M3)
+
+}  // namespace ferry_amd

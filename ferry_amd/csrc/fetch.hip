@@ -1,0 +1,186 @@
+// fetch.hip -- drain of the device miss ring into the HBM slot pool.
+//
+// Persistent workgroups, one deque each.  Every wavefront pops one miss at a
+// time from its own deque head; when that is empty it scans all deques,
+// picks the fullest and steals min(max(rem/2, 1), steal_chunk) entries from its
+// tail, never more than rem/2+1 (the reference's steal bound,
+// src/runtime/wla_multigpu.cuh:1147-1152, 1518-1526; src/runtime/multigpu.cuh:
+// 153-175).  A miss is copied by one wavefront: 16-byte loads straight from
+// the pinned host tier (one PCIe hop, no staging ring, unlike
+// HostStagedChannel::submit, src/comm/host_staged_channel.cpp:43-74) into the
+// slot.  The last workgroup to finish accounts the drain and rewinds every
+// deque, so the ring is empty and reusable when the kernel ends.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ferry_amd {
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int NV>
+__device__ inline void copy_block(const FetchArgs& a, const ferry_miss& m, int lane) {
+  const uint64_t h = host_index(m.set, m.block, (uint64_t)a.g.max_blocks, a.g.host_blocks);
+  const u32x4* src = reinterpret_cast<const u32x4*>(a.host + h * a.g.bb);
+  u32x4* dst = reinterpret_cast<u32x4*>(a.pool + ((uint64_t)m.set * (uint64_t)a.g.C + m.slot) * a.g.bb);
+  u32x4 r[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) r[i] = __builtin_nontemporal_load(src + i * kWave + lane);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) dst[i * kWave + lane] = r[i];
+  if (a.pool_scales && lane < 2)
+    a.pool_scales[((uint64_t)m.set * (uint64_t)a.g.C + m.slot) * 2 + lane] = a.host_scales[h * 2 + lane];
+}
+
+__device__ inline ferry_miss load_entry(const ferry_miss* p) {
+  ferry_miss m;
+  m.block = p->block;
+  m.slot = p->slot;
+  m.evicted = p->evicted;
+  m.set = p->set;
+  return m;
+}
+
+}  // namespace
+
+template <int NV>
+__global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int W = gridDim.x;
+  const int me = blockIdx.x;
+  uint64_t* state = a.ring.state;
+  uint64_t steals = 0, stolen = 0, copied = 0;
+  // Every iteration either copies at least one miss or observes a CAS lost to
+  // a peer that made progress; the guard only bounds a broken protocol.
+  for (long guard = 0;; ++guard) {
+    if (guard > (1L << 28)) {
+      if (lane == 0) set_error(a.err, FERRY_ESPIN);
+      break;
+    }
+    // own deque: pop one from the head
+    int got = 0;
+    uint32_t idx = 0;
+    if (lane == 0) {
+      const uint32_t capw = a.ring.cap[me];
+      uint64_t st = aload64(state + me);
+      for (int tries = 0; tries < (1 << 20); ++tries) {
+        const uint32_t h = (uint32_t)st;
+        const uint32_t t = min((uint32_t)(st >> 32), capw);
+        if (h >= t) break;
+        const uint64_t prev = atomicCAS((unsigned long long*)(state + me), st, st + 1);
+        if (prev == st) {
+          got = 1;
+          idx = h;
+          break;
+        }
+        st = prev;
+      }
+    }
+    got = first_lane_i(got);
+    if (got) {
+      idx = first_lane_u(idx);
+      copy_block<NV>(a, load_entry(a.ring.entries + a.ring.seg[me] + idx), lane);
+      ++copied;
+      continue;
+    }
+    if (!a.steal) break;
+    // victim = fullest deque
+    uint32_t best = 0;
+    int bw = W;
+    for (int w = lane; w < W; w += kWave) {
+      const uint64_t st = aload64(state + w);
+      const uint32_t h = (uint32_t)st, t = min((uint32_t)(st >> 32), a.ring.cap[w]);
+      const uint32_t rem = t > h ? t - h : 0;
+      if (rem > best) {
+        best = rem;
+        bw = w;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint32_t ob = __shfl_xor(best, off);
+      const int ow = __shfl_xor(bw, off);
+      if (ob > best || (ob == best && ow < bw)) {
+        best = ob;
+        bw = ow;
+      }
+    }
+    best = first_lane_u(best);
+    bw = first_lane_i(bw);
+    if (best == 0) break;  // every deque is drained
+    int ok = 0;
+    uint32_t s0 = 0, s1 = 0;
+    if (lane == 0) {
+      const uint64_t st = aload64(state + bw);
+      const uint32_t h = (uint32_t)st, t = min((uint32_t)(st >> 32), a.ring.cap[bw]);
+      if (t > h) {
+        const uint32_t rem = t - h;
+        const uint32_t m = min(max(rem / 2, 1u), a.steal_chunk);
+        const uint64_t nst = ((uint64_t)(t - m) << 32) | h;
+        if (atomicCAS((unsigned long long*)(state + bw), st, nst) == st) {
+          ok = 1;
+          s0 = t - m;
+          s1 = t;
+        }
+      }
+    }
+    ok = first_lane_i(ok);
+    if (!ok) continue;
+    s0 = first_lane_u(s0);
+    s1 = first_lane_u(s1);
+    const ferry_miss* seg = a.ring.entries + a.ring.seg[bw];
+    for (uint32_t i = s0; i < s1; ++i) copy_block<NV>(a, load_entry(seg + i), lane);
+    ++steals;
+    stolen += s1 - s0;
+    copied += s1 - s0;
+  }
+  if (lane == 0) {
+    if (copied) atomicAdd(a.stats + kStatDrain, (unsigned long long)copied);
+    if (steals) {
+      atomicAdd(a.stats + kStatSteals, (unsigned long long)steals);
+      atomicAdd(a.stats + kStatStolen, (unsigned long long)stolen);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    const uint32_t prev = atomicAdd(a.done, 1u);
+    if (prev == (uint32_t)W - 1) {
+      __threadfence();
+      for (int w = 0; w < W; ++w) astore64(state + w, 0ull);
+      const unsigned long long total = atomicExch(a.stats + kStatDrain, 0ull);
+      atomicAdd(a.stats + kStatMisses, total);
+      atomicAdd(a.stats + kStatBytes, total * a.g.bb);
+      atomicExch(a.stats + kStatLast, total);
+      astore(a.done, 0u);
+      __threadfence();
+    }
+  }
+}
+
+template __global__ void k_fetch<4>(FetchArgs);
+template __global__ void k_fetch<8>(FetchArgs);
+template __global__ void k_fetch<16>(FetchArgs);
+
+// Queue externally built misses: each thread appends one entry to the tail of
+// its set's worker deque.
+__global__ void k_missq_push(Geo g, Ring ring, const ferry_miss* m, uint32_t n, int* err) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const ferry_miss e = m[i];
+  if (e.set >= (uint32_t)g.n_sets || e.slot >= (uint32_t)g.C || e.block >= (uint32_t)g.max_blocks) {
+    set_error(err, FERRY_EINVAL);
+    return;
+  }
+  const uint32_t w = ring.worker_of_set[e.set];
+  const uint64_t old = atomicAdd((unsigned long long*)(ring.state + w), 1ull << 32);
+  const uint32_t t = (uint32_t)(old >> 32);
+  if (t >= ring.cap[w]) {
+    set_error(err, FERRY_ESPIN);
+    return;
+  }
+  ring.entries[ring.seg[w] + t] = e;
+}
+
+}  // namespace ferry_amd

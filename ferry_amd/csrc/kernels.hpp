@@ -1,0 +1,60 @@
+// kernels.hpp -- device data structures and kernel declarations.
+#pragma once
+
+#include "common.hpp"
+
+namespace ferry_amd {
+
+// Per-set LRU state in HBM (see lru.hip for the rule it implements).
+struct SetState {
+  uint32_t* fill;  // [n_sets] slots in use; free slots are [fill, C)
+  uint32_t* ord;   // [n_sets][C] local slots, least recent first
+  uint32_t* tag;   // [n_sets][C] block held by each slot (kNone if free)
+  uint32_t* map;   // [n_sets][max_blocks] slot holding each block (kNone)
+};
+
+// Device miss ring: one deque per fetch worker, each a fixed segment of
+// `entries`.  state[w] packs (tail << 32 | head) relative to the segment, so
+// owner pops (head++) and thief steals (tail -= m) are single 64-bit CASes.
+struct Ring {
+  ferry_miss* entries;
+  uint64_t* state;
+  const uint32_t* seg;            // [W] segment start
+  const uint32_t* cap;            // [W] segment capacity
+  const uint32_t* worker_of_set;  // [n_sets]
+};
+
+// Device counters (unsigned long long).
+enum StatSlot { kStatMisses = 0, kStatBytes, kStatSteals, kStatStolen, kStatLast, kStatDrain, kStatCount };
+
+struct FetchArgs {
+  Geo g;
+  Ring ring;
+  const uint8_t* host;
+  const float* host_scales;
+  uint8_t* pool;
+  float* pool_scales;
+  int steal;
+  uint32_t steal_chunk;
+  unsigned long long* stats;
+  uint32_t* done;
+  int* err;
+};
+
+template <bool SERIAL>
+__global__ void k_lru_step(Geo g, const uint32_t* sel, uint32_t* slots_out, uint32_t* miss_count,
+                           ferry_miss* misses, uint8_t* miss_flag, SetState st, Ring ring, int* err);
+__global__ void k_sets_reset(Geo g, SetState st);
+
+template <int NV>
+__global__ void k_fetch(FetchArgs a);
+__global__ void k_missq_push(Geo g, Ring ring, const ferry_miss* m, uint32_t n, int* err);
+
+template <int DT, int G>
+__global__ void k_attn(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
+                       const float* pool_scales, float* out, float qscale, int* err);
+
+__global__ void k_hosttier_fill(Geo g, uint8_t* host, float* scales, uint64_t seed, float mult,
+                                float mult8, float scale_base);
+
+}  // namespace ferry_amd

@@ -1,0 +1,290 @@
+// lru.hip -- miss bookkeeping of one decode step: dedup, LRU slot assignment
+// and eviction, miss-ring push.  One wavefront owns one set (owner, layer, kv
+// head) for the whole step, so no two waves ever touch the same set state.
+//
+// Rule (one "sub-step" = the whole step in FERRY_LRU_STEP, one selection in
+// FERRY_LRU_SERIAL; with one selection it is exactly the reference's kv_touch,
+// src/runtime/wla_multigpu.cuh:1937-1962 / missstream.cuh:137-161):
+//   hit  = block resident when the sub-step starts;
+//   miss = first occurrence, in canonical order (member request, then
+//          selection index), of a non-resident block; later occurrences hit
+//          the in-flight fetch (dedup, kv_exec.cuh:210-223 dedups per step);
+//   the q-th miss takes free slot fill+q while free slots remain, else the
+//          least recently used resident slot not touched in this sub-step;
+//   new LRU order = untouched survivors in old order ++ touched slots ordered
+//          by their last occurrence.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ferry_amd {
+
+namespace {
+
+struct SetView {
+  int o, l, h, n;  // owner, layer, kv head, selections of the set this step
+};
+
+__device__ inline size_t sel_index(const Geo& g, const SetView& s, int p) {
+  const int m = p / g.k, j = p - m * g.k;
+  return ((size_t)((s.o * g.group + m) * g.L + s.l) * g.Hkv + s.h) * (size_t)g.k + j;
+}
+
+// One batched sub-step over positions [p0, p0 + cnt).  Returns the number of
+// misses appended at mo[0..), or a negative FERRY_E* code.
+__device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, int cnt,
+                       const uint32_t* __restrict__ sel, uint32_t* __restrict__ slots_out,
+                       uint8_t* __restrict__ miss_flag, uint32_t* __restrict__ map,
+                       int* lastpos, uint32_t* sord, uint32_t* stag, uint32_t* smblk,
+                       uint32_t* svict, uint32_t& fill, ferry_miss* __restrict__ mo,
+                       const Ring& ring, uint32_t worker) {
+  const int lane = lane_id();
+  const int C = g.C;
+  const int pend = p0 + cnt;
+  // phase 1: classify (hits mark their slot; misses race for first occurrence)
+  for (int c = p0; c < pend; c += kWave) {
+    const int p = c + lane;
+    if (p < pend) {
+      const uint32_t x = sel[sel_index(g, sv, p)];
+      const uint32_t v = aload(map + x);
+      if (v < (uint32_t)C)
+        atomicMax(lastpos + v, p);
+      else
+        atomicMin(map + x, kPend | (uint32_t)p);
+    }
+  }
+  wave_fence();
+  // phase 2: rank misses by first occurrence
+  int M = 0;
+  for (int c = p0; c < pend; c += kWave) {
+    const int p = c + lane;
+    bool is_miss = false;
+    uint32_t x = 0;
+    if (p < pend) {
+      x = sel[sel_index(g, sv, p)];
+      is_miss = aload(map + x) == (kPend | (uint32_t)p);
+      if (miss_flag) miss_flag[sel_index(g, sv, p)] = is_miss ? 1 : 0;
+    }
+    const uint64_t mask = ballot(is_miss);
+    if (is_miss) smblk[M + lanes_below(mask)] = x;
+    M += __builtin_popcountll(mask);
+  }
+  // phase 3: victims = least recent untouched residents, oldest first
+  const int freeslots = C - (int)fill;
+  const int need = M > freeslots ? M - freeslots : 0;
+  int nv = 0;
+  for (int c = 0; c < (int)fill && nv < need; c += kWave) {
+    const int i = c + lane;
+    bool untouched = false;
+    uint32_t o = 0;
+    if (i < (int)fill) {
+      o = sord[i];
+      untouched = lastpos[o] < 0;
+    }
+    const uint64_t mask = ballot(untouched);
+    const int r = nv + lanes_below(mask);
+    if (untouched && r < need) svict[r] = o;
+    nv += __builtin_popcountll(mask);
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (nv < need) {
+    for (int q = lane; q < M; q += kWave) astore(map + smblk[q], kNone);
+    wave_fence();
+    return FERRY_ECAPACITY;
+  }
+  // reserve M entries at the tail of this set's worker deque
+  ferry_miss* rdst = nullptr;
+  if (M > 0) {
+    uint64_t old = 0;
+    if (lane == 0)
+      old = atomicAdd((unsigned long long*)(ring.state + worker), (unsigned long long)M << 32);
+    const uint32_t t0 = (uint32_t)(first_lane_u64(old) >> 32);
+    if (t0 + (uint32_t)M > ring.cap[worker]) {
+      for (int q = lane; q < M; q += kWave) astore(map + smblk[q], kNone);
+      wave_fence();
+      return FERRY_ESPIN;
+    }
+    rdst = ring.entries + ring.seg[worker] + t0;
+  }
+  // phase 4: assign slots, evict, publish block -> slot, write the ring
+  for (int q = lane; q < M; q += kWave) {
+    const uint32_t x = smblk[q];
+    uint32_t v, ev = kNone;
+    if (q < freeslots) {
+      v = fill + (uint32_t)q;
+    } else {
+      v = svict[q - freeslots];
+      ev = stag[v];
+      if (ev < (uint32_t)g.max_blocks) astore(map + ev, kNone);
+    }
+    stag[v] = x;
+    astore(map + x, v);
+    ferry_miss m;
+    m.block = x;
+    m.slot = v;
+    m.evicted = ev;
+    m.set = set;
+    mo[q] = m;
+    rdst[q] = m;
+  }
+  wave_fence();
+  // phase 4b: slot of every position; last occurrence per touched slot
+  for (int c = p0; c < pend; c += kWave) {
+    const int p = c + lane;
+    if (p < pend) {
+      const size_t gi = sel_index(g, sv, p);
+      const uint32_t v = aload(map + sel[gi]);
+      slots_out[gi] = set * (uint32_t)C + v;
+      atomicMax(lastpos + v, p);
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  // phase 5: new LRU order
+  int w = 0;
+  for (int c = 0; c < (int)fill; c += kWave) {
+    const int i = c + lane;
+    bool keep = false;
+    uint32_t o = 0;
+    if (i < (int)fill) {
+      o = sord[i];
+      keep = lastpos[o] < 0;
+    }
+    const uint64_t mask = ballot(keep);
+    __builtin_amdgcn_wave_barrier();
+    if (keep && w + lanes_below(mask) < C) sord[w + lanes_below(mask)] = o;
+    w += __builtin_popcountll(mask);
+  }
+  for (int c = p0; c < pend; c += kWave) {
+    const int p = c + lane;
+    bool emit = false;
+    uint32_t v = 0;
+    if (p < pend) {
+      v = aload(map + sel[sel_index(g, sv, p)]);
+      emit = lastpos[v] == p;
+    }
+    const uint64_t mask = ballot(emit);
+    if (emit && w + lanes_below(mask) < C) sord[w + lanes_below(mask)] = v;
+    w += __builtin_popcountll(mask);
+  }
+  fill += (uint32_t)(M < freeslots ? M : freeslots);
+  if (w != (int)fill) return FERRY_ESTATE;
+  // phase 6: clear the marks of this sub-step
+  for (int c = p0; c < pend; c += kWave) {
+    const int p = c + lane;
+    if (p < pend) lastpos[aload(map + sel[sel_index(g, sv, p)])] = -1;
+  }
+  __builtin_amdgcn_wave_barrier();
+  return M;
+}
+
+}  // namespace
+
+template <bool SERIAL>
+__global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restrict__ sel,
+                                                  uint32_t* __restrict__ slots_out,
+                                                  uint32_t* __restrict__ miss_count,
+                                                  ferry_miss* __restrict__ misses,
+                                                  uint8_t* __restrict__ miss_flag,
+                                                  SetState st, Ring ring, int* __restrict__ err) {
+  extern __shared__ uint32_t lds[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wpb = blockDim.x >> 6;
+  const int set = blockIdx.x * wpb + wave;
+  if (set >= g.n_sets) return;  // no workgroup barriers follow
+  const int C = g.C;
+  uint32_t* base = lds + (size_t)wave * (3 * C + 2 * g.max_sel);
+  int* lastpos = (int*)base;
+  uint32_t* sord = base + C;
+  uint32_t* stag = base + 2 * C;
+  uint32_t* smblk = base + 3 * C;
+  uint32_t* svict = smblk + g.max_sel;
+
+  SetView sv;
+  sv.h = set % g.Hkv;
+  sv.l = (set / g.Hkv) % g.L;
+  sv.o = set / (g.Hkv * g.L);
+  const int mem = min(g.group, g.n_req - sv.o * g.group);
+  sv.n = mem * g.k;
+
+  uint32_t* map = st.map + (size_t)set * (size_t)g.max_blocks;
+  uint32_t* gord = st.ord + (size_t)set * C;
+  uint32_t* gtag = st.tag + (size_t)set * C;
+  uint32_t fill = st.fill[set];
+  for (int i = lane; i < C; i += kWave) {
+    lastpos[i] = -1;
+    sord[i] = gord[i];
+    stag[i] = gtag[i];
+  }
+  // range check of every selected id before touching the map
+  bool bad = false;
+  for (int p = lane; p < sv.n; p += kWave) bad |= sel[sel_index(g, sv, p)] >= (uint32_t)g.max_blocks;
+  if (ballot(bad)) {
+    if (lane == 0) {
+      set_error(err, FERRY_ERANGE);
+      miss_count[set] = 0;
+    }
+    return;
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  ferry_miss* mo = misses + (size_t)set * g.max_sel;
+  const uint32_t worker = ring.worker_of_set[set];
+  int total = 0, rc = 0;
+  if (!SERIAL) {
+    rc = substep(g, sv, (uint32_t)set, 0, sv.n, sel, slots_out, miss_flag, map, lastpos, sord, stag,
+                 smblk, svict, fill, mo, ring, worker);
+    if (rc >= 0) total = rc;
+  } else {
+    for (int p = 0; p < sv.n; ++p) {
+      rc = substep(g, sv, (uint32_t)set, p, 1, sel, slots_out, miss_flag, map, lastpos, sord, stag,
+                   smblk, svict, fill, mo + total, ring, worker);
+      if (rc < 0) break;
+      total += rc;
+    }
+    if (rc >= 0) {
+      // every selection's slot must still hold its block at the end of the step
+      wave_fence();
+      bool lost = false;
+      for (int p = lane; p < sv.n; p += kWave) {
+        const size_t gi = sel_index(g, sv, p);
+        lost |= stag[aload(slots_out + gi) - (uint32_t)set * (uint32_t)C] != sel[gi];
+      }
+      if (ballot(lost)) rc = FERRY_ECAPACITY;
+    }
+  }
+  if (rc < 0) {
+    if (lane == 0) {
+      set_error(err, rc);
+      miss_count[set] = 0;
+    }
+    return;
+  }
+  for (int i = lane; i < C; i += kWave) {
+    gord[i] = i < (int)fill ? sord[i] : kNone;
+    gtag[i] = stag[i];
+  }
+  if (lane == 0) {
+    st.fill[set] = fill;
+    miss_count[set] = (uint32_t)total;
+  }
+}
+
+template __global__ void k_lru_step<false>(Geo, const uint32_t*, uint32_t*, uint32_t*, ferry_miss*,
+                                           uint8_t*, SetState, Ring, int*);
+template __global__ void k_lru_step<true>(Geo, const uint32_t*, uint32_t*, uint32_t*, ferry_miss*,
+                                          uint8_t*, SetState, Ring, int*);
+
+// Reset all sets: empty order, no tags, map cleared.
+__global__ void k_sets_reset(Geo g, SetState st) {
+  const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const size_t nslots = (size_t)g.n_sets * g.C;
+  const size_t nmap = (size_t)g.n_sets * g.max_blocks;
+  for (size_t i = tid; i < nslots; i += stride) {
+    st.ord[i] = kNone;
+    st.tag[i] = kNone;
+  }
+  for (size_t i = tid; i < nmap; i += stride) st.map[i] = kNone;
+  for (size_t i = tid; i < (size_t)g.n_sets; i += stride) st.fill[i] = 0;
+}
+
+}  // namespace ferry_amd

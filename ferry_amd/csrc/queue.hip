@@ -1,0 +1,61 @@
+// queue.hip -- exactly-once acceptance of the device MPMC ring.
+//
+// One kernel, roles split by block index as in the reference's pc_kernel
+// (src/benches/bench_queue.cu:26-59): producer blocks push unique task ids,
+// consumer blocks pop them and count arrivals per id in seen[].  The grid is
+// small enough to be co-resident, and every wait in the queue is bounded.
+#include "common.hpp"
+#include "../../include/ferry/gpu_bounded_queue.hpp"
+
+namespace ferry_amd {
+
+__global__ __launch_bounds__(256) void k_queue_pc(ferry::DeviceQueue* q, uint64_t per_thread,
+                                                  uint32_t n_prod_blocks, uint32_t* seen,
+                                                  unsigned long long* popped,
+                                                  unsigned long long* dups, int* done,
+                                                  int* prod_blocks_done, ferry::ReservationMode mode) {
+  if (blockIdx.x < n_prod_blocks) {
+    const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (uint64_t i = 0; i < per_thread; ++i) {
+      const uint64_t task = tid * per_thread + i;
+      long tries = 0;
+      while (!ferry::dq_push(q, task, mode)) {
+        if (__hip_atomic_load(&q->status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
+            ++tries > ferry::kQueueSpinLimit) {
+          atomicExch(&q->status, 2);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(4);
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __threadfence();
+      if (atomicAdd(prod_blocks_done, 1) + 1 == (int)n_prod_blocks) atomicExch(done, 1);
+    }
+  } else {
+    long idle = 0;
+    unsigned long long mine = 0;
+    while (true) {
+      uint64_t task;
+      if (ferry::dq_pop(q, &task)) {
+        if (atomicAdd(seen + task, 1u) != 0u) atomicAdd(dups, 1ull);
+        ++mine;
+        idle = 0;
+      } else {
+        const int d = __hip_atomic_load(done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+        if ((d && ferry::dq_size(q) == 0) ||
+            __hip_atomic_load(&q->status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+          break;
+        if (++idle > ferry::kQueueSpinLimit) {
+          atomicExch(&q->status, 3);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(4);
+      }
+    }
+    atomicAdd(popped, mine);
+  }
+}
+
+}  // namespace ferry_amd

@@ -1,0 +1,519 @@
+// runtime.hip -- executor context and the C-ABI (include/ferry_amd.h).
+//
+// The context owns every buffer of the path: the HBM slot pool, per-set LRU
+// state, the device miss ring and the pinned host tier.  Entry points launch
+// on the caller's stream and never synchronise, except the explicitly
+// synchronous ones (stats, state copies, the queue self-test).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+#include "../../include/ferry/gpu_bounded_queue.hpp"
+
+using namespace ferry_amd;
+
+namespace ferry_amd {
+__global__ void k_queue_pc(ferry::DeviceQueue* q, uint64_t per_thread, uint32_t n_prod_blocks,
+                           uint32_t* seen, unsigned long long* popped, unsigned long long* dups,
+                           int* done, int* prod_blocks_done, ferry::ReservationMode mode);
+}
+
+namespace {
+
+thread_local std::string g_err = "";
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define HIPC(expr)                                                                         \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess)                                                                  \
+      return fail(e_ == hipErrorOutOfMemory ? FERRY_ENOMEM : FERRY_EHIP,                   \
+                  std::string(#expr) + ": " + hipGetErrorString(e_) + " (" __FILE__ ":" + \
+                      std::to_string(__LINE__) + ")");                                     \
+  } while (0)
+
+int esize_of(int dtype) { return dtype == FERRY_F32 ? 4 : (dtype == FERRY_FP8_E4M3 ? 1 : 2); }
+
+float value_mult(double std_) { return (float)(std_ / (65536.0 / std::sqrt(3.0))); }
+
+}  // namespace
+
+struct ferry_ctx {
+  ferry_config cfg{};
+  int device = 0;
+  Geo g{};
+  uint8_t* pool = nullptr;
+  float* pool_scales = nullptr;
+  SetState st{};
+  ferry_miss* ring_entries = nullptr;
+  uint64_t* ring_state = nullptr;
+  uint32_t* ring_seg = nullptr;
+  uint32_t* ring_cap = nullptr;
+  uint32_t* worker_of_set = nullptr;
+  unsigned long long* stats = nullptr;
+  uint32_t* done = nullptr;
+  int* err = nullptr;
+  uint8_t* host = nullptr;      // host pointer of the pinned tier
+  uint8_t* host_dev = nullptr;  // its device-visible address
+  float* host_scales = nullptr;
+  float* host_scales_dev = nullptr;
+  int lru_wpb = 1;
+  size_t lru_lds = 0;
+  uint64_t steps = 0, selections = 0;
+
+  Ring ring() const {
+    Ring r;
+    r.entries = ring_entries;
+    r.state = ring_state;
+    r.seg = ring_seg;
+    r.cap = ring_cap;
+    r.worker_of_set = worker_of_set;
+    return r;
+  }
+};
+
+namespace {
+
+int validate(const ferry_config* c) {
+  if (!c) return fail(FERRY_EINVAL, "null config");
+  if (c->n_req < 1 || c->group < 1 || c->n_layers < 1 || c->kv_heads < 1 || c->q_heads < 1 ||
+      c->k < 1 || c->slots_per_set < 1 || c->max_blocks < 1 || c->host_blocks < 1)
+    return fail(FERRY_EINVAL, "sizes must be positive");
+  if (c->q_heads % c->kv_heads) return fail(FERRY_EINVAL, "q_heads must be a multiple of kv_heads");
+  const int grp = c->q_heads / c->kv_heads;
+  if (grp != 1 && grp != 2 && grp != 4 && grp != 8)
+    return fail(FERRY_EINVAL, "q_heads/kv_heads must be 1, 2, 4 or 8");
+  if (c->head_dim != 128) return fail(FERRY_EINVAL, "head_dim must be 128");
+  if (c->block_tokens != 16) return fail(FERRY_EINVAL, "block_tokens must be 16");
+  if (c->dtype < FERRY_F32 || c->dtype > FERRY_FP8_E4M3) return fail(FERRY_EINVAL, "bad dtype");
+  if (c->lru_mode != FERRY_LRU_STEP && c->lru_mode != FERRY_LRU_SERIAL)
+    return fail(FERRY_EINVAL, "bad lru_mode");
+  if (c->assign != FERRY_ASSIGN_SPREAD && c->assign != FERRY_ASSIGN_AFFINITY)
+    return fail(FERRY_EINVAL, "bad assign");
+  if (c->fetch_workers < 0) return fail(FERRY_EINVAL, "fetch_workers < 0");
+  if ((uint64_t)c->max_blocks >= (uint64_t)kPend) return fail(FERRY_EINVAL, "max_blocks too large");
+  return FERRY_OK;
+}
+
+template <typename T>
+int dalloc(T** p, size_t n) {
+  HIPC(hipMalloc((void**)p, std::max<size_t>(n, 1) * sizeof(T)));
+  return FERRY_OK;
+}
+
+void release(ferry_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  void* dev[] = {c->pool, c->pool_scales, c->st.fill, c->st.ord, c->st.tag, c->st.map,
+                 c->ring_entries, c->ring_state, c->ring_seg, c->ring_cap, c->worker_of_set,
+                 c->stats, c->done, c->err};
+  for (void* p : dev)
+    if (p) (void)hipFree(p);
+  if (c->host) (void)hipHostFree(c->host);
+  if (c->host_scales) (void)hipHostFree(c->host_scales);
+  delete c;
+}
+
+int check_ctx(const ferry_ctx* c) { return c ? FERRY_OK : fail(FERRY_EINVAL, "null context"); }
+
+}  // namespace
+
+extern "C" {
+
+const char* ferry_last_error(void) { return g_err.c_str(); }
+const char* ferry_version(void) { return "ferry_amd 0.1 (gfx950)"; }
+
+int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
+  if (!out) return fail(FERRY_EINVAL, "null out");
+  *out = nullptr;
+  int rc = validate(cfg);
+  if (rc) return rc;
+  HIPC(hipSetDevice(device));
+  ferry_ctx* c = new ferry_ctx();
+  c->cfg = *cfg;
+  c->device = device;
+  Geo& g = c->g;
+  g.n_req = cfg->n_req;
+  g.group = cfg->group;
+  g.L = cfg->n_layers;
+  g.Hkv = cfg->kv_heads;
+  g.Hq = cfg->q_heads;
+  g.D = cfg->head_dim;
+  g.T = cfg->block_tokens;
+  g.k = cfg->k;
+  g.C = cfg->slots_per_set;
+  g.max_blocks = cfg->max_blocks;
+  g.n_owners = (cfg->n_req + cfg->group - 1) / cfg->group;
+  g.n_sets = g.n_owners * g.L * g.Hkv;
+  g.pool_slots = 0;
+  g.max_sel = cfg->group * cfg->k;
+  g.dtype = cfg->dtype;
+  g.esize = esize_of(cfg->dtype);
+  g.bb = 2ull * g.T * g.D * g.esize;
+  g.host_blocks = cfg->host_blocks;
+  g.pool_slots = (uint64_t)g.n_sets * (uint64_t)g.C;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1)
+    cus = 256;
+  g.workers = cfg->fetch_workers > 0 ? cfg->fetch_workers : 2 * cus;
+  if ((uint64_t)g.n_sets * (uint64_t)g.C >= 0xFFFFFFFFull ||
+      (uint64_t)g.n_sets * (uint64_t)g.max_sel >= 0xFFFFFFFFull) {
+    delete c;
+    return fail(FERRY_EINVAL, "too many slots or selections for 32-bit ids");
+  }
+  // bookkeeping launch shape: waves per workgroup bounded by 64 KiB of LDS
+  const size_t per_wave = (size_t)(3 * g.C + 2 * g.max_sel) * 4;
+  if (per_wave > 65536) {
+    delete c;
+    return fail(FERRY_EINVAL, "slots_per_set/group*k too large for the bookkeeping LDS budget");
+  }
+  c->lru_wpb = 4;
+  while (c->lru_wpb > 1 && per_wave * c->lru_wpb > 65536) c->lru_wpb >>= 1;
+  c->lru_lds = per_wave * c->lru_wpb;
+
+  const size_t nslots = (size_t)g.n_sets * g.C;
+#define TRY(x)        \
+  do {                \
+    rc = (x);         \
+    if (rc) {         \
+      release(c);     \
+      return rc;      \
+    }                 \
+  } while (0)
+  TRY(dalloc(&c->pool, nslots * g.bb));
+  if (g.dtype == FERRY_FP8_E4M3) TRY(dalloc(&c->pool_scales, nslots * 2));
+  TRY(dalloc(&c->st.fill, g.n_sets));
+  TRY(dalloc(&c->st.ord, nslots));
+  TRY(dalloc(&c->st.tag, nslots));
+  TRY(dalloc(&c->st.map, (size_t)g.n_sets * g.max_blocks));
+  // ring: worker segments sized for every miss their sets can produce
+  const int W = g.workers;
+  std::vector<uint32_t> wos(g.n_sets), cnt(W, 0), seg(W, 0), cap(W, 0);
+  for (int s = 0; s < g.n_sets; ++s) {
+    const int owner = s / (g.L * g.Hkv);
+    wos[s] = (uint32_t)((cfg->assign == FERRY_ASSIGN_AFFINITY ? owner : s) % W);
+    cnt[wos[s]]++;
+  }
+  uint64_t total = 0;
+  for (int w = 0; w < W; ++w) {
+    seg[w] = (uint32_t)total;
+    cap[w] = cnt[w] * (uint32_t)g.max_sel;
+    total += cap[w];
+  }
+  TRY(dalloc(&c->ring_entries, total));
+  TRY(dalloc(&c->ring_state, W));
+  TRY(dalloc(&c->ring_seg, W));
+  TRY(dalloc(&c->ring_cap, W));
+  TRY(dalloc(&c->worker_of_set, g.n_sets));
+  TRY(dalloc(&c->stats, kStatCount));
+  TRY(dalloc(&c->done, 1));
+  TRY(dalloc(&c->err, 1));
+#define HIPT(x)                                                                        \
+  do {                                                                                 \
+    hipError_t e_ = (x);                                                               \
+    if (e_ != hipSuccess) {                                                            \
+      release(c);                                                                      \
+      return fail(FERRY_EHIP, std::string(#x) + ": " + hipGetErrorString(e_));         \
+    }                                                                                  \
+  } while (0)
+  HIPT(hipMemcpy(c->ring_seg, seg.data(), W * 4, hipMemcpyHostToDevice));
+  HIPT(hipMemcpy(c->ring_cap, cap.data(), W * 4, hipMemcpyHostToDevice));
+  HIPT(hipMemcpy(c->worker_of_set, wos.data(), (size_t)g.n_sets * 4, hipMemcpyHostToDevice));
+  HIPT(hipMemset(c->ring_state, 0, W * 8));
+  HIPT(hipMemset(c->stats, 0, kStatCount * 8));
+  HIPT(hipMemset(c->done, 0, 4));
+  HIPT(hipMemset(c->err, 0, 4));
+  HIPT(hipMemset(c->pool, 0, nslots * g.bb));
+  // pinned host tier, mapped into the device address space
+  const size_t hbytes = (size_t)g.host_blocks * g.bb;
+  if (hipHostMalloc((void**)&c->host, hbytes, hipHostMallocMapped) != hipSuccess) {
+    c->host = nullptr;
+    release(c);
+    return fail(FERRY_ENOMEM, "hipHostMalloc of the host tier failed");
+  }
+  HIPT(hipHostGetDevicePointer((void**)&c->host_dev, c->host, 0));
+  if (g.dtype == FERRY_FP8_E4M3) {
+    if (hipHostMalloc((void**)&c->host_scales, (size_t)g.host_blocks * 8, hipHostMallocMapped) != hipSuccess) {
+      c->host_scales = nullptr;
+      release(c);
+      return fail(FERRY_ENOMEM, "hipHostMalloc of the host scales failed");
+    }
+    HIPT(hipHostGetDevicePointer((void**)&c->host_scales_dev, c->host_scales, 0));
+  }
+  hipLaunchKernelGGL(k_sets_reset, dim3(1024), dim3(256), 0, 0, g, c->st);
+  HIPT(hipGetLastError());
+  HIPT(hipDeviceSynchronize());
+#undef TRY
+#undef HIPT
+  *out = c;
+  return FERRY_OK;
+}
+
+int ferry_ctx_destroy(ferry_ctx* ctx) {
+  if (!ctx) return FERRY_OK;
+  (void)hipSetDevice(ctx->device);
+  (void)hipDeviceSynchronize();
+  release(ctx);
+  return FERRY_OK;
+}
+
+int ferry_ctx_config(const ferry_ctx* ctx, ferry_config* out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!out) return fail(FERRY_EINVAL, "null out");
+  *out = ctx->cfg;
+  out->fetch_workers = ctx->g.workers;
+  return FERRY_OK;
+}
+
+int ferry_ctx_sizes(const ferry_ctx* ctx, uint32_t* n_sets, uint32_t* max_sel,
+                    uint64_t* block_bytes, uint64_t* pool_slots) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (n_sets) *n_sets = (uint32_t)ctx->g.n_sets;
+  if (max_sel) *max_sel = (uint32_t)ctx->g.max_sel;
+  if (block_bytes) *block_bytes = ctx->g.bb;
+  if (pool_slots) *pool_slots = (uint64_t)ctx->g.n_sets * ctx->g.C;
+  return FERRY_OK;
+}
+
+int ferry_hosttier_fill(ferry_ctx* ctx, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  HIPC(hipSetDevice(ctx->device));
+  const Geo& g = ctx->g;
+  const float mult = value_mult(ctx->cfg.value_std);
+  const float mult8 = value_mult(96.0);
+  const float base = (float)((double)ctx->cfg.value_std / 96.0);
+  hipLaunchKernelGGL(k_hosttier_fill, dim3(4096), dim3(256), 0, (hipStream_t)stream, g,
+                     ctx->host_dev, ctx->host_scales_dev, ctx->cfg.host_seed, mult, mult8, base);
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_hosttier_view(ferry_ctx* ctx, void** bytes, float** scales) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (bytes) *bytes = ctx->host;
+  if (scales) *scales = ctx->host_scales;
+  return FERRY_OK;
+}
+
+int ferry_pool_view(ferry_ctx* ctx, void** pool, float** scales) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (pool) *pool = ctx->pool;
+  if (scales) *scales = ctx->pool_scales;
+  return FERRY_OK;
+}
+
+int ferry_sets_reset(ferry_ctx* ctx, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  HIPC(hipSetDevice(ctx->device));
+  hipLaunchKernelGGL(k_sets_reset, dim3(1024), dim3(256), 0, (hipStream_t)stream, ctx->g, ctx->st);
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_sets_state(ferry_ctx* ctx, uint32_t* fill, uint32_t* ord, uint32_t* tag) {
+  if (int rc = check_ctx(ctx)) return rc;
+  HIPC(hipSetDevice(ctx->device));
+  HIPC(hipDeviceSynchronize());
+  const size_t ns = (size_t)ctx->g.n_sets, nsl = ns * ctx->g.C;
+  if (fill) HIPC(hipMemcpy(fill, ctx->st.fill, ns * 4, hipMemcpyDeviceToHost));
+  if (ord) HIPC(hipMemcpy(ord, ctx->st.ord, nsl * 4, hipMemcpyDeviceToHost));
+  if (tag) HIPC(hipMemcpy(tag, ctx->st.tag, nsl * 4, hipMemcpyDeviceToHost));
+  return FERRY_OK;
+}
+
+int ferry_bookkeep_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots,
+                        uint32_t* miss_count, ferry_miss* misses, uint8_t* miss_flag,
+                        void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!sel || !slots || !miss_count || !misses) return fail(FERRY_EINVAL, "null buffer");
+  HIPC(hipSetDevice(ctx->device));
+  const Geo& g = ctx->g;
+  const int wpb = ctx->lru_wpb;
+  const dim3 grid((g.n_sets + wpb - 1) / wpb), block(64 * wpb);
+  if (ctx->cfg.lru_mode == FERRY_LRU_SERIAL)
+    hipLaunchKernelGGL(k_lru_step<true>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
+                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), ctx->err);
+  else
+    hipLaunchKernelGGL(k_lru_step<false>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
+                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), ctx->err);
+  HIPC(hipGetLastError());
+  ctx->steps++;
+  ctx->selections += (uint64_t)g.n_req * g.L * g.Hkv * g.k;
+  return FERRY_OK;
+}
+
+int ferry_missq_push(ferry_ctx* ctx, const ferry_miss* misses, uint32_t n, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (n == 0) return FERRY_OK;
+  if (!misses) return fail(FERRY_EINVAL, "null misses");
+  HIPC(hipSetDevice(ctx->device));
+  hipLaunchKernelGGL(k_missq_push, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, ctx->g,
+                     ctx->ring(), misses, n, ctx->err);
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_missq_drain(ferry_ctx* ctx, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  HIPC(hipSetDevice(ctx->device));
+  FetchArgs a;
+  a.g = ctx->g;
+  a.ring = ctx->ring();
+  a.host = ctx->host_dev;
+  a.host_scales = ctx->host_scales_dev;
+  a.pool = ctx->pool;
+  a.pool_scales = ctx->pool_scales;
+  a.steal = ctx->cfg.steal;
+  a.steal_chunk = 8;
+  a.stats = ctx->stats;
+  a.done = ctx->done;
+  a.err = ctx->err;
+  const dim3 grid(ctx->g.workers), block(256);
+  switch (ctx->g.bb / 1024) {
+    case 4: hipLaunchKernelGGL(k_fetch<4>, grid, block, 0, (hipStream_t)stream, a); break;
+    case 8: hipLaunchKernelGGL(k_fetch<8>, grid, block, 0, (hipStream_t)stream, a); break;
+    case 16: hipLaunchKernelGGL(k_fetch<16>, grid, block, 0, (hipStream_t)stream, a); break;
+    default: return fail(FERRY_EINVAL, "unsupported block size");
+  }
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_fetch_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots, uint32_t* miss_count,
+                     ferry_miss* misses, uint8_t* miss_flag, void* stream) {
+  int rc = ferry_bookkeep_step(ctx, sel, slots, miss_count, misses, miss_flag, stream);
+  if (rc) return rc;
+  return ferry_missq_drain(ctx, stream);
+}
+
+int ferry_sparse_decode(ferry_ctx* ctx, const float* q, const uint32_t* slots, float* out,
+                        void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!q || !slots || !out) return fail(FERRY_EINVAL, "null buffer");
+  HIPC(hipSetDevice(ctx->device));
+  const Geo& g = ctx->g;
+  const dim3 grid((unsigned)(g.n_req * g.L * g.Hkv)), block(256);
+  const float qscale = (float)(1.4426950408889634 / std::sqrt((double)g.D));
+  const int G = g.Hq / g.Hkv;
+  hipStream_t s = (hipStream_t)stream;
+#define ATTN(DT, GG)                                                                       \
+  hipLaunchKernelGGL((k_attn<DT, GG>), grid, block, 0, s, g, q, slots, ctx->pool,          \
+                     ctx->pool_scales, out, qscale, ctx->err)
+#define ATTN_G(DT)          \
+  switch (G) {              \
+    case 1: ATTN(DT, 1); break; \
+    case 2: ATTN(DT, 2); break; \
+    case 4: ATTN(DT, 4); break; \
+    default: ATTN(DT, 8); break; \
+  }
+  switch (g.dtype) {
+    case FERRY_F32: ATTN_G(FERRY_F32); break;
+    case FERRY_F16: ATTN_G(FERRY_F16); break;
+    case FERRY_BF16: ATTN_G(FERRY_BF16); break;
+    default: ATTN_G(FERRY_FP8_E4M3); break;
+  }
+#undef ATTN_G
+#undef ATTN
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_stats_get(ferry_ctx* ctx, ferry_stats* out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!out) return fail(FERRY_EINVAL, "null out");
+  HIPC(hipSetDevice(ctx->device));
+  HIPC(hipDeviceSynchronize());
+  unsigned long long s[kStatCount];
+  int err = 0;
+  HIPC(hipMemcpy(s, ctx->stats, sizeof(s), hipMemcpyDeviceToHost));
+  HIPC(hipMemcpy(&err, ctx->err, 4, hipMemcpyDeviceToHost));
+  std::memset(out, 0, sizeof(*out));
+  out->steps = ctx->steps;
+  out->selections = ctx->selections;
+  out->misses = s[kStatMisses];
+  out->fetched_bytes = s[kStatBytes];
+  out->steals = s[kStatSteals];
+  out->stolen = s[kStatStolen];
+  out->last_misses = s[kStatLast];
+  out->device_error = err;
+  return FERRY_OK;
+}
+
+int ferry_stats_reset(ferry_ctx* ctx) {
+  if (int rc = check_ctx(ctx)) return rc;
+  HIPC(hipSetDevice(ctx->device));
+  HIPC(hipDeviceSynchronize());
+  HIPC(hipMemset(ctx->stats, 0, kStatCount * 8));
+  HIPC(hipMemset(ctx->err, 0, 4));
+  ctx->steps = ctx->selections = 0;
+  return FERRY_OK;
+}
+
+int ferry_queue_selftest(int device, uint64_t capacity, uint64_t n_tasks, int producers,
+                         int consumers, int mode, uint64_t* popped, uint64_t* duplicates,
+                         float* ms) {
+  if (producers < 256 || consumers < 256 || producers % 256 || consumers % 256)
+    return fail(FERRY_EINVAL, "producers/consumers must be positive multiples of 256");
+  if (producers + consumers > 8192) return fail(FERRY_EINVAL, "at most 8192 threads (co-residency)");
+  if (n_tasks == 0 || n_tasks % (uint64_t)producers) return fail(FERRY_EINVAL, "n_tasks must be a multiple of producers");
+  if (n_tasks > (1ull << 28)) return fail(FERRY_EINVAL, "n_tasks too large");
+  if (mode != 0 && mode != 1) return fail(FERRY_EINVAL, "bad mode");
+  HIPC(hipSetDevice(device));
+  ferry::GPUBoundedQueue q(capacity, mode ? ferry::ReservationMode::kWaveBatched
+                                          : ferry::ReservationMode::kPerThread);
+  if (!q.ok()) return fail(FERRY_ENOMEM, "queue allocation failed");
+  uint32_t* seen = nullptr;
+  unsigned long long* counters = nullptr;
+  int* flags = nullptr;
+  HIPC(hipMalloc(&seen, n_tasks * 4));
+  HIPC(hipMalloc(&counters, 16));
+  HIPC(hipMalloc(&flags, 8));
+  HIPC(hipMemset(seen, 0, n_tasks * 4));
+  HIPC(hipMemset(counters, 0, 16));
+  HIPC(hipMemset(flags, 0, 8));
+  hipEvent_t e0, e1;
+  HIPC(hipEventCreate(&e0));
+  HIPC(hipEventCreate(&e1));
+  const uint32_t pb = producers / 256, cb = consumers / 256;
+  HIPC(hipEventRecord(e0, 0));
+  hipLaunchKernelGGL(k_queue_pc, dim3(pb + cb), dim3(256), 0, 0, q.device_ptr(),
+                     n_tasks / (uint64_t)producers, pb, seen, counters, counters + 1, flags, flags + 1,
+                     q.mode());
+  HIPC(hipGetLastError());
+  HIPC(hipEventRecord(e1, 0));
+  HIPC(hipEventSynchronize(e1));
+  float t = 0.0f;
+  HIPC(hipEventElapsedTime(&t, e0, e1));
+  unsigned long long c[2];
+  HIPC(hipMemcpy(c, counters, 16, hipMemcpyDeviceToHost));
+  // every id must have arrived exactly once
+  std::vector<uint32_t> h(n_tasks);
+  HIPC(hipMemcpy(h.data(), seen, n_tasks * 4, hipMemcpyDeviceToHost));
+  uint64_t missing = 0;
+  for (uint32_t v : h) missing += v == 0;
+  const auto snap = q.snapshot();
+  (void)hipFree(seen);
+  (void)hipFree(counters);
+  (void)hipFree(flags);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (popped) *popped = c[0];
+  if (duplicates) *duplicates = c[1];
+  if (ms) *ms = t;
+  if (snap.status) return fail(FERRY_ESPIN, "queue wait bound exceeded (status " + std::to_string(snap.status) + ")");
+  if (missing) return fail(FERRY_ESTATE, std::to_string(missing) + " task ids never popped");
+  return FERRY_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,205 @@
+// selgen.cpp -- synthetic selection streams (host side of the workload).
+//
+// ferry_selgen_*: the executor's workloads.  For every (request r, layer l,
+// kv head h) a step keeps each block of r's previous selection with
+// probability `reuse` (inter-step locality, the knob of the reference's
+// generator, src/workloads/missstream.cuh:127-128), then completes the
+// selection to k distinct blocks with popularity-rank draws (Zipf(s) or
+// uniform) mapped through an owner-shared affine permutation and rejected when
+// outside r's context or already taken.  The k blocks are sorted (top-k page
+// indices are sorted, tools/capture_miss_trace.py:158-159) and group members'
+// private blocks are renamed into the set's id space after the shared prefix.
+// Every draw is a counter-based hash of (seed, step, r, l, h, draw index), so
+// requests are generated independently in parallel.
+//
+// ferry_refgen_selections: the selection half of replay_miss_stream
+// (src/workloads/missstream.cuh:104-133) with std::mt19937_64.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <random>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/ferry_amd.h"
+
+namespace {
+
+uint64_t mix64(uint64_t seed, uint64_t idx) {
+  uint64_t z = seed + idx * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+constexpr uint64_t kSaltCtx = 0x43545842ull;
+constexpr uint64_t kSaltSel = 0x53454C31ull;
+constexpr uint64_t kSaltPerm = 0x5045524Dull;
+constexpr uint64_t kSaltKeep = 0x4B454550ull;
+constexpr uint64_t kPermPrime = 1000003ull;
+constexpr int kDrawLimit = 65536;
+
+}  // namespace
+
+struct ferry_selgen {
+  ferry_selgen_config cfg;
+  std::vector<int32_t> ctx;
+  std::vector<int32_t> nperm;  // per owner: largest member context
+  std::vector<double> cum;     // Zipf cumulative weights of ranks 0..nmax-1
+  std::vector<uint32_t> state; // previous logical selection per (r, l, h)
+  int nmax = 0;
+  int max_blocks = 0;
+};
+
+extern "C" {
+
+int ferry_ctx_uniform(uint64_t seed, int32_t n_req, int32_t lo, int32_t hi, int32_t* out) {
+  if (n_req < 0 || hi < lo || !out) return FERRY_EINVAL;
+  const uint64_t span = (uint64_t)(hi - lo + 1);
+  for (int r = 0; r < n_req; ++r) out[r] = lo + (int32_t)(mix64(seed ^ kSaltCtx, (uint64_t)r) % span);
+  return FERRY_OK;
+}
+
+int ferry_selgen_create(const ferry_selgen_config* cfg, const int32_t* ctx_blocks, ferry_selgen** out) {
+  if (!cfg || !ctx_blocks || !out) return FERRY_EINVAL;
+  if (cfg->n_req < 1 || cfg->group < 1 || cfg->n_layers < 1 || cfg->kv_heads < 1 || cfg->k < 1 ||
+      cfg->reuse < 0.0 || cfg->reuse > 1.0 || cfg->prefix_blocks < 0)
+    return FERRY_EINVAL;
+  ferry_selgen* g = new ferry_selgen();
+  g->cfg = *cfg;
+  g->ctx.assign(ctx_blocks, ctx_blocks + cfg->n_req);
+  for (int r = 0; r < cfg->n_req; ++r) {
+    if (g->ctx[r] < cfg->k || g->ctx[r] >= (int)kPermPrime) {
+      delete g;
+      return FERRY_EINVAL;
+    }
+    g->nmax = std::max(g->nmax, g->ctx[r]);
+  }
+  const int nown = (cfg->n_req + cfg->group - 1) / cfg->group;
+  g->nperm.assign(nown, 0);
+  for (int r = 0; r < cfg->n_req; ++r) g->nperm[r / cfg->group] = std::max(g->nperm[r / cfg->group], g->ctx[r]);
+  for (int o = 0; o < nown; ++o) {
+    const int np = g->nperm[o];
+    const int pre = std::min(cfg->prefix_blocks, np);
+    g->max_blocks = std::max(g->max_blocks, pre + cfg->group * (np - pre));
+  }
+  if (cfg->dist == 1) {
+    g->cum.resize(g->nmax);
+    double acc = 0.0;
+    for (int i = 0; i < g->nmax; ++i) {
+      acc += std::pow((double)(i + 1), -cfg->zipf_s);
+      g->cum[i] = acc;
+    }
+  }
+  g->state.assign((size_t)cfg->n_req * cfg->n_layers * cfg->kv_heads * cfg->k, 0u);
+  *out = g;
+  return FERRY_OK;
+}
+
+int ferry_selgen_destroy(ferry_selgen* g) {
+  delete g;
+  return FERRY_OK;
+}
+
+int ferry_selgen_max_blocks(const ferry_selgen* g, int32_t* out) {
+  if (!g || !out) return FERRY_EINVAL;
+  *out = g->max_blocks;
+  return FERRY_OK;
+}
+
+int ferry_selgen_step(ferry_selgen* g, int32_t step, uint32_t* out) {
+  if (!g || !out || step < 0) return FERRY_EINVAL;
+  const ferry_selgen_config& c = g->cfg;
+  const int L = c.n_layers, H = c.kv_heads, k = c.k;
+  const uint64_t keep_thr = (uint64_t)(c.reuse * 4294967296.0);
+  const bool carry = step > 0 && c.reuse > 0.0;
+  int nthreads = (int)std::min<unsigned>(16u, std::max(1u, std::thread::hardware_concurrency()));
+  nthreads = std::min(nthreads, c.n_req);
+  std::vector<int> rc(nthreads, 0);
+  auto work = [&](int tid) {
+    std::vector<uint8_t> taken(g->nmax, 0);
+    for (int r = tid; r < c.n_req; r += nthreads) {
+      const int o = r / c.group, m = r % c.group;
+      const int nr = g->ctx[r];
+      const int np = g->nperm[o];
+      const int pre = std::min(c.prefix_blocks, np);
+      for (int l = 0; l < L; ++l)
+        for (int h = 0; h < H; ++h) {
+          const size_t row = ((size_t)(r * L + l) * H + h) * k;
+          uint32_t* st = g->state.data() + row;
+          uint32_t* so = out + row;
+          const uint64_t off = mix64(c.seed ^ kSaltPerm, (uint64_t)((o * L + l) * H + h)) % (uint64_t)np;
+          const uint64_t base =
+              ((((uint64_t)step * (uint64_t)c.n_req + (uint64_t)r) * (uint64_t)L + (uint64_t)l) *
+                   (uint64_t)H + (uint64_t)h) * (uint64_t)kDrawLimit;
+          int got = 0;
+          if (carry)
+            for (int j = 0; j < k; ++j)
+              if ((mix64(c.seed ^ kSaltKeep, base + (uint64_t)j) >> 32) < keep_thr) {
+                so[got++] = st[j];
+                taken[st[j]] = 1;
+              }
+          for (int i = 0; i < kDrawLimit && got < k; ++i) {
+            const uint64_t u = mix64(c.seed ^ kSaltSel, base + (uint64_t)i);
+            uint64_t rank;
+            if (c.dist == 1) {
+              const double thr = (double)(u >> 11) * (1.0 / 9007199254740992.0) * g->cum[np - 1];
+              rank = (uint64_t)(std::upper_bound(g->cum.begin(), g->cum.begin() + np, thr) - g->cum.begin());
+            } else {
+              rank = ((u >> 32) * (uint64_t)np) >> 32;
+            }
+            const uint64_t b = (rank * kPermPrime + off) % (uint64_t)np;
+            if (b >= (uint64_t)nr || taken[b]) continue;
+            taken[b] = 1;
+            so[got++] = (uint32_t)b;
+          }
+          for (int j = 0; j < got; ++j) taken[so[j]] = 0;
+          if (got < k) {
+            rc[tid] = FERRY_ESTATE;
+            return;
+          }
+          std::sort(so, so + k);
+          std::memcpy(st, so, (size_t)k * 4);
+          for (int j = 0; j < k; ++j)
+            if (so[j] >= (uint32_t)pre)
+              so[j] = (uint32_t)pre + (uint32_t)m * (uint32_t)(np - pre) + (so[j] - (uint32_t)pre);
+        }
+    }
+  };
+  std::vector<std::thread> th;
+  for (int t = 1; t < nthreads; ++t) th.emplace_back(work, t);
+  work(0);
+  for (auto& t : th) t.join();
+  for (int v : rc)
+    if (v) return v;
+  return FERRY_OK;
+}
+
+int ferry_refgen_selections(int32_t R, int32_t L, int32_t S, int32_t sel, uint64_t seed, uint32_t* out) {
+  if (R < 1 || L < 1 || S < 1 || sel < 1 || !out) return FERRY_EINVAL;
+  std::mt19937_64 rng(seed);
+  std::vector<std::vector<uint32_t>> prev((size_t)R * L);
+  size_t ev = 0;
+  for (int r = 0; r < R; ++r)
+    for (int s = 0; s < S; ++s) {
+      const uint64_t hist = 64 + (uint64_t)s * 8;
+      for (int l = 0; l < L; ++l) {
+        auto& pv = prev[(size_t)r * L + l];
+        std::vector<uint32_t> cur(sel);
+        for (int i = 0; i < sel; ++i) {
+          uint64_t blk;
+          if (!pv.empty() && (double)(rng() % 1000) / 1000.0 < 0.66)
+            blk = pv[rng() % pv.size()];
+          else
+            blk = rng() % hist;
+          cur[i] = (uint32_t)blk;
+          out[ev++] = (uint32_t)blk;
+        }
+        pv.swap(cur);
+      }
+    }
+  return FERRY_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,233 @@
+/*
+ * ferry_amd.h -- C-ABI of the MI355X-native sparse KV miss-stream executor.
+ *
+ * One GPU, one process.  Every entry point takes plain pointers and sizes;
+ * device buffers are caller-owned unless stated; every call that launches
+ * work takes an explicit hipStream_t (passed as void*, 0 = null stream).
+ * Every function returns an int status (FERRY_OK == 0, negative on error) and
+ * never exits the process; the reference aborted instead
+ * (src/common/cuda_check.cuh:9-28, src/workloads/miss_trace.cuh:64-71).
+ *
+ * The reference exposes this path as header-only C++ (namespace ferry) with
+ * no FFI; each entry point below names the reference interface it replaces.
+ * Reference paths are relative to the clearleo126/ferry source tree.
+ */
+#ifndef FERRY_AMD_H
+#define FERRY_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define FERRY_OK 0
+#define FERRY_EINVAL (-1)    /* invalid argument or configuration */
+#define FERRY_EHIP (-2)      /* HIP runtime error (see ferry_last_error) */
+#define FERRY_ERANGE (-3)    /* a selected block id >= max_blocks */
+#define FERRY_ECAPACITY (-4) /* a step selects more distinct blocks than a set can hold */
+#define FERRY_ENOMEM (-5)    /* device or pinned host allocation failed */
+#define FERRY_ESPIN (-6)     /* a bounded device wait ran out (queue protocol) */
+#define FERRY_ESTATE (-7)    /* inconsistent set state detected on device */
+
+/* ---- KV element types ---- */
+#define FERRY_F32 0
+#define FERRY_F16 1
+#define FERRY_BF16 2
+#define FERRY_FP8_E4M3 3 /* OCP E4M3FN + one fp32 scale per block for K and V */
+
+/* ---- LRU granularity ---- */
+#define FERRY_LRU_STEP 0   /* one batched update per decode step (executor rule) */
+#define FERRY_LRU_SERIAL 1 /* one update per selection: replay_miss_stream/kv_touch */
+
+/* ---- miss -> fetch-worker assignment ---- */
+#define FERRY_ASSIGN_SPREAD 0   /* set id modulo workers */
+#define FERRY_ASSIGN_AFFINITY 1 /* request (owner) modulo workers */
+
+/* Geometry and policy of one executor.  Sets are (owner, layer, kv head)
+ * with owner = request / group; each set owns slots_per_set slots of the HBM
+ * pool.  Replaces MissSpec (src/workloads/missstream.cuh:23-76) widened from
+ * (request, layer, 4-token all-head block) to (request, layer, head,
+ * block_tokens block). */
+typedef struct ferry_config {
+  int32_t n_req;         /* decode batch B */
+  int32_t group;         /* requests per owner (prefix group); 1 = private sets */
+  int32_t n_layers;      /* L */
+  int32_t kv_heads;      /* Hkv */
+  int32_t q_heads;       /* Hq (multiple of Hkv) */
+  int32_t head_dim;      /* D (128) */
+  int32_t block_tokens;  /* tokens per block (16) */
+  int32_t k;             /* selected blocks per (request, layer, kv head) */
+  int32_t slots_per_set; /* HBM slots per set */
+  int32_t max_blocks;    /* block ids of a set are < max_blocks */
+  int32_t dtype;         /* FERRY_F32 .. FERRY_FP8_E4M3 */
+  int32_t lru_mode;      /* FERRY_LRU_STEP or FERRY_LRU_SERIAL */
+  uint64_t host_blocks;  /* host-tier capacity in blocks (aliased modulo) */
+  uint64_t host_seed;    /* host-tier content seed */
+  float value_std;       /* standard deviation of K/V values */
+  int32_t fetch_workers; /* persistent fetch workgroups; 0 = 2 per CU */
+  int32_t steal;         /* 1 = fetch workers steal from each other */
+  int32_t assign;        /* FERRY_ASSIGN_SPREAD or FERRY_ASSIGN_AFFINITY */
+} ferry_config;
+
+/* One fetched block: written per set in miss order. */
+typedef struct ferry_miss {
+  uint32_t block;   /* block id fetched */
+  uint32_t slot;    /* local slot in the set, [0, slots_per_set) */
+  uint32_t evicted; /* block id evicted from that slot, 0xFFFFFFFF if none */
+  uint32_t set;     /* set id = (owner * n_layers + layer) * kv_heads + head */
+} ferry_miss;
+
+/* Counters; replaces WlAStats / WlaMultiStats (src/workloads/kv_exec.cuh:39-45,
+ * src/runtime/wla_multigpu.cuh:177-233). */
+typedef struct ferry_stats {
+  uint64_t steps;          /* fetch steps run */
+  uint64_t selections;     /* selections processed */
+  uint64_t misses;         /* unique blocks fetched (refill events of 1 block) */
+  uint64_t fetched_bytes;  /* host-tier bytes moved into the pool */
+  uint64_t steals;         /* successful steals between fetch workers */
+  uint64_t stolen;         /* misses moved by steals */
+  uint64_t last_misses;    /* misses of the most recent step */
+  int32_t device_error;    /* first device-side error (FERRY_E*), 0 if none */
+  int32_t pad;
+} ferry_stats;
+
+typedef struct ferry_ctx ferry_ctx;
+
+/* Text of the last error on this thread (never NULL). */
+const char* ferry_last_error(void);
+/* Library version string. */
+const char* ferry_version(void);
+
+/* Create an executor on `device`: allocates the HBM slot pool, the per-set
+ * LRU state, the miss ring and the pinned host tier.  Replaces the
+ * allocations inside run_miss_workload (src/workloads/kv_exec.cuh:78-99) and
+ * WlaMultiGpuCtx (src/runtime/wla_multigpu.cuh:435-623). */
+int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out);
+int ferry_ctx_destroy(ferry_ctx* ctx);
+int ferry_ctx_config(const ferry_ctx* ctx, ferry_config* out);
+/* Sizes: n_sets, max selections per set, block bytes (K+V, no scales),
+ * pool slots. */
+int ferry_ctx_sizes(const ferry_ctx* ctx, uint32_t* n_sets, uint32_t* max_sel,
+                    uint64_t* block_bytes, uint64_t* pool_slots);
+
+/* Fill the pinned host tier with its deterministic content (K then V,
+ * [block_tokens][head_dim] each; fp8 adds two fp32 scales per block).  The
+ * reference fills its slab with uniform halves (src/workloads/kv_exec.cuh:78-86)
+ * or a tile (src/runtime/wla_multigpu.cuh:532-544). */
+int ferry_hosttier_fill(ferry_ctx* ctx, void* stream);
+/* Host pointers of the pinned tier (bytes: host_blocks*block_bytes; scales:
+ * host_blocks*2 floats, NULL unless fp8). */
+int ferry_hosttier_view(ferry_ctx* ctx, void** bytes, float** scales);
+/* Device pointers of the HBM pool (slot-major, block_bytes per slot) and its
+ * scales (2 floats per slot, NULL unless fp8). */
+int ferry_pool_view(ferry_ctx* ctx, void** pool, float** scales);
+
+/* Forget every resident block (all sets empty).  Replaces
+ * GPUBoundedQueue::reset + cache re-init (src/queue/gpu_bounded_queue.cuh:176-181). */
+int ferry_sets_reset(ferry_ctx* ctx, void* stream);
+/* Copy per-set LRU state to host arrays: fill[n_sets], ord[n_sets][slots]
+ * (local slots, LRU first), tag[n_sets][slots] (block per slot). */
+int ferry_sets_state(ferry_ctx* ctx, uint32_t* fill, uint32_t* ord, uint32_t* tag);
+
+/* One decode step of bookkeeping + miss fetch:
+ *   sel        [B][L][Hkv][k] set block ids (device, u32)
+ *   slots      [B][L][Hkv][k] out: pool slot of each selection (device, u32)
+ *   miss_count [n_sets] out: misses per set (device, u32)
+ *   misses     [n_sets][max_sel] out: fetched blocks per set in miss order
+ *   miss_flag  [B][L][Hkv][k] out, optional (NULL): 1 where the selection
+ *              missed (first toucher), else 0
+ * dedups, assigns and evicts slots by LRU, pushes the misses onto the device
+ * miss ring and drains it with persistent fetch workgroups that read the host
+ * tier directly (16-byte loads over the host link) into the HBM pool.
+ * Replaces run_miss_workload mode C (src/workloads/kv_exec.cuh:188-292) and
+ * the exec_step C engine + kv_touch (src/runtime/wla_multigpu.cuh:2527-2604,
+ * 1937-1962). */
+int ferry_fetch_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots,
+                     uint32_t* miss_count, ferry_miss* misses,
+                     uint8_t* miss_flag, void* stream);
+
+/* The two halves of ferry_fetch_step, for callers that place them on
+ * different streams or interpose work.  ferry_bookkeep_step leaves the
+ * misses queued on the device miss ring; ferry_missq_drain fetches them. */
+int ferry_bookkeep_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots,
+                        uint32_t* miss_count, ferry_miss* misses,
+                        uint8_t* miss_flag, void* stream);
+/* Queue n externally built misses (device array) onto the ring.  Replaces
+ * dq_push producers of GPUBoundedQueue (src/queue/gpu_bounded_queue.cuh:70-126). */
+int ferry_missq_push(ferry_ctx* ctx, const ferry_miss* misses, uint32_t n,
+                     void* stream);
+/* Drain the ring: persistent workgroups pop their own deque and steal from
+ * the fullest peer's tail.  Replaces HostStagedChannel::submit/sync
+ * (src/comm/host_staged_channel.cpp:43-87) and the cross-GPU steal rules
+ * (src/runtime/wla_multigpu.cuh:1147-1152, 1518-1526). */
+int ferry_missq_drain(ferry_ctx* ctx, void* stream);
+
+/* Block-sparse decode attention over the selected blocks:
+ *   q     [B][L][Hq][D] fp32 (device)
+ *   slots [B][L][Hkv][k] pool slots from ferry_fetch_step (device)
+ *   out   [B][L][Hq][D] fp32 (device)
+ * softmax(q K^T / sqrt(D)) V over every token of the k blocks, fp32
+ * accumulation, online softmax.  Replaces the FMA proxy attn_kernel /
+ * wla_attn_kernel (src/workloads/kv_exec.cuh:30-37,
+ * src/runtime/wla_multigpu.cuh:96-103). */
+int ferry_sparse_decode(ferry_ctx* ctx, const float* q, const uint32_t* slots,
+                        float* out, void* stream);
+
+/* Counters (synchronises the device). */
+int ferry_stats_get(ferry_ctx* ctx, ferry_stats* out);
+int ferry_stats_reset(ferry_ctx* ctx);
+
+/* ---- device queue self-test (bench_queue equivalent) ----
+ * Producers push n_tasks unique ids through the MPMC ring (dq_push), consumers
+ * pop them (dq_pop) and mark a seen[] map; returns popped count and duplicate
+ * flag.  mode: 0 per-thread reservation, 1 wave-batched (64-slot) reservation.
+ * Replaces pc_kernel/run_once (src/benches/bench_queue.cu:26-123). */
+int ferry_queue_selftest(int device, uint64_t capacity, uint64_t n_tasks,
+                         int producers, int consumers, int mode,
+                         uint64_t* popped, uint64_t* duplicates, float* ms);
+
+/* ---- synthetic workload generator (host) ----
+ * Stateful per-(request, layer, kv head) top-k selection: keep each previous
+ * block with probability `reuse`, complete to k distinct blocks by Zipf(s)
+ * (or uniform) popularity draws over an owner-shared permutation.  The
+ * reference's generator is replay_miss_stream (src/workloads/missstream.cuh:
+ * 104-170); ferry_refgen_* below reproduces that one exactly. */
+typedef struct ferry_selgen_config {
+  int32_t n_req, group, n_layers, kv_heads, k;
+  int32_t dist;          /* 0 uniform, 1 Zipf */
+  double zipf_s;
+  double reuse;
+  int32_t prefix_blocks; /* blocks shared by a group (ids [0, prefix)) */
+  int32_t pad;
+  uint64_t seed;
+} ferry_selgen_config;
+typedef struct ferry_selgen ferry_selgen;
+/* ctx_blocks: per-request context length in blocks (copied). */
+int ferry_selgen_create(const ferry_selgen_config* cfg, const int32_t* ctx_blocks,
+                        ferry_selgen** out);
+int ferry_selgen_destroy(ferry_selgen* g);
+/* Set block-id bound (use as ferry_config.max_blocks). */
+int ferry_selgen_max_blocks(const ferry_selgen* g, int32_t* out);
+/* Generate step `step` (steps must be generated in order) into host array
+ * out [B][L][Hkv][k]. */
+int ferry_selgen_step(ferry_selgen* g, int32_t step, uint32_t* out);
+/* Per-request context lengths uniform in [lo, hi] blocks. */
+int ferry_ctx_uniform(uint64_t seed, int32_t n_req, int32_t lo, int32_t hi,
+                      int32_t* out);
+
+/* Reference generator: the selections replay_miss_stream draws
+ * (src/workloads/missstream.cuh:104-133, std::mt19937_64(seed)) for
+ * R requests x S steps x L layers x sel, in the reference's (r, s, l, k)
+ * event order, as u32 block ids in out[R*S*L*sel].  The hit/miss flags are
+ * not produced here: run them through ferry_fetch_step with
+ * FERRY_LRU_SERIAL, group 1, kv_heads 1, k = sel, slots_per_set = hot. */
+int ferry_refgen_selections(int32_t R, int32_t L, int32_t S, int32_t sel,
+                            uint64_t seed, uint32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,1044 @@
+/*
+ * oracle.c -- CPU restatement of the per-GPU sparse KV miss-stream executor.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker).  Loaded by tests/, by
+ * __graft_entry__.smoke() and by the cpu_baseline leg of bench.py; never by
+ * the product.  See oracle.h for the map of functions to reference files.
+ * Paths in citations are relative to the clearleo126/ferry source tree.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math, so the
+ * float and double arithmetic below is plain IEEE and reproducible).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ */
+/* primitives                                                          */
+/* ------------------------------------------------------------------ */
+
+/* splitmix64 finaliser (Vigna) applied to seed + idx * golden gamma: the
+ * counter-based hash every synthetic draw in the executor derives from. */
+uint64_t ora_mix64(uint64_t seed, uint64_t idx) {
+  uint64_t z = seed + idx * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+static uint32_t f32_bits(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  return u;
+}
+static float bits_f32(uint32_t u) {
+  float x;
+  memcpy(&x, &u, 4);
+  return x;
+}
+
+/* IEEE binary32 -> binary16, round to nearest even, overflow to inf. */
+uint16_t ora_f32_to_f16(float x) {
+  uint32_t u = f32_bits(x);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  uint32_t exp = (u >> 23) & 0xFFu;
+  uint32_t man = u & 0x7FFFFFu;
+  if (exp == 0xFFu) return sign | 0x7C00u | (man ? 0x200u : 0u);
+  int e = (int)exp - 127 + 15;
+  if (e >= 31) return sign | 0x7C00u;
+  if (e <= 0) {
+    if (e < -10) return sign;
+    /* subnormal: shift the implicit-one mantissa right, RNE */
+    uint32_t m = man | 0x800000u;
+    int shift = 14 - e; /* 14..24 */
+    uint32_t q = m >> shift;
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return sign | (uint16_t)q;
+  }
+  uint32_t q = ((uint32_t)e << 10) | (man >> 13);
+  uint32_t rem = man & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++; /* may carry into exp */
+  return sign | (uint16_t)q;
+}
+
+float ora_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1Fu;
+  uint32_t man = h & 0x3FFu;
+  if (exp == 0) {
+    float v = (float)man * (1.0f / 16777216.0f); /* man * 2^-24 */
+    return sign ? -v : v;
+  }
+  if (exp == 31) return bits_f32(sign | 0x7F800000u | (man << 13));
+  return bits_f32(sign | ((exp - 15 + 127) << 23) | (man << 13));
+}
+
+uint16_t ora_f32_to_bf16(float x) {
+  uint32_t u = f32_bits(x);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x7FFFFFu))
+    return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float ora_bf16_to_f32(uint16_t h) { return bits_f32((uint32_t)h << 16); }
+
+/* binary32 -> OCP FP8 E4M3 (E4M3FN: bias 7, no infinities, NaN = S.1111.111,
+ * max finite 448), round to nearest even, saturating to +-448. */
+uint8_t ora_f32_to_e4m3(float x) {
+  uint32_t u = f32_bits(x);
+  uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+  uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return sign | 0x7Fu;      /* NaN */
+  if (bits_f32(a) >= 464.0f) return sign | 0x7Eu; /* saturate to 448 */
+  int e = (int)(a >> 23) - 127;
+  if (e < -6) {
+    /* subnormal grid: multiples of 2^-9 (8 == smallest normal 0x08) */
+    float n = rintf(bits_f32(a) * 512.0f);
+    return sign | (uint8_t)n;
+  }
+  uint32_t man = a & 0x7FFFFFu;
+  uint32_t q = man >> 20;
+  uint32_t rem = man & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) q++;
+  if (q == 8u) {
+    q = 0;
+    e++;
+  }
+  return sign | (uint8_t)(((uint32_t)(e + 7) << 3) | q);
+}
+
+float ora_e4m3_to_f32(uint8_t v) {
+  int sign = v & 0x80;
+  int exp = (v >> 3) & 0xF;
+  int man = v & 0x7;
+  float r;
+  if (exp == 0xF && man == 0x7) return NAN;
+  if (exp == 0)
+    r = (float)man * (1.0f / 512.0f);
+  else
+    r = ldexpf(1.0f + (float)man / 8.0f, exp - 7);
+  return sign ? -r : r;
+}
+
+double ora_decode(int dtype, uint32_t v) {
+  switch (dtype) {
+    case ORA_F32: return (double)bits_f32(v);
+    case ORA_F16: return (double)ora_f16_to_f32((uint16_t)v);
+    case ORA_BF16: return (double)ora_bf16_to_f32((uint16_t)v);
+    default: return (double)ora_e4m3_to_f32((uint8_t)v);
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* mt19937_64 (Matsumoto-Nishimura 64-bit MT; C++ [rand.predef]).      */
+/* replay_miss_stream seeds std::mt19937_64 (missstream.cuh:106).      */
+/* ------------------------------------------------------------------ */
+#define MT_N 312
+#define MT_M 156
+#define MT_UPPER 0xFFFFFFFF80000000ull
+#define MT_LOWER 0x7FFFFFFFull
+
+void ora_mt64_seed(ora_mt64* g, uint64_t seed) {
+  g->mt[0] = seed;
+  for (int i = 1; i < MT_N; ++i)
+    g->mt[i] = 6364136223846793005ull * (g->mt[i - 1] ^ (g->mt[i - 1] >> 62)) +
+               (uint64_t)i;
+  g->idx = MT_N;
+}
+
+uint64_t ora_mt64_next(ora_mt64* g) {
+  static const uint64_t mag[2] = {0ull, 0xB5026F5AA96619E9ull};
+  if (g->idx >= MT_N) {
+    int i;
+    uint64_t x;
+    for (i = 0; i < MT_N - MT_M; ++i) {
+      x = (g->mt[i] & MT_UPPER) | (g->mt[i + 1] & MT_LOWER);
+      g->mt[i] = g->mt[i + MT_M] ^ (x >> 1) ^ mag[x & 1ull];
+    }
+    for (; i < MT_N - 1; ++i) {
+      x = (g->mt[i] & MT_UPPER) | (g->mt[i + 1] & MT_LOWER);
+      g->mt[i] = g->mt[i + (MT_M - MT_N)] ^ (x >> 1) ^ mag[x & 1ull];
+    }
+    x = (g->mt[MT_N - 1] & MT_UPPER) | (g->mt[0] & MT_LOWER);
+    g->mt[MT_N - 1] = g->mt[MT_M - 1] ^ (x >> 1) ^ mag[x & 1ull];
+    g->idx = 0;
+  }
+  uint64_t y = g->mt[g->idx++];
+  y ^= (y >> 29) & 0x5555555555555555ull;
+  y ^= (y << 17) & 0x71D67FFFEDA60000ull;
+  y ^= (y << 37) & 0xFFF7EEE000000000ull;
+  y ^= y >> 43;
+  return y;
+}
+
+/* ------------------------------------------------------------------ */
+/* reference replay: missstream.cuh:104-170                            */
+/* ------------------------------------------------------------------ */
+int ora_ref_replay(int R, int L, int S, int sel, int hot, uint64_t seed,
+                   uint64_t* blocks, uint8_t* miss, uint64_t* counts) {
+  if (R <= 0 || L <= 0 || S <= 0 || sel <= 0 || hot <= 0) return -1;
+  ora_mt64 rng;
+  ora_mt64_seed(&rng, seed);
+  const size_t nrl = (size_t)R * L;
+  /* per (r, l): deque of cached blocks (array, front = index 0), previous
+   * step's selection */
+  uint64_t* dq = (uint64_t*)malloc(nrl * (size_t)hot * sizeof(uint64_t));
+  int* dq_n = (int*)calloc(nrl, sizeof(int));
+  uint64_t* prev = (uint64_t*)malloc(nrl * (size_t)sel * sizeof(uint64_t));
+  int* prev_n = (int*)calloc(nrl, sizeof(int));
+  uint64_t* cur = (uint64_t*)malloc((size_t)sel * sizeof(uint64_t));
+  if (!dq || !dq_n || !prev || !prev_n || !cur) return -2;
+  uint64_t selects = 0, misses = 0;
+  size_t ev = 0;
+  for (int r = 0; r < R; ++r) {
+    for (int s = 0; s < S; ++s) {
+      const uint64_t hist_blocks = 64 + (uint64_t)s * 8; /* :118 */
+      for (int l = 0; l < L; ++l) {
+        const size_t rl = (size_t)r * L + l;
+        uint64_t* d = dq + rl * (size_t)hot;
+        uint64_t* pv = prev + rl * (size_t)sel;
+        const int pn = prev_n[rl];
+        for (int i = 0; i < sel; ++i) { /* :125-133 */
+          uint64_t blk;
+          if (pn > 0 && (double)(ora_mt64_next(&rng) % 1000) / 1000.0 < 0.66)
+            blk = pv[ora_mt64_next(&rng) % (uint64_t)pn];
+          else
+            blk = ora_mt64_next(&rng) % hist_blocks;
+          cur[i] = blk;
+        }
+        for (int i = 0; i < sel; ++i) { /* :137-161 */
+          const uint64_t blk = cur[i];
+          ++selects;
+          int pos = -1;
+          for (int j = 0; j < dq_n[rl]; ++j)
+            if (d[j] == blk) {
+              pos = j;
+              break;
+            }
+          const int hit = pos >= 0;
+          if (blocks) blocks[ev] = blk;
+          if (miss) miss[ev] = (uint8_t)!hit;
+          ++ev;
+          if (hit) {
+            memmove(d + pos, d + pos + 1,
+                    (size_t)(dq_n[rl] - pos - 1) * sizeof(uint64_t));
+            d[dq_n[rl] - 1] = blk;
+          } else {
+            ++misses;
+            if (dq_n[rl] >= hot) {
+              memmove(d, d + 1, (size_t)(dq_n[rl] - 1) * sizeof(uint64_t));
+              dq_n[rl]--;
+            }
+            d[dq_n[rl]++] = blk;
+          }
+        }
+        memcpy(pv, cur, (size_t)sel * sizeof(uint64_t)); /* :162 */
+        prev_n[rl] = sel;
+      }
+    }
+  }
+  if (counts) {
+    counts[0] = selects;
+    counts[1] = misses;
+  }
+  free(dq);
+  free(dq_n);
+  free(prev);
+  free(prev_n);
+  free(cur);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* reference C-mode refill planner: kv_exec.cuh:188-292               */
+/* ------------------------------------------------------------------ */
+typedef struct {
+  int layer;
+  uint64_t block;
+} ref_missref;
+
+static int cmp_missref(const void* a, const void* b) {
+  const ref_missref* x = (const ref_missref*)a;
+  const ref_missref* y = (const ref_missref*)b;
+  if (x->layer != y->layer) return x->layer < y->layer ? -1 : 1;
+  if (x->block != y->block) return x->block < y->block ? -1 : 1;
+  return 0;
+}
+
+/* AdaptiveBatchPolicy::choose_mb (adaptive_batch.cuh:31-36) */
+static double choose_mb(double pending, double min_mb, double max_mb,
+                        double target) {
+  double g = pending / target;
+  if (g < min_mb) g = min_mb;
+  if (g > max_mb) g = max_mb;
+  return g;
+}
+
+uint64_t ora_ref_cmode_runs(int R, int L, int S, int sel, int hot,
+                            uint64_t c4, double min_mb, double max_mb,
+                            double target_batches, const uint64_t* blocks,
+                            const uint8_t* miss, uint64_t* refill_bytes) {
+  const size_t per_step = (size_t)L * sel;
+  ref_missref* ml = (ref_missref*)malloc(per_step * sizeof(ref_missref));
+  uint64_t events = 0, bytes = 0;
+  size_t ev_i = 0;
+  for (int r = 0; r < R; ++r) {
+    for (int s = 0; s < S; ++s) {
+      size_t n = 0;
+      for (int l = 0; l < L; ++l) /* :201-207 */
+        for (int k = 0; k < sel; ++k) {
+          const size_t e = ev_i + (size_t)l * sel + k;
+          if (miss[e]) {
+            ml[n].layer = l;
+            ml[n].block = blocks[e];
+            ++n;
+          }
+        }
+      ev_i += per_step;
+      qsort(ml, n, sizeof(ref_missref), cmp_missref); /* :211-217 */
+      size_t u = 0;                                   /* :218-223 */
+      for (size_t i = 0; i < n; ++i)
+        if (u == 0 || ml[i].layer != ml[u - 1].layer ||
+            ml[i].block != ml[u - 1].block)
+          ml[u++] = ml[i];
+      n = u;
+      size_t i0 = 0;
+      while (i0 < n) { /* :229-273 */
+        const double pending_mb = (double)(n - i0) * (double)c4 / (1 << 20);
+        const double gmb = choose_mb(pending_mb, min_mb, max_mb, target_batches);
+        size_t take = (size_t)(gmb * (1 << 20) / (double)c4);
+        if (take < 1) take = 1;
+        if (take > n - i0) take = n - i0;
+        size_t k = 0;
+        while (k < take) {
+          const ref_missref m0 = ml[i0 + k];
+          size_t run = 1;
+          while (k + run < take && ml[i0 + k + run].layer == m0.layer &&
+                 ml[i0 + k + run].block == m0.block + run)
+            ++run;
+          bytes += run * c4; /* both branches move run*c4 bytes */
+          (void)hot;
+          ++events;
+          k += run;
+        }
+        i0 += take;
+      }
+    }
+  }
+  free(ml);
+  if (refill_bytes) *refill_bytes = bytes;
+  return events;
+}
+
+/* ------------------------------------------------------------------ */
+/* LRU set engine                                                      */
+/* ------------------------------------------------------------------ */
+#define PEND 0x80000000u
+
+int ora_lru_init(ora_lru* s, int cap, int max_blocks) {
+  s->cap = cap;
+  s->max_blocks = max_blocks;
+  s->ord = (uint32_t*)malloc((size_t)cap * 4);
+  s->tag = (uint32_t*)malloc((size_t)cap * 4);
+  s->map = (uint32_t*)malloc((size_t)max_blocks * 4);
+  if (!s->ord || !s->tag || !s->map) return -1;
+  ora_lru_reset(s);
+  return 0;
+}
+
+void ora_lru_free(ora_lru* s) {
+  free(s->ord);
+  free(s->tag);
+  free(s->map);
+  s->ord = s->tag = s->map = NULL;
+}
+
+void ora_lru_reset(ora_lru* s) {
+  s->fill = 0;
+  for (int i = 0; i < s->cap; ++i) {
+    s->ord[i] = ORA_NONE;
+    s->tag[i] = ORA_NONE;
+  }
+  for (int i = 0; i < s->max_blocks; ++i) s->map[i] = ORA_NONE;
+}
+
+/* One batched sub-step.  Semantics (the executor's bookkeeping rule):
+ *  - hit  = block resident when the sub-step starts;
+ *  - miss = first occurrence (canonical order) of a non-resident block; later
+ *    occurrences of that block hit the in-flight fetch (dedup);
+ *  - the q-th miss takes free slot fill+q while free slots remain, then the
+ *    least recently used resident slot NOT touched in this sub-step;
+ *  - afterwards the LRU order is: untouched survivors in their old order,
+ *    then every touched slot ordered by its last occurrence.
+ * With n == 1 this is exactly kv_touch / the replay LRU
+ * (wla_multigpu.cuh:1937-1962, missstream.cuh:137-161): a hit moves to the
+ * MRU end, a miss evicts the front when full and is appended. */
+int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
+                    uint32_t* slot_out, ora_miss* miss_out, int* n_miss,
+                    uint8_t* flag_out) {
+  const int cap = s->cap;
+  for (int p = 0; p < n; ++p)
+    if (x[p] >= (uint32_t)s->max_blocks) return -1;
+  int* lastpos = (int*)malloc((size_t)cap * sizeof(int));
+  uint32_t* mblk = (uint32_t*)malloc((size_t)(n ? n : 1) * 4);
+  uint32_t* victim = (uint32_t*)malloc((size_t)(n ? n : 1) * 4);
+  uint32_t* nord = (uint32_t*)malloc((size_t)cap * 4);
+  for (int i = 0; i < cap; ++i) lastpos[i] = -1;
+  /* phase 1: classify */
+  for (int p = 0; p < n; ++p) {
+    const uint32_t v = s->map[x[p]];
+    if (v == ORA_NONE)
+      s->map[x[p]] = PEND | (uint32_t)p;
+    else if (!(v & PEND))
+      lastpos[v] = p;
+  }
+  /* phase 2: misses in order of first occurrence */
+  int M = 0;
+  for (int p = 0; p < n; ++p) {
+    const int first = s->map[x[p]] == (PEND | (uint32_t)p);
+    if (flag_out) flag_out[p] = (uint8_t)first;
+    if (first) mblk[M++] = x[p];
+  }
+  /* phase 3: victims */
+  const int freeslots = cap - (int)s->fill;
+  const int need = M > freeslots ? M - freeslots : 0;
+  int nv = 0;
+  for (uint32_t i = 0; i < s->fill && nv < need; ++i)
+    if (lastpos[s->ord[i]] < 0) victim[nv++] = s->ord[i];
+  if (nv < need) {
+    for (int q = 0; q < M; ++q) s->map[mblk[q]] = ORA_NONE;
+    free(lastpos);
+    free(mblk);
+    free(victim);
+    free(nord);
+    return -2;
+  }
+  /* phase 4: assign */
+  for (int q = 0; q < M; ++q) {
+    const uint32_t v = q < freeslots ? s->fill + (uint32_t)q : victim[q - freeslots];
+    uint32_t ev = ORA_NONE;
+    if (q >= freeslots) {
+      ev = s->tag[v];
+      s->map[ev] = ORA_NONE;
+    }
+    s->tag[v] = mblk[q];
+    s->map[mblk[q]] = v;
+    miss_out[q].block = mblk[q];
+    miss_out[q].slot = v;
+    miss_out[q].evicted = ev;
+    miss_out[q].set = set;
+  }
+  for (int p = 0; p < n; ++p) {
+    const uint32_t v = s->map[x[p]];
+    slot_out[p] = v;
+    lastpos[v] = p;
+  }
+  /* phase 5: new LRU order */
+  uint32_t w = 0;
+  for (uint32_t i = 0; i < s->fill; ++i)
+    if (lastpos[s->ord[i]] < 0) nord[w++] = s->ord[i];
+  for (int p = 0; p < n; ++p)
+    if (lastpos[slot_out[p]] == p) nord[w++] = slot_out[p];
+  s->fill += (uint32_t)(M < freeslots ? M : freeslots);
+  memcpy(s->ord, nord, (size_t)w * 4);
+  free(lastpos);
+  free(mblk);
+  free(victim);
+  free(nord);
+  *n_miss = M;
+  return w == s->fill ? 0 : -4;
+}
+
+/* Deque LRU, restating the replay's per-touch loop (missstream.cuh:137-161)
+ * over a single (request, layer) stream. */
+int ora_deque_lru_run(int cap, const uint32_t* x, int n, uint8_t* miss_flag) {
+  uint32_t* d = (uint32_t*)malloc((size_t)cap * 4);
+  int dn = 0;
+  for (int i = 0; i < n; ++i) {
+    int pos = -1;
+    for (int j = 0; j < dn; ++j)
+      if (d[j] == x[i]) {
+        pos = j;
+        break;
+      }
+    miss_flag[i] = pos < 0;
+    if (pos >= 0) {
+      memmove(d + pos, d + pos + 1, (size_t)(dn - pos - 1) * 4);
+      d[dn - 1] = x[i];
+    } else {
+      if (dn >= cap) {
+        memmove(d, d + 1, (size_t)(dn - 1) * 4);
+        dn--;
+      }
+      d[dn++] = x[i];
+    }
+  }
+  free(d);
+  return 0;
+}
+
+/* Timestamp LRU with step-batched semantics, written independently of the
+ * order-list engine above (linear scans; small sizes only). */
+int ora_tslru_init(ora_tslru* s, int cap, int max_blocks) {
+  s->cap = cap;
+  s->max_blocks = max_blocks;
+  s->tag = (uint32_t*)malloc((size_t)cap * 4);
+  s->stamp = (uint64_t*)calloc((size_t)cap, 8);
+  s->clock = 0;
+  s->fill = 0;
+  for (int i = 0; i < cap; ++i) s->tag[i] = ORA_NONE;
+  return s->tag && s->stamp ? 0 : -1;
+}
+
+void ora_tslru_free(ora_tslru* s) {
+  free(s->tag);
+  free(s->stamp);
+}
+
+int ora_tslru_step(ora_tslru* s, const uint32_t* x, int n, uint32_t* slot_out,
+                   uint32_t* miss_blocks, uint32_t* miss_slots, int* n_miss) {
+  const int cap = s->cap;
+  uint8_t* used = (uint8_t*)calloc((size_t)cap, 1);
+  int M = 0;
+  /* resident lookup at step start; collect first-occurrence misses */
+  for (int p = 0; p < n; ++p) {
+    int found = -1;
+    for (uint32_t j = 0; j < s->fill; ++j)
+      if (s->tag[j] == x[p]) found = (int)j;
+    if (found >= 0) {
+      used[found] = 1;
+      slot_out[p] = (uint32_t)found;
+      continue;
+    }
+    int dup = 0;
+    for (int q = 0; q < M; ++q)
+      if (miss_blocks[q] == x[p]) dup = 1;
+    if (!dup) miss_blocks[M++] = x[p];
+    slot_out[p] = ORA_NONE;
+  }
+  /* assign: free slots ascending, then least stamp among unused residents */
+  for (int q = 0; q < M; ++q) {
+    uint32_t v;
+    if (s->fill < (uint32_t)cap) {
+      v = s->fill++;
+    } else {
+      int best = -1;
+      for (int j = 0; j < cap; ++j)
+        if (!used[j] && (best < 0 || s->stamp[j] < s->stamp[best])) best = j;
+      if (best < 0) {
+        free(used);
+        return -2;
+      }
+      v = (uint32_t)best;
+    }
+    used[v] = 1;
+    s->tag[v] = miss_blocks[q];
+    miss_slots[q] = v;
+  }
+  for (int p = 0; p < n; ++p) {
+    if (slot_out[p] == ORA_NONE)
+      for (int q = 0; q < M; ++q)
+        if (miss_blocks[q] == x[p]) slot_out[p] = miss_slots[q];
+    s->stamp[slot_out[p]] = s->clock + (uint64_t)p + 1;
+  }
+  s->clock += (uint64_t)n + 1;
+  free(used);
+  *n_miss = M;
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* executor geometry and step                                          */
+/* ------------------------------------------------------------------ */
+int ora_n_owners(const ora_geom* g) { return (g->n_req + g->group - 1) / g->group; }
+int ora_n_sets(const ora_geom* g) { return ora_n_owners(g) * g->n_layers * g->kv_heads; }
+int ora_members(const ora_geom* g, int o) {
+  const int m = g->n_req - o * g->group;
+  return m < g->group ? m : g->group;
+}
+int ora_max_sel_per_set(const ora_geom* g) { return g->group * g->k; }
+
+static int esize(int dtype) {
+  return dtype == ORA_F32 ? 4 : (dtype == ORA_FP8 ? 1 : 2);
+}
+
+uint64_t ora_block_bytes(const ora_geom* g) {
+  return 2ull * (uint64_t)g->block_tokens * (uint64_t)g->head_dim *
+         (uint64_t)esize(g->dtype);
+}
+
+/* Host-tier block index of (set, block): the logical host tier holds every
+ * (set, block) at set * max_blocks + block; the physical tier aliases it
+ * modulo its capacity, as the reference's slab does (wla_multigpu.cuh:
+ * 323-332, `block % cap`). */
+uint64_t ora_host_index(const ora_geom* g, uint32_t set, uint32_t block) {
+  return ((uint64_t)set * (uint64_t)g->max_blocks + block) % g->host_blocks;
+}
+
+struct ora_exec {
+  ora_geom g;
+  ora_lru* sets;
+  uint32_t* x;
+  uint32_t* slot;
+  uint8_t* flag;
+};
+
+ora_exec* ora_exec_create(const ora_geom* g) {
+  ora_exec* e = (ora_exec*)calloc(1, sizeof(ora_exec));
+  e->g = *g;
+  const int ns = ora_n_sets(g);
+  e->sets = (ora_lru*)calloc((size_t)ns, sizeof(ora_lru));
+  for (int i = 0; i < ns; ++i)
+    if (ora_lru_init(&e->sets[i], g->cap, g->max_blocks)) return NULL;
+  e->x = (uint32_t*)malloc((size_t)ora_max_sel_per_set(g) * 4);
+  e->slot = (uint32_t*)malloc((size_t)ora_max_sel_per_set(g) * 4);
+  e->flag = (uint8_t*)malloc((size_t)ora_max_sel_per_set(g));
+  return e;
+}
+
+void ora_exec_destroy(ora_exec* e) {
+  if (!e) return;
+  const int ns = ora_n_sets(&e->g);
+  for (int i = 0; i < ns; ++i) ora_lru_free(&e->sets[i]);
+  free(e->sets);
+  free(e->x);
+  free(e->slot);
+  free(e->flag);
+  free(e);
+}
+
+int ora_exec_step(ora_exec* e, const uint32_t* sel, uint32_t* slots_out,
+                  uint32_t* miss_count, ora_miss* misses, uint64_t* counts,
+                  uint8_t* flags) {
+  const ora_geom* g = &e->g;
+  const int L = g->n_layers, H = g->kv_heads, k = g->k;
+  const int nown = ora_n_owners(g), maxsel = ora_max_sel_per_set(g);
+  uint64_t nsel = 0, nmiss = 0;
+  for (int o = 0; o < nown; ++o)
+    for (int l = 0; l < L; ++l)
+      for (int h = 0; h < H; ++h) {
+        const uint32_t set = (uint32_t)((o * L + l) * H + h);
+        const int mem = ora_members(g, o);
+        const int n = mem * k;
+        for (int m = 0; m < mem; ++m) {
+          const int r = o * g->group + m;
+          memcpy(e->x + (size_t)m * k, sel + ((size_t)(r * L + l) * H + h) * k,
+                 (size_t)k * 4);
+        }
+        ora_miss* mo = misses + (size_t)set * maxsel;
+        int M = 0;
+        if (g->granularity == 0) {
+          const int rc = ora_lru_substep(&e->sets[set], set, e->x, n, e->slot, mo, &M, e->flag);
+          if (rc) return rc;
+        } else {
+          for (int p = 0; p < n; ++p) {
+            int m1 = 0;
+            const int rc = ora_lru_substep(&e->sets[set], set, e->x + p, 1,
+                                           e->slot + p, mo + M, &m1, e->flag + p);
+            if (rc) return rc;
+            M += m1;
+          }
+          /* every selected block must still be resident at step end */
+          for (int p = 0; p < n; ++p)
+            if (e->sets[set].tag[e->slot[p]] != e->x[p]) return -3;
+        }
+        miss_count[set] = (uint32_t)M;
+        nsel += (uint64_t)n;
+        nmiss += (uint64_t)M;
+        for (int m = 0; m < mem; ++m) {
+          const int r = o * g->group + m;
+          uint32_t* so = slots_out + ((size_t)(r * L + l) * H + h) * k;
+          for (int j = 0; j < k; ++j)
+            so[j] = set * (uint32_t)g->cap + e->slot[m * k + j];
+          if (flags)
+            memcpy(flags + ((size_t)(r * L + l) * H + h) * k, e->flag + (size_t)m * k,
+                   (size_t)k);
+        }
+      }
+  if (counts) {
+    counts[0] = nsel;
+    counts[1] = nmiss;
+    counts[2] = nsel - nmiss;
+  }
+  return 0;
+}
+
+void ora_exec_state(const ora_exec* e, uint32_t* fill, uint32_t* ord,
+                    uint32_t* tag) {
+  const int ns = ora_n_sets(&e->g), cap = e->g.cap;
+  for (int i = 0; i < ns; ++i) {
+    fill[i] = e->sets[i].fill;
+    memcpy(ord + (size_t)i * cap, e->sets[i].ord, (size_t)cap * 4);
+    memcpy(tag + (size_t)i * cap, e->sets[i].tag, (size_t)cap * 4);
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* workload generators                                                 */
+/* ------------------------------------------------------------------ */
+#define SALT_CTX 0x43545842ull  /* context lengths */
+#define SALT_SEL 0x53454C31ull  /* selection draws */
+#define SALT_PERM 0x5045524Dull /* popularity permutation offsets */
+#define SALT_HOST 0x484F5354ull /* host tier values */
+#define SALT_SCALE 0x5343414Cull /* fp8 block scales */
+#define SALT_KEEP 0x4B454550ull  /* inter-step reuse draws */
+#define PERM_PRIME 1000003ull
+#define DRAW_LIMIT 65536
+
+void ora_ctx_uniform(uint64_t seed, int n_req, int lo, int hi, int* out) {
+  const uint64_t span = (uint64_t)(hi - lo + 1);
+  for (int r = 0; r < n_req; ++r)
+    out[r] = lo + (int)(ora_mix64(seed ^ SALT_CTX, (uint64_t)r) % span);
+}
+
+/* permutation domain of an owner: its largest member context */
+static int owner_nperm(const ora_selgen* s, int o) {
+  int m = 0;
+  for (int r = o * s->group; r < (o + 1) * s->group && r < s->n_req; ++r)
+    if (s->ctx_blocks[r] > m) m = s->ctx_blocks[r];
+  return m;
+}
+
+int ora_selgen_max_blocks(const ora_selgen* s) {
+  const int nown = (s->n_req + s->group - 1) / s->group;
+  int mx = 0;
+  for (int o = 0; o < nown; ++o) {
+    const int np = owner_nperm(s, o);
+    const int pre = s->prefix_blocks < np ? s->prefix_blocks : np;
+    const int b = pre + s->group * (np - pre);
+    if (b > mx) mx = b;
+  }
+  return mx;
+}
+
+static int cmp_u32(const void* a, const void* b) {
+  const uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
+  return x < y ? -1 : (x > y);
+}
+
+/* Selections of one step.  For every (request r, layer l, kv head h):
+ *  - step 0 (or reuse == 0): nothing is carried over;
+ *  - later steps: each block of r's previous selection is kept with
+ *    probability `reuse` (inter-step reuse, the locality knob of the
+ *    reference generator, missstream.cuh:127-128);
+ *  - the selection is completed to k distinct blocks by drawing popularity
+ *    ranks from Zipf(s) (or uniform) over the owner's permutation domain,
+ *    mapping rank -> block through the owner's affine permutation
+ *    (rank*P + off) mod n, and rejecting blocks outside r's context or
+ *    already taken;
+ *  - the k blocks are sorted ascending (top-k page indices are sorted,
+ *    tools/capture_miss_trace.py:158-159); `state` keeps them (logical ids)
+ *    for the next step, `out` names them in the set's id space (shared prefix
+ *    ids first, then each member's private range). */
+int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
+                    uint32_t* out) {
+  const int L = s->n_layers, H = s->kv_heads, k = s->k;
+  int nmax = 0;
+  for (int r = 0; r < s->n_req; ++r)
+    if (s->ctx_blocks[r] > nmax) nmax = s->ctx_blocks[r];
+  double* cum = NULL;
+  if (s->dist == 1) {
+    cum = (double*)malloc((size_t)nmax * sizeof(double));
+    double acc = 0.0;
+    for (int i = 0; i < nmax; ++i) {
+      acc += pow((double)(i + 1), -s->zipf_s);
+      cum[i] = acc;
+    }
+  }
+  const uint64_t keep_thr = (uint64_t)(s->reuse * 4294967296.0);
+  const int carry = step > 0 && s->reuse > 0.0;
+  uint8_t* taken = (uint8_t*)calloc((size_t)nmax, 1);
+  for (int r = 0; r < s->n_req; ++r) {
+    const int o = r / s->group, m = r % s->group;
+    const int nr = s->ctx_blocks[r];
+    const int np = owner_nperm(s, o);
+    const int pre = s->prefix_blocks < np ? s->prefix_blocks : np;
+    if (k > nr) {
+      free(cum);
+      free(taken);
+      return -1;
+    }
+    for (int l = 0; l < L; ++l)
+      for (int h = 0; h < H; ++h) {
+        const size_t row = ((size_t)(r * L + l) * H + h) * k;
+        uint32_t* st = state + row;
+        uint32_t* so = out + row;
+        const uint64_t off =
+            ora_mix64(s->seed ^ SALT_PERM, (uint64_t)((o * L + l) * H + h)) %
+            (uint64_t)np;
+        const uint64_t base =
+            ((((uint64_t)step * (uint64_t)s->n_req + (uint64_t)r) * (uint64_t)L +
+              (uint64_t)l) * (uint64_t)H + (uint64_t)h) * (uint64_t)DRAW_LIMIT;
+        int got = 0;
+        if (carry)
+          for (int j = 0; j < k; ++j) {
+            const uint64_t u = ora_mix64(s->seed ^ SALT_KEEP, base + (uint64_t)j) >> 32;
+            if (u < keep_thr) {
+              so[got++] = st[j];
+              taken[st[j]] = 1;
+            }
+          }
+        for (int i = 0; i < DRAW_LIMIT && got < k; ++i) {
+          const uint64_t u = ora_mix64(s->seed ^ SALT_SEL, base + (uint64_t)i);
+          uint64_t rank;
+          if (s->dist == 1) {
+            const double thr = (double)(u >> 11) * (1.0 / 9007199254740992.0) *
+                               cum[np - 1];
+            int lo = 0, hi = np - 1; /* first i with cum[i] > thr */
+            while (lo < hi) {
+              const int mid = (lo + hi) >> 1;
+              if (cum[mid] > thr)
+                hi = mid;
+              else
+                lo = mid + 1;
+            }
+            rank = (uint64_t)lo;
+          } else {
+            rank = ((u >> 32) * (uint64_t)np) >> 32;
+          }
+          const uint64_t b = (rank * PERM_PRIME + off) % (uint64_t)np;
+          if (b >= (uint64_t)nr || taken[b]) continue;
+          taken[b] = 1;
+          so[got++] = (uint32_t)b;
+        }
+        for (int j = 0; j < got; ++j) taken[so[j]] = 0;
+        if (got < k) {
+          free(cum);
+          free(taken);
+          return -2;
+        }
+        qsort(so, (size_t)k, 4, cmp_u32);
+        memcpy(st, so, (size_t)k * 4);
+        for (int j = 0; j < k; ++j)
+          if (so[j] >= (uint32_t)pre)
+            so[j] = (uint32_t)pre + (uint32_t)m * (uint32_t)(np - pre) +
+                    (so[j] - (uint32_t)pre);
+      }
+  }
+  free(cum);
+  free(taken);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* host tier content                                                   */
+/* ------------------------------------------------------------------ */
+/* Values are Irwin-Hall(4) sums of 16-bit uniforms from the hash, centred
+ * and scaled by a float multiplier (std / (65536/sqrt(3))), i.e. zero mean and
+ * the requested standard deviation; fp8 blocks store codes of std 96 and a
+ * per-block float scale so that code*scale has the requested std. */
+static float value_mult(float std) {
+  return (float)((double)std / (65536.0 / sqrt(3.0)));
+}
+
+static int32_t irwin_hall(uint64_t w) {
+  return (int32_t)(w & 0xFFFFu) + (int32_t)((w >> 16) & 0xFFFFu) +
+         (int32_t)((w >> 32) & 0xFFFFu) + (int32_t)(w >> 48) - 131070;
+}
+
+uint32_t ora_host_elem(const ora_geom* g, uint64_t h, uint32_t e) {
+  const uint64_t E = 2ull * (uint64_t)g->block_tokens * (uint64_t)g->head_dim;
+  const int32_t sv = irwin_hall(ora_mix64(g->seed ^ SALT_HOST, h * E + e));
+  if (g->dtype == ORA_FP8) {
+    const float c = (float)sv * value_mult(96.0f);
+    return ora_f32_to_e4m3(c);
+  }
+  const float x = (float)sv * value_mult(g->value_std);
+  switch (g->dtype) {
+    case ORA_F32: return f32_bits(x);
+    case ORA_F16: return ora_f32_to_f16(x);
+    default: return ora_f32_to_bf16(x);
+  }
+}
+
+float ora_host_scale(const ora_geom* g, uint64_t h, int kv) {
+  if (g->dtype != ORA_FP8) return 1.0f;
+  const float base = (float)((double)g->value_std / 96.0);
+  const uint64_t u = ora_mix64(g->seed ^ SALT_SCALE, h * 2ull + (uint64_t)kv) >> 56;
+  return base * (0.75f + (float)u / 512.0f);
+}
+
+void ora_host_block(const ora_geom* g, uint64_t h, void* bytes, float* scales) {
+  const uint32_t E = 2u * (uint32_t)g->block_tokens * (uint32_t)g->head_dim;
+  const int es = esize(g->dtype);
+  uint8_t* b = (uint8_t*)bytes;
+  for (uint32_t e = 0; e < E; ++e) {
+    const uint32_t v = ora_host_elem(g, h, e);
+    memcpy(b + (size_t)e * es, &v, (size_t)es); /* little endian */
+  }
+  if (scales) {
+    scales[0] = ora_host_scale(g, h, 0);
+    scales[1] = ora_host_scale(g, h, 1);
+  }
+}
+
+void ora_host_fill(const ora_geom* g, uint8_t* host, float* host_scales) {
+  const uint64_t bb = ora_block_bytes(g);
+  for (uint64_t h = 0; h < g->host_blocks; ++h)
+    ora_host_block(g, h, host + h * bb, host_scales ? host_scales + 2 * h : NULL);
+}
+
+/* ------------------------------------------------------------------ */
+/* attention                                                           */
+/* ------------------------------------------------------------------ */
+/* Textbook decode attention over the selected blocks: s_t = q.K_t/sqrt(D),
+ * p = softmax(s) over every token of every selected block, out = sum p_t V_t
+ * (the semantics the reference's FMA proxy stands in for,
+ * src/workloads/kv_exec.cuh:30-37; selection as in
+ * tools/capture_miss_trace.py:146-159). */
+int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
+                      double* out) {
+  const int L = g->n_layers, Hq = g->q_heads, Hk = g->kv_heads, D = g->head_dim;
+  const int T = g->block_tokens, k = g->k, grp = Hq / Hk;
+  const int ntok = k * T;
+  double* s = (double*)malloc((size_t)ntok * sizeof(double));
+  double* V = (double*)malloc((size_t)ntok * D * sizeof(double));
+  double* K = (double*)malloc((size_t)ntok * D * sizeof(double));
+  const double isd = 1.0 / sqrt((double)D);
+  for (int r = 0; r < g->n_req; ++r) {
+    const int o = r / g->group;
+    for (int l = 0; l < L; ++l)
+      for (int h = 0; h < Hk; ++h) {
+        const uint32_t set = (uint32_t)((o * L + l) * Hk + h);
+        const uint32_t* bl = sel + ((size_t)(r * L + l) * Hk + h) * k;
+        for (int j = 0; j < k; ++j) {
+          const uint64_t hi = ora_host_index(g, set, bl[j]);
+          const double sk = ora_host_scale(g, hi, 0), sv = ora_host_scale(g, hi, 1);
+          for (int t = 0; t < T; ++t)
+            for (int d = 0; d < D; ++d) {
+              const size_t row = (size_t)(j * T + t) * D + d;
+              K[row] = ora_decode(g->dtype, ora_host_elem(g, hi, (uint32_t)(t * D + d))) * sk;
+              V[row] = ora_decode(g->dtype,
+                                  ora_host_elem(g, hi, (uint32_t)((T + t) * D + d))) * sv;
+            }
+        }
+        for (int gq = 0; gq < grp; ++gq) {
+          const int hq = h * grp + gq;
+          const float* qv = q + ((size_t)(r * L + l) * Hq + hq) * D;
+          double mx = -INFINITY;
+          for (int t = 0; t < ntok; ++t) {
+            double acc = 0.0;
+            for (int d = 0; d < D; ++d) acc += (double)qv[d] * K[(size_t)t * D + d];
+            s[t] = acc * isd;
+            if (s[t] > mx) mx = s[t];
+          }
+          double den = 0.0;
+          for (int t = 0; t < ntok; ++t) {
+            s[t] = exp(s[t] - mx);
+            den += s[t];
+          }
+          double* ov = out + ((size_t)(r * L + l) * Hq + hq) * D;
+          for (int d = 0; d < D; ++d) {
+            double acc = 0.0;
+            for (int t = 0; t < ntok; ++t) acc += s[t] * V[(size_t)t * D + d];
+            ov[d] = acc / den;
+          }
+        }
+      }
+  }
+  free(s);
+  free(V);
+  free(K);
+  return 0;
+}
+
+static float load_elem_f32(int dtype, const uint8_t* p, size_t i) {
+  switch (dtype) {
+    case ORA_F32: {
+      float v;
+      memcpy(&v, p + i * 4, 4);
+      return v;
+    }
+    case ORA_F16: {
+      uint16_t v;
+      memcpy(&v, p + i * 2, 2);
+      return ora_f16_to_f32(v);
+    }
+    case ORA_BF16: {
+      uint16_t v;
+      memcpy(&v, p + i * 2, 2);
+      return ora_bf16_to_f32(v);
+    }
+    default: return ora_e4m3_to_f32(p[i]);
+  }
+}
+
+int ora_attention_pool_f32(const ora_geom* g, const uint32_t* slots,
+                           const uint8_t* pool, const float* pool_scales,
+                           const float* q, float* out) {
+  const int L = g->n_layers, Hq = g->q_heads, Hk = g->kv_heads, D = g->head_dim;
+  const int T = g->block_tokens, k = g->k, grp = Hq / Hk;
+  const uint64_t bb = ora_block_bytes(g);
+  const float isd = 1.0f / sqrtf((float)D);
+  float* acc = (float*)malloc((size_t)D * sizeof(float));
+  float* sc = (float*)malloc((size_t)T * sizeof(float));
+  for (int r = 0; r < g->n_req; ++r)
+    for (int l = 0; l < L; ++l)
+      for (int h = 0; h < Hk; ++h) {
+        const uint32_t* sl = slots + ((size_t)(r * L + l) * Hk + h) * k;
+        for (int gq = 0; gq < grp; ++gq) {
+          const int hq = h * grp + gq;
+          const float* qv = q + ((size_t)(r * L + l) * Hq + hq) * D;
+          float m = -INFINITY, den = 0.0f;
+          for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+          for (int j = 0; j < k; ++j) {
+            const uint8_t* blk = pool + (size_t)sl[j] * bb;
+            const float sk = pool_scales ? pool_scales[2 * (size_t)sl[j]] : 1.0f;
+            const float sv = pool_scales ? pool_scales[2 * (size_t)sl[j] + 1] : 1.0f;
+            float bm = -INFINITY;
+            for (int t = 0; t < T; ++t) {
+              float a = 0.0f;
+              for (int d = 0; d < D; ++d)
+                a += qv[d] * load_elem_f32(g->dtype, blk, (size_t)t * D + d);
+              sc[t] = a * sk * isd;
+              if (sc[t] > bm) bm = sc[t];
+            }
+            const float mn = bm > m ? bm : m;
+            const float alpha = expf(m - mn);
+            den *= alpha;
+            for (int d = 0; d < D; ++d) acc[d] *= alpha;
+            for (int t = 0; t < T; ++t) {
+              const float p = expf(sc[t] - mn);
+              den += p;
+              const float pv = p * sv;
+              for (int d = 0; d < D; ++d)
+                acc[d] += pv * load_elem_f32(g->dtype, blk, (size_t)(T + t) * D + d);
+            }
+            m = mn;
+          }
+          float* ov = out + ((size_t)(r * L + l) * Hq + hq) * D;
+          for (int d = 0; d < D; ++d) ov[d] = acc[d] / den;
+        }
+      }
+  free(acc);
+  free(sc);
+  return 0;
+}
+
+int ora_cpu_step(ora_exec* e, const uint32_t* sel, const uint8_t* host,
+                 const float* host_scales, uint8_t* pool, float* pool_scales,
+                 const float* q, float* out, uint32_t* slots_scratch,
+                 uint32_t* miss_count, ora_miss* misses, uint64_t* counts) {
+  const ora_geom* g = &e->g;
+  int rc = ora_exec_step(e, sel, slots_scratch, miss_count, misses, counts, NULL);
+  if (rc) return rc;
+  const uint64_t bb = ora_block_bytes(g);
+  const int ns = ora_n_sets(g), maxsel = ora_max_sel_per_set(g);
+  for (int s = 0; s < ns; ++s)
+    for (uint32_t i = 0; i < miss_count[s]; ++i) {
+      const ora_miss* m = misses + (size_t)s * maxsel + i;
+      const uint64_t hi = ora_host_index(g, m->set, m->block);
+      const uint64_t dst = (uint64_t)m->set * (uint64_t)g->cap + m->slot;
+      memcpy(pool + dst * bb, host + hi * bb, bb);
+      if (pool_scales && host_scales) {
+        pool_scales[2 * dst] = host_scales[2 * hi];
+        pool_scales[2 * dst + 1] = host_scales[2 * hi + 1];
+      }
+    }
+  return ora_attention_pool_f32(g, slots_scratch, pool, pool_scales, q, out);
+}

@@ -1,0 +1,226 @@
+/*
+ * oracle.h -- CPU restatement of the per-GPU sparse KV miss-stream executor.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/,
+ * __graft_entry__.smoke() and the cpu_baseline leg of bench.py may load it.
+ * The product (ferry_amd/) never links, loads or calls it.
+ *
+ * Contents (each function cites the reference file:line it restates; paths
+ * are relative to the clearleo126/ferry source tree):
+ *   - std::mt19937_64 (the generator replay_miss_stream seeds)
+ *   - ora_ref_replay: src/workloads/missstream.cuh:104-170
+ *   - ora_ref_cmode_runs: src/workloads/kv_exec.cuh:188-292 and
+ *     src/runtime/wla_multigpu.cuh:2527-2604 (dedup + adaptive batches +
+ *     run coalescing), with AdaptiveBatchPolicy::choose_mb
+ *     (src/runtime/adaptive_batch.cuh:31-36)
+ *   - the executor's LRU set engine (generalises kv_touch,
+ *     src/runtime/wla_multigpu.cuh:1937-1962, to (owner, layer, kv head)
+ *     sets with explicit slot ids), plus two independent restatements used
+ *     only to cross-check it (a deque LRU and a timestamp LRU)
+ *   - synthetic selection generators for the five workloads
+ *   - host-tier addressing and content (the reference aliases its host slab
+ *     modulo capacity: src/runtime/wla_multigpu.cuh:323-332)
+ *   - fp64 block-sparse decode attention (textbook softmax attention; the
+ *     reference only has an FMA proxy at src/workloads/kv_exec.cuh:30-37 and
+ *     the selection semantics of tools/capture_miss_trace.py:139-159)
+ *   - a timed fp32 CPU executor step (cpu_baseline of bench.py)
+ *
+ * Parity pins (tests/test_oracle.py): golden counts held in the reference's
+ * logs, the C++ standard's mt19937_64 known answer, a build of the
+ * reference's own header under oracle/_ref, and brute-force / closed-form
+ * checks for everything the reference does not hold.
+ */
+#ifndef FERRY_ORACLE_H
+#define FERRY_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORA_NONE 0xFFFFFFFFu
+
+/* dtype codes shared with include/ferry_amd.h */
+enum { ORA_F32 = 0, ORA_F16 = 1, ORA_BF16 = 2, ORA_FP8 = 3 };
+
+/* ---------------- primitives ---------------- */
+uint64_t ora_mix64(uint64_t seed, uint64_t idx);
+uint16_t ora_f32_to_f16(float x);
+float ora_f16_to_f32(uint16_t h);
+uint16_t ora_f32_to_bf16(float x);
+float ora_bf16_to_f32(uint16_t h);
+uint8_t ora_f32_to_e4m3(float x);
+float ora_e4m3_to_f32(uint8_t v);
+
+/* ---------------- mt19937_64 ---------------- */
+typedef struct {
+  uint64_t mt[312];
+  int idx;
+} ora_mt64;
+void ora_mt64_seed(ora_mt64* g, uint64_t seed);
+uint64_t ora_mt64_next(ora_mt64* g);
+
+/* ---------------- reference replay ---------------- */
+/* Restates replay_miss_stream (missstream.cuh:104-170).  Event order is
+ * (r, s, l, k) exactly as the reference pushes MissEvent.  blocks/miss may be
+ * NULL.  counts[0] = total_selects, counts[1] = total_misses. */
+int ora_ref_replay(int R, int L, int S, int sel, int hot, uint64_t seed,
+                   uint64_t* blocks, uint8_t* miss, uint64_t* counts);
+
+/* Restates the C-mode refill planner of run_miss_workload
+ * (kv_exec.cuh:188-292): per (r, s) gather all-layer misses, sort by
+ * (layer, block), unique, cut adaptive batches, coalesce consecutive blocks of
+ * one layer inside a batch unless the direct-mapped slot range wraps.
+ * Returns refill_events (submits); *refill_bytes receives the bytes. */
+uint64_t ora_ref_cmode_runs(int R, int L, int S, int sel, int hot,
+                            uint64_t c4_bytes, double min_mb, double max_mb,
+                            double target_batches, const uint64_t* blocks,
+                            const uint8_t* miss, uint64_t* refill_bytes);
+
+/* ---------------- LRU set engine ---------------- */
+typedef struct {
+  uint32_t block;   /* block id fetched into the slot */
+  uint32_t slot;    /* local slot index in [0, cap) */
+  uint32_t evicted; /* block id evicted from the slot, or ORA_NONE */
+  uint32_t set;     /* set id */
+} ora_miss;
+
+typedef struct {
+  int cap;         /* slots per set */
+  int max_blocks;  /* block ids are < max_blocks */
+  uint32_t fill;   /* slots in use; free slots are [fill, cap) */
+  uint32_t* ord;   /* [cap] local slots, LRU first; first `fill` valid */
+  uint32_t* tag;   /* [cap] block id per slot (ORA_NONE when free) */
+  uint32_t* map;   /* [max_blocks] local slot per block (ORA_NONE) */
+} ora_lru;
+
+int ora_lru_init(ora_lru* s, int cap, int max_blocks);
+void ora_lru_free(ora_lru* s);
+void ora_lru_reset(ora_lru* s);
+/* One batched sub-step over x[0..n) in canonical order.  slot_out[p] gets
+ * the local slot holding x[p] after the sub-step; misses (first occurrences of
+ * non-resident blocks, in order) are appended to miss_out with set id `set`.
+ * Returns 0, -1 (block id out of range) or -2 (more distinct blocks than the
+ * slots that may be reused in this sub-step). */
+int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
+                    uint32_t* slot_out, ora_miss* miss_out, int* n_miss,
+                    uint8_t* flag_out);
+
+/* Independent restatements (cross-checks only). */
+/* Deque LRU with per-touch semantics (missstream.cuh:137-161). */
+int ora_deque_lru_run(int cap, const uint32_t* x, int n, uint8_t* miss_flag);
+/* Timestamp LRU with step-batched semantics (victim = least recent stamp
+ * among slots not selected in the step). */
+typedef struct {
+  int cap, max_blocks;
+  uint32_t* tag;
+  uint64_t* stamp;
+  uint64_t clock;
+  uint32_t fill;
+} ora_tslru;
+int ora_tslru_init(ora_tslru* s, int cap, int max_blocks);
+void ora_tslru_free(ora_tslru* s);
+int ora_tslru_step(ora_tslru* s, const uint32_t* x, int n, uint32_t* slot_out,
+                   uint32_t* miss_blocks, uint32_t* miss_slots, int* n_miss);
+
+/* ---------------- executor geometry ---------------- */
+typedef struct {
+  int n_req;       /* B requests */
+  int group;       /* requests per owner (1 = private sets) */
+  int n_layers;    /* L */
+  int kv_heads;    /* Hkv */
+  int q_heads;     /* Hq */
+  int head_dim;    /* D */
+  int block_tokens;/* T */
+  int k;           /* selected blocks per (request, layer, kv head) */
+  int cap;         /* slots per set */
+  int max_blocks;  /* set block ids < max_blocks */
+  int dtype;       /* ORA_F32 / ORA_F16 / ORA_BF16 / ORA_FP8 */
+  int granularity; /* 0 = step-batched, 1 = serial (per selection) */
+  uint64_t host_blocks; /* host tier capacity in blocks */
+  uint64_t seed;   /* host tier content seed */
+  float value_std; /* std of K/V values */
+} ora_geom;
+
+int ora_n_owners(const ora_geom* g);
+int ora_n_sets(const ora_geom* g);
+int ora_members(const ora_geom* g, int owner);
+int ora_max_sel_per_set(const ora_geom* g);
+uint64_t ora_block_bytes(const ora_geom* g); /* K+V bytes, scales excluded */
+uint64_t ora_host_index(const ora_geom* g, uint32_t set, uint32_t block);
+
+/* Executor state = one ora_lru per set. */
+typedef struct ora_exec ora_exec;
+ora_exec* ora_exec_create(const ora_geom* g);
+void ora_exec_destroy(ora_exec* e);
+/* One decode step of bookkeeping.  sel: [B][L][Hkv][k] set block ids.
+ * slots_out: [B][L][Hkv][k] global slot ids (set * cap + local).
+ * miss_count: [n_sets]; misses: [n_sets][max_sel_per_set].  counts[0..2] =
+ * selections, misses, hits.  Returns 0 or a negative error. */
+int ora_exec_step(ora_exec* e, const uint32_t* sel, uint32_t* slots_out,
+                  uint32_t* miss_count, ora_miss* misses, uint64_t* counts,
+                  uint8_t* flags);
+/* Per-set state export for parity: fill[n_sets], ord[n_sets][cap],
+ * tag[n_sets][cap]. */
+void ora_exec_state(const ora_exec* e, uint32_t* fill, uint32_t* ord,
+                    uint32_t* tag);
+
+/* ---------------- workload generators ---------------- */
+typedef struct {
+  int n_req, group, n_layers, kv_heads, k;
+  int dist;          /* 0 = uniform, 1 = zipf */
+  double zipf_s;
+  double reuse;      /* probability a selected block is kept next step */
+  int prefix_blocks; /* shared prefix blocks per group (0 = none) */
+  uint64_t seed;
+  const int* ctx_blocks; /* [n_req] logical context length in blocks */
+} ora_selgen;
+
+/* Per-request context lengths: uniform integer in [lo, hi]. */
+void ora_ctx_uniform(uint64_t seed, int n_req, int lo, int hi, int* out);
+/* Set block-id bound for a generator (max over owners). */
+int ora_selgen_max_blocks(const ora_selgen* s);
+/* Selections of one step: out [B][L][Hkv][k] set block ids; state [same]
+ * carries each request's logical selection from step to step. */
+int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
+                    uint32_t* out);
+
+/* ---------------- host tier ---------------- */
+/* Element e of host block h (K then V, [T][D] each) as the stored encoding
+ * widened to uint32 (f32 bits, f16/bf16 bits, or an e4m3 byte). */
+uint32_t ora_host_elem(const ora_geom* g, uint64_t h, uint32_t e);
+/* Per-block dequant scales (fp8 only; 1.0 otherwise): kv = 0 K, 1 V. */
+float ora_host_scale(const ora_geom* g, uint64_t h, int kv);
+/* Fill one host block's bytes (bb bytes) and its two scales. */
+void ora_host_block(const ora_geom* g, uint64_t h, void* bytes, float* scales);
+double ora_decode(int dtype, uint32_t v);
+
+/* ---------------- attention ---------------- */
+/* fp64 block-sparse decode attention with keys read from the host tier by
+ * (set, block).  q, out: [B][L][Hq][D] (q fp32, out fp64). */
+int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
+                      double* out);
+/* Same attention, but K/V read from a host pool image laid out like the HBM
+ * pool (slot-major, bb bytes per slot, scales[slot][2]) through the slot
+ * table; fp32 accumulation.  Used by the CPU baseline. */
+int ora_attention_pool_f32(const ora_geom* g, const uint32_t* slots,
+                           const uint8_t* pool, const float* pool_scales,
+                           const float* q, float* out);
+
+/* ---------------- CPU executor step (cpu_baseline) ---------------- */
+/* Bookkeeping + memcpy gather from the host tier image into the pool image +
+ * fp32 attention.  host: [host_blocks][bb] bytes, host_scales [host_blocks][2].
+ * pool: [n_sets*cap][bb], pool_scales [n_sets*cap][2]. */
+int ora_cpu_step(ora_exec* e, const uint32_t* sel, const uint8_t* host,
+                 const float* host_scales, uint8_t* pool, float* pool_scales,
+                 const float* q, float* out, uint32_t* slots_scratch,
+                 uint32_t* miss_count, ora_miss* misses, uint64_t* counts);
+/* Materialise the host tier image (used by the CPU baseline). */
+void ora_host_fill(const ora_geom* g, uint8_t* host, float* host_scales);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,264 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and
+by the cpu_baseline leg of bench.py, as the checker.  The product never
+imports it.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = os.path.join(_HERE, "liboracle.so")
+
+F32, F16, BF16, FP8 = 0, 1, 2, 3
+NONE = 0xFFFFFFFF
+
+
+def build():
+    """Compile liboracle.so (and oracle/_ref when the reference tree exists)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def _load():
+    if not os.path.exists(_LIB):
+        build()
+    return C.CDLL(_LIB)
+
+
+lib = _load()
+
+_u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+_u64p = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+MISS_DTYPE = np.dtype([("block", "<u4"), ("slot", "<u4"), ("evicted", "<u4"), ("set", "<u4")])
+_missp = np.ctypeslib.ndpointer(MISS_DTYPE, flags="C_CONTIGUOUS")
+
+
+class Geom(C.Structure):
+    _fields_ = [
+        ("n_req", C.c_int), ("group", C.c_int), ("n_layers", C.c_int),
+        ("kv_heads", C.c_int), ("q_heads", C.c_int), ("head_dim", C.c_int),
+        ("block_tokens", C.c_int), ("k", C.c_int), ("cap", C.c_int),
+        ("max_blocks", C.c_int), ("dtype", C.c_int), ("granularity", C.c_int),
+        ("host_blocks", C.c_uint64), ("seed", C.c_uint64), ("value_std", C.c_float),
+    ]
+
+
+class SelGen(C.Structure):
+    _fields_ = [
+        ("n_req", C.c_int), ("group", C.c_int), ("n_layers", C.c_int),
+        ("kv_heads", C.c_int), ("k", C.c_int), ("dist", C.c_int),
+        ("zipf_s", C.c_double), ("reuse", C.c_double), ("prefix_blocks", C.c_int), ("seed", C.c_uint64),
+        ("ctx_blocks", C.POINTER(C.c_int)),
+    ]
+
+
+class MT64(C.Structure):
+    _fields_ = [("mt", C.c_uint64 * 312), ("idx", C.c_int)]
+
+
+class LRU(C.Structure):
+    _fields_ = [("cap", C.c_int), ("max_blocks", C.c_int), ("fill", C.c_uint32),
+                ("ord", C.POINTER(C.c_uint32)), ("tag", C.POINTER(C.c_uint32)),
+                ("map", C.POINTER(C.c_uint32))]
+
+
+class TSLRU(C.Structure):
+    _fields_ = [("cap", C.c_int), ("max_blocks", C.c_int),
+                ("tag", C.POINTER(C.c_uint32)), ("stamp", C.POINTER(C.c_uint64)),
+                ("clock", C.c_uint64), ("fill", C.c_uint32)]
+
+
+def _sig(name, res, *args):
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+    return f
+
+
+_sig("ora_mix64", C.c_uint64, C.c_uint64, C.c_uint64)
+_sig("ora_f32_to_f16", C.c_uint16, C.c_float)
+_sig("ora_f16_to_f32", C.c_float, C.c_uint16)
+_sig("ora_f32_to_bf16", C.c_uint16, C.c_float)
+_sig("ora_bf16_to_f32", C.c_float, C.c_uint16)
+_sig("ora_f32_to_e4m3", C.c_uint8, C.c_float)
+_sig("ora_e4m3_to_f32", C.c_float, C.c_uint8)
+_sig("ora_mt64_seed", None, C.POINTER(MT64), C.c_uint64)
+_sig("ora_mt64_next", C.c_uint64, C.POINTER(MT64))
+_sig("ora_ref_replay", C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_uint64,
+     C.c_void_p, C.c_void_p, _u64p)
+_sig("ora_ref_cmode_runs", C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+     C.c_uint64, C.c_double, C.c_double, C.c_double, _u64p, _u8p, C.POINTER(C.c_uint64))
+_sig("ora_lru_init", C.c_int, C.POINTER(LRU), C.c_int, C.c_int)
+_sig("ora_lru_free", None, C.POINTER(LRU))
+_sig("ora_lru_substep", C.c_int, C.POINTER(LRU), C.c_uint32, _u32p, C.c_int, _u32p, _missp,
+     C.POINTER(C.c_int), C.c_void_p)
+_sig("ora_deque_lru_run", C.c_int, C.c_int, _u32p, C.c_int, _u8p)
+_sig("ora_tslru_init", C.c_int, C.POINTER(TSLRU), C.c_int, C.c_int)
+_sig("ora_tslru_free", None, C.POINTER(TSLRU))
+_sig("ora_tslru_step", C.c_int, C.POINTER(TSLRU), _u32p, C.c_int, _u32p, _u32p, _u32p,
+     C.POINTER(C.c_int))
+_sig("ora_n_sets", C.c_int, C.POINTER(Geom))
+_sig("ora_max_sel_per_set", C.c_int, C.POINTER(Geom))
+_sig("ora_block_bytes", C.c_uint64, C.POINTER(Geom))
+_sig("ora_host_index", C.c_uint64, C.POINTER(Geom), C.c_uint32, C.c_uint32)
+_sig("ora_exec_create", C.c_void_p, C.POINTER(Geom))
+_sig("ora_exec_destroy", None, C.c_void_p)
+_sig("ora_exec_step", C.c_int, C.c_void_p, _u32p, _u32p, _u32p, _missp, _u64p, _u8p)
+_sig("ora_exec_state", None, C.c_void_p, _u32p, _u32p, _u32p)
+_sig("ora_ctx_uniform", None, C.c_uint64, C.c_int, C.c_int, C.c_int, _i32p)
+_sig("ora_selgen_max_blocks", C.c_int, C.POINTER(SelGen))
+_sig("ora_selgen_step", C.c_int, C.POINTER(SelGen), C.c_int, _u32p, _u32p)
+_sig("ora_host_elem", C.c_uint32, C.POINTER(Geom), C.c_uint64, C.c_uint32)
+_sig("ora_host_scale", C.c_float, C.POINTER(Geom), C.c_uint64, C.c_int)
+_sig("ora_host_block", None, C.POINTER(Geom), C.c_uint64, C.c_void_p, C.c_void_p)
+_sig("ora_host_fill", None, C.POINTER(Geom), C.c_void_p, C.c_void_p)
+_sig("ora_attention_f64", C.c_int, C.POINTER(Geom), _u32p, _f32p, _f64p)
+_sig("ora_attention_pool_f32", C.c_int, C.POINTER(Geom), _u32p, C.c_void_p, C.c_void_p,
+     _f32p, _f32p)
+_sig("ora_cpu_step", C.c_int, C.c_void_p, _u32p, C.c_void_p, C.c_void_p, C.c_void_p,
+     C.c_void_p, _f32p, _f32p, _u32p, _u32p, _missp, _u64p)
+
+
+def esize(dtype):
+    return {F32: 4, F16: 2, BF16: 2, FP8: 1}[dtype]
+
+
+# ---------------------------------------------------------------- reference replay
+def ref_replay(R, L, S, sel, hot, seed=42, events=True):
+    """Restated replay_miss_stream; returns (blocks u64, miss u8, selects, misses)."""
+    n = R * L * S * sel
+    blocks = np.zeros(n, np.uint64) if events else None
+    miss = np.zeros(n, np.uint8) if events else None
+    counts = np.zeros(2, np.uint64)
+    rc = lib.ora_ref_replay(R, L, S, sel, hot, seed,
+                            blocks.ctypes.data if events else None,
+                            miss.ctypes.data if events else None, counts)
+    if rc:
+        raise RuntimeError(f"ora_ref_replay rc={rc}")
+    return blocks, miss, int(counts[0]), int(counts[1])
+
+
+def ref_cmode_runs(R, L, S, sel, hot, c4, blocks, miss, min_mb=1.0, max_mb=4.0, target=4.0):
+    rb = C.c_uint64(0)
+    ev = lib.ora_ref_cmode_runs(R, L, S, sel, hot, c4, min_mb, max_mb, target,
+                                np.ascontiguousarray(blocks, np.uint64),
+                                np.ascontiguousarray(miss, np.uint8), C.byref(rb))
+    return int(ev), int(rb.value)
+
+
+# ---------------------------------------------------------------- executor
+class Executor:
+    """Oracle executor: one LRU set per (owner, layer, kv head)."""
+
+    def __init__(self, geom: Geom):
+        self.g = geom
+        self.ptr = lib.ora_exec_create(C.byref(geom))
+        if not self.ptr:
+            raise MemoryError("ora_exec_create")
+        self.n_sets = lib.ora_n_sets(C.byref(geom))
+        self.max_sel = lib.ora_max_sel_per_set(C.byref(geom))
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            lib.ora_exec_destroy(self.ptr)
+            self.ptr = None
+
+    def step(self, sel):
+        g = self.g
+        sel = np.ascontiguousarray(sel, np.uint32).reshape(-1)
+        slots = np.zeros(sel.size, np.uint32)
+        mc = np.zeros(self.n_sets, np.uint32)
+        misses = np.zeros(self.n_sets * self.max_sel, MISS_DTYPE)
+        counts = np.zeros(3, np.uint64)
+        flags = np.zeros(sel.size, np.uint8)
+        rc = lib.ora_exec_step(self.ptr, sel, slots, mc, misses, counts, flags)
+        if rc:
+            raise RuntimeError(f"ora_exec_step rc={rc}")
+        self.last_flags = flags
+        return slots, mc, misses.reshape(self.n_sets, self.max_sel), counts
+
+    def state(self):
+        cap = self.g.cap
+        fill = np.zeros(self.n_sets, np.uint32)
+        ord_ = np.zeros(self.n_sets * cap, np.uint32)
+        tag = np.zeros(self.n_sets * cap, np.uint32)
+        lib.ora_exec_state(self.ptr, fill, ord_, tag)
+        return fill, ord_.reshape(self.n_sets, cap), tag.reshape(self.n_sets, cap)
+
+
+def make_geom(**kw):
+    g = Geom()
+    defaults = dict(group=1, q_heads=None, head_dim=128, block_tokens=16, dtype=F16,
+                    granularity=0, host_blocks=1 << 16, seed=7, value_std=0.5)
+    defaults.update(kw)
+    if defaults["q_heads"] is None:
+        defaults["q_heads"] = defaults["kv_heads"]
+    for k, v in defaults.items():
+        setattr(g, k, v)
+    return g
+
+
+def selgen(n_req, n_layers, kv_heads, k, ctx_blocks, dist=1, zipf_s=1.1, reuse=0.66,
+           group=1, prefix_blocks=0, seed=1):
+    ctx = np.ascontiguousarray(ctx_blocks, np.int32)
+    s = SelGen(n_req, group, n_layers, kv_heads, k, dist, zipf_s, reuse, prefix_blocks, seed,
+               ctx.ctypes.data_as(C.POINTER(C.c_int)))
+    s._ctx = ctx  # keep alive
+    s._state = np.zeros(n_req * n_layers * kv_heads * k, np.uint32)
+    return s
+
+
+def selgen_step(s: SelGen, step):
+    """Selections of `step`; steps must be generated in order (state carries)."""
+    out = np.zeros(s.n_req * s.n_layers * s.kv_heads * s.k, np.uint32)
+    rc = lib.ora_selgen_step(C.byref(s), step, s._state, out)
+    if rc:
+        raise RuntimeError(f"ora_selgen_step rc={rc}")
+    return out
+
+
+def selgen_max_blocks(s: SelGen):
+    return lib.ora_selgen_max_blocks(C.byref(s))
+
+
+def ctx_uniform(seed, n_req, lo, hi):
+    out = np.zeros(n_req, np.int32)
+    lib.ora_ctx_uniform(seed, n_req, lo, hi, out)
+    return out
+
+
+def host_block(g: Geom, h):
+    bb = lib.ora_block_bytes(C.byref(g))
+    buf = np.zeros(bb, np.uint8)
+    sc = np.zeros(2, np.float32)
+    lib.ora_host_block(C.byref(g), h, buf.ctypes.data, sc.ctypes.data)
+    return buf, sc
+
+
+def host_fill(g: Geom):
+    bb = lib.ora_block_bytes(C.byref(g))
+    host = np.zeros(g.host_blocks * bb, np.uint8)
+    sc = np.zeros(g.host_blocks * 2, np.float32)
+    lib.ora_host_fill(C.byref(g), host.ctypes.data, sc.ctypes.data)
+    return host, sc
+
+
+def attention_f64(g: Geom, sel, q):
+    out = np.zeros(q.size, np.float64)
+    rc = lib.ora_attention_f64(C.byref(g), np.ascontiguousarray(sel, np.uint32).reshape(-1),
+                               np.ascontiguousarray(q, np.float32).reshape(-1), out)
+    if rc:
+        raise RuntimeError("ora_attention_f64")
+    return out.reshape(q.shape)
+
+
+def host_index(g: Geom, set_id, block):
+    return int(lib.ora_host_index(C.byref(g), set_id, block))
