@@ -54,7 +54,10 @@ template <int DT>
 __device__ inline void decode(const u32x4& w, float* f) {
   if constexpr (DT == FERRY_F32) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = __builtin_bit_cast(float, w[i]);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t u = w[i];  // bit_cast of a vector element would read element 0
+      f[i] = __builtin_bit_cast(float, u);
+    }
   } else if constexpr (DT == FERRY_F16) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -63,7 +63,7 @@ int ferry_ctx_uniform(uint64_t seed, int32_t n_req, int32_t lo, int32_t hi, int3
 
 int ferry_selgen_create(const ferry_selgen_config* cfg, const int32_t* ctx_blocks, ferry_selgen** out) {
   if (!cfg || !ctx_blocks || !out) return FERRY_EINVAL;
-  if (cfg->n_req < 1 || cfg->group < 1 || cfg->n_layers < 1 || cfg->kv_heads < 1 || cfg->k < 1 ||
+  if (cfg->n_req < 1 || cfg->n_req > 65536 || cfg->group < 1 || cfg->n_layers < 1 || cfg->kv_heads < 1 || cfg->k < 1 ||
       cfg->reuse < 0.0 || cfg->reuse > 1.0 || cfg->prefix_blocks < 0)
     return FERRY_EINVAL;
   ferry_selgen* g = new ferry_selgen();
@@ -130,9 +130,10 @@ int ferry_selgen_step(ferry_selgen* g, int32_t step, uint32_t* out) {
           uint32_t* st = g->state.data() + row;
           uint32_t* so = out + row;
           const uint64_t off = mix64(c.seed ^ kSaltPerm, (uint64_t)((o * L + l) * H + h)) % (uint64_t)np;
+          // draw index of (step, r, l, h): independent of the batch size
           const uint64_t base =
-              ((((uint64_t)step * (uint64_t)c.n_req + (uint64_t)r) * (uint64_t)L + (uint64_t)l) *
-                   (uint64_t)H + (uint64_t)h) * (uint64_t)kDrawLimit;
+              (((((uint64_t)step << 16) | (uint64_t)r) * (uint64_t)L + (uint64_t)l) * (uint64_t)H +
+               (uint64_t)h) * (uint64_t)kDrawLimit;
           int got = 0;
           if (carry)
             for (int j = 0; j < k; ++j)

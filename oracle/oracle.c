@@ -772,8 +772,8 @@ int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
             ora_mix64(s->seed ^ SALT_PERM, (uint64_t)((o * L + l) * H + h)) %
             (uint64_t)np;
         const uint64_t base =
-            ((((uint64_t)step * (uint64_t)s->n_req + (uint64_t)r) * (uint64_t)L +
-              (uint64_t)l) * (uint64_t)H + (uint64_t)h) * (uint64_t)DRAW_LIMIT;
+            (((((uint64_t)step << 16) | (uint64_t)r) * (uint64_t)L + (uint64_t)l) *
+                 (uint64_t)H + (uint64_t)h) * (uint64_t)DRAW_LIMIT;
         int got = 0;
         if (carry)
           for (int j = 0; j < k; ++j) {
