@@ -58,15 +58,48 @@ def parse():
                     help="summarise a rocprofv3 results database instead of benchmarking")
     ap.add_argument("--last", type=int, default=0,
                     help="with --rocprof-summary: also average the last N dispatches per kernel")
+    ap.add_argument("--pmc-copy", action="store_true",
+                    help="first run a plain 1 GiB device copy (counter calibration)")
+    ap.add_argument("--pmc-summary", metavar="CSV",
+                    help="summarise a rocprofv3 counter_collection.csv instead of benchmarking")
     return ap.parse_args()
+
+
+def pmc_summary(csv_path, last):
+    """Per-kernel average of each counter over the last N dispatches (markdown)."""
+    import csv
+
+    per = {}
+    with open(csv_path) as f:
+        for row in csv.DictReader(f):
+            name = row["Kernel_Name"].split("(")[0].replace("void ", "")
+            key = (name, row["Counter_Name"])
+            per.setdefault(key, {})
+            did = int(row["Dispatch_Id"])
+            per[key][did] = per[key].get(did, 0.0) + float(row["Counter_Value"])
+    lines = ["| kernel | counter | dispatches | avg per dispatch (all) | avg (last N) |",
+             "|---|---|---|---|---|"]
+    for (name, ctr), d in sorted(per.items()):
+        vals = [d[k] for k in sorted(d)]
+        n = last or len(vals)
+        lines.append(f"| `{name}` | {ctr} | {len(vals)} | {np.mean(vals):.1f} | "
+                     f"{np.mean(vals[-n:]):.1f} |")
+    return "\n".join(lines)
 
 
 def rocprof_summary(db_path, last):
     """Per-kernel dispatch statistics from a rocprofv3 database (markdown)."""
     import sqlite3
 
-    cur = sqlite3.connect(db_path).cursor()
-    rows = cur.execute("select name, start, end from kernels order by start").fetchall()
+    if db_path.endswith(".csv"):  # rocprofv3 --output-format csv kernel_trace.csv
+        import csv
+
+        with open(db_path) as f:
+            rows = sorted(((r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+                           for r in csv.DictReader(f)), key=lambda x: x[1])
+    else:
+        cur = sqlite3.connect(db_path).cursor()
+        rows = cur.execute("select name, start, end from kernels order by start").fetchall()
     per = {}
     for name, t0, t1 in rows:
         per.setdefault(name.split("(")[0].replace("void ", ""), []).append((t1 - t0) / 1e3)
@@ -128,6 +161,9 @@ def main():
     if a.rocprof_summary:
         print(rocprof_summary(a.rocprof_summary, a.last))
         return
+    if a.pmc_summary:
+        print(pmc_summary(a.pmc_summary, a.last))
+        return
     if a.gpus != 1:
         print(f"bench.py runs on exactly one GPU (this build has no multi-GPU path); "
               f"got --gpus {a.gpus}", file=sys.stderr)
@@ -141,6 +177,12 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream()
+    if a.pmc_copy:  # known-size copy: reads and writes exactly 1 GiB
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     ctx = F.ctx_uniform(2, B, clo, chi)
     sg = F.SelGen(B, L, H, k, ctx, dist=1, zipf_s=zipf, reuse=reuse, seed=3)

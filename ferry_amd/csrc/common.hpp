@@ -150,8 +150,12 @@ __device__ inline uint64_t first_lane_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 // Ordering point for one wavefront's global + LDS traffic between phases.
+// Every word that other lanes rewrite is read with an L1-bypassing relaxed
+// atomic (aload) and written with atomics that complete in L2, so waiting for
+// this wave's outstanding accesses (workgroup scope: s_waitcnt, no L2
+// writeback or invalidate) is all the ordering one wavefront needs.
 __device__ inline void wave_fence() {
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent");
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   __builtin_amdgcn_wave_barrier();
 }
 // L1-bypassing relaxed accesses for words other lanes of the wave rewrite.
