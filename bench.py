@@ -13,12 +13,21 @@ Default workload (the 7B decode shape): 64 requests x 32 layers x 32 heads
 gives ~10% misses in steady state.  Selections and q are generated and
 uploaded before the timed region; the host tier is pinned host memory.
 
+The timed steps run ferry_decode_step: layers are cut into --chunks ranges
+and the bookkeeping + fetch of range c+1 run on a side stream while range c
+attends on the main stream.
+
 Prints ONE JSON line.  `value` is whole-step decode tokens/s (B / step time).
-Kernel rates come from HIP events on the executor's stream:
+Kernel rates come from HIP events around separate launches of each kernel:
   roofline        attention kernel vs 8 TB/s HBM (algorithmic bytes/launch)
   roofline_fetch  fetch kernel vs the PCIe Gen5 x16 host link (63.0 GB/s)
 cpu_baseline times the oracle's C restatement of the same step (1 thread) on
-2 of the 64 requests.
+2 of the requests (a whole prefix group for grouped workloads).
+
+Other workloads (--workload): gqa128k (long-context GQA, bf16, ~30% misses),
+prefix_fp8 (shared-prefix groups, fp8 + scales, cross-request dedup), skew
+(lognormal per-request miss counts; prints a stealing on/off sweep over Zipf
+skew with 304 persistent fetch workgroups), small.
 """
 import argparse
 import json
@@ -36,9 +45,21 @@ HBM_PEAK_GBS = 8000.0
 LINK_PEAK_GBS = 32e9 * 16 * 128 / 130 / 8 / 1e9  # PCIe Gen5 x16, one direction
 
 WORKLOADS = {
-    # name: (B, L, Hkv, Hq, k, ctx_lo_blocks, ctx_hi_blocks, slots_per_set, dtype, zipf, reuse)
-    "7b": (64, 32, 32, 32, 64, 256, 2048, 320, "f16", 1.1, 0.66),
-    "small": (8, 4, 8, 8, 64, 256, 2048, 320, "f16", 1.1, 0.66),
+    # 7B-shape steady decode (the headline)
+    "7b": dict(B=64, L=32, Hq=32, Hkv=32, k=64, ctx=(256, 2048), C=320, dtype="f16", zipf=1.1,
+               reuse=0.66, group=1, prefix=0),
+    # long-context GQA, host-tier heavy (~30% misses), bf16
+    "gqa128k": dict(B=16, L=32, Hq=32, Hkv=8, k=128, ctx=(8192, 8192), C=128, dtype="bf16",
+                    zipf=1.1, reuse=0.66, group=1, prefix=0),
+    # shared-prefix agent decode: 8 groups x 16 requests, 8192-token prefix + [512, 4096]
+    # private tokens, GQA 32/8, fp8 E4M3 with per-block scales; dedup across the group
+    "prefix_fp8": dict(B=128, L=32, Hq=32, Hkv=8, k=64, ctx=(32, 256), C=1536, dtype="fp8",
+                       zipf=1.1, reuse=0.66, group=16, prefix=512),
+    # skewed per-request miss counts (lognormal(2, 1.2) fresh blocks per step), 7B shape
+    "skew": dict(B=64, L=32, Hq=32, Hkv=32, k=64, ctx=(256, 2048), C=320, dtype="f16", zipf=1.0,
+                 reuse=0.66, group=1, prefix=0),
+    "small": dict(B=8, L=4, Hq=8, Hkv=8, k=64, ctx=(256, 2048), C=320, dtype="f16", zipf=1.1,
+                  reuse=0.66, group=1, prefix=0),
 }
 
 
@@ -54,6 +75,8 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--steal", type=int, default=1)
     ap.add_argument("--workers", type=int, default=0)
+    ap.add_argument("--chunks", type=int, default=8,
+                    help="layer chunks of the fetch/attention overlap (1 = no side stream)")
     ap.add_argument("--rocprof-summary", metavar="DB",
                     help="summarise a rocprofv3 results database instead of benchmarking")
     ap.add_argument("--last", type=int, default=0,
@@ -114,20 +137,39 @@ def rocprof_summary(db_path, last):
     return "\n".join(lines)
 
 
-def cpu_baseline(B, L, H, Hq, k, ctx, C, max_blocks, sg_seed, zipf, reuse, host_bytes,
-                 host_blocks, n_req, steps):
+def contexts(F, w):
+    """Per-request context lengths (blocks) and the selection generator."""
+    lo, hi = w["ctx"]
+    ctx = F.ctx_uniform(2, w["B"], lo, hi) + w["prefix"]
+    return ctx
+
+
+def lognormal_reuse(B, k, mu=2.0, sigma=1.2, seed=17):
+    """Per-request reuse so that the fresh (re-drawn) blocks of a (request,
+    layer, head) per step follow lognormal(mu, sigma), capped at k."""
+    z = np.random.default_rng(seed).standard_normal(B)
+    fresh = np.minimum(np.exp(mu + sigma * z), k)
+    return np.clip(1.0 - fresh / k, 0.0, 1.0)
+
+
+def cpu_baseline(w, ctx, max_blocks, host_bytes, host_scales, host_blocks, n_req, steps, reuse_r):
     """Oracle C path (bookkeeping + memcpy gather + fp32 attention), 1 thread,
     on the first n_req requests of the same workload and the same host tier."""
-    import ctypes as Cty
     from oracle import pyoracle as O
 
-    g = O.make_geom(n_req=n_req, n_layers=L, kv_heads=H, q_heads=Hq, k=k, cap=C,
-                    max_blocks=max_blocks, dtype=O.F16, host_blocks=host_blocks, seed=7,
+    dt = {"f16": O.F16, "bf16": O.BF16, "fp8": O.FP8, "f32": O.F32}[w["dtype"]]
+    L, H, Hq, k, C = w["L"], w["Hkv"], w["Hq"], w["k"], w["C"]
+    n_req = max(n_req, w["group"])
+    g = O.make_geom(n_req=n_req, group=w["group"], n_layers=L, kv_heads=H, q_heads=Hq, k=k, cap=C,
+                    max_blocks=max_blocks, dtype=dt, host_blocks=host_blocks, seed=7,
                     value_std=0.5)
     ex = O.Executor(g)
-    sg = O.selgen(n_req, L, H, k, ctx[:n_req], dist=1, zipf_s=zipf, reuse=reuse, seed=sg_seed)
-    bb = O.lib.ora_block_bytes(Cty.byref(g))
+    sg = O.selgen(n_req, L, H, k, ctx[:n_req], dist=1, zipf_s=w["zipf"], reuse=w["reuse"],
+                  group=w["group"], prefix_blocks=w["prefix"], seed=3,
+                  reuse_r=None if reuse_r is None else reuse_r[:n_req])
+    bb = O.lib.ora_block_bytes(O.C.byref(g))
     pool = np.zeros(ex.n_sets * C * bb, np.uint8)
+    pscale = np.zeros(ex.n_sets * C * 2, np.float32) if host_scales is not None else None
     rng = np.random.default_rng(1)
     q = rng.standard_normal((n_req, L, Hq, 128)).astype(np.float32)
     out = np.zeros(q.size, np.float32)
@@ -139,21 +181,135 @@ def cpu_baseline(B, L, H, Hq, k, ctx, C, max_blocks, sg_seed, zipf, reuse, host_
     for t in range(steps + 1):  # step 0 is the cold fill, not timed
         sel = O.selgen_step(sg, t)
         t0 = time.perf_counter()
-        rc = O.lib.ora_cpu_step(ex.ptr, sel, host_bytes.ctypes.data, None, pool.ctypes.data,
-                                None, q.reshape(-1), out, slots, mc, ms, cnt)
-        dt = time.perf_counter() - t0
+        rc = O.lib.ora_cpu_step(ex.ptr, sel, host_bytes.ctypes.data,
+                                None if host_scales is None else host_scales.ctypes.data,
+                                pool.ctypes.data, None if pscale is None else pscale.ctypes.data,
+                                q.reshape(-1), out, slots, mc, ms, cnt)
+        dt_s = time.perf_counter() - t0
         if rc:
             raise RuntimeError(f"ora_cpu_step rc={rc}")
         if t:
-            times.append(dt)
+            times.append(dt_s)
             misses.append(int(cnt[1]))
     t_step = float(np.mean(times))
     return {"value": round(n_req / t_step, 3), "unit": "tok/s", "cores": 1, "kind": "port",
             "sample": f"oracle C step (bookkeeping + memcpy gather + fp32 attention) on "
-                      f"{n_req} of {B} requests x {L} layers x {H} heads, {steps} steps after "
-                      f"one untimed cold step; {t_step * 1e3:.0f} ms/step",
+                      f"{n_req} of {w['B']} requests x {L} layers x {H} kv heads, {steps} steps "
+                      f"after one untimed cold step; {t_step * 1e3:.0f} ms/step",
             "miss_blocks_per_s": round(float(np.mean(misses)) / t_step, 1),
             "ms_per_step": round(t_step * 1e3, 1)}
+
+
+def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_cpu=True):
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()  # default priority
+    B, L, H, Hq, k, C = w["B"], w["L"], w["Hkv"], w["Hq"], w["k"], w["C"]
+    dtype = {"f16": F.F16, "bf16": F.BF16, "fp8": F.FP8, "f32": F.F32}[w["dtype"]]
+    steal = a.steal if steal is None else steal
+    workers = a.workers if workers is None else workers
+    zipf = w["zipf"] if zipf is None else zipf
+    ctx = contexts(F, w)
+    sg = F.SelGen(B, L, H, k, ctx, dist=1, zipf_s=zipf, reuse=w["reuse"], group=w["group"],
+                  prefix_blocks=w["prefix"], seed=3)
+    reuse_r = None
+    if a.workload == "skew":
+        reuse_r = lognormal_reuse(B, k)
+        sg.set_reuse(reuse_r)
+    n_steps = a.warmup + 2 * a.steps
+    t0 = time.perf_counter()
+    sels = [torch.from_numpy(sg.step(t).view(np.int32)).to(dev) for t in range(n_steps)]
+    gen_s = time.perf_counter() - t0
+    qs = [torch.randn((B, L, Hq, 128), device=dev, dtype=torch.float32) for _ in range(2)]
+    out = torch.empty_like(qs[0])
+    if assign is None:
+        assign = F.ASSIGN_AFFINITY if a.workload == "skew" else F.ASSIGN_SPREAD
+    ex = F.Executor(B, L, H, k, C, sg.max_blocks, q_heads=Hq, group=w["group"], dtype=dtype,
+                    host_blocks=a.host_blocks, fetch_workers=workers, steal=steal, assign=assign)
+    ex.hosttier_fill()
+    bufs = ex.alloc_step_buffers()
+    torch.cuda.synchronize()
+
+    def step(t):
+        if a.chunks > 1:
+            ex.decode_step(sels[t], qs[t & 1], bufs, out, chunks=a.chunks, stream=stream,
+                           side_stream=side)
+        else:
+            ex.decode_step(sels[t], qs[t & 1], bufs, out, chunks=1, stream=stream)
+
+    for t in range(a.warmup):
+        step(t)
+    torch.cuda.synchronize()
+    st0 = ex.stats()
+    # timed region: K whole steps, synchronised on both sides
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(a.warmup, a.warmup + a.steps):
+        step(t)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    st1 = ex.stats()
+    if st1["device_error"]:
+        raise RuntimeError(f"device error {st1['device_error']}")
+    timed_misses = st1["misses"] - st0["misses"]
+
+    # per-kernel durations: K further steps, each kernel bracketed by HIP events
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
+    m0, s0 = ex.stats()["misses"], ex.stats()["steals"]
+    for i in range(a.steps):
+        t = a.warmup + a.steps + i
+        e = evs[i]
+        e[0].record(stream)
+        ex.bookkeep_step(sels[t], bufs, flags=False)
+        e[1].record(stream)
+        ex.missq_drain()
+        e[2].record(stream)
+        ex.sparse_decode(qs[t & 1], bufs["slots"], out)
+        e[3].record(stream)
+    torch.cuda.synchronize()
+    st2 = ex.stats()
+    ev_misses = st2["misses"] - m0
+    t_book = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    t_fetch = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    t_attn = float(np.mean([e[2].elapsed_time(e[3]) for e in evs]))
+
+    sel_per_step = B * L * H * k
+    bb = ex.block_bytes
+    scale_bytes = 8 if dtype == F.FP8 else 0
+    attn_bytes = sel_per_step * (bb + scale_bytes) + 2 * B * L * Hq * 128 * 4 + sel_per_step * 4
+    fetch_bytes = ev_misses / a.steps * (bb + scale_bytes)
+    ms_step = elapsed / a.steps * 1e3
+    attn_gbs = attn_bytes / (t_attn * 1e-3) / 1e9
+    link_gbs = fetch_bytes / (t_fetch * 1e-3) / 1e9
+    G = Hq // H
+    res = {
+        "ms_per_step": round(ms_step, 3),
+        "value": round(B / (ms_step * 1e-3), 2),
+        "miss_rate": round(timed_misses / (a.steps * sel_per_step), 4),
+        "miss_blocks_per_s": round(timed_misses / elapsed, 1),
+        "miss_blocks_per_s_fetch_kernel": round(ev_misses / a.steps / (t_fetch * 1e-3), 1),
+        "attention_tok_per_s": round(B / (t_attn * 1e-3), 1),
+        "kernel_ms": {"bookkeep": round(t_book, 4), "fetch": round(t_fetch, 4),
+                      "attention": round(t_attn, 4)},
+        "roofline": {"bound": "hbm", "kernel": f"k_attn<{w['dtype']},{G}>",
+                     "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "roofline_fetch": {"bound": "host-link", "kernel": f"k_fetch<{bb // 1024}>",
+                           "achieved": round(link_gbs, 2), "peak": round(LINK_PEAK_GBS, 2),
+                           "unit": "GB/s", "frac": round(link_gbs / LINK_PEAK_GBS, 4)},
+        "steals_per_step": round((st2["steals"] - s0) / a.steps, 1),
+        "selection_gen_s": round(gen_s, 2),
+        "config_extra": {"slots_per_set": C, "host_tier_blocks": a.host_blocks,
+                         "fetch_workers": ex.cfg.fetch_workers, "steal": steal,
+                         "assign": "affinity" if assign == F.ASSIGN_AFFINITY else "spread",
+                         "chunks": a.chunks, "zipf": zipf},
+    }
+    if want_cpu and not a.no_cpu:
+        host, hsc = ex.hosttier_array()
+        res["cpu_baseline"] = cpu_baseline(w, ctx, sg.max_blocks, host, hsc, a.host_blocks,
+                                           a.cpu_reqs, a.cpu_steps, reuse_r)
+    ex.close()
+    return res
 
 
 def main():
@@ -172,129 +328,62 @@ def main():
 
     import ferry_amd as F
 
-    B, L, H, Hq, k, clo, chi, C, dts, zipf, reuse = WORKLOADS[a.workload]
-    dtype = {"f16": F.F16, "bf16": F.BF16, "fp8": F.FP8, "f32": F.F32}[dts]
-    dev = torch.device("cuda", 0)
     torch.cuda.set_device(0)
-    stream = torch.cuda.current_stream()
     if a.pmc_copy:  # known-size copy: reads and writes exactly 1 GiB
-        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-
-    ctx = F.ctx_uniform(2, B, clo, chi)
-    sg = F.SelGen(B, L, H, k, ctx, dist=1, zipf_s=zipf, reuse=reuse, seed=3)
-    n_steps = a.warmup + a.steps
-    t0 = time.perf_counter()
-    sels = [torch.from_numpy(sg.step(t).view(np.int32)).to(dev) for t in range(n_steps)]
-    gen_s = time.perf_counter() - t0
-    qs = [torch.randn((B, L, Hq, 128), device=dev, dtype=torch.float32) for _ in range(2)]
-    out = torch.empty_like(qs[0])
-
-    ex = F.Executor(B, L, H, k, C, sg.max_blocks, q_heads=Hq, dtype=dtype,
-                    host_blocks=a.host_blocks, fetch_workers=a.workers, steal=a.steal)
-    ex.hosttier_fill()
-    bufs = ex.alloc_step_buffers()
-    torch.cuda.synchronize()
-
-    def step(t, ev=None):
-        if ev is not None:
-            ev[0].record(stream)
-        ex.bookkeep_step(sels[t], bufs, flags=False)
-        if ev is not None:
-            ev[1].record(stream)
-        ex.missq_drain()
-        if ev is not None:
-            ev[2].record(stream)
-        ex.sparse_decode(qs[t & 1], bufs["slots"], out)
-        if ev is not None:
-            ev[3].record(stream)
-
-    for t in range(a.warmup):
-        step(t)
-    torch.cuda.synchronize()
-    st0 = ex.stats()
-    # timed region: K whole steps
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for t in range(a.warmup, n_steps):
-        step(t)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    st1 = ex.stats()
-    if st1["device_error"]:
-        raise RuntimeError(f"device error {st1['device_error']}")
-    timed_misses = st1["misses"] - st0["misses"]
-
-    # per-kernel durations: the same steps again would change the LRU state, so
-    # time K further steps with events between the launches
-    extra = [torch.from_numpy(sg.step(n_steps + i).view(np.int32)).to(dev) for i in range(a.steps)]
-    sels.extend(extra)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
-    miss_before = ex.stats()["misses"]
-    for i in range(a.steps):
-        step(n_steps + i, evs[i])
-    torch.cuda.synchronize()
-    ev_misses = ex.stats()["misses"] - miss_before
-    t_book = np.mean([e[0].elapsed_time(e[1]) for e in evs])
-    t_fetch = np.mean([e[1].elapsed_time(e[2]) for e in evs])
-    t_attn = np.mean([e[2].elapsed_time(e[3]) for e in evs])
-
-    sel_per_step = B * L * H * k
-    bb = ex.block_bytes
-    attn_bytes = sel_per_step * bb + 2 * B * L * Hq * 128 * 4 + sel_per_step * 4
-    fetch_bytes = ev_misses / a.steps * bb
-    ms_step = elapsed / a.steps * 1e3
-    attn_gbs = attn_bytes / (t_attn * 1e-3) / 1e9
-    link_gbs = fetch_bytes / (t_fetch * 1e-3) / 1e9
-
+    w = WORKLOADS[a.workload]
+    if a.workload == "skew":
+        # stealing on vs off over the Zipf skew sweep, 304 persistent workgroups,
+        # request-affinity assignment of misses to workgroups
+        rows = []
+        for s in (0.6, 1.0, 1.4):
+            for steal in (0, 1):
+                r = run(a, w, F, torch, steal=steal, workers=304, zipf=s, want_cpu=False)
+                rows.append({"zipf": s, "steal": steal, "fetch_ms": r["kernel_ms"]["fetch"],
+                             "ms_per_step": r["ms_per_step"], "miss_rate": r["miss_rate"],
+                             "link_gbs": r["roofline_fetch"]["achieved"],
+                             "steals_per_step": r["steals_per_step"]})
+                print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        print(json.dumps({"workload": "skew", "rows": rows}), flush=True)
+        return
+    r = run(a, w, F, torch)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
+    if a.workload == "7b" and os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("attention_bytes_per_launch")
-
+    r["roofline"]["traffic"] = traffic
+    lo, hi = w["ctx"]
+    desc = (f"B={w['B']}, L={w['L']}, Hq={w['Hq']}, Hkv={w['Hkv']}, D=128, {w['dtype']} KV, "
+            f"16-token blocks, ctx {'U[%d,%d]' % (lo * 16, hi * 16) if lo != hi else lo * 16} "
+            f"tokens{' + %d shared prefix tokens in groups of %d' % (w['prefix'] * 16, w['group']) if w['group'] > 1 else ''}, "
+            f"top-k {w['k']} (Zipf {w['zipf']}, reuse {w['reuse']}), {w['C']} slots/set")
     res = {
         "metric": METRIC,
-        "value": round(B / (ms_step * 1e-3), 2),
+        "value": r["value"],
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(ms_step, 3),
+        "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": dts,
+        "dtype": w["dtype"],
         "data": "synthetic",
-        "config": {
-            "workload": f"7B-shape steady decode ({a.workload}): B={B}, L={L}, Hq={Hq}, Hkv={H}, "
-                        f"D=128, {dts} KV, 16-token blocks, ctx U[{clo * 16},{chi * 16}] tokens, "
-                        f"top-k {k} (Zipf {zipf}, reuse {reuse}), {C} slots/set",
-            "batch": B, "layers": L, "q_heads": Hq, "kv_heads": H, "top_k": k,
-            "slots_per_set": C, "host_tier_blocks": a.host_blocks,
-            "fetch_workers": ex.cfg.fetch_workers, "steal": a.steal,
-        },
-        "miss_rate": round(timed_misses / (a.steps * sel_per_step), 4),
-        "miss_blocks_per_s": round(timed_misses / elapsed, 1),
-        "miss_blocks_per_s_fetch_kernel": round(ev_misses / a.steps / (t_fetch * 1e-3), 1),
-        "attention_tok_per_s": round(B / (t_attn * 1e-3), 1),
-        "kernel_ms": {"bookkeep": round(float(t_book), 4), "fetch": round(float(t_fetch), 4),
-                      "attention": round(float(t_attn), 4)},
-        "roofline": {"bound": "hbm", "kernel": "k_attn<f16,1>", "achieved": round(attn_gbs, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
-        "roofline_fetch": {"bound": "host-link", "kernel": "k_fetch<8>",
-                           "achieved": round(link_gbs, 2), "peak": round(LINK_PEAK_GBS, 2),
-                           "unit": "GB/s", "frac": round(link_gbs / LINK_PEAK_GBS, 4)},
-        "selection_gen_s": round(gen_s, 2),
+        "config": dict({"workload": f"{a.workload}: {desc}", "batch": w["B"],
+                        "layers": w["L"], "q_heads": w["Hq"], "kv_heads": w["Hkv"],
+                        "top_k": w["k"]}, **r.pop("config_extra")),
     }
-    if not a.no_cpu:
-        host, _ = ex.hosttier_array()
-        res["cpu_baseline"] = cpu_baseline(B, L, H, Hq, k, ctx, C, sg.max_blocks, 3, zipf, reuse,
-                                           host, a.host_blocks, min(a.cpu_reqs, B), a.cpu_steps)
+    for key in ("miss_rate", "miss_blocks_per_s", "miss_blocks_per_s_fetch_kernel",
+                "attention_tok_per_s", "kernel_ms", "roofline", "roofline_fetch",
+                "steals_per_step", "selection_gen_s", "cpu_baseline"):
+        if key in r:
+            res[key] = r[key]
     print(json.dumps(res), flush=True)
 
 

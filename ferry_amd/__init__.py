@@ -95,6 +95,10 @@ _PROTOS = {
     "ferry_sets_state": (C.c_int, [_vp, _vp, _vp, _vp]),
     "ferry_fetch_step": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ferry_bookkeep_step": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ferry_bookkeep_layers": (C.c_int, [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ferry_sparse_decode_layers": (C.c_int, [_vp, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "ferry_decode_step": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp]),
+    "ferry_selgen_set_reuse": (C.c_int, [_vp, _vp]),
     "ferry_missq_push": (C.c_int, [_vp, _vp, C.c_uint32, _vp]),
     "ferry_missq_drain": (C.c_int, [_vp, _vp]),
     "ferry_sparse_decode": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
@@ -194,6 +198,25 @@ class Executor:
                                        _ptr(bufs["miss_count"]), _ptr(bufs["misses"]),
                                        _ptr(bufs["miss_flag"]) if flags else None,
                                        _stream(stream)), "ferry_bookkeep_step")
+
+    def bookkeep_layers(self, l0, nl, sel, bufs, stream=None, flags=True):
+        _check(lib.ferry_bookkeep_layers(self._h, l0, nl, _ptr(sel), _ptr(bufs["slots"]),
+                                         _ptr(bufs["miss_count"]), _ptr(bufs["misses"]),
+                                         _ptr(bufs["miss_flag"]) if flags else None,
+                                         _stream(stream)), "ferry_bookkeep_layers")
+
+    def sparse_decode_layers(self, l0, nl, q, slots, out, stream=None):
+        _check(lib.ferry_sparse_decode_layers(self._h, l0, nl, _ptr(q), _ptr(slots), _ptr(out),
+                                              _stream(stream)), "ferry_sparse_decode_layers")
+
+    def decode_step(self, sel, q, bufs, out, chunks=8, stream=None, side_stream=None):
+        """Whole step; fetch of layer chunk c+1 (side stream) overlaps attention
+        of chunk c (stream).  side_stream None runs everything on one stream."""
+        _check(lib.ferry_decode_step(self._h, _ptr(sel), _ptr(q), _ptr(bufs["slots"]), _ptr(out),
+                                     _ptr(bufs["miss_count"]), _ptr(bufs["misses"]), chunks,
+                                     _stream(stream),
+                                     None if side_stream is None else _stream(side_stream)),
+               "ferry_decode_step")
 
     def missq_push(self, misses, n, stream=None):
         _check(lib.ferry_missq_push(self._h, _ptr(misses), n, _stream(stream)), "ferry_missq_push")
@@ -302,6 +325,12 @@ class SelGen:
         _check(lib.ferry_selgen_max_blocks(h, C.byref(mb)), "ferry_selgen_max_blocks")
         self.max_blocks = mb.value
         self.shape = (n_req, n_layers, kv_heads, k)
+
+    def set_reuse(self, reuse):
+        """Per-request reuse probabilities (None: the configured one for all)."""
+        self._reuse = None if reuse is None else np.ascontiguousarray(reuse, np.float64)
+        _check(lib.ferry_selgen_set_reuse(self._h, None if self._reuse is None
+                                          else self._reuse.ctypes.data), "ferry_selgen_set_reuse")
 
     def step(self, step):
         out = np.zeros(self.shape, np.uint32)

@@ -94,8 +94,8 @@ __global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q
                                               const uint32_t* __restrict__ slots,
                                               const uint8_t* __restrict__ pool,
                                               const float* __restrict__ pool_scales,
-                                              float* __restrict__ out, float qscale,
-                                              int* __restrict__ err) {
+                                              float* __restrict__ out, float qscale, int l0,
+                                              int nl, int* __restrict__ err) {
   constexpr int ES = DT == FERRY_F32 ? 4 : (DT == FERRY_FP8_E4M3 ? 1 : 2);
   constexpr int D = 128, T = 16;
   constexpr int EPV = 16 / ES;   // elements per 16-byte word
@@ -107,9 +107,10 @@ __global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q
 
   __shared__ float red[4][G][LPT][EPV + 2];
 
-  const int row = blockIdx.x;  // (r * L + l) * Hkv + h
-  const int h = row % g.Hkv;
-  const int rl = row / g.Hkv;
+  // (request, layer in [l0, l0 + nl), kv head) of this workgroup
+  const int h = blockIdx.x % g.Hkv;
+  const int rl = (blockIdx.x / (nl * g.Hkv)) * g.L + l0 + (blockIdx.x / g.Hkv) % nl;
+  const int row = rl * g.Hkv + h;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int dg = lane % LPT;
 
@@ -130,25 +131,49 @@ __global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q
     for (int e = 0; e < EPV; ++e) acc[gq][e] = 0.0f;
   }
 
+  // Slot ids of this wavefront's blocks (j = wave, wave+4, ...), 64 at a time,
+  // one per lane; each block reads its id with readlane (no dependent load).
   const uint32_t* sl = slots + (size_t)row * g.k;
   const int k = g.k;
-  for (int j = wave; j < k; j += 4) {
-    uint64_t slot = sl[j];
+  const int nb = k > wave ? (k - wave + 3) / 4 : 0;
+  auto slot_of = [&](uint32_t sidx, int i) -> uint64_t {
+    uint64_t slot = (uint32_t)__builtin_amdgcn_readlane((int)sidx, i & 63);
     if (slot >= g.pool_slots) {  // never read outside the pool
       set_error(err, FERRY_ERANGE);
       slot = 0;
     }
+    return slot;
+  };
+  auto load_block = [&](uint64_t slot, u32x4* kr, u32x4* vr) {
     const u32x4* kp = reinterpret_cast<const u32x4*>(pool + slot * g.bb);
     const u32x4* vp = kp + TILE_WORDS;
-    u32x4 kr[NLD], vr[NLD];
 #pragma unroll
     for (int ld = 0; ld < NLD; ++ld) kr[ld] = kp[ld * 64 + lane];
 #pragma unroll
     for (int ld = 0; ld < NLD; ++ld) vr[ld] = vp[ld * 64 + lane];
+  };
+  uint32_t sidx = 0;
+  u32x4 kr[NLD], vr[NLD], nk[NLD], nv[NLD];
+  uint64_t cur = 0;
+  if (nb > 0) {
+    sidx = lane < nb ? sl[wave + 4 * lane] : 0u;
+    cur = slot_of(sidx, 0);
+    load_block(cur, kr, vr);
+  }
+  // Double-buffer K/V (next block in flight while this one is consumed) where
+  // the registers allow it; wide GQA groups keep occupancy instead.
+  constexpr bool kPrefetch = G <= 2;
+  for (int i = 0; i < nb; ++i) {
+    uint64_t nxt = 0;
+    if (i + 1 < nb) {
+      if (((i + 1) & 63) == 0) sidx = (lane + i + 1) < nb ? sl[wave + 4 * (lane + i + 1)] : 0u;
+      nxt = slot_of(sidx, i + 1);
+      if constexpr (kPrefetch) load_block(nxt, nk, nv);
+    }
     float ks = 1.0f, vs = 1.0f;
     if constexpr (DT == FERRY_FP8_E4M3) {
-      ks = pool_scales[2 * slot] * 256.0f;
-      vs = pool_scales[2 * slot + 1] * 256.0f;
+      ks = pool_scales[2 * cur] * 256.0f;
+      vs = pool_scales[2 * cur + 1] * 256.0f;
     }
     float kf[NLD][EPV];
 #pragma unroll
@@ -189,6 +214,16 @@ __global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q
         acc[gq][e] = a;
       }
     }
+    if constexpr (kPrefetch) {
+#pragma unroll
+      for (int ld = 0; ld < NLD; ++ld) {
+        kr[ld] = nk[ld];
+        vr[ld] = nv[ld];
+      }
+    } else if (i + 1 < nb) {
+      load_block(nxt, kr, vr);
+    }
+    cur = nxt;
   }
 
   // merge the TPL rows of the wavefront (lanes with the same dim chunk)
@@ -242,7 +277,7 @@ __global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q
 
 #define FERRY_ATTN_INST(DT, G)                                                              \
   template __global__ void k_attn<DT, G>(Geo, const float*, const uint32_t*, const uint8_t*, \
-                                         const float*, float*, float, int*);
+                                         const float*, float*, float, int, int, int*);
 #define FERRY_ATTN_INST_G(DT) \
   FERRY_ATTN_INST(DT, 1)      \
   FERRY_ATTN_INST(DT, 2)      \

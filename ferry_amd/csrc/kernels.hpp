@@ -43,7 +43,8 @@ struct FetchArgs {
 
 template <bool SERIAL>
 __global__ void k_lru_step(Geo g, const uint32_t* sel, uint32_t* slots_out, uint32_t* miss_count,
-                           ferry_miss* misses, uint8_t* miss_flag, SetState st, Ring ring, int* err);
+                           ferry_miss* misses, uint8_t* miss_flag, SetState st, Ring ring, int l0,
+                           int nl, int* err);
 __global__ void k_sets_reset(Geo g, SetState st);
 
 template <int NV>
@@ -52,7 +53,7 @@ __global__ void k_missq_push(Geo g, Ring ring, const ferry_miss* m, uint32_t n, 
 
 template <int DT, int G>
 __global__ void k_attn(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
-                       const float* pool_scales, float* out, float qscale, int* err);
+                       const float* pool_scales, float* out, float qscale, int l0, int nl, int* err);
 
 __global__ void k_hosttier_fill(Geo g, uint8_t* host, float* scales, uint64_t seed, float mult,
                                 float mult8, float scale_base);

@@ -184,12 +184,15 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
                                                   uint32_t* __restrict__ miss_count,
                                                   ferry_miss* __restrict__ misses,
                                                   uint8_t* __restrict__ miss_flag,
-                                                  SetState st, Ring ring, int* __restrict__ err) {
+                                                  SetState st, Ring ring, int l0, int nl,
+                                                  int* __restrict__ err) {
   extern __shared__ uint32_t lds[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wpb = blockDim.x >> 6;
-  const int set = blockIdx.x * wpb + wave;
-  if (set >= g.n_sets) return;  // no workgroup barriers follow
+  // this wave's set among those of layers [l0, l0 + nl)
+  const int idx = blockIdx.x * wpb + wave;
+  if (idx >= g.n_owners * nl * g.Hkv) return;  // no workgroup barriers follow
+  const int set = ((idx / (nl * g.Hkv)) * g.L + l0 + (idx / g.Hkv) % nl) * g.Hkv + idx % g.Hkv;
   const int C = g.C;
   uint32_t* base = lds + (size_t)wave * (3 * C + 2 * g.max_sel);
   int* lastpos = (int*)base;
@@ -269,9 +272,9 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
 }
 
 template __global__ void k_lru_step<false>(Geo, const uint32_t*, uint32_t*, uint32_t*, ferry_miss*,
-                                           uint8_t*, SetState, Ring, int*);
+                                           uint8_t*, SetState, Ring, int, int, int*);
 template __global__ void k_lru_step<true>(Geo, const uint32_t*, uint32_t*, uint32_t*, ferry_miss*,
-                                          uint8_t*, SetState, Ring, int*);
+                                          uint8_t*, SetState, Ring, int, int, int*);
 
 // Reset all sets: empty order, no tags, map cleared.
 __global__ void k_sets_reset(Geo g, SetState st) {

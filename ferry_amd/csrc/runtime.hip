@@ -71,6 +71,7 @@ struct ferry_ctx {
   int lru_wpb = 1;
   size_t lru_lds = 0;
   uint64_t steps = 0, selections = 0;
+  std::vector<hipEvent_t> events;  // layer-chunk pipeline of ferry_decode_step
 
   Ring ring() const {
     Ring r;
@@ -122,6 +123,7 @@ void release(ferry_ctx* c) {
     if (p) (void)hipFree(p);
   if (c->host) (void)hipHostFree(c->host);
   if (c->host_scales) (void)hipHostFree(c->host_scales);
+  for (hipEvent_t e : c->events) (void)hipEventDestroy(e);
   delete c;
 }
 
@@ -253,6 +255,8 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   }
   hipLaunchKernelGGL(k_sets_reset, dim3(1024), dim3(256), 0, 0, g, c->st);
   HIPT(hipGetLastError());
+  c->events.resize((size_t)g.L + 1, nullptr);
+  for (auto& e : c->events) HIPT(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   HIPT(hipDeviceSynchronize());
 #undef TRY
 #undef HIPT
@@ -332,25 +336,34 @@ int ferry_sets_state(ferry_ctx* ctx, uint32_t* fill, uint32_t* ord, uint32_t* ta
   return FERRY_OK;
 }
 
+int ferry_bookkeep_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const uint32_t* sel,
+                          uint32_t* slots, uint32_t* miss_count, ferry_miss* misses,
+                          uint8_t* miss_flag, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!sel || !slots || !miss_count || !misses) return fail(FERRY_EINVAL, "null buffer");
+  const Geo& g = ctx->g;
+  if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
+  HIPC(hipSetDevice(ctx->device));
+  const int wpb = ctx->lru_wpb;
+  const int nsets = g.n_owners * nl * g.Hkv;
+  const dim3 grid((nsets + wpb - 1) / wpb), block(64 * wpb);
+  if (ctx->cfg.lru_mode == FERRY_LRU_SERIAL)
+    hipLaunchKernelGGL(k_lru_step<true>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
+                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->err);
+  else
+    hipLaunchKernelGGL(k_lru_step<false>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
+                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->err);
+  HIPC(hipGetLastError());
+  if (l0 + nl == g.L) ctx->steps++;
+  ctx->selections += (uint64_t)g.n_req * nl * g.Hkv * g.k;
+  return FERRY_OK;
+}
+
 int ferry_bookkeep_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots,
                         uint32_t* miss_count, ferry_miss* misses, uint8_t* miss_flag,
                         void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
-  if (!sel || !slots || !miss_count || !misses) return fail(FERRY_EINVAL, "null buffer");
-  HIPC(hipSetDevice(ctx->device));
-  const Geo& g = ctx->g;
-  const int wpb = ctx->lru_wpb;
-  const dim3 grid((g.n_sets + wpb - 1) / wpb), block(64 * wpb);
-  if (ctx->cfg.lru_mode == FERRY_LRU_SERIAL)
-    hipLaunchKernelGGL(k_lru_step<true>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
-                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), ctx->err);
-  else
-    hipLaunchKernelGGL(k_lru_step<false>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
-                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), ctx->err);
-  HIPC(hipGetLastError());
-  ctx->steps++;
-  ctx->selections += (uint64_t)g.n_req * g.L * g.Hkv * g.k;
-  return FERRY_OK;
+  return ferry_bookkeep_layers(ctx, 0, ctx->g.L, sel, slots, miss_count, misses, miss_flag, stream);
 }
 
 int ferry_missq_push(ferry_ctx* ctx, const ferry_miss* misses, uint32_t n, void* stream) {
@@ -397,19 +410,20 @@ int ferry_fetch_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots, uint3
   return ferry_missq_drain(ctx, stream);
 }
 
-int ferry_sparse_decode(ferry_ctx* ctx, const float* q, const uint32_t* slots, float* out,
-                        void* stream) {
+int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
+                               const uint32_t* slots, float* out, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
   if (!q || !slots || !out) return fail(FERRY_EINVAL, "null buffer");
-  HIPC(hipSetDevice(ctx->device));
   const Geo& g = ctx->g;
-  const dim3 grid((unsigned)(g.n_req * g.L * g.Hkv)), block(256);
+  if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
+  HIPC(hipSetDevice(ctx->device));
+  const dim3 grid((unsigned)(g.n_req * nl * g.Hkv)), block(256);
   const float qscale = (float)(1.4426950408889634 / std::sqrt((double)g.D));
   const int G = g.Hq / g.Hkv;
   hipStream_t s = (hipStream_t)stream;
 #define ATTN(DT, GG)                                                                       \
   hipLaunchKernelGGL((k_attn<DT, GG>), grid, block, 0, s, g, q, slots, ctx->pool,          \
-                     ctx->pool_scales, out, qscale, ctx->err)
+                     ctx->pool_scales, out, qscale, l0, nl, ctx->err)
 #define ATTN_G(DT)          \
   switch (G) {              \
     case 1: ATTN(DT, 1); break; \
@@ -426,6 +440,43 @@ int ferry_sparse_decode(ferry_ctx* ctx, const float* q, const uint32_t* slots, f
 #undef ATTN_G
 #undef ATTN
   HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_sparse_decode(ferry_ctx* ctx, const float* q, const uint32_t* slots, float* out,
+                        void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  return ferry_sparse_decode_layers(ctx, 0, ctx->g.L, q, slots, out, stream);
+}
+
+int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint32_t* slots,
+                      float* out, uint32_t* miss_count, ferry_miss* misses, int32_t chunks,
+                      void* stream, void* side_stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  const int L = ctx->g.L;
+  if (chunks < 1) return fail(FERRY_EINVAL, "chunks < 1");
+  chunks = std::min(chunks, L);
+  const int per = (L + chunks - 1) / chunks;
+  hipStream_t ms = (hipStream_t)stream, ss = (hipStream_t)side_stream;
+  const bool overlap = ss != nullptr && ss != ms;
+  HIPC(hipSetDevice(ctx->device));
+  if (overlap) {  // the side stream must not recycle slots the main stream still reads
+    HIPC(hipEventRecord(ctx->events[L], ms));
+    HIPC(hipStreamWaitEvent(ss, ctx->events[L], 0));
+  }
+  int c = 0;
+  for (int l0 = 0; l0 < L; l0 += per, ++c) {
+    const int nl = std::min(per, L - l0);
+    hipStream_t fs = overlap ? ss : ms;
+    int rc = ferry_bookkeep_layers(ctx, l0, nl, sel, slots, miss_count, misses, nullptr, fs);
+    if (!rc) rc = ferry_missq_drain(ctx, fs);
+    if (rc) return rc;
+    if (overlap) {
+      HIPC(hipEventRecord(ctx->events[c], ss));
+      HIPC(hipStreamWaitEvent(ms, ctx->events[c], 0));
+    }
+    if ((rc = ferry_sparse_decode_layers(ctx, l0, nl, q, slots, out, ms))) return rc;
+  }
   return FERRY_OK;
 }
 

@@ -48,6 +48,7 @@ struct ferry_selgen {
   std::vector<int32_t> nperm;  // per owner: largest member context
   std::vector<double> cum;     // Zipf cumulative weights of ranks 0..nmax-1
   std::vector<uint32_t> state; // previous logical selection per (r, l, h)
+  std::vector<double> reuse;   // per-request reuse (empty = cfg.reuse for all)
   int nmax = 0;
   int max_blocks = 0;
 };
@@ -97,6 +98,18 @@ int ferry_selgen_create(const ferry_selgen_config* cfg, const int32_t* ctx_block
   return FERRY_OK;
 }
 
+int ferry_selgen_set_reuse(ferry_selgen* g, const double* reuse) {
+  if (!g) return FERRY_EINVAL;
+  if (!reuse) {
+    g->reuse.clear();
+    return FERRY_OK;
+  }
+  for (int r = 0; r < g->cfg.n_req; ++r)
+    if (!(reuse[r] >= 0.0 && reuse[r] <= 1.0)) return FERRY_EINVAL;
+  g->reuse.assign(reuse, reuse + g->cfg.n_req);
+  return FERRY_OK;
+}
+
 int ferry_selgen_destroy(ferry_selgen* g) {
   delete g;
   return FERRY_OK;
@@ -112,8 +125,7 @@ int ferry_selgen_step(ferry_selgen* g, int32_t step, uint32_t* out) {
   if (!g || !out || step < 0) return FERRY_EINVAL;
   const ferry_selgen_config& c = g->cfg;
   const int L = c.n_layers, H = c.kv_heads, k = c.k;
-  const uint64_t keep_thr = (uint64_t)(c.reuse * 4294967296.0);
-  const bool carry = step > 0 && c.reuse > 0.0;
+  const bool carry = step > 0;
   int nthreads = (int)std::min<unsigned>(16u, std::max(1u, std::thread::hardware_concurrency()));
   nthreads = std::min(nthreads, c.n_req);
   std::vector<int> rc(nthreads, 0);
@@ -124,6 +136,8 @@ int ferry_selgen_step(ferry_selgen* g, int32_t step, uint32_t* out) {
       const int nr = g->ctx[r];
       const int np = g->nperm[o];
       const int pre = std::min(c.prefix_blocks, np);
+      const double reuse = g->reuse.empty() ? c.reuse : g->reuse[r];
+      const uint64_t keep_thr = (uint64_t)(reuse * 4294967296.0);
       for (int l = 0; l < L; ++l)
         for (int h = 0; h < H; ++h) {
           const size_t row = ((size_t)(r * L + l) * H + h) * k;
@@ -135,7 +149,7 @@ int ferry_selgen_step(ferry_selgen* g, int32_t step, uint32_t* out) {
               (((((uint64_t)step << 16) | (uint64_t)r) * (uint64_t)L + (uint64_t)l) * (uint64_t)H +
                (uint64_t)h) * (uint64_t)kDrawLimit;
           int got = 0;
-          if (carry)
+          if (carry && reuse > 0.0)
             for (int j = 0; j < k; ++j)
               if ((mix64(c.seed ^ kSaltKeep, base + (uint64_t)j) >> 32) < keep_thr) {
                 so[got++] = st[j];

@@ -155,6 +155,11 @@ int ferry_fetch_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots,
 int ferry_bookkeep_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots,
                         uint32_t* miss_count, ferry_miss* misses,
                         uint8_t* miss_flag, void* stream);
+/* Bookkeeping of layers [l0, l0 + nl) only (same buffers and semantics as
+ * ferry_bookkeep_step, which is l0 = 0, nl = n_layers). */
+int ferry_bookkeep_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const uint32_t* sel,
+                          uint32_t* slots, uint32_t* miss_count, ferry_miss* misses,
+                          uint8_t* miss_flag, void* stream);
 /* Queue n externally built misses (device array) onto the ring.  Replaces
  * dq_push producers of GPUBoundedQueue (src/queue/gpu_bounded_queue.cuh:70-126). */
 int ferry_missq_push(ferry_ctx* ctx, const ferry_miss* misses, uint32_t n,
@@ -175,6 +180,23 @@ int ferry_missq_drain(ferry_ctx* ctx, void* stream);
  * src/runtime/wla_multigpu.cuh:96-103). */
 int ferry_sparse_decode(ferry_ctx* ctx, const float* q, const uint32_t* slots,
                         float* out, void* stream);
+
+/* Attention of layers [l0, l0 + nl) only. */
+int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
+                               const uint32_t* slots, float* out, void* stream);
+
+/* One whole decode step with the fetch overlapped with attention: layers are
+ * cut into `chunks` ranges; bookkeeping and fetch of each range run on
+ * side_stream, and attention of a range starts on `stream` as soon as its
+ * fetch is done, while the next range is fetched.  side_stream NULL (or equal
+ * to stream) runs the same sequence on one stream.  When this returns, work
+ * queued on `stream` after it observes the whole step.  Replaces the refill /
+ * compute overlap of run_miss_workload mode C: batches submitted to the
+ * channel, compute waiting on the last arrival (src/workloads/kv_exec.cuh:
+ * 228-286, src/comm/host_staged_channel.cuh:55-63). */
+int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint32_t* slots,
+                      float* out, uint32_t* miss_count, ferry_miss* misses, int32_t chunks,
+                      void* stream, void* side_stream);
 
 /* Counters (synchronises the device). */
 int ferry_stats_get(ferry_ctx* ctx, ferry_stats* out);
@@ -209,6 +231,9 @@ typedef struct ferry_selgen ferry_selgen;
 int ferry_selgen_create(const ferry_selgen_config* cfg, const int32_t* ctx_blocks,
                         ferry_selgen** out);
 int ferry_selgen_destroy(ferry_selgen* g);
+/* Per-request reuse probabilities (array of n_req in [0, 1]; NULL restores
+ * the configured reuse for every request). */
+int ferry_selgen_set_reuse(ferry_selgen* g, const double* reuse);
 /* Set block-id bound (use as ferry_config.max_blocks). */
 int ferry_selgen_max_blocks(const ferry_selgen* g, int32_t* out);
 /* Generate step `step` (steps must be generated in order) into host array

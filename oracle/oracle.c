@@ -750,14 +750,15 @@ int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
       cum[i] = acc;
     }
   }
-  const uint64_t keep_thr = (uint64_t)(s->reuse * 4294967296.0);
-  const int carry = step > 0 && s->reuse > 0.0;
+  const int carry = step > 0;
   uint8_t* taken = (uint8_t*)calloc((size_t)nmax, 1);
   for (int r = 0; r < s->n_req; ++r) {
     const int o = r / s->group, m = r % s->group;
     const int nr = s->ctx_blocks[r];
     const int np = owner_nperm(s, o);
     const int pre = s->prefix_blocks < np ? s->prefix_blocks : np;
+    const double reuse = s->reuse_r ? s->reuse_r[r] : s->reuse;
+    const uint64_t keep_thr = (uint64_t)(reuse * 4294967296.0);
     if (k > nr) {
       free(cum);
       free(taken);
@@ -775,7 +776,7 @@ int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
             (((((uint64_t)step << 16) | (uint64_t)r) * (uint64_t)L + (uint64_t)l) *
                  (uint64_t)H + (uint64_t)h) * (uint64_t)DRAW_LIMIT;
         int got = 0;
-        if (carry)
+        if (carry && reuse > 0.0)
           for (int j = 0; j < k; ++j) {
             const uint64_t u = ora_mix64(s->seed ^ SALT_KEEP, base + (uint64_t)j) >> 32;
             if (u < keep_thr) {

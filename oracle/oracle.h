@@ -176,6 +176,7 @@ typedef struct {
   int prefix_blocks; /* shared prefix blocks per group (0 = none) */
   uint64_t seed;
   const int* ctx_blocks; /* [n_req] logical context length in blocks */
+  const double* reuse_r; /* [n_req] per-request reuse, or NULL (use reuse) */
 } ora_selgen;
 
 /* Per-request context lengths: uniform integer in [lo, hi]. */

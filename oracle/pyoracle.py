@@ -56,7 +56,7 @@ class SelGen(C.Structure):
         ("n_req", C.c_int), ("group", C.c_int), ("n_layers", C.c_int),
         ("kv_heads", C.c_int), ("k", C.c_int), ("dist", C.c_int),
         ("zipf_s", C.c_double), ("reuse", C.c_double), ("prefix_blocks", C.c_int), ("seed", C.c_uint64),
-        ("ctx_blocks", C.POINTER(C.c_int)),
+        ("ctx_blocks", C.POINTER(C.c_int)), ("reuse_r", C.POINTER(C.c_double)),
     ]
 
 
@@ -207,11 +207,14 @@ def make_geom(**kw):
 
 
 def selgen(n_req, n_layers, kv_heads, k, ctx_blocks, dist=1, zipf_s=1.1, reuse=0.66,
-           group=1, prefix_blocks=0, seed=1):
+           group=1, prefix_blocks=0, seed=1, reuse_r=None):
     ctx = np.ascontiguousarray(ctx_blocks, np.int32)
+    rr = None if reuse_r is None else np.ascontiguousarray(reuse_r, np.float64)
     s = SelGen(n_req, group, n_layers, kv_heads, k, dist, zipf_s, reuse, prefix_blocks, seed,
-               ctx.ctypes.data_as(C.POINTER(C.c_int)))
+               ctx.ctypes.data_as(C.POINTER(C.c_int)),
+               rr.ctypes.data_as(C.POINTER(C.c_double)) if rr is not None else None)
     s._ctx = ctx  # keep alive
+    s._rr = rr
     s._state = np.zeros(n_req * n_layers * kv_heads * k, np.uint32)
     return s
 

@@ -74,3 +74,19 @@ def test_invalid_config_rejected_before_any_device_call(bad):
     assert F.lib.ferry_ctx_create(C.byref(cfg), 0, C.byref(h)) == -1
     assert not h.value
     assert F.lib.ferry_last_error()
+
+
+def test_selgen_per_request_reuse_matches_oracle():
+    B, L, H, k = 5, 2, 3, 16
+    ctx = F.ctx_uniform(4, B, 40, 200)
+    rr = np.array([0.0, 0.25, 0.66, 0.9, 1.0])
+    mine = F.SelGen(B, L, H, k, ctx, reuse=0.5, seed=8)
+    mine.set_reuse(rr)
+    ref = O.selgen(B, L, H, k, ctx, reuse=0.5, seed=8, reuse_r=rr)
+    prev = None
+    for step in range(6):
+        a = mine.step(step)
+        assert np.array_equal(a.reshape(-1), O.selgen_step(ref, step))
+        if prev is not None:  # reuse 1.0 keeps the whole selection, 0.0 redraws all of it
+            assert np.array_equal(a[4], prev[4])
+        prev = a

@@ -285,3 +285,47 @@ def test_steady_state_properties_at_scale():
     hidx = (m[:, 3].astype(np.int64) * sg.max_blocks + m[:, 0]) % (1 << 15)
     assert np.array_equal(got, host.reshape(-1, ex.block_bytes)[hidx])
     assert 0.02 < st["last_misses"] / (n_req * L * H * k) < 0.3
+
+
+def test_decode_step_overlap_matches_sequential():
+    # layer-chunked pipeline (fetch of chunk c+1 on a side stream while chunk c
+    # attends) must produce exactly the sequential step's slots, pool and output
+    n_req, L, Hkv, Hq, k, cap = 4, 6, 2, 8, 16, 40
+    mb, sels = _zipf_stream(n_req, L, Hkv, k, 60, 300, 5)
+    seq = Pair(n_req, L, Hkv, Hq, k, cap, mb, F.BF16)
+    ovl = Pair(n_req, L, Hkv, Hq, k, cap, mb, F.BF16)
+    side = torch.cuda.Stream()
+    rng = np.random.default_rng(3)
+    for t, sel in enumerate(sels):
+        q = torch.from_numpy(rng.standard_normal((n_req, L, Hq, 128)).astype(np.float32)).cuda()
+        o1, o2 = torch.empty_like(q), torch.empty_like(q)
+        d = torch.from_numpy(sel.view(np.int32)).cuda()
+        seq.ex.fetch_step(d, seq.bufs)
+        seq.ex.sparse_decode(q, seq.bufs["slots"], o1)
+        ovl.ex.decode_step(d, q, ovl.bufs, o2, chunks=4, side_stream=side)
+        torch.cuda.synchronize()
+        assert np.array_equal(_u32(seq.bufs["slots"]), _u32(ovl.bufs["slots"]))
+        assert torch.equal(o1, o2)
+        assert ovl.ex.stats()["device_error"] == 0
+    f1, o1_, t1 = seq.ex.sets_state()
+    f2, o2_, t2 = ovl.ex.sets_state()
+    assert np.array_equal(f1, f2) and np.array_equal(o1_, o2_) and np.array_equal(t1, t2)
+    allslots = np.arange(seq.ex.pool_slots)
+    assert np.array_equal(seq.ex.pool_slots_bytes(allslots), ovl.ex.pool_slots_bytes(allslots))
+    ovl.check_attention(sels[-1], seed=11)
+
+
+def test_per_layer_bookkeeping_equals_whole_step():
+    n_req, L, H, k, cap = 3, 4, 2, 16, 32
+    mb, sels = _zipf_stream(n_req, L, H, k, 60, 200, 4)
+    p = Pair(n_req, L, H, H, k, cap, mb, F.F16)
+    for sel in sels:
+        d = torch.from_numpy(sel.view(np.int32)).cuda()
+        for l0 in range(L):
+            p.ex.bookkeep_layers(l0, 1, d, p.bufs)
+            p.ex.missq_drain()
+        torch.cuda.synchronize()
+        oslots, omc, _, _ = p.ox.step(sel)
+        assert np.array_equal(_u32(p.bufs["slots"]).reshape(-1), oslots)
+        assert np.array_equal(_u32(p.bufs["miss_count"]), omc)
+    p.check_state()
