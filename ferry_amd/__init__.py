@@ -24,7 +24,7 @@ import torch  # noqa: F401  (HIP runtime + device memory; load before the librar
 __all__ = [
     "FerryError", "Executor", "SelGen", "queue_selftest", "refgen_selections",
     "ctx_uniform", "lib", "LIB_PATH", "F32", "F16", "BF16", "FP8", "LRU_STEP", "LRU_SERIAL",
-    "ASSIGN_SPREAD", "ASSIGN_AFFINITY", "MISS_DTYPE",
+    "ASSIGN_SPREAD", "ASSIGN_AFFINITY", "ATTN_AUTO", "ATTN_VALU", "ATTN_MFMA", "MISS_DTYPE",
 ]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libferry_amd.so")
@@ -36,6 +36,7 @@ lib = C.CDLL(LIB_PATH)
 F32, F16, BF16, FP8 = 0, 1, 2, 3
 LRU_STEP, LRU_SERIAL = 0, 1
 ASSIGN_SPREAD, ASSIGN_AFFINITY = 0, 1
+ATTN_AUTO, ATTN_VALU, ATTN_MFMA = 0, 1, 2
 ESIZE = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 MISS_DTYPE = np.dtype([("block", "<u4"), ("slot", "<u4"), ("evicted", "<u4"), ("set", "<u4")])
 
@@ -58,6 +59,7 @@ class Config(C.Structure):
         ("max_blocks", C.c_int32), ("dtype", C.c_int32), ("lru_mode", C.c_int32),
         ("host_blocks", C.c_uint64), ("host_seed", C.c_uint64), ("value_std", C.c_float),
         ("fetch_workers", C.c_int32), ("steal", C.c_int32), ("assign", C.c_int32),
+        ("attn", C.c_int32),
     ]
 
 
@@ -146,10 +148,10 @@ class Executor:
     def __init__(self, n_req, n_layers, kv_heads, k, slots_per_set, max_blocks,
                  q_heads=None, group=1, head_dim=128, block_tokens=16, dtype=F16,
                  lru_mode=LRU_STEP, host_blocks=1 << 16, host_seed=7, value_std=0.5,
-                 fetch_workers=0, steal=1, assign=ASSIGN_SPREAD, device=0):
+                 fetch_workers=0, steal=1, assign=ASSIGN_SPREAD, attn=ATTN_AUTO, device=0):
         cfg = Config(n_req, group, n_layers, kv_heads, q_heads or kv_heads, head_dim,
                      block_tokens, k, slots_per_set, max_blocks, dtype, lru_mode,
-                     host_blocks, host_seed, value_std, fetch_workers, steal, assign)
+                     host_blocks, host_seed, value_std, fetch_workers, steal, assign, attn)
         self.device = device
         torch.cuda.set_device(device)
         h = _vp()

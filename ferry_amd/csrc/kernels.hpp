@@ -55,6 +55,12 @@ template <int DT, int G>
 __global__ void k_attn(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
                        const float* pool_scales, float* out, float qscale, int l0, int nl, int* err);
 
+// MFMA variant for GQA groups (G >= 2) of 16/8-bit KV (attn_mfma.hip).
+template <int DT, int G>
+__global__ void k_attn_mfma(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
+                            const float* pool_scales, float* out, float qscale, int l0, int nl,
+                            int* err);
+
 __global__ void k_hosttier_fill(Geo g, uint8_t* host, float* scales, uint64_t seed, float mult,
                                 float mult8, float scale_base);
 

@@ -102,6 +102,10 @@ int validate(const ferry_config* c) {
     return fail(FERRY_EINVAL, "bad lru_mode");
   if (c->assign != FERRY_ASSIGN_SPREAD && c->assign != FERRY_ASSIGN_AFFINITY)
     return fail(FERRY_EINVAL, "bad assign");
+  if (c->attn != FERRY_ATTN_AUTO && c->attn != FERRY_ATTN_VALU && c->attn != FERRY_ATTN_MFMA)
+    return fail(FERRY_EINVAL, "bad attn");
+  if (c->attn == FERRY_ATTN_MFMA && (grp < 2 || c->dtype == FERRY_F32))
+    return fail(FERRY_EINVAL, "the MFMA attention kernel needs q_heads/kv_heads >= 2 and 16/8-bit KV");
   if (c->fetch_workers < 0) return fail(FERRY_EINVAL, "fetch_workers < 0");
   if ((uint64_t)c->max_blocks >= (uint64_t)kPend) return fail(FERRY_EINVAL, "max_blocks too large");
   return FERRY_OK;
@@ -421,18 +425,34 @@ int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const flo
   const float qscale = (float)(1.4426950408889634 / std::sqrt((double)g.D));
   const int G = g.Hq / g.Hkv;
   hipStream_t s = (hipStream_t)stream;
-#define ATTN(DT, GG)                                                                       \
-  hipLaunchKernelGGL((k_attn<DT, GG>), grid, block, 0, s, g, q, slots, ctx->pool,          \
+  const bool mfma = g.dtype != FERRY_F32 && G >= 2 && ctx->cfg.attn != FERRY_ATTN_VALU;
+#define ATTN(K, DT, GG)                                                                    \
+  hipLaunchKernelGGL((K<DT, GG>), grid, block, 0, s, g, q, slots, ctx->pool,              \
                      ctx->pool_scales, out, qscale, l0, nl, ctx->err)
-#define ATTN_G(DT)          \
-  switch (G) {              \
-    case 1: ATTN(DT, 1); break; \
-    case 2: ATTN(DT, 2); break; \
-    case 4: ATTN(DT, 4); break; \
-    default: ATTN(DT, 8); break; \
+#define ATTN_G(DT)                                      \
+  if (mfma) {                                           \
+    switch (G) {                                        \
+      case 2: ATTN(k_attn_mfma, DT, 2); break;          \
+      case 4: ATTN(k_attn_mfma, DT, 4); break;          \
+      default: ATTN(k_attn_mfma, DT, 8); break;         \
+    }                                                   \
+  } else {                                              \
+    switch (G) {                                        \
+      case 1: ATTN(k_attn, DT, 1); break;               \
+      case 2: ATTN(k_attn, DT, 2); break;               \
+      case 4: ATTN(k_attn, DT, 4); break;               \
+      default: ATTN(k_attn, DT, 8); break;              \
+    }                                                   \
   }
   switch (g.dtype) {
-    case FERRY_F32: ATTN_G(FERRY_F32); break;
+    case FERRY_F32:
+      switch (G) {
+        case 1: ATTN(k_attn, FERRY_F32, 1); break;
+        case 2: ATTN(k_attn, FERRY_F32, 2); break;
+        case 4: ATTN(k_attn, FERRY_F32, 4); break;
+        default: ATTN(k_attn, FERRY_F32, 8); break;
+      }
+      break;
     case FERRY_F16: ATTN_G(FERRY_F16); break;
     case FERRY_BF16: ATTN_G(FERRY_BF16); break;
     default: ATTN_G(FERRY_FP8_E4M3); break;

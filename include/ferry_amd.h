@@ -46,6 +46,11 @@ extern "C" {
 #define FERRY_ASSIGN_SPREAD 0   /* set id modulo workers */
 #define FERRY_ASSIGN_AFFINITY 1 /* request (owner) modulo workers */
 
+/* ---- attention kernel selection ---- */
+#define FERRY_ATTN_AUTO 0 /* MFMA for GQA groups (q_heads/kv_heads >= 2) of 16/8-bit KV, else VALU */
+#define FERRY_ATTN_VALU 1 /* vector-ALU kernel for every shape */
+#define FERRY_ATTN_MFMA 2 /* MFMA kernel; needs q_heads/kv_heads >= 2 and 16/8-bit KV */
+
 /* Geometry and policy of one executor.  Sets are (owner, layer, kv head)
  * with owner = request / group; each set owns slots_per_set slots of the HBM
  * pool.  Replaces MissSpec (src/workloads/missstream.cuh:23-76) widened from
@@ -70,6 +75,7 @@ typedef struct ferry_config {
   int32_t fetch_workers; /* persistent fetch workgroups; 0 = 2 per CU */
   int32_t steal;         /* 1 = fetch workers steal from each other */
   int32_t assign;        /* FERRY_ASSIGN_SPREAD or FERRY_ASSIGN_AFFINITY */
+  int32_t attn;          /* FERRY_ATTN_AUTO, FERRY_ATTN_VALU or FERRY_ATTN_MFMA */
 } ferry_config;
 
 /* One fetched block: written per set in miss order. */

@@ -26,13 +26,15 @@ class Pair:
     """A GPU executor and its oracle twin built from the same geometry."""
 
     def __init__(self, n_req, L, Hkv, Hq, k, cap, max_blocks, dtype, group=1, lru=0,
-                 host_blocks=4099, steal=1, assign=0, workers=0, seed=7, value_std=0.5):
+                 host_blocks=4099, steal=1, assign=0, workers=0, seed=7, value_std=0.5,
+                 attn=F.ATTN_AUTO):
         print(f"[pair] B={n_req} L={L} Hkv={Hkv} Hq={Hq} k={k} C={cap} mb={max_blocks} "
-              f"dtype={dtype} group={group} lru={lru} steal={steal} assign={assign}", flush=True)
+              f"dtype={dtype} group={group} lru={lru} steal={steal} assign={assign} attn={attn}",
+              flush=True)
         self.ex = F.Executor(n_req, L, Hkv, k, cap, max_blocks, q_heads=Hq, group=group,
                              dtype=dtype, lru_mode=lru, host_blocks=host_blocks, host_seed=seed,
                              value_std=value_std, fetch_workers=workers, steal=steal,
-                             assign=assign)
+                             assign=assign, attn=attn)
         self.g = O.make_geom(n_req=n_req, group=group, n_layers=L, kv_heads=Hkv, q_heads=Hq,
                              k=k, cap=cap, max_blocks=max_blocks, dtype=dtype, granularity=lru,
                              host_blocks=host_blocks, seed=seed, value_std=value_std)
@@ -94,10 +96,10 @@ class Pair:
             gs = self.ex.pool_slot_scales(gslots)
             assert np.array_equal(gs, self.hsc.reshape(-1, 2)[hidx.astype(np.int64)])
 
-    def check_attention(self, sel, seed=0):
+    def check_attention(self, sel, seed=0, q_std=1.0):
         g = self.g
         rng = np.random.default_rng(seed)
-        q = rng.standard_normal((g.n_req, g.n_layers, g.q_heads, 128)).astype(np.float32)
+        q = (rng.standard_normal((g.n_req, g.n_layers, g.q_heads, 128)) * q_std).astype(np.float32)
         dq = torch.from_numpy(q).cuda()
         out = torch.empty_like(dq)
         self.ex.sparse_decode(dq, self.bufs["slots"], out)
@@ -329,3 +331,35 @@ def test_per_layer_bookkeeping_equals_whole_step():
         assert np.array_equal(_u32(p.bufs["slots"]).reshape(-1), oslots)
         assert np.array_equal(_u32(p.bufs["miss_count"]), omc)
     p.check_state()
+
+
+@pytest.mark.parametrize("dtype", [F.F16, F.BF16, F.FP8])
+@pytest.mark.parametrize("G", [2, 4, 8])
+def test_mfma_attention_matches_oracle_and_valu(dtype, G):
+    # GQA head groups on the matrix cores against the fp64 oracle, and the
+    # vector-ALU kernel on the same pool within the same tolerance.  k=13 gives
+    # the four wavefronts unequal block counts.
+    n_req, L, Hkv, k = 3, 2, 2, 13
+    mb, sels = _zipf_stream(n_req, L, Hkv, k, 40, 200, 2, seed=G)
+    pm = Pair(n_req, L, Hkv, Hkv * G, k, 32, mb, dtype, attn=F.ATTN_MFMA)
+    pv = Pair(n_req, L, Hkv, Hkv * G, k, 32, mb, dtype, attn=F.ATTN_VALU)
+    for t, sel in enumerate(sels):
+        pm.step(sel)
+        pv.step(sel)
+    for q_std in (1.0, 4.0):  # 4.0: peaked softmax, scores up to ~30 in log2 units
+        pm.check_attention(sels[-1], seed=5, q_std=q_std)
+        pv.check_attention(sels[-1], seed=5, q_std=q_std)
+    assert pm.ex.stats()["device_error"] == 0
+
+
+def test_mfma_attention_long_selection():
+    # k = 300 blocks per kv head: 75 blocks per wavefront, so the slot ids are
+    # re-read past the first 64 (one per lane) inside the kernel.
+    n_req, L, Hkv, G, k = 2, 1, 2, 4, 300
+    mb, sels = _zipf_stream(n_req, L, Hkv, k, 400, 600, 1, seed=4)
+    for dtype in (F.BF16, F.FP8):
+        p = Pair(n_req, L, Hkv, Hkv * G, k, 320, mb, dtype, host_blocks=1 << 13,
+                 attn=F.ATTN_MFMA)
+        p.step(sels[0])
+        p.check_attention(sels[0], seed=2)
+        p.ex.close()
