@@ -75,6 +75,8 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--steal", type=int, default=1)
     ap.add_argument("--workers", type=int, default=0)
+    ap.add_argument("--attn", default="auto", choices=["auto", "valu", "mfma"],
+                    help="attention kernel: MFMA for GQA groups of 16/8-bit KV (auto), or forced")
     ap.add_argument("--chunks", type=int, default=8,
                     help="layer chunks of the fetch/attention overlap (1 = no side stream)")
     ap.add_argument("--rocprof-summary", metavar="DB",
@@ -224,8 +226,10 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     out = torch.empty_like(qs[0])
     if assign is None:
         assign = F.ASSIGN_AFFINITY if a.workload == "skew" else F.ASSIGN_SPREAD
+    attn = {"auto": F.ATTN_AUTO, "valu": F.ATTN_VALU, "mfma": F.ATTN_MFMA}[a.attn]
     ex = F.Executor(B, L, H, k, C, sg.max_blocks, q_heads=Hq, group=w["group"], dtype=dtype,
-                    host_blocks=a.host_blocks, fetch_workers=workers, steal=steal, assign=assign)
+                    host_blocks=a.host_blocks, fetch_workers=workers, steal=steal, assign=assign,
+                    attn=attn)
     ex.hosttier_fill()
     bufs = ex.alloc_step_buffers()
     torch.cuda.synchronize()
@@ -268,6 +272,14 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
         e[3].record(stream)
     torch.cuda.synchronize()
     st2 = ex.stats()
+    # attention alone, back to back over the last step's slot table
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record(stream)
+    for i in range(a.steps):
+        ex.sparse_decode(qs[i & 1], bufs["slots"], out)
+    r1.record(stream)
+    torch.cuda.synchronize()
+    t_attn_rep = r0.elapsed_time(r1) / a.steps
     ev_misses = st2["misses"] - m0
     t_book = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
     t_fetch = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
@@ -282,6 +294,8 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     attn_gbs = attn_bytes / (t_attn * 1e-3) / 1e9
     link_gbs = fetch_bytes / (t_fetch * 1e-3) / 1e9
     G = Hq // H
+    mfma = dtype != F.F32 and G >= 2 and attn != F.ATTN_VALU
+    attn_kernel = f"k_attn{'_mfma' if mfma else ''}<{w['dtype']},{G}>"
     res = {
         "ms_per_step": round(ms_step, 3),
         "value": round(B / (ms_step * 1e-3), 2),
@@ -290,8 +304,8 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
         "miss_blocks_per_s_fetch_kernel": round(ev_misses / a.steps / (t_fetch * 1e-3), 1),
         "attention_tok_per_s": round(B / (t_attn * 1e-3), 1),
         "kernel_ms": {"bookkeep": round(t_book, 4), "fetch": round(t_fetch, 4),
-                      "attention": round(t_attn, 4)},
-        "roofline": {"bound": "hbm", "kernel": f"k_attn<{w['dtype']},{G}>",
+                      "attention": round(t_attn, 4), "attention_back_to_back": round(t_attn_rep, 4)},
+        "roofline": {"bound": "hbm", "kernel": attn_kernel,
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "roofline_fetch": {"bound": "host-link", "kernel": f"k_fetch<{bb // 1024}>",

@@ -6,8 +6,7 @@
 // the per-step top-k block selection of tools/capture_miss_trace.py:139-159.
 //
 // Work decomposition (HBM-bound, ~1-8 flop/byte): one workgroup per
-// (request, layer, kv head); its four wavefronts take every fourth selected
-// block.  A block is K[T][D] then V[T][D].  Each 16-byte load instruction of a
+// (request, layer, kv head); its W wavefronts take every W-th selected block.  A block is K[T][D] then V[T][D].  Each 16-byte load instruction of a
 // wavefront covers one contiguous KiB of the tile, so lane l holds the
 // EPV-element dim chunk (l % LPT) of token (l / LPT) + ld * TPL.  The q.K dot
 // product is reduced over the LPT lanes of a row with DPP row ops (no LDS);
@@ -89,8 +88,8 @@ struct Softmax {
 
 }  // namespace
 
-template <int DT, int G>
-__global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q,
+template <int DT, int G, int W>
+__global__ __launch_bounds__(W * 64) void k_attn(Geo g, const float* __restrict__ q,
                                               const uint32_t* __restrict__ slots,
                                               const uint8_t* __restrict__ pool,
                                               const float* __restrict__ pool_scales,
@@ -104,8 +103,10 @@ __global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q
   constexpr int NLD = T / TPL;   // load instructions per K (or V) tile
   constexpr uint32_t TILE_WORDS = T * D * ES / 16;
   constexpr float kNeg = -1.0e30f;
+  constexpr int NPF = G <= 2 ? 2 : 1;  // prefetch ring depth (wide groups keep occupancy)
 
-  __shared__ float red[4][G][LPT][EPV + 2];
+  __shared__ float red[W][G][LPT][EPV + 2];
+  __shared__ uint32_t ids[kMaxTopK];
 
   // (request, layer in [l0, l0 + nl), kv head) of this workgroup
   const int h = blockIdx.x % g.Hkv;
@@ -131,101 +132,104 @@ __global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q
     for (int e = 0; e < EPV; ++e) acc[gq][e] = 0.0f;
   }
 
-  // Slot ids of this wavefront's blocks (j = wave, wave+4, ...), 64 at a time,
-  // one per lane; each block reads its id with readlane (no dependent load).
+  // The row's slot ids are staged in LDS: a slot lookup is then an LDS read
+  // (lgkmcnt) that never waits on the block loads in flight (vmcnt).
   const uint32_t* sl = slots + (size_t)row * g.k;
   const int k = g.k;
-  const int nb = k > wave ? (k - wave + 3) / 4 : 0;
-  auto slot_of = [&](uint32_t sidx, int i) -> uint64_t {
-    uint64_t slot = (uint32_t)__builtin_amdgcn_readlane((int)sidx, i & 63);
-    if (slot >= g.pool_slots) {  // never read outside the pool
-      set_error(err, FERRY_ERANGE);
-      slot = 0;
-    }
-    return slot;
+  for (int j = threadIdx.x; j < k; j += W * 64) ids[j] = sl[j];
+  __syncthreads();
+  // Ring of NPF block buffers (NPF = 1: load, then consume).  While block j
+  // (= wave + W*j of the row) is consumed, blocks j+1 .. j+NPF-1 are in flight;
+  // the loop is unrolled by NPF so every buffer index is static, and every
+  // iteration issues its load (past the end it re-reads the last block, an L2
+  // hit) so the compiler's load counters stay exact.
+  const int nb = k > wave ? (k - wave + W - 1) / W : 0;
+  // A slot outside the pool is read as slot 0 and reported once at the end
+  // (no branch in the block loop).
+  bool bad_slot = false;
+  auto slot_at = [&](int j) -> uint64_t {
+    const uint64_t slot =
+        (uint32_t)__builtin_amdgcn_readfirstlane((int)ids[wave + W * min(j, nb - 1)]);
+    const bool bad = slot >= g.pool_slots;
+    bad_slot |= bad;
+    return bad ? 0 : slot;
   };
-  auto load_block = [&](uint64_t slot, u32x4* kr, u32x4* vr) {
+  u32x4 kb[NPF][NLD], vb[NPF][NLD];
+  float ksb[NPF], vsb[NPF];
+  auto issue = [&](int j, int b) {
+    const uint64_t slot = slot_at(j);
     const u32x4* kp = reinterpret_cast<const u32x4*>(pool + slot * g.bb);
     const u32x4* vp = kp + TILE_WORDS;
 #pragma unroll
-    for (int ld = 0; ld < NLD; ++ld) kr[ld] = kp[ld * 64 + lane];
+    for (int ld = 0; ld < NLD; ++ld) kb[b][ld] = kp[ld * 64 + lane];
 #pragma unroll
-    for (int ld = 0; ld < NLD; ++ld) vr[ld] = vp[ld * 64 + lane];
-  };
-  uint32_t sidx = 0;
-  u32x4 kr[NLD], vr[NLD], nk[NLD], nv[NLD];
-  uint64_t cur = 0;
-  if (nb > 0) {
-    sidx = lane < nb ? sl[wave + 4 * lane] : 0u;
-    cur = slot_of(sidx, 0);
-    load_block(cur, kr, vr);
-  }
-  // Double-buffer K/V (next block in flight while this one is consumed) where
-  // the registers allow it; wide GQA groups keep occupancy instead.
-  constexpr bool kPrefetch = G <= 2;
-  for (int i = 0; i < nb; ++i) {
-    uint64_t nxt = 0;
-    if (i + 1 < nb) {
-      if (((i + 1) & 63) == 0) sidx = (lane + i + 1) < nb ? sl[wave + 4 * (lane + i + 1)] : 0u;
-      nxt = slot_of(sidx, i + 1);
-      if constexpr (kPrefetch) load_block(nxt, nk, nv);
-    }
-    float ks = 1.0f, vs = 1.0f;
+    for (int ld = 0; ld < NLD; ++ld) vb[b][ld] = vp[ld * 64 + lane];
     if constexpr (DT == FERRY_FP8_E4M3) {
-      ks = pool_scales[2 * cur] * 256.0f;
-      vs = pool_scales[2 * cur + 1] * 256.0f;
+      ksb[b] = pool_scales[2 * slot] * 256.0f;
+      vsb[b] = pool_scales[2 * slot + 1] * 256.0f;
+    } else {
+      ksb[b] = vsb[b] = 1.0f;
     }
-    float kf[NLD][EPV];
+  };
+  if (nb > 0) {
 #pragma unroll
-    for (int ld = 0; ld < NLD; ++ld) decode<DT>(kr[ld], kf[ld]);
-    float s[G][NLD];
+    for (int b = 0; b < NPF - 1; ++b) issue(b, b);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int i0 = 0; i0 < nb; i0 += NPF) {
 #pragma unroll
-    for (int gq = 0; gq < G; ++gq)
+    for (int b = 0; b < NPF; ++b) {
+      const int i = i0 + b;
+      if (i >= nb) break;
+      issue(i + NPF - 1, (b + NPF - 1) % NPF);
+      // keep the prefetch here: the scheduler would sink it to its first use
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4* kr = kb[b];
+      const u32x4* vr = vb[b];
+      const float ks = ksb[b], vs = vsb[b];
+      float kf[NLD][EPV];
 #pragma unroll
-      for (int ld = 0; ld < NLD; ++ld) {
-        float a = 0.0f;
+      for (int ld = 0; ld < NLD; ++ld) decode<DT>(kr[ld], kf[ld]);
+      float s[G][NLD];
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) a = __builtin_fmaf(qv[gq][e], kf[ld][e], a);
-        s[gq][ld] = group_sum<LPT>(a) * ks;
-      }
-    float vf[NLD][EPV];
+      for (int gq = 0; gq < G; ++gq)
 #pragma unroll
-    for (int ld = 0; ld < NLD; ++ld) decode<DT>(vr[ld], vf[ld]);
+        for (int ld = 0; ld < NLD; ++ld) {
+          float a = 0.0f;
 #pragma unroll
-    for (int gq = 0; gq < G; ++gq) {
-      float mb = s[gq][0];
+          for (int e = 0; e < EPV; ++e) a = __builtin_fmaf(qv[gq][e], kf[ld][e], a);
+          s[gq][ld] = group_sum<LPT>(a) * ks;
+        }
+      float vf[NLD][EPV];
 #pragma unroll
-      for (int ld = 1; ld < NLD; ++ld) mb = fmaxf(mb, s[gq][ld]);
-      const float mn = fmaxf(sm[gq].m, mb);
-      const float alpha = exp2_fast(sm[gq].m - mn);
-      float p[NLD], psum = 0.0f;
+      for (int ld = 0; ld < NLD; ++ld) decode<DT>(vr[ld], vf[ld]);
 #pragma unroll
-      for (int ld = 0; ld < NLD; ++ld) {
-        p[ld] = exp2_fast(s[gq][ld] - mn);
-        psum += p[ld];
-      }
-      sm[gq].l = sm[gq].l * alpha + psum;
-      sm[gq].m = mn;
+      for (int gq = 0; gq < G; ++gq) {
+        float mb = s[gq][0];
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) {
-        float a = acc[gq][e] * alpha;
+        for (int ld = 1; ld < NLD; ++ld) mb = fmaxf(mb, s[gq][ld]);
+        const float mn = fmaxf(sm[gq].m, mb);
+        const float alpha = exp2_fast(sm[gq].m - mn);
+        float p[NLD], psum = 0.0f;
 #pragma unroll
-        for (int ld = 0; ld < NLD; ++ld) a = __builtin_fmaf(p[ld] * vs, vf[ld][e], a);
-        acc[gq][e] = a;
+        for (int ld = 0; ld < NLD; ++ld) {
+          p[ld] = exp2_fast(s[gq][ld] - mn);
+          psum += p[ld];
+        }
+        sm[gq].l = sm[gq].l * alpha + psum;
+        sm[gq].m = mn;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          float a = acc[gq][e] * alpha;
+#pragma unroll
+          for (int ld = 0; ld < NLD; ++ld) a = __builtin_fmaf(p[ld] * vs, vf[ld][e], a);
+          acc[gq][e] = a;
+        }
       }
     }
-    if constexpr (kPrefetch) {
-#pragma unroll
-      for (int ld = 0; ld < NLD; ++ld) {
-        kr[ld] = nk[ld];
-        vr[ld] = nv[ld];
-      }
-    } else if (i + 1 < nb) {
-      load_block(nxt, kr, vr);
-    }
-    cur = nxt;
   }
 
+  if (bad_slot && lane == 0) set_error(err, FERRY_ERANGE);
   // merge the TPL rows of the wavefront (lanes with the same dim chunk)
 #pragma unroll
   for (int off = LPT; off < 64; off <<= 1) {
@@ -254,15 +258,15 @@ __global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q
     }
   }
   __syncthreads();
-  // merge the four wavefronts and write out
+  // merge the W wavefronts and write out
   for (int t = threadIdx.x; t < G * LPT; t += blockDim.x) {
     const int gq = t / LPT, c = t % LPT;
     float m = red[0][gq][c][0];
-    for (int w = 1; w < 4; ++w) m = fmaxf(m, red[w][gq][c][0]);
+    for (int w = 1; w < W; ++w) m = fmaxf(m, red[w][gq][c][0]);
     float l = 0.0f, o[EPV];
 #pragma unroll
     for (int e = 0; e < EPV; ++e) o[e] = 0.0f;
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float a = exp2_fast(red[w][gq][c][0] - m);
       l += red[w][gq][c][1] * a;
 #pragma unroll
@@ -275,17 +279,21 @@ __global__ __launch_bounds__(256) void k_attn(Geo g, const float* __restrict__ q
   }
 }
 
-#define FERRY_ATTN_INST(DT, G)                                                              \
-  template __global__ void k_attn<DT, G>(Geo, const float*, const uint32_t*, const uint8_t*, \
-                                         const float*, float*, float, int, int, int*);
-#define FERRY_ATTN_INST_G(DT) \
-  FERRY_ATTN_INST(DT, 1)      \
-  FERRY_ATTN_INST(DT, 2)      \
-  FERRY_ATTN_INST(DT, 4)      \
-  FERRY_ATTN_INST(DT, 8)
-FERRY_ATTN_INST_G(FERRY_F32)
-FERRY_ATTN_INST_G(FERRY_F16)
-FERRY_ATTN_INST_G(FERRY_BF16)
-FERRY_ATTN_INST_G(FERRY_FP8_E4M3)
+#define FERRY_ATTN_INST(DT, G, W)                                                       \
+  template __global__ void k_attn<DT, G, W>(Geo, const float*, const uint32_t*,          \
+                                            const uint8_t*, const float*, float*, float, \
+                                            int, int, int*);
+#define FERRY_ATTN_INST_G(DT, W) \
+  FERRY_ATTN_INST(DT, 1, W)      \
+  FERRY_ATTN_INST(DT, 2, W)      \
+  FERRY_ATTN_INST(DT, 4, W)      \
+  FERRY_ATTN_INST(DT, 8, W)
+#define FERRY_ATTN_INST_ALL(W)          \
+  FERRY_ATTN_INST_G(FERRY_F32, W)       \
+  FERRY_ATTN_INST_G(FERRY_F16, W)       \
+  FERRY_ATTN_INST_G(FERRY_BF16, W)      \
+  FERRY_ATTN_INST_G(FERRY_FP8_E4M3, W)
+FERRY_ATTN_INST_ALL(4)
+FERRY_ATTN_INST_ALL(8)
 
 }  // namespace ferry_amd

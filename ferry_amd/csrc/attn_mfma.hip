@@ -11,7 +11,7 @@
 //   S^T[16 tok][16 hd] = K[16 tok][128] . Q^T[128][16 hd]   (4x mfma 16x16x32)
 //   O^T[128][16 hd]   += V^T[128][16 tok] . P^T[16 tok][16 hd] (8x mfma 16x16x16)
 // with the G heads padded to the 16 columns of the tile.  One workgroup per
-// (request, layer, kv head); its four wavefronts take every fourth block.
+// (request, layer, kv head); its W wavefronts take every W-th block.
 //
 // Operand layouts (lane l, n = l % 16, grp = l / 16):
 //  * A of 16x16xK: lane holds A[m = n][k in grp's K/4 slice]; B likewise with
@@ -73,8 +73,8 @@ __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 }  // namespace
 
-template <int DT, int G>
-__global__ __launch_bounds__(256) void k_attn_mfma(Geo g, const float* __restrict__ q,
+template <int DT, int G, int W>
+__global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __restrict__ q,
                                                    const uint32_t* __restrict__ slots,
                                                    const uint8_t* __restrict__ pool,
                                                    const float* __restrict__ pool_scales,
@@ -91,9 +91,11 @@ __global__ __launch_bounds__(256) void k_attn_mfma(Geo g, const float* __restric
   constexpr int EPW = 16 / ES;         // elements per K word
   constexpr int SUB = EPW / 8;         // 8-element MFMA k-slices per K word
   constexpr float kNeg = -1.0e30f;
+  constexpr int NPF = 3;  // prefetch ring depth
 
-  __shared__ float red_o[4][G][D];
-  __shared__ float red_ml[4][G][2];
+  __shared__ float red_o[W][G][D];
+  __shared__ float red_ml[W][G][2];
+  __shared__ uint32_t ids[kMaxTopK];
 
   const int h = blockIdx.x % g.Hkv;
   const int rl = (blockIdx.x / (nl * g.Hkv)) * g.L + l0 + (blockIdx.x / g.Hkv) % nl;
@@ -139,16 +141,22 @@ __global__ __launch_bounds__(256) void k_attn_mfma(Geo g, const float* __restric
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // The row's slot ids are staged in LDS: a slot lookup is then an LDS read
+  // (lgkmcnt) that never waits on the block loads in flight (vmcnt).
   const uint32_t* sl = slots + (size_t)row * g.k;
   const int k = g.k;
-  const int nblk = k > wave ? (k - wave + 3) / 4 : 0;
-  auto slot_of = [&](uint32_t sidx, int i) -> uint64_t {
-    uint64_t slot = (uint32_t)__builtin_amdgcn_readlane((int)sidx, i & 63);
-    if (slot >= g.pool_slots) {  // never read outside the pool
-      set_error(err, FERRY_ERANGE);
-      slot = 0;
-    }
-    return slot;
+  for (int j = threadIdx.x; j < k; j += W * 64) ids[j] = sl[j];
+  __syncthreads();
+  const int nblk = k > wave ? (k - wave + W - 1) / W : 0;
+  // A slot outside the pool is read as slot 0 and reported once at the end
+  // (no branch in the block loop).
+  bool bad_slot = false;
+  auto slot_at = [&](int j) -> uint64_t {
+    const uint64_t slot =
+        (uint32_t)__builtin_amdgcn_readfirstlane((int)ids[wave + W * min(j, nblk - 1)]);
+    const bool bad = slot >= g.pool_slots;
+    bad_slot |= bad;
+    return bad ? 0 : slot;
   };
   // K words: token n, byte offset 16*(4*w + grp) of its row.  V words: tokens
   // 4*grp+i, bytes [8n, 8n+8) elements of the row (16 B for 16-bit, 8 B fp8).
@@ -171,128 +179,137 @@ __global__ __launch_bounds__(256) void k_attn_mfma(Geo g, const float* __restric
     }
   };
 
-  uint32_t sidx = 0;
-  u32x4 kw[NKW], nkw[NKW];
-  uint32_t vw[4][VW], nvw[4][VW];
-  uint64_t cur = 0;
-  if (nblk > 0) {
-    sidx = lane < nblk ? sl[wave + 4 * lane] : 0u;
-    cur = slot_of(sidx, 0);
-    load_block(cur, kw, vw);
-  }
-  for (int i = 0; i < nblk; ++i) {
-    uint64_t nxt = 0;
-    if (i + 1 < nblk) {
-      if (((i + 1) & 63) == 0) sidx = (lane + i + 1) < nblk ? sl[wave + 4 * (lane + i + 1)] : 0u;
-      nxt = slot_of(sidx, i + 1);
-      load_block(nxt, nkw, nvw);
-    }
-    float ks = 1.0f, vs = 1.0f;
+  // Ring of NPF block buffers: while block j (= wave + W*j of the row) is
+  // consumed, blocks j+1 .. j+NPF-1 are in flight.  The loop is unrolled by NPF
+  // so every buffer index is static, and every iteration issues its load (past
+  // the end it re-reads the last block, an L2 hit) so the compiler's load
+  // counters stay exact.
+  u32x4 kb[NPF][NKW];
+  uint32_t vb[NPF][4][VW];
+  float ksb[NPF], vsb[NPF];
+  auto issue = [&](int j, int b) {
+    const uint64_t slot = slot_at(j);
+    load_block(slot, kb[b], vb[b]);
     if constexpr (F8) {
-      ks = pool_scales[2 * cur];
-      vs = pool_scales[2 * cur + 1];
-    }
-    // ---- scores S^T = K . Q^T
-    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int w = kk / SUB, sub = kk % SUB;
-      u32x4 a;
-      if constexpr (F8) {
-        const u32x2 lo = e4m3x4_to_f16(kw[w][2 * sub]), hi = e4m3x4_to_f16(kw[w][2 * sub + 1]);
-        a = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      } else {
-        a = kw[w];
-      }
-      const u32x4 bh = {qhi[kk][0], qhi[kk][1], qhi[kk][2], qhi[kk][3]};
-      if constexpr (BF) {
-        const u32x4 bl = {qlo[kk][0], qlo[kk][1], qlo[kk][2], qlo[kk][3]};
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                    __builtin_bit_cast(bf16x8, bh), s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                    __builtin_bit_cast(bf16x8, bl), s, 0, 0, 0);
-      } else {
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                   __builtin_bit_cast(f16x8, bh), s, 0, 0, 0);
-      }
-    }
-    // ---- online softmax of head n over tokens 4*grp+i (max shared by the 4 groups)
-    float sv[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) sv[t] = s[t] * ks;
-    float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
-    const float mn = fmaxf(m, bm);
-    const float alpha = exp2_fast(m - mn);
-    m = mn;
-    float p[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) p[t] = exp2_fast(sv[t] - mn);
-    lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    float fac = alpha;
-    if constexpr (F8) {
-      fac = alpha * (vs_cur * __builtin_amdgcn_rcpf(vs));
-      vs_cur = vs;
-    }
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc[nb] *= fac;
-    // ---- P^T operand
-    u32x2 ph, pl;
-    if constexpr (BF) {
-      uint32_t hb[4];
-      float r[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        hb[t] = __builtin_bit_cast(uint32_t, p[t]) & 0xFFFF0000u;
-        r[t] = p[t] - __builtin_bit_cast(float, hb[t]);
-      }
-      ph = u32x2{perm(hb[1], hb[0], kSelHi), perm(hb[3], hb[2], kSelHi)};
-      pl = u32x2{perm(__builtin_bit_cast(uint32_t, r[1]), __builtin_bit_cast(uint32_t, r[0]), kSelHi),
-                 perm(__builtin_bit_cast(uint32_t, r[3]), __builtin_bit_cast(uint32_t, r[2]), kSelHi)};
+      ksb[b] = pool_scales[2 * slot];
+      vsb[b] = pool_scales[2 * slot + 1];
     } else {
-      const f16x4 pv = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
-      ph = __builtin_bit_cast(u32x2, pv);
-      pl = u32x2{0u, 0u};
+      ksb[b] = vsb[b] = 1.0f;
     }
-    // ---- V^T operands (dim 8n + nb, tokens 4*grp + 0..3) and O^T += V^T . P^T
-    uint32_t vh[4][4];  // per token: 8 halves of dims 8n..8n+7
+  };
+  if (nblk > 0) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if constexpr (F8) {
-        const u32x2 lo = e4m3x4_to_f16(vw[t][0]), hi = e4m3x4_to_f16(vw[t][1]);
-        vh[t][0] = lo[0], vh[t][1] = lo[1], vh[t][2] = hi[0], vh[t][3] = hi[1];
-      } else {
+    for (int b = 0; b < NPF - 1; ++b) issue(b, b);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int i0 = 0; i0 < nblk; i0 += NPF) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) vh[t][w] = vw[t][w];
+    for (int b = 0; b < NPF; ++b) {
+      const int i = i0 + b;
+      if (i < nblk) {
+        issue(i + NPF - 1, (b + NPF - 1) % NPF);
+      // keep the prefetch here: the scheduler would sink it to its first use
+      __builtin_amdgcn_sched_barrier(0);
+        const u32x4* kw = kb[b];
+        const uint32_t(*vw)[VW] = vb[b];
+        const float ks = ksb[b], vs = vsb[b];
+        // ---- scores S^T = K . Q^T
+        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int w = kk / SUB, sub = kk % SUB;
+          u32x4 a;
+          if constexpr (F8) {
+            const u32x2 lo = e4m3x4_to_f16(kw[w][2 * sub]);
+            const u32x2 hi = e4m3x4_to_f16(kw[w][2 * sub + 1]);
+            a = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          } else {
+            a = kw[w];
+          }
+          const u32x4 bh = {qhi[kk][0], qhi[kk][1], qhi[kk][2], qhi[kk][3]};
+          if constexpr (BF) {
+            const u32x4 bl = {qlo[kk][0], qlo[kk][1], qlo[kk][2], qlo[kk][3]};
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                        __builtin_bit_cast(bf16x8, bh), s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                        __builtin_bit_cast(bf16x8, bl), s, 0, 0, 0);
+          } else {
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                       __builtin_bit_cast(f16x8, bh), s, 0, 0, 0);
+          }
+        }
+        // ---- online softmax of head n over tokens 4*grp+i (max shared by the 4 groups)
+        float sv[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) sv[t] = s[t] * ks;
+        float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float mn = fmaxf(m, bm);
+        const float alpha = exp2_fast(m - mn);
+        m = mn;
+        float p[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) p[t] = exp2_fast(sv[t] - mn);
+        lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+        float fac = alpha;
+        if constexpr (F8) {
+          fac = alpha * (vs_cur * __builtin_amdgcn_rcpf(vs));
+          vs_cur = vs;
+        }
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[nb] *= fac;
+        // ---- P^T operand
+        u32x2 ph, pl;
+        if constexpr (BF) {
+          uint32_t hb[4];
+          float r[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            hb[t] = __builtin_bit_cast(uint32_t, p[t]) & 0xFFFF0000u;
+            r[t] = p[t] - __builtin_bit_cast(float, hb[t]);
+          }
+          ph = u32x2{perm(hb[1], hb[0], kSelHi), perm(hb[3], hb[2], kSelHi)};
+          const uint32_t r0 = __builtin_bit_cast(uint32_t, r[0]), r1 = __builtin_bit_cast(uint32_t, r[1]);
+          const uint32_t r2 = __builtin_bit_cast(uint32_t, r[2]), r3 = __builtin_bit_cast(uint32_t, r[3]);
+          pl = u32x2{perm(r1, r0, kSelHi), perm(r3, r2, kSelHi)};
+        } else {
+          const f16x4 pv = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+          ph = __builtin_bit_cast(u32x2, pv);
+          pl = u32x2{0u, 0u};
+        }
+        // ---- V^T operands (dim 8n + nb, tokens 4*grp + 0..3) and O^T += V^T . P^T
+        uint32_t vh[4][4];  // per token: 8 halves of dims 8n..8n+7
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if constexpr (F8) {
+            const u32x2 lo = e4m3x4_to_f16(vw[t][0]), hi = e4m3x4_to_f16(vw[t][1]);
+            vh[t][0] = lo[0], vh[t][1] = lo[1], vh[t][2] = hi[0], vh[t][3] = hi[1];
+          } else {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) vh[t][w] = vw[t][w];
+          }
+        }
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          const int w = nb >> 1;
+          const uint32_t sel = (nb & 1) ? kSelHi : kSelLo;
+          const u32x2 a = {perm(vh[1][w], vh[0][w], sel), perm(vh[3][w], vh[2][w], sel)};
+          if constexpr (BF) {
+            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                __builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, ph), acc[nb], 0, 0, 0);
+            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                __builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, pl), acc[nb], 0, 0, 0);
+          } else {
+            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                __builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, ph), acc[nb], 0, 0, 0);
+          }
+        }
       }
     }
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const int w = nb >> 1;
-      const uint32_t sel = (nb & 1) ? kSelHi : kSelLo;
-      const u32x2 a = {perm(vh[1][w], vh[0][w], sel), perm(vh[3][w], vh[2][w], sel)};
-      if constexpr (BF) {
-        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-            __builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, ph), acc[nb], 0, 0, 0);
-        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-            __builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, pl), acc[nb], 0, 0, 0);
-      } else {
-        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(
-            __builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, ph), acc[nb], 0, 0, 0);
-      }
-    }
-    if (i + 1 < nblk) {
-#pragma unroll
-      for (int w = 0; w < NKW; ++w) kw[w] = nkw[w];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int w = 0; w < VW; ++w) vw[t][w] = nvw[t][w];
-    }
-    cur = nxt;
   }
 
+  if (bad_slot && lane == 0) set_error(err, FERRY_ERANGE);
   // ---- per-wave totals: l over the 4 lane groups; O^T rows to LDS
   lsum += __shfl_xor(lsum, 16);
   lsum += __shfl_xor(lsum, 32);
@@ -307,13 +324,13 @@ __global__ __launch_bounds__(256) void k_attn_mfma(Geo g, const float* __restric
     }
   }
   __syncthreads();
-  // ---- merge the four wavefronts and write out
+  // ---- merge the W wavefronts and write out
   for (int t = threadIdx.x; t < G * D; t += blockDim.x) {
     const int hq = t / D, d = t % D;
     float mx = red_ml[0][hq][0];
-    for (int w = 1; w < 4; ++w) mx = fmaxf(mx, red_ml[w][hq][0]);
+    for (int w = 1; w < W; ++w) mx = fmaxf(mx, red_ml[w][hq][0]);
     float l = 0.0f, o = 0.0f;
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float a = exp2_fast(red_ml[w][hq][0] - mx);
       l += red_ml[w][hq][1] * a;
       o += red_o[w][hq][d] * a;
@@ -322,16 +339,19 @@ __global__ __launch_bounds__(256) void k_attn_mfma(Geo g, const float* __restric
   }
 }
 
-#define FERRY_ATTN_MFMA_INST(DT, G)                                                     \
-  template __global__ void k_attn_mfma<DT, G>(Geo, const float*, const uint32_t*,       \
-                                              const uint8_t*, const float*, float*, float, \
-                                              int, int, int*);
-#define FERRY_ATTN_MFMA_INST_G(DT) \
-  FERRY_ATTN_MFMA_INST(DT, 2)      \
-  FERRY_ATTN_MFMA_INST(DT, 4)      \
-  FERRY_ATTN_MFMA_INST(DT, 8)
-FERRY_ATTN_MFMA_INST_G(FERRY_F16)
-FERRY_ATTN_MFMA_INST_G(FERRY_BF16)
-FERRY_ATTN_MFMA_INST_G(FERRY_FP8_E4M3)
+#define FERRY_ATTN_MFMA_INST(DT, G, W)                                                    \
+  template __global__ void k_attn_mfma<DT, G, W>(Geo, const float*, const uint32_t*,         \
+                                                 const uint8_t*, const float*, float*, float, \
+                                                 int, int, int*);
+#define FERRY_ATTN_MFMA_INST_G(DT, W) \
+  FERRY_ATTN_MFMA_INST(DT, 2, W)      \
+  FERRY_ATTN_MFMA_INST(DT, 4, W)      \
+  FERRY_ATTN_MFMA_INST(DT, 8, W)
+#define FERRY_ATTN_MFMA_INST_ALL(W)        \
+  FERRY_ATTN_MFMA_INST_G(FERRY_F16, W)     \
+  FERRY_ATTN_MFMA_INST_G(FERRY_BF16, W)    \
+  FERRY_ATTN_MFMA_INST_G(FERRY_FP8_E4M3, W)
+FERRY_ATTN_MFMA_INST_ALL(4)
+FERRY_ATTN_MFMA_INST_ALL(8)
 
 }  // namespace ferry_amd

@@ -15,6 +15,9 @@ namespace ferry_amd {
 constexpr uint32_t kNone = 0xFFFFFFFFu;
 constexpr uint32_t kPend = 0x80000000u;  // map entry: pending miss, low bits = position
 constexpr int kWave = 64;
+// Largest top-k per (request, layer, kv head): the attention kernels stage a
+// row's slot ids in LDS (4 KiB).
+constexpr int kMaxTopK = 1024;
 
 // Immutable executor geometry, passed to kernels by value.
 struct Geo {

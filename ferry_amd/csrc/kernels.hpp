@@ -51,12 +51,14 @@ template <int NV>
 __global__ void k_fetch(FetchArgs a);
 __global__ void k_missq_push(Geo g, Ring ring, const ferry_miss* m, uint32_t n, int* err);
 
-template <int DT, int G>
+// Vector-ALU attention (attn.hip); W wavefronts per workgroup.
+template <int DT, int G, int W>
 __global__ void k_attn(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
                        const float* pool_scales, float* out, float qscale, int l0, int nl, int* err);
 
-// MFMA variant for GQA groups (G >= 2) of 16/8-bit KV (attn_mfma.hip).
-template <int DT, int G>
+// MFMA variant for GQA groups (G >= 2) of 16/8-bit KV (attn_mfma.hip); W
+// wavefronts per workgroup.
+template <int DT, int G, int W>
 __global__ void k_attn_mfma(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
                             const float* pool_scales, float* out, float qscale, int l0, int nl,
                             int* err);

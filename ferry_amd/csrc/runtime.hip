@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -72,6 +73,7 @@ struct ferry_ctx {
   size_t lru_lds = 0;
   uint64_t steps = 0, selections = 0;
   std::vector<hipEvent_t> events;  // layer-chunk pipeline of ferry_decode_step
+  int attn_waves = 0;              // wavefronts per attention workgroup (FERRY_ATTN_WAVES), 0 = default
 
   Ring ring() const {
     Ring r;
@@ -91,6 +93,7 @@ int validate(const ferry_config* c) {
   if (c->n_req < 1 || c->group < 1 || c->n_layers < 1 || c->kv_heads < 1 || c->q_heads < 1 ||
       c->k < 1 || c->slots_per_set < 1 || c->max_blocks < 1 || c->host_blocks < 1)
     return fail(FERRY_EINVAL, "sizes must be positive");
+  if (c->k > kMaxTopK) return fail(FERRY_EINVAL, "k must be <= 1024");
   if (c->q_heads % c->kv_heads) return fail(FERRY_EINVAL, "q_heads must be a multiple of kv_heads");
   const int grp = c->q_heads / c->kv_heads;
   if (grp != 1 && grp != 2 && grp != 4 && grp != 8)
@@ -135,6 +138,85 @@ int check_ctx(const ferry_ctx* c) { return c ? FERRY_OK : fail(FERRY_EINVAL, "nu
 
 }  // namespace
 
+namespace {
+
+struct AttnArgs {
+  Geo g;
+  const float* q;
+  const uint32_t* slots;
+  const uint8_t* pool;
+  const float* pool_scales;
+  float* out;
+  float qscale;
+  int l0, nl;
+  int* err;
+};
+
+// Which attention kernel runs and how many wavefronts share one (request,
+// layer, kv head) row.  MFMA for GQA groups of 16/8-bit KV unless the config
+// asks for the VALU kernel.  Four wavefronts per row; eight (FERRY_ATTN_WAVES=8)
+// measured the same on MI355X.
+struct AttnPlan {
+  bool mfma;
+  int dtype, G, waves;
+};
+
+AttnPlan attn_plan(const ferry_ctx* ctx) {
+  const Geo& g = ctx->g;
+  AttnPlan p;
+  p.dtype = g.dtype;
+  p.G = g.Hq / g.Hkv;
+  p.mfma = g.dtype != FERRY_F32 && p.G >= 2 && ctx->cfg.attn != FERRY_ATTN_VALU;
+  p.waves = 4;
+  if (ctx->attn_waves == 8) p.waves = 8;
+  return p;
+}
+
+template <int DT, int G, int W>
+void launch_valu(const dim3& grid, hipStream_t s, const AttnArgs& a) {
+  hipLaunchKernelGGL((k_attn<DT, G, W>), grid, dim3(W * 64), 0, s, a.g, a.q, a.slots, a.pool,
+                     a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
+}
+template <int DT, int G, int W>
+void launch_mfma(const dim3& grid, hipStream_t s, const AttnArgs& a) {
+  hipLaunchKernelGGL((k_attn_mfma<DT, G, W>), grid, dim3(W * 64), 0, s, a.g, a.q, a.slots,
+                     a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
+}
+template <int DT, int G>
+void launch_g(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs& a) {
+  if constexpr (DT != FERRY_F32 && G >= 2) {
+    if (p.mfma) {
+      switch (p.waves) {
+        case 8: launch_mfma<DT, G, 8>(grid, s, a); return;
+        default: launch_mfma<DT, G, 4>(grid, s, a); return;
+      }
+    }
+  }
+  switch (p.waves) {
+    case 8: launch_valu<DT, G, 8>(grid, s, a); return;
+    default: launch_valu<DT, G, 4>(grid, s, a); return;
+  }
+}
+template <int DT>
+void launch_dt(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs& a) {
+  switch (p.G) {
+    case 1: launch_g<DT, 1>(p, grid, s, a); return;
+    case 2: launch_g<DT, 2>(p, grid, s, a); return;
+    case 4: launch_g<DT, 4>(p, grid, s, a); return;
+    default: launch_g<DT, 8>(p, grid, s, a); return;
+  }
+}
+void launch_attn(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs& a) {
+  switch (p.dtype) {
+    case FERRY_F32: launch_dt<FERRY_F32>(p, grid, s, a); return;
+    case FERRY_F16: launch_dt<FERRY_F16>(p, grid, s, a); return;
+    case FERRY_BF16: launch_dt<FERRY_BF16>(p, grid, s, a); return;
+    default: launch_dt<FERRY_FP8_E4M3>(p, grid, s, a); return;
+  }
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* ferry_last_error(void) { return g_err.c_str(); }
@@ -148,6 +230,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   HIPC(hipSetDevice(device));
   ferry_ctx* c = new ferry_ctx();
   c->cfg = *cfg;
+  if (const char* e = std::getenv("FERRY_ATTN_WAVES")) c->attn_waves = std::atoi(e);
   c->device = device;
   Geo& g = c->g;
   g.n_req = cfg->n_req;
@@ -421,44 +504,11 @@ int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const flo
   const Geo& g = ctx->g;
   if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
   HIPC(hipSetDevice(ctx->device));
-  const dim3 grid((unsigned)(g.n_req * nl * g.Hkv)), block(256);
+  const dim3 grid((unsigned)(g.n_req * nl * g.Hkv));
   const float qscale = (float)(1.4426950408889634 / std::sqrt((double)g.D));
-  const int G = g.Hq / g.Hkv;
-  hipStream_t s = (hipStream_t)stream;
-  const bool mfma = g.dtype != FERRY_F32 && G >= 2 && ctx->cfg.attn != FERRY_ATTN_VALU;
-#define ATTN(K, DT, GG)                                                                    \
-  hipLaunchKernelGGL((K<DT, GG>), grid, block, 0, s, g, q, slots, ctx->pool,              \
-                     ctx->pool_scales, out, qscale, l0, nl, ctx->err)
-#define ATTN_G(DT)                                      \
-  if (mfma) {                                           \
-    switch (G) {                                        \
-      case 2: ATTN(k_attn_mfma, DT, 2); break;          \
-      case 4: ATTN(k_attn_mfma, DT, 4); break;          \
-      default: ATTN(k_attn_mfma, DT, 8); break;         \
-    }                                                   \
-  } else {                                              \
-    switch (G) {                                        \
-      case 1: ATTN(k_attn, DT, 1); break;               \
-      case 2: ATTN(k_attn, DT, 2); break;               \
-      case 4: ATTN(k_attn, DT, 4); break;               \
-      default: ATTN(k_attn, DT, 8); break;              \
-    }                                                   \
-  }
-  switch (g.dtype) {
-    case FERRY_F32:
-      switch (G) {
-        case 1: ATTN(k_attn, FERRY_F32, 1); break;
-        case 2: ATTN(k_attn, FERRY_F32, 2); break;
-        case 4: ATTN(k_attn, FERRY_F32, 4); break;
-        default: ATTN(k_attn, FERRY_F32, 8); break;
-      }
-      break;
-    case FERRY_F16: ATTN_G(FERRY_F16); break;
-    case FERRY_BF16: ATTN_G(FERRY_BF16); break;
-    default: ATTN_G(FERRY_FP8_E4M3); break;
-  }
-#undef ATTN_G
-#undef ATTN
+  const AttnArgs a{g, q, slots, ctx->pool, ctx->pool_scales, out, qscale, l0, nl, ctx->err};
+  const AttnPlan p = attn_plan(ctx);
+  launch_attn(p, grid, (hipStream_t)stream, a);
   HIPC(hipGetLastError());
   return FERRY_OK;
 }
