@@ -280,6 +280,12 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     r1.record(stream)
     torch.cuda.synchronize()
     t_attn_rep = r0.elapsed_time(r1) / a.steps
+    # ceilings: plain reads of the same bytes (attention slots; host-tier blocks)
+    _, _, gather_gbs = ex.bw_probe(F.PROBE_HBM_GATHER, B * L * H, slots=bufs["slots"],
+                                   iters=max(3, a.steps // 2), stream=stream)
+    n_host = int(min(a.host_blocks, max(1, (st2["misses"] - m0) // a.steps)))
+    _, _, hread_gbs = ex.bw_probe(F.PROBE_HOST_READ, n_host, iters=3, stream=stream)
+    _, _, hdma_gbs = ex.bw_probe(F.PROBE_HOST_DMA, n_host, iters=3, stream=stream)
     ev_misses = st2["misses"] - m0
     t_book = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
     t_fetch = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
@@ -307,10 +313,14 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
                       "attention": round(t_attn, 4), "attention_back_to_back": round(t_attn_rep, 4)},
         "roofline": {"bound": "hbm", "kernel": attn_kernel,
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "plain_gather_gbs": round(gather_gbs, 1),
+                     "frac_of_plain_gather": round(attn_gbs / gather_gbs, 4)},
         "roofline_fetch": {"bound": "host-link", "kernel": f"k_fetch<{bb // 1024}>",
                            "achieved": round(link_gbs, 2), "peak": round(LINK_PEAK_GBS, 2),
-                           "unit": "GB/s", "frac": round(link_gbs / LINK_PEAK_GBS, 4)},
+                           "unit": "GB/s", "frac": round(link_gbs / LINK_PEAK_GBS, 4),
+                           "plain_read_gbs": round(hread_gbs, 2), "dma_copy_gbs": round(hdma_gbs, 2),
+                           "frac_of_plain_read": round(link_gbs / hread_gbs, 4)},
         "steals_per_step": round((st2["steals"] - s0) / a.steps, 1),
         "selection_gen_s": round(gen_s, 2),
         "config_extra": {"slots_per_set": C, "host_tier_blocks": a.host_blocks,

@@ -37,6 +37,7 @@ F32, F16, BF16, FP8 = 0, 1, 2, 3
 LRU_STEP, LRU_SERIAL = 0, 1
 ASSIGN_SPREAD, ASSIGN_AFFINITY = 0, 1
 ATTN_AUTO, ATTN_VALU, ATTN_MFMA = 0, 1, 2
+PROBE_HBM_GATHER, PROBE_HOST_READ, PROBE_HOST_DMA = 0, 1, 2
 ESIZE = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 MISS_DTYPE = np.dtype([("block", "<u4"), ("slot", "<u4"), ("evicted", "<u4"), ("set", "<u4")])
 
@@ -105,6 +106,8 @@ _PROTOS = {
     "ferry_missq_drain": (C.c_int, [_vp, _vp]),
     "ferry_sparse_decode": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "ferry_stats_get": (C.c_int, [_vp, C.POINTER(Stats)]),
+    "ferry_bw_probe": (C.c_int, [_vp, C.c_int, _vp, C.c_uint64, C.c_int,
+                                 C.POINTER(C.c_uint64), C.POINTER(C.c_float), _vp]),
     "ferry_stats_reset": (C.c_int, [_vp]),
     "ferry_queue_selftest": (C.c_int, [C.c_int, C.c_uint64, C.c_uint64, C.c_int, C.c_int,
                                        C.c_int, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
@@ -238,6 +241,14 @@ class Executor:
         s = Stats()
         _check(lib.ferry_stats_get(self._h, C.byref(s)), "ferry_stats_get")
         return {f: getattr(s, f) for f, _ in Stats._fields_ if f != "pad"}
+
+    def bw_probe(self, kind, n, slots=None, iters=5, stream=None):
+        """Plain-read bandwidth ceiling (ferry_bw_probe): returns (bytes per
+        launch, mean ms per launch, GB/s)."""
+        b, ms = C.c_uint64(), C.c_float()
+        _check(lib.ferry_bw_probe(self._h, kind, _ptr(slots), n, iters, C.byref(b), C.byref(ms),
+                                  _stream(stream)), "ferry_bw_probe")
+        return b.value, ms.value, b.value / (ms.value * 1e-3) / 1e9
 
     def stats_reset(self):
         _check(lib.ferry_stats_reset(self._h), "ferry_stats_reset")

@@ -63,6 +63,14 @@ __global__ void k_attn_mfma(Geo g, const float* q, const uint32_t* slots, const 
                             const float* pool_scales, float* out, float qscale, int l0, int nl,
                             int* err);
 
+// Bandwidth ceilings (probe.hip): the attention kernels' loads without their
+// math, and device-direct host-tier reads without the fetch bookkeeping.
+template <int NLD>
+__global__ void k_probe_gather(const uint8_t* pool, uint64_t bb, const uint32_t* slots, int k,
+                               uint64_t pool_slots, uint32_t* sink);
+template <int NV>
+__global__ void k_probe_host(const uint8_t* host, uint64_t bb, uint64_t n_blocks, uint32_t* sink);
+
 __global__ void k_hosttier_fill(Geo g, uint8_t* host, float* scales, uint64_t seed, float mult,
                                 float mult8, float scale_base);
 

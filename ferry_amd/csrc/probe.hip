@@ -1,0 +1,101 @@
+// probe.hip -- bandwidth ceilings for the roofline.
+//
+// The executor's kernels are bound by HBM (attention) and by the host link
+// (fetch).  These probes move the same bytes with no other work, so a kernel's
+// achieved rate can be read against what plain reads reach on the same part:
+//  * k_probe_gather: the attention kernels' loads (the k pool slots of every
+//    (request, layer, kv head) row, ids staged in LDS, a two-block ring per
+//    wavefront) with the softmax and products replaced by an XOR;
+//  * k_probe_host: device-direct 16-byte reads of consecutive host-tier
+//    blocks over the host link, as the fetch kernel issues them, without the
+//    ring bookkeeping or the pool writes.
+// They play the role of the reference's host-staged bandwidth sweep
+// (probe_host_staged_bandwidth, src/topo/topo.cpp:68-129), measured here for
+// the one-hop device-direct path instead of the two-hop pinned ring.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ferry_amd {
+
+namespace {
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+}
+
+template <int NLD>
+__global__ __launch_bounds__(256) void k_probe_gather(const uint8_t* __restrict__ pool, uint64_t bb,
+                                                      const uint32_t* __restrict__ slots, int k,
+                                                      uint64_t pool_slots,
+                                                      uint32_t* __restrict__ sink) {
+  constexpr int W = 4, NPF = 2;
+  __shared__ uint32_t ids[kMaxTopK];
+  __shared__ uint32_t red[W];
+  const int row = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t* sl = slots + (size_t)row * k;
+  for (int j = threadIdx.x; j < k; j += W * 64) ids[j] = sl[j];
+  __syncthreads();
+  const int nb = k > wave ? (k - wave + W - 1) / W : 0;
+  u32x4 buf[NPF][NLD];
+  auto issue = [&](int j, int b) {
+    uint64_t slot = (uint32_t)__builtin_amdgcn_readfirstlane((int)ids[wave + W * min(j, nb - 1)]);
+    slot = slot < pool_slots ? slot : 0;
+    const u32x4* p = reinterpret_cast<const u32x4*>(pool + slot * bb);
+#pragma unroll
+    for (int ld = 0; ld < NLD; ++ld) buf[b][ld] = p[ld * 64 + lane];
+  };
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  if (nb > 0) {
+    issue(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int i0 = 0; i0 < nb; i0 += NPF) {
+#pragma unroll
+    for (int b = 0; b < NPF; ++b) {
+      const int i = i0 + b;
+      if (i >= nb) break;
+      issue(i + 1, (b + 1) % NPF);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int ld = 0; ld < NLD; ++ld) acc ^= buf[b][ld];
+    }
+  }
+  uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off);
+  if (lane == 0) red[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[row] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void k_probe_host(const uint8_t* __restrict__ host, uint64_t bb,
+                                                    uint64_t n_blocks, uint32_t* __restrict__ sink) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const uint64_t n_waves = (uint64_t)gridDim.x * (blockDim.x >> 6);
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (uint64_t b = wave; b < n_blocks; b += n_waves) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(host + b * bb);
+    u32x4 r[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) r[i] = __builtin_nontemporal_load(src + i * kWave + lane);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) acc ^= r[i];
+  }
+  uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off);
+  if (lane == 0) sink[wave] = x;
+}
+
+template __global__ void k_probe_gather<4>(const uint8_t*, uint64_t, const uint32_t*, int, uint64_t,
+                                           uint32_t*);
+template __global__ void k_probe_gather<8>(const uint8_t*, uint64_t, const uint32_t*, int, uint64_t,
+                                           uint32_t*);
+template __global__ void k_probe_gather<16>(const uint8_t*, uint64_t, const uint32_t*, int,
+                                            uint64_t, uint32_t*);
+template __global__ void k_probe_host<4>(const uint8_t*, uint64_t, uint64_t, uint32_t*);
+template __global__ void k_probe_host<8>(const uint8_t*, uint64_t, uint64_t, uint32_t*);
+template __global__ void k_probe_host<16>(const uint8_t*, uint64_t, uint64_t, uint32_t*);
+
+}  // namespace ferry_amd

@@ -74,6 +74,10 @@ struct ferry_ctx {
   uint64_t steps = 0, selections = 0;
   std::vector<hipEvent_t> events;  // layer-chunk pipeline of ferry_decode_step
   int attn_waves = 0;              // wavefronts per attention workgroup (FERRY_ATTN_WAVES), 0 = default
+  uint32_t* probe_sink = nullptr;  // bandwidth probes: one word per row / wavefront
+  size_t probe_sink_words = 0;
+  uint8_t* probe_dst = nullptr;    // bandwidth probes: DMA destination
+  size_t probe_dst_bytes = 0;
 
   Ring ring() const {
     Ring r;
@@ -125,7 +129,7 @@ void release(ferry_ctx* c) {
   (void)hipSetDevice(c->device);
   void* dev[] = {c->pool, c->pool_scales, c->st.fill, c->st.ord, c->st.tag, c->st.map,
                  c->ring_entries, c->ring_state, c->ring_seg, c->ring_cap, c->worker_of_set,
-                 c->stats, c->done, c->err};
+                 c->stats, c->done, c->err, c->probe_sink, c->probe_dst};
   for (void* p : dev)
     if (p) (void)hipFree(p);
   if (c->host) (void)hipHostFree(c->host);
@@ -547,6 +551,78 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
     }
     if ((rc = ferry_sparse_decode_layers(ctx, l0, nl, q, slots, out, ms))) return rc;
   }
+  return FERRY_OK;
+}
+
+int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, int iters,
+                   uint64_t* bytes, float* ms, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (kind < FERRY_PROBE_HBM_GATHER || kind > FERRY_PROBE_HOST_DMA) return fail(FERRY_EINVAL, "bad kind");
+  if (n < 1 || iters < 1) return fail(FERRY_EINVAL, "n and iters must be positive");
+  if (kind == FERRY_PROBE_HBM_GATHER && (!slots || n > 0x7FFFFFFFull))
+    return fail(FERRY_EINVAL, "gather needs a slot table of at most 2^31 rows");
+  if (kind != FERRY_PROBE_HBM_GATHER && n > ctx->g.host_blocks)
+    return fail(FERRY_EINVAL, "more blocks than the host tier holds");
+  const Geo& g = ctx->g;
+  HIPC(hipSetDevice(ctx->device));
+  hipStream_t s = (hipStream_t)stream;
+  const int host_waves = g.workers * 4;
+  const size_t words = kind == FERRY_PROBE_HBM_GATHER ? (size_t)n : (size_t)host_waves;
+  if (ctx->probe_sink_words < words) {
+    if (ctx->probe_sink) HIPC(hipFree(ctx->probe_sink));
+    ctx->probe_sink = nullptr;
+    ctx->probe_sink_words = 0;
+    HIPC(hipMalloc(&ctx->probe_sink, words * 4));
+    ctx->probe_sink_words = words;
+  }
+  const uint64_t moved = kind == FERRY_PROBE_HBM_GATHER ? n * (uint64_t)g.k * g.bb : n * g.bb;
+  if (kind == FERRY_PROBE_HOST_DMA && ctx->probe_dst_bytes < moved) {
+    if (ctx->probe_dst) HIPC(hipFree(ctx->probe_dst));
+    ctx->probe_dst = nullptr;
+    ctx->probe_dst_bytes = 0;
+    HIPC(hipMalloc(&ctx->probe_dst, moved));
+    ctx->probe_dst_bytes = moved;
+  }
+  const int nld = (int)(g.bb / 1024);
+  if (nld != 4 && nld != 8 && nld != 16) return fail(FERRY_EINVAL, "unsupported block size");
+  auto launch = [&]() -> hipError_t {
+    if (kind == FERRY_PROBE_HBM_GATHER) {
+      const dim3 grid((unsigned)n), block(256);
+      if (nld == 4)
+        hipLaunchKernelGGL(k_probe_gather<4>, grid, block, 0, s, ctx->pool, g.bb, slots, g.k, g.pool_slots, ctx->probe_sink);
+      else if (nld == 8)
+        hipLaunchKernelGGL(k_probe_gather<8>, grid, block, 0, s, ctx->pool, g.bb, slots, g.k, g.pool_slots, ctx->probe_sink);
+      else
+        hipLaunchKernelGGL(k_probe_gather<16>, grid, block, 0, s, ctx->pool, g.bb, slots, g.k, g.pool_slots, ctx->probe_sink);
+      return hipGetLastError();
+    }
+    if (kind == FERRY_PROBE_HOST_READ) {
+      const dim3 grid((unsigned)g.workers), block(256);
+      if (nld == 4)
+        hipLaunchKernelGGL(k_probe_host<4>, grid, block, 0, s, ctx->host_dev, g.bb, n, ctx->probe_sink);
+      else if (nld == 8)
+        hipLaunchKernelGGL(k_probe_host<8>, grid, block, 0, s, ctx->host_dev, g.bb, n, ctx->probe_sink);
+      else
+        hipLaunchKernelGGL(k_probe_host<16>, grid, block, 0, s, ctx->host_dev, g.bb, n, ctx->probe_sink);
+      return hipGetLastError();
+    }
+    return hipMemcpyAsync(ctx->probe_dst, ctx->host, moved, hipMemcpyHostToDevice, s);
+  };
+  HIPC(launch());  // warm-up
+  hipEvent_t e0, e1;
+  HIPC(hipEventCreate(&e0));
+  HIPC(hipEventCreate(&e1));
+  hipError_t err = hipEventRecord(e0, s);
+  for (int i = 0; i < iters && err == hipSuccess; ++i) err = launch();
+  if (err == hipSuccess) err = hipEventRecord(e1, s);
+  if (err == hipSuccess) err = hipEventSynchronize(e1);
+  float t = 0.0f;
+  if (err == hipSuccess) err = hipEventElapsedTime(&t, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  HIPC(err);
+  if (bytes) *bytes = moved;
+  if (ms) *ms = t / (float)iters;
   return FERRY_OK;
 }
 

@@ -204,6 +204,25 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
                       float* out, uint32_t* miss_count, ferry_miss* misses, int32_t chunks,
                       void* stream, void* side_stream);
 
+/* ---- bandwidth ceilings ----
+ * Plain reads of the bytes the executor's kernels move, timed with HIP events
+ * on `stream` over `iters` launches after one warm-up (synchronises):
+ *   FERRY_PROBE_HBM_GATHER  the attention loads without the math: the k pool
+ *                           slots of each of the n rows of `slots` ([n][k],
+ *                           device); bytes = n*k*block_bytes
+ *   FERRY_PROBE_HOST_READ   device-direct 16-byte reads of host-tier blocks
+ *                           [0, n) by the fetch workgroups, no pool writes
+ *   FERRY_PROBE_HOST_DMA    hipMemcpyAsync of host-tier blocks [0, n) into
+ *                           device memory (the copy engines)
+ * `bytes` gets the bytes moved per launch, `ms` the mean launch time.  The
+ * reference sweeps its host-staged channel the same way
+ * (probe_host_staged_bandwidth, src/topo/topo.cpp:68-129). */
+#define FERRY_PROBE_HBM_GATHER 0
+#define FERRY_PROBE_HOST_READ 1
+#define FERRY_PROBE_HOST_DMA 2
+int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, int iters,
+                   uint64_t* bytes, float* ms, void* stream);
+
 /* Counters (synchronises the device). */
 int ferry_stats_get(ferry_ctx* ctx, ferry_stats* out);
 int ferry_stats_reset(ferry_ctx* ctx);

@@ -363,3 +363,20 @@ def test_mfma_attention_long_selection():
         p.step(sels[0])
         p.check_attention(sels[0], seed=2)
         p.ex.close()
+
+
+def test_bandwidth_probes_move_the_stated_bytes():
+    # ferry_bw_probe: gather of a step's slot table, host reads and DMA copies
+    n_req, L, H, k = 4, 2, 2, 16
+    mb, sels = _zipf_stream(n_req, L, H, k, 60, 200, 1)
+    p = Pair(n_req, L, H, H, k, 32, mb, F.F16)
+    p.step(sels[0])
+    rows = n_req * L * H
+    b, ms, gbs = p.ex.bw_probe(F.PROBE_HBM_GATHER, rows, slots=p.bufs["slots"], iters=2)
+    assert b == rows * k * p.bb and ms > 0 and gbs > 0
+    for kind in (F.PROBE_HOST_READ, F.PROBE_HOST_DMA):
+        b, ms, gbs = p.ex.bw_probe(kind, 512, iters=2)
+        assert b == 512 * p.bb and ms > 0 and gbs > 0
+    with pytest.raises(F.FerryError):
+        p.ex.bw_probe(F.PROBE_HOST_READ, 1 << 40)  # more than the host tier holds
+    assert p.ex.stats()["device_error"] == 0
