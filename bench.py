@@ -377,9 +377,9 @@ def main():
     r = run(a, w, F, torch)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if a.workload == "7b" and os.path.exists(tpath):
+    if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("attention_bytes_per_launch")
+            traffic = json.load(f).get(a.workload, {}).get("bytes_per_launch")
     r["roofline"]["traffic"] = traffic
     lo, hi = w["ctx"]
     desc = (f"B={w['B']}, L={w['L']}, Hq={w['Hq']}, Hkv={w['Hkv']}, D=128, {w['dtype']} KV, "
