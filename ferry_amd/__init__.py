@@ -14,6 +14,9 @@ Reference interfaces mirrored (clearleo126/ferry, paths relative to its tree):
   Executor.sparse_decode   attn_kernel / wla_attn_kernel (real attention here)
   queue_selftest           bench_queue (src/benches/bench_queue.cu:62-123)
   SelGen / refgen_selections  replay_miss_stream (src/workloads/missstream.cuh:104)
+  arrivals / Sched         request arrivals and the per-GPU tick loop
+                           (src/runtime/wla_multigpu.cuh:497-501, 829-864,
+                           2610-2665)
 """
 import ctypes as C
 import os
@@ -22,9 +25,10 @@ import numpy as np
 import torch  # noqa: F401  (HIP runtime + device memory; load before the library)
 
 __all__ = [
-    "FerryError", "Executor", "SelGen", "queue_selftest", "refgen_selections",
-    "ctx_uniform", "lib", "LIB_PATH", "F32", "F16", "BF16", "FP8", "LRU_STEP", "LRU_SERIAL",
-    "ASSIGN_SPREAD", "ASSIGN_AFFINITY", "ATTN_AUTO", "ATTN_VALU", "ATTN_MFMA", "MISS_DTYPE",
+    "FerryError", "Executor", "SelGen", "Sched", "queue_selftest", "refgen_selections",
+    "ctx_uniform", "arrivals", "lib", "LIB_PATH", "F32", "F16", "BF16", "FP8", "LRU_STEP",
+    "LRU_SERIAL", "ASSIGN_SPREAD", "ASSIGN_AFFINITY", "ATTN_AUTO", "ATTN_VALU", "ATTN_MFMA",
+    "MISS_DTYPE", "EMPTY", "ARRIVAL_STEADY", "ARRIVAL_BURSTY", "ARRIVAL_POISSON", "ARRIVAL_MMPP",
 ]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libferry_amd.so")
@@ -38,6 +42,8 @@ LRU_STEP, LRU_SERIAL = 0, 1
 ASSIGN_SPREAD, ASSIGN_AFFINITY = 0, 1
 ATTN_AUTO, ATTN_VALU, ATTN_MFMA = 0, 1, 2
 PROBE_HBM_GATHER, PROBE_HOST_READ, PROBE_HOST_DMA = 0, 1, 2
+ARRIVAL_STEADY, ARRIVAL_BURSTY, ARRIVAL_POISSON, ARRIVAL_MMPP = 0, 1, 2, 3
+EMPTY = 0xFFFFFFFF  # selection id of an empty position (and its slot)
 ESIZE = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 MISS_DTYPE = np.dtype([("block", "<u4"), ("slot", "<u4"), ("evicted", "<u4"), ("set", "<u4")])
 
@@ -96,6 +102,17 @@ _PROTOS = {
     "ferry_pool_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),
     "ferry_sets_reset": (C.c_int, [_vp, _vp]),
     "ferry_sets_state": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "ferry_sets_reset_owners": (C.c_int, [_vp, _vp, C.c_uint32, _vp]),
+    "ferry_selgen_admit": (C.c_int, [_vp, _i32, _i32, _i32, _i32]),
+    "ferry_selgen_retire": (C.c_int, [_vp, _i32]),
+    "ferry_arrivals": (C.c_int, [C.c_int, C.c_uint32, C.c_double, C.c_double, C.c_double,
+                                 C.c_uint64, _vp]),
+    "ferry_sched_create": (C.c_int, [_i32, C.c_uint32, _vp, _vp, C.POINTER(_vp)]),
+    "ferry_sched_destroy": (C.c_int, [_vp]),
+    "ferry_sched_tick": (C.c_int, [_vp, C.c_double, _vp, _vp, _vp, C.POINTER(_i32), _vp,
+                                   C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32)]),
+    "ferry_sched_next_arrival": (C.c_int, [_vp, C.POINTER(C.c_double)]),
+    "ferry_sched_request_ticks": (C.c_int, [_vp, _vp, _vp]),
     "ferry_fetch_step": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ferry_bookkeep_step": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ferry_bookkeep_layers": (C.c_int, [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -236,6 +253,11 @@ class Executor:
     def sets_reset(self, stream=None):
         _check(lib.ferry_sets_reset(self._h, _stream(stream)), "ferry_sets_reset")
 
+    def reset_owners(self, owners, stream=None):
+        """Empty the sets of the owners in `owners` (int32 device tensor)."""
+        _check(lib.ferry_sets_reset_owners(self._h, _ptr(owners), int(owners.numel()),
+                                           _stream(stream)), "ferry_sets_reset_owners")
+
     # ---- inspection (synchronous) ---------------------------------------
     def stats(self):
         s = Stats()
@@ -350,6 +372,15 @@ class SelGen:
         _check(lib.ferry_selgen_step(self._h, step, out.ctypes.data), "ferry_selgen_step")
         return out
 
+    def admit(self, lane, request_id, ctx_blocks, step):
+        """Request `request_id` (context ctx_blocks) takes `lane` from `step` on."""
+        _check(lib.ferry_selgen_admit(self._h, lane, request_id, ctx_blocks, step),
+               "ferry_selgen_admit")
+
+    def retire(self, lane):
+        """`lane` produces empty rows until its next admission."""
+        _check(lib.ferry_selgen_retire(self._h, lane), "ferry_selgen_retire")
+
     def __del__(self):
         h, self._h = getattr(self, "_h", None), None
         if h and lib is not None:
@@ -360,6 +391,60 @@ def ctx_uniform(seed, n_req, lo, hi):
     out = np.zeros(n_req, np.int32)
     _check(lib.ferry_ctx_uniform(seed, n_req, lo, hi, out.ctypes.data), "ferry_ctx_uniform")
     return out
+
+
+def arrivals(kind, n, gap_ms, period_ms=50.0, ratio=10.0, seed=0):
+    """Arrival times (ms) of n requests (ferry_arrivals)."""
+    out = np.zeros(n, np.float64)
+    _check(lib.ferry_arrivals(kind, n, gap_ms, period_ms, ratio, seed, out.ctypes.data),
+           "ferry_arrivals")
+    return out
+
+
+class Sched:
+    """Tick scheduler of one executor (ferry_sched_*): `lanes` batch lanes
+    serve requests that arrive at arrive_ms and decode len_steps steps."""
+
+    def __init__(self, lanes, arrive_ms, len_steps):
+        self.lanes = lanes
+        self._arr = np.ascontiguousarray(arrive_ms, np.float64)
+        self._len = np.ascontiguousarray(len_steps, np.int32)
+        self.n = self._arr.size
+        h = _vp()
+        _check(lib.ferry_sched_create(lanes, self.n, self._arr.ctypes.data,
+                                      self._len.ctypes.data, C.byref(h)), "ferry_sched_create")
+        self._h = h
+
+    def tick(self, now_ms):
+        """One tick: returns dict(lane_req, lane_step, admitted, retired,
+        resident, done)."""
+        lr = np.zeros(self.lanes, np.int32)
+        ls = np.zeros(self.lanes, np.int32)
+        ad = np.zeros(self.lanes, np.int32)
+        rt = np.zeros(self.lanes, np.int32)
+        na, nr, nres, done = _i32(), _i32(), _i32(), _i32()
+        _check(lib.ferry_sched_tick(self._h, now_ms, lr.ctypes.data, ls.ctypes.data,
+                                    ad.ctypes.data, C.byref(na), rt.ctypes.data, C.byref(nr),
+                                    C.byref(nres), C.byref(done)), "ferry_sched_tick")
+        return dict(lane_req=lr, lane_step=ls, admitted=ad[:na.value].copy(),
+                    retired=rt[:nr.value].copy(), resident=nres.value, done=bool(done.value))
+
+    def next_arrival(self):
+        v = C.c_double()
+        _check(lib.ferry_sched_next_arrival(self._h, C.byref(v)), "ferry_sched_next_arrival")
+        return v.value
+
+    def request_ticks(self):
+        a = np.zeros(self.n, np.int32)
+        d = np.zeros(self.n, np.int32)
+        _check(lib.ferry_sched_request_ticks(self._h, a.ctypes.data, d.ctypes.data),
+               "ferry_sched_request_ticks")
+        return a, d
+
+    def __del__(self):
+        h, self._h = getattr(self, "_h", None), None
+        if h and lib is not None:
+            lib.ferry_sched_destroy(h)
 
 
 def refgen_selections(R, L, S, sel, seed=42):

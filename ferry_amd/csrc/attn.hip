@@ -13,6 +13,7 @@
 // every row of lanes then runs its own online softmax over the tokens it
 // holds, and rows, then wavefronts, are merged at the end.  Q heads of one kv
 // head (GQA group G) share every K/V load.
+#include "attn_common.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -107,6 +108,7 @@ __global__ __launch_bounds__(W * 64) void k_attn(Geo g, const float* __restrict_
 
   __shared__ float red[W][G][LPT][EPV + 2];
   __shared__ uint32_t ids[kMaxTopK];
+  __shared__ int id_cnt[kMaxTopK / 64];
 
   // (request, layer in [l0, l0 + nl), kv head) of this workgroup
   const int h = blockIdx.x % g.Hkv;
@@ -133,11 +135,9 @@ __global__ __launch_bounds__(W * 64) void k_attn(Geo g, const float* __restrict_
   }
 
   // The row's slot ids are staged in LDS: a slot lookup is then an LDS read
-  // (lgkmcnt) that never waits on the block loads in flight (vmcnt).
-  const uint32_t* sl = slots + (size_t)row * g.k;
-  const int k = g.k;
-  for (int j = threadIdx.x; j < k; j += W * 64) ids[j] = sl[j];
-  __syncthreads();
+  // (lgkmcnt) that never waits on the block loads in flight (vmcnt).  Empty
+  // positions are dropped, so k is the number of blocks this row attends to.
+  const int k = stage_row_ids<W>(slots + (size_t)row * g.k, g.k, ids, id_cnt);
   // Ring of NPF block buffers (NPF = 1: load, then consume).  While block j
   // (= wave + W*j of the row) is consumed, blocks j+1 .. j+NPF-1 are in flight;
   // the loop is unrolled by NPF so every buffer index is static, and every
@@ -272,7 +272,8 @@ __global__ __launch_bounds__(W * 64) void k_attn(Geo g, const float* __restrict_
 #pragma unroll
       for (int e = 0; e < EPV; ++e) o[e] += red[w][gq][c][2 + e] * a;
     }
-    const float inv = 1.0f / l;
+    // a row with no selected block (request not resident) attends to nothing: 0
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     float* op = out + ((size_t)rl * g.Hq + (size_t)h * G + gq) * D + c * EPV;
 #pragma unroll
     for (int e = 0; e < EPV; ++e) op[e] = o[e] * inv;

@@ -1,0 +1,54 @@
+// attn_common.hpp -- device helpers shared by the two attention kernels.
+#pragma once
+
+#include "common.hpp"
+
+namespace ferry_amd {
+
+// Stage the k slot ids of one (request, layer, kv head) row in LDS `ids`,
+// dropping empty positions (kNone) and keeping the order of the others, and
+// return how many were kept.  A row of a request that is not resident this
+// step is all kNone (0 kept); a short context gives a ragged row.
+// Every thread of the W-wavefront workgroup must call it: each thread holds
+// up to kMaxTopK / (64 W) ids in registers, each wavefront counts its 64-id
+// chunks with a ballot, and after one barrier every kept id is written at
+// (ids kept in earlier chunks) + (kept lanes below it in its chunk).
+// `cnt` is LDS scratch of kMaxTopK / 64 ints.  Ends with a barrier.
+template <int W>
+__device__ inline int stage_row_ids(const uint32_t* __restrict__ sl, int k, uint32_t* ids,
+                                    int* cnt) {
+  constexpr int NT = W * 64;
+  constexpr int PER = kMaxTopK / NT;
+  const int tid = threadIdx.x, lane = tid & 63;
+  uint32_t v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int j = tid + i * NT;
+    v[i] = j < k ? sl[j] : kNone;
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int j = tid + i * NT;  // chunk j / 64 is the same for the whole wavefront
+    const uint64_t m = ballot(v[i] != kNone);
+    if (lane == 0) cnt[j >> 6] = __builtin_popcountll(m);
+  }
+  __syncthreads();
+  const int nchunks = (k + 63) >> 6;
+  int total = 0;
+  for (int c = 0; c < nchunks; ++c) total += cnt[c];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int j = tid + i * NT;
+    const bool keep = v[i] != kNone;
+    const uint64_t m = ballot(keep);
+    if (j < k && keep) {
+      int base = 0;
+      for (int c = 0; c < (j >> 6); ++c) base += cnt[c];
+      ids[base + lanes_below(m)] = v[i];
+    }
+  }
+  __syncthreads();
+  return total;
+}
+
+}  // namespace ferry_amd

@@ -33,6 +33,7 @@
 // (v_cvt_scalef32_pk_f16_fp8 with scale 1); the per-block K scale multiplies
 // the scores and the accumulator is kept in units of the current block's V
 // scale (rescaled by vs_prev / vs at each block, times vs_last at the end).
+#include "attn_common.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -96,6 +97,7 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
   __shared__ float red_o[W][G][D];
   __shared__ float red_ml[W][G][2];
   __shared__ uint32_t ids[kMaxTopK];
+  __shared__ int id_cnt[kMaxTopK / 64];
 
   const int h = blockIdx.x % g.Hkv;
   const int rl = (blockIdx.x / (nl * g.Hkv)) * g.L + l0 + (blockIdx.x / g.Hkv) % nl;
@@ -142,11 +144,9 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
   for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // The row's slot ids are staged in LDS: a slot lookup is then an LDS read
-  // (lgkmcnt) that never waits on the block loads in flight (vmcnt).
-  const uint32_t* sl = slots + (size_t)row * g.k;
-  const int k = g.k;
-  for (int j = threadIdx.x; j < k; j += W * 64) ids[j] = sl[j];
-  __syncthreads();
+  // (lgkmcnt) that never waits on the block loads in flight (vmcnt).  Empty
+  // positions are dropped, so k is the number of blocks this row attends to.
+  const int k = stage_row_ids<W>(slots + (size_t)row * g.k, g.k, ids, id_cnt);
   const int nblk = k > wave ? (k - wave + W - 1) / W : 0;
   // A slot outside the pool is read as slot 0 and reported once at the end
   // (no branch in the block loop).
@@ -335,7 +335,8 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
       l += red_ml[w][hq][1] * a;
       o += red_o[w][hq][d] * a;
     }
-    out[((size_t)rl * g.Hq + (size_t)h * G + hq) * D + d] = o / l;
+    // a row with no selected block (request not resident) attends to nothing: 0
+    out[((size_t)rl * g.Hq + (size_t)h * G + hq) * D + d] = l > 0.0f ? o / l : 0.0f;
   }
 }
 

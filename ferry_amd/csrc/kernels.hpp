@@ -25,7 +25,9 @@ struct Ring {
 };
 
 // Device counters (unsigned long long).
-enum StatSlot { kStatMisses = 0, kStatBytes, kStatSteals, kStatStolen, kStatLast, kStatDrain, kStatCount };
+enum StatSlot {
+  kStatMisses = 0, kStatBytes, kStatSteals, kStatStolen, kStatLast, kStatDrain, kStatSel, kStatCount
+};
 
 struct FetchArgs {
   Geo g;
@@ -44,8 +46,9 @@ struct FetchArgs {
 template <bool SERIAL>
 __global__ void k_lru_step(Geo g, const uint32_t* sel, uint32_t* slots_out, uint32_t* miss_count,
                            ferry_miss* misses, uint8_t* miss_flag, SetState st, Ring ring, int l0,
-                           int nl, int* err);
+                           int nl, unsigned long long* stats, int* err);
 __global__ void k_sets_reset(Geo g, SetState st);
+__global__ void k_sets_reset_owners(Geo g, SetState st, const uint32_t* owners, uint32_t n, int* err);
 
 template <int NV>
 __global__ void k_fetch(FetchArgs a);

@@ -13,6 +13,10 @@
 //          least recently used resident slot not touched in this sub-step;
 //   new LRU order = untouched survivors in old order ++ touched slots ordered
 //          by their last occurrence.
+// A selection id of kNone (0xFFFFFFFF) is an empty position: it is neither a
+// hit nor a miss, its slot is reported as kNone, and it touches no state.  A
+// request that is not resident this step has a row of empty positions; a
+// short context has a ragged row (fewer than k blocks to choose from).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -43,8 +47,8 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
   // phase 1: classify (hits mark their slot; misses race for first occurrence)
   for (int c = p0; c < pend; c += kWave) {
     const int p = c + lane;
-    if (p < pend) {
-      const uint32_t x = sel[sel_index(g, sv, p)];
+    const uint32_t x = p < pend ? sel[sel_index(g, sv, p)] : kNone;
+    if (x != kNone) {
       const uint32_t v = aload(map + x);
       if (v < (uint32_t)C)
         atomicMax(lastpos + v, p);
@@ -58,10 +62,10 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
   for (int c = p0; c < pend; c += kWave) {
     const int p = c + lane;
     bool is_miss = false;
-    uint32_t x = 0;
+    uint32_t x = kNone;
     if (p < pend) {
       x = sel[sel_index(g, sv, p)];
-      is_miss = aload(map + x) == (kPend | (uint32_t)p);
+      is_miss = x != kNone && aload(map + x) == (kPend | (uint32_t)p);
       if (miss_flag) miss_flag[sel_index(g, sv, p)] = is_miss ? 1 : 0;
     }
     const uint64_t mask = ballot(is_miss);
@@ -132,9 +136,14 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
     const int p = c + lane;
     if (p < pend) {
       const size_t gi = sel_index(g, sv, p);
-      const uint32_t v = aload(map + sel[gi]);
-      slots_out[gi] = set * (uint32_t)C + v;
-      atomicMax(lastpos + v, p);
+      const uint32_t x = sel[gi];
+      if (x == kNone) {
+        slots_out[gi] = kNone;
+      } else {
+        const uint32_t v = aload(map + x);
+        slots_out[gi] = set * (uint32_t)C + v;
+        atomicMax(lastpos + v, p);
+      }
     }
   }
   __builtin_amdgcn_wave_barrier();
@@ -157,8 +166,9 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
     const int p = c + lane;
     bool emit = false;
     uint32_t v = 0;
-    if (p < pend) {
-      v = aload(map + sel[sel_index(g, sv, p)]);
+    const uint32_t x = p < pend ? sel[sel_index(g, sv, p)] : kNone;
+    if (x != kNone) {
+      v = aload(map + x);
       emit = lastpos[v] == p;
     }
     const uint64_t mask = ballot(emit);
@@ -170,7 +180,8 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
   // phase 6: clear the marks of this sub-step
   for (int c = p0; c < pend; c += kWave) {
     const int p = c + lane;
-    if (p < pend) lastpos[aload(map + sel[sel_index(g, sv, p)])] = -1;
+    const uint32_t x = p < pend ? sel[sel_index(g, sv, p)] : kNone;
+    if (x != kNone) lastpos[aload(map + x)] = -1;
   }
   __builtin_amdgcn_wave_barrier();
   return M;
@@ -185,6 +196,7 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
                                                   ferry_miss* __restrict__ misses,
                                                   uint8_t* __restrict__ miss_flag,
                                                   SetState st, Ring ring, int l0, int nl,
+                                                  unsigned long long* __restrict__ stats,
                                                   int* __restrict__ err) {
   extern __shared__ uint32_t lds[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -219,7 +231,12 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   }
   // range check of every selected id before touching the map
   bool bad = false;
-  for (int p = lane; p < sv.n; p += kWave) bad |= sel[sel_index(g, sv, p)] >= (uint32_t)g.max_blocks;
+  int nsel = 0;  // non-empty positions
+  for (int p = lane; p < sv.n; p += kWave) {
+    const uint32_t x = sel[sel_index(g, sv, p)];
+    bad |= x != kNone && x >= (uint32_t)g.max_blocks;
+    nsel += __builtin_popcountll(ballot(x != kNone));
+  }
   if (ballot(bad)) {
     if (lane == 0) {
       set_error(err, FERRY_ERANGE);
@@ -249,7 +266,8 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
       bool lost = false;
       for (int p = lane; p < sv.n; p += kWave) {
         const size_t gi = sel_index(g, sv, p);
-        lost |= stag[aload(slots_out + gi) - (uint32_t)set * (uint32_t)C] != sel[gi];
+        if (sel[gi] != kNone)
+          lost |= stag[aload(slots_out + gi) - (uint32_t)set * (uint32_t)C] != sel[gi];
       }
       if (ballot(lost)) rc = FERRY_ECAPACITY;
     }
@@ -268,13 +286,45 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   if (lane == 0) {
     st.fill[set] = fill;
     miss_count[set] = (uint32_t)total;
+    if (nsel) atomicAdd(stats + kStatSel, (unsigned long long)nsel);
   }
 }
 
 template __global__ void k_lru_step<false>(Geo, const uint32_t*, uint32_t*, uint32_t*, ferry_miss*,
-                                           uint8_t*, SetState, Ring, int, int, int*);
+                                           uint8_t*, SetState, Ring, int, int,
+                                           unsigned long long*, int*);
 template __global__ void k_lru_step<true>(Geo, const uint32_t*, uint32_t*, uint32_t*, ferry_miss*,
-                                          uint8_t*, SetState, Ring, int, int, int*);
+                                          uint8_t*, SetState, Ring, int, int, unsigned long long*,
+                                          int*);
+
+// Reset the sets of the listed owners (a new request takes over a lane):
+// one wavefront per set clears the map entries its tags point at, then the
+// tags, the order and the fill.  Owner ids must be < n_owners (checked).
+__global__ __launch_bounds__(256) void k_sets_reset_owners(Geo g, SetState st,
+                                                           const uint32_t* __restrict__ owners,
+                                                           uint32_t n, int* __restrict__ err) {
+  const int wpb = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const size_t idx = (size_t)blockIdx.x * wpb + (threadIdx.x >> 6);
+  const size_t per_owner = (size_t)g.L * g.Hkv;
+  if (idx >= (size_t)n * per_owner) return;
+  const uint32_t o = owners[idx / per_owner];
+  if (o >= (uint32_t)g.n_owners) {
+    if (lane == 0) set_error(err, FERRY_EINVAL);
+    return;
+  }
+  const size_t set = (size_t)o * per_owner + idx % per_owner;
+  uint32_t* map = st.map + set * (size_t)g.max_blocks;
+  uint32_t* tag = st.tag + set * (size_t)g.C;
+  uint32_t* ord = st.ord + set * (size_t)g.C;
+  for (int i = lane; i < g.C; i += kWave) {
+    const uint32_t b = tag[i];
+    if (b < (uint32_t)g.max_blocks) map[b] = kNone;
+    tag[i] = kNone;
+    ord[i] = kNone;
+  }
+  if (lane == 0) st.fill[set] = 0;
+}
 
 // Reset all sets: empty order, no tags, map cleared.
 __global__ void k_sets_reset(Geo g, SetState st) {

@@ -71,7 +71,7 @@ struct ferry_ctx {
   float* host_scales_dev = nullptr;
   int lru_wpb = 1;
   size_t lru_lds = 0;
-  uint64_t steps = 0, selections = 0;
+  uint64_t steps = 0;
   std::vector<hipEvent_t> events;  // layer-chunk pipeline of ferry_decode_step
   int attn_waves = 0;              // wavefronts per attention workgroup (FERRY_ATTN_WAVES), 0 = default
   uint32_t* probe_sink = nullptr;  // bandwidth probes: one word per row / wavefront
@@ -416,6 +416,19 @@ int ferry_sets_reset(ferry_ctx* ctx, void* stream) {
   return FERRY_OK;
 }
 
+int ferry_sets_reset_owners(ferry_ctx* ctx, const uint32_t* owners, uint32_t n, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (n == 0) return FERRY_OK;
+  if (!owners) return fail(FERRY_EINVAL, "null owners");
+  if (n > (uint32_t)ctx->g.n_owners) return fail(FERRY_EINVAL, "more owners than the executor has");
+  HIPC(hipSetDevice(ctx->device));
+  const uint64_t waves = (uint64_t)n * ctx->g.L * ctx->g.Hkv;
+  hipLaunchKernelGGL(k_sets_reset_owners, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, ctx->g, ctx->st, owners, n, ctx->err);
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
 int ferry_sets_state(ferry_ctx* ctx, uint32_t* fill, uint32_t* ord, uint32_t* tag) {
   if (int rc = check_ctx(ctx)) return rc;
   HIPC(hipSetDevice(ctx->device));
@@ -440,13 +453,14 @@ int ferry_bookkeep_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const uint32_t
   const dim3 grid((nsets + wpb - 1) / wpb), block(64 * wpb);
   if (ctx->cfg.lru_mode == FERRY_LRU_SERIAL)
     hipLaunchKernelGGL(k_lru_step<true>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
-                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->err);
+                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->stats,
+                       ctx->err);
   else
     hipLaunchKernelGGL(k_lru_step<false>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
-                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->err);
+                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->stats,
+                       ctx->err);
   HIPC(hipGetLastError());
   if (l0 + nl == g.L) ctx->steps++;
-  ctx->selections += (uint64_t)g.n_req * nl * g.Hkv * g.k;
   return FERRY_OK;
 }
 
@@ -637,7 +651,7 @@ int ferry_stats_get(ferry_ctx* ctx, ferry_stats* out) {
   HIPC(hipMemcpy(&err, ctx->err, 4, hipMemcpyDeviceToHost));
   std::memset(out, 0, sizeof(*out));
   out->steps = ctx->steps;
-  out->selections = ctx->selections;
+  out->selections = s[kStatSel];
   out->misses = s[kStatMisses];
   out->fetched_bytes = s[kStatBytes];
   out->steals = s[kStatSteals];
@@ -653,7 +667,7 @@ int ferry_stats_reset(ferry_ctx* ctx) {
   HIPC(hipDeviceSynchronize());
   HIPC(hipMemset(ctx->stats, 0, kStatCount * 8));
   HIPC(hipMemset(ctx->err, 0, 4));
-  ctx->steps = ctx->selections = 0;
+  ctx->steps = 0;
   return FERRY_OK;
 }
 

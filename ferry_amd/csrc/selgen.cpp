@@ -12,6 +12,13 @@
 // Every draw is a counter-based hash of (seed, step, r, l, h, draw index), so
 // requests are generated independently in parallel.
 //
+// Lanes and requests: row r of a step is batch lane r.  By default lane r
+// holds request r from step 0.  ferry_selgen_admit puts a new request (id,
+// context) into a lane from a given step on; its draws are then keyed by
+// (request id, steps since admission) and it starts without carry-over, as a
+// fresh decode does.  A retired lane produces rows of FERRY_EMPTY.  A context
+// shorter than k blocks selects all of them and pads the row with FERRY_EMPTY.
+//
 // ferry_refgen_selections: the selection half of replay_miss_stream
 // (src/workloads/missstream.cuh:104-133) with std::mt19937_64.
 #include <algorithm>
@@ -49,6 +56,9 @@ struct ferry_selgen {
   std::vector<double> cum;     // Zipf cumulative weights of ranks 0..nmax-1
   std::vector<uint32_t> state; // previous logical selection per (r, l, h)
   std::vector<double> reuse;   // per-request reuse (empty = cfg.reuse for all)
+  std::vector<int32_t> rid;    // request id held by each lane
+  std::vector<int32_t> start;  // step at which that request was admitted
+  std::vector<uint8_t> active; // lane holds a request
   int nmax = 0;
   int max_blocks = 0;
 };
@@ -71,7 +81,7 @@ int ferry_selgen_create(const ferry_selgen_config* cfg, const int32_t* ctx_block
   g->cfg = *cfg;
   g->ctx.assign(ctx_blocks, ctx_blocks + cfg->n_req);
   for (int r = 0; r < cfg->n_req; ++r) {
-    if (g->ctx[r] < cfg->k || g->ctx[r] >= (int)kPermPrime) {
+    if (g->ctx[r] < 1 || g->ctx[r] >= (int)kPermPrime) {
       delete g;
       return FERRY_EINVAL;
     }
@@ -94,7 +104,31 @@ int ferry_selgen_create(const ferry_selgen_config* cfg, const int32_t* ctx_block
     }
   }
   g->state.assign((size_t)cfg->n_req * cfg->n_layers * cfg->kv_heads * cfg->k, 0u);
+  g->rid.resize(cfg->n_req);
+  for (int r = 0; r < cfg->n_req; ++r) g->rid[r] = r;
+  g->start.assign(cfg->n_req, 0);
+  g->active.assign(cfg->n_req, 1);
   *out = g;
+  return FERRY_OK;
+}
+
+int ferry_selgen_admit(ferry_selgen* g, int32_t lane, int32_t request_id, int32_t ctx_blocks,
+                       int32_t step) {
+  if (!g || lane < 0 || lane >= g->cfg.n_req) return FERRY_EINVAL;
+  if (g->cfg.group != 1) return FERRY_EINVAL;  // a group's lanes share one permutation
+  if (request_id < 0 || request_id >= 65536 || step < 0) return FERRY_EINVAL;
+  if (ctx_blocks < 1 || ctx_blocks > g->nmax) return FERRY_EINVAL;
+  g->rid[lane] = request_id;
+  g->ctx[lane] = ctx_blocks;
+  g->nperm[lane] = ctx_blocks;
+  g->start[lane] = step;
+  g->active[lane] = 1;
+  return FERRY_OK;
+}
+
+int ferry_selgen_retire(ferry_selgen* g, int32_t lane) {
+  if (!g || lane < 0 || lane >= g->cfg.n_req) return FERRY_EINVAL;
+  g->active[lane] = 0;
   return FERRY_OK;
 }
 
@@ -125,37 +159,50 @@ int ferry_selgen_step(ferry_selgen* g, int32_t step, uint32_t* out) {
   if (!g || !out || step < 0) return FERRY_EINVAL;
   const ferry_selgen_config& c = g->cfg;
   const int L = c.n_layers, H = c.kv_heads, k = c.k;
-  const bool carry = step > 0;
+  for (int r = 0; r < c.n_req; ++r)
+    if (g->active[r] && step < g->start[r]) return FERRY_EINVAL;
   int nthreads = (int)std::min<unsigned>(16u, std::max(1u, std::thread::hardware_concurrency()));
   nthreads = std::min(nthreads, c.n_req);
   std::vector<int> rc(nthreads, 0);
   auto work = [&](int tid) {
     std::vector<uint8_t> taken(g->nmax, 0);
     for (int r = tid; r < c.n_req; r += nthreads) {
+      if (!g->active[r]) {
+        std::fill(out + (size_t)r * L * H * k, out + (size_t)(r + 1) * L * H * k, FERRY_EMPTY);
+        continue;
+      }
       const int o = r / c.group, m = r % c.group;
       const int nr = g->ctx[r];
       const int np = g->nperm[o];
       const int pre = std::min(c.prefix_blocks, np);
       const double reuse = g->reuse.empty() ? c.reuse : g->reuse[r];
       const uint64_t keep_thr = (uint64_t)(reuse * 4294967296.0);
+      const uint64_t rid = (uint64_t)g->rid[r];
+      const uint64_t lstep = (uint64_t)(step - g->start[r]);  // steps since admission
+      const bool carry = lstep > 0;
+      const int ke = std::min(k, nr);  // a short context selects all its blocks
+      // permutation of the owner; a lane taken over by request `rid` gets rid's
+      const uint64_t pown = c.group == 1 ? rid : (uint64_t)o;
       for (int l = 0; l < L; ++l)
         for (int h = 0; h < H; ++h) {
           const size_t row = ((size_t)(r * L + l) * H + h) * k;
           uint32_t* st = g->state.data() + row;
           uint32_t* so = out + row;
-          const uint64_t off = mix64(c.seed ^ kSaltPerm, (uint64_t)((o * L + l) * H + h)) % (uint64_t)np;
-          // draw index of (step, r, l, h): independent of the batch size
+          const uint64_t off = mix64(c.seed ^ kSaltPerm, (pown * L + l) * H + h) % (uint64_t)np;
+          // draw index of (steps since admission, request, l, h): independent
+          // of the batch size and of the lane
           const uint64_t base =
-              (((((uint64_t)step << 16) | (uint64_t)r) * (uint64_t)L + (uint64_t)l) * (uint64_t)H +
-               (uint64_t)h) * (uint64_t)kDrawLimit;
+              ((((lstep << 16) | rid) * (uint64_t)L + (uint64_t)l) * (uint64_t)H + (uint64_t)h) *
+              (uint64_t)kDrawLimit;
           int got = 0;
           if (carry && reuse > 0.0)
             for (int j = 0; j < k; ++j)
-              if ((mix64(c.seed ^ kSaltKeep, base + (uint64_t)j) >> 32) < keep_thr) {
+              if (st[j] != FERRY_EMPTY &&
+                  (mix64(c.seed ^ kSaltKeep, base + (uint64_t)j) >> 32) < keep_thr) {
                 so[got++] = st[j];
                 taken[st[j]] = 1;
               }
-          for (int i = 0; i < kDrawLimit && got < k; ++i) {
+          for (int i = 0; i < kDrawLimit && got < ke; ++i) {
             const uint64_t u = mix64(c.seed ^ kSaltSel, base + (uint64_t)i);
             uint64_t rank;
             if (c.dist == 1) {
@@ -170,13 +217,14 @@ int ferry_selgen_step(ferry_selgen* g, int32_t step, uint32_t* out) {
             so[got++] = (uint32_t)b;
           }
           for (int j = 0; j < got; ++j) taken[so[j]] = 0;
-          if (got < k) {
+          if (got < ke) {
             rc[tid] = FERRY_ESTATE;
             return;
           }
-          std::sort(so, so + k);
+          std::sort(so, so + ke);
+          std::fill(so + ke, so + k, FERRY_EMPTY);
           std::memcpy(st, so, (size_t)k * 4);
-          for (int j = 0; j < k; ++j)
+          for (int j = 0; j < ke; ++j)
             if (so[j] >= (uint32_t)pre)
               so[j] = (uint32_t)pre + (uint32_t)m * (uint32_t)(np - pre) + (so[j] - (uint32_t)pre);
         }

@@ -90,7 +90,7 @@ typedef struct ferry_miss {
  * src/runtime/wla_multigpu.cuh:177-233). */
 typedef struct ferry_stats {
   uint64_t steps;          /* fetch steps run */
-  uint64_t selections;     /* selections processed */
+  uint64_t selections;     /* non-empty selections processed */
   uint64_t misses;         /* unique blocks fetched (refill events of 1 block) */
   uint64_t fetched_bytes;  /* host-tier bytes moved into the pool */
   uint64_t steals;         /* successful steals between fetch workers */
@@ -134,12 +134,29 @@ int ferry_pool_view(ferry_ctx* ctx, void** pool, float** scales);
 /* Forget every resident block (all sets empty).  Replaces
  * GPUBoundedQueue::reset + cache re-init (src/queue/gpu_bounded_queue.cuh:176-181). */
 int ferry_sets_reset(ferry_ctx* ctx, void* stream);
+/* Forget the resident blocks of the listed owners only: owners is a device
+ * array of n owner ids (request / group), n <= number of owners.  Used when a
+ * new request takes over a lane of the batch; other owners' sets are
+ * untouched.  An owner id out of range is latched as FERRY_EINVAL in the
+ * device error word.  The reference gives every request id its own hot
+ * cache segment for the whole run (src/runtime/wla_multigpu.cuh:468, 517)
+ * and trims a group's LRU when a member leaves (grp_trim, :1923-1936); here
+ * a batch lane is reused by successive requests, so it starts cold. */
+int ferry_sets_reset_owners(ferry_ctx* ctx, const uint32_t* owners, uint32_t n, void* stream);
 /* Copy per-set LRU state to host arrays: fill[n_sets], ord[n_sets][slots]
  * (local slots, LRU first), tag[n_sets][slots] (block per slot). */
 int ferry_sets_state(ferry_ctx* ctx, uint32_t* fill, uint32_t* ord, uint32_t* tag);
 
+/* Empty positions.  A selection id of FERRY_EMPTY (0xFFFFFFFF) selects
+ * nothing: it is neither hit nor miss, its slot comes back as FERRY_EMPTY,
+ * and attention skips it.  A request that is not resident this step passes a
+ * row of FERRY_EMPTY (its attention output is 0); a context shorter than k
+ * blocks passes a ragged row (the reference's trace format allows fewer
+ * selected pages at a short tail, tools/capture_miss_trace.py:36-37). */
+#define FERRY_EMPTY 0xFFFFFFFFu
+
 /* One decode step of bookkeeping + miss fetch:
- *   sel        [B][L][Hkv][k] set block ids (device, u32)
+ *   sel        [B][L][Hkv][k] set block ids (device, u32; FERRY_EMPTY allowed)
  *   slots      [B][L][Hkv][k] out: pool slot of each selection (device, u32)
  *   miss_count [n_sets] out: misses per set (device, u32)
  *   misses     [n_sets][max_sel] out: fetched blocks per set in miss order
@@ -267,6 +284,67 @@ int ferry_selgen_step(ferry_selgen* g, int32_t step, uint32_t* out);
 /* Per-request context lengths uniform in [lo, hi] blocks. */
 int ferry_ctx_uniform(uint64_t seed, int32_t n_req, int32_t lo, int32_t hi,
                       int32_t* out);
+/* Lane turnover (group 1 only).  ferry_selgen_admit puts request
+ * `request_id` (< 65536) with a context of ctx_blocks (1 .. the largest
+ * context given at creation) into `lane` from step `step` on: its draws are
+ * keyed by (request id, steps since admission), it starts with no carried
+ * selection, and a context shorter than k selects all its blocks and pads
+ * the row with FERRY_EMPTY.  ferry_selgen_retire makes a lane produce rows of
+ * FERRY_EMPTY until its next admission.  Replaces the request lifetime of
+ * the reference's per-GPU executor: a request is resident from its arrival
+ * until it has run len[r] steps (src/runtime/wla_multigpu.cuh:829-864,
+ * src/workloads/missstream.cuh:68-81). */
+int ferry_selgen_admit(ferry_selgen* g, int32_t lane, int32_t request_id, int32_t ctx_blocks,
+                       int32_t step);
+int ferry_selgen_retire(ferry_selgen* g, int32_t lane);
+
+/* ---- request arrivals and the per-GPU tick scheduler ----
+ * Arrival times in ms of n requests (out_ms[n], non-decreasing, first
+ * arrival after one gap):
+ *   FERRY_ARRIVAL_STEADY   every gap_ms
+ *   FERRY_ARRIVAL_BURSTY   request r after 40*gap_ms when r % 16 == 0, else
+ *                          after 0.1*gap_ms (the reference's bursty rule,
+ *                          src/runtime/wla_multigpu.cuh:497-501)
+ *   FERRY_ARRIVAL_POISSON  exponential gaps of mean gap_ms
+ *   FERRY_ARRIVAL_MMPP     Markov-modulated Poisson: two states of rate
+ *                          1/gap_ms and ratio/gap_ms, exponential sojourns
+ *                          of mean period_ms, starting in the slow state
+ * Draws are counter-based hashes of (seed, index). */
+#define FERRY_ARRIVAL_STEADY 0
+#define FERRY_ARRIVAL_BURSTY 1
+#define FERRY_ARRIVAL_POISSON 2
+#define FERRY_ARRIVAL_MMPP 3
+int ferry_arrivals(int kind, uint32_t n, double gap_ms, double period_ms, double ratio,
+                   uint64_t seed, double* out_ms);
+
+/* Tick scheduler of one GPU's executor: `lanes` batch lanes, n requests
+ * with arrival times arrive_ms[n] and decode lengths len_steps[n] (>= 1).
+ * Each ferry_sched_tick(now_ms) is one executor tick:
+ *   1. every request resident in the previous tick has run one more step;
+ *      those that reached len_steps leave their lanes (tick_end,
+ *      src/runtime/wla_multigpu.cuh:834-864);
+ *   2. requests with arrive_ms <= now_ms join a FIFO in arrival order (ties
+ *      by id) and take free lanes, lowest lane first;
+ *   3. out: lane_req[lanes] = request in each lane (-1 idle),
+ *      lane_step[lanes] = that request's step index in this tick,
+ *      admitted[0..*n_admitted) = lanes that received a new request,
+ *      retired[0..*n_retired) = lanes whose request left in step 1 (and
+ *      were not refilled), *n_resident, *done = 1 once every request has
+ *      finished (then nothing is resident).
+ * The reference's exec loop runs every resident request once per tick
+ * (src/runtime/wla_multigpu.cuh:2610-2665); its residency is unbounded, which
+ * is lanes >= n here. */
+typedef struct ferry_sched ferry_sched;
+int ferry_sched_create(int32_t lanes, uint32_t n, const double* arrive_ms,
+                       const int32_t* len_steps, ferry_sched** out);
+int ferry_sched_destroy(ferry_sched* s);
+int ferry_sched_tick(ferry_sched* s, double now_ms, int32_t* lane_req, int32_t* lane_step,
+                     int32_t* admitted, int32_t* n_admitted, int32_t* retired,
+                     int32_t* n_retired, int32_t* n_resident, int32_t* done);
+/* Arrival time of the next request not yet admitted (+inf if none), and the
+ * per-request admission tick and completion tick (-1 until known). */
+int ferry_sched_next_arrival(const ferry_sched* s, double* ms);
+int ferry_sched_request_ticks(const ferry_sched* s, int32_t* admit_tick, int32_t* done_tick);
 
 /* Reference generator: the selections replay_miss_stream draws
  * (src/workloads/missstream.cuh:104-133, std::mt19937_64(seed)) for

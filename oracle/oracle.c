@@ -383,7 +383,7 @@ int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
                     uint8_t* flag_out) {
   const int cap = s->cap;
   for (int p = 0; p < n; ++p)
-    if (x[p] >= (uint32_t)s->max_blocks) return -1;
+    if (x[p] != ORA_NONE && x[p] >= (uint32_t)s->max_blocks) return -1;
   int* lastpos = (int*)malloc((size_t)cap * sizeof(int));
   uint32_t* mblk = (uint32_t*)malloc((size_t)(n ? n : 1) * 4);
   uint32_t* victim = (uint32_t*)malloc((size_t)(n ? n : 1) * 4);
@@ -391,6 +391,7 @@ int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
   for (int i = 0; i < cap; ++i) lastpos[i] = -1;
   /* phase 1: classify */
   for (int p = 0; p < n; ++p) {
+    if (x[p] == ORA_NONE) continue; /* empty position: touches nothing */
     const uint32_t v = s->map[x[p]];
     if (v == ORA_NONE)
       s->map[x[p]] = PEND | (uint32_t)p;
@@ -400,7 +401,7 @@ int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
   /* phase 2: misses in order of first occurrence */
   int M = 0;
   for (int p = 0; p < n; ++p) {
-    const int first = s->map[x[p]] == (PEND | (uint32_t)p);
+    const int first = x[p] != ORA_NONE && s->map[x[p]] == (PEND | (uint32_t)p);
     if (flag_out) flag_out[p] = (uint8_t)first;
     if (first) mblk[M++] = x[p];
   }
@@ -434,6 +435,10 @@ int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
     miss_out[q].set = set;
   }
   for (int p = 0; p < n; ++p) {
+    if (x[p] == ORA_NONE) {
+      slot_out[p] = ORA_NONE;
+      continue;
+    }
     const uint32_t v = s->map[x[p]];
     slot_out[p] = v;
     lastpos[v] = p;
@@ -443,7 +448,7 @@ int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
   for (uint32_t i = 0; i < s->fill; ++i)
     if (lastpos[s->ord[i]] < 0) nord[w++] = s->ord[i];
   for (int p = 0; p < n; ++p)
-    if (lastpos[slot_out[p]] == p) nord[w++] = slot_out[p];
+    if (slot_out[p] != ORA_NONE && lastpos[slot_out[p]] == p) nord[w++] = slot_out[p];
   s->fill += (uint32_t)(M < freeslots ? M : freeslots);
   memcpy(s->ord, nord, (size_t)w * 4);
   free(lastpos);
@@ -645,16 +650,17 @@ int ora_exec_step(ora_exec* e, const uint32_t* sel, uint32_t* slots_out,
           }
           /* every selected block must still be resident at step end */
           for (int p = 0; p < n; ++p)
-            if (e->sets[set].tag[e->slot[p]] != e->x[p]) return -3;
+            if (e->x[p] != ORA_NONE && e->sets[set].tag[e->slot[p]] != e->x[p]) return -3;
         }
         miss_count[set] = (uint32_t)M;
-        nsel += (uint64_t)n;
+        for (int p = 0; p < n; ++p) nsel += e->x[p] != ORA_NONE;
         nmiss += (uint64_t)M;
         for (int m = 0; m < mem; ++m) {
           const int r = o * g->group + m;
           uint32_t* so = slots_out + ((size_t)(r * L + l) * H + h) * k;
           for (int j = 0; j < k; ++j)
-            so[j] = set * (uint32_t)g->cap + e->slot[m * k + j];
+            so[j] = e->slot[m * k + j] == ORA_NONE ? ORA_NONE
+                                                    : set * (uint32_t)g->cap + e->slot[m * k + j];
           if (flags)
             memcpy(flags + ((size_t)(r * L + l) * H + h) * k, e->flag + (size_t)m * k,
                    (size_t)k);
@@ -665,6 +671,14 @@ int ora_exec_step(ora_exec* e, const uint32_t* sel, uint32_t* slots_out,
     counts[1] = nmiss;
     counts[2] = nsel - nmiss;
   }
+  return 0;
+}
+
+int ora_exec_reset_owner(ora_exec* e, int owner) {
+  const ora_geom* g = &e->g;
+  if (owner < 0 || owner >= ora_n_owners(g)) return -1;
+  const int per = g->n_layers * g->kv_heads;
+  for (int i = 0; i < per; ++i) ora_lru_reset(&e->sets[owner * per + i]);
   return 0;
 }
 
@@ -750,41 +764,54 @@ int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
       cum[i] = acc;
     }
   }
-  const int carry = step > 0;
   uint8_t* taken = (uint8_t*)calloc((size_t)nmax, 1);
   for (int r = 0; r < s->n_req; ++r) {
+    const size_t rows = (size_t)L * H * k;
+    if (s->active && !s->active[r]) { /* idle lane: every position empty */
+      for (size_t i = 0; i < rows; ++i) out[(size_t)r * rows + i] = ORA_NONE;
+      continue;
+    }
     const int o = r / s->group, m = r % s->group;
     const int nr = s->ctx_blocks[r];
     const int np = owner_nperm(s, o);
     const int pre = s->prefix_blocks < np ? s->prefix_blocks : np;
     const double reuse = s->reuse_r ? s->reuse_r[r] : s->reuse;
     const uint64_t keep_thr = (uint64_t)(reuse * 4294967296.0);
-    if (k > nr) {
+    /* the request in lane r: its id and the step it was admitted at */
+    const uint64_t rid = s->rid ? (uint64_t)s->rid[r] : (uint64_t)r;
+    const int start = s->start ? s->start[r] : 0;
+    if (step < start || nr < 1) {
       free(cum);
       free(taken);
       return -1;
     }
+    const uint64_t lstep = (uint64_t)(step - start);
+    const int carry = lstep > 0;
+    const int ke = k < nr ? k : nr; /* a short context selects all its blocks */
+    const uint64_t pown = s->group == 1 ? rid : (uint64_t)o;
     for (int l = 0; l < L; ++l)
       for (int h = 0; h < H; ++h) {
         const size_t row = ((size_t)(r * L + l) * H + h) * k;
         uint32_t* st = state + row;
         uint32_t* so = out + row;
         const uint64_t off =
-            ora_mix64(s->seed ^ SALT_PERM, (uint64_t)((o * L + l) * H + h)) %
+            ora_mix64(s->seed ^ SALT_PERM, (pown * (uint64_t)L + (uint64_t)l) * (uint64_t)H +
+                                               (uint64_t)h) %
             (uint64_t)np;
         const uint64_t base =
-            (((((uint64_t)step << 16) | (uint64_t)r) * (uint64_t)L + (uint64_t)l) *
-                 (uint64_t)H + (uint64_t)h) * (uint64_t)DRAW_LIMIT;
+            ((((lstep << 16) | rid) * (uint64_t)L + (uint64_t)l) * (uint64_t)H + (uint64_t)h) *
+            (uint64_t)DRAW_LIMIT;
         int got = 0;
         if (carry && reuse > 0.0)
           for (int j = 0; j < k; ++j) {
+            if (st[j] == ORA_NONE) continue;
             const uint64_t u = ora_mix64(s->seed ^ SALT_KEEP, base + (uint64_t)j) >> 32;
             if (u < keep_thr) {
               so[got++] = st[j];
               taken[st[j]] = 1;
             }
           }
-        for (int i = 0; i < DRAW_LIMIT && got < k; ++i) {
+        for (int i = 0; i < DRAW_LIMIT && got < ke; ++i) {
           const uint64_t u = ora_mix64(s->seed ^ SALT_SEL, base + (uint64_t)i);
           uint64_t rank;
           if (s->dist == 1) {
@@ -808,14 +835,15 @@ int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
           so[got++] = (uint32_t)b;
         }
         for (int j = 0; j < got; ++j) taken[so[j]] = 0;
-        if (got < k) {
+        if (got < ke) {
           free(cum);
           free(taken);
           return -2;
         }
-        qsort(so, (size_t)k, 4, cmp_u32);
+        qsort(so, (size_t)ke, 4, cmp_u32);
+        for (int j = ke; j < k; ++j) so[j] = ORA_NONE;
         memcpy(st, so, (size_t)k * 4);
-        for (int j = 0; j < k; ++j)
+        for (int j = 0; j < ke; ++j)
           if (so[j] >= (uint32_t)pre)
             so[j] = (uint32_t)pre + (uint32_t)m * (uint32_t)(np - pre) +
                     (so[j] - (uint32_t)pre);
@@ -823,6 +851,68 @@ int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
   }
   free(cum);
   free(taken);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* request arrivals                                                    */
+/* ------------------------------------------------------------------ */
+#define SALT_ARRIVE 0x41525256ull
+#define SALT_SOJOURN 0x534F4A4Eull
+
+static double unit_open0(uint64_t seed, uint64_t salt, uint64_t i) {
+  /* 53 random bits + 1 over 2^53: uniform on (0, 1] */
+  return (double)((ora_mix64(seed ^ salt, i) >> 11) + 1) / 9007199254740992.0;
+}
+
+/* Arrival times (ms).  Steady and bursty follow the reference's dispatcher
+ * (src/runtime/wla_multigpu.cuh:497-501: t += gap, or t += 40 gap every 16th
+ * request and 0.1 gap otherwise).  Poisson draws exponential gaps by
+ * inversion.  The Markov-modulated process alternates a slow state (mean gap
+ * `gap`) and a fast one (gap / ratio); state lifetimes are exponential of
+ * mean `period`; a gap that would cross the state's end is dropped and
+ * redrawn from the end at the new rate, which is exact by memorylessness. */
+int ora_arrivals(int kind, uint32_t n, double gap, double period, double ratio,
+                 uint64_t seed, double* out) {
+  if (!(gap > 0.0)) return -1;
+  double t = 0.0;
+  if (kind == 0) {
+    for (uint32_t r = 0; r < n; ++r) {
+      t += gap;
+      out[r] = t;
+    }
+  } else if (kind == 1) {
+    for (uint32_t r = 0; r < n; ++r) {
+      t += (r % 16 == 0) ? 40.0 * gap : 0.1 * gap;
+      out[r] = t;
+    }
+  } else if (kind == 2) {
+    for (uint32_t r = 0; r < n; ++r) {
+      t += -gap * log(unit_open0(seed, SALT_ARRIVE, r));
+      out[r] = t;
+    }
+  } else if (kind == 3) {
+    if (!(period > 0.0) || !(ratio > 0.0)) return -1;
+    uint64_t ia = 0, is = 0;
+    int fast = 0;
+    double state_end = -period * log(unit_open0(seed, SALT_SOJOURN, is++));
+    for (uint32_t r = 0; r < n; ++r) {
+      for (;;) {
+        const double mean = fast ? gap / ratio : gap;
+        const double d = -mean * log(unit_open0(seed, SALT_ARRIVE, ia++));
+        if (t + d < state_end) {
+          t += d;
+          break;
+        }
+        t = state_end;
+        fast = !fast;
+        state_end = t - period * log(unit_open0(seed, SALT_SOJOURN, is++));
+      }
+      out[r] = t;
+    }
+  } else {
+    return -1;
+  }
   return 0;
 }
 
@@ -896,10 +986,10 @@ int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
                       double* out) {
   const int L = g->n_layers, Hq = g->q_heads, Hk = g->kv_heads, D = g->head_dim;
   const int T = g->block_tokens, k = g->k, grp = Hq / Hk;
-  const int ntok = k * T;
-  double* s = (double*)malloc((size_t)ntok * sizeof(double));
-  double* V = (double*)malloc((size_t)ntok * D * sizeof(double));
-  double* K = (double*)malloc((size_t)ntok * D * sizeof(double));
+  const int ntok_max = k * T;
+  double* s = (double*)malloc((size_t)ntok_max * sizeof(double));
+  double* V = (double*)malloc((size_t)ntok_max * D * sizeof(double));
+  double* K = (double*)malloc((size_t)ntok_max * D * sizeof(double));
   const double isd = 1.0 / sqrt((double)D);
   for (int r = 0; r < g->n_req; ++r) {
     const int o = r / g->group;
@@ -907,8 +997,11 @@ int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
       for (int h = 0; h < Hk; ++h) {
         const uint32_t set = (uint32_t)((o * L + l) * Hk + h);
         const uint32_t* bl = sel + ((size_t)(r * L + l) * Hk + h) * k;
-        for (int j = 0; j < k; ++j) {
-          const uint64_t hi = ora_host_index(g, set, bl[j]);
+        int nv = 0; /* selected blocks of the row, empty positions skipped */
+        for (int jj = 0; jj < k; ++jj) {
+          if (bl[jj] == ORA_NONE) continue;
+          const int j = nv++;
+          const uint64_t hi = ora_host_index(g, set, bl[jj]);
           const double sk = ora_host_scale(g, hi, 0), sv = ora_host_scale(g, hi, 1);
           for (int t = 0; t < T; ++t)
             for (int d = 0; d < D; ++d) {
@@ -918,9 +1011,15 @@ int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
                                   ora_host_elem(g, hi, (uint32_t)((T + t) * D + d))) * sv;
             }
         }
+        const int ntok = nv * T;
         for (int gq = 0; gq < grp; ++gq) {
           const int hq = h * grp + gq;
           const float* qv = q + ((size_t)(r * L + l) * Hq + hq) * D;
+          double* ov = out + ((size_t)(r * L + l) * Hq + hq) * D;
+          if (ntok == 0) { /* nothing selected (request not resident): 0 */
+            for (int d = 0; d < D; ++d) ov[d] = 0.0;
+            continue;
+          }
           double mx = -INFINITY;
           for (int t = 0; t < ntok; ++t) {
             double acc = 0.0;
@@ -933,7 +1032,6 @@ int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
             s[t] = exp(s[t] - mx);
             den += s[t];
           }
-          double* ov = out + ((size_t)(r * L + l) * Hq + hq) * D;
           for (int d = 0; d < D; ++d) {
             double acc = 0.0;
             for (int t = 0; t < ntok; ++t) acc += s[t] * V[(size_t)t * D + d];
@@ -988,6 +1086,7 @@ int ora_attention_pool_f32(const ora_geom* g, const uint32_t* slots,
           float m = -INFINITY, den = 0.0f;
           for (int d = 0; d < D; ++d) acc[d] = 0.0f;
           for (int j = 0; j < k; ++j) {
+            if (sl[j] == ORA_NONE) continue; /* empty position */
             const uint8_t* blk = pool + (size_t)sl[j] * bb;
             const float sk = pool_scales ? pool_scales[2 * (size_t)sl[j]] : 1.0f;
             const float sv = pool_scales ? pool_scales[2 * (size_t)sl[j] + 1] : 1.0f;
@@ -1013,7 +1112,7 @@ int ora_attention_pool_f32(const ora_geom* g, const uint32_t* slots,
             m = mn;
           }
           float* ov = out + ((size_t)(r * L + l) * Hq + hq) * D;
-          for (int d = 0; d < D; ++d) ov[d] = acc[d] / den;
+          for (int d = 0; d < D; ++d) ov[d] = den > 0.0f ? acc[d] / den : 0.0f;
         }
       }
   free(acc);

@@ -162,6 +162,8 @@ void ora_exec_destroy(ora_exec* e);
 int ora_exec_step(ora_exec* e, const uint32_t* sel, uint32_t* slots_out,
                   uint32_t* miss_count, ora_miss* misses, uint64_t* counts,
                   uint8_t* flags);
+/* Empty the sets of one owner (a new request takes over its lane). */
+int ora_exec_reset_owner(ora_exec* e, int owner);
 /* Per-set state export for parity: fill[n_sets], ord[n_sets][cap],
  * tag[n_sets][cap]. */
 void ora_exec_state(const ora_exec* e, uint32_t* fill, uint32_t* ord,
@@ -177,6 +179,12 @@ typedef struct {
   uint64_t seed;
   const int* ctx_blocks; /* [n_req] logical context length in blocks */
   const double* reuse_r; /* [n_req] per-request reuse, or NULL (use reuse) */
+  /* Lane turnover (NULL = lane r holds request r from step 0, all active):
+   * the request id in each lane, the step it was admitted at, and whether
+   * the lane holds a request at all (idle lanes give empty rows). */
+  const int* rid;
+  const int* start;
+  const uint8_t* active;
 } ora_selgen;
 
 /* Per-request context lengths: uniform integer in [lo, hi]. */
@@ -184,9 +192,15 @@ void ora_ctx_uniform(uint64_t seed, int n_req, int lo, int hi, int* out);
 /* Set block-id bound for a generator (max over owners). */
 int ora_selgen_max_blocks(const ora_selgen* s);
 /* Selections of one step: out [B][L][Hkv][k] set block ids; state [same]
- * carries each request's logical selection from step to step. */
+ * carries each request's logical selection from step to step.  A row of a
+ * context shorter than k holds all its blocks, then ORA_NONE. */
 int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
                     uint32_t* out);
+
+/* ---------------- request arrivals ---------------- */
+/* kind 0 steady, 1 bursty, 2 Poisson, 3 Markov-modulated Poisson; out[n] ms. */
+int ora_arrivals(int kind, uint32_t n, double gap, double period, double ratio,
+                 uint64_t seed, double* out);
 
 /* ---------------- host tier ---------------- */
 /* Element e of host block h (K then V, [T][D] each) as the stored encoding

@@ -57,6 +57,8 @@ class SelGen(C.Structure):
         ("kv_heads", C.c_int), ("k", C.c_int), ("dist", C.c_int),
         ("zipf_s", C.c_double), ("reuse", C.c_double), ("prefix_blocks", C.c_int), ("seed", C.c_uint64),
         ("ctx_blocks", C.POINTER(C.c_int)), ("reuse_r", C.POINTER(C.c_double)),
+        ("rid", C.POINTER(C.c_int)), ("start", C.POINTER(C.c_int)),
+        ("active", C.POINTER(C.c_uint8)),
     ]
 
 
@@ -113,6 +115,9 @@ _sig("ora_exec_create", C.c_void_p, C.POINTER(Geom))
 _sig("ora_exec_destroy", None, C.c_void_p)
 _sig("ora_exec_step", C.c_int, C.c_void_p, _u32p, _u32p, _u32p, _missp, _u64p, _u8p)
 _sig("ora_exec_state", None, C.c_void_p, _u32p, _u32p, _u32p)
+_sig("ora_exec_reset_owner", C.c_int, C.c_void_p, C.c_int)
+_sig("ora_arrivals", C.c_int, C.c_int, C.c_uint32, C.c_double, C.c_double, C.c_double,
+     C.c_uint64, _f64p)
 _sig("ora_ctx_uniform", None, C.c_uint64, C.c_int, C.c_int, C.c_int, _i32p)
 _sig("ora_selgen_max_blocks", C.c_int, C.POINTER(SelGen))
 _sig("ora_selgen_step", C.c_int, C.POINTER(SelGen), C.c_int, _u32p, _u32p)
@@ -185,6 +190,10 @@ class Executor:
         self.last_flags = flags
         return slots, mc, misses.reshape(self.n_sets, self.max_sel), counts
 
+    def reset_owner(self, owner):
+        if lib.ora_exec_reset_owner(self.ptr, owner):
+            raise ValueError(f"owner {owner}")
+
     def state(self):
         cap = self.g.cap
         fill = np.zeros(self.n_sets, np.uint32)
@@ -216,7 +225,26 @@ def selgen(n_req, n_layers, kv_heads, k, ctx_blocks, dist=1, zipf_s=1.1, reuse=0
     s._ctx = ctx  # keep alive
     s._rr = rr
     s._state = np.zeros(n_req * n_layers * kv_heads * k, np.uint32)
+    # lane turnover: request id, admission step and activity of each lane
+    s._rid = np.arange(n_req, dtype=np.int32)
+    s._start = np.zeros(n_req, np.int32)
+    s._active = np.ones(n_req, np.uint8)
+    s.rid = s._rid.ctypes.data_as(C.POINTER(C.c_int))
+    s.start = s._start.ctypes.data_as(C.POINTER(C.c_int))
+    s.active = s._active.ctypes.data_as(C.POINTER(C.c_uint8))
     return s
+
+
+def selgen_admit(s: SelGen, lane, request_id, ctx_blocks, step):
+    """Request `request_id` with context ctx_blocks takes `lane` from `step`."""
+    s._rid[lane] = request_id
+    s._start[lane] = step
+    s._ctx[lane] = ctx_blocks
+    s._active[lane] = 1
+
+
+def selgen_retire(s: SelGen, lane):
+    s._active[lane] = 0
 
 
 def selgen_step(s: SelGen, step):
@@ -265,3 +293,45 @@ def attention_f64(g: Geom, sel, q):
 
 def host_index(g: Geom, set_id, block):
     return int(lib.ora_host_index(C.byref(g), set_id, block))
+
+
+def arrivals(kind, n, gap_ms, period_ms=50.0, ratio=10.0, seed=0):
+    out = np.zeros(n, np.float64)
+    if lib.ora_arrivals(kind, n, gap_ms, period_ms, ratio, seed, out):
+        raise ValueError("ora_arrivals")
+    return out
+
+
+def sched_run(lanes, arrive_ms, len_steps, clock_ms):
+    """Tick scheduler of one executor, restated for small cases.
+
+    Tick t starts at clock_ms[t].  A request is resident from the tick of its
+    admission until it has run len_steps ticks (the reference retires a
+    request in tick_end once next_step reaches its length,
+    src/runtime/wla_multigpu.cuh:834-857).  Arrived requests queue in arrival
+    order (ties by id) and fill free lanes, lowest lane first.  Returns the
+    lane -> request table of every tick ([ticks][lanes], -1 idle) and each
+    request's admission and last tick (-1 if never).
+    """
+    n = len(arrive_ms)
+    queue = sorted(range(n), key=lambda r: (arrive_ms[r], r))
+    lane_of = [-1] * lanes
+    ran = [0] * n
+    admit, last = [-1] * n, [-1] * n
+    table = []
+    qi = 0  # queue[:qi] have been admitted
+    for t, now in enumerate(clock_ms):
+        for ln in range(lanes):  # the previous tick ran every resident request
+            r = lane_of[ln]
+            if r >= 0 and t > 0:
+                ran[r] += 1
+                if ran[r] == len_steps[r]:
+                    last[r] = t - 1
+                    lane_of[ln] = -1
+        for ln in range(lanes):
+            if lane_of[ln] < 0 and qi < n and arrive_ms[queue[qi]] <= now:
+                lane_of[ln] = queue[qi]
+                admit[queue[qi]] = t
+                qi += 1
+        table.append(list(lane_of))
+    return np.array(table, np.int32).reshape(len(clock_ms), lanes), admit, last
