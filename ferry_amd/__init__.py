@@ -29,6 +29,7 @@ __all__ = [
     "ctx_uniform", "arrivals", "lib", "LIB_PATH", "F32", "F16", "BF16", "FP8", "LRU_STEP",
     "LRU_SERIAL", "ASSIGN_SPREAD", "ASSIGN_AFFINITY", "ATTN_AUTO", "ATTN_VALU", "ATTN_MFMA",
     "MISS_DTYPE", "EMPTY", "ARRIVAL_STEADY", "ARRIVAL_BURSTY", "ARRIVAL_POISSON", "ARRIVAL_MMPP",
+    "SCHED_FIFO", "SCHED_PINNED", "trace_load",
 ]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libferry_amd.so")
@@ -44,6 +45,7 @@ ATTN_AUTO, ATTN_VALU, ATTN_MFMA = 0, 1, 2
 PROBE_HBM_GATHER, PROBE_HOST_READ, PROBE_HOST_DMA = 0, 1, 2
 ARRIVAL_STEADY, ARRIVAL_BURSTY, ARRIVAL_POISSON, ARRIVAL_MMPP = 0, 1, 2, 3
 EMPTY = 0xFFFFFFFF  # selection id of an empty position (and its slot)
+SCHED_FIFO, SCHED_PINNED = 0, 1
 ESIZE = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 MISS_DTYPE = np.dtype([("block", "<u4"), ("slot", "<u4"), ("evicted", "<u4"), ("set", "<u4")])
 
@@ -87,6 +89,16 @@ class SelGenConfig(C.Structure):
     ]
 
 
+class TraceInfo(C.Structure):
+    _fields_ = [
+        ("requests", C.c_uint32), ("steps", C.c_uint32), ("layers", C.c_uint32),
+        ("page_tokens", C.c_uint32), ("block_tokens", C.c_uint32), ("kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32), ("sel_pages", C.c_uint32), ("sel_blocks", C.c_uint32),
+        ("short_records", C.c_uint32), ("unique_blocks", C.c_uint64),
+        ("max_blocks_per_req", C.c_uint64),
+    ]
+
+
 _vp = C.c_void_p
 _i32 = C.c_int32
 _PROTOS = {
@@ -107,7 +119,8 @@ _PROTOS = {
     "ferry_selgen_retire": (C.c_int, [_vp, _i32]),
     "ferry_arrivals": (C.c_int, [C.c_int, C.c_uint32, C.c_double, C.c_double, C.c_double,
                                  C.c_uint64, _vp]),
-    "ferry_sched_create": (C.c_int, [_i32, C.c_uint32, _vp, _vp, C.POINTER(_vp)]),
+    "ferry_sched_create": (C.c_int, [_i32, _i32, C.c_uint32, _vp, _vp, C.POINTER(_vp)]),
+    "ferry_trace_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(TraceInfo), _vp, C.c_uint64]),
     "ferry_sched_destroy": (C.c_int, [_vp]),
     "ferry_sched_tick": (C.c_int, [_vp, C.c_double, _vp, _vp, _vp, C.POINTER(_i32), _vp,
                                    C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32)]),
@@ -405,14 +418,15 @@ class Sched:
     """Tick scheduler of one executor (ferry_sched_*): `lanes` batch lanes
     serve requests that arrive at arrive_ms and decode len_steps steps."""
 
-    def __init__(self, lanes, arrive_ms, len_steps):
+    def __init__(self, lanes, arrive_ms, len_steps, pinned=False):
         self.lanes = lanes
         self._arr = np.ascontiguousarray(arrive_ms, np.float64)
         self._len = np.ascontiguousarray(len_steps, np.int32)
         self.n = self._arr.size
         h = _vp()
-        _check(lib.ferry_sched_create(lanes, self.n, self._arr.ctypes.data,
-                                      self._len.ctypes.data, C.byref(h)), "ferry_sched_create")
+        _check(lib.ferry_sched_create(lanes, SCHED_PINNED if pinned else SCHED_FIFO, self.n,
+                                      self._arr.ctypes.data, self._len.ctypes.data, C.byref(h)),
+               "ferry_sched_create")
         self._h = h
 
     def tick(self, now_ms):
@@ -445,6 +459,17 @@ class Sched:
         h, self._h = getattr(self, "_h", None), None
         if h and lib is not None:
             lib.ferry_sched_destroy(h)
+
+
+def trace_load(path, strict=True):
+    """Read an FMT1 selection trace: (info dict, dense ids [R, S, L, sel_blocks])."""
+    info = TraceInfo()
+    p = os.fsencode(path)
+    _check(lib.ferry_trace_load(p, int(strict), C.byref(info), None, 0), "ferry_trace_load")
+    ids = np.zeros((info.requests, info.steps, info.layers, info.sel_blocks), np.uint32)
+    _check(lib.ferry_trace_load(p, int(strict), C.byref(info), ids.ctypes.data, ids.size),
+           "ferry_trace_load")
+    return {f: getattr(info, f) for f, _ in TraceInfo._fields_}, ids
 
 
 def refgen_selections(R, L, S, sel, seed=42):

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "errors.hpp"
 #include "kernels.hpp"
 #include "../../include/ferry/gpu_bounded_queue.hpp"
 
@@ -34,6 +35,12 @@ int fail(int code, const std::string& msg) {
   g_err = msg;
   return code;
 }
+
+}  // namespace
+
+int ferry_amd::report(int code, const std::string& msg) { return fail(code, msg); }
+
+namespace {
 
 #define HIPC(expr)                                                                         \
   do {                                                                                     \

@@ -6,8 +6,10 @@
 // (src/runtime/wla_multigpu.cuh:829-864, 2610-2665).  Requests become resident
 // at their arrival time, which is steady or bursty in the reference
 // (:497-501).  Here residency is bounded by the executor's batch lanes: an
-// arrived request waits in a FIFO until a lane is free, and one executor
-// decode step runs every resident lane at once.  The scheduler is pure host
+// arrived request waits in a FIFO until a lane is free (any lane, or with
+// FERRY_SCHED_PINNED only lane r mod lanes, which keeps a request's lane --
+// and so its prefix group's sets -- fixed), and one executor decode step runs
+// every resident lane at once.  The scheduler is pure host
 // logic; the caller supplies the clock (wall or virtual) and applies the
 // admissions (lane reset, generator admission) before launching the step.
 #include <algorithm>
@@ -44,12 +46,15 @@ double expo(double mean, uint64_t seed, uint64_t salt, uint64_t i) {
 
 struct ferry_sched {
   int32_t lanes = 0;
+  int32_t policy = FERRY_SCHED_FIFO;
   uint32_t n = 0;
   std::vector<double> arrive;
   std::vector<int32_t> len;
   std::vector<uint32_t> order;  // requests by (arrival, id)
   uint32_t head = 0;            // order[head, next) are waiting
   uint32_t next = 0;            // order[next, n) have not arrived
+  std::vector<std::vector<uint32_t>> lane_q;  // FERRY_SCHED_PINNED: waiting per lane
+  std::vector<size_t> lane_qh;                 // ... and the head of each
   std::vector<int32_t> lane_req, lane_step;
   std::vector<int32_t> steps_done, admit_tick, done_tick;
   uint32_t completed = 0;
@@ -101,14 +106,18 @@ int ferry_arrivals(int kind, uint32_t n, double gap_ms, double period_ms, double
   }
 }
 
-int ferry_sched_create(int32_t lanes, uint32_t n, const double* arrive_ms,
+int ferry_sched_create(int32_t lanes, int32_t policy, uint32_t n, const double* arrive_ms,
                        const int32_t* len_steps, ferry_sched** out) {
   if (!out || lanes < 1 || (n && (!arrive_ms || !len_steps))) return FERRY_EINVAL;
+  if (policy != FERRY_SCHED_FIFO && policy != FERRY_SCHED_PINNED) return FERRY_EINVAL;
   for (uint32_t r = 0; r < n; ++r)
     if (len_steps[r] < 1 || !std::isfinite(arrive_ms[r])) return FERRY_EINVAL;
   ferry_sched* s = new ferry_sched();
   s->lanes = lanes;
+  s->policy = policy;
   s->n = n;
+  s->lane_q.assign(lanes, {});
+  s->lane_qh.assign(lanes, 0);
   s->arrive.assign(arrive_ms, arrive_ms + n);
   s->len.assign(len_steps, len_steps + n);
   s->order.resize(n);
@@ -146,12 +155,23 @@ int ferry_sched_tick(ferry_sched* s, double now_ms, int32_t* lane_req, int32_t* 
         left.push_back(ln);
       }
     }
-  // 2. arrivals join the FIFO; free lanes take its head, lowest lane first
-  while (s->next < s->n && s->arrive[s->order[s->next]] <= now_ms) ++s->next;
+  // 2. arrivals join the FIFO (FERRY_SCHED_PINNED: their lane's FIFO); free
+  //    lanes take the head, lowest lane first
+  while (s->next < s->n && s->arrive[s->order[s->next]] <= now_ms) {
+    const uint32_t r = s->order[s->next++];
+    if (s->policy == FERRY_SCHED_PINNED) s->lane_q[r % (uint32_t)s->lanes].push_back(r);
+  }
   int32_t na = 0;
-  for (int32_t ln = 0; ln < s->lanes && s->head < s->next; ++ln) {
+  for (int32_t ln = 0; ln < s->lanes; ++ln) {
     if (s->lane_req[ln] >= 0) continue;
-    const uint32_t r = s->order[s->head++];
+    uint32_t r;
+    if (s->policy == FERRY_SCHED_PINNED) {
+      if (s->lane_qh[ln] == s->lane_q[ln].size()) continue;
+      r = s->lane_q[ln][s->lane_qh[ln]++];
+    } else {
+      if (s->head == s->next) break;
+      r = s->order[s->head++];
+    }
     s->lane_req[ln] = (int32_t)r;
     s->admit_tick[r] = s->tick;
     if (admitted) admitted[na] = ln;

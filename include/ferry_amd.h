@@ -324,7 +324,11 @@ int ferry_arrivals(int kind, uint32_t n, double gap_ms, double period_ms, double
  *      those that reached len_steps leave their lanes (tick_end,
  *      src/runtime/wla_multigpu.cuh:834-864);
  *   2. requests with arrive_ms <= now_ms join a FIFO in arrival order (ties
- *      by id) and take free lanes, lowest lane first;
+ *      by id) and take free lanes, lowest lane first.  With policy
+ *      FERRY_SCHED_PINNED request r only ever runs in lane r % lanes (one
+ *      FIFO per lane): lanes >= n gives every request its own lane, as the
+ *      reference's per-request hot caches do, and a request stays in its
+ *      prefix group's lanes;
  *   3. out: lane_req[lanes] = request in each lane (-1 idle),
  *      lane_step[lanes] = that request's step index in this tick,
  *      admitted[0..*n_admitted) = lanes that received a new request,
@@ -334,8 +338,10 @@ int ferry_arrivals(int kind, uint32_t n, double gap_ms, double period_ms, double
  * The reference's exec loop runs every resident request once per tick
  * (src/runtime/wla_multigpu.cuh:2610-2665); its residency is unbounded, which
  * is lanes >= n here. */
+#define FERRY_SCHED_FIFO 0
+#define FERRY_SCHED_PINNED 1
 typedef struct ferry_sched ferry_sched;
-int ferry_sched_create(int32_t lanes, uint32_t n, const double* arrive_ms,
+int ferry_sched_create(int32_t lanes, int32_t policy, uint32_t n, const double* arrive_ms,
                        const int32_t* len_steps, ferry_sched** out);
 int ferry_sched_destroy(ferry_sched* s);
 int ferry_sched_tick(ferry_sched* s, double now_ms, int32_t* lane_req, int32_t* lane_step,
@@ -345,6 +351,28 @@ int ferry_sched_tick(ferry_sched* s, double now_ms, int32_t* lane_req, int32_t* 
  * per-request admission tick and completion tick (-1 until known). */
 int ferry_sched_next_arrival(const ferry_sched* s, double* ms);
 int ferry_sched_request_ticks(const ferry_sched* s, int32_t* admit_tick, int32_t* done_tick);
+
+/* ---- FMT1 selection traces ----
+ * tools/capture_miss_trace.py records real top-k selections as FMT1 (header
+ * :27-38: "FMT1", version 1, R, steps, layers, page_tokens, block_tokens,
+ * kv_heads, head_dim, sel_pages as u32; then per (request, step, layer) a u16
+ * count and count u32 chained-hash block ids).  ferry_trace_load reads one:
+ * raw ids are renamed to dense ids in order of first appearance over the
+ * whole trace, as load_miss_trace does (src/workloads/miss_trace.cuh:75-185).
+ * out_ids (NULL: header and counts only) gets R*steps*layers*sel_blocks ids
+ * in (r, s, l, k) order, sel_blocks = sel_pages*page_tokens/block_tokens.  A
+ * record with fewer ids is FERRY_EINVAL when `strict` (the reference refuses
+ * it, :123-129) and is padded with FERRY_EMPTY otherwise.  Bad files return
+ * FERRY_EINVAL with the reason in ferry_last_error(); nothing exits. */
+typedef struct ferry_trace_info {
+  uint32_t requests, steps, layers, page_tokens, block_tokens, kv_heads, head_dim, sel_pages;
+  uint32_t sel_blocks;         /* ids per (request, step, layer) record */
+  uint32_t short_records;      /* records padded with FERRY_EMPTY */
+  uint64_t unique_blocks;      /* distinct raw ids; dense ids are [0, unique_blocks) */
+  uint64_t max_blocks_per_req; /* most distinct ids one request selects */
+} ferry_trace_info;
+int ferry_trace_load(const char* path, int strict, ferry_trace_info* info, uint32_t* out_ids,
+                     uint64_t capacity);
 
 /* Reference generator: the selections replay_miss_stream draws
  * (src/workloads/missstream.cuh:104-133, std::mt19937_64(seed)) for

@@ -6,6 +6,7 @@ imports it.
 """
 import ctypes as C
 import os
+import struct
 import subprocess
 
 import numpy as np
@@ -302,14 +303,15 @@ def arrivals(kind, n, gap_ms, period_ms=50.0, ratio=10.0, seed=0):
     return out
 
 
-def sched_run(lanes, arrive_ms, len_steps, clock_ms):
+def sched_run(lanes, arrive_ms, len_steps, clock_ms, pinned=False):
     """Tick scheduler of one executor, restated for small cases.
 
     Tick t starts at clock_ms[t].  A request is resident from the tick of its
     admission until it has run len_steps ticks (the reference retires a
     request in tick_end once next_step reaches its length,
     src/runtime/wla_multigpu.cuh:834-857).  Arrived requests queue in arrival
-    order (ties by id) and fill free lanes, lowest lane first.  Returns the
+    order (ties by id) and fill free lanes, lowest lane first; `pinned`
+    requests only take lane r % lanes.  Returns the
     lane -> request table of every tick ([ticks][lanes], -1 idle) and each
     request's admission and last tick (-1 if never).
     """
@@ -328,10 +330,64 @@ def sched_run(lanes, arrive_ms, len_steps, clock_ms):
                 if ran[r] == len_steps[r]:
                     last[r] = t - 1
                     lane_of[ln] = -1
-        for ln in range(lanes):
-            if lane_of[ln] < 0 and qi < n and arrive_ms[queue[qi]] <= now:
-                lane_of[ln] = queue[qi]
-                admit[queue[qi]] = t
-                qi += 1
+        if pinned:
+            for ln in range(lanes):
+                if lane_of[ln] >= 0:
+                    continue
+                mine = [r for r in queue if r % lanes == ln and admit[r] < 0
+                        and arrive_ms[r] <= now]
+                if mine:
+                    lane_of[ln] = mine[0]
+                    admit[mine[0]] = t
+        else:
+            for ln in range(lanes):
+                if lane_of[ln] < 0 and qi < n and arrive_ms[queue[qi]] <= now:
+                    lane_of[ln] = queue[qi]
+                    admit[queue[qi]] = t
+                    qi += 1
         table.append(list(lane_of))
     return np.array(table, np.int32).reshape(len(clock_ms), lanes), admit, last
+
+
+def trace_load(path, strict=True):
+    """FMT1 trace reader restated with numpy (tools/capture_miss_trace.py:27-38
+    header, :366-370 records; dense renaming in order of first appearance as
+    in src/workloads/miss_trace.cuh:136-145).  Returns (header dict, dense ids
+    [R, S, L, sel_blocks] with NONE padding, unique count, max distinct ids of
+    one request).  Raises ValueError where the product returns FERRY_EINVAL."""
+    raw = open(path, "rb").read()
+    if raw[:4] != b"FMT1":
+        raise ValueError("magic")
+    if len(raw) < 40:
+        raise ValueError("header")
+    ver, R, S, L, PT, BT, KV, D, SEL = struct.unpack_from("<9I", raw, 4)
+    if ver != 1 or BT == 0 or PT == 0 or PT % BT:
+        raise ValueError("header")
+    nb = SEL * (PT // BT)
+    recs, pos = [], 40
+    for _ in range(R * S * L):
+        if pos + 2 > len(raw):
+            raise ValueError("truncated")
+        (cnt,) = struct.unpack_from("<H", raw, pos)
+        pos += 2
+        if cnt > nb or (strict and cnt < nb):
+            raise ValueError("count")
+        if pos + 4 * cnt > len(raw):
+            raise ValueError("truncated")
+        recs.append(np.frombuffer(raw, "<u4", cnt, pos))
+        pos += 4 * cnt
+    flat = np.concatenate(recs) if recs else np.zeros(0, np.uint32)
+    uniq, first, inv = np.unique(flat, return_index=True, return_inverse=True)
+    rank = np.empty(len(uniq), np.int64)
+    rank[np.argsort(first, kind="stable")] = np.arange(len(uniq))
+    dense = rank[inv].astype(np.uint32)
+    out = np.full((R * S * L, nb), NONE, np.uint32)
+    i = 0
+    for j, rec in enumerate(recs):
+        out[j, :len(rec)] = dense[i:i + len(rec)]
+        i += len(rec)
+    per_req = [len(np.unique(np.concatenate(recs[r * S * L:(r + 1) * S * L])))
+               if S * L else 0 for r in range(R)]
+    hdr = dict(requests=R, steps=S, layers=L, page_tokens=PT, block_tokens=BT, kv_heads=KV,
+               head_dim=D, sel_pages=SEL, sel_blocks=nb)
+    return hdr, out.reshape(R, S, L, nb), len(uniq), max(per_req) if per_req else 0

@@ -235,6 +235,24 @@ def test_scheduler_matches_oracle_and_invariants(seed):
     assert s.tick(clock[-1] + 1)["done"]
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_pinned_scheduler_matches_oracle(seed):
+    rng = np.random.default_rng(100 + seed)
+    n, lanes = int(rng.integers(5, 50)), int(rng.integers(1, 7))
+    arrive = np.round(np.sort(rng.exponential(2.0, n).cumsum()))
+    lens = rng.integers(1, 9, n).astype(np.int32)
+    clock = np.arange(float(lens.sum() + arrive[-1] + 5))
+    s = F.Sched(lanes, arrive, lens, pinned=True)
+    table = np.array([s.tick(now)["lane_req"] for now in clock])
+    otab, oa, od = O.sched_run(lanes, arrive, lens, clock, pinned=True)
+    assert np.array_equal(table, otab)
+    a, d = s.request_ticks()
+    assert list(a) == oa and list(d) == od
+    for r in range(n):  # request r only ever runs in lane r % lanes
+        assert set(np.nonzero(table == r)[1]) == {r % lanes}
+        assert np.count_nonzero(table == r) == lens[r]
+
+
 def test_scheduler_unbounded_lanes_admits_on_arrival():
     """With at least as many lanes as requests (the reference's unbounded
     residency) a request is admitted at the first tick at or after its arrival."""
