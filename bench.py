@@ -43,6 +43,7 @@ sys.path.insert(0, ROOT)
 METRIC = "miss-blocks/s + sparse-decode tok/s @7B shape; HBM & host-link GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
 LINK_PEAK_GBS = 32e9 * 16 * 128 / 130 / 8 / 1e9  # PCIe Gen5 x16, one direction
+MMPP_RATIO = 10.0  # fast-state rate / slow-state rate of the Markov-modulated arrivals
 
 WORKLOADS = {
     # 7B-shape steady decode (the headline)
@@ -79,6 +80,14 @@ def parse():
                     help="attention kernel: MFMA for GQA groups of 16/8-bit KV (auto), or forced")
     ap.add_argument("--chunks", type=int, default=8,
                     help="layer chunks of the fetch/attention overlap (1 = no side stream)")
+    ap.add_argument("--arrivals", default="none", choices=["none", "poisson", "mmpp"],
+                    help="request arrivals instead of a full steady batch: requests wait for a "
+                         "lane, decode --len steps and leave (lane reset on admission)")
+    ap.add_argument("--len", default="16,48", help="request decode lengths lo,hi (steps)")
+    ap.add_argument("--gap-ticks", type=float, default=0.0,
+                    help="mean inter-arrival gap in ticks (0: 0.9 of the lanes' service rate)")
+    ap.add_argument("--mmpp-period", type=float, default=1.0,
+                    help="mean sojourn of each MMPP state, in ticks (rates 1x and 10x)")
     ap.add_argument("--rocprof-summary", metavar="DB",
                     help="summarise a rocprofv3 results database instead of benchmarking")
     ap.add_argument("--last", type=int, default=0,
@@ -336,6 +345,125 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     return res
 
 
+def arrival_plan(a, w, F, n_ticks, zipf):
+    """Virtual-clock schedule of an arrival run (one time unit = one tick).
+    The first B requests are queued at t=0 with residual lengths so that the
+    lanes start full; further requests arrive as a Poisson or Markov-modulated
+    Poisson process at 0.9 of the lanes' service rate.  Returns per tick the
+    selections, the lanes admitted (their sets are reset) and the resident
+    count, plus the per-request arrival/admission ticks."""
+    B, L, H, k = w["B"], w["L"], w["Hkv"], w["k"]
+    if w["group"] != 1:
+        raise SystemExit("arrivals need private sets (group 1): a prefix group's lanes share sets")
+    lo_len, hi_len = map(int, a.len.split(","))
+    gap = a.gap_ticks or (lo_len + hi_len) / 2.0 / B / 0.9  # mean gap over the run
+    n_req = min(65535, B + int(n_ticks / gap * 2) + 16)
+    kind = F.ARRIVAL_MMPP if a.arrivals == "mmpp" else F.ARRIVAL_POISSON
+    # the MMPP spends half its time at each rate (equal mean sojourns): its
+    # slow-state gap is (1 + ratio) / 2 times the mean gap
+    slow_gap = gap * (1 + MMPP_RATIO) / 2 if kind == F.ARRIVAL_MMPP else gap
+    arrive = np.concatenate([np.zeros(B), F.arrivals(kind, n_req - B, slow_gap, a.mmpp_period,
+                                                     MMPP_RATIO, seed=5)])
+    lens = F.ctx_uniform(6, n_req, lo_len, hi_len)
+    lens[:B] = F.ctx_uniform(8, B, 1, hi_len)  # residual lengths of the initial batch
+    lo, hi = w["ctx"]
+    ctxs = F.ctx_uniform(7, n_req, lo, hi)
+    sg = F.SelGen(B, L, H, k, np.full(B, hi, np.int32), dist=1, zipf_s=zipf, reuse=w["reuse"],
+                  seed=3)
+    reuse_req = lognormal_reuse(n_req, k) if a.workload == "skew" else None
+    lane_reuse = np.full(B, w["reuse"])
+    for ln in range(B):
+        sg.retire(ln)
+    sched = F.Sched(B, arrive, lens)
+    plan = []
+    for t in range(n_ticks):
+        r = sched.tick(float(t))
+        for ln in r["retired"]:
+            sg.retire(int(ln))
+        for ln in r["admitted"]:
+            rid = int(r["lane_req"][ln])
+            sg.admit(int(ln), rid, int(ctxs[rid]), t)
+            if reuse_req is not None:
+                lane_reuse[ln] = reuse_req[rid]
+        if reuse_req is not None and len(r["admitted"]):
+            sg.set_reuse(lane_reuse)
+        plan.append((sg.step(t), np.array(r["admitted"], np.int32), r["resident"]))
+    admit, _ = sched.request_ticks()
+    return plan, arrive, admit, sg.max_blocks, gap
+
+
+def run_arrivals(a, w, F, torch, zipf=None, workers=None, steal=None):
+    """Arrival-driven run: warmup ticks (lanes turn over), then --steps timed
+    ticks.  Each tick resets the sets of newly admitted lanes on the stream and
+    runs one decode step over the resident lanes (idle lanes are empty rows)."""
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()  # default priority
+    B, L, H, Hq, k, C = w["B"], w["L"], w["Hkv"], w["Hq"], w["k"], w["C"]
+    zipf = w["zipf"] if zipf is None else zipf
+    lo_len, hi_len = map(int, a.len.split(","))
+    warm = max(a.warmup, (lo_len + hi_len) // 2 + 8)
+    n_ticks = warm + a.steps
+    t0 = time.perf_counter()
+    plan, arrive, admit, max_blocks, gap = arrival_plan(a, w, F, n_ticks, zipf)
+    gen_s = time.perf_counter() - t0
+    sels = [torch.from_numpy(p[0].view(np.int32)).to(dev) for p in plan]
+    adm = [torch.from_numpy(p[1]).to(dev) if len(p[1]) else None for p in plan]
+    dtype = {"f16": F.F16, "bf16": F.BF16, "fp8": F.FP8, "f32": F.F32}[w["dtype"]]
+    ex = F.Executor(B, L, H, k, C, max_blocks, q_heads=Hq, dtype=dtype, host_blocks=a.host_blocks,
+                    fetch_workers=a.workers if workers is None else workers,
+                    steal=a.steal if steal is None else steal,
+                    assign=F.ASSIGN_AFFINITY if a.workload == "skew" else F.ASSIGN_SPREAD)
+    ex.hosttier_fill()
+    bufs = ex.alloc_step_buffers()
+    qs = [torch.randn((B, L, Hq, 128), device=dev, dtype=torch.float32) for _ in range(2)]
+    out = torch.empty_like(qs[0])
+    torch.cuda.synchronize()
+
+    def tick(t):
+        if adm[t] is not None:
+            ex.reset_owners(adm[t], stream=stream)
+        ex.decode_step(sels[t], qs[t & 1], bufs, out, chunks=a.chunks, stream=stream,
+                       side_stream=side if a.chunks > 1 else None)
+
+    for t in range(warm):
+        tick(t)
+    torch.cuda.synchronize()
+    st0 = ex.stats()
+    t0 = time.perf_counter()
+    for t in range(warm, n_ticks):
+        tick(t)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    st1 = ex.stats()
+    if st1["device_error"]:
+        raise RuntimeError(f"device error {st1['device_error']}")
+    ex.close()
+    tokens = sum(p[2] for p in plan[warm:])
+    ms_tick = elapsed / a.steps * 1e3
+    waited = np.array([admit[r] - arrive[r] for r in range(len(arrive))
+                       if warm <= admit[r] < n_ticks and arrive[r] > 0])
+    misses = st1["misses"] - st0["misses"]
+    sel = st1["selections"] - st0["selections"]
+    return {
+        "ms_per_step": round(ms_tick, 3),
+        "value": round(tokens / elapsed, 2),
+        "miss_rate": round(misses / max(sel, 1), 4),
+        "miss_blocks_per_s": round(misses / elapsed, 1),
+        "arrivals": {"process": a.arrivals, "mean_gap_ticks": round(gap, 4),
+                     "mean_rate_req_per_s": round(1e3 / (gap * ms_tick), 2),
+                     "mmpp_period_ms": round(a.mmpp_period * ms_tick, 1) if a.arrivals == "mmpp"
+                     else None,
+                     "len_steps": [lo_len, hi_len], "warmup_ticks": warm,
+                     "mean_resident_lanes": round(tokens / a.steps, 2), "lanes": B,
+                     "admitted_in_timed_ticks": int(sum(len(p[1]) for p in plan[warm:])),
+                     "queue_wait_ticks_mean": round(float(waited.mean()), 3) if waited.size else 0.0,
+                     "queue_wait_ticks_p99": round(float(np.percentile(waited, 99)), 3)
+                     if waited.size else 0.0},
+        "selection_gen_s": round(gen_s, 2),
+    }
+
+
 def main():
     a = parse()
     if a.rocprof_summary:
@@ -360,6 +488,22 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     w = WORKLOADS[a.workload]
+    if a.arrivals != "none":
+        if a.workload == "skew":  # the stealing sweep of config 3 under MMPP arrivals
+            rows = []
+            for zs in (0.6, 1.0, 1.4):
+                for steal in (0, 1):
+                    r = run_arrivals(a, w, F, torch, zipf=zs, workers=304, steal=steal)
+                    rows.append(dict({"zipf": zs, "steal": steal}, **r))
+                    print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+            print(json.dumps({"workload": f"skew+{a.arrivals}", "rows": rows}), flush=True)
+            return
+        r = run_arrivals(a, w, F, torch)
+        print(json.dumps({"metric": "decode tok/s under request arrivals (lane turnover)",
+                          "workload": f"{a.workload}+{a.arrivals}", "n_gpus": 1,
+                          "steps": a.steps, "dtype": w["dtype"], "data": "synthetic",
+                          "higher_is_better": True, **r}), flush=True)
+        return
     if a.workload == "skew":
         # stealing on vs off over the Zipf skew sweep, 304 persistent workgroups,
         # request-affinity assignment of misses to workgroups

@@ -10,10 +10,13 @@ namespace ferry_amd {
 // return how many were kept.  A row of a request that is not resident this
 // step is all kNone (0 kept); a short context gives a ragged row.
 // Every thread of the W-wavefront workgroup must call it: each thread holds
-// up to kMaxTopK / (64 W) ids in registers, each wavefront counts its 64-id
-// chunks with a ballot, and after one barrier every kept id is written at
-// (ids kept in earlier chunks) + (kept lanes below it in its chunk).
-// `cnt` is LDS scratch of kMaxTopK / 64 ints.  Ends with a barrier.
+// up to kMaxTopK / (64 W) ids in registers and stores them in place, and each
+// wavefront counts its 64-id chunks with a ballot.  After one barrier every
+// thread sums the counts; when all k ids are kept (a full row, the common
+// case) the in-place copy is the answer.  Otherwise (a workgroup-uniform
+// branch) every kept id is rewritten at (ids kept in earlier chunks) + (kept
+// lanes below it in its chunk), behind a second barrier.  `cnt` is LDS
+// scratch of kMaxTopK / 64 ints.  Ends with a barrier.
 template <int W>
 __device__ inline int stage_row_ids(const uint32_t* __restrict__ sl, int k, uint32_t* ids,
                                     int* cnt) {
@@ -25,6 +28,7 @@ __device__ inline int stage_row_ids(const uint32_t* __restrict__ sl, int k, uint
   for (int i = 0; i < PER; ++i) {
     const int j = tid + i * NT;
     v[i] = j < k ? sl[j] : kNone;
+    if (j < k) ids[j] = v[i];
   }
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -36,6 +40,7 @@ __device__ inline int stage_row_ids(const uint32_t* __restrict__ sl, int k, uint
   const int nchunks = (k + 63) >> 6;
   int total = 0;
   for (int c = 0; c < nchunks; ++c) total += cnt[c];
+  if (total == k) return total;  // uniform: every thread read the same counts
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int j = tid + i * NT;

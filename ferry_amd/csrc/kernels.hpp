@@ -25,9 +25,13 @@ struct Ring {
 };
 
 // Device counters (unsigned long long).
-enum StatSlot {
-  kStatMisses = 0, kStatBytes, kStatSteals, kStatStolen, kStatLast, kStatDrain, kStatSel, kStatCount
-};
+enum StatSlot { kStatMisses = 0, kStatBytes, kStatSteals, kStatStolen, kStatLast, kStatDrain, kStatCount };
+
+// Non-empty selections are counted by every set's wavefront; one counter
+// would serialise tens of thousands of atomics, so set s adds into counter
+// s % kSelCounters, each on its own 128-byte line (kSelStride u64 apart).
+constexpr int kSelCounters = 256;
+constexpr int kSelStride = 16;
 
 struct FetchArgs {
   Geo g;
@@ -46,7 +50,7 @@ struct FetchArgs {
 template <bool SERIAL>
 __global__ void k_lru_step(Geo g, const uint32_t* sel, uint32_t* slots_out, uint32_t* miss_count,
                            ferry_miss* misses, uint8_t* miss_flag, SetState st, Ring ring, int l0,
-                           int nl, unsigned long long* stats, int* err);
+                           int nl, unsigned long long* sel_counts, int* err);
 __global__ void k_sets_reset(Geo g, SetState st);
 __global__ void k_sets_reset_owners(Geo g, SetState st, const uint32_t* owners, uint32_t n, int* err);
 

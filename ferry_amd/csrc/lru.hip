@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
                                                   ferry_miss* __restrict__ misses,
                                                   uint8_t* __restrict__ miss_flag,
                                                   SetState st, Ring ring, int l0, int nl,
-                                                  unsigned long long* __restrict__ stats,
+                                                  unsigned long long* __restrict__ sel_counts,
                                                   int* __restrict__ err) {
   extern __shared__ uint32_t lds[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -286,7 +286,8 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   if (lane == 0) {
     st.fill[set] = fill;
     miss_count[set] = (uint32_t)total;
-    if (nsel) atomicAdd(stats + kStatSel, (unsigned long long)nsel);
+    if (nsel)
+      atomicAdd(sel_counts + (size_t)(set % kSelCounters) * kSelStride, (unsigned long long)nsel);
   }
 }
 

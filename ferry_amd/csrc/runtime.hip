@@ -70,6 +70,7 @@ struct ferry_ctx {
   uint32_t* ring_cap = nullptr;
   uint32_t* worker_of_set = nullptr;
   unsigned long long* stats = nullptr;
+  unsigned long long* sel_counts = nullptr;  // [kSelCounters * kSelStride]
   uint32_t* done = nullptr;
   int* err = nullptr;
   uint8_t* host = nullptr;      // host pointer of the pinned tier
@@ -136,7 +137,7 @@ void release(ferry_ctx* c) {
   (void)hipSetDevice(c->device);
   void* dev[] = {c->pool, c->pool_scales, c->st.fill, c->st.ord, c->st.tag, c->st.map,
                  c->ring_entries, c->ring_state, c->ring_seg, c->ring_cap, c->worker_of_set,
-                 c->stats, c->done, c->err, c->probe_sink, c->probe_dst};
+                 c->stats, c->sel_counts, c->done, c->err, c->probe_sink, c->probe_dst};
   for (void* p : dev)
     if (p) (void)hipFree(p);
   if (c->host) (void)hipHostFree(c->host);
@@ -317,6 +318,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   TRY(dalloc(&c->ring_cap, W));
   TRY(dalloc(&c->worker_of_set, g.n_sets));
   TRY(dalloc(&c->stats, kStatCount));
+  TRY(dalloc(&c->sel_counts, (size_t)kSelCounters * kSelStride));
   TRY(dalloc(&c->done, 1));
   TRY(dalloc(&c->err, 1));
 #define HIPT(x)                                                                        \
@@ -332,6 +334,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   HIPT(hipMemcpy(c->worker_of_set, wos.data(), (size_t)g.n_sets * 4, hipMemcpyHostToDevice));
   HIPT(hipMemset(c->ring_state, 0, W * 8));
   HIPT(hipMemset(c->stats, 0, kStatCount * 8));
+  HIPT(hipMemset(c->sel_counts, 0, (size_t)kSelCounters * kSelStride * 8));
   HIPT(hipMemset(c->done, 0, 4));
   HIPT(hipMemset(c->err, 0, 4));
   HIPT(hipMemset(c->pool, 0, nslots * g.bb));
@@ -460,11 +463,11 @@ int ferry_bookkeep_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const uint32_t
   const dim3 grid((nsets + wpb - 1) / wpb), block(64 * wpb);
   if (ctx->cfg.lru_mode == FERRY_LRU_SERIAL)
     hipLaunchKernelGGL(k_lru_step<true>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
-                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->stats,
+                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->sel_counts,
                        ctx->err);
   else
     hipLaunchKernelGGL(k_lru_step<false>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
-                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->stats,
+                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->sel_counts,
                        ctx->err);
   HIPC(hipGetLastError());
   if (l0 + nl == g.L) ctx->steps++;
@@ -653,12 +656,16 @@ int ferry_stats_get(ferry_ctx* ctx, ferry_stats* out) {
   HIPC(hipSetDevice(ctx->device));
   HIPC(hipDeviceSynchronize());
   unsigned long long s[kStatCount];
+  std::vector<unsigned long long> sc((size_t)kSelCounters * kSelStride);
   int err = 0;
   HIPC(hipMemcpy(s, ctx->stats, sizeof(s), hipMemcpyDeviceToHost));
+  HIPC(hipMemcpy(sc.data(), ctx->sel_counts, sc.size() * 8, hipMemcpyDeviceToHost));
+  unsigned long long nsel = 0;
+  for (int i = 0; i < kSelCounters; ++i) nsel += sc[(size_t)i * kSelStride];
   HIPC(hipMemcpy(&err, ctx->err, 4, hipMemcpyDeviceToHost));
   std::memset(out, 0, sizeof(*out));
   out->steps = ctx->steps;
-  out->selections = s[kStatSel];
+  out->selections = nsel;
   out->misses = s[kStatMisses];
   out->fetched_bytes = s[kStatBytes];
   out->steals = s[kStatSteals];
@@ -673,6 +680,7 @@ int ferry_stats_reset(ferry_ctx* ctx) {
   HIPC(hipSetDevice(ctx->device));
   HIPC(hipDeviceSynchronize());
   HIPC(hipMemset(ctx->stats, 0, kStatCount * 8));
+  HIPC(hipMemset(ctx->sel_counts, 0, (size_t)kSelCounters * kSelStride * 8));
   HIPC(hipMemset(ctx->err, 0, 4));
   ctx->steps = 0;
   return FERRY_OK;
