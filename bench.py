@@ -289,6 +289,31 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     r1.record(stream)
     torch.cuda.synchronize()
     t_attn_rep = r0.elapsed_time(r1) / a.steps
+    # top-k selection (Quest bound) over every request's whole context, the
+    # step upstream of the miss queue: one launch reads the K summary of every
+    # context block of every (request, layer, kv head)
+    select = None
+    if w["group"] == 1:
+        # one summary record per (set, block): no two blocks share one, so no
+        # summary read is served by another block's cache line
+        hb = a.host_blocks
+        ex.summaries_build(-(-ex.n_sets * sg.max_blocks // hb) * hb, stream)
+        dctx = torch.from_numpy(np.ascontiguousarray(ctx, np.int32)).to(dev)
+        tsel = torch.empty_like(sels[0])
+        ex.select_topk(qs[0], dctx, tsel, stream=stream)
+        es0, es1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        es0.record(stream)
+        for i in range(a.steps):
+            ex.select_topk(qs[i & 1], dctx, tsel, stream=stream)
+        es1.record(stream)
+        torch.cuda.synchronize()
+        t_sel = es0.elapsed_time(es1) / a.steps
+        rec = 2 * 128 * F.ESIZE[dtype] + (4 if dtype == F.FP8 else 0)
+        sel_bytes = int(ctx.sum()) * L * H * rec + B * L * Hq * 128 * 4 + B * L * H * k * 4
+        select = {"bound": "hbm", "kernel": f"k_select_topk<{w['dtype']},{Hq // H}>",
+                  "ms": round(t_sel, 4), "context_blocks_per_launch": int(ctx.sum()) * L * H,
+                  "achieved": round(sel_bytes / (t_sel * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                  "unit": "GB/s", "frac": round(sel_bytes / (t_sel * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     # ceilings: plain reads of the same bytes (attention slots; host-tier blocks)
     _, _, gather_gbs = ex.bw_probe(F.PROBE_HBM_GATHER, B * L * H, slots=bufs["slots"],
                                    iters=max(3, a.steps // 2), stream=stream)
@@ -330,6 +355,7 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
                            "unit": "GB/s", "frac": round(link_gbs / LINK_PEAK_GBS, 4),
                            "plain_read_gbs": round(hread_gbs, 2), "dma_copy_gbs": round(hdma_gbs, 2),
                            "frac_of_plain_read": round(link_gbs / hread_gbs, 4)},
+        "roofline_select": select,
         "steals_per_step": round((st2["steals"] - s0) / a.steps, 1),
         "selection_gen_s": round(gen_s, 2),
         "config_extra": {"slots_per_set": C, "host_tier_blocks": a.host_blocks,
@@ -549,7 +575,7 @@ def main():
     }
     for key in ("miss_rate", "miss_blocks_per_s", "miss_blocks_per_s_fetch_kernel",
                 "attention_tok_per_s", "kernel_ms", "roofline", "roofline_fetch",
-                "steals_per_step", "selection_gen_s", "cpu_baseline"):
+                "roofline_select", "steals_per_step", "selection_gen_s", "cpu_baseline"):
         if key in r:
             res[key] = r[key]
     print(json.dumps(res), flush=True)

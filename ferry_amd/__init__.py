@@ -29,7 +29,7 @@ __all__ = [
     "ctx_uniform", "arrivals", "lib", "LIB_PATH", "F32", "F16", "BF16", "FP8", "LRU_STEP",
     "LRU_SERIAL", "ASSIGN_SPREAD", "ASSIGN_AFFINITY", "ATTN_AUTO", "ATTN_VALU", "ATTN_MFMA",
     "MISS_DTYPE", "EMPTY", "ARRIVAL_STEADY", "ARRIVAL_BURSTY", "ARRIVAL_POISSON", "ARRIVAL_MMPP",
-    "SCHED_FIFO", "SCHED_PINNED", "trace_load",
+    "SCHED_FIFO", "SCHED_PINNED", "trace_load", "TOPK_PER_HEAD", "TOPK_LAYER_MAX",
 ]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libferry_amd.so")
@@ -46,6 +46,7 @@ PROBE_HBM_GATHER, PROBE_HOST_READ, PROBE_HOST_DMA = 0, 1, 2
 ARRIVAL_STEADY, ARRIVAL_BURSTY, ARRIVAL_POISSON, ARRIVAL_MMPP = 0, 1, 2, 3
 EMPTY = 0xFFFFFFFF  # selection id of an empty position (and its slot)
 SCHED_FIFO, SCHED_PINNED = 0, 1
+TOPK_PER_HEAD, TOPK_LAYER_MAX = 0, 1
 ESIZE = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 MISS_DTYPE = np.dtype([("block", "<u4"), ("slot", "<u4"), ("evicted", "<u4"), ("set", "<u4")])
 
@@ -121,6 +122,10 @@ _PROTOS = {
                                  C.c_uint64, _vp]),
     "ferry_sched_create": (C.c_int, [_i32, _i32, C.c_uint32, _vp, _vp, C.POINTER(_vp)]),
     "ferry_trace_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(TraceInfo), _vp, C.c_uint64]),
+    "ferry_summaries_build": (C.c_int, [_vp, C.c_uint64, _vp]),
+    "ferry_summaries_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(C.c_uint64)]),
+    "ferry_select_topk": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp, _vp]),
+    "ferry_select_topk_layers": (C.c_int, [_vp, _i32, _i32, _vp, _vp, C.c_int, _vp, _vp]),
     "ferry_sched_destroy": (C.c_int, [_vp]),
     "ferry_sched_tick": (C.c_int, [_vp, C.c_double, _vp, _vp, _vp, C.POINTER(_i32), _vp,
                                    C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32)]),
@@ -262,6 +267,38 @@ class Executor:
     def sparse_decode(self, q, slots, out, stream=None):
         _check(lib.ferry_sparse_decode(self._h, _ptr(q), _ptr(slots), _ptr(out), _stream(stream)),
                "ferry_sparse_decode")
+
+    def summaries_build(self, n_records=0, stream=None):
+        """K min/max summaries for select_topk: n_records records (a multiple of
+        the host tier's blocks; 0 = one per host-tier block)."""
+        _check(lib.ferry_summaries_build(self._h, n_records, _stream(stream)),
+               "ferry_summaries_build")
+
+    def summaries_array(self):
+        """Device summaries copied to host: uint8 [records, 2*128*esize] and
+        fp8 K scales [records] (or None)."""
+        p, sc, n = _vp(), _vp(), C.c_uint64()
+        _check(lib.ferry_summaries_view(self._h, C.byref(p), C.byref(sc), C.byref(n)),
+               "ferry_summaries_view")
+        hb = n.value
+        rec = 2 * 128 * ESIZE[self.cfg.dtype]
+        sums = _gather_d2h(p.value, hb * rec, [0]).reshape(hb, rec)
+        scales = None
+        if sc.value:
+            scales = _gather_d2h(sc.value, hb * 4, [0]).view(np.float32).reshape(hb)
+        return sums, scales
+
+    def select_topk(self, q, ctx_blocks, sel, mode=TOPK_PER_HEAD, stream=None, layers=None):
+        """Top-k blocks of every (request, layer, kv head) from q (device
+        tensors: q [B,L,Hq,128] fp32, ctx_blocks [B] int32, sel out [B,L,Hkv,k])."""
+        if layers is None:
+            _check(lib.ferry_select_topk(self._h, _ptr(q), _ptr(ctx_blocks), mode, _ptr(sel),
+                                         _stream(stream)), "ferry_select_topk")
+        else:
+            l0, nl = layers
+            _check(lib.ferry_select_topk_layers(self._h, l0, nl, _ptr(q), _ptr(ctx_blocks), mode,
+                                                _ptr(sel), _stream(stream)),
+                   "ferry_select_topk_layers")
 
     def sets_reset(self, stream=None):
         _check(lib.ferry_sets_reset(self._h, _stream(stream)), "ferry_sets_reset")

@@ -81,4 +81,16 @@ __global__ void k_probe_host(const uint8_t* host, uint64_t bb, uint64_t n_blocks
 __global__ void k_hosttier_fill(Geo g, uint8_t* host, float* scales, uint64_t seed, float mult,
                                 float mult8, float scale_base);
 
+// Top-k block selection (select.hip): per-host-block K min/max summaries and
+// the Quest-bound scoring + radix top-k kernel.
+template <int DT>
+__global__ void k_summaries_build(Geo g, const uint8_t* host, const float* host_scales, uint8_t* sums,
+                                  float* sum_scales);
+__global__ void k_summaries_tile(uint8_t* sums, float* scales, uint64_t host_blocks, uint64_t total,
+                                 uint32_t rec);
+template <int DT, int G, bool LAYER, int W>
+__global__ void k_select_topk(Geo g, const float* q, const int32_t* ctx_blocks, const uint8_t* sums,
+                              const float* sum_scales, uint64_t sum_mod, uint32_t* sel, int l0, int nl,
+                              int max_n, int* err);
+
 }  // namespace ferry_amd

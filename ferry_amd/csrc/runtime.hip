@@ -86,6 +86,9 @@ struct ferry_ctx {
   size_t probe_sink_words = 0;
   uint8_t* probe_dst = nullptr;    // bandwidth probes: DMA destination
   size_t probe_dst_bytes = 0;
+  uint8_t* sums = nullptr;         // top-k selection: K min/max records [sum_blocks][2][D]
+  float* sum_scales = nullptr;     // ... and their K scales (fp8)
+  uint64_t sum_blocks = 0;         // records; block (set, b) uses (set*max_blocks + b) mod this
 
   Ring ring() const {
     Ring r;
@@ -137,7 +140,8 @@ void release(ferry_ctx* c) {
   (void)hipSetDevice(c->device);
   void* dev[] = {c->pool, c->pool_scales, c->st.fill, c->st.ord, c->st.tag, c->st.map,
                  c->ring_entries, c->ring_state, c->ring_seg, c->ring_cap, c->worker_of_set,
-                 c->stats, c->sel_counts, c->done, c->err, c->probe_sink, c->probe_dst};
+                 c->stats, c->sel_counts, c->done, c->err, c->probe_sink, c->probe_dst,
+                 c->sums, c->sum_scales};
   for (void* p : dev)
     if (p) (void)hipFree(p);
   if (c->host) (void)hipHostFree(c->host);
@@ -576,6 +580,143 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
     if ((rc = ferry_sparse_decode_layers(ctx, l0, nl, q, slots, out, ms))) return rc;
   }
   return FERRY_OK;
+}
+
+int ferry_summaries_build(ferry_ctx* ctx, uint64_t n_records, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  const Geo& g = ctx->g;
+  const uint64_t S = n_records ? n_records : g.host_blocks;
+  if (S % g.host_blocks)
+    return fail(FERRY_EINVAL, "summary records must be a multiple of the host tier's blocks");
+  const uint64_t rec = 2ull * g.D * g.esize;
+  HIPC(hipSetDevice(ctx->device));
+  if (ctx->sums && ctx->sum_blocks != S) {
+    HIPC(hipDeviceSynchronize());
+    HIPC(hipFree(ctx->sums));
+    if (ctx->sum_scales) HIPC(hipFree(ctx->sum_scales));
+    ctx->sums = nullptr;
+    ctx->sum_scales = nullptr;
+    ctx->sum_blocks = 0;
+  }
+  if (!ctx->sums) {
+    HIPC(hipMalloc(&ctx->sums, S * rec));
+    if (g.dtype == FERRY_FP8_E4M3) HIPC(hipMalloc(&ctx->sum_scales, S * 4ull));
+    ctx->sum_blocks = S;
+  }
+  const unsigned blocks = (unsigned)std::min<uint64_t>((g.host_blocks + 3) / 4, 16384);
+  hipStream_t s = (hipStream_t)stream;
+  switch (g.dtype) {
+    case FERRY_F32:
+      hipLaunchKernelGGL(k_summaries_build<FERRY_F32>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev,
+                         ctx->host_scales_dev, ctx->sums, ctx->sum_scales);
+      break;
+    case FERRY_F16:
+      hipLaunchKernelGGL(k_summaries_build<FERRY_F16>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev,
+                         ctx->host_scales_dev, ctx->sums, ctx->sum_scales);
+      break;
+    case FERRY_BF16:
+      hipLaunchKernelGGL(k_summaries_build<FERRY_BF16>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev,
+                         ctx->host_scales_dev, ctx->sums, ctx->sum_scales);
+      break;
+    default:
+      hipLaunchKernelGGL(k_summaries_build<FERRY_FP8_E4M3>, dim3(blocks), dim3(256), 0, s, g,
+                         ctx->host_dev, ctx->host_scales_dev, ctx->sums, ctx->sum_scales);
+  }
+  HIPC(hipGetLastError());
+  if (S > g.host_blocks) {
+    hipLaunchKernelGGL(k_summaries_tile, dim3(8192), dim3(256), 0, s, ctx->sums, ctx->sum_scales,
+                       g.host_blocks, S, (uint32_t)rec);
+    HIPC(hipGetLastError());
+  }
+  return FERRY_OK;
+}
+
+int ferry_summaries_view(ferry_ctx* ctx, void** sums, float** scales, uint64_t* n_records) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (sums) *sums = ctx->sums;
+  if (scales) *scales = ctx->sum_scales;
+  if (n_records) *n_records = ctx->sum_blocks;
+  return FERRY_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+struct SelArgs {
+  Geo g;
+  const float* q;
+  const int32_t* ctx_blocks;
+  const uint8_t* sums;
+  const float* sum_scales;
+  uint64_t sum_mod;
+  uint32_t* sel;
+  int l0, nl, max_n;
+  int* err;
+};
+
+template <int DT, int G, bool LAYER>
+void launch_sel(const dim3& grid, size_t lds, hipStream_t s, const SelArgs& a) {
+  hipLaunchKernelGGL((k_select_topk<DT, G, LAYER, 4>), grid, dim3(256), lds, s, a.g, a.q, a.ctx_blocks,
+                     a.sums, a.sum_scales, a.sum_mod, a.sel, a.l0, a.nl, a.max_n, a.err);
+}
+template <int DT, bool LAYER>
+void launch_sel_g(int G, const dim3& grid, size_t lds, hipStream_t s, const SelArgs& a) {
+  switch (G) {
+    case 1: launch_sel<DT, 1, LAYER>(grid, lds, s, a); return;
+    case 2: launch_sel<DT, 2, LAYER>(grid, lds, s, a); return;
+    case 4: launch_sel<DT, 4, LAYER>(grid, lds, s, a); return;
+    default: launch_sel<DT, 8, LAYER>(grid, lds, s, a); return;
+  }
+}
+template <bool LAYER>
+void launch_sel_dt(int dtype, int G, const dim3& grid, size_t lds, hipStream_t s, const SelArgs& a) {
+  switch (dtype) {
+    case FERRY_F32: launch_sel_g<FERRY_F32, LAYER>(G, grid, lds, s, a); return;
+    case FERRY_F16: launch_sel_g<FERRY_F16, LAYER>(G, grid, lds, s, a); return;
+    case FERRY_BF16: launch_sel_g<FERRY_BF16, LAYER>(G, grid, lds, s, a); return;
+    default: launch_sel_g<FERRY_FP8_E4M3, LAYER>(G, grid, lds, s, a); return;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ferry_select_topk_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
+                             const int32_t* ctx_blocks, int mode, uint32_t* sel, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!q || !ctx_blocks || !sel) return fail(FERRY_EINVAL, "null buffer");
+  const Geo& g = ctx->g;
+  if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
+  if (mode != FERRY_TOPK_PER_HEAD && mode != FERRY_TOPK_LAYER_MAX) return fail(FERRY_EINVAL, "bad mode");
+  if (g.group != 1)
+    return fail(FERRY_EINVAL, "top-k selection needs private sets (group 1): a group's members select "
+                              "from their own contexts");
+  if (!ctx->sums) return fail(FERRY_EINVAL, "block summaries not built (ferry_summaries_build)");
+  const bool layer = mode == FERRY_TOPK_LAYER_MAX;
+  const int G = g.Hq / g.Hkv;
+  const int Gq = layer ? g.Hq : G;
+  const size_t lds = ((size_t)Gq * g.D + (size_t)g.max_blocks) * 4;
+  if (lds > 65536)
+    return fail(FERRY_EINVAL, "max_blocks (plus the query heads of a row) exceed the selection's 64 KiB "
+                              "of LDS");
+  HIPC(hipSetDevice(ctx->device));
+  const dim3 grid((unsigned)((size_t)g.n_req * nl * (layer ? 1 : g.Hkv)));
+  const SelArgs a{g,   q,   ctx_blocks,    ctx->sums, ctx->sum_scales, ctx->sum_blocks,
+                  sel, l0,  nl,            g.max_blocks, ctx->err};
+  if (layer)
+    launch_sel_dt<true>(g.dtype, G, grid, lds, (hipStream_t)stream, a);
+  else
+    launch_sel_dt<false>(g.dtype, G, grid, lds, (hipStream_t)stream, a);
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_select_topk(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks, int mode, uint32_t* sel,
+                      void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  return ferry_select_topk_layers(ctx, 0, ctx->g.L, q, ctx_blocks, mode, sel, stream);
 }
 
 int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, int iters,

@@ -1,0 +1,382 @@
+// select.hip -- on-device top-k block selection (Quest bound) feeding the
+// miss queue.
+//
+// The reference selects pages on the host side of a model hook
+// (tools/capture_miss_trace.py:139-159): per page and KV head, the
+// elementwise min and max of K over the page's tokens; per query head, the
+// bound sum_d max(q_d * kmax_d, q_d * kmin_d) (an upper bound of q.k over the
+// page); max over the query heads of a KV head; top-k pages, returned in
+// ascending page order.  Its per-layer variant takes the max over every head
+// of the layer and shares one selection (FERRY_TOPK_LAYER_MAX).  A page is
+// one 16-token block here, and a context shorter than k selects all of its
+// blocks (min(k, n_pages), :157-158), padding the row with FERRY_EMPTY.
+//
+// Block summaries live in HBM: record i holds the min and max of a K tile per
+// dim, in the KV element type (fp8: E4M3 codes, the block's K scale kept
+// beside them and applied to the bound).  Block (set, b) uses record
+// (set * max_blocks + b) mod S.  S is a multiple of the host tier's size, so
+// blocks that share a record share their host-tier content: S = host_blocks
+// is the smallest table, S >= sets * max_blocks gives every block its own
+// record, as a serving system that summarises each written page has.
+//
+// Since kmax >= kmin, max(q kmax, q kmin) = q * (q >= 0 ? kmax : kmin): which
+// of the two a dim uses is fixed by the sign of q for the whole row, so the
+// bound costs one select and one fused multiply-add per (head, dim).
+// Every fp32 operation has a fixed order so the selection is bit-exact
+// against the CPU oracle: lane p of a block's 16 lanes accumulates dims
+// 8p..8p+7 left to right with fma (acc = fma(q_d, k_d, acc), acc = 0 first);
+// the 16 partial sums are combined by an xor butterfly (8, 4, 2, 1); max is
+// `a > b ? a : b`; keys are the order-preserving map of the float bits (so
+// -0 < +0), and equal keys go to the lower block id.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ferry_amd {
+
+namespace {
+
+template <int DT>
+__device__ inline uint32_t elem_bits(const uint8_t* p, int i) {
+  if constexpr (DT == FERRY_F32) return reinterpret_cast<const uint32_t*>(p)[i];
+  else if constexpr (DT == FERRY_FP8_E4M3) return p[i];
+  else return reinterpret_cast<const uint16_t*>(p)[i];
+}
+
+// Exact decode of one stored element.
+template <int DT>
+__device__ inline float elem_f32(uint32_t v) {
+  if constexpr (DT == FERRY_F32) {
+    return bits_f32(v);
+  } else if constexpr (DT == FERRY_F16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)v);
+  } else if constexpr (DT == FERRY_BF16) {
+    return bits_f32(v << 16);
+  } else {  // OCP E4M3FN: (-1)^s 2^(e-7) (1 + m/8), subnormal m 2^-9
+    const uint32_t s = (v & 0x80u) << 24, e = (v >> 3) & 0xFu, m = v & 7u;
+    if (e == 0) return bits_f32(f32_bits((float)m * 0.001953125f) | s);
+    return bits_f32(s | ((e + 120u) << 23) | (m << 20));
+  }
+}
+
+// The 8 elements [i0, i0 + 8) of a summary record, widened exactly to fp32,
+// with one vector load (16 B for 16-bit elements, 8 B fp8, 2 x 16 B fp32).
+template <int DT>
+__device__ inline void load8(const uint8_t* rec, int i0, float* f) {
+  if constexpr (DT == FERRY_F32) {
+    const uint4 a = *reinterpret_cast<const uint4*>(rec + 4 * i0);
+    const uint4 b = *reinterpret_cast<const uint4*>(rec + 4 * i0 + 16);
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = bits_f32(w[e]);
+  } else if constexpr (DT == FERRY_FP8_E4M3) {
+    const uint2 a = *reinterpret_cast<const uint2*>(rec + i0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = elem_f32<DT>(((e < 4 ? a.x : a.y) >> (8 * (e & 3))) & 0xFFu);
+  } else {
+    const uint4 a = *reinterpret_cast<const uint4*>(rec + 2 * i0);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = elem_f32<DT>((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+  }
+}
+
+__device__ inline float fmax_det(float a, float b) { return a > b ? a : b; }
+
+// order-preserving map of float bits to unsigned keys
+__device__ inline uint32_t fkey(float x) {
+  const uint32_t u = f32_bits(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// sum over the 16 lanes of a row: xor 8, 4, 2, 1 (ds_swizzle bitmask mode)
+__device__ inline float row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), (8 << 10) | 0x1F));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), (4 << 10) | 0x1F));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), (2 << 10) | 0x1F));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), (1 << 10) | 0x1F));
+  return v;
+}
+
+// Inclusive scan of (a, b) over the NT threads of the workgroup; wtot is LDS
+// scratch of 2*W words.  Returns the exclusive prefixes.
+template <int W>
+__device__ inline void block_excl_scan2(uint32_t a, uint32_t b, uint32_t* wtot, uint32_t& ea,
+                                        uint32_t& eb) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t ia = a, ib = b;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t oa = __shfl_up(ia, off), ob = __shfl_up(ib, off);
+    if (lane >= off) {
+      ia += oa;
+      ib += ob;
+    }
+  }
+  if (lane == 63) {
+    wtot[wave] = ia;
+    wtot[W + wave] = ib;
+  }
+  __syncthreads();
+  uint32_t pa = 0, pb = 0;
+  for (int w = 0; w < wave; ++w) {
+    pa += wtot[w];
+    pb += wtot[W + w];
+  }
+  ea = pa + ia - a;
+  eb = pb + ib - b;
+}
+
+}  // namespace
+
+// One wavefront per host-tier block: min and max over the 16 tokens of every
+// K dim (lane l: dims 2l, 2l+1), stored as the element that attains them;
+// the first of equal values (token order) is kept.
+template <int DT>
+__global__ __launch_bounds__(256) void k_summaries_build(Geo g, const uint8_t* __restrict__ host,
+                                                         const float* __restrict__ host_scales,
+                                                         uint8_t* __restrict__ sums,
+                                                         float* __restrict__ sum_scales) {
+  constexpr int ES = DT == FERRY_F32 ? 4 : (DT == FERRY_FP8_E4M3 ? 1 : 2);
+  constexpr int D = 128;
+  const int lane = threadIdx.x & 63;
+  const uint64_t waves = (uint64_t)gridDim.x * (blockDim.x >> 6);
+  for (uint64_t h = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); h < g.host_blocks;
+       h += waves) {
+    const uint8_t* kt = host + h * g.bb;
+    uint8_t* out = sums + h * (uint64_t)(2 * D * ES);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int d = 2 * lane + c;
+      uint32_t bmin = elem_bits<DT>(kt, d), bmax = bmin;
+      float fmin = elem_f32<DT>(bmin), fmax = fmin;
+      for (int t = 1; t < 16; ++t) {
+        const uint32_t b = elem_bits<DT>(kt, t * D + d);
+        const float f = elem_f32<DT>(b);
+        if (f < fmin) {
+          fmin = f;
+          bmin = b;
+        }
+        if (f > fmax) {
+          fmax = f;
+          bmax = b;
+        }
+      }
+      if constexpr (ES == 4) {
+        reinterpret_cast<uint32_t*>(out)[d] = bmin;
+        reinterpret_cast<uint32_t*>(out)[D + d] = bmax;
+      } else if constexpr (ES == 2) {
+        reinterpret_cast<uint16_t*>(out)[d] = (uint16_t)bmin;
+        reinterpret_cast<uint16_t*>(out)[D + d] = (uint16_t)bmax;
+      } else {
+        out[d] = (uint8_t)bmin;
+        out[D + d] = (uint8_t)bmax;
+      }
+    }
+    if (DT == FERRY_FP8_E4M3 && lane == 0) sum_scales[h] = host_scales[2 * h];
+  }
+}
+
+// Records [host_blocks, S) repeat records [0, host_blocks): record i is the
+// summary of host block i mod host_blocks (16-byte copies, scales too).
+__global__ __launch_bounds__(256) void k_summaries_tile(uint8_t* __restrict__ sums, float* __restrict__ scales,
+                                                        uint64_t host_blocks, uint64_t total, uint32_t rec) {
+  const uint64_t words = (uint64_t)rec / 16;
+  const uint64_t n = (total - host_blocks) * words;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  uint4* dst = reinterpret_cast<uint4*>(sums + host_blocks * rec);
+  const uint4* src = reinterpret_cast<const uint4*>(sums);
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint64_t r = i / words, w = i % words;
+    dst[i] = src[((host_blocks + r) % host_blocks) * words + w];
+  }
+  if (scales)
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total - host_blocks; i += stride)
+      scales[host_blocks + i] = scales[(host_blocks + i) % host_blocks];
+}
+
+// One workgroup (W wavefronts) per (request, layer, kv head) row, or per
+// (request, layer) with LAYER.  Phase 1 scores every block of the request's
+// context into LDS keys (16 lanes per block, 4 blocks per wavefront pass);
+// phase 2 finds the k-th largest key by 4 radix passes of 8 bits; phase 3
+// writes the selected block ids in ascending order (ties to lower ids).
+// Dynamic LDS: q[Gq][128] floats, then keys[max_n].
+template <int DT, int G, bool LAYER, int W>
+__global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __restrict__ q,
+                                                        const int32_t* __restrict__ ctx_blocks,
+                                                        const uint8_t* __restrict__ sums,
+                                                        const float* __restrict__ sum_scales,
+                                                        uint64_t sum_mod, uint32_t* __restrict__ sel,
+                                                        int l0, int nl, int max_n,
+                                                        int* __restrict__ err) {
+  constexpr int ES = DT == FERRY_F32 ? 4 : (DT == FERRY_FP8_E4M3 ? 1 : 2);
+  constexpr int D = 128, NT = W * 64;
+  constexpr uint32_t REC = 2 * D * ES;  // summary bytes per block
+  extern __shared__ uint32_t lds[];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wtot[2 * W];
+  __shared__ uint32_t sh_prefix, sh_need;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nkv = LAYER ? g.Hkv : 1;  // kv heads scored per row
+  const int Gq = G * nkv;             // query heads per row
+  float* qs = reinterpret_cast<float*>(lds);
+  uint32_t* keys = lds + Gq * D;
+
+  const int hrow = LAYER ? 0 : blockIdx.x % g.Hkv;
+  const int rl_idx = LAYER ? blockIdx.x : blockIdx.x / g.Hkv;  // (request, layer in range)
+  const int r = rl_idx / nl, l = l0 + rl_idx % nl;
+  const int rl = r * g.L + l;
+  int n = ctx_blocks[r];
+  if (n < 0) n = 0;
+  if (n > max_n || n > g.max_blocks) {
+    if (tid == 0) set_error(err, FERRY_ERANGE);
+    n = 0;
+  }
+  const int k = g.k;
+  const int kk = n < k ? n : k;
+  auto out_row = [&](int hh) { return sel + ((size_t)rl * g.Hkv + hh) * (size_t)k; };
+
+  if (n > k) {
+    // ---- phase 1: scores
+    const int grp = lane >> 4, p = lane & 15;
+    // the row's query dims of this lane (8 per head), and whether each uses kmax
+    float qr[G][8];
+    if (!LAYER) {
+#pragma unroll
+      for (int gq = 0; gq < G; ++gq)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          qr[gq][e] = q[((size_t)rl * g.Hq + (size_t)(hrow * G + gq)) * D + 8 * p + e];
+    } else {
+      for (int i = tid; i < Gq * D; i += NT) qs[i] = q[(size_t)rl * g.Hq * D + i];
+      __syncthreads();
+    }
+    for (int b0 = 4 * wave; b0 < n; b0 += 4 * W) {
+      const int b = b0 + grp;
+      const bool live = b < n;
+      float score = 0.0f;
+      for (int hh = 0; hh < nkv; ++hh) {
+        const int hk = LAYER ? hh : hrow;
+        const uint64_t set = (uint64_t)rl * g.Hkv + hk;
+        const uint64_t hb = host_index(set, live ? (uint32_t)b : 0u, (uint64_t)g.max_blocks, sum_mod);
+        const uint8_t* rec = sums + hb * REC;
+        float kmn[8], kmx[8];
+        load8<DT>(rec, 8 * p, kmn);
+        load8<DT>(rec, D + 8 * p, kmx);
+        if (LAYER) {
+#pragma unroll
+          for (int gq = 0; gq < G; ++gq)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qr[gq][e] = qs[(hh * G + gq) * D + 8 * p + e];
+        }
+        float sk = 0.0f;
+#pragma unroll
+        for (int gq = 0; gq < G; ++gq) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            acc = __fmaf_rn(qr[gq][e], qr[gq][e] >= 0.0f ? kmx[e] : kmn[e], acc);
+          const float bound = row16_sum(acc);
+          sk = gq == 0 ? bound : fmax_det(bound, sk);
+        }
+        if constexpr (DT == FERRY_FP8_E4M3) sk = __fmul_rn(sk, sum_scales[hb]);
+        score = hh == 0 ? sk : fmax_det(sk, score);
+      }
+      if (live && p == 0) keys[b] = fkey(score);
+    }
+    __syncthreads();
+    // ---- phase 2: the kk-th largest key (radix select, 8 bits per pass)
+    uint32_t prefix = 0, mask = 0, need = (uint32_t)kk;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int i = tid; i < 256; i += NT) hist[i] = 0;
+      __syncthreads();
+      for (int i = tid; i < n; i += NT) {
+        const uint32_t key = keys[i];
+        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 0xFFu], 1u);
+      }
+      __syncthreads();
+      if (wave == 0) {
+        uint32_t c[4], sum = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          c[e] = hist[255 - 4 * lane - e];
+          sum += c[e];
+        }
+        uint32_t incl = sum;
+        for (int off = 1; off < 64; off <<= 1) {
+          const uint32_t o = __shfl_up(incl, off);
+          if (lane >= off) incl += o;
+        }
+        const uint32_t excl = incl - sum;
+        if (excl < need && incl >= need) {
+          uint32_t acc = excl;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (acc + c[e] >= need && acc < need) {
+              sh_prefix = prefix | ((uint32_t)(255 - 4 * lane - e) << shift);
+              sh_need = need - acc;
+            }
+            acc += c[e];
+          }
+        }
+      }
+      __syncthreads();
+      prefix = sh_prefix;
+      need = sh_need;
+      mask |= 0xFFu << shift;
+    }
+    // ---- phase 3: keys above the threshold, then the lowest-id ties, in id order
+    const uint32_t T = prefix;
+    const int chunk = (n + NT - 1) / NT;
+    const int c0 = tid * chunk, c1 = min(n, c0 + chunk);
+    uint32_t gt = 0, eq = 0;
+    for (int i = c0; i < c1; ++i) {
+      const uint32_t key = keys[i];
+      gt += key > T;
+      eq += key == T;
+    }
+    uint32_t gt_before, eq_before;
+    block_excl_scan2<W>(gt, eq, wtot, gt_before, eq_before);
+    uint32_t pos = gt_before + min(eq_before, need), ties = eq_before;
+    for (int i = c0; i < c1; ++i) {
+      const uint32_t key = keys[i];
+      bool take = key > T;
+      if (key == T) take = ties++ < need;
+      if (take) {
+        for (int hh = 0; hh < (LAYER ? g.Hkv : 1); ++hh) out_row(LAYER ? hh : hrow)[pos] = (uint32_t)i;
+        ++pos;
+      }
+    }
+  } else {
+    // a context of at most k blocks: every block, in order
+    for (int j = tid; j < kk; j += NT)
+      for (int hh = 0; hh < (LAYER ? g.Hkv : 1); ++hh) out_row(LAYER ? hh : hrow)[j] = (uint32_t)j;
+  }
+  for (int j = kk + tid; j < k; j += NT)
+    for (int hh = 0; hh < (LAYER ? g.Hkv : 1); ++hh) out_row(LAYER ? hh : hrow)[j] = kNone;
+}
+
+#define FERRY_SUMS_INST(DT)                                                                 \
+  template __global__ void k_summaries_build<DT>(Geo, const uint8_t*, const float*, uint8_t*, \
+                                                 float*);
+FERRY_SUMS_INST(FERRY_F32)
+FERRY_SUMS_INST(FERRY_F16)
+FERRY_SUMS_INST(FERRY_BF16)
+FERRY_SUMS_INST(FERRY_FP8_E4M3)
+
+#define FERRY_SEL_INST(DT, G, LAYER)                                                           \
+  template __global__ void k_select_topk<DT, G, LAYER, 4>(Geo, const float*, const int32_t*,     \
+                                                          const uint8_t*, const float*, uint64_t,  \
+                                                          uint32_t*, int, int, int, int*);
+#define FERRY_SEL_INST_G(DT, LAYER) \
+  FERRY_SEL_INST(DT, 1, LAYER)      \
+  FERRY_SEL_INST(DT, 2, LAYER)      \
+  FERRY_SEL_INST(DT, 4, LAYER)      \
+  FERRY_SEL_INST(DT, 8, LAYER)
+#define FERRY_SEL_INST_ALL(LAYER)          \
+  FERRY_SEL_INST_G(FERRY_F32, LAYER)       \
+  FERRY_SEL_INST_G(FERRY_F16, LAYER)       \
+  FERRY_SEL_INST_G(FERRY_BF16, LAYER)      \
+  FERRY_SEL_INST_G(FERRY_FP8_E4M3, LAYER)
+FERRY_SEL_INST_ALL(false)
+FERRY_SEL_INST_ALL(true)
+
+}  // namespace ferry_amd

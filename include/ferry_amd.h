@@ -221,6 +221,46 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
                       float* out, uint32_t* miss_count, ferry_miss* misses, int32_t chunks,
                       void* stream, void* side_stream);
 
+/* ---- top-k block selection (Quest bound) ----
+ * The step upstream of the miss queue: choose each request's k blocks from
+ * the query, as tools/capture_miss_trace.py:139-159 does with its "quest"
+ * method.  Per block (= page of 16 tokens) and kv head, the elementwise min
+ * and max of K over the block's tokens bound the attention score of any of
+ * its tokens: bound = sum_d max(q_d kmax_d, q_d kmin_d).  The score of a
+ * block is the max of the bound over the query heads of the kv head
+ * (FERRY_TOPK_PER_HEAD: one selection per (request, layer, kv head)), or
+ * over every head of the layer (FERRY_TOPK_LAYER_MAX: one selection per
+ * (request, layer), written to every kv head's row, as the capture tool
+ * does).  The k highest scores win, ties to the lower block id; the row is
+ * written in ascending block order.  A context of n < k blocks selects all n
+ * and pads the row with FERRY_EMPTY; n = 0 gives an empty row (a request that
+ * is not resident).  fp32 scores are computed in a fixed order, so the
+ * selection is reproducible bit for bit.
+ *
+ * ferry_summaries_build computes the K min/max of every host-tier block
+ * (reading the pinned tier once; call it again after writing the tier) into
+ * n_records records [n_records][2][head_dim] in the KV element type (fp8:
+ * E4M3 codes; the block's K scale is kept beside them and multiplies the
+ * bound).  Block (set, b) reads record (set*max_blocks + b) mod n_records.
+ * n_records must be a multiple of host_blocks (0 means host_blocks, the
+ * smallest table); n_records >= sets*max_blocks gives every block a record
+ * of its own, as a server that summarises each page it writes has, and is
+ * what the selection's memory traffic should be measured with.
+ * ferry_summaries_view returns their device pointers and record count.
+ * ferry_select_topk: q [B][L][Hq][D] fp32 (device), ctx_blocks [B] int32
+ * (device, context length of each request in blocks, <= max_blocks), sel
+ * [B][L][Hkv][k] u32 out (device) -- the input of ferry_fetch_step.  Needs
+ * group == 1 and (query heads per row * D + max_blocks) * 4 <= 64 KiB. */
+#define FERRY_TOPK_PER_HEAD 0
+#define FERRY_TOPK_LAYER_MAX 1
+int ferry_summaries_build(ferry_ctx* ctx, uint64_t n_records, void* stream);
+int ferry_summaries_view(ferry_ctx* ctx, void** sums, float** scales, uint64_t* n_records);
+int ferry_select_topk(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks, int mode,
+                      uint32_t* sel, void* stream);
+/* Selection of layers [l0, l0 + nl) only. */
+int ferry_select_topk_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
+                             const int32_t* ctx_blocks, int mode, uint32_t* sel, void* stream);
+
 /* ---- bandwidth ceilings ----
  * Plain reads of the bytes the executor's kernels move, timed with HIP events
  * on `stream` over `iters` launches after one warm-up (synchronises):

@@ -917,6 +917,157 @@ int ora_arrivals(int kind, uint32_t n, double gap, double period, double ratio,
 }
 
 /* ------------------------------------------------------------------ */
+/* top-k block selection (Quest bound)                                 */
+/* ------------------------------------------------------------------ */
+/* K min/max of host block h per dim over its tokens (the page summary of
+ * tools/capture_miss_trace.py:140-143), as decoded floats; of equal values
+ * the first in token order is kept. */
+void ora_summary(const ora_geom* g, uint64_t h, float* kmin, float* kmax) {
+  const int D = g->head_dim, T = g->block_tokens;
+  for (int d = 0; d < D; ++d) {
+    float mn = (float)ora_decode(g->dtype, ora_host_elem(g, h, (uint32_t)d)), mx = mn;
+    for (int t = 1; t < T; ++t) {
+      const float f = (float)ora_decode(g->dtype, ora_host_elem(g, h, (uint32_t)(t * D + d)));
+      if (f < mn) mn = f;
+      if (f > mx) mx = f;
+    }
+    kmin[d] = mn;
+    kmax[d] = mx;
+  }
+}
+
+static float max_det(float a, float b) { return a > b ? a : b; }
+
+/* The bound sum_d max(q_d kmax_d, q_d kmin_d) (capture_miss_trace.py:145),
+ * written q_d * (q_d >= 0 ? kmax_d : kmin_d) since kmax >= kmin, in fp32 and in
+ * one fixed order: 16 partial sums of 8 consecutive dims each, accumulated
+ * left to right with correctly rounded fma from 0, then pairs (i, i^8),
+ * (i, i^4), (i, i^2), (i, i^1). */
+static float quest_bound(const float* q, const float* kmin, const float* kmax) {
+  float s[16];
+  for (int p = 0; p < 16; ++p) {
+    float acc = 0.0f;
+    for (int e = 0; e < 8; ++e) {
+      const int d = 8 * p + e;
+      acc = fmaf(q[d], q[d] >= 0.0f ? kmax[d] : kmin[d], acc);
+    }
+    s[p] = acc;
+  }
+  for (int w = 8; w >= 1; w >>= 1) {
+    float t[16];
+    for (int i = 0; i < 16; ++i) t[i] = s[i] + s[i ^ w];
+    memcpy(s, t, sizeof s);
+  }
+  return s[0];
+}
+
+/* Score of block b for kv head h of (request r, layer l): the max of the
+ * bound over the kv head's query heads (capture_miss_trace.py:146), times the
+ * block's K scale for fp8. */
+static float head_score(const ora_geom* g, const float* q, int r, int l, int h, uint32_t b,
+                        float* kmin, float* kmax) {
+  const int L = g->n_layers, Hk = g->kv_heads, Hq = g->q_heads, D = g->head_dim;
+  const int G = Hq / Hk;
+  const uint32_t set = (uint32_t)((r * L + l) * Hk + h);
+  const uint64_t hb = ora_host_index(g, set, b);
+  ora_summary(g, hb, kmin, kmax);
+  float sc = 0.0f;
+  for (int gq = 0; gq < G; ++gq) {
+    const float* qv = q + ((size_t)(r * L + l) * Hq + (size_t)(h * G + gq)) * D;
+    const float bd = quest_bound(qv, kmin, kmax);
+    sc = gq == 0 ? bd : max_det(bd, sc);
+  }
+  if (g->dtype == ORA_FP8) sc = sc * ora_host_scale(g, hb, 0);
+  return sc;
+}
+
+int ora_quest_scores(const ora_geom* g, const float* q, const int* ctx_blocks, int mode,
+                     int stride, float* out) {
+  const int L = g->n_layers, Hk = g->kv_heads, D = g->head_dim;
+  float* kmin = (float*)malloc((size_t)D * sizeof(float));
+  float* kmax = (float*)malloc((size_t)D * sizeof(float));
+  size_t row = 0;
+  for (int r = 0; r < g->n_req; ++r)
+    for (int l = 0; l < L; ++l)
+      for (int h = 0; h < (mode ? 1 : Hk); ++h, ++row) {
+        const int n = ctx_blocks[r] < stride ? ctx_blocks[r] : stride;
+        for (int b = 0; b < n; ++b) {
+          float sc;
+          if (mode) { /* the layer's max over every head (capture_miss_trace.py:147) */
+            sc = head_score(g, q, r, l, 0, (uint32_t)b, kmin, kmax);
+            for (int hh = 1; hh < Hk; ++hh)
+              sc = max_det(head_score(g, q, r, l, hh, (uint32_t)b, kmin, kmax), sc);
+          } else {
+            sc = head_score(g, q, r, l, h, (uint32_t)b, kmin, kmax);
+          }
+          out[row * (size_t)stride + b] = sc;
+        }
+      }
+  free(kmin);
+  free(kmax);
+  return 0;
+}
+
+/* order-preserving key of a float's bits (-0 below +0) */
+static uint32_t fkey(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+typedef struct {
+  uint32_t key, id;
+} keyed;
+
+static int cmp_keyed(const void* a, const void* b) {
+  const keyed *x = (const keyed*)a, *y = (const keyed*)b;
+  if (x->key != y->key) return x->key > y->key ? -1 : 1; /* higher score first */
+  return x->id < y->id ? -1 : (x->id > y->id); /* then the lower block id */
+}
+
+/* Top-k blocks of every (request, layer, kv head) row: the min(k, n) highest
+ * scores (capture_miss_trace.py:157-158: topk(score, min(sel, n_pages))),
+ * written in ascending block order (:158 .sort()), padded with ORA_NONE.
+ * mode 1 writes one selection per (request, layer) to every kv head's row. */
+int ora_select_topk(const ora_geom* g, const float* q, const int* ctx_blocks, int mode,
+                    uint32_t* sel) {
+  const int L = g->n_layers, Hk = g->kv_heads, k = g->k;
+  int nmax = 1;
+  for (int r = 0; r < g->n_req; ++r) {
+    if (ctx_blocks[r] > g->max_blocks) return -1;
+    if (ctx_blocks[r] > nmax) nmax = ctx_blocks[r];
+  }
+  const size_t rows = (size_t)g->n_req * L * (mode ? 1 : Hk);
+  float* sc = (float*)malloc(rows * (size_t)nmax * sizeof(float));
+  keyed* kv = (keyed*)malloc((size_t)nmax * sizeof(keyed));
+  uint32_t* pick = (uint32_t*)malloc((size_t)nmax * 4);
+  ora_quest_scores(g, q, ctx_blocks, mode, nmax, sc);
+  size_t row = 0;
+  for (int r = 0; r < g->n_req; ++r)
+    for (int l = 0; l < L; ++l)
+      for (int h = 0; h < (mode ? 1 : Hk); ++h, ++row) {
+        const int n = ctx_blocks[r] > 0 ? ctx_blocks[r] : 0;
+        const int kk = n < k ? n : k;
+        for (int b = 0; b < n; ++b) {
+          kv[b].key = fkey(sc[row * (size_t)nmax + b]);
+          kv[b].id = (uint32_t)b;
+        }
+        qsort(kv, (size_t)n, sizeof(keyed), cmp_keyed);
+        for (int j = 0; j < kk; ++j) pick[j] = kv[j].id;
+        qsort(pick, (size_t)kk, 4, cmp_u32);
+        for (int hh = 0; hh < Hk; ++hh) {
+          if (!mode && hh != h) continue;
+          uint32_t* o = sel + ((size_t)(r * L + l) * Hk + hh) * k;
+          for (int j = 0; j < k; ++j) o[j] = j < kk ? pick[j] : ORA_NONE;
+        }
+      }
+  free(sc);
+  free(kv);
+  free(pick);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
 /* host tier content                                                   */
 /* ------------------------------------------------------------------ */
 /* Values are Irwin-Hall(4) sums of 16-bit uniforms from the hash, centred

@@ -212,6 +212,18 @@ float ora_host_scale(const ora_geom* g, uint64_t h, int kv);
 void ora_host_block(const ora_geom* g, uint64_t h, void* bytes, float* scales);
 double ora_decode(int dtype, uint32_t v);
 
+/* ---------------- top-k block selection ---------------- */
+/* K min/max of host block h per dim (decoded floats). */
+void ora_summary(const ora_geom* g, uint64_t h, float* kmin, float* kmax);
+/* Quest scores of blocks [0, min(ctx, stride)) of every row (mode 0: rows are
+ * (request, layer, kv head); mode 1: (request, layer), max over all heads);
+ * out[row][stride]. */
+int ora_quest_scores(const ora_geom* g, const float* q, const int* ctx_blocks, int mode,
+                     int stride, float* out);
+/* Top-k selection into sel [B][L][Hkv][k] (ascending ids, ORA_NONE padding). */
+int ora_select_topk(const ora_geom* g, const float* q, const int* ctx_blocks, int mode,
+                    uint32_t* sel);
+
 /* ---------------- attention ---------------- */
 /* fp64 block-sparse decode attention with keys read from the host tier by
  * (set, block).  q, out: [B][L][Hq][D] (q fp32, out fp64). */

@@ -129,6 +129,9 @@ _sig("ora_host_fill", None, C.POINTER(Geom), C.c_void_p, C.c_void_p)
 _sig("ora_attention_f64", C.c_int, C.POINTER(Geom), _u32p, _f32p, _f64p)
 _sig("ora_attention_pool_f32", C.c_int, C.POINTER(Geom), _u32p, C.c_void_p, C.c_void_p,
      _f32p, _f32p)
+_sig("ora_summary", None, C.POINTER(Geom), C.c_uint64, _f32p, _f32p)
+_sig("ora_quest_scores", C.c_int, C.POINTER(Geom), _f32p, _i32p, C.c_int, C.c_int, _f32p)
+_sig("ora_select_topk", C.c_int, C.POINTER(Geom), _f32p, _i32p, C.c_int, _u32p)
 _sig("ora_cpu_step", C.c_int, C.c_void_p, _u32p, C.c_void_p, C.c_void_p, C.c_void_p,
      C.c_void_p, _f32p, _f32p, _u32p, _u32p, _missp, _u64p)
 
@@ -391,3 +394,29 @@ def trace_load(path, strict=True):
     hdr = dict(requests=R, steps=S, layers=L, page_tokens=PT, block_tokens=BT, kv_heads=KV,
                head_dim=D, sel_pages=SEL, sel_blocks=nb)
     return hdr, out.reshape(R, S, L, nb), len(uniq), max(per_req) if per_req else 0
+
+
+def summary(g: Geom, h):
+    kmin = np.zeros(g.head_dim, np.float32)
+    kmax = np.zeros(g.head_dim, np.float32)
+    lib.ora_summary(C.byref(g), h, kmin, kmax)
+    return kmin, kmax
+
+
+def quest_scores(g: Geom, q, ctx_blocks, mode=0):
+    """Scores [rows, max ctx] (NaN where a row's context ends)."""
+    ctx = np.ascontiguousarray(ctx_blocks, np.int32)
+    stride = max(1, int(ctx.max()))
+    rows = g.n_req * g.n_layers * (1 if mode else g.kv_heads)
+    out = np.full(rows * stride, np.nan, np.float32)
+    lib.ora_quest_scores(C.byref(g), np.ascontiguousarray(q, np.float32).reshape(-1), ctx, mode,
+                         stride, out)
+    return out.reshape(rows, stride)
+
+
+def select_topk(g: Geom, q, ctx_blocks, mode=0):
+    sel = np.zeros(g.n_req * g.n_layers * g.kv_heads * g.k, np.uint32)
+    if lib.ora_select_topk(C.byref(g), np.ascontiguousarray(q, np.float32).reshape(-1),
+                           np.ascontiguousarray(ctx_blocks, np.int32), mode, sel):
+        raise ValueError("context longer than max_blocks")
+    return sel.reshape(g.n_req, g.n_layers, g.kv_heads, g.k)

@@ -1,0 +1,150 @@
+"""GPU parity of the on-device top-k block selection (Quest bound): block
+summaries and selections bit-exact against the oracle, and the selection
+feeding the executor (bookkeeping, fetch, attention) end to end."""
+import numpy as np
+import pytest
+import torch
+
+import ferry_amd as F
+from oracle import pyoracle as O
+
+from test_gpu_parity import TOL, Pair
+
+pytestmark = pytest.mark.gpu
+
+
+def _decode_summary_bytes(dtype, raw):
+    """[n, 2*128*esize] bytes -> float32 [n, 2, 128] (exact)."""
+    n = raw.shape[0]
+    if dtype == F.F32:
+        return raw.view(np.float32).reshape(n, 2, 128)
+    if dtype == F.F16:
+        return raw.view(np.float16).astype(np.float32).reshape(n, 2, 128)
+    if dtype == F.BF16:
+        return (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(n, 2, 128)
+    codes = raw.reshape(-1)
+    f = np.array([O.lib.ora_e4m3_to_f32(int(c)) for c in range(256)], np.float32)[codes]
+    return f.reshape(n, 2, 128)
+
+
+@pytest.mark.parametrize("dtype", [F.F32, F.F16, F.BF16, F.FP8])
+def test_summaries_bit_exact(dtype):
+    p = Pair(2, 1, 2, 2, 8, 8, 64, dtype, host_blocks=1031)
+    p.ex.summaries_build()
+    torch.cuda.synchronize()
+    raw, scales = p.ex.summaries_array()
+    got = _decode_summary_bytes(dtype, raw)
+    for h in range(1031):
+        kmin, kmax = O.summary(p.g, h)
+        assert np.array_equal(got[h, 0].view(np.uint32), kmin.view(np.uint32)), h
+        assert np.array_equal(got[h, 1].view(np.uint32), kmax.view(np.uint32)), h
+    if dtype == F.FP8:
+        assert np.array_equal(scales, p.hsc.reshape(-1, 2)[:, 0])
+
+
+@pytest.mark.parametrize("dtype,Hkv,Hq,host_blocks", [
+    (F.F16, 4, 4, 4099),     # MHA
+    (F.BF16, 2, 8, 4099),    # GQA-4
+    (F.FP8, 2, 8, 4099),     # fp8 + K scales
+    (F.F32, 2, 4, 7),        # a tiny host tier: aliased blocks tie
+    (F.BF16, 1, 8, 4099),    # GQA-8
+])
+@pytest.mark.parametrize("mode", [F.TOPK_PER_HEAD, F.TOPK_LAYER_MAX])
+def test_select_topk_bit_exact(dtype, Hkv, Hq, host_blocks, mode):
+    n_req, L, k, mb = 6, 2, 16, 300
+    p = Pair(n_req, L, Hkv, Hq, k, 64, mb, dtype, host_blocks=host_blocks)
+    p.ex.summaries_build()
+    rng = np.random.default_rng(dtype * 7 + Hq + mode)
+    ctx = np.array([300, 9, 0, 16, 17, 211], np.int32)  # full, ragged, empty, == k, k + 1
+    for t in range(2):
+        q = rng.standard_normal((n_req, L, Hq, 128)).astype(np.float32)
+        sel = torch.empty((n_req, L, Hkv, k), dtype=torch.int32, device="cuda")
+        p.ex.select_topk(torch.from_numpy(q).cuda(), torch.from_numpy(ctx).cuda(), sel, mode)
+        torch.cuda.synchronize()
+        got = sel.cpu().numpy().view(np.uint32)
+        want = O.select_topk(p.g, q, ctx, mode)
+        assert np.array_equal(got, want)
+    assert p.ex.stats()["device_error"] == 0
+
+
+def test_one_record_per_block_gives_the_same_selection():
+    """A table with a record per (set, block) (3x the host tier here) repeats
+    the host-tier records and selects exactly what the small table does."""
+    n_req, L, Hkv, Hq, k, mb, hb = 4, 2, 2, 8, 16, 384, 1031
+    p = Pair(n_req, L, Hkv, Hq, k, 64, mb, F.FP8, host_blocks=hb)
+    q = torch.randn((n_req, L, Hq, 128), device="cuda")
+    ctx = torch.tensor([384, 100, 17, 250], dtype=torch.int32, device="cuda")
+    a = torch.empty((n_req, L, Hkv, k), dtype=torch.int32, device="cuda")
+    b = torch.empty_like(a)
+    p.ex.summaries_build()
+    p.ex.select_topk(q, ctx, a)
+    torch.cuda.synchronize()
+    small, small_sc = p.ex.summaries_array()
+    p.ex.summaries_build(3 * hb)
+    p.ex.select_topk(q, ctx, b)
+    torch.cuda.synchronize()
+    big, big_sc = p.ex.summaries_array()
+    assert big.shape[0] == 3 * hb
+    assert np.array_equal(big, np.tile(small, (3, 1)))
+    assert np.array_equal(big_sc, np.tile(small_sc, 3))
+    assert torch.equal(a, b)
+    with pytest.raises(F.FerryError, match="multiple"):
+        p.ex.summaries_build(hb + 1)
+
+
+def test_select_layers_equals_whole_step():
+    n_req, L, Hkv, Hq, k = 3, 4, 2, 4, 12
+    p = Pair(n_req, L, Hkv, Hq, k, 48, 200, F.F16)
+    p.ex.summaries_build()
+    q = torch.randn((n_req, L, Hq, 128), device="cuda")
+    ctx = torch.tensor([200, 50, 7], dtype=torch.int32, device="cuda")
+    a = torch.empty((n_req, L, Hkv, k), dtype=torch.int32, device="cuda")
+    b = torch.full_like(a, -1)
+    p.ex.select_topk(q, ctx, a)
+    p.ex.select_topk(q, ctx, b, layers=(0, 3))
+    p.ex.select_topk(q, ctx, b, layers=(3, 1))
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_selection_feeds_the_executor():
+    """q -> top-k selection -> bookkeeping/fetch -> attention, over several
+    decode steps, against the oracle at every stage."""
+    n_req, L, Hkv, Hq, k, cap, mb = 4, 2, 2, 8, 24, 96, 400
+    p = Pair(n_req, L, Hkv, Hq, k, cap, mb, F.BF16)
+    p.ex.summaries_build()
+    rng = np.random.default_rng(11)
+    ctx = np.array([400, 120, 20, 333], np.int32)
+    dctx = torch.from_numpy(ctx).cuda()
+    base = rng.standard_normal((n_req, L, Hq, 128)).astype(np.float32)
+    for t in range(4):
+        # slowly drifting queries, so consecutive selections overlap
+        q = (base + 0.3 * rng.standard_normal(base.shape)).astype(np.float32)
+        dq = torch.from_numpy(q).cuda()
+        sel = torch.empty((n_req, L, Hkv, k), dtype=torch.int32, device="cuda")
+        p.ex.select_topk(dq, dctx, sel)
+        torch.cuda.synchronize()
+        s = sel.cpu().numpy().view(np.uint32).reshape(-1)
+        assert np.array_equal(s, O.select_topk(p.g, q, ctx, 0).reshape(-1))
+        p.check_fetched_bytes(p.step(s))
+        p.check_state()
+        out = torch.empty_like(dq)
+        p.ex.sparse_decode(dq, p.bufs["slots"], out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(-1, 128).astype(np.float64)
+        ref = O.attention_f64(p.g, s, q).reshape(-1, 128)
+        rel = np.abs(got - ref).max(axis=1) / np.abs(ref).max(axis=1)
+        assert rel.max() < TOL[F.BF16], rel.max()
+
+
+def test_selection_errors():
+    p = Pair(2, 1, 2, 2, 8, 16, 64, F.F16)
+    q = torch.zeros((2, 1, 2, 128), device="cuda")
+    sel = torch.empty((2, 1, 2, 8), dtype=torch.int32, device="cuda")
+    with pytest.raises(F.FerryError, match="summaries not built"):
+        p.ex.select_topk(q, torch.tensor([10, 10], dtype=torch.int32, device="cuda"), sel)
+    p.ex.summaries_build()
+    p.ex.select_topk(q, torch.tensor([65, 10], dtype=torch.int32, device="cuda"), sel)
+    torch.cuda.synchronize()
+    assert p.ex.stats()["device_error"] == -3  # FERRY_ERANGE: context longer than max_blocks
+    assert np.all(sel.cpu().numpy()[0] == -1)  # that row is left empty
