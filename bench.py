@@ -551,6 +551,10 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get(a.workload, {}).get("bytes_per_launch")
     r["roofline"]["traffic"] = traffic
+    if r.get("roofline_select") and os.path.exists(tpath):
+        with open(tpath) as f:
+            r["roofline_select"]["traffic"] = json.load(f).get(a.workload + "_select", {}).get(
+                "bytes_per_launch")
     lo, hi = w["ctx"]
     desc = (f"B={w['B']}, L={w['L']}, Hq={w['Hq']}, Hkv={w['Hkv']}, D=128, {w['dtype']} KV, "
             f"16-token blocks, ctx {'U[%d,%d]' % (lo * 16, hi * 16) if lo != hi else lo * 16} "
