@@ -15,7 +15,9 @@ uploaded before the timed region; the host tier is pinned host memory.
 
 The timed steps run ferry_decode_step: layers are cut into --chunks ranges
 and the bookkeeping + fetch of range c+1 run on a side stream while range c
-attends on the main stream.
+attends on the main stream.  By default the count is adaptive: the reference's
+batch rule (clamp(pending MB / 8, 64, 512) MB per chunk) on the bytes the
+previous step fetched.
 
 Prints ONE JSON line.  `value` is whole-step decode tokens/s (B / step time).
 Kernel rates come from HIP events around separate launches of each kernel:
@@ -78,8 +80,9 @@ def parse():
     ap.add_argument("--workers", type=int, default=0)
     ap.add_argument("--attn", default="auto", choices=["auto", "valu", "mfma"],
                     help="attention kernel: MFMA for GQA groups of 16/8-bit KV (auto), or forced")
-    ap.add_argument("--chunks", type=int, default=8,
-                    help="layer chunks of the fetch/attention overlap (1 = no side stream)")
+    ap.add_argument("--chunks", type=int, default=0,
+                    help="layer chunks of the fetch/attention overlap (1 = no side stream, "
+                         "0 = adaptive from the last step's fetched bytes)")
     ap.add_argument("--arrivals", default="none", choices=["none", "poisson", "mmpp"],
                     help="request arrivals instead of a full steady batch: requests wait for a "
                          "lane, decode --len steps and leave (lane reset on admission)")
@@ -244,7 +247,7 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     torch.cuda.synchronize()
 
     def step(t):
-        if a.chunks > 1:
+        if a.chunks != 1:
             ex.decode_step(sels[t], qs[t & 1], bufs, out, chunks=a.chunks, stream=stream,
                            side_stream=side)
         else:
@@ -361,7 +364,9 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
         "config_extra": {"slots_per_set": C, "host_tier_blocks": a.host_blocks,
                          "fetch_workers": ex.cfg.fetch_workers, "steal": steal,
                          "assign": "affinity" if assign == F.ASSIGN_AFFINITY else "spread",
-                         "chunks": a.chunks, "zipf": zipf},
+                         "chunks": a.chunks if a.chunks else
+                         f"adaptive ({ex.decode_chunks(int(timed_misses / a.steps))})",
+                         "zipf": zipf},
     }
     if want_cpu and not a.no_cpu:
         host, hsc = ex.hosttier_array()
@@ -450,7 +455,7 @@ def run_arrivals(a, w, F, torch, zipf=None, workers=None, steal=None):
         if adm[t] is not None:
             ex.reset_owners(adm[t], stream=stream)
         ex.decode_step(sels[t], qs[t & 1], bufs, out, chunks=a.chunks, stream=stream,
-                       side_stream=side if a.chunks > 1 else None)
+                       side_stream=side if a.chunks != 1 else None)
 
     for t in range(warm):
         tick(t)

@@ -123,6 +123,8 @@ _PROTOS = {
     "ferry_sched_create": (C.c_int, [_i32, _i32, C.c_uint32, _vp, _vp, C.POINTER(_vp)]),
     "ferry_trace_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(TraceInfo), _vp, C.c_uint64]),
     "ferry_summaries_build": (C.c_int, [_vp, C.c_uint64, _vp]),
+    "ferry_set_batch_policy": (C.c_int, [_vp, C.c_double, C.c_double, C.c_double]),
+    "ferry_decode_chunks": (C.c_int, [_vp, C.c_uint64, C.POINTER(_i32)]),
     "ferry_summaries_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(C.c_uint64)]),
     "ferry_select_topk": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp, _vp]),
     "ferry_select_topk_layers": (C.c_int, [_vp, _i32, _i32, _vp, _vp, C.c_int, _vp, _vp]),
@@ -249,9 +251,20 @@ class Executor:
         _check(lib.ferry_sparse_decode_layers(self._h, l0, nl, _ptr(q), _ptr(slots), _ptr(out),
                                               _stream(stream)), "ferry_sparse_decode_layers")
 
-    def decode_step(self, sel, q, bufs, out, chunks=8, stream=None, side_stream=None):
+    def set_batch_policy(self, min_mb=64.0, max_mb=512.0, target_batches=8.0):
+        _check(lib.ferry_set_batch_policy(self._h, min_mb, max_mb, target_batches),
+               "ferry_set_batch_policy")
+
+    def decode_chunks(self, pending_blocks):
+        """Layer chunks the adaptive policy picks for a step fetching this many blocks."""
+        n = _i32()
+        _check(lib.ferry_decode_chunks(self._h, pending_blocks, C.byref(n)), "ferry_decode_chunks")
+        return n.value
+
+    def decode_step(self, sel, q, bufs, out, chunks=0, stream=None, side_stream=None):
         """Whole step; fetch of layer chunk c+1 (side stream) overlaps attention
-        of chunk c (stream).  side_stream None runs everything on one stream."""
+        of chunk c (stream).  side_stream None runs everything on one stream.
+        chunks 0 = adaptive (from the last step's fetched bytes)."""
         _check(lib.ferry_decode_step(self._h, _ptr(sel), _ptr(q), _ptr(bufs["slots"]), _ptr(out),
                                      _ptr(bufs["miss_count"]), _ptr(bufs["misses"]), chunks,
                                      _stream(stream),

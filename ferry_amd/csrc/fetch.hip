@@ -1,11 +1,16 @@
 // fetch.hip -- drain of the device miss ring into the HBM slot pool.
 //
 // Persistent workgroups, one deque each.  Every wavefront pops one miss at a
-// time from its own deque head; when that is empty it scans all deques,
-// picks the fullest and steals min(max(rem/2, 1), steal_chunk) entries from its
-// tail, never more than rem/2+1 (the reference's steal bound,
-// src/runtime/wla_multigpu.cuh:1147-1152, 1518-1526; src/runtime/multigpu.cuh:
-// 153-175).  A miss is copied by one wavefront: 16-byte loads straight from
+// time from its own deque head; when that is empty it looks for a victim and
+// steals min(max(rem/2, 1), steal_chunk) entries from its tail, never more
+// than rem/2+1 (the reference's steal bound, src/runtime/wla_multigpu.cuh:
+// 1147-1152, 1518-1526; src/runtime/multigpu.cuh:153-175).  Victims are
+// searched 64 deques at a time (one per lane), starting at a window that
+// differs per wavefront, and the fullest deque of the first non-empty window
+// is robbed: thieves spread over the victims instead of all racing for the
+// single fullest deque, which serialised the end of every drain.  A thief
+// whose CAS loses backs off briefly.  A wavefront stops after a scan of all
+// deques finds them empty.  A miss is copied by one wavefront: 16-byte loads straight from
 // the pinned host tier (one PCIe hop, no staging ring, unlike
 // HostStagedChannel::submit, src/comm/host_staged_channel.cpp:43-74) into the
 // slot.  The last workgroup to finish accounts the drain and rewinds every
@@ -85,29 +90,34 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
       continue;
     }
     if (!a.steal) break;
-    // victim = fullest deque
+    // victim = fullest deque of the first non-empty 64-deque window, windows
+    // visited from this wavefront's own starting point
     uint32_t best = 0;
     int bw = W;
-    for (int w = lane; w < W; w += kWave) {
-      const uint64_t st = aload64(state + w);
-      const uint32_t h = (uint32_t)st, t = min((uint32_t)(st >> 32), a.ring.cap[w]);
-      const uint32_t rem = t > h ? t - h : 0;
-      if (rem > best) {
-        best = rem;
-        bw = w;
+    const int nwin = (W + kWave - 1) / kWave;
+    const int wave_id = me * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
+    for (int i = 0; i < nwin && best == 0; ++i) {
+      const int w = ((wave_id + i) % nwin) * kWave + lane;
+      uint32_t rem = 0;
+      if (w < W) {
+        const uint64_t st = aload64(state + w);
+        const uint32_t h = (uint32_t)st, t = min((uint32_t)(st >> 32), a.ring.cap[w]);
+        rem = t > h ? t - h : 0;
       }
-    }
+      best = rem;
+      bw = rem ? w : W;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const uint32_t ob = __shfl_xor(best, off);
-      const int ow = __shfl_xor(bw, off);
-      if (ob > best || (ob == best && ow < bw)) {
-        best = ob;
-        bw = ow;
+      for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t ob = __shfl_xor(best, off);
+        const int ow = __shfl_xor(bw, off);
+        if (ob > best || (ob == best && ow < bw)) {
+          best = ob;
+          bw = ow;
+        }
       }
+      best = first_lane_u(best);
+      bw = first_lane_i(bw);
     }
-    best = first_lane_u(best);
-    bw = first_lane_i(bw);
     if (best == 0) break;  // every deque is drained
     int ok = 0;
     uint32_t s0 = 0, s1 = 0;
@@ -126,7 +136,10 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
       }
     }
     ok = first_lane_i(ok);
-    if (!ok) continue;
+    if (!ok) {  // a peer took it first: back off before looking again
+      __builtin_amdgcn_s_sleep(2);
+      continue;
+    }
     s0 = first_lane_u(s0);
     s1 = first_lane_u(s1);
     const ferry_miss* seg = a.ring.entries + a.ring.seg[bw];
@@ -153,6 +166,7 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
       atomicAdd(a.stats + kStatMisses, total);
       atomicAdd(a.stats + kStatBytes, total * a.g.bb);
       atomicExch(a.stats + kStatLast, total);
+      atomicAdd(a.step_acc, total);
       astore(a.done, 0u);
       __threadfence();
     }
@@ -162,6 +176,13 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
 template __global__ void k_fetch<4>(FetchArgs);
 template __global__ void k_fetch<8>(FetchArgs);
 template __global__ void k_fetch<16>(FetchArgs);
+
+__global__ void k_step_close(unsigned long long* step_acc, unsigned long long* last) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    *last = *step_acc;
+    *step_acc = 0ull;
+  }
+}
 
 // Queue externally built misses: each thread appends one entry to the tail of
 // its set's worker deque.

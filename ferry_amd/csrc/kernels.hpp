@@ -43,6 +43,7 @@ struct FetchArgs {
   int steal;
   uint32_t steal_chunk;
   unsigned long long* stats;
+  unsigned long long* step_acc;  // blocks fetched since the last k_step_close
   uint32_t* done;
   int* err;
 };
@@ -57,6 +58,8 @@ __global__ void k_sets_reset_owners(Geo g, SetState st, const uint32_t* owners, 
 template <int NV>
 __global__ void k_fetch(FetchArgs a);
 __global__ void k_missq_push(Geo g, Ring ring, const ferry_miss* m, uint32_t n, int* err);
+// End of a decode step: last = blocks fetched in the step, then step_acc = 0.
+__global__ void k_step_close(unsigned long long* step_acc, unsigned long long* last);
 
 // Vector-ALU attention (attn.hip); W wavefronts per workgroup.
 template <int DT, int G, int W>

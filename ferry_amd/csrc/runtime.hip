@@ -71,6 +71,9 @@ struct ferry_ctx {
   uint32_t* worker_of_set = nullptr;
   unsigned long long* stats = nullptr;
   unsigned long long* sel_counts = nullptr;  // [kSelCounters * kSelStride]
+  unsigned long long* step_acc = nullptr;    // [2]: blocks fetched in this step, in the last one
+  unsigned long long* pend_host = nullptr;   // pinned: the last step's count, copied at step end
+  double pol_min_mb = 64.0, pol_max_mb = 512.0, pol_target = 8.0;  // adaptive layer chunking
   uint32_t* done = nullptr;
   int* err = nullptr;
   uint8_t* host = nullptr;      // host pointer of the pinned tier
@@ -140,10 +143,11 @@ void release(ferry_ctx* c) {
   (void)hipSetDevice(c->device);
   void* dev[] = {c->pool, c->pool_scales, c->st.fill, c->st.ord, c->st.tag, c->st.map,
                  c->ring_entries, c->ring_state, c->ring_seg, c->ring_cap, c->worker_of_set,
-                 c->stats, c->sel_counts, c->done, c->err, c->probe_sink, c->probe_dst,
-                 c->sums, c->sum_scales};
+                 c->stats, c->sel_counts, c->step_acc, c->done, c->err, c->probe_sink,
+                 c->probe_dst, c->sums, c->sum_scales};
   for (void* p : dev)
     if (p) (void)hipFree(p);
+  if (c->pend_host) (void)hipHostFree(c->pend_host);
   if (c->host) (void)hipHostFree(c->host);
   if (c->host_scales) (void)hipHostFree(c->host_scales);
   for (hipEvent_t e : c->events) (void)hipEventDestroy(e);
@@ -323,6 +327,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   TRY(dalloc(&c->worker_of_set, g.n_sets));
   TRY(dalloc(&c->stats, kStatCount));
   TRY(dalloc(&c->sel_counts, (size_t)kSelCounters * kSelStride));
+  TRY(dalloc(&c->step_acc, 2));
   TRY(dalloc(&c->done, 1));
   TRY(dalloc(&c->err, 1));
 #define HIPT(x)                                                                        \
@@ -339,6 +344,13 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   HIPT(hipMemset(c->ring_state, 0, W * 8));
   HIPT(hipMemset(c->stats, 0, kStatCount * 8));
   HIPT(hipMemset(c->sel_counts, 0, (size_t)kSelCounters * kSelStride * 8));
+  HIPT(hipMemset(c->step_acc, 0, 16));
+  if (hipHostMalloc((void**)&c->pend_host, 8, hipHostMallocDefault) != hipSuccess) {
+    c->pend_host = nullptr;
+    release(c);
+    return fail(FERRY_ENOMEM, "hipHostMalloc of the step counter failed");
+  }
+  *c->pend_host = 0;
   HIPT(hipMemset(c->done, 0, 4));
   HIPT(hipMemset(c->err, 0, 4));
   HIPT(hipMemset(c->pool, 0, nslots * g.bb));
@@ -509,6 +521,7 @@ int ferry_missq_drain(ferry_ctx* ctx, void* stream) {
   a.steal = ctx->cfg.steal;
   a.steal_chunk = 8;
   a.stats = ctx->stats;
+  a.step_acc = ctx->step_acc;
   a.done = ctx->done;
   a.err = ctx->err;
   const dim3 grid(ctx->g.workers), block(256);
@@ -551,12 +564,37 @@ int ferry_sparse_decode(ferry_ctx* ctx, const float* q, const uint32_t* slots, f
   return ferry_sparse_decode_layers(ctx, 0, ctx->g.L, q, slots, out, stream);
 }
 
+int ferry_set_batch_policy(ferry_ctx* ctx, double min_mb, double max_mb, double target_batches) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!(min_mb > 0.0) || !(max_mb >= min_mb) || !(target_batches > 0.0))
+    return fail(FERRY_EINVAL, "need 0 < min_mb <= max_mb and target_batches > 0");
+  ctx->pol_min_mb = min_mb;
+  ctx->pol_max_mb = max_mb;
+  ctx->pol_target = target_batches;
+  return FERRY_OK;
+}
+
+int ferry_decode_chunks(const ferry_ctx* ctx, uint64_t pending_blocks, int32_t* chunks) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!chunks) return fail(FERRY_EINVAL, "null out");
+  const double mb = (double)pending_blocks * (double)ctx->g.bb / 1048576.0;
+  // AdaptiveBatchPolicy::choose_mb: clamp(pending / target, min, max) MB per batch
+  const double g = std::min(std::max(mb / ctx->pol_target, ctx->pol_min_mb), ctx->pol_max_mb);
+  const double n = std::ceil(mb / g);
+  *chunks = (int32_t)std::min<double>(std::max(n, 1.0), (double)ctx->g.L);
+  return FERRY_OK;
+}
+
 int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint32_t* slots,
                       float* out, uint32_t* miss_count, ferry_miss* misses, int32_t chunks,
                       void* stream, void* side_stream) {
   if (int rc = check_ctx(ctx)) return rc;
   const int L = ctx->g.L;
-  if (chunks < 1) return fail(FERRY_EINVAL, "chunks < 1");
+  if (chunks < 0) return fail(FERRY_EINVAL, "chunks < 0");
+  if (chunks == 0) {  // adaptive: from the blocks the last finished step fetched
+    const uint64_t last = *reinterpret_cast<volatile unsigned long long*>(ctx->pend_host);
+    if (int rc = ferry_decode_chunks(ctx, last, &chunks)) return rc;
+  }
   chunks = std::min(chunks, L);
   const int per = (L + chunks - 1) / chunks;
   hipStream_t ms = (hipStream_t)stream, ss = (hipStream_t)side_stream;
@@ -579,6 +617,10 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
     }
     if ((rc = ferry_sparse_decode_layers(ctx, l0, nl, q, slots, out, ms))) return rc;
   }
+  // the step's fetched blocks, for the next step's adaptive chunking
+  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(64), 0, ms, ctx->step_acc, ctx->step_acc + 1);
+  HIPC(hipGetLastError());
+  HIPC(hipMemcpyAsync(ctx->pend_host, ctx->step_acc + 1, 8, hipMemcpyDeviceToHost, ms));
   return FERRY_OK;
 }
 

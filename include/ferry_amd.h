@@ -220,6 +220,19 @@ int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const flo
 int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint32_t* slots,
                       float* out, uint32_t* miss_count, ferry_miss* misses, int32_t chunks,
                       void* stream, void* side_stream);
+/* chunks == 0 chooses the chunk count with the reference's adaptive batch
+ * rule (AdaptiveBatchPolicy::choose_mb, src/runtime/adaptive_batch.cuh:31-36;
+ * take rule kv_exec.cuh:230-235): the bytes the last finished step fetched
+ * are `pending`, a chunk moves g = clamp(pending / target_batches, min_mb,
+ * max_mb) MB, and the step runs ceil(pending / g) chunks (1 .. n_layers; 1
+ * before any step has finished).  A chunk costs three launches and a drain,
+ * so the GPU policy works in larger units than the reference's channel
+ * submits: defaults min 64 MB, max 512 MB, target 8 batches.  The count is
+ * read from pinned memory that each step's end copies into, so the host never
+ * waits for the device.  ferry_decode_chunks gives the count for a pending
+ * number of blocks. */
+int ferry_set_batch_policy(ferry_ctx* ctx, double min_mb, double max_mb, double target_batches);
+int ferry_decode_chunks(const ferry_ctx* ctx, uint64_t pending_blocks, int32_t* chunks);
 
 /* ---- top-k block selection (Quest bound) ----
  * The step upstream of the miss queue: choose each request's k blocks from

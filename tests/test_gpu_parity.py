@@ -289,13 +289,17 @@ def test_steady_state_properties_at_scale():
     assert 0.02 < st["last_misses"] / (n_req * L * H * k) < 0.3
 
 
-def test_decode_step_overlap_matches_sequential():
+@pytest.mark.parametrize("chunks", [4, 0])
+def test_decode_step_overlap_matches_sequential(chunks):
     # layer-chunked pipeline (fetch of chunk c+1 on a side stream while chunk c
-    # attends) must produce exactly the sequential step's slots, pool and output
+    # attends) must produce exactly the sequential step's slots, pool and output;
+    # chunks 0 picks the count from the previous step's fetched bytes
     n_req, L, Hkv, Hq, k, cap = 4, 6, 2, 8, 16, 40
     mb, sels = _zipf_stream(n_req, L, Hkv, k, 60, 300, 5)
     seq = Pair(n_req, L, Hkv, Hq, k, cap, mb, F.BF16)
     ovl = Pair(n_req, L, Hkv, Hq, k, cap, mb, F.BF16)
+    if chunks == 0:  # small units, so that these small steps are cut into several chunks
+        ovl.ex.set_batch_policy(min_mb=0.01, max_mb=0.05, target_batches=4)
     side = torch.cuda.Stream()
     rng = np.random.default_rng(3)
     for t, sel in enumerate(sels):
@@ -304,7 +308,7 @@ def test_decode_step_overlap_matches_sequential():
         d = torch.from_numpy(sel.view(np.int32)).cuda()
         seq.ex.fetch_step(d, seq.bufs)
         seq.ex.sparse_decode(q, seq.bufs["slots"], o1)
-        ovl.ex.decode_step(d, q, ovl.bufs, o2, chunks=4, side_stream=side)
+        ovl.ex.decode_step(d, q, ovl.bufs, o2, chunks=chunks, side_stream=side)
         torch.cuda.synchronize()
         assert np.array_equal(_u32(seq.bufs["slots"]), _u32(ovl.bufs["slots"]))
         assert torch.equal(o1, o2)
@@ -315,6 +319,25 @@ def test_decode_step_overlap_matches_sequential():
     allslots = np.arange(seq.ex.pool_slots)
     assert np.array_equal(seq.ex.pool_slots_bytes(allslots), ovl.ex.pool_slots_bytes(allslots))
     ovl.check_attention(sels[-1], seed=11)
+
+
+def test_adaptive_chunk_policy_known_answers():
+    # AdaptiveBatchPolicy::choose_mb (src/runtime/adaptive_batch.cuh:31-36) in GPU
+    # units: g = clamp(pending_MB / 8, 64, 512) MB per chunk, ceil(pending / g)
+    # chunks, at least 1 and at most L.  8 KiB blocks: 1 MB = 128 blocks.
+    p = Pair(2, 32, 2, 2, 8, 16, 64, F.F16)
+    bb = p.ex.block_bytes
+    assert bb == 8192
+    mb = 1 << 20
+    cases = {0: 1, 1: 1, 64 * mb // bb: 1, 65 * mb // bb: 2, 184 * mb // bb: 3,
+             1290 * mb // bb: 8, 3440 * mb // bb: 8, 8192 * mb // bb: 16,
+             (1 << 40) // bb: 32}
+    for blocks, want in cases.items():
+        assert p.ex.decode_chunks(blocks) == want, (blocks, want)
+    p.ex.set_batch_policy(1.0, 4.0, 4.0)  # the reference's channel defaults
+    assert p.ex.decode_chunks(16 * mb // bb) == 4 and p.ex.decode_chunks(2 * mb // bb) == 2
+    with pytest.raises(F.FerryError):
+        p.ex.set_batch_policy(8.0, 4.0, 4.0)
 
 
 def test_per_layer_bookkeeping_equals_whole_step():
