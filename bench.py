@@ -23,6 +23,8 @@ Prints ONE JSON line.  `value` is whole-step decode tokens/s (B / step time).
 Kernel rates come from HIP events around separate launches of each kernel:
   roofline        attention kernel vs 8 TB/s HBM (algorithmic bytes/launch)
   roofline_fetch  fetch kernel vs the PCIe Gen5 x16 host link (63.0 GB/s)
+  roofline_select top-k selection over every context block vs HBM
+  roofline_handoff export / import of one owner's resident KV vs HBM
 cpu_baseline times the oracle's C restatement of the same step (1 thread) on
 2 of the requests (a whole prefix group for grouped workloads).
 
@@ -323,6 +325,7 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     n_host = int(min(a.host_blocks, max(1, (st2["misses"] - m0) // a.steps)))
     _, _, hread_gbs = ex.bw_probe(F.PROBE_HOST_READ, n_host, iters=3, stream=stream)
     _, _, hdma_gbs = ex.bw_probe(F.PROBE_HOST_DMA, n_host, iters=3, stream=stream)
+    handoff = run_handoff(a, ex, F, torch, stream, dtype)
     ev_misses = st2["misses"] - m0
     t_book = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
     t_fetch = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
@@ -359,6 +362,7 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
                            "plain_read_gbs": round(hread_gbs, 2), "dma_copy_gbs": round(hdma_gbs, 2),
                            "frac_of_plain_read": round(link_gbs / hread_gbs, 4)},
         "roofline_select": select,
+        "roofline_handoff": handoff,
         "steals_per_step": round((st2["steals"] - s0) / a.steps, 1),
         "selection_gen_s": round(gen_s, 2),
         "config_extra": {"slots_per_set": C, "host_tier_blocks": a.host_blocks,
@@ -374,6 +378,44 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
                                            a.cpu_reqs, a.cpu_steps, reuse_r)
     ex.close()
     return res
+
+
+def run_handoff(a, ex, F, torch, stream, dtype):
+    """Owner hand-off in steady state: export of owner 0's resident KV and LRU
+    state into an image, and import of that image into owner 1 (the per-GPU
+    halves of moving a request; the image crossing the link is not timed).
+    Algorithmic bytes per launch pair: every resident block (and its fp8
+    scales) read once and written once; the LRU metadata (about 40 bytes per
+    block) is left out of the count."""
+    img = ex.alloc_owner_image()
+    ex.owner_export(0, img, stream)
+    torch.cuda.synchronize()
+    resident = int(img[24:32].cpu().numpy().view(np.uint64)[0])
+    it = max(3, a.steps // 2)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    ev[0].record(stream)
+    for _ in range(it):
+        ex.owner_export(0, img, stream)
+    ev[1].record(stream)
+    for _ in range(it):
+        ex.owner_import(1, img, stream)
+    ev[2].record(stream)
+    torch.cuda.synchronize()
+    if ex.stats()["device_error"]:
+        raise RuntimeError("owner import refused the exported image")
+    t_exp = ev[0].elapsed_time(ev[1]) / it
+    t_imp = ev[1].elapsed_time(ev[2]) / it
+    per = ex.block_bytes + (8 if dtype == F.FP8 else 0)
+    moved = 2 * resident * per
+    del img
+    bb = ex.block_bytes // 1024
+    return {"bound": "hbm", "kernel": f"k_owner_export_data<{bb}> + k_owner_import_data<{bb}>",
+            "resident_blocks": resident, "image_gb": round(resident * per / 1e9, 3),
+            "export_ms": round(t_exp, 4), "import_ms": round(t_imp, 4),
+            "export_gbs": round(moved / (t_exp * 1e-3) / 1e9, 1),
+            "import_gbs": round(moved / (t_imp * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac_export": round(moved / (t_exp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "frac_import": round(moved / (t_imp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def arrival_plan(a, w, F, n_ticks, zipf):
@@ -584,7 +626,8 @@ def main():
     }
     for key in ("miss_rate", "miss_blocks_per_s", "miss_blocks_per_s_fetch_kernel",
                 "attention_tok_per_s", "kernel_ms", "roofline", "roofline_fetch",
-                "roofline_select", "steals_per_step", "selection_gen_s", "cpu_baseline"):
+                "roofline_select", "roofline_handoff", "steals_per_step", "selection_gen_s",
+                "cpu_baseline"):
         if key in r:
             res[key] = r[key]
     print(json.dumps(res), flush=True)

@@ -124,6 +124,9 @@ _PROTOS = {
     "ferry_trace_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(TraceInfo), _vp, C.c_uint64]),
     "ferry_summaries_build": (C.c_int, [_vp, C.c_uint64, _vp]),
     "ferry_set_batch_policy": (C.c_int, [_vp, C.c_double, C.c_double, C.c_double]),
+    "ferry_owner_image_bytes": (C.c_int, [_vp, C.POINTER(C.c_uint64)]),
+    "ferry_owner_export": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint64, _vp]),
+    "ferry_owner_import": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint64, _vp]),
     "ferry_decode_chunks": (C.c_int, [_vp, C.c_uint64, C.POINTER(_i32)]),
     "ferry_summaries_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(C.c_uint64)]),
     "ferry_select_topk": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp, _vp]),
@@ -250,6 +253,24 @@ class Executor:
     def sparse_decode_layers(self, l0, nl, q, slots, out, stream=None):
         _check(lib.ferry_sparse_decode_layers(self._h, l0, nl, _ptr(q), _ptr(slots), _ptr(out),
                                               _stream(stream)), "ferry_sparse_decode_layers")
+
+    def owner_image_bytes(self):
+        n = C.c_uint64()
+        _check(lib.ferry_owner_image_bytes(self._h, C.byref(n)), "ferry_owner_image_bytes")
+        return n.value
+
+    def alloc_owner_image(self):
+        """A device buffer for one owner image (uint8 tensor)."""
+        return torch.empty(self.owner_image_bytes(), dtype=torch.uint8,
+                           device=torch.device("cuda", self.device))
+
+    def owner_export(self, owner, image, stream=None):
+        _check(lib.ferry_owner_export(self._h, owner, _ptr(image), image.numel(), _stream(stream)),
+               "ferry_owner_export")
+
+    def owner_import(self, owner, image, stream=None):
+        _check(lib.ferry_owner_import(self._h, owner, _ptr(image), image.numel(), _stream(stream)),
+               "ferry_owner_import")
 
     def set_batch_policy(self, min_mb=64.0, max_mb=512.0, target_batches=8.0):
         _check(lib.ferry_set_batch_policy(self._h, min_mb, max_mb, target_batches),

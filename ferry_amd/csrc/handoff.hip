@@ -1,0 +1,228 @@
+// handoff.hip -- export and import of one owner's resident KV (the per-GPU
+// halves of moving a request between executors).
+//
+// The reference migrates a request in "delta" mode (src/runtime/wla_multigpu.cuh:
+// 1367-1428): the victim gathers the request's resident slots into a
+// contiguous staging buffer (wla_slot_gather_kernel, :154-162), the buffer
+// crosses the link, the consumer scatters it back to the same slot offsets
+// (wla_slot_scatter_kernel, :163-171) and takes over the LRU state
+// (kv_handoff, :1970-1994).  Here an owner's image holds, for each of its
+// (layer, kv head) sets, the LRU fill, order and tags and the bytes of its
+// resident slots, compacted in LRU order.  Resident slots are always
+// [0, fill) (free slots are handed out in order and only reset returns them),
+// so the importer keeps the exporter's slot ids and its state ends up equal
+// bit for bit.
+//
+// Image layout (device memory, offsets in bytes from its start):
+//   [0, 64)          header: magic, sets, slots_per_set, block_bytes, dtype,
+//                    max_blocks, resident blocks (u64)
+//   fill[sets], start[sets]                      u32 each
+//   ord[sets * C], tag[sets * C]                 u32, per set from start[s]:
+//                                                local slots in LRU order and
+//                                                their blocks
+//   scales[sets * C][2]                          fp32 (fp8 KV only)
+//   data[sets * C][block_bytes]                  from a 256-byte boundary:
+//                                                resident blocks, compacted
+// Only data[0, resident) is filled; ferry_owner_image_bytes gives the
+// capacity for a full owner.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ferry_amd {
+
+namespace {
+
+constexpr uint32_t kImageMagic = 0x4E574F46u;  // "FOWN"
+
+struct ImageHeader {
+  uint32_t magic, sets, slots, bb, dtype, max_blocks;
+  unsigned long long resident;
+};
+
+__device__ inline ImageLayout image_layout(const Geo& g) { return make_image_layout(g); }
+
+// Forget every block of one set (map entries of its tags, tags, order, fill).
+__device__ inline void clear_set(const Geo& g, SetState st, size_t set, int lane) {
+  const uint32_t C = (uint32_t)g.C;
+  uint32_t* map = st.map + set * (size_t)g.max_blocks;
+  uint32_t* tag = st.tag + set * C;
+  uint32_t* ord = st.ord + set * C;
+  for (uint32_t i = lane; i < C; i += kWave) {
+    const uint32_t b = tag[i];
+    if (b < (uint32_t)g.max_blocks) map[b] = kNone;
+  }
+  wave_fence();
+  for (uint32_t i = lane; i < C; i += kWave) {
+    tag[i] = kNone;
+    ord[i] = kNone;
+  }
+  if (lane == 0) st.fill[set] = 0;
+  wave_fence();
+}
+
+}  // namespace
+
+// One workgroup: header, fill and start (exclusive prefix of the fills) of
+// the owner's sets.
+__global__ __launch_bounds__(256) void k_owner_export_meta(Geo g, SetState st, uint32_t owner,
+                                                           uint8_t* __restrict__ image) {
+  const ImageLayout lay = image_layout(g);
+  const uint32_t S = (uint32_t)(g.L * g.Hkv);
+  uint32_t* fill = reinterpret_cast<uint32_t*>(image + lay.fill);
+  uint32_t* start = reinterpret_cast<uint32_t*>(image + lay.start);
+  for (uint32_t s = threadIdx.x; s < S; s += blockDim.x) fill[s] = st.fill[(size_t)owner * S + s];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long acc = 0;
+    for (uint32_t s = 0; s < S; ++s) {
+      start[s] = (uint32_t)acc;
+      acc += fill[s];
+    }
+    ImageHeader* h = reinterpret_cast<ImageHeader*>(image);
+    h->magic = kImageMagic;
+    h->sets = S;
+    h->slots = (uint32_t)g.C;
+    h->bb = (uint32_t)g.bb;
+    h->dtype = (uint32_t)g.dtype;
+    h->max_blocks = (uint32_t)g.max_blocks;
+    h->resident = acc;
+  }
+}
+
+// One wavefront per (set, LRU position i): position i < fill copies its slot's
+// block into the data area at start[set] + i (16-byte loads, NV per lane) and
+// records slot, tag and fp8 scales.
+template <int NV>
+__global__ __launch_bounds__(256) void k_owner_export_data(Geo g, SetState st, uint32_t owner,
+                                                           const uint8_t* __restrict__ pool,
+                                                           const float* __restrict__ pool_scales,
+                                                           uint8_t* __restrict__ image) {
+  const ImageLayout lay = image_layout(g);
+  const uint32_t S = (uint32_t)(g.L * g.Hkv), C = (uint32_t)g.C;
+  const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (wave >= (uint64_t)S * C) return;
+  const uint32_t s = (uint32_t)(wave / C), i = (uint32_t)(wave % C);
+  const uint32_t* fill = reinterpret_cast<const uint32_t*>(image + lay.fill);
+  const uint32_t* start = reinterpret_cast<const uint32_t*>(image + lay.start);
+  if (i >= fill[s]) return;
+  const size_t set = (size_t)owner * S + s;
+  const uint32_t slot = st.ord[set * C + i];
+  const size_t pos = (size_t)start[s] + i;
+  const size_t gslot = set * C + slot;
+  if (lane == 0) {
+    reinterpret_cast<uint32_t*>(image + lay.ord)[pos] = slot;
+    reinterpret_cast<uint32_t*>(image + lay.tag)[pos] = st.tag[gslot];
+    if (pool_scales) {
+      reinterpret_cast<float*>(image + lay.scales)[2 * pos] = pool_scales[2 * gslot];
+      reinterpret_cast<float*>(image + lay.scales)[2 * pos + 1] = pool_scales[2 * gslot + 1];
+    }
+  }
+  const uint4* src = reinterpret_cast<const uint4*>(pool + gslot * g.bb);
+  uint4* dst = reinterpret_cast<uint4*>(image + lay.data + pos * g.bb);
+  uint4 r[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) r[v] = src[v * kWave + lane];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) dst[v * kWave + lane] = r[v];
+}
+
+// One wavefront per set of the importing owner: forget the set's blocks, check
+// the image against this executor's geometry, then take the image's fill,
+// order, tags and map entries.  A mismatching or malformed image latches
+// FERRY_EINVAL and leaves the set empty (so the data kernel writes nothing).
+__global__ __launch_bounds__(256) void k_owner_import_meta(Geo g, SetState st, uint32_t owner,
+                                                           const uint8_t* __restrict__ image,
+                                                           int* __restrict__ err) {
+  const ImageLayout lay = image_layout(g);
+  const uint32_t S = (uint32_t)(g.L * g.Hkv), C = (uint32_t)g.C;
+  const uint32_t s = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (s >= S) return;
+  const ImageHeader* h = reinterpret_cast<const ImageHeader*>(image);
+  const uint32_t* fill = reinterpret_cast<const uint32_t*>(image + lay.fill);
+  const uint32_t* start = reinterpret_cast<const uint32_t*>(image + lay.start);
+  const uint32_t* iord = reinterpret_cast<const uint32_t*>(image + lay.ord);
+  const uint32_t* itag = reinterpret_cast<const uint32_t*>(image + lay.tag);
+  const size_t set = (size_t)owner * S + s;
+  clear_set(g, st, set, lane);
+  const bool hdr_ok = h->magic == kImageMagic && h->sets == S && h->slots == C &&
+                      h->bb == (uint32_t)g.bb && h->dtype == (uint32_t)g.dtype &&
+                      h->max_blocks == (uint32_t)g.max_blocks && h->resident <= (unsigned long long)S * C;
+  const uint32_t f = hdr_ok ? fill[s] : 0, p0 = hdr_ok ? start[s] : 0;
+  bool bad = !hdr_ok || f > C || (unsigned long long)p0 + f > h->resident;
+  for (uint32_t i = lane; i < f && !bad; i += kWave)
+    bad |= iord[p0 + i] >= f || itag[p0 + i] >= (uint32_t)g.max_blocks;
+  if (ballot(bad)) {
+    if (lane == 0) set_error(err, FERRY_EINVAL);
+    return;
+  }
+  uint32_t* map = st.map + set * (size_t)g.max_blocks;
+  uint32_t* tag = st.tag + set * C;
+  uint32_t* ord = st.ord + set * C;
+  for (uint32_t i = lane; i < f; i += kWave) {
+    const uint32_t slot = iord[p0 + i], b = itag[p0 + i];
+    ord[i] = slot;
+    astore(tag + slot, b);
+    astore(map + b, slot);
+  }
+  wave_fence();
+  // The order must be a permutation of [0, f) with distinct blocks: a repeated
+  // slot leaves some slot below f untagged, and a slot or block repeated with
+  // another partner fails to read back through tag or map.
+  bool dup = false;
+  for (uint32_t i = lane; i < f; i += kWave) {
+    const uint32_t slot = iord[p0 + i], b = itag[p0 + i];
+    dup |= aload(tag + slot) != b || aload(map + b) != slot || aload(tag + i) == kNone;
+  }
+  if (ballot(dup)) {
+    clear_set(g, st, set, lane);
+    if (lane == 0) set_error(err, FERRY_EINVAL);
+    return;
+  }
+  if (lane == 0) st.fill[set] = f;
+}
+
+// One wavefront per (set, LRU position i < fill): the image block goes back to
+// its slot (and its fp8 scales).  Runs after k_owner_import_meta validated the
+// image; a set it refused has fill 0 in the importer and nothing is written.
+template <int NV>
+__global__ __launch_bounds__(256) void k_owner_import_data(Geo g, SetState st, uint32_t owner,
+                                                           uint8_t* __restrict__ pool,
+                                                           float* __restrict__ pool_scales,
+                                                           const uint8_t* __restrict__ image) {
+  const ImageLayout lay = image_layout(g);
+  const uint32_t S = (uint32_t)(g.L * g.Hkv), C = (uint32_t)g.C;
+  const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (wave >= (uint64_t)S * C) return;
+  const uint32_t s = (uint32_t)(wave / C), i = (uint32_t)(wave % C);
+  const size_t set = (size_t)owner * S + s;
+  const uint32_t f = st.fill[set];  // 0 unless the meta kernel accepted the image
+  if (i >= f) return;
+  const size_t pos = (size_t)reinterpret_cast<const uint32_t*>(image + lay.start)[s] + i;
+  const uint32_t slot = reinterpret_cast<const uint32_t*>(image + lay.ord)[pos];
+  const size_t gslot = set * C + slot;
+  if (lane == 0 && pool_scales) {
+    pool_scales[2 * gslot] = reinterpret_cast<const float*>(image + lay.scales)[2 * pos];
+    pool_scales[2 * gslot + 1] = reinterpret_cast<const float*>(image + lay.scales)[2 * pos + 1];
+  }
+  const uint4* src = reinterpret_cast<const uint4*>(image + lay.data + pos * g.bb);
+  uint4* dst = reinterpret_cast<uint4*>(pool + gslot * g.bb);
+  uint4 r[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) r[v] = src[v * kWave + lane];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) dst[v * kWave + lane] = r[v];
+}
+
+#define FERRY_HANDOFF_INST(NV)                                                                    \
+  template __global__ void k_owner_export_data<NV>(Geo, SetState, uint32_t, const uint8_t*,       \
+                                                   const float*, uint8_t*);                        \
+  template __global__ void k_owner_import_data<NV>(Geo, SetState, uint32_t, uint8_t*, float*,     \
+                                                   const uint8_t*);
+FERRY_HANDOFF_INST(4)
+FERRY_HANDOFF_INST(8)
+FERRY_HANDOFF_INST(16)
+
+}  // namespace ferry_amd

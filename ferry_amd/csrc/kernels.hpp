@@ -84,6 +84,34 @@ __global__ void k_probe_host(const uint8_t* host, uint64_t bb, uint64_t n_blocks
 __global__ void k_hosttier_fill(Geo g, uint8_t* host, float* scales, uint64_t seed, float mult,
                                 float mult8, float scale_base);
 
+// Byte offsets of an owner image (handoff.hip): header, fill[S], start[S],
+// ord[S*C], tag[S*C], scales[S*C][2] (fp8 only), then the data from a
+// 256-byte boundary, S = L * Hkv sets of C slots.
+struct ImageLayout {
+  uint64_t fill, start, ord, tag, scales, data, bytes;
+};
+__host__ __device__ inline ImageLayout make_image_layout(const Geo& g) {
+  const uint64_t S = (uint64_t)g.L * (uint64_t)g.Hkv, N = S * (uint64_t)g.C;
+  ImageLayout l;
+  l.fill = 64;
+  l.start = l.fill + 4 * S;
+  l.ord = l.start + 4 * S;
+  l.tag = l.ord + 4 * N;
+  l.scales = l.tag + 4 * N;
+  const uint64_t sc = g.dtype == FERRY_FP8_E4M3 ? 8 * N : 0;
+  l.data = (l.scales + sc + 255) / 256 * 256;
+  l.bytes = l.data + N * g.bb;
+  return l;
+}
+__global__ void k_owner_export_meta(Geo g, SetState st, uint32_t owner, uint8_t* image);
+template <int NV>
+__global__ void k_owner_export_data(Geo g, SetState st, uint32_t owner, const uint8_t* pool,
+                                    const float* pool_scales, uint8_t* image);
+__global__ void k_owner_import_meta(Geo g, SetState st, uint32_t owner, const uint8_t* image, int* err);
+template <int NV>
+__global__ void k_owner_import_data(Geo g, SetState st, uint32_t owner, uint8_t* pool, float* pool_scales,
+                                    const uint8_t* image);
+
 // Top-k block selection (select.hip): per-host-block K min/max summaries and
 // the Quest-bound scoring + radix top-k kernel.
 template <int DT>

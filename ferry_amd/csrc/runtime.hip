@@ -761,6 +761,71 @@ int ferry_select_topk(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks,
   return ferry_select_topk_layers(ctx, 0, ctx->g.L, q, ctx_blocks, mode, sel, stream);
 }
 
+int ferry_owner_image_bytes(const ferry_ctx* ctx, uint64_t* bytes) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!bytes) return fail(FERRY_EINVAL, "null out");
+  *bytes = make_image_layout(ctx->g).bytes;
+  return FERRY_OK;
+}
+
+namespace {
+
+int owner_check(ferry_ctx* ctx, uint32_t owner, const void* image, uint64_t image_bytes) {
+  if (!image) return fail(FERRY_EINVAL, "null image");
+  if (owner >= (uint32_t)ctx->g.n_owners) return fail(FERRY_EINVAL, "owner out of range");
+  if (image_bytes < make_image_layout(ctx->g).bytes)
+    return fail(FERRY_EINVAL, "image buffer smaller than ferry_owner_image_bytes");
+  if ((uintptr_t)image % 256) return fail(FERRY_EINVAL, "image must be 256-byte aligned");
+  return FERRY_OK;
+}
+
+}  // namespace
+
+int ferry_owner_export(ferry_ctx* ctx, uint32_t owner, void* image, uint64_t image_bytes, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = owner_check(ctx, owner, image, image_bytes)) return rc;
+  const Geo& g = ctx->g;
+  HIPC(hipSetDevice(ctx->device));
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* im = (uint8_t*)image;
+  hipLaunchKernelGGL(k_owner_export_meta, dim3(1), dim3(256), 0, s, g, ctx->st, owner, im);
+  HIPC(hipGetLastError());
+  const uint64_t waves = (uint64_t)g.L * g.Hkv * g.C;
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  switch (g.bb / 1024) {
+    case 4: hipLaunchKernelGGL(k_owner_export_data<4>, grid, block, 0, s, g, ctx->st, owner, ctx->pool, ctx->pool_scales, im); break;
+    case 8: hipLaunchKernelGGL(k_owner_export_data<8>, grid, block, 0, s, g, ctx->st, owner, ctx->pool, ctx->pool_scales, im); break;
+    case 16: hipLaunchKernelGGL(k_owner_export_data<16>, grid, block, 0, s, g, ctx->st, owner, ctx->pool, ctx->pool_scales, im); break;
+    default: return fail(FERRY_EINVAL, "unsupported block size");
+  }
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_owner_import(ferry_ctx* ctx, uint32_t owner, const void* image, uint64_t image_bytes,
+                       void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = owner_check(ctx, owner, image, image_bytes)) return rc;
+  const Geo& g = ctx->g;
+  HIPC(hipSetDevice(ctx->device));
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t* im = (const uint8_t*)image;
+  const unsigned sets = (unsigned)(g.L * g.Hkv);
+  hipLaunchKernelGGL(k_owner_import_meta, dim3((sets + 3) / 4), dim3(256), 0, s, g, ctx->st, owner, im,
+                     ctx->err);
+  HIPC(hipGetLastError());
+  const uint64_t waves = (uint64_t)sets * g.C;
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  switch (g.bb / 1024) {
+    case 4: hipLaunchKernelGGL(k_owner_import_data<4>, grid, block, 0, s, g, ctx->st, owner, ctx->pool, ctx->pool_scales, im); break;
+    case 8: hipLaunchKernelGGL(k_owner_import_data<8>, grid, block, 0, s, g, ctx->st, owner, ctx->pool, ctx->pool_scales, im); break;
+    case 16: hipLaunchKernelGGL(k_owner_import_data<16>, grid, block, 0, s, g, ctx->st, owner, ctx->pool, ctx->pool_scales, im); break;
+    default: return fail(FERRY_EINVAL, "unsupported block size");
+  }
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
 int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, int iters,
                    uint64_t* bytes, float* ms, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;

@@ -274,6 +274,27 @@ int ferry_select_topk(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks,
 int ferry_select_topk_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
                              const int32_t* ctx_blocks, int mode, uint32_t* sel, void* stream);
 
+/* ---- owner hand-off (the per-GPU halves of moving a request) ----
+ * ferry_owner_export writes an image of one owner's sets: per (layer, kv
+ * head) set its LRU fill, order and tags, fp8 scales, and the bytes of its
+ * resident slots compacted in LRU order.  ferry_owner_import makes `owner`'s
+ * sets of this (or another) executor of the same geometry equal to the image:
+ * same fill, order, tags and slot ids, same pool bytes; the owner's previous
+ * blocks are forgotten.  `image` is device memory of at least
+ * ferry_owner_image_bytes (256-byte aligned).  Only the first part of the
+ * data area is used: the blocks resident in the owner, which is what crosses
+ * a link when the request moves.  An image that does not match this
+ * executor (geometry, dtype, slots, max_blocks) or is malformed latches
+ * FERRY_EINVAL and leaves the affected sets empty.  Replaces the delta
+ * migration of steal_from -- slot gather, transfer, slot scatter and
+ * kv_handoff(carry) (src/runtime/wla_multigpu.cuh:154-171, 1367-1428,
+ * 1970-1994); dropping a request's cache instead (kv_handoff without carry)
+ * is ferry_sets_reset_owners. */
+int ferry_owner_image_bytes(const ferry_ctx* ctx, uint64_t* bytes);
+int ferry_owner_export(ferry_ctx* ctx, uint32_t owner, void* image, uint64_t image_bytes, void* stream);
+int ferry_owner_import(ferry_ctx* ctx, uint32_t owner, const void* image, uint64_t image_bytes,
+                       void* stream);
+
 /* ---- bandwidth ceilings ----
  * Plain reads of the bytes the executor's kernels move, timed with HIP events
  * on `stream` over `iters` launches after one warm-up (synchronises):

@@ -682,6 +682,27 @@ int ora_exec_reset_owner(ora_exec* e, int owner) {
   return 0;
 }
 
+/* A request moved with its cache (kv_handoff with carry,
+ * src/runtime/wla_multigpu.cuh:1970-1994): the sets of owner `dst_owner` of
+ * `dst` become copies of the sets of `src_owner` of `src` (same geometry). */
+int ora_exec_copy_owner(const ora_exec* src, int src_owner, ora_exec* dst, int dst_owner) {
+  const ora_geom *a = &src->g, *b = &dst->g;
+  if (a->cap != b->cap || a->max_blocks != b->max_blocks || a->n_layers != b->n_layers ||
+      a->kv_heads != b->kv_heads || src_owner < 0 || src_owner >= ora_n_owners(a) ||
+      dst_owner < 0 || dst_owner >= ora_n_owners(b))
+    return -1;
+  const int per = a->n_layers * a->kv_heads;
+  for (int i = 0; i < per; ++i) {
+    const ora_lru* s = &src->sets[src_owner * per + i];
+    ora_lru* d = &dst->sets[dst_owner * per + i];
+    d->fill = s->fill;
+    memcpy(d->ord, s->ord, (size_t)s->cap * 4);
+    memcpy(d->tag, s->tag, (size_t)s->cap * 4);
+    memcpy(d->map, s->map, (size_t)s->max_blocks * 4);
+  }
+  return 0;
+}
+
 void ora_exec_state(const ora_exec* e, uint32_t* fill, uint32_t* ord,
                     uint32_t* tag) {
   const int ns = ora_n_sets(&e->g), cap = e->g.cap;

@@ -164,6 +164,8 @@ int ora_exec_step(ora_exec* e, const uint32_t* sel, uint32_t* slots_out,
                   uint8_t* flags);
 /* Empty the sets of one owner (a new request takes over its lane). */
 int ora_exec_reset_owner(ora_exec* e, int owner);
+/* Copy owner src_owner's sets of src onto owner dst_owner of dst. */
+int ora_exec_copy_owner(const ora_exec* src, int src_owner, ora_exec* dst, int dst_owner);
 /* Per-set state export for parity: fill[n_sets], ord[n_sets][cap],
  * tag[n_sets][cap]. */
 void ora_exec_state(const ora_exec* e, uint32_t* fill, uint32_t* ord,

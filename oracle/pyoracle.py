@@ -117,6 +117,7 @@ _sig("ora_exec_destroy", None, C.c_void_p)
 _sig("ora_exec_step", C.c_int, C.c_void_p, _u32p, _u32p, _u32p, _missp, _u64p, _u8p)
 _sig("ora_exec_state", None, C.c_void_p, _u32p, _u32p, _u32p)
 _sig("ora_exec_reset_owner", C.c_int, C.c_void_p, C.c_int)
+_sig("ora_exec_copy_owner", C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int)
 _sig("ora_arrivals", C.c_int, C.c_int, C.c_uint32, C.c_double, C.c_double, C.c_double,
      C.c_uint64, _f64p)
 _sig("ora_ctx_uniform", None, C.c_uint64, C.c_int, C.c_int, C.c_int, _i32p)
@@ -193,6 +194,10 @@ class Executor:
             raise RuntimeError(f"ora_exec_step rc={rc}")
         self.last_flags = flags
         return slots, mc, misses.reshape(self.n_sets, self.max_sel), counts
+
+    def copy_owner_from(self, src, src_owner, dst_owner):
+        if lib.ora_exec_copy_owner(src.ptr, src_owner, self.ptr, dst_owner):
+            raise ValueError("geometry or owner mismatch")
 
     def reset_owner(self, owner):
         if lib.ora_exec_reset_owner(self.ptr, owner):

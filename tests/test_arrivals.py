@@ -130,6 +130,39 @@ def test_reset_owner_makes_the_lane_cold():
     assert list(mc) == [0, 4]
 
 
+def test_copied_owner_behaves_like_its_source():
+    """After an owner's sets are copied into another executor's lane, the same
+    future selections give the same hits, slots and evictions there as in the
+    source lane (the state a hand-off must carry)."""
+    g = _geom(n_req=3, L=2, H=2, Hq=2, k=6, cap=10, mb=40)
+    rng = np.random.default_rng(3)
+    draw = lambda: np.stack([rng.choice(40, 6, replace=False) for _ in range(12)]).astype(np.uint32)
+    x, y = O.Executor(g), O.Executor(g)
+    for _ in range(5):
+        x.step(draw())
+    for _ in range(3):
+        y.step(draw())
+    y.copy_owner_from(x, 0, 2)
+    xf, xo, xt = x.state()
+    yf, yo, yt = y.state()
+    assert np.array_equal(yf[8:12], xf[0:4]) and np.array_equal(yt[8:12], xt[0:4])
+    for _ in range(6):
+        s = draw()
+        sx = s.copy()
+        sy = s.copy()
+        sy[8:12] = s[0:4]
+        xs, xmc, xm, _ = x.step(sx)
+        ys, ymc, ym, _ = y.step(sy)
+        # slots are global ids (set * cap + slot): lane 2's sets start 8 sets on
+        assert np.array_equal(ys.reshape(12, 6)[8:12] - 80, xs.reshape(12, 6)[0:4])
+        assert np.array_equal(ymc[8:12], xmc[0:4])
+        for a, b in zip(range(0, 4), range(8, 12)):
+            assert np.array_equal(ym[b, :ymc[b]][["block", "slot", "evicted"]],
+                                  xm[a, :xmc[a]][["block", "slot", "evicted"]])
+    with pytest.raises(ValueError):
+        y.copy_owner_from(O.Executor(_geom(n_req=3, L=2, H=2, Hq=2, k=6, cap=11, mb=40)), 0, 0)
+
+
 # ---------------------------------------------------------------- arrivals
 def test_steady_and_bursty_arrivals_closed_form():
     n, gap = 40, 2.5
