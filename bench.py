@@ -407,7 +407,17 @@ def run_handoff(a, ex, F, torch, stream, dtype):
     t_imp = ev[1].elapsed_time(ev[2]) / it
     per = ex.block_bytes + (8 if dtype == F.FP8 else 0)
     moved = 2 * resident * per
-    del img
+    # ceiling: a plain device-to-device copy of the same number of bytes
+    src = img[: resident * per]
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    ev[0].record(stream)
+    for _ in range(it):
+        dst.copy_(src)
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    copy_gbs = moved / (ev[0].elapsed_time(ev[1]) / it * 1e-3) / 1e9
+    del img, src, dst
     bb = ex.block_bytes // 1024
     return {"bound": "hbm", "kernel": f"k_owner_export_data<{bb}> + k_owner_import_data<{bb}>",
             "resident_blocks": resident, "image_gb": round(resident * per / 1e9, 3),
@@ -415,7 +425,8 @@ def run_handoff(a, ex, F, torch, stream, dtype):
             "export_gbs": round(moved / (t_exp * 1e-3) / 1e9, 1),
             "import_gbs": round(moved / (t_imp * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac_export": round(moved / (t_exp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "frac_import": round(moved / (t_imp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "frac_import": round(moved / (t_imp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "plain_copy_gbs": round(copy_gbs, 1)}
 
 
 def arrival_plan(a, w, F, n_ticks, zipf):
