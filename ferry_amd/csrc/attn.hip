@@ -89,7 +89,7 @@ struct Softmax {
 
 }  // namespace
 
-template <int DT, int G, int W>
+template <int DT, int G, int W, bool NT>
 __global__ __launch_bounds__(W * 64) void k_attn(Geo g, const float* __restrict__ q,
                                               const uint32_t* __restrict__ slots,
                                               const uint8_t* __restrict__ pool,
@@ -161,9 +161,9 @@ __global__ __launch_bounds__(W * 64) void k_attn(Geo g, const float* __restrict_
     const u32x4* kp = reinterpret_cast<const u32x4*>(pool + slot * g.bb);
     const u32x4* vp = kp + TILE_WORDS;
 #pragma unroll
-    for (int ld = 0; ld < NLD; ++ld) kb[b][ld] = kp[ld * 64 + lane];
+    for (int ld = 0; ld < NLD; ++ld) kb[b][ld] = load_kv<NT>(kp + ld * 64 + lane);
 #pragma unroll
-    for (int ld = 0; ld < NLD; ++ld) vb[b][ld] = vp[ld * 64 + lane];
+    for (int ld = 0; ld < NLD; ++ld) vb[b][ld] = load_kv<NT>(vp + ld * 64 + lane);
     if constexpr (DT == FERRY_FP8_E4M3) {
       ksb[b] = pool_scales[2 * slot] * 256.0f;
       vsb[b] = pool_scales[2 * slot + 1] * 256.0f;
@@ -280,10 +280,13 @@ __global__ __launch_bounds__(W * 64) void k_attn(Geo g, const float* __restrict_
   }
 }
 
-#define FERRY_ATTN_INST(DT, G, W)                                                       \
-  template __global__ void k_attn<DT, G, W>(Geo, const float*, const uint32_t*,          \
-                                            const uint8_t*, const float*, float*, float, \
-                                            int, int, int*);
+#define FERRY_ATTN_INST(DT, G, W)                                                          \
+  template __global__ void k_attn<DT, G, W, false>(Geo, const float*, const uint32_t*,        \
+                                                   const uint8_t*, const float*, float*, float, \
+                                                   int, int, int*);                            \
+  template __global__ void k_attn<DT, G, W, true>(Geo, const float*, const uint32_t*,         \
+                                                  const uint8_t*, const float*, float*, float,  \
+                                                  int, int, int*);
 #define FERRY_ATTN_INST_G(DT, W) \
   FERRY_ATTN_INST(DT, 1, W)      \
   FERRY_ATTN_INST(DT, 2, W)      \

@@ -74,7 +74,7 @@ __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 }  // namespace
 
-template <int DT, int G, int W>
+template <int DT, int G, int W, bool NT>
 __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __restrict__ q,
                                                    const uint32_t* __restrict__ slots,
                                                    const uint8_t* __restrict__ pool,
@@ -165,15 +165,15 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
     const uint8_t* base = pool + slot * g.bb;
 #pragma unroll
     for (int w = 0; w < NKW; ++w)
-      kw[w] = *reinterpret_cast<const u32x4*>(base + n * ROW + 16 * (4 * w + grp));
+      kw[w] = load_kv<NT>(reinterpret_cast<const u32x4*>(base + n * ROW + 16 * (4 * w + grp)));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint8_t* vp = base + KTILE + (4 * grp + i) * ROW + 8 * ES * n;
       if constexpr (F8) {
-        const u32x2 v = *reinterpret_cast<const u32x2*>(vp);
+        const u32x2 v = load_kv<NT>(reinterpret_cast<const u32x2*>(vp));
         vw[i][0] = v[0], vw[i][1] = v[1];
       } else {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(vp);
+        const u32x4 v = load_kv<NT>(reinterpret_cast<const u32x4*>(vp));
         vw[i][0] = v[0], vw[i][1] = v[1], vw[i][2] = v[2], vw[i][3] = v[3];
       }
     }
@@ -340,10 +340,13 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
   }
 }
 
-#define FERRY_ATTN_MFMA_INST(DT, G, W)                                                    \
-  template __global__ void k_attn_mfma<DT, G, W>(Geo, const float*, const uint32_t*,         \
-                                                 const uint8_t*, const float*, float*, float, \
-                                                 int, int, int*);
+#define FERRY_ATTN_MFMA_INST(DT, G, W)                                                     \
+  template __global__ void k_attn_mfma<DT, G, W, false>(Geo, const float*, const uint32_t*,   \
+                                                        const uint8_t*, const float*, float*,  \
+                                                        float, int, int, int*);                \
+  template __global__ void k_attn_mfma<DT, G, W, true>(Geo, const float*, const uint32_t*,    \
+                                                       const uint8_t*, const float*, float*,   \
+                                                       float, int, int, int*);
 #define FERRY_ATTN_MFMA_INST_G(DT, W) \
   FERRY_ATTN_MFMA_INST(DT, 2, W)      \
   FERRY_ATTN_MFMA_INST(DT, 4, W)      \

@@ -41,6 +41,23 @@ struct ImageHeader {
 
 __device__ inline ImageLayout image_layout(const Geo& g) { return make_image_layout(g); }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// One block by one wavefront, NV 16-byte words per lane.  Both sides are
+// streamed (non-temporal): each byte moves once, and the slots written here
+// are next read by attention, whose own non-temporal loads run slower when
+// the lines still sit in cache from ordinary stores.
+template <int NV>
+__device__ inline void copy_block(const uint8_t* src_b, uint8_t* dst_b, int lane) {
+  const u32x4* src = reinterpret_cast<const u32x4*>(src_b);
+  u32x4* dst = reinterpret_cast<u32x4*>(dst_b);
+  u32x4 r[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) r[v] = __builtin_nontemporal_load(src + v * kWave + lane);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) __builtin_nontemporal_store(r[v], dst + v * kWave + lane);
+}
+
 // Forget every block of one set (map entries of its tags, tags, order, fill).
 __device__ inline void clear_set(const Geo& g, SetState st, size_t set, int lane) {
   const uint32_t C = (uint32_t)g.C;
@@ -118,13 +135,7 @@ __global__ __launch_bounds__(256) void k_owner_export_data(Geo g, SetState st, u
       reinterpret_cast<float*>(image + lay.scales)[2 * pos + 1] = pool_scales[2 * gslot + 1];
     }
   }
-  const uint4* src = reinterpret_cast<const uint4*>(pool + gslot * g.bb);
-  uint4* dst = reinterpret_cast<uint4*>(image + lay.data + pos * g.bb);
-  uint4 r[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) r[v] = src[v * kWave + lane];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) dst[v * kWave + lane] = r[v];
+  copy_block<NV>(pool + gslot * g.bb, image + lay.data + pos * g.bb, lane);
 }
 
 // One wavefront per set of the importing owner: forget the set's blocks, check
@@ -207,13 +218,7 @@ __global__ __launch_bounds__(256) void k_owner_import_data(Geo g, SetState st, u
     pool_scales[2 * gslot] = reinterpret_cast<const float*>(image + lay.scales)[2 * pos];
     pool_scales[2 * gslot + 1] = reinterpret_cast<const float*>(image + lay.scales)[2 * pos + 1];
   }
-  const uint4* src = reinterpret_cast<const uint4*>(image + lay.data + pos * g.bb);
-  uint4* dst = reinterpret_cast<uint4*>(pool + gslot * g.bb);
-  uint4 r[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) r[v] = src[v * kWave + lane];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) dst[v * kWave + lane] = r[v];
+  copy_block<NV>(image + lay.data + pos * g.bb, pool + gslot * g.bb, lane);
 }
 
 #define FERRY_HANDOFF_INST(NV)                                                                    \

@@ -61,14 +61,15 @@ __global__ void k_missq_push(Geo g, Ring ring, const ferry_miss* m, uint32_t n, 
 // End of a decode step: last = blocks fetched in the step, then step_acc = 0.
 __global__ void k_step_close(unsigned long long* step_acc, unsigned long long* last);
 
-// Vector-ALU attention (attn.hip); W wavefronts per workgroup.
-template <int DT, int G, int W>
+// Vector-ALU attention (attn.hip); W wavefronts per workgroup; NT selects
+// non-temporal K/V loads.
+template <int DT, int G, int W, bool NT>
 __global__ void k_attn(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
                        const float* pool_scales, float* out, float qscale, int l0, int nl, int* err);
 
 // MFMA variant for GQA groups (G >= 2) of 16/8-bit KV (attn_mfma.hip); W
-// wavefronts per workgroup.
-template <int DT, int G, int W>
+// wavefronts per workgroup; NT as for k_attn.
+template <int DT, int G, int W, bool NT>
 __global__ void k_attn_mfma(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
                             const float* pool_scales, float* out, float qscale, int l0, int nl,
                             int* err);

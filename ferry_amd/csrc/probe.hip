@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256) void k_probe_gather(const uint8_t* __restrict_
     slot = slot < pool_slots ? slot : 0;
     const u32x4* p = reinterpret_cast<const u32x4*>(pool + slot * bb);
 #pragma unroll
-    for (int ld = 0; ld < NLD; ++ld) buf[b][ld] = p[ld * 64 + lane];
+    for (int ld = 0; ld < NLD; ++ld) buf[b][ld] = __builtin_nontemporal_load(p + ld * 64 + lane);
   };
   u32x4 acc = {0u, 0u, 0u, 0u};
   if (nb > 0) {

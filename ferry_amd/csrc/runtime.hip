@@ -85,6 +85,7 @@ struct ferry_ctx {
   uint64_t steps = 0;
   std::vector<hipEvent_t> events;  // layer-chunk pipeline of ferry_decode_step
   int attn_waves = 0;              // wavefronts per attention workgroup (FERRY_ATTN_WAVES), 0 = default
+  int attn_loads = 0;              // K/V loads (FERRY_ATTN_LOADS): 0 = by plan, 1 = nt, 2 = temporal
   uint32_t* probe_sink = nullptr;  // bandwidth probes: one word per row / wavefront
   size_t probe_sink_words = 0;
   uint8_t* probe_dst = nullptr;    // bandwidth probes: DMA destination
@@ -175,9 +176,11 @@ struct AttnArgs {
 // Which attention kernel runs and how many wavefronts share one (request,
 // layer, kv head) row.  MFMA for GQA groups of 16/8-bit KV unless the config
 // asks for the VALU kernel.  Four wavefronts per row; eight (FERRY_ATTN_WAVES=8)
-// measured the same on MI355X.
+// measured the same on MI355X.  K/V loads are non-temporal unless requests
+// share prefix-group sets (group > 1), whose blocks the member rows of one
+// launch re-read from cache; FERRY_ATTN_LOADS=nt|temporal overrides.
 struct AttnPlan {
-  bool mfma;
+  bool mfma, nt;
   int dtype, G, waves;
 };
 
@@ -189,32 +192,41 @@ AttnPlan attn_plan(const ferry_ctx* ctx) {
   p.mfma = g.dtype != FERRY_F32 && p.G >= 2 && ctx->cfg.attn != FERRY_ATTN_VALU;
   p.waves = 4;
   if (ctx->attn_waves == 8) p.waves = 8;
+  p.nt = ctx->attn_loads ? ctx->attn_loads == 1 : g.group == 1;
   return p;
 }
 
 template <int DT, int G, int W>
-void launch_valu(const dim3& grid, hipStream_t s, const AttnArgs& a) {
-  hipLaunchKernelGGL((k_attn<DT, G, W>), grid, dim3(W * 64), 0, s, a.g, a.q, a.slots, a.pool,
-                     a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
+void launch_valu(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs& a) {
+  if (p.nt)
+    hipLaunchKernelGGL((k_attn<DT, G, W, true>), grid, dim3(W * 64), 0, s, a.g, a.q, a.slots,
+                       a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
+  else
+    hipLaunchKernelGGL((k_attn<DT, G, W, false>), grid, dim3(W * 64), 0, s, a.g, a.q, a.slots,
+                       a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
 }
 template <int DT, int G, int W>
-void launch_mfma(const dim3& grid, hipStream_t s, const AttnArgs& a) {
-  hipLaunchKernelGGL((k_attn_mfma<DT, G, W>), grid, dim3(W * 64), 0, s, a.g, a.q, a.slots,
-                     a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
+void launch_mfma(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs& a) {
+  if (p.nt)
+    hipLaunchKernelGGL((k_attn_mfma<DT, G, W, true>), grid, dim3(W * 64), 0, s, a.g, a.q,
+                       a.slots, a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
+  else
+    hipLaunchKernelGGL((k_attn_mfma<DT, G, W, false>), grid, dim3(W * 64), 0, s, a.g, a.q,
+                       a.slots, a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
 }
 template <int DT, int G>
 void launch_g(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs& a) {
   if constexpr (DT != FERRY_F32 && G >= 2) {
     if (p.mfma) {
       switch (p.waves) {
-        case 8: launch_mfma<DT, G, 8>(grid, s, a); return;
-        default: launch_mfma<DT, G, 4>(grid, s, a); return;
+        case 8: launch_mfma<DT, G, 8>(p, grid, s, a); return;
+        default: launch_mfma<DT, G, 4>(p, grid, s, a); return;
       }
     }
   }
   switch (p.waves) {
-    case 8: launch_valu<DT, G, 8>(grid, s, a); return;
-    default: launch_valu<DT, G, 4>(grid, s, a); return;
+    case 8: launch_valu<DT, G, 8>(p, grid, s, a); return;
+    default: launch_valu<DT, G, 4>(p, grid, s, a); return;
   }
 }
 template <int DT>
@@ -251,6 +263,8 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   ferry_ctx* c = new ferry_ctx();
   c->cfg = *cfg;
   if (const char* e = std::getenv("FERRY_ATTN_WAVES")) c->attn_waves = std::atoi(e);
+  if (const char* e = std::getenv("FERRY_ATTN_LOADS"))
+    c->attn_loads = std::string(e) == "nt" ? 1 : (std::string(e) == "temporal" ? 2 : 0);
   c->device = device;
   Geo& g = c->g;
   g.n_req = cfg->n_req;

@@ -375,6 +375,31 @@ def test_mfma_attention_matches_oracle_and_valu(dtype, G):
     assert pm.ex.stats()["device_error"] == 0
 
 
+@pytest.mark.parametrize("dtype,G,attn", [(F.F32, 1, F.ATTN_AUTO), (F.F16, 1, F.ATTN_AUTO),
+                                           (F.BF16, 4, F.ATTN_VALU), (F.BF16, 4, F.ATTN_MFMA),
+                                           (F.FP8, 4, F.ATTN_MFMA), (F.FP8, 2, F.ATTN_VALU)])
+def test_attention_load_flavours_are_bit_identical(dtype, G, attn, monkeypatch):
+    # Non-temporal and temporal K/V loads differ only in cache policy: the
+    # outputs must be bit-identical, and both within tolerance of the oracle.
+    n_req, L, Hkv, k = 3, 2, 2, 13
+    mb, sels = _zipf_stream(n_req, L, Hkv, k, 40, 200, 2, seed=9)
+    outs = []
+    for flavour in ("nt", "temporal"):
+        monkeypatch.setenv("FERRY_ATTN_LOADS", flavour)
+        p = Pair(n_req, L, Hkv, Hkv * G, k, 32, mb, dtype, attn=attn)
+        for sel in sels:
+            p.step(sel)
+        p.check_attention(sels[-1], seed=5)
+        q = torch.from_numpy(np.random.default_rng(5).standard_normal(
+            (n_req, L, Hkv * G, 128)).astype(np.float32)).cuda()
+        out = torch.empty_like(q)
+        p.ex.sparse_decode(q, p.bufs["slots"], out)
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+        p.ex.close()
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_mfma_attention_long_selection():
     # k = 300 blocks per kv head: 75 blocks per wavefront, so the slot ids are
     # re-read past the first 64 (one per lane) inside the kernel.
