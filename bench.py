@@ -613,6 +613,11 @@ def main():
         with open(tpath) as f:
             r["roofline_select"]["traffic"] = json.load(f).get(a.workload + "_select", {}).get(
                 "bytes_per_launch")
+    if r.get("roofline_handoff") and os.path.exists(tpath):
+        with open(tpath) as f:
+            ho = json.load(f).get(a.workload + "_handoff")
+        r["roofline_handoff"]["traffic"] = (
+            {"export": ho["export_bytes"], "import": ho["import_bytes"]} if ho else None)
     lo, hi = w["ctx"]
     desc = (f"B={w['B']}, L={w['L']}, Hq={w['Hq']}, Hkv={w['Hkv']}, D=128, {w['dtype']} KV, "
             f"16-token blocks, ctx {'U[%d,%d]' % (lo * 16, hi * 16) if lo != hi else lo * 16} "
