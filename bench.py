@@ -26,7 +26,9 @@ Kernel rates come from HIP events around separate launches of each kernel:
   roofline_select top-k selection over every context block vs HBM
   roofline_handoff export / import of one owner's resident KV vs HBM
 cpu_baseline times the oracle's C restatement of the same step (1 thread) on
-2 of the requests (a whole prefix group for grouped workloads).
+2 of the requests (a whole prefix group for grouped workloads), and again on
+every usable host core (at most 16) with one replica of those requests per
+thread (`cpu_baseline.all_cores`).
 
 Other workloads (--workload): gqa128k (long-context GQA, bf16, ~30% misses),
 prefix_fp8 (shared-prefix groups, fp8 + scales, cross-request dedup), skew
@@ -208,12 +210,78 @@ def cpu_baseline(w, ctx, max_blocks, host_bytes, host_scales, host_blocks, n_req
             times.append(dt_s)
             misses.append(int(cnt[1]))
     t_step = float(np.mean(times))
-    return {"value": round(n_req / t_step, 3), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"oracle C step (bookkeeping + memcpy gather + fp32 attention) on "
-                      f"{n_req} of {w['B']} requests x {L} layers x {H} kv heads, {steps} steps "
-                      f"after one untimed cold step; {t_step * 1e3:.0f} ms/step",
-            "miss_blocks_per_s": round(float(np.mean(misses)) / t_step, 1),
-            "ms_per_step": round(t_step * 1e3, 1)}
+    res = {"value": round(n_req / t_step, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+           "sample": f"oracle C step (bookkeeping + memcpy gather + fp32 attention) on "
+                     f"{n_req} of {w['B']} requests x {L} layers x {H} kv heads, {steps} steps "
+                     f"after one untimed cold step; {t_step * 1e3:.0f} ms/step",
+           "miss_blocks_per_s": round(float(np.mean(misses)) / t_step, 1),
+           "ms_per_step": round(t_step * 1e3, 1)}
+    del pool, pscale, ex
+    res["all_cores"] = cpu_baseline_threads(g, sg_args=(n_req, L, H, k, ctx[:n_req], w, reuse_r),
+                                            host_bytes=host_bytes, host_scales=host_scales,
+                                            steps=steps, q=q)
+    return res
+
+
+def cpu_baseline_threads(g, sg_args, host_bytes, host_scales, steps, q):
+    """The same oracle step on every host core the process may use (at most 16,
+    the host share of one GPU): one independent replica of the sampled requests
+    per thread, all stepping concurrently (the C calls release the GIL)."""
+    import threading
+
+    from oracle import pyoracle as O
+
+    n_req, L, H, k, ctx, w, reuse_r = sg_args
+    T = max(1, min(16, len(os.sched_getaffinity(0))))
+    sg = O.selgen(n_req, L, H, k, ctx, dist=1, zipf_s=w["zipf"], reuse=w["reuse"],
+                  group=w["group"], prefix_blocks=w["prefix"], seed=3,
+                  reuse_r=None if reuse_r is None else reuse_r)
+    sels = [O.selgen_step(sg, t) for t in range(steps + 1)]
+    bb = O.lib.ora_block_bytes(O.C.byref(g))
+    reps = []
+    for _ in range(T):
+        ex = O.Executor(g)
+        reps.append(dict(ex=ex, pool=np.zeros(ex.n_sets * g.cap * bb, np.uint8),
+                         pscale=(np.zeros(ex.n_sets * g.cap * 2, np.float32)
+                                 if host_scales is not None else None),
+                         out=np.zeros(q.size, np.float32),
+                         slots=np.zeros(n_req * L * H * k, np.uint32),
+                         mc=np.zeros(ex.n_sets, np.uint32),
+                         ms=np.zeros(ex.n_sets * ex.max_sel, O.MISS_DTYPE),
+                         cnt=np.zeros(3, np.uint64), rc=0))
+    start = threading.Barrier(T + 1)
+    done = threading.Barrier(T + 1)
+
+    def worker(r):
+        def one(t):
+            rc = O.lib.ora_cpu_step(r["ex"].ptr, sels[t], host_bytes.ctypes.data,
+                                    None if host_scales is None else host_scales.ctypes.data,
+                                    r["pool"].ctypes.data,
+                                    None if r["pscale"] is None else r["pscale"].ctypes.data,
+                                    q.reshape(-1), r["out"], r["slots"], r["mc"], r["ms"], r["cnt"])
+            r["rc"] = r["rc"] or rc
+        one(0)  # cold fill, untimed
+        start.wait()
+        for t in range(1, steps + 1):
+            one(t)
+        done.wait()
+
+    th = [threading.Thread(target=worker, args=(r,)) for r in reps]
+    for t in th:
+        t.start()
+    start.wait()
+    t0 = time.perf_counter()
+    done.wait()
+    wall = time.perf_counter() - t0
+    for t in th:
+        t.join()
+    if any(r["rc"] for r in reps):
+        raise RuntimeError("ora_cpu_step failed in a worker thread")
+    return {"value": round(T * n_req * steps / wall, 3), "unit": "tok/s", "cores": T,
+            "sample": f"{T} threads, each an independent replica of the same {n_req} requests, "
+                      f"{steps} concurrent steps after one untimed cold step; "
+                      f"{wall / steps * 1e3:.0f} ms per concurrent step",
+            "ms_per_step": round(wall / steps * 1e3, 1)}
 
 
 def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_cpu=True):
