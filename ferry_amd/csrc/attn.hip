@@ -141,8 +141,10 @@ __global__ __launch_bounds__(W * 64) void k_attn(Geo g, const float* __restrict_
   // Ring of NPF block buffers (NPF = 1: load, then consume).  While block j
   // (= wave + W*j of the row) is consumed, blocks j+1 .. j+NPF-1 are in flight;
   // the loop is unrolled by NPF so every buffer index is static, and every
-  // iteration issues its load (past the end it re-reads the last block, an L2
-  // hit) so the compiler's load counters stay exact.
+  // iteration issues its loads so the compiler's load counters stay exact.
+  // Past the end of the row those loads are never consumed: every lane then
+  // reads the same 16 bytes of the last block, one line per instruction
+  // (non-temporal loads would not find a re-read whole block in cache).
   const int nb = k > wave ? (k - wave + W - 1) / W : 0;
   // A slot outside the pool is read as slot 0 and reported once at the end
   // (no branch in the block loop).
@@ -160,10 +162,11 @@ __global__ __launch_bounds__(W * 64) void k_attn(Geo g, const float* __restrict_
     const uint64_t slot = slot_at(j);
     const u32x4* kp = reinterpret_cast<const u32x4*>(pool + slot * g.bb);
     const u32x4* vp = kp + TILE_WORDS;
+    const int live = j < nb ? 1 : 0;  // wave-uniform
 #pragma unroll
-    for (int ld = 0; ld < NLD; ++ld) kb[b][ld] = load_kv<NT>(kp + ld * 64 + lane);
+    for (int ld = 0; ld < NLD; ++ld) kb[b][ld] = load_kv<NT>(kp + (ld * 64 + lane) * live);
 #pragma unroll
-    for (int ld = 0; ld < NLD; ++ld) vb[b][ld] = load_kv<NT>(vp + ld * 64 + lane);
+    for (int ld = 0; ld < NLD; ++ld) vb[b][ld] = load_kv<NT>(vp + (ld * 64 + lane) * live);
     if constexpr (DT == FERRY_FP8_E4M3) {
       ksb[b] = pool_scales[2 * slot] * 256.0f;
       vsb[b] = pool_scales[2 * slot + 1] * 256.0f;

@@ -161,14 +161,17 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
   // K words: token n, byte offset 16*(4*w + grp) of its row.  V words: tokens
   // 4*grp+i, bytes [8n, 8n+8) elements of the row (16 B for 16-bit, 8 B fp8).
   constexpr int VW = F8 ? 2 : 4;  // dwords of V per token per lane
-  auto load_block = [&](uint64_t slot, u32x4* kw, uint32_t (*vw)[VW]) {
+  // live = 0 (past the end of the row; the loads are never consumed): every
+  // lane reads the block's first 16 bytes, one line per instruction.
+  auto load_block = [&](uint64_t slot, int live, u32x4* kw, uint32_t (*vw)[VW]) {
     const uint8_t* base = pool + slot * g.bb;
 #pragma unroll
     for (int w = 0; w < NKW; ++w)
-      kw[w] = load_kv<NT>(reinterpret_cast<const u32x4*>(base + n * ROW + 16 * (4 * w + grp)));
+      kw[w] = load_kv<NT>(
+          reinterpret_cast<const u32x4*>(base + (n * ROW + 16 * (4 * w + grp)) * live));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint8_t* vp = base + KTILE + (4 * grp + i) * ROW + 8 * ES * n;
+      const uint8_t* vp = base + (KTILE + (4 * grp + i) * ROW + 8 * ES * n) * live;
       if constexpr (F8) {
         const u32x2 v = load_kv<NT>(reinterpret_cast<const u32x2*>(vp));
         vw[i][0] = v[0], vw[i][1] = v[1];
@@ -181,15 +184,15 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
 
   // Ring of NPF block buffers: while block j (= wave + W*j of the row) is
   // consumed, blocks j+1 .. j+NPF-1 are in flight.  The loop is unrolled by NPF
-  // so every buffer index is static, and every iteration issues its load (past
-  // the end it re-reads the last block, an L2 hit) so the compiler's load
-  // counters stay exact.
+  // so every buffer index is static, and every iteration issues its loads (past
+  // the end, one line of the last block) so the compiler's load counters stay
+  // exact.
   u32x4 kb[NPF][NKW];
   uint32_t vb[NPF][4][VW];
   float ksb[NPF], vsb[NPF];
   auto issue = [&](int j, int b) {
     const uint64_t slot = slot_at(j);
-    load_block(slot, kb[b], vb[b]);
+    load_block(slot, j < nblk ? 1 : 0, kb[b], vb[b]);
     if constexpr (F8) {
       ksb[b] = pool_scales[2 * slot];
       vsb[b] = pool_scales[2 * slot + 1];

@@ -5,7 +5,8 @@
 // achieved rate can be read against what plain reads reach on the same part:
 //  * k_probe_gather: the attention kernels' loads (the k pool slots of every
 //    (request, layer, kv head) row, ids staged in LDS, a two-block ring per
-//    wavefront) with the softmax and products replaced by an XOR;
+//    wavefront, non-temporal 16-byte loads) with the softmax and products
+//    replaced by an XOR;
 //  * k_probe_host: device-direct 16-byte reads of consecutive host-tier
 //    blocks over the host link, as the fetch kernel issues them, without the
 //    ring bookkeeping or the pool writes.
@@ -40,8 +41,10 @@ __global__ __launch_bounds__(256) void k_probe_gather(const uint8_t* __restrict_
     uint64_t slot = (uint32_t)__builtin_amdgcn_readfirstlane((int)ids[wave + W * min(j, nb - 1)]);
     slot = slot < pool_slots ? slot : 0;
     const u32x4* p = reinterpret_cast<const u32x4*>(pool + slot * bb);
+    const int live = j < nb ? 1 : 0;  // past the end: one line per instruction
 #pragma unroll
-    for (int ld = 0; ld < NLD; ++ld) buf[b][ld] = __builtin_nontemporal_load(p + ld * 64 + lane);
+    for (int ld = 0; ld < NLD; ++ld)
+      buf[b][ld] = __builtin_nontemporal_load(p + (ld * 64 + lane) * live);
   };
   u32x4 acc = {0u, 0u, 0u, 0u};
   if (nb > 0) {
