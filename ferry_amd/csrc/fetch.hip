@@ -1,16 +1,20 @@
 // fetch.hip -- drain of the device miss ring into the HBM slot pool.
 //
 // Persistent workgroups, one deque each.  Every wavefront pops one miss at a
-// time from its own deque head; when that is empty it looks for a victim and
-// steals min(max(rem/2, 1), steal_chunk) entries from its tail, never more
-// than rem/2+1 (the reference's steal bound, src/runtime/wla_multigpu.cuh:
+// time from its own deque head; when that is empty it looks for a victim with
+// more than its fair share ceil(remaining / deques) and steals
+// min(steal_chunk, rem - fair, rem/2 + 1) entries from its tail (the
+// reference's excess rule and take, src/runtime/wla_multigpu.cuh:882-884,
 // 1147-1152, 1518-1526; src/runtime/multigpu.cuh:153-175).  Victims are
 // searched 64 deques at a time (one per lane), starting at a window that
-// differs per wavefront, and the fullest deque of the first non-empty window
-// is robbed: thieves spread over the victims instead of all racing for the
-// single fullest deque, which serialised the end of every drain.  A thief
-// whose CAS loses backs off briefly.  A wavefront stops after a scan of all
-// deques finds them empty.  A miss is copied by one wavefront: 16-byte loads straight from
+// differs per wavefront, and the fullest deque of the first window with an
+// excess is robbed: thieves spread over the victims instead of all racing for
+// the single fullest deque.  A thief whose CAS loses backs off briefly.  A
+// wavefront stops when no deque holds twice its fair share (and two entries
+// per wavefront of a workgroup more): a balanced drain's entries stay with
+// their own deque's wavefronts (measured at the 7B shape: stealing on every
+// excess made the step 4.5% slower than no stealing), while skewed deques are
+// still robbed.  A miss is copied by one wavefront: 16-byte loads straight from
 // the pinned host tier (one PCIe hop, no staging ring, unlike
 // HostStagedChannel::submit, src/comm/host_staged_channel.cpp:43-74) into the
 // slot.  The last workgroup to finish accounts the drain and rewinds every
@@ -50,6 +54,33 @@ __device__ inline ferry_miss load_entry(const ferry_miss* p) {
   return m;
 }
 
+// K consecutive ring entries copied by one wavefront with all K blocks in
+// flight at once (a thief's stolen range; its own deque's entries come one at a
+// time, shared with the other wavefronts of its workgroup).
+template <int NV, int K>
+__device__ inline void copy_blocks(const FetchArgs& a, const ferry_miss* e, int lane) {
+  ferry_miss m[K];
+#pragma unroll
+  for (int b = 0; b < K; ++b) m[b] = load_entry(e + b);
+  u32x4 r[K][NV];
+  uint64_t h[K];
+#pragma unroll
+  for (int b = 0; b < K; ++b) {
+    h[b] = host_index(m[b].set, m[b].block, (uint64_t)a.g.max_blocks, a.g.host_blocks);
+    const u32x4* src = reinterpret_cast<const u32x4*>(a.host + h[b] * a.g.bb);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) r[b][i] = __builtin_nontemporal_load(src + i * kWave + lane);
+  }
+#pragma unroll
+  for (int b = 0; b < K; ++b) {
+    const uint64_t slot = (uint64_t)m[b].set * (uint64_t)a.g.C + m[b].slot;
+    u32x4* dst = reinterpret_cast<u32x4*>(a.pool + slot * a.g.bb);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) __builtin_nontemporal_store(r[b][i], dst + i * kWave + lane);
+    if (a.pool_scales && lane < 2) a.pool_scales[slot * 2 + lane] = a.host_scales[h[b] * 2 + lane];
+  }
+}
+
 }  // namespace
 
 template <int NV>
@@ -71,12 +102,12 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
     uint32_t idx = 0;
     if (lane == 0) {
       const uint32_t capw = a.ring.cap[me];
-      uint64_t st = aload64(state + me);
+      uint64_t st = aload64(state + (size_t)me * kStateStride);
       for (int tries = 0; tries < (1 << 20); ++tries) {
         const uint32_t h = (uint32_t)st;
         const uint32_t t = min((uint32_t)(st >> 32), capw);
         if (h >= t) break;
-        const uint64_t prev = atomicCAS((unsigned long long*)(state + me), st, st + 1);
+        const uint64_t prev = atomicCAS((unsigned long long*)(state + (size_t)me * kStateStride), st, st + 1);
         if (prev == st) {
           got = 1;
           idx = h;
@@ -93,22 +124,40 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
       continue;
     }
     if (!a.steal) break;
-    // victim = fullest deque of the first non-empty 64-deque window, windows
-    // visited from this wavefront's own starting point
-    uint32_t best = 0;
-    int bw = W;
+    // Fair share = ceil(remaining / deques), from one pass over every deque.
+    // The victim is the fullest deque of the first 64-deque window, visited
+    // from this wavefront's own starting point, that holds more than its fair
+    // share: thieves spread over the victims instead of racing for one.  No
+    // deque above its share (a balanced drain's end): the wavefront leaves the
+    // rest to the deques' own wavefronts.
     const int nwin = (W + kWave - 1) / kWave;
     const int wave_id = me * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
+    auto rem_of = [&](int w) -> uint32_t {
+      if (w >= W) return 0u;
+      const uint64_t st = aload64(state + (size_t)w * kStateStride);
+      const uint32_t h = (uint32_t)st, t = min((uint32_t)(st >> 32), a.ring.cap[w]);
+      return t > h ? t - h : 0u;
+    };
+    uint64_t total = 0;
+    for (int i = 0; i < nwin; ++i) total += rem_of(i * kWave + lane);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
+    total = first_lane_u64(total);
+    if (total == 0) break;  // every deque is drained
+    const uint32_t fair = (uint32_t)((total + (uint64_t)W - 1) / (uint64_t)W);
+    // A victim must hold at least twice its share, and two entries per
+    // wavefront of a workgroup above it.  The link, not the wavefronts, bounds
+    // a drain: a deque a few entries or percent above the others finishes with
+    // them, and robbing it only adds atomics and a late copy; a deque holding
+    // several shares (skewed, request-affine misses) would end the drain late.
+    const uint32_t floor_rem = max(2u * fair, fair + 2u * (blockDim.x >> 6));
+    uint32_t best = 0;
+    int bw = W;
     for (int i = 0; i < nwin && best == 0; ++i) {
       const int w = ((wave_id + i) % nwin) * kWave + lane;
-      uint32_t rem = 0;
-      if (w < W) {
-        const uint64_t st = aload64(state + w);
-        const uint32_t h = (uint32_t)st, t = min((uint32_t)(st >> 32), a.ring.cap[w]);
-        rem = t > h ? t - h : 0;
-      }
-      best = rem;
-      bw = rem ? w : W;
+      const uint32_t rem = rem_of(w);
+      best = rem > floor_rem ? rem : 0u;
+      bw = best ? w : W;
 #pragma unroll
       for (int off = 32; off > 0; off >>= 1) {
         const uint32_t ob = __shfl_xor(best, off);
@@ -121,17 +170,18 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
       best = first_lane_u(best);
       bw = first_lane_i(bw);
     }
-    if (best == 0) break;  // every deque is drained
+    if (best == 0) break;  // no deque far enough above its fair share
     int ok = 0;
     uint32_t s0 = 0, s1 = 0;
     if (lane == 0) {
-      const uint64_t st = aload64(state + bw);
+      const uint64_t st = aload64(state + (size_t)bw * kStateStride);
       const uint32_t h = (uint32_t)st, t = min((uint32_t)(st >> 32), a.ring.cap[bw]);
-      if (t > h) {
-        const uint32_t rem = t - h;
-        const uint32_t m = min(max(rem / 2, 1u), a.steal_chunk);
+      const uint32_t rem = t > h ? t - h : 0u;
+      if (rem > floor_rem) {
+        // the reference's take: min(k, cur - fair, cur/2 + 1)
+        const uint32_t m = min(min(a.steal_chunk, rem - fair), rem / 2 + 1);
         const uint64_t nst = ((uint64_t)(t - m) << 32) | h;
-        if (atomicCAS((unsigned long long*)(state + bw), st, nst) == st) {
+        if (atomicCAS((unsigned long long*)(state + (size_t)bw * kStateStride), st, nst) == st) {
           ok = 1;
           s0 = t - m;
           s1 = t;
@@ -146,7 +196,10 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
     s0 = first_lane_u(s0);
     s1 = first_lane_u(s1);
     const ferry_miss* seg = a.ring.entries + a.ring.seg[bw];
-    for (uint32_t i = s0; i < s1; ++i) copy_block<NV>(a, load_entry(seg + i), lane);
+    constexpr int KS = NV <= 8 ? 4 : 2;  // stolen blocks in flight (registers: KS * NV * 4)
+    uint32_t i = s0;
+    for (; i + KS <= s1; i += KS) copy_blocks<NV, KS>(a, seg + i, lane);
+    for (; i < s1; ++i) copy_block<NV>(a, load_entry(seg + i), lane);
     ++steals;
     stolen += s1 - s0;
     copied += s1 - s0;
@@ -164,7 +217,7 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
     const uint32_t prev = atomicAdd(a.done, 1u);
     if (prev == (uint32_t)W - 1) {
       __threadfence();
-      for (int w = 0; w < W; ++w) astore64(state + w, 0ull);
+      for (int w = 0; w < W; ++w) astore64(state + (size_t)w * kStateStride, 0ull);
       const unsigned long long total = atomicExch(a.stats + kStatDrain, 0ull);
       atomicAdd(a.stats + kStatMisses, total);
       atomicAdd(a.stats + kStatBytes, total * a.g.bb);
@@ -198,7 +251,7 @@ __global__ void k_missq_push(Geo g, Ring ring, const ferry_miss* m, uint32_t n, 
     return;
   }
   const uint32_t w = ring.worker_of_set[e.set];
-  const uint64_t old = atomicAdd((unsigned long long*)(ring.state + w), 1ull << 32);
+  const uint64_t old = atomicAdd((unsigned long long*)(ring.state + (size_t)w * kStateStride), 1ull << 32);
   const uint32_t t = (uint32_t)(old >> 32);
   if (t >= ring.cap[w]) {
     set_error(err, FERRY_ESPIN);

@@ -16,6 +16,11 @@ struct SetState {
 // Device miss ring: one deque per fetch worker, each a fixed segment of
 // `entries`.  state[w] packs (tail << 32 | head) relative to the segment, so
 // owner pops (head++) and thief steals (tail -= m) are single 64-bit CASes.
+// Deque w's state word (head | tail << 32) is state[w * kStateStride]: one
+// 128-byte line per deque, so owners' pops, pushes and thieves' scans of
+// different deques do not contend for the same L2 lines.
+constexpr int kStateStride = 16;
+
 struct Ring {
   ferry_miss* entries;
   uint64_t* state;

@@ -100,7 +100,8 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
   if (M > 0) {
     uint64_t old = 0;
     if (lane == 0)
-      old = atomicAdd((unsigned long long*)(ring.state + worker), (unsigned long long)M << 32);
+      old = atomicAdd((unsigned long long*)(ring.state + (size_t)worker * kStateStride),
+                      (unsigned long long)M << 32);
     const uint32_t t0 = (uint32_t)(first_lane_u64(old) >> 32);
     if (t0 + (uint32_t)M > ring.cap[worker]) {
       for (int q = lane; q < M; q += kWave) astore(map + smblk[q], kNone);

@@ -155,6 +155,19 @@ void release(ferry_ctx* c) {
   delete c;
 }
 
+// Spread assignment hashes the set id (lowbias32, C. Wellons' published
+// 32-bit integer hash).  Set id modulo the worker count put every owner's
+// sets of one layer range on the same few workers whenever L * Hkv is a
+// multiple of it, so a layer chunk's misses filled a quarter of the deques.
+uint32_t spread_hash(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
 int check_ctx(const ferry_ctx* c) { return c ? FERRY_OK : fail(FERRY_EINVAL, "null context"); }
 
 }  // namespace
@@ -289,7 +302,11 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1)
     cus = 256;
-  g.workers = cfg->fetch_workers > 0 ? cfg->fetch_workers : 2 * cus;
+  // One fetch workgroup per 4 CUs by default: 256 wavefronts with a block each
+  // in flight fill the host link (57.5 GB/s at the 7B shape, against 55 GB/s
+  // with 2 per CU), and the CUs they leave idle run the attention that
+  // overlaps the fetch (the 7B step: 64.2 ms, against 67-68 ms).
+  g.workers = cfg->fetch_workers > 0 ? cfg->fetch_workers : std::max(1, cus / 4);
   if ((uint64_t)g.n_sets * (uint64_t)g.C >= 0xFFFFFFFFull ||
       (uint64_t)g.n_sets * (uint64_t)g.max_sel >= 0xFFFFFFFFull) {
     delete c;
@@ -325,7 +342,8 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   std::vector<uint32_t> wos(g.n_sets), cnt(W, 0), seg(W, 0), cap(W, 0);
   for (int s = 0; s < g.n_sets; ++s) {
     const int owner = s / (g.L * g.Hkv);
-    wos[s] = (uint32_t)((cfg->assign == FERRY_ASSIGN_AFFINITY ? owner : s) % W);
+    wos[s] = cfg->assign == FERRY_ASSIGN_AFFINITY ? (uint32_t)(owner % W)
+                                                  : spread_hash((uint32_t)s) % (uint32_t)W;
     cnt[wos[s]]++;
   }
   uint64_t total = 0;
@@ -335,7 +353,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
     total += cap[w];
   }
   TRY(dalloc(&c->ring_entries, total));
-  TRY(dalloc(&c->ring_state, W));
+  TRY(dalloc(&c->ring_state, (size_t)W * kStateStride));
   TRY(dalloc(&c->ring_seg, W));
   TRY(dalloc(&c->ring_cap, W));
   TRY(dalloc(&c->worker_of_set, g.n_sets));
@@ -355,7 +373,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   HIPT(hipMemcpy(c->ring_seg, seg.data(), W * 4, hipMemcpyHostToDevice));
   HIPT(hipMemcpy(c->ring_cap, cap.data(), W * 4, hipMemcpyHostToDevice));
   HIPT(hipMemcpy(c->worker_of_set, wos.data(), (size_t)g.n_sets * 4, hipMemcpyHostToDevice));
-  HIPT(hipMemset(c->ring_state, 0, W * 8));
+  HIPT(hipMemset(c->ring_state, 0, (size_t)W * kStateStride * 8));
   HIPT(hipMemset(c->stats, 0, kStatCount * 8));
   HIPT(hipMemset(c->sel_counts, 0, (size_t)kSelCounters * kSelStride * 8));
   HIPT(hipMemset(c->step_acc, 0, 16));

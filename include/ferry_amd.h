@@ -43,7 +43,7 @@ extern "C" {
 #define FERRY_LRU_SERIAL 1 /* one update per selection: replay_miss_stream/kv_touch */
 
 /* ---- miss -> fetch-worker assignment ---- */
-#define FERRY_ASSIGN_SPREAD 0   /* set id modulo workers */
+#define FERRY_ASSIGN_SPREAD 0   /* hash of the set id modulo workers */
 #define FERRY_ASSIGN_AFFINITY 1 /* request (owner) modulo workers */
 
 /* ---- attention kernel selection ---- */
@@ -72,7 +72,7 @@ typedef struct ferry_config {
   uint64_t host_blocks;  /* host-tier capacity in blocks (aliased modulo) */
   uint64_t host_seed;    /* host-tier content seed */
   float value_std;       /* standard deviation of K/V values */
-  int32_t fetch_workers; /* persistent fetch workgroups; 0 = 2 per CU */
+  int32_t fetch_workers; /* persistent fetch workgroups; 0 = 1 per 4 CUs */
   int32_t steal;         /* 1 = fetch workers steal from each other */
   int32_t assign;        /* FERRY_ASSIGN_SPREAD or FERRY_ASSIGN_AFFINITY */
   int32_t attn;          /* FERRY_ATTN_AUTO, FERRY_ATTN_VALU or FERRY_ATTN_MFMA */
