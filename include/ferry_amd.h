@@ -188,9 +188,10 @@ int ferry_bookkeep_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const uint32_t
 int ferry_missq_push(ferry_ctx* ctx, const ferry_miss* misses, uint32_t n,
                      void* stream);
 /* Drain the ring: persistent workgroups pop their own deque and steal from
- * the fullest peer's tail.  Replaces HostStagedChannel::submit/sync
- * (src/comm/host_staged_channel.cpp:43-87) and the cross-GPU steal rules
- * (src/runtime/wla_multigpu.cuh:1147-1152, 1518-1526). */
+ * the tail of a peer holding at least twice its fair share.  Replaces
+ * HostStagedChannel::submit/sync (src/comm/host_staged_channel.cpp:43-87) and
+ * the cross-GPU steal rules (src/runtime/wla_multigpu.cuh:882-884, 1147-1152,
+ * 1518-1526). */
 int ferry_missq_drain(ferry_ctx* ctx, void* stream);
 
 /* Block-sparse decode attention over the selected blocks:
