@@ -103,6 +103,65 @@ __device__ inline float row16_sum(float v) {
   return v;
 }
 
+template <int X>
+__device__ inline float swz_xor(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), (X << 10) | 0x1F));
+}
+
+// One transposition level of the G-head reduction over a 16-lane row: a lane
+// holding N head partials keeps the lower half (bit X of its row position
+// clear) or the upper half, and adds the partner's partials of the same heads,
+// own value first, as the plain butterfly's step X does.
+template <int X, int N>
+__device__ inline void transpose_level(float* v, int p) {
+  const bool hi = (p & X) != 0;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float send = hi ? v[i] : v[i + N / 2];
+    const float keep = hi ? v[i + N / 2] : v[i];
+    v[i] = keep + swz_xor<X>(send);
+  }
+}
+
+// The Quest bound of every query head (acc[h]: this lane's 8-dim partial of
+// head h) summed over the 16 lanes of the row, and their maximum taken in head
+// order, valid in the row's lane 0.  With one head this is the xor 8, 4, 2, 1
+// butterfly.  With G heads the first log2(G) levels are transposed, so each
+// sum is formed in one lane group instead of all 16 lanes (G = 4: 5 swizzles
+// and 5 adds instead of 16 and 16); every sum is the same additions in the
+// same order as the butterfly's, and the maximum is the same chain, so the
+// result is bit-identical.  Head h ends in lane h * 16 / G of the row.
+template <int G>
+__device__ inline float heads_bound_max(float (&acc)[G], int p) {
+  if constexpr (G == 1) {
+    return row16_sum(acc[0]);
+  } else {
+    transpose_level<8, G>(acc, p);
+    if constexpr (G >= 4) transpose_level<4, G / 2>(acc, p);
+    if constexpr (G >= 8) transpose_level<2, G / 4>(acc, p);
+    float v = acc[0];
+    if constexpr (G < 4) v += swz_xor<4>(v);
+    if constexpr (G < 8) v += swz_xor<2>(v);
+    v += swz_xor<1>(v);
+    float sk = v;
+#pragma unroll
+    for (int h = 1; h < G; ++h) {
+      float other;
+      switch (h * 16 / G) {  // compile-time after unrolling
+        case 2: other = swz_xor<2>(v); break;
+        case 4: other = swz_xor<4>(v); break;
+        case 6: other = swz_xor<6>(v); break;
+        case 8: other = swz_xor<8>(v); break;
+        case 10: other = swz_xor<10>(v); break;
+        case 12: other = swz_xor<12>(v); break;
+        default: other = swz_xor<14>(v); break;
+      }
+      sk = fmax_det(other, sk);
+    }
+    return sk;
+  }
+}
+
 // Inclusive scan of (a, b) over the NT threads of the workgroup; wtot is LDS
 // scratch of 2*W words.  Returns the exclusive prefixes.
 template <int W>
@@ -255,38 +314,51 @@ __global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __re
       for (int i = tid; i < Gq * D; i += NT) qs[i] = q[(size_t)rl * g.Hq * D + i];
       __syncthreads();
     }
-    for (int b0 = 4 * wave; b0 < n; b0 += 4 * W) {
-      const int b = b0 + grp;
-      const bool live = b < n;
-      float score = 0.0f;
+    // U passes of 4 blocks per wavefront are loaded before any is scored: the
+    // keys take most of the LDS at long contexts, so few workgroups share a
+    // CU and each wavefront must keep several records in flight
+    constexpr int U = G >= 8 ? 2 : 4;
+    for (int b0 = 4 * wave; b0 < n; b0 += 4 * W * U) {
+      float score[U];
       for (int hh = 0; hh < nkv; ++hh) {
         const int hk = LAYER ? hh : hrow;
         const uint64_t set = (uint64_t)rl * g.Hkv + hk;
-        const uint64_t hb = host_index(set, live ? (uint32_t)b : 0u, (uint64_t)g.max_blocks, sum_mod);
-        const uint8_t* rec = sums + hb * REC;
-        float kmn[8], kmx[8];
-        load8<DT>(rec, 8 * p, kmn);
-        load8<DT>(rec, D + 8 * p, kmx);
+        float kmn[U][8], kmx[U][8];
+        uint64_t hbs[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int b = b0 + 4 * W * u + grp;
+          hbs[u] = host_index(set, b < n ? (uint32_t)b : 0u, (uint64_t)g.max_blocks, sum_mod);
+          const uint8_t* rec = sums + hbs[u] * REC;
+          load8<DT>(rec, 8 * p, kmn[u]);
+          load8<DT>(rec, D + 8 * p, kmx[u]);
+        }
         if (LAYER) {
 #pragma unroll
           for (int gq = 0; gq < G; ++gq)
 #pragma unroll
             for (int e = 0; e < 8; ++e) qr[gq][e] = qs[(hh * G + gq) * D + 8 * p + e];
         }
-        float sk = 0.0f;
 #pragma unroll
-        for (int gq = 0; gq < G; ++gq) {
-          float acc = 0.0f;
+        for (int u = 0; u < U; ++u) {
+          float acc[G];
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            acc = __fmaf_rn(qr[gq][e], qr[gq][e] >= 0.0f ? kmx[e] : kmn[e], acc);
-          const float bound = row16_sum(acc);
-          sk = gq == 0 ? bound : fmax_det(bound, sk);
+          for (int gq = 0; gq < G; ++gq) {
+            acc[gq] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              acc[gq] = __fmaf_rn(qr[gq][e], qr[gq][e] >= 0.0f ? kmx[u][e] : kmn[u][e], acc[gq]);
+          }
+          float sk = heads_bound_max<G>(acc, p);
+          if constexpr (DT == FERRY_FP8_E4M3) sk = __fmul_rn(sk, sum_scales[hbs[u]]);
+          score[u] = hh == 0 ? sk : fmax_det(sk, score[u]);
         }
-        if constexpr (DT == FERRY_FP8_E4M3) sk = __fmul_rn(sk, sum_scales[hb]);
-        score = hh == 0 ? sk : fmax_det(sk, score);
       }
-      if (live && p == 0) keys[b] = fkey(score);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int b = b0 + 4 * W * u + grp;
+        if (b < n && p == 0) keys[b] = fkey(score[u]);
+      }
     }
     __syncthreads();
     // ---- phase 2: the kk-th largest key (radix select, 8 bits per pass)
