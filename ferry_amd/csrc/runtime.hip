@@ -623,12 +623,38 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
   if (int rc = check_ctx(ctx)) return rc;
   const int L = ctx->g.L;
   if (chunks < 0) return fail(FERRY_EINVAL, "chunks < 0");
-  if (chunks == 0) {  // adaptive: from the blocks the last finished step fetched
-    const uint64_t last = *reinterpret_cast<volatile unsigned long long*>(ctx->pend_host);
+  const bool adaptive = chunks == 0;
+  uint64_t last = 0;
+  if (adaptive) {  // from the blocks the last finished step fetched
+    last = *reinterpret_cast<volatile unsigned long long*>(ctx->pend_host);
     if (int rc = ferry_decode_chunks(ctx, last, &chunks)) return rc;
   }
   chunks = std::min(chunks, L);
-  const int per = (L + chunks - 1) / chunks;
+  // Layer ranges: `chunks` even ranges, except that the adaptive count also
+  // shortens the last one.  Its attention is the one the fetch cannot hide;
+  // the range before it attends while the last range is fetched, which takes
+  // longer as long as the last range has at least 2 r times its layers, r =
+  // (attention time) / (fetch time) of a layer at typical MI355X rates
+  // (6.5 TB/s HBM reads, 55 GB/s host link; 2 for the slowdown of sharing the
+  // GPU with the fetch).  At the 7B shape r = 0.08: the last range is one layer.
+  std::vector<int> first(chunks + 1, L);
+  {
+    int tail = (L + chunks - 1) / chunks;
+    if (adaptive && chunks >= 2 && last > 0) {
+      const Geo& g = ctx->g;
+      const double kv = (double)g.bb + (g.dtype == FERRY_FP8_E4M3 ? 8.0 : 0.0);
+      const double attn_s = (double)g.n_req * g.L * g.Hkv * g.k * kv / 6.5e12;
+      const double fetch_s = (double)last * (double)g.bb / 55e9;
+      const int rest = (L - 1 + chunks - 2) / (chunks - 1);  // layers of the other ranges
+      const double want = std::ceil(2.0 * attn_s / fetch_s * rest);
+      if (want < (double)tail) tail = std::max(1, (int)want);
+    }
+    // the other chunks - 1 ranges split L - tail layers as evenly as possible
+    const int head = L - tail, nh = chunks - 1;
+    for (int c = 0; c < nh; ++c) first[c] = c * head / nh;
+    first[nh] = head;
+    first[chunks] = L;
+  }
   hipStream_t ms = (hipStream_t)stream, ss = (hipStream_t)side_stream;
   const bool overlap = ss != nullptr && ss != ms;
   HIPC(hipSetDevice(ctx->device));
@@ -636,9 +662,9 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
     HIPC(hipEventRecord(ctx->events[L], ms));
     HIPC(hipStreamWaitEvent(ss, ctx->events[L], 0));
   }
-  int c = 0;
-  for (int l0 = 0; l0 < L; l0 += per, ++c) {
-    const int nl = std::min(per, L - l0);
+  for (int c = 0; c < chunks; ++c) {
+    const int l0 = first[c], nl = first[c + 1] - first[c];
+    if (nl <= 0) continue;
     hipStream_t fs = overlap ? ss : ms;
     int rc = ferry_bookkeep_layers(ctx, l0, nl, sel, slots, miss_count, misses, nullptr, fs);
     if (!rc) rc = ferry_missq_drain(ctx, fs);

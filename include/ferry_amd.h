@@ -231,7 +231,9 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
  * submits: defaults min 64 MB, max 512 MB, target 8 batches.  The count is
  * read from pinned memory that each step's end copies into, so the host never
  * waits for the device.  ferry_decode_chunks gives the count for a pending
- * number of blocks. */
+ * number of blocks.  The adaptive step also shortens the last range (down to
+ * one layer) when attention is cheap next to the fetch, since its attention
+ * is the part the fetch cannot hide; an explicit count gives even ranges. */
 int ferry_set_batch_policy(ferry_ctx* ctx, double min_mb, double max_mb, double target_batches);
 int ferry_decode_chunks(const ferry_ctx* ctx, uint64_t pending_blocks, int32_t* chunks);
 
