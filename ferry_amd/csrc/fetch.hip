@@ -85,6 +85,9 @@ __device__ inline void copy_blocks(const FetchArgs& a, const ferry_miss* e, int 
 
 template <int NV>
 __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
+  // the fetch shares CUs with the attention it overlaps: its few wavefronts
+  // issue first so the host link never waits on them
+  __builtin_amdgcn_s_setprio(3);
   const int lane = threadIdx.x & 63;
   const int W = gridDim.x;
   const int me = blockIdx.x;
