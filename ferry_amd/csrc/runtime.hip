@@ -66,6 +66,8 @@ struct ferry_ctx {
   SetState st{};
   ferry_miss* ring_entries = nullptr;
   uint64_t* ring_state = nullptr;
+  ferry_miss* ring_entries2 = nullptr;  // second ring: decode_step alternates layer ranges
+  uint64_t* ring_state2 = nullptr;
   uint32_t* ring_seg = nullptr;
   uint32_t* ring_cap = nullptr;
   uint32_t* worker_of_set = nullptr;
@@ -83,7 +85,9 @@ struct ferry_ctx {
   int lru_wpb = 1;
   size_t lru_lds = 0;
   uint64_t steps = 0;
-  std::vector<hipEvent_t> events;  // layer-chunk pipeline of ferry_decode_step
+  std::vector<hipEvent_t> events;   // layer-chunk pipeline of ferry_decode_step: fetch done
+  std::vector<hipEvent_t> booked;   // ... and bookkeeping done
+  hipStream_t book = nullptr;       // ... whose bookkeeping runs on this stream
   int attn_waves = 0;              // wavefronts per attention workgroup (FERRY_ATTN_WAVES), 0 = default
   int attn_loads = 0;              // K/V loads (FERRY_ATTN_LOADS): 0 = by plan, 1 = nt, 2 = temporal
   uint32_t* probe_sink = nullptr;  // bandwidth probes: one word per row / wavefront
@@ -94,10 +98,10 @@ struct ferry_ctx {
   float* sum_scales = nullptr;     // ... and their K scales (fp8)
   uint64_t sum_blocks = 0;         // records; block (set, b) uses (set*max_blocks + b) mod this
 
-  Ring ring() const {
+  Ring ring(int which = 0) const {
     Ring r;
-    r.entries = ring_entries;
-    r.state = ring_state;
+    r.entries = which ? ring_entries2 : ring_entries;
+    r.state = which ? ring_state2 : ring_state;
     r.seg = ring_seg;
     r.cap = ring_cap;
     r.worker_of_set = worker_of_set;
@@ -143,7 +147,8 @@ void release(ferry_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   void* dev[] = {c->pool, c->pool_scales, c->st.fill, c->st.ord, c->st.tag, c->st.map,
-                 c->ring_entries, c->ring_state, c->ring_seg, c->ring_cap, c->worker_of_set,
+                 c->ring_entries, c->ring_state, c->ring_entries2, c->ring_state2,
+                 c->ring_seg, c->ring_cap, c->worker_of_set,
                  c->stats, c->sel_counts, c->step_acc, c->done, c->err, c->probe_sink,
                  c->probe_dst, c->sums, c->sum_scales};
   for (void* p : dev)
@@ -152,6 +157,8 @@ void release(ferry_ctx* c) {
   if (c->host) (void)hipHostFree(c->host);
   if (c->host_scales) (void)hipHostFree(c->host_scales);
   for (hipEvent_t e : c->events) (void)hipEventDestroy(e);
+  for (hipEvent_t e : c->booked) (void)hipEventDestroy(e);
+  if (c->book) (void)hipStreamDestroy(c->book);
   delete c;
 }
 
@@ -262,6 +269,15 @@ void launch_attn(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnA
 
 }  // namespace
 
+namespace {
+
+int bookkeep_ring(ferry_ctx* ctx, int32_t l0, int32_t nl, const uint32_t* sel, uint32_t* slots,
+                  uint32_t* miss_count, ferry_miss* misses, uint8_t* miss_flag, void* stream,
+                  int which);
+int drain_ring(ferry_ctx* ctx, void* stream, int which);
+
+}  // namespace
+
 extern "C" {
 
 const char* ferry_last_error(void) { return g_err.c_str(); }
@@ -354,6 +370,8 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   }
   TRY(dalloc(&c->ring_entries, total));
   TRY(dalloc(&c->ring_state, (size_t)W * kStateStride));
+  TRY(dalloc(&c->ring_entries2, total));
+  TRY(dalloc(&c->ring_state2, (size_t)W * kStateStride));
   TRY(dalloc(&c->ring_seg, W));
   TRY(dalloc(&c->ring_cap, W));
   TRY(dalloc(&c->worker_of_set, g.n_sets));
@@ -374,6 +392,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   HIPT(hipMemcpy(c->ring_cap, cap.data(), W * 4, hipMemcpyHostToDevice));
   HIPT(hipMemcpy(c->worker_of_set, wos.data(), (size_t)g.n_sets * 4, hipMemcpyHostToDevice));
   HIPT(hipMemset(c->ring_state, 0, (size_t)W * kStateStride * 8));
+  HIPT(hipMemset(c->ring_state2, 0, (size_t)W * kStateStride * 8));
   HIPT(hipMemset(c->stats, 0, kStatCount * 8));
   HIPT(hipMemset(c->sel_counts, 0, (size_t)kSelCounters * kSelStride * 8));
   HIPT(hipMemset(c->step_acc, 0, 16));
@@ -406,6 +425,8 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   HIPT(hipGetLastError());
   c->events.resize((size_t)g.L + 1, nullptr);
   for (auto& e : c->events) HIPT(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  c->booked.resize((size_t)g.L, nullptr);
+  for (auto& e : c->booked) HIPT(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   HIPT(hipDeviceSynchronize());
 #undef TRY
 #undef HIPT
@@ -502,6 +523,21 @@ int ferry_bookkeep_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const uint32_t
                           uint32_t* slots, uint32_t* miss_count, ferry_miss* misses,
                           uint8_t* miss_flag, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
+  return bookkeep_ring(ctx, l0, nl, sel, slots, miss_count, misses, miss_flag, stream, 0);
+}
+
+int ferry_missq_drain(ferry_ctx* ctx, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  return drain_ring(ctx, stream, 0);
+}
+
+}  // extern "C"
+
+namespace {
+
+int bookkeep_ring(ferry_ctx* ctx, int32_t l0, int32_t nl, const uint32_t* sel, uint32_t* slots,
+                  uint32_t* miss_count, ferry_miss* misses, uint8_t* miss_flag, void* stream,
+                  int which) {
   if (!sel || !slots || !miss_count || !misses) return fail(FERRY_EINVAL, "null buffer");
   const Geo& g = ctx->g;
   if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
@@ -511,41 +547,22 @@ int ferry_bookkeep_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const uint32_t
   const dim3 grid((nsets + wpb - 1) / wpb), block(64 * wpb);
   if (ctx->cfg.lru_mode == FERRY_LRU_SERIAL)
     hipLaunchKernelGGL(k_lru_step<true>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
-                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->sel_counts,
-                       ctx->err);
+                       miss_count, misses, miss_flag, ctx->st, ctx->ring(which), l0, nl,
+                       ctx->sel_counts, ctx->err);
   else
     hipLaunchKernelGGL(k_lru_step<false>, grid, block, ctx->lru_lds, (hipStream_t)stream, g, sel, slots,
-                       miss_count, misses, miss_flag, ctx->st, ctx->ring(), l0, nl, ctx->sel_counts,
-                       ctx->err);
+                       miss_count, misses, miss_flag, ctx->st, ctx->ring(which), l0, nl,
+                       ctx->sel_counts, ctx->err);
   HIPC(hipGetLastError());
   if (l0 + nl == g.L) ctx->steps++;
   return FERRY_OK;
 }
 
-int ferry_bookkeep_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots,
-                        uint32_t* miss_count, ferry_miss* misses, uint8_t* miss_flag,
-                        void* stream) {
-  if (int rc = check_ctx(ctx)) return rc;
-  return ferry_bookkeep_layers(ctx, 0, ctx->g.L, sel, slots, miss_count, misses, miss_flag, stream);
-}
-
-int ferry_missq_push(ferry_ctx* ctx, const ferry_miss* misses, uint32_t n, void* stream) {
-  if (int rc = check_ctx(ctx)) return rc;
-  if (n == 0) return FERRY_OK;
-  if (!misses) return fail(FERRY_EINVAL, "null misses");
-  HIPC(hipSetDevice(ctx->device));
-  hipLaunchKernelGGL(k_missq_push, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, ctx->g,
-                     ctx->ring(), misses, n, ctx->err);
-  HIPC(hipGetLastError());
-  return FERRY_OK;
-}
-
-int ferry_missq_drain(ferry_ctx* ctx, void* stream) {
-  if (int rc = check_ctx(ctx)) return rc;
+int drain_ring(ferry_ctx* ctx, void* stream, int which) {
   HIPC(hipSetDevice(ctx->device));
   FetchArgs a;
   a.g = ctx->g;
-  a.ring = ctx->ring();
+  a.ring = ctx->ring(which);
   a.host = ctx->host_dev;
   a.host_scales = ctx->host_scales_dev;
   a.pool = ctx->pool;
@@ -566,6 +583,29 @@ int ferry_missq_drain(ferry_ctx* ctx, void* stream) {
   HIPC(hipGetLastError());
   return FERRY_OK;
 }
+
+}  // namespace
+
+extern "C" {
+
+int ferry_bookkeep_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots,
+                        uint32_t* miss_count, ferry_miss* misses, uint8_t* miss_flag,
+                        void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  return ferry_bookkeep_layers(ctx, 0, ctx->g.L, sel, slots, miss_count, misses, miss_flag, stream);
+}
+
+int ferry_missq_push(ferry_ctx* ctx, const ferry_miss* misses, uint32_t n, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (n == 0) return FERRY_OK;
+  if (!misses) return fail(FERRY_EINVAL, "null misses");
+  HIPC(hipSetDevice(ctx->device));
+  hipLaunchKernelGGL(k_missq_push, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, ctx->g,
+                     ctx->ring(), misses, n, ctx->err);
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
 
 int ferry_fetch_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots, uint32_t* miss_count,
                      ferry_miss* misses, uint8_t* miss_flag, void* stream) {
@@ -658,22 +698,43 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
   hipStream_t ms = (hipStream_t)stream, ss = (hipStream_t)side_stream;
   const bool overlap = ss != nullptr && ss != ms;
   HIPC(hipSetDevice(ctx->device));
-  if (overlap) {  // the side stream must not recycle slots the main stream still reads
-    HIPC(hipEventRecord(ctx->events[L], ms));
-    HIPC(hipStreamWaitEvent(ss, ctx->events[L], 0));
-  }
-  for (int c = 0; c < chunks; ++c) {
-    const int l0 = first[c], nl = first[c + 1] - first[c];
-    if (nl <= 0) continue;
-    hipStream_t fs = overlap ? ss : ms;
-    int rc = ferry_bookkeep_layers(ctx, l0, nl, sel, slots, miss_count, misses, nullptr, fs);
-    if (!rc) rc = ferry_missq_drain(ctx, fs);
-    if (rc) return rc;
-    if (overlap) {
-      HIPC(hipEventRecord(ctx->events[c], ss));
-      HIPC(hipStreamWaitEvent(ms, ctx->events[c], 0));
+  if (!sel || !slots || !miss_count || !misses) return fail(FERRY_EINVAL, "null buffer");
+  if (!overlap) {  // one stream: bookkeeping, fetch and attention range by range
+    for (int c = 0; c < chunks; ++c) {
+      const int l0 = first[c], nl = first[c + 1] - first[c];
+      if (nl <= 0) continue;
+      int rc = bookkeep_ring(ctx, l0, nl, sel, slots, miss_count, misses, nullptr, ms, 0);
+      if (!rc) rc = drain_ring(ctx, ms, 0);
+      if (!rc) rc = ferry_sparse_decode_layers(ctx, l0, nl, q, slots, out, ms);
+      if (rc) return rc;
     }
-    if ((rc = ferry_sparse_decode_layers(ctx, l0, nl, q, slots, out, ms))) return rc;
+  } else {
+    // Three streams.  Bookkeeping of range c (its own stream) pushes into ring
+    // c mod 2 and waits only for the fetch of range c - 2, the last user of
+    // that ring; the fetch of c (side stream) waits for its bookkeeping; the
+    // attention of c (main stream) for its fetch.  Ranges touch disjoint sets,
+    // slots and outputs, so the bookkeeping of c + 1 runs while c is fetched
+    // and the link does not wait for it.
+    if (!ctx->book) HIPC(hipStreamCreateWithFlags(&ctx->book, hipStreamNonBlocking));
+    HIPC(hipEventRecord(ctx->events[L], ms));  // slots the main stream still reads
+    HIPC(hipStreamWaitEvent(ss, ctx->events[L], 0));
+    HIPC(hipStreamWaitEvent(ctx->book, ctx->events[L], 0));
+    int prev[2] = {-1, -1};  // last range fetched from each ring
+    for (int c = 0; c < chunks; ++c) {
+      const int l0 = first[c], nl = first[c + 1] - first[c];
+      if (nl <= 0) continue;
+      const int r = c & 1;
+      if (prev[r] >= 0) HIPC(hipStreamWaitEvent(ctx->book, ctx->events[prev[r]], 0));
+      int rc = bookkeep_ring(ctx, l0, nl, sel, slots, miss_count, misses, nullptr, ctx->book, r);
+      if (rc) return rc;
+      HIPC(hipEventRecord(ctx->booked[c], ctx->book));
+      HIPC(hipStreamWaitEvent(ss, ctx->booked[c], 0));
+      if ((rc = drain_ring(ctx, ss, r))) return rc;
+      HIPC(hipEventRecord(ctx->events[c], ss));
+      prev[r] = c;
+      HIPC(hipStreamWaitEvent(ms, ctx->events[c], 0));
+      if ((rc = ferry_sparse_decode_layers(ctx, l0, nl, q, slots, out, ms))) return rc;
+    }
   }
   // the step's fetched blocks, for the next step's adaptive chunking
   hipLaunchKernelGGL(k_step_close, dim3(1), dim3(64), 0, ms, ctx->step_acc, ctx->step_acc + 1);

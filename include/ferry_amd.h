@@ -210,11 +210,13 @@ int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const flo
                                const uint32_t* slots, float* out, void* stream);
 
 /* One whole decode step with the fetch overlapped with attention: layers are
- * cut into `chunks` ranges; bookkeeping and fetch of each range run on
- * side_stream, and attention of a range starts on `stream` as soon as its
- * fetch is done, while the next range is fetched.  side_stream NULL (or equal
- * to stream) runs the same sequence on one stream.  When this returns, work
- * queued on `stream` after it observes the whole step.  Replaces the refill /
+ * cut into `chunks` ranges; the fetch of each range runs on side_stream, and
+ * attention of a range starts on `stream` as soon as its fetch is done, while
+ * the next range is fetched.  Bookkeeping runs on a third stream the context
+ * owns (default priority), one range ahead, into one of two miss rings, so the
+ * fetch of a range never waits for its bookkeeping.  side_stream NULL (or
+ * equal to stream) runs the same sequence on one stream.  When this returns,
+ * work queued on `stream` after it observes the whole step.  Replaces the refill /
  * compute overlap of run_miss_workload mode C: batches submitted to the
  * channel, compute waiting on the last arrival (src/workloads/kv_exec.cuh:
  * 228-286, src/comm/host_staged_channel.cuh:55-63). */
