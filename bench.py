@@ -16,7 +16,7 @@ uploaded before the timed region; the host tier is pinned host memory.
 The timed steps run ferry_decode_step: layers are cut into --chunks ranges
 and the bookkeeping + fetch of range c+1 run on a side stream while range c
 attends on the main stream.  By default the count is adaptive: the reference's
-batch rule (clamp(pending MB / 8, 64, 512) MB per chunk) on the bytes the
+batch rule (clamp(pending MB / 8, 32, 512) MB per chunk) on the bytes the
 previous step fetched.
 
 Prints ONE JSON line.  `value` is whole-step decode tokens/s (B / step time).

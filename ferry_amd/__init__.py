@@ -272,7 +272,7 @@ class Executor:
         _check(lib.ferry_owner_import(self._h, owner, _ptr(image), image.numel(), _stream(stream)),
                "ferry_owner_import")
 
-    def set_batch_policy(self, min_mb=64.0, max_mb=512.0, target_batches=8.0):
+    def set_batch_policy(self, min_mb=32.0, max_mb=512.0, target_batches=8.0):
         _check(lib.ferry_set_batch_policy(self._h, min_mb, max_mb, target_batches),
                "ferry_set_batch_policy")
 

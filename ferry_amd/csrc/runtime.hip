@@ -75,7 +75,7 @@ struct ferry_ctx {
   unsigned long long* sel_counts = nullptr;  // [kSelCounters * kSelStride]
   unsigned long long* step_acc = nullptr;    // [2]: blocks fetched in this step, in the last one
   unsigned long long* pend_host = nullptr;   // pinned: the last step's count, copied at step end
-  double pol_min_mb = 64.0, pol_max_mb = 512.0, pol_target = 8.0;  // adaptive layer chunking
+  double pol_min_mb = 32.0, pol_max_mb = 512.0, pol_target = 8.0;  // adaptive layer chunking
   uint32_t* done = nullptr;
   int* err = nullptr;
   uint8_t* host = nullptr;      // host pointer of the pinned tier

@@ -230,7 +230,7 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
  * max_mb) MB, and the step runs ceil(pending / g) chunks (1 .. n_layers; 1
  * before any step has finished).  A chunk costs three launches and a drain,
  * so the GPU policy works in larger units than the reference's channel
- * submits: defaults min 64 MB, max 512 MB, target 8 batches.  The count is
+ * submits: defaults min 32 MB, max 512 MB, target 8 batches.  The count is
  * read from pinned memory that each step's end copies into, so the host never
  * waits for the device.  ferry_decode_chunks gives the count for a pending
  * number of blocks.  The adaptive step also shortens the last range (down to

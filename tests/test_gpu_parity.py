@@ -323,13 +323,13 @@ def test_decode_step_overlap_matches_sequential(chunks):
 
 def test_adaptive_chunk_policy_known_answers():
     # AdaptiveBatchPolicy::choose_mb (src/runtime/adaptive_batch.cuh:31-36) in GPU
-    # units: g = clamp(pending_MB / 8, 64, 512) MB per chunk, ceil(pending / g)
+    # units: g = clamp(pending_MB / 8, 32, 512) MB per chunk, ceil(pending / g)
     # chunks, at least 1 and at most L.  8 KiB blocks: 1 MB = 128 blocks.
     p = Pair(2, 32, 2, 2, 8, 16, 64, F.F16)
     bb = p.ex.block_bytes
     assert bb == 8192
     mb = 1 << 20
-    cases = {0: 1, 1: 1, 64 * mb // bb: 1, 65 * mb // bb: 2, 184 * mb // bb: 3,
+    cases = {0: 1, 1: 1, 32 * mb // bb: 1, 33 * mb // bb: 2, 184 * mb // bb: 6,
              1290 * mb // bb: 8, 3440 * mb // bb: 8, 8192 * mb // bb: 16,
              (1 << 40) // bb: 32}
     for blocks, want in cases.items():
