@@ -79,22 +79,39 @@ __device__ inline void clear_set(const Geo& g, SetState st, size_t set, int lane
 
 }  // namespace
 
-// One workgroup: header, fill and start (exclusive prefix of the fills) of
-// the owner's sets.
+// One workgroup of 256 threads: fill and start (exclusive prefix of the
+// fills) of the owner's sets, and the header.  Thread t takes a run of
+// consecutive sets; the runs' totals are scanned across the workgroup
+// (wavefront shuffles, then the 4 wavefront totals through LDS).
 __global__ __launch_bounds__(256) void k_owner_export_meta(Geo g, SetState st, uint32_t owner,
                                                            uint8_t* __restrict__ image) {
   const ImageLayout lay = image_layout(g);
   const uint32_t S = (uint32_t)(g.L * g.Hkv);
   uint32_t* fill = reinterpret_cast<uint32_t*>(image + lay.fill);
   uint32_t* start = reinterpret_cast<uint32_t*>(image + lay.start);
-  for (uint32_t s = threadIdx.x; s < S; s += blockDim.x) fill[s] = st.fill[(size_t)owner * S + s];
+  __shared__ unsigned long long wsum[4];
+  const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const uint32_t per = (S + 255) / 256, s0 = min(S, t * per), s1 = min(S, s0 + per);
+  unsigned long long run = 0;
+  for (uint32_t s = s0; s < s1; ++s) {
+    const uint32_t f = st.fill[(size_t)owner * S + s];
+    fill[s] = f;
+    run += f;
+  }
+  unsigned long long incl = run;
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned long long o = __shfl_up(incl, off);
+    if ((int)lane >= off) incl += o;
+  }
+  if (lane == 63) wsum[wave] = incl;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned long long acc = 0;
-    for (uint32_t s = 0; s < S; ++s) {
-      start[s] = (uint32_t)acc;
-      acc += fill[s];
-    }
+  unsigned long long acc = incl - run;
+  for (uint32_t w = 0; w < wave; ++w) acc += wsum[w];
+  for (uint32_t s = s0; s < s1; ++s) {
+    start[s] = (uint32_t)acc;
+    acc += fill[s];
+  }
+  if (t == 255) {
     ImageHeader* h = reinterpret_cast<ImageHeader*>(image);
     h->magic = kImageMagic;
     h->sets = S;
