@@ -177,7 +177,8 @@ class Executor:
         self.max_sel = lib.ora_max_sel_per_set(C.byref(geom))
 
     def __del__(self):
-        if getattr(self, "ptr", None):
+        # at interpreter exit the module globals may already be gone
+        if getattr(self, "ptr", None) and lib is not None:
             lib.ora_exec_destroy(self.ptr)
             self.ptr = None
 
