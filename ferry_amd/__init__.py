@@ -112,6 +112,7 @@ _PROTOS = {
                                   C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "ferry_hosttier_fill": (C.c_int, [_vp, _vp]),
     "ferry_hosttier_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),
+    "ferry_hosttier_register": (C.c_int, [_vp, _vp, C.c_uint64, _vp, C.c_uint64]),
     "ferry_pool_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),
     "ferry_sets_reset": (C.c_int, [_vp, _vp]),
     "ferry_sets_state": (C.c_int, [_vp, _vp, _vp, _vp]),
@@ -367,6 +368,15 @@ class Executor:
         _check(lib.ferry_sets_state(self._h, fill.ctypes.data, ord_.ctypes.data, tag.ctypes.data),
                "ferry_sets_state")
         return fill, ord_, tag
+
+    def hosttier_register(self, host, scales=None):
+        """Use the caller's pinned host memory (a pin_memory uint8 CPU tensor of
+        host_blocks * block_bytes, plus float32 scales for fp8) as the host tier.
+        The tensors are kept alive by the executor."""
+        sb = 0 if scales is None else scales.numel() * scales.element_size()
+        _check(lib.ferry_hosttier_register(self._h, _ptr(host), host.numel() * host.element_size(),
+                                           _ptr(scales), sb), "ferry_hosttier_register")
+        self._registered = (host, scales)
 
     def hosttier_array(self):
         """numpy view of the pinned host tier (bytes) and fp8 scales (or None)."""

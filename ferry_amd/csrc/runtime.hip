@@ -79,6 +79,7 @@ struct ferry_ctx {
   uint32_t* done = nullptr;
   int* err = nullptr;
   uint8_t* host = nullptr;      // host pointer of the pinned tier
+  bool host_owned = true;       // false once the caller registered its own tier
   uint8_t* host_dev = nullptr;  // its device-visible address
   float* host_scales = nullptr;
   float* host_scales_dev = nullptr;
@@ -154,8 +155,10 @@ void release(ferry_ctx* c) {
   for (void* p : dev)
     if (p) (void)hipFree(p);
   if (c->pend_host) (void)hipHostFree(c->pend_host);
-  if (c->host) (void)hipHostFree(c->host);
-  if (c->host_scales) (void)hipHostFree(c->host_scales);
+  if (c->host_owned) {
+    if (c->host) (void)hipHostFree(c->host);
+    if (c->host_scales) (void)hipHostFree(c->host_scales);
+  }
   for (hipEvent_t e : c->events) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->booked) (void)hipEventDestroy(e);
   if (c->book) (void)hipStreamDestroy(c->book);
@@ -470,6 +473,41 @@ int ferry_hosttier_fill(ferry_ctx* ctx, void* stream) {
   hipLaunchKernelGGL(k_hosttier_fill, dim3(4096), dim3(256), 0, (hipStream_t)stream, g,
                      ctx->host_dev, ctx->host_scales_dev, ctx->cfg.host_seed, mult, mult8, base);
   HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_hosttier_register(ferry_ctx* ctx, void* host, uint64_t host_bytes, float* scales,
+                            uint64_t scale_bytes) {
+  if (int rc = check_ctx(ctx)) return rc;
+  const Geo& g = ctx->g;
+  const bool f8 = g.dtype == FERRY_FP8_E4M3;
+  if (!host) return fail(FERRY_EINVAL, "null host tier");
+  if (host_bytes < (uint64_t)g.host_blocks * g.bb)
+    return fail(FERRY_EINVAL, "host tier smaller than host_blocks * block_bytes");
+  if (f8 && (!scales || scale_bytes < (uint64_t)g.host_blocks * 8))
+    return fail(FERRY_EINVAL, "fp8 needs host_blocks * 2 fp32 scales");
+  if (!f8 && scales) return fail(FERRY_EINVAL, "scales are for fp8 KV only");
+  HIPC(hipSetDevice(ctx->device));
+  void* dev = nullptr;
+  void* sdev = nullptr;
+  if (hipHostGetDevicePointer(&dev, host, 0) != hipSuccess || !dev) {
+    (void)hipGetLastError();
+    return fail(FERRY_EINVAL, "host tier must be pinned, device-mapped memory (hipHostMalloc)");
+  }
+  if (scales && (hipHostGetDevicePointer(&sdev, scales, 0) != hipSuccess || !sdev)) {
+    (void)hipGetLastError();
+    return fail(FERRY_EINVAL, "host scales must be pinned, device-mapped memory (hipHostMalloc)");
+  }
+  HIPC(hipDeviceSynchronize());  // nothing may still read the tier being replaced
+  if (ctx->host_owned) {
+    if (ctx->host) HIPC(hipHostFree(ctx->host));
+    if (ctx->host_scales) HIPC(hipHostFree(ctx->host_scales));
+  }
+  ctx->host = (uint8_t*)host;
+  ctx->host_dev = (uint8_t*)dev;
+  ctx->host_scales = scales;
+  ctx->host_scales_dev = (float*)sdev;
+  ctx->host_owned = false;
   return FERRY_OK;
 }
 

@@ -124,6 +124,17 @@ int ferry_ctx_sizes(const ferry_ctx* ctx, uint32_t* n_sets, uint32_t* max_sel,
  * reference fills its slab with uniform halves (src/workloads/kv_exec.cuh:78-86)
  * or a tile (src/runtime/wla_multigpu.cuh:532-544). */
 int ferry_hosttier_fill(ferry_ctx* ctx, void* stream);
+/* Use the caller's pinned host memory as the tier instead of the context's
+ * own: `host` holds host_blocks * block_bytes bytes in the same layout (block
+ * i at i * block_bytes), `scales` host_blocks * 2 fp32 for fp8 KV (NULL
+ * otherwise).  Both must be pinned and mapped into the device's address space
+ * (hipHostMalloc; registering pageable memory is not supported), stay valid
+ * until the context is destroyed and are not freed by it.  Waits for the
+ * device, then frees the context's own tier.  Replaces the host slab that
+ * run_miss_workload allocated for itself (src/workloads/kv_exec.cuh:78-92) with
+ * the caller-owned slab the reference's ownership model describes. */
+int ferry_hosttier_register(ferry_ctx* ctx, void* host, uint64_t host_bytes, float* scales,
+                            uint64_t scale_bytes);
 /* Host pointers of the pinned tier (bytes: host_blocks*block_bytes; scales:
  * host_blocks*2 floats, NULL unless fp8). */
 int ferry_hosttier_view(ferry_ctx* ctx, void** bytes, float** scales);
