@@ -681,6 +681,11 @@ def main():
         with open(tpath) as f:
             r["roofline_select"]["traffic"] = json.load(f).get(a.workload + "_select", {}).get(
                 "bytes_per_launch")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            fo = json.load(f).get(a.workload + "_fetch")
+        r["roofline_fetch"]["traffic"] = (
+            {"read": fo["read_bytes"], "write": fo["write_bytes"]} if fo else None)
     if r.get("roofline_handoff") and os.path.exists(tpath):
         with open(tpath) as f:
             ho = json.load(f).get(a.workload + "_handoff")
