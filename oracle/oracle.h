@@ -24,11 +24,20 @@
  *     reference only has an FMA proxy at src/workloads/kv_exec.cuh:30-37 and
  *     the selection semantics of tools/capture_miss_trace.py:139-159)
  *   - a timed fp32 CPU executor step (cpu_baseline of bench.py)
+ *   - lane turnover: owner reset, empty selection positions and request
+ *     arrivals (steady and bursty: src/runtime/wla_multigpu.cuh:497-501;
+ *     Poisson and Markov-modulated), the owner copy of a hand-off
+ *     (kv_handoff with carry, src/runtime/wla_multigpu.cuh:1970-1994)
+ *   - top-k block selection by the Quest bound: per-block K min/max
+ *     summaries, scores and ascending top-k
+ *     (tools/capture_miss_trace.py:139-159)
  *
- * Parity pins (tests/test_oracle.py): golden counts held in the reference's
- * logs, the C++ standard's mt19937_64 known answer, a build of the
- * reference's own header under oracle/_ref, and brute-force / closed-form
- * checks for everything the reference does not hold.
+ * Parity pins (tests/test_oracle.py, test_arrivals.py, test_select.py,
+ * test_trace.py): golden counts held in the reference's logs, the C++
+ * standard's mt19937_64 known answer, a build of the reference's own header
+ * under oracle/_ref, and brute-force, closed-form or independent numpy
+ * restatements for everything the reference does not hold.  Every function
+ * here has such a check.
  */
 #ifndef FERRY_ORACLE_H
 #define FERRY_ORACLE_H
