@@ -131,3 +131,37 @@ def test_truncated_and_oversized_records_are_refused(tmp_path):
         F.trace_load(str(p), strict=False)
     with pytest.raises(F.FerryError, match="cannot open"):
         F.trace_load(str(tmp_path / "missing.bin"))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_corrupted_files_load_or_refuse(tmp_path, seed):
+    """Random truncations, bit flips, overwritten header fields and garbage:
+    the reader either loads a trace of the header's shape or raises
+    FerryError, and when it loads, the oracle's reader agrees."""
+    rng = np.random.default_rng(seed)
+    p = tmp_path / "t.bin"
+    write_fmt1(p, chained_trace(3, 2, 2, 2, 2, seed=seed), R=3, S=2, L=2, sel_pages=2)
+    raw = bytearray(p.read_bytes())
+    for i in range(60):
+        b = bytearray(raw)
+        kind = i % 4
+        if kind == 0:
+            b = b[:int(rng.integers(0, len(b)))]
+        elif kind == 1:
+            for _ in range(int(rng.integers(1, 8))):
+                j = int(rng.integers(0, len(b)))
+                b[j] ^= 1 << int(rng.integers(0, 8))
+        elif kind == 2:  # a header field (R, S, L, geometry or sel_pages) overwritten
+            j = 8 + 4 * int(rng.integers(0, 8))
+            b[j:j + 4] = struct.pack("<I", int(rng.choice([0, 1, 3, 7, 1 << 20, 0xFFFFFFFF])))
+        else:
+            b = bytearray(rng.integers(0, 256, int(rng.integers(0, 200)), dtype=np.uint8).tobytes())
+        q = tmp_path / f"c{i}.bin"
+        q.write_bytes(bytes(b))
+        try:
+            info, ids = F.trace_load(str(q), strict=False)
+        except F.FerryError:
+            continue
+        assert ids.shape == (info["requests"], info["steps"], info["layers"], info["sel_blocks"])
+        _, oids, _, _ = O.trace_load(str(q), strict=False)
+        assert np.array_equal(ids, oids)
