@@ -258,6 +258,79 @@ __global__ __launch_bounds__(256) void k_summaries_tile(uint8_t* __restrict__ su
       scales[host_blocks + i] = scales[(host_blocks + i) % host_blocks];
 }
 
+// The kk largest of keys[0, n) (n > kk), ids written in ascending order to
+// `nrows` output rows `row_stride` apart, ties to the lower ids.  Phase 1 finds
+// the kk-th largest key by 4 radix passes of 8 bits over LDS histograms (a
+// wavefront-wide suffix scan over the bins); phase 2 counts, per thread's
+// chunk, keys above it and ties, scans the counts over the workgroup and
+// writes.  hist: 256 LDS words, wtot: 2 W, sh: 2.  Every thread must call it.
+template <int W>
+__device__ void topk_ascending(const uint32_t* keys, int n, int kk, uint32_t* hist, uint32_t* wtot,
+                               uint32_t* sh, uint32_t* out, int nrows, size_t row_stride) {
+  constexpr int NT = W * 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t prefix = 0, mask = 0, need = (uint32_t)kk;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += NT) hist[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += NT) {
+      const uint32_t key = keys[i];
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 0xFFu], 1u);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      uint32_t c[4], sum = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        c[e] = hist[255 - 4 * lane - e];
+        sum += c[e];
+      }
+      uint32_t incl = sum;
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
+      }
+      const uint32_t excl = incl - sum;
+      if (excl < need && incl >= need) {
+        uint32_t acc = excl;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (acc + c[e] >= need && acc < need) {
+            sh[0] = prefix | ((uint32_t)(255 - 4 * lane - e) << shift);
+            sh[1] = need - acc;
+          }
+          acc += c[e];
+        }
+      }
+    }
+    __syncthreads();
+    prefix = sh[0];
+    need = sh[1];
+    mask |= 0xFFu << shift;
+  }
+  const uint32_t T = prefix;
+  const int chunk = (n + NT - 1) / NT;
+  const int c0 = tid * chunk, c1 = min(n, c0 + chunk);
+  uint32_t gt = 0, eq = 0;
+  for (int i = c0; i < c1; ++i) {
+    const uint32_t key = keys[i];
+    gt += key > T;
+    eq += key == T;
+  }
+  uint32_t gt_before, eq_before;
+  block_excl_scan2<W>(gt, eq, wtot, gt_before, eq_before);
+  uint32_t pos = gt_before + min(eq_before, need), ties = eq_before;
+  for (int i = c0; i < c1; ++i) {
+    const uint32_t key = keys[i];
+    bool take = key > T;
+    if (key == T) take = ties++ < need;
+    if (take) {
+      for (int r = 0; r < nrows; ++r) out[r * row_stride + pos] = (uint32_t)i;
+      ++pos;
+    }
+  }
+}
+
 // One workgroup (W wavefronts) per (request, layer, kv head) row, or per
 // (request, layer) with LAYER.  Phase 1 scores every block of the request's
 // context into LDS keys (16 lanes per block, 4 blocks per wavefront pass);
@@ -278,7 +351,7 @@ __global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __re
   extern __shared__ uint32_t lds[];
   __shared__ uint32_t hist[256];
   __shared__ uint32_t wtot[2 * W];
-  __shared__ uint32_t sh_prefix, sh_need;
+  __shared__ uint32_t sh[2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nkv = LAYER ? g.Hkv : 1;  // kv heads scored per row
   const int Gq = G * nkv;             // query heads per row
@@ -361,68 +434,8 @@ __global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __re
       }
     }
     __syncthreads();
-    // ---- phase 2: the kk-th largest key (radix select, 8 bits per pass)
-    uint32_t prefix = 0, mask = 0, need = (uint32_t)kk;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int i = tid; i < 256; i += NT) hist[i] = 0;
-      __syncthreads();
-      for (int i = tid; i < n; i += NT) {
-        const uint32_t key = keys[i];
-        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 0xFFu], 1u);
-      }
-      __syncthreads();
-      if (wave == 0) {
-        uint32_t c[4], sum = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          c[e] = hist[255 - 4 * lane - e];
-          sum += c[e];
-        }
-        uint32_t incl = sum;
-        for (int off = 1; off < 64; off <<= 1) {
-          const uint32_t o = __shfl_up(incl, off);
-          if (lane >= off) incl += o;
-        }
-        const uint32_t excl = incl - sum;
-        if (excl < need && incl >= need) {
-          uint32_t acc = excl;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (acc + c[e] >= need && acc < need) {
-              sh_prefix = prefix | ((uint32_t)(255 - 4 * lane - e) << shift);
-              sh_need = need - acc;
-            }
-            acc += c[e];
-          }
-        }
-      }
-      __syncthreads();
-      prefix = sh_prefix;
-      need = sh_need;
-      mask |= 0xFFu << shift;
-    }
-    // ---- phase 3: keys above the threshold, then the lowest-id ties, in id order
-    const uint32_t T = prefix;
-    const int chunk = (n + NT - 1) / NT;
-    const int c0 = tid * chunk, c1 = min(n, c0 + chunk);
-    uint32_t gt = 0, eq = 0;
-    for (int i = c0; i < c1; ++i) {
-      const uint32_t key = keys[i];
-      gt += key > T;
-      eq += key == T;
-    }
-    uint32_t gt_before, eq_before;
-    block_excl_scan2<W>(gt, eq, wtot, gt_before, eq_before);
-    uint32_t pos = gt_before + min(eq_before, need), ties = eq_before;
-    for (int i = c0; i < c1; ++i) {
-      const uint32_t key = keys[i];
-      bool take = key > T;
-      if (key == T) take = ties++ < need;
-      if (take) {
-        for (int hh = 0; hh < (LAYER ? g.Hkv : 1); ++hh) out_row(LAYER ? hh : hrow)[pos] = (uint32_t)i;
-        ++pos;
-      }
-    }
+    topk_ascending<W>(keys, n, kk, hist, wtot, sh, out_row(LAYER ? 0 : hrow), LAYER ? g.Hkv : 1,
+                      (size_t)k);
   } else {
     // a context of at most k blocks: every block, in order
     for (int j = tid; j < kk; j += NT)
