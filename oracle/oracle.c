@@ -1046,6 +1046,97 @@ static int cmp_keyed(const void* a, const void* b) {
   return x->id < y->id ? -1 : (x->id > y->id); /* then the lower block id */
 }
 
+int ora_mass_scores(const ora_geom* g, const float* q, const int* ctx_blocks, int stride,
+                    double* out) {
+  const int L = g->n_layers, Hk = g->kv_heads, G = g->q_heads / g->kv_heads;
+  const int D = g->head_dim, T = g->block_tokens;
+  int nmax = 0;
+  for (int r = 0; r < g->n_req; ++r) {
+    if (ctx_blocks[r] > g->max_blocks) return -1;
+    if (ctx_blocks[r] > nmax) nmax = ctx_blocks[r];
+  }
+  const double scaling = 1.0 / sqrt((double)D);
+  double* logit = (double*)malloc((size_t)(nmax > 0 ? nmax : 1) * T * sizeof(double));
+  for (int r = 0; r < g->n_req; ++r)
+    for (int l = 0; l < L; ++l) {
+      const int n = ctx_blocks[r] > 0 ? (ctx_blocks[r] < stride ? ctx_blocks[r] : stride) : 0;
+      double* sc = out + (size_t)(r * L + l) * stride;
+      for (int b = 0; b < n; ++b) sc[b] = 0.0;
+      for (int h = 0; h < Hk; ++h) {
+        const uint32_t set = (uint32_t)((r * L + l) * Hk + h);
+        for (int gq = 0; gq < G; ++gq) {
+          const float* qv = q + (((size_t)(r * L + l) * g->q_heads) + (size_t)(h * G + gq)) * D;
+          double mx = -INFINITY;
+          for (int b = 0; b < n; ++b) {
+            const uint64_t hb = ora_host_index(g, set, (uint32_t)b);
+            const double ks = (double)ora_host_scale(g, hb, 0);
+            for (int t = 0; t < T; ++t) {
+              double dot = 0.0;
+              for (int d = 0; d < D; ++d)
+                dot += (double)qv[d] * ora_decode(g->dtype, ora_host_elem(g, hb, (uint32_t)(t * D + d)));
+              const double x = dot * ks * scaling;
+              logit[(size_t)b * T + t] = x;
+              if (x > mx) mx = x;
+            }
+          }
+          double z = 0.0;
+          for (size_t i = 0; i < (size_t)n * T; ++i) z += exp(logit[i] - mx);
+          for (int b = 0; b < n; ++b) {
+            double m = 0.0;
+            for (int t = 0; t < T; ++t) m += exp(logit[(size_t)b * T + t] - mx);
+            sc[b] += m / z;
+          }
+        }
+      }
+    }
+  free(logit);
+  return 0;
+}
+
+typedef struct {
+  double score;
+  uint32_t id;
+} dkeyed;
+
+static int cmp_dkeyed(const void* a, const void* b) {
+  const dkeyed *x = (const dkeyed*)a, *y = (const dkeyed*)b;
+  if (x->score != y->score) return x->score > y->score ? -1 : 1; /* more mass first */
+  return x->id < y->id ? -1 : (x->id > y->id);                   /* then the lower id */
+}
+
+int ora_select_mass(const ora_geom* g, const float* q, const int* ctx_blocks, uint32_t* sel) {
+  const int L = g->n_layers, Hk = g->kv_heads, k = g->k;
+  int nmax = 1;
+  for (int r = 0; r < g->n_req; ++r) {
+    if (ctx_blocks[r] > g->max_blocks) return -1;
+    if (ctx_blocks[r] > nmax) nmax = ctx_blocks[r];
+  }
+  double* sc = (double*)malloc((size_t)g->n_req * L * nmax * sizeof(double));
+  dkeyed* kv = (dkeyed*)malloc((size_t)nmax * sizeof(dkeyed));
+  uint32_t* pick = (uint32_t*)malloc((size_t)nmax * 4);
+  ora_mass_scores(g, q, ctx_blocks, nmax, sc);
+  for (int r = 0; r < g->n_req; ++r)
+    for (int l = 0; l < L; ++l) {
+      const int n = ctx_blocks[r] > 0 ? ctx_blocks[r] : 0;
+      const int kk = n < k ? n : k;
+      for (int b = 0; b < n; ++b) {
+        kv[b].score = sc[(size_t)(r * L + l) * nmax + b];
+        kv[b].id = (uint32_t)b;
+      }
+      qsort(kv, (size_t)n, sizeof(dkeyed), cmp_dkeyed);
+      for (int j = 0; j < kk; ++j) pick[j] = kv[j].id;
+      qsort(pick, (size_t)kk, 4, cmp_u32);
+      for (int hh = 0; hh < Hk; ++hh) {
+        uint32_t* o = sel + ((size_t)(r * L + l) * Hk + hh) * k;
+        for (int j = 0; j < k; ++j) o[j] = j < kk ? pick[j] : ORA_NONE;
+      }
+    }
+  free(sc);
+  free(kv);
+  free(pick);
+  return 0;
+}
+
 /* Top-k blocks of every (request, layer, kv head) row: the min(k, n) highest
  * scores (capture_miss_trace.py:157-158: topk(score, min(sel, n_pages))),
  * written in ascending block order (:158 .sort()), padded with ORA_NONE.

@@ -235,6 +235,20 @@ int ora_quest_scores(const ora_geom* g, const float* q, const int* ctx_blocks, i
 int ora_select_topk(const ora_geom* g, const float* q, const int* ctx_blocks, int mode,
                     uint32_t* sel);
 
+/* Exact softmax mass per block, the capture tool's "mass" method
+ * (tools/capture_miss_trace.py:147-155), in double: for (request r, layer l),
+ * each kv head h (set (r*L + l)*Hkv + h; block b's K = the K half of host
+ * block ora_host_index(set, b), fp8 K times its scale) and each of its G query
+ * heads, p_t = softmax over the context's n*T tokens of q . k_t / sqrt(D), and
+ * score[b] = sum over h, its query heads and b's T tokens of p_t.
+ * out[(r*L + l) * stride + b] for b < min(ctx, stride). */
+int ora_mass_scores(const ora_geom* g, const float* q, const int* ctx_blocks, int stride,
+                    double* out);
+/* The min(k, n) blocks of highest mass of every (request, layer), ties to the
+ * lower ids, in ascending order, written to every kv head's row of sel
+ * [B][L][Hkv][k] (ORA_NONE padding): the tool keeps one page list per layer. */
+int ora_select_mass(const ora_geom* g, const float* q, const int* ctx_blocks, uint32_t* sel);
+
 /* ---------------- attention ---------------- */
 /* fp64 block-sparse decode attention with keys read from the host tier by
  * (set, block).  q, out: [B][L][Hq][D] (q fp32, out fp64). */

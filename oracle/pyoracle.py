@@ -133,6 +133,9 @@ _sig("ora_attention_pool_f32", C.c_int, C.POINTER(Geom), _u32p, C.c_void_p, C.c_
 _sig("ora_summary", None, C.POINTER(Geom), C.c_uint64, _f32p, _f32p)
 _sig("ora_quest_scores", C.c_int, C.POINTER(Geom), _f32p, _i32p, C.c_int, C.c_int, _f32p)
 _sig("ora_select_topk", C.c_int, C.POINTER(Geom), _f32p, _i32p, C.c_int, _u32p)
+_sig("ora_mass_scores", C.c_int, C.POINTER(Geom), _f32p, _i32p, C.c_int,
+     np.ctypeslib.ndpointer(np.float64, flags="C"))
+_sig("ora_select_mass", C.c_int, C.POINTER(Geom), _f32p, _i32p, _u32p)
 _sig("ora_cpu_step", C.c_int, C.c_void_p, _u32p, C.c_void_p, C.c_void_p, C.c_void_p,
      C.c_void_p, _f32p, _f32p, _u32p, _u32p, _missp, _u64p)
 
@@ -418,6 +421,25 @@ def quest_scores(g: Geom, q, ctx_blocks, mode=0):
     lib.ora_quest_scores(C.byref(g), np.ascontiguousarray(q, np.float32).reshape(-1), ctx, mode,
                          stride, out)
     return out.reshape(rows, stride)
+
+
+def mass_scores(g: Geom, q, ctx_blocks):
+    """Softmax mass per block, double [B, L, max ctx] (NaN past a context)."""
+    ctx = np.ascontiguousarray(ctx_blocks, np.int32)
+    stride = max(1, int(ctx.max()))
+    out = np.full(g.n_req * g.n_layers * stride, np.nan, np.float64)
+    if lib.ora_mass_scores(C.byref(g), np.ascontiguousarray(q, np.float32).reshape(-1), ctx,
+                           stride, out):
+        raise ValueError("context longer than max_blocks")
+    return out.reshape(g.n_req, g.n_layers, stride)
+
+
+def select_mass(g: Geom, q, ctx_blocks):
+    sel = np.zeros(g.n_req * g.n_layers * g.kv_heads * g.k, np.uint32)
+    if lib.ora_select_mass(C.byref(g), np.ascontiguousarray(q, np.float32).reshape(-1),
+                           np.ascontiguousarray(ctx_blocks, np.int32), sel):
+        raise ValueError("context longer than max_blocks")
+    return sel.reshape(g.n_req, g.n_layers, g.kv_heads, g.k)
 
 
 def select_topk(g: Geom, q, ctx_blocks, mode=0):

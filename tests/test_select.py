@@ -119,3 +119,76 @@ def test_zero_query_selects_the_first_blocks():
     g = _geom(O.BF16, n_req=1, L=1, H=2, Hq=2)
     sel = O.select_topk(g, np.zeros((1, 1, 2, 128), np.float32), np.array([40], np.int32), 0)
     assert np.array_equal(sel[0, 0], np.tile(np.arange(8, dtype=np.uint32), (2, 1)))
+
+
+# ---------------------------------------------------------------- mass method
+def _mass_numpy(g, q, ctx):
+    """The capture tool's mass scores (tools/capture_miss_trace.py:147-155) with
+    torch.softmax in float64 over K decoded here: [B, L, n]."""
+    B, L, Hk, Hq = g.n_req, g.n_layers, g.kv_heads, g.q_heads
+    G, T = Hq // Hk, g.block_tokens
+    out = np.full((B, L, int(ctx.max())), np.nan)
+    for r in range(B):
+        n = int(ctx[r])
+        for l in range(L):
+            score = np.zeros(n)
+            for h in range(Hk):
+                set_ = (r * L + l) * Hk + h
+                K = np.concatenate([(lambda kt: kt[0] * kt[1])(_decode_block(g, O.host_index(g, set_, b)))
+                                    for b in range(n)])  # [n*T, D]
+                qg = q[r, l, h * G:(h + 1) * G].astype(np.float64)  # [G, D]
+                logits = torch.from_numpy(qg @ K.T / np.sqrt(g.head_dim))
+                attn = torch.softmax(logits, dim=-1).numpy()
+                score += attn.reshape(G, n, T).sum(-1).sum(0)
+            out[r, l, :n] = score
+    return out
+
+
+@pytest.mark.parametrize("dtype", [O.F32, O.F16, O.BF16, O.FP8])
+def test_mass_scores_against_torch_softmax(dtype):
+    g = _geom(dtype, n_req=2, L=2, H=2, Hq=4, mb=48, host_blocks=97)
+    rng = np.random.default_rng(10 + dtype)
+    q = (rng.standard_normal((2, 2, 4, 128)) * 2).astype(np.float32)
+    ctx = np.array([30, 11], np.int32)
+    got = O.mass_scores(g, q, ctx)
+    want = _mass_numpy(g, q, ctx)
+    assert np.allclose(np.nan_to_num(got), np.nan_to_num(want), rtol=1e-12, atol=1e-15)
+    # every query head's softmax sums to 1: a layer holds Hq of mass
+    assert np.allclose(np.nansum(got, axis=2), 4.0, rtol=0, atol=1e-12)
+
+
+def test_mass_selection_special_cases():
+    g = _geom(O.F16, n_req=2, L=1, H=2, Hq=4, k=6, mb=48, host_blocks=97)
+    ctx = np.array([20, 4], np.int32)
+    # q = 0: every token weighs the same, every block ties: the lowest ids
+    sel = O.select_mass(g, np.zeros((2, 1, 4, 128), np.float32), ctx)
+    assert np.array_equal(sel[0, 0, 0], np.arange(6, dtype=np.uint32))
+    # a context of at most k blocks: all of them, then EMPTY, in every kv head's row
+    assert np.array_equal(sel[1, 0, 1], np.array([0, 1, 2, 3, O.NONE, O.NONE], np.uint32))
+    # q along one token's key, large: that token's block takes nearly all the mass
+    k13, ks = _decode_block(g, O.host_index(g, 0, 13))
+    q = np.zeros((2, 1, 4, 128), np.float32)
+    q[0, 0, :2] = (k13[5] * ks * 50.0).astype(np.float32)  # both heads of kv head 0
+    s = O.mass_scores(g, q, ctx)
+    # kv head 0's two heads put (almost) all their mass on block 13; kv head 1's
+    # (q = 0) spread theirs evenly, 2/20 per block
+    assert int(np.nanargmax(s[0, 0])) == 13 and abs(s[0, 0, 13] - 2.1) < 1e-6
+    assert np.allclose(np.delete(s[0, 0], 13), 0.1, atol=1e-6)
+    assert 13 in O.select_mass(g, q, ctx)[0, 0, 0]
+
+
+def test_mass_selection_is_lexsort_of_scores():
+    g = _geom(O.BF16, n_req=3, L=2, H=2, Hq=8, k=7, mb=64, host_blocks=131)
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((3, 2, 8, 128)).astype(np.float32)
+    ctx = np.array([64, 7, 33], np.int32)
+    sc = O.mass_scores(g, q, ctx)
+    sel = O.select_mass(g, q, ctx)
+    for r in range(3):
+        for l in range(2):
+            n = int(ctx[r])
+            order = np.lexsort((np.arange(n), -sc[r, l, :n]))[:min(7, n)]
+            want = np.full(7, O.NONE, np.uint32)
+            want[:len(order)] = np.sort(order)
+            for h in range(2):
+                assert np.array_equal(sel[r, l, h], want)
