@@ -132,6 +132,10 @@ _PROTOS = {
     "ferry_summaries_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(C.c_uint64)]),
     "ferry_select_topk": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp, _vp]),
     "ferry_select_topk_layers": (C.c_int, [_vp, _i32, _i32, _vp, _vp, C.c_int, _vp, _vp]),
+    "ferry_ktiles_build": (C.c_int, [_vp, C.c_uint64, _vp]),
+    "ferry_ktiles_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(C.c_uint64)]),
+    "ferry_select_mass": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "ferry_select_mass_layers": (C.c_int, [_vp, _i32, _i32, _vp, _vp, _vp, _vp]),
     "ferry_sched_destroy": (C.c_int, [_vp]),
     "ferry_sched_tick": (C.c_int, [_vp, C.c_double, _vp, _vp, _vp, C.POINTER(_i32), _vp,
                                    C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32)]),
@@ -334,6 +338,36 @@ class Executor:
             _check(lib.ferry_select_topk_layers(self._h, l0, nl, _ptr(q), _ptr(ctx_blocks), mode,
                                                 _ptr(sel), _stream(stream)),
                    "ferry_select_topk_layers")
+
+    def ktiles_build(self, n_records=0, stream=None):
+        """Dense K table for select_mass: n_records records (a multiple of the
+        host tier's blocks; 0 = one per host-tier block)."""
+        _check(lib.ferry_ktiles_build(self._h, n_records, _stream(stream)), "ferry_ktiles_build")
+
+    def ktiles_array(self):
+        """The K table copied to host: uint8 [records, block_bytes / 2] and fp8
+        K scales [records] (or None)."""
+        p, sc, n = _vp(), _vp(), C.c_uint64()
+        _check(lib.ferry_ktiles_view(self._h, C.byref(p), C.byref(sc), C.byref(n)),
+               "ferry_ktiles_view")
+        rec = self.block_bytes // 2
+        kt = _gather_d2h(p.value, n.value * rec, [0]).reshape(n.value, rec)
+        scales = None
+        if sc.value:
+            scales = _gather_d2h(sc.value, n.value * 4, [0]).view(np.float32).reshape(n.value)
+        return kt, scales
+
+    def select_mass(self, q, ctx_blocks, sel, stream=None, layers=None):
+        """The softmax-mass top-k of every (request, layer), written to every kv
+        head's row of sel [B,L,Hkv,k] (device tensors as for select_topk)."""
+        if layers is None:
+            _check(lib.ferry_select_mass(self._h, _ptr(q), _ptr(ctx_blocks), _ptr(sel),
+                                         _stream(stream)), "ferry_select_mass")
+        else:
+            l0, nl = layers
+            _check(lib.ferry_select_mass_layers(self._h, l0, nl, _ptr(q), _ptr(ctx_blocks),
+                                                _ptr(sel), _stream(stream)),
+                   "ferry_select_mass_layers")
 
     def sets_reset(self, stream=None):
         _check(lib.ferry_sets_reset(self._h, _stream(stream)), "ferry_sets_reset")

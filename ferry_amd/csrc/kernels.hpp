@@ -130,4 +130,14 @@ __global__ void k_select_topk(Geo g, const float* q, const int32_t* ctx_blocks, 
                               const float* sum_scales, uint64_t sum_mod, uint32_t* sel, int l0, int nl,
                               int max_n, int* err);
 
+// Mass method of the top-k selection (select.hip): the dense K table and the
+// per-(request, layer) softmax-mass scoring + radix top-k.
+template <int NV>
+__global__ void k_ktiles_build(Geo g, const uint8_t* host, const float* host_scales, uint8_t* kt,
+                               float* kt_scales);
+template <int DT, int G, int W>
+__global__ void k_select_mass(Geo g, const float* q, const int32_t* ctx_blocks, const uint8_t* kt,
+                              const float* kt_scales, uint64_t kt_mod, uint32_t* sel, int l0, int nl,
+                              int max_n, int* err);
+
 }  // namespace ferry_amd

@@ -98,6 +98,9 @@ struct ferry_ctx {
   uint8_t* sums = nullptr;         // top-k selection: K min/max records [sum_blocks][2][D]
   float* sum_scales = nullptr;     // ... and their K scales (fp8)
   uint64_t sum_blocks = 0;         // records; block (set, b) uses (set*max_blocks + b) mod this
+  uint8_t* ktab = nullptr;         // mass selection: K halves of host blocks [kt_records][T][D]
+  float* ktab_scales = nullptr;    // ... and their K scales (fp8)
+  uint64_t kt_records = 0;         // records, addressed like the summaries
 
   Ring ring(int which = 0) const {
     Ring r;
@@ -151,7 +154,7 @@ void release(ferry_ctx* c) {
                  c->ring_entries, c->ring_state, c->ring_entries2, c->ring_state2,
                  c->ring_seg, c->ring_cap, c->worker_of_set,
                  c->stats, c->sel_counts, c->step_acc, c->done, c->err, c->probe_sink,
-                 c->probe_dst, c->sums, c->sum_scales};
+                 c->probe_dst, c->sums, c->sum_scales, c->ktab, c->ktab_scales};
   for (void* p : dev)
     if (p) (void)hipFree(p);
   if (c->pend_host) (void)hipHostFree(c->pend_host);
@@ -916,6 +919,98 @@ int ferry_select_topk(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks,
                       void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
   return ferry_select_topk_layers(ctx, 0, ctx->g.L, q, ctx_blocks, mode, sel, stream);
+}
+
+int ferry_ktiles_build(ferry_ctx* ctx, uint64_t n_records, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  const Geo& g = ctx->g;
+  const uint64_t S = n_records ? n_records : g.host_blocks;
+  if (S % g.host_blocks) return fail(FERRY_EINVAL, "K records must be a multiple of the host tier's blocks");
+  const uint64_t KT = g.bb / 2;
+  HIPC(hipSetDevice(ctx->device));
+  hipStream_t s = (hipStream_t)stream;
+  if (ctx->ktab && ctx->kt_records != S) {
+    HIPC(hipDeviceSynchronize());
+    HIPC(hipFree(ctx->ktab));
+    if (ctx->ktab_scales) HIPC(hipFree(ctx->ktab_scales));
+    ctx->ktab = nullptr;
+    ctx->ktab_scales = nullptr;
+    ctx->kt_records = 0;
+  }
+  if (!ctx->ktab) {
+    HIPC(hipMalloc(&ctx->ktab, S * KT));
+    if (g.dtype == FERRY_FP8_E4M3) HIPC(hipMalloc(&ctx->ktab_scales, S * 4ull));
+    ctx->kt_records = S;
+  }
+  const unsigned blocks = (unsigned)std::min<uint64_t>((g.host_blocks + 3) / 4, 16384);
+  switch (KT / 1024) {
+    case 2: hipLaunchKernelGGL(k_ktiles_build<2>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev, ctx->host_scales_dev, ctx->ktab, ctx->ktab_scales); break;
+    case 4: hipLaunchKernelGGL(k_ktiles_build<4>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev, ctx->host_scales_dev, ctx->ktab, ctx->ktab_scales); break;
+    case 8: hipLaunchKernelGGL(k_ktiles_build<8>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev, ctx->host_scales_dev, ctx->ktab, ctx->ktab_scales); break;
+    default: return fail(FERRY_EINVAL, "unsupported block size");
+  }
+  HIPC(hipGetLastError());
+  // records past the host tier's repeat it: block (set, b) reads record
+  // (set * max_blocks + b) mod S, whose content is host block (... ) mod host_blocks
+  const uint64_t hb = g.host_blocks;
+  for (uint64_t c = 1; c < S / hb; ++c) {
+    HIPC(hipMemcpyAsync(ctx->ktab + c * hb * KT, ctx->ktab, hb * KT, hipMemcpyDeviceToDevice, s));
+    if (ctx->ktab_scales)
+      HIPC(hipMemcpyAsync(ctx->ktab_scales + c * hb, ctx->ktab_scales, hb * 4, hipMemcpyDeviceToDevice, s));
+  }
+  return FERRY_OK;
+}
+
+int ferry_ktiles_view(ferry_ctx* ctx, void** ktiles, float** scales, uint64_t* n_records) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (ktiles) *ktiles = ctx->ktab;
+  if (scales) *scales = ctx->ktab_scales;
+  if (n_records) *n_records = ctx->kt_records;
+  return FERRY_OK;
+}
+
+int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
+                             const int32_t* ctx_blocks, uint32_t* sel, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!q || !ctx_blocks || !sel) return fail(FERRY_EINVAL, "null buffer");
+  const Geo& g = ctx->g;
+  if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
+  if (g.group != 1)
+    return fail(FERRY_EINVAL, "top-k selection needs private sets (group 1): a group's members select "
+                              "from their own contexts");
+  if (!ctx->ktab) return fail(FERRY_EINVAL, "K table not built (ferry_ktiles_build)");
+  const size_t lds = (size_t)g.max_blocks * 4;
+  if (lds > 60 * 1024) return fail(FERRY_EINVAL, "max_blocks exceed the mass selection's 60 KiB of LDS");
+  HIPC(hipSetDevice(ctx->device));
+  const dim3 grid((unsigned)((size_t)g.n_req * nl)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  const int G = g.Hq / g.Hkv;
+#define FERRY_MASS_LAUNCH(DT, GG)                                                                  \
+  hipLaunchKernelGGL((k_select_mass<DT, GG, 4>), grid, block, lds, s, g, q, ctx_blocks, ctx->ktab, \
+                     ctx->ktab_scales, ctx->kt_records, sel, l0, nl, g.max_blocks, ctx->err)
+#define FERRY_MASS_G(DT)                       \
+  switch (G) {                                 \
+    case 1: FERRY_MASS_LAUNCH(DT, 1); break;   \
+    case 2: FERRY_MASS_LAUNCH(DT, 2); break;   \
+    case 4: FERRY_MASS_LAUNCH(DT, 4); break;   \
+    default: FERRY_MASS_LAUNCH(DT, 8); break;  \
+  }
+  switch (g.dtype) {
+    case FERRY_F32: FERRY_MASS_G(FERRY_F32); break;
+    case FERRY_F16: FERRY_MASS_G(FERRY_F16); break;
+    case FERRY_BF16: FERRY_MASS_G(FERRY_BF16); break;
+    default: FERRY_MASS_G(FERRY_FP8_E4M3); break;
+  }
+#undef FERRY_MASS_G
+#undef FERRY_MASS_LAUNCH
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_select_mass(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks, uint32_t* sel,
+                      void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  return ferry_select_mass_layers(ctx, 0, ctx->g.L, q, ctx_blocks, sel, stream);
 }
 
 int ferry_owner_image_bytes(const ferry_ctx* ctx, uint64_t* bytes) {

@@ -445,6 +445,243 @@ __global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __re
     for (int hh = 0; hh < (LAYER ? g.Hkv : 1); ++hh) out_row(LAYER ? hh : hrow)[j] = kNone;
 }
 
+// ---------------------------------------------------------------- mass method
+// The capture tool's second selection method (tools/capture_miss_trace.py:
+// 147-155): a block's score is the softmax mass its tokens take, summed over
+// every query head of the layer, and each layer gets one page list.  It needs
+// every context token's key, so it reads a dense K table (the K half of each
+// host-tier block, records addressed like the summaries) instead of the
+// summaries.
+
+// One wavefront per host-tier block: its K half (NV KiB) copied device-direct
+// from the pinned tier into record h, and its K scale (fp8).
+template <int NV>
+__global__ __launch_bounds__(256) void k_ktiles_build(Geo g, const uint8_t* __restrict__ host,
+                                                      const float* __restrict__ host_scales,
+                                                      uint8_t* __restrict__ kt,
+                                                      float* __restrict__ kt_scales) {
+  const uint64_t wave = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const uint64_t nw = ((uint64_t)gridDim.x * blockDim.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  for (uint64_t h = wave; h < (uint64_t)g.host_blocks; h += nw) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(host + h * g.bb);
+    u32x4* dst = reinterpret_cast<u32x4*>(kt + h * (uint64_t)NV * 1024);
+    u32x4 r[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) r[v] = __builtin_nontemporal_load(src + v * kWave + lane);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) dst[v * kWave + lane] = r[v];
+    if (kt_scales && lane == 0) kt_scales[h] = host_scales[2 * h];
+  }
+}
+
+namespace {
+
+// The 16/ES elements of one 16-byte word of a K row, decoded exactly.
+template <int DT, int EPL>
+__device__ inline void decode_word(const u32x4& w, float* f) {
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    if constexpr (DT == FERRY_F32) f[e] = bits_f32(w[e]);
+    else if constexpr (DT == FERRY_FP8_E4M3) f[e] = elem_f32<DT>((w[e >> 2] >> (8 * (e & 3))) & 0xFFu);
+    else f[e] = elem_f32<DT>((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+  }
+}
+
+// sum over the LPT lanes of a token row (xor butterfly within 32 lanes)
+template <int LPT>
+__device__ inline float row_sum(float v) {
+  if constexpr (LPT >= 32) v += swz_xor<16>(v);
+  if constexpr (LPT >= 16) v += swz_xor<8>(v);
+  if constexpr (LPT >= 8) v += swz_xor<4>(v);
+  v += swz_xor<2>(v);
+  v += swz_xor<1>(v);
+  return v;
+}
+
+// (m, s) of a softmax in the exp2 domain merged with another
+__device__ inline void lse_merge(float& m, float& s, float om, float os) {
+  const float mn = fmaxf(m, om);
+  s = mn == -INFINITY ? 0.0f : s * exp2f(m - mn) + os * exp2f(om - mn);
+  m = mn;
+}
+
+}  // namespace
+
+// One workgroup (W wavefronts) per (request, layer).  For each kv head:
+// pass 1 computes every query head's softmax maximum and normaliser over all
+// the context's tokens (online, exp2 domain, merged over lanes and
+// wavefronts); pass 2 recomputes the logits and adds each block's mass (its
+// tokens' probabilities, summed over the query heads) to its LDS score.  The
+// lanes of a wavefront cover one block: lane (t, p) holds 16 bytes of row
+// t + TPI i of K for i < NI, the dims of its 16-byte word, and the query dims
+// to match; a row's dot product is summed over its LPT lanes.  The scores
+// then go through the same radix top-k as the Quest method, and the layer's
+// list is written to every kv head's row.  Dynamic LDS: max_n floats.
+template <int DT, int G, int W>
+__global__ __launch_bounds__(W * 64) void k_select_mass(Geo g, const float* __restrict__ q,
+                                                        const int32_t* __restrict__ ctx_blocks,
+                                                        const uint8_t* __restrict__ kt,
+                                                        const float* __restrict__ kt_scales,
+                                                        uint64_t kt_mod, uint32_t* __restrict__ sel,
+                                                        int l0, int nl, int max_n,
+                                                        int* __restrict__ err) {
+  constexpr int ES = DT == FERRY_F32 ? 4 : (DT == FERRY_FP8_E4M3 ? 1 : 2);
+  constexpr int D = 128, T = 16, NT = W * 64;
+  constexpr int EPL = 16 / ES, LPT = D / EPL, TPI = 64 / LPT, NI = T / TPI;
+  constexpr uint32_t KT = T * D * ES;
+  constexpr int U = 2;  // blocks in flight per wavefront
+  extern __shared__ uint32_t lds[];
+  float* score = reinterpret_cast<float*>(lds);
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wtot[2 * W];
+  __shared__ uint32_t sh[2];
+  __shared__ float red_m[W][G], red_s[W][G], lse_m[G], lse_zi[G];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int p = lane % LPT;
+  const int r = blockIdx.x / nl, l = l0 + blockIdx.x % nl;
+  const int rl = r * g.L + l;
+  int n = ctx_blocks[r];
+  if (n < 0) n = 0;
+  if (n > max_n || n > g.max_blocks) {
+    if (tid == 0) set_error(err, FERRY_ERANGE);
+    n = 0;
+  }
+  const int k = g.k;
+  const int kk = n < k ? n : k;
+  uint32_t* out0 = sel + (size_t)rl * g.Hkv * (size_t)k;
+
+  if (n > k) {
+    for (int b = tid; b < n; b += NT) score[b] = 0.0f;
+    const float qmul = 1.4426950408889634f / sqrtf((float)D);  // log2(e) / sqrt(D)
+    for (int h = 0; h < g.Hkv; ++h) {
+      const uint64_t set = (uint64_t)rl * g.Hkv + h;
+      float qr[G][EPL];
+#pragma unroll
+      for (int gq = 0; gq < G; ++gq)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e)
+          qr[gq][e] = q[((size_t)rl * g.Hq + (size_t)(h * G + gq)) * D + p * EPL + e] * qmul;
+      // the U blocks b0 + W u of this wavefront: records, K words, K scales
+      auto load = [&](int b0, u32x4 (&w)[U][NI], float (&ks)[U]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int b = b0 + W * u;
+          const uint64_t rec = host_index(set, b < n ? (uint32_t)b : 0u, (uint64_t)g.max_blocks, kt_mod);
+          const u32x4* base = reinterpret_cast<const u32x4*>(kt + rec * KT);
+#pragma unroll
+          for (int i = 0; i < NI; ++i) w[u][i] = __builtin_nontemporal_load(base + i * 64 + lane);
+          ks[u] = kt_scales ? kt_scales[rec] : 1.0f;
+        }
+      };
+      // logits of the token rows this lane's group holds, for every query head
+      auto logits = [&](const u32x4& word, float ksc, float (&x)[G]) {
+        float kf[EPL];
+        decode_word<DT, EPL>(word, kf);
+#pragma unroll
+        for (int gq = 0; gq < G; ++gq) {
+          float a = 0.0f;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) a = __fmaf_rn(qr[gq][e], kf[e], a);
+          x[gq] = row_sum<LPT>(a) * ksc;
+        }
+      };
+      // ---- pass 1: softmax maximum and normaliser of every query head
+      float m[G], s[G];
+#pragma unroll
+      for (int gq = 0; gq < G; ++gq) m[gq] = -INFINITY, s[gq] = 0.0f;
+      for (int b0 = wave; b0 < n; b0 += W * U) {
+        u32x4 w[U][NI];
+        float ks[U];
+        load(b0, w, ks);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (b0 + W * u >= n) break;  // wavefront-uniform
+#pragma unroll
+          for (int i = 0; i < NI; ++i) {
+            float x[G];
+            logits(w[u][i], ks[u], x);
+            if (p == 0) {
+#pragma unroll
+              for (int gq = 0; gq < G; ++gq) lse_merge(m[gq], s[gq], x[gq], 1.0f);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int gq = 0; gq < G; ++gq) {
+        float mm = m[gq], ss = s[gq];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) lse_merge(mm, ss, __shfl_xor(mm, off), __shfl_xor(ss, off));
+        if (lane == 0) {
+          red_m[wave][gq] = mm;
+          red_s[wave][gq] = ss;
+        }
+      }
+      __syncthreads();
+      if (tid < G) {
+        float mm = -INFINITY, ss = 0.0f;
+        for (int w = 0; w < W; ++w) lse_merge(mm, ss, red_m[w][tid], red_s[w][tid]);
+        lse_m[tid] = mm;
+        lse_zi[tid] = 1.0f / ss;
+      }
+      __syncthreads();
+      float M[G], Zi[G];
+#pragma unroll
+      for (int gq = 0; gq < G; ++gq) M[gq] = lse_m[gq], Zi[gq] = lse_zi[gq];
+      // ---- pass 2: each block's probability mass, summed over the heads
+      for (int b0 = wave; b0 < n; b0 += W * U) {
+        u32x4 w[U][NI];
+        float ks[U];
+        load(b0, w, ks);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (b0 + W * u >= n) break;
+          float bm = 0.0f;
+#pragma unroll
+          for (int i = 0; i < NI; ++i) {
+            float x[G];
+            logits(w[u][i], ks[u], x);
+            if (p == 0) {
+#pragma unroll
+              for (int gq = 0; gq < G; ++gq) bm += exp2f(x[gq] - M[gq]) * Zi[gq];
+            }
+          }
+#pragma unroll
+          for (int off = 32; off > 0; off >>= 1) bm += __shfl_xor(bm, off);
+          if (lane == 0) score[b0 + W * u] += bm;
+        }
+      }
+      __syncthreads();
+    }
+    for (int b = tid; b < n; b += NT) lds[b] = fkey(score[b]);
+    __syncthreads();
+    topk_ascending<W>(lds, n, kk, hist, wtot, sh, out0, g.Hkv, (size_t)k);
+  } else {
+    for (int j = tid; j < kk; j += NT)
+      for (int hh = 0; hh < g.Hkv; ++hh) out0[(size_t)hh * k + j] = (uint32_t)j;
+  }
+  for (int j = kk + tid; j < k; j += NT)
+    for (int hh = 0; hh < g.Hkv; ++hh) out0[(size_t)hh * k + j] = kNone;
+}
+
+#define FERRY_MASS_INST(DT, G)                                                                  \
+  template __global__ void k_select_mass<DT, G, 4>(Geo, const float*, const int32_t*,           \
+                                                   const uint8_t*, const float*, uint64_t,      \
+                                                   uint32_t*, int, int, int, int*);
+#define FERRY_MASS_INST_G(DT) \
+  FERRY_MASS_INST(DT, 1)      \
+  FERRY_MASS_INST(DT, 2)      \
+  FERRY_MASS_INST(DT, 4)      \
+  FERRY_MASS_INST(DT, 8)
+FERRY_MASS_INST_G(FERRY_F32)
+FERRY_MASS_INST_G(FERRY_F16)
+FERRY_MASS_INST_G(FERRY_BF16)
+FERRY_MASS_INST_G(FERRY_FP8_E4M3)
+template __global__ void k_ktiles_build<2>(Geo, const uint8_t*, const float*, uint8_t*, float*);
+template __global__ void k_ktiles_build<4>(Geo, const uint8_t*, const float*, uint8_t*, float*);
+template __global__ void k_ktiles_build<8>(Geo, const uint8_t*, const float*, uint8_t*, float*);
+
 #define FERRY_SUMS_INST(DT)                                                                 \
   template __global__ void k_summaries_build<DT>(Geo, const uint8_t*, const float*, uint8_t*, \
                                                  float*);

@@ -290,6 +290,26 @@ int ferry_select_topk(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks,
 int ferry_select_topk_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
                              const int32_t* ctx_blocks, int mode, uint32_t* sel, void* stream);
 
+/* The capture tool's "mass" method (tools/capture_miss_trace.py:147-155): a
+ * block's score is the softmax probability its tokens take, softmax over the
+ * whole context of q . k / sqrt(head_dim), summed over every query head of the
+ * layer; each (request, layer) gets the min(k, ctx) blocks of highest score in
+ * ascending order (ties to the lower ids), written to every kv head's row of
+ * sel, EMPTY-padded.  It reads every context token's key from a dense K table
+ * in HBM: ferry_ktiles_build copies the K half of each host-tier block into
+ * n_records records (a multiple of host_blocks; 0 = one per host block; block
+ * (set, b) reads record (set * max_blocks + b) mod n_records, as the
+ * summaries), device-direct from the pinned tier, fp8 K scales included.
+ * q [B][L][Hq][128] fp32 and ctx_blocks [B] int32 on the device; group 1
+ * only; max_blocks <= 15360 (one score per block in LDS).  A context longer
+ * than max_blocks latches FERRY_ERANGE and leaves that row EMPTY. */
+int ferry_ktiles_build(ferry_ctx* ctx, uint64_t n_records, void* stream);
+int ferry_ktiles_view(ferry_ctx* ctx, void** ktiles, float** scales, uint64_t* n_records);
+int ferry_select_mass(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks, uint32_t* sel,
+                      void* stream);
+int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
+                             const int32_t* ctx_blocks, uint32_t* sel, void* stream);
+
 /* ---- owner hand-off (the per-GPU halves of moving a request) ----
  * ferry_owner_export writes an image of one owner's sets: per (layer, kv
  * head) set its LRU fill, order and tags, fp8 scales, and the bytes of its
