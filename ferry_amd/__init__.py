@@ -345,8 +345,10 @@ class Executor:
         _check(lib.ferry_ktiles_build(self._h, n_records, _stream(stream)), "ferry_ktiles_build")
 
     def ktiles_array(self):
-        """The K table copied to host: uint8 [records, block_bytes / 2] and fp8
-        K scales [records] (or None)."""
+        """The K table copied to host: uint8 [records, block_bytes / 2] (fp32
+        row-major; 16-bit and fp8 lane-transposed: 16-byte word c of token row
+        t at word 64 (c // 4) + 16 (c % 4) + t) and fp8 K scales [records] (or
+        None)."""
         p, sc, n = _vp(), _vp(), C.c_uint64()
         _check(lib.ferry_ktiles_view(self._h, C.byref(p), C.byref(sc), C.byref(n)),
                "ferry_ktiles_view")

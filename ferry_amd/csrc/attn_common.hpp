@@ -1,4 +1,5 @@
-// attn_common.hpp -- device helpers shared by the two attention kernels.
+// attn_common.hpp -- device helpers shared by the attention kernels and the
+// matrix-core selection kernel.
 #pragma once
 
 #include "common.hpp"
@@ -14,6 +15,23 @@ template <bool NT, typename T>
 __device__ inline T load_kv(const T* p) {
   if constexpr (NT) return __builtin_nontemporal_load(p);
   else return *p;
+}
+
+typedef uint32_t mx_u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 mx_f16x2 __attribute__((ext_vector_type(2)));
+
+// 4 OCP E4M3 codes (one dword) -> 4 exact fp16 values (two dwords).
+__device__ inline mx_u32x2 e4m3x4_to_f16(uint32_t w) {
+  const mx_f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false);
+  const mx_f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true);
+  return mx_u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+}
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs)
+__device__ inline uint16_t bf16_rne(float x) {
+  uint32_t u = __builtin_bit_cast(uint32_t, x);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
 }
 
 // Stage the k slot ids of one (request, layer, kv head) row in LDS `ids`,

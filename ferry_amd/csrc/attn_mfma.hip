@@ -57,19 +57,6 @@ __device__ inline uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) 
   return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
-// 4 OCP E4M3 codes (one dword) -> 4 exact fp16 values (two dwords).
-__device__ inline u32x2 e4m3x4_to_f16(uint32_t w) {
-  const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false);
-  const f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true);
-  return u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
-}
-
-__device__ inline uint16_t bf16_rne(float x) {
-  uint32_t u = __builtin_bit_cast(uint32_t, x);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 }  // namespace

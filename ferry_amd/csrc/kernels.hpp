@@ -134,10 +134,16 @@ __global__ void k_select_topk(Geo g, const float* q, const int32_t* ctx_blocks, 
 // per-(request, layer) softmax-mass scoring + radix top-k.
 template <int NV>
 __global__ void k_ktiles_build(Geo g, const uint8_t* host, const float* host_scales, uint8_t* kt,
-                               float* kt_scales);
+                               float* kt_scales, int perm);
 template <int DT, int G, int W>
 __global__ void k_select_mass(Geo g, const float* q, const int32_t* ctx_blocks, const uint8_t* kt,
-                              const float* kt_scales, uint64_t kt_mod, uint32_t* sel, int l0, int nl,
-                              int max_n, int* err);
+                              const float* kt_scales, uint64_t kt_mod, float* ws, uint32_t* sel, int l0,
+                              int nl, int max_n, int* err);
+template <int DT, int G, int W>
+__global__ void k_select_mass_mfma(Geo g, const float* q, const int32_t* ctx_blocks, const uint8_t* kt,
+                                   const float* kt_scales, uint64_t kt_mod, float* ws, uint32_t* sel,
+                                   int l0, int nl, int max_n, int* err);
+// persistent workgroups of k_select_mass; each holds max_blocks * G * 2 floats of workspace
+constexpr int kMassWgs = 2048;
 
 }  // namespace ferry_amd

@@ -101,6 +101,8 @@ struct ferry_ctx {
   uint8_t* ktab = nullptr;         // mass selection: K halves of host blocks [kt_records][T][D]
   float* ktab_scales = nullptr;    // ... and their K scales (fp8)
   uint64_t kt_records = 0;         // records, addressed like the summaries
+  float* mass_ws = nullptr;        // per-workgroup (max, sum) of every block and query head
+  int kt_perm = 0;                 // K table words lane-transposed for the matrix-core loads
 
   Ring ring(int which = 0) const {
     Ring r;
@@ -154,7 +156,7 @@ void release(ferry_ctx* c) {
                  c->ring_entries, c->ring_state, c->ring_entries2, c->ring_state2,
                  c->ring_seg, c->ring_cap, c->worker_of_set,
                  c->stats, c->sel_counts, c->step_acc, c->done, c->err, c->probe_sink,
-                 c->probe_dst, c->sums, c->sum_scales, c->ktab, c->ktab_scales};
+                 c->probe_dst, c->sums, c->sum_scales, c->ktab, c->ktab_scales, c->mass_ws};
   for (void* p : dev)
     if (p) (void)hipFree(p);
   if (c->pend_host) (void)hipHostFree(c->pend_host);
@@ -921,6 +923,9 @@ int ferry_select_topk(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks,
   return ferry_select_topk_layers(ctx, 0, ctx->g.L, q, ctx_blocks, mode, sel, stream);
 }
 
+// one float score per context block in LDS
+constexpr uint64_t kMassLds = 60 * 1024;
+
 int ferry_ktiles_build(ferry_ctx* ctx, uint64_t n_records, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
   const Geo& g = ctx->g;
@@ -942,11 +947,16 @@ int ferry_ktiles_build(ferry_ctx* ctx, uint64_t n_records, void* stream) {
     if (g.dtype == FERRY_FP8_E4M3) HIPC(hipMalloc(&ctx->ktab_scales, S * 4ull));
     ctx->kt_records = S;
   }
+  if (!ctx->mass_ws && (uint64_t)g.max_blocks * 4 <= kMassLds) {
+    const uint64_t wgs = std::min<uint64_t>((uint64_t)g.n_req * g.L, kMassWgs);
+    HIPC(hipMalloc(&ctx->mass_ws, wgs * g.max_blocks * (uint64_t)(g.Hq / g.Hkv) * 8));
+  }
+  ctx->kt_perm = g.dtype != FERRY_F32;
   const unsigned blocks = (unsigned)std::min<uint64_t>((g.host_blocks + 3) / 4, 16384);
   switch (KT / 1024) {
-    case 2: hipLaunchKernelGGL(k_ktiles_build<2>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev, ctx->host_scales_dev, ctx->ktab, ctx->ktab_scales); break;
-    case 4: hipLaunchKernelGGL(k_ktiles_build<4>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev, ctx->host_scales_dev, ctx->ktab, ctx->ktab_scales); break;
-    case 8: hipLaunchKernelGGL(k_ktiles_build<8>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev, ctx->host_scales_dev, ctx->ktab, ctx->ktab_scales); break;
+    case 2: hipLaunchKernelGGL(k_ktiles_build<2>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev, ctx->host_scales_dev, ctx->ktab, ctx->ktab_scales, ctx->kt_perm); break;
+    case 4: hipLaunchKernelGGL(k_ktiles_build<4>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev, ctx->host_scales_dev, ctx->ktab, ctx->ktab_scales, ctx->kt_perm); break;
+    case 8: hipLaunchKernelGGL(k_ktiles_build<8>, dim3(blocks), dim3(256), 0, s, g, ctx->host_dev, ctx->host_scales_dev, ctx->ktab, ctx->ktab_scales, ctx->kt_perm); break;
     default: return fail(FERRY_EINVAL, "unsupported block size");
   }
   HIPC(hipGetLastError());
@@ -980,26 +990,30 @@ int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float
                               "from their own contexts");
   if (!ctx->ktab) return fail(FERRY_EINVAL, "K table not built (ferry_ktiles_build)");
   const size_t lds = (size_t)g.max_blocks * 4;
-  if (lds > 60 * 1024) return fail(FERRY_EINVAL, "max_blocks exceed the mass selection's 60 KiB of LDS");
+  if (lds > kMassLds) return fail(FERRY_EINVAL, "max_blocks exceed the mass selection's 60 KiB of LDS");
   HIPC(hipSetDevice(ctx->device));
-  const dim3 grid((unsigned)((size_t)g.n_req * nl)), block(256);
+  const dim3 grid((unsigned)std::min<size_t>((size_t)g.n_req * nl, kMassWgs));
   hipStream_t s = (hipStream_t)stream;
   const int G = g.Hq / g.Hkv;
-#define FERRY_MASS_LAUNCH(DT, GG)                                                                  \
-  hipLaunchKernelGGL((k_select_mass<DT, GG, 4>), grid, block, lds, s, g, q, ctx_blocks, ctx->ktab, \
-                     ctx->ktab_scales, ctx->kt_records, sel, l0, nl, g.max_blocks, ctx->err)
-#define FERRY_MASS_G(DT)                       \
-  switch (G) {                                 \
-    case 1: FERRY_MASS_LAUNCH(DT, 1); break;   \
-    case 2: FERRY_MASS_LAUNCH(DT, 2); break;   \
-    case 4: FERRY_MASS_LAUNCH(DT, 4); break;   \
-    default: FERRY_MASS_LAUNCH(DT, 8); break;  \
+  // vector ALUs (4 wavefronts) for fp32 K, matrix cores (8 wavefronts) for
+  // 16-bit and fp8 K; the wider workgroup keeps more blocks in flight when
+  // there are few (request, layer) items
+#define FERRY_MASS_LAUNCH(KERN, DT, GG, WW)                                                      \
+  hipLaunchKernelGGL((KERN<DT, GG, WW>), grid, dim3(64 * WW), lds, s, g, q, ctx_blocks,         \
+                     ctx->ktab, ctx->ktab_scales, ctx->kt_records, ctx->mass_ws, sel, l0, nl,   \
+                     g.max_blocks, ctx->err)
+#define FERRY_MASS_G(KERN, DT, WW)                       \
+  switch (G) {                                           \
+    case 1: FERRY_MASS_LAUNCH(KERN, DT, 1, WW); break;   \
+    case 2: FERRY_MASS_LAUNCH(KERN, DT, 2, WW); break;   \
+    case 4: FERRY_MASS_LAUNCH(KERN, DT, 4, WW); break;   \
+    default: FERRY_MASS_LAUNCH(KERN, DT, 8, WW); break;  \
   }
   switch (g.dtype) {
-    case FERRY_F32: FERRY_MASS_G(FERRY_F32); break;
-    case FERRY_F16: FERRY_MASS_G(FERRY_F16); break;
-    case FERRY_BF16: FERRY_MASS_G(FERRY_BF16); break;
-    default: FERRY_MASS_G(FERRY_FP8_E4M3); break;
+    case FERRY_F32: FERRY_MASS_G(k_select_mass, FERRY_F32, 4); break;
+    case FERRY_F16: FERRY_MASS_G(k_select_mass_mfma, FERRY_F16, 8); break;
+    case FERRY_BF16: FERRY_MASS_G(k_select_mass_mfma, FERRY_BF16, 8); break;
+    default: FERRY_MASS_G(k_select_mass_mfma, FERRY_FP8_E4M3, 8); break;
   }
 #undef FERRY_MASS_G
 #undef FERRY_MASS_LAUNCH

@@ -28,6 +28,7 @@
 // the 16 partial sums are combined by an xor butterfly (8, 4, 2, 1); max is
 // `a > b ? a : b`; keys are the order-preserving map of the float bits (so
 // -0 < +0), and equal keys go to the lower block id.
+#include "attn_common.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -454,15 +455,21 @@ __global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __re
 // summaries.
 
 // One wavefront per host-tier block: its K half (NV KiB) copied device-direct
-// from the pinned tier into record h, and its K scale (fp8).
+// from the pinned tier into record h, and its K scale (fp8).  perm = 1 (16-bit
+// and fp8 K) stores the record lane-transposed for the matrix-core kernel:
+// 16-byte word c of token row t goes to word 64 (c / 4) + 16 (c % 4) + t, so
+// each of that kernel's load instructions reads 1 KiB contiguous (lane l =
+// 16 grp + n takes word 4 w + grp of row n).  perm = 0 keeps the row-major
+// order (fp32 K, read by the vector-ALU kernel).
 template <int NV>
 __global__ __launch_bounds__(256) void k_ktiles_build(Geo g, const uint8_t* __restrict__ host,
                                                       const float* __restrict__ host_scales,
                                                       uint8_t* __restrict__ kt,
-                                                      float* __restrict__ kt_scales) {
+                                                      float* __restrict__ kt_scales, int perm) {
   const uint64_t wave = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const uint64_t nw = ((uint64_t)gridDim.x * blockDim.x) >> 6;
   const int lane = threadIdx.x & 63;
+  constexpr int WPR = NV * 4;  // 16-byte words per token row (16 rows)
   for (uint64_t h = wave; h < (uint64_t)g.host_blocks; h += nw) {
     const u32x4* src = reinterpret_cast<const u32x4*>(host + h * g.bb);
     u32x4* dst = reinterpret_cast<u32x4*>(kt + h * (uint64_t)NV * 1024);
@@ -470,7 +477,10 @@ __global__ __launch_bounds__(256) void k_ktiles_build(Geo g, const uint8_t* __re
 #pragma unroll
     for (int v = 0; v < NV; ++v) r[v] = __builtin_nontemporal_load(src + v * kWave + lane);
 #pragma unroll
-    for (int v = 0; v < NV; ++v) dst[v * kWave + lane] = r[v];
+    for (int v = 0; v < NV; ++v) {
+      const int c = (v * kWave + lane) % WPR, row = (v * kWave + lane) / WPR;
+      dst[perm ? (c / 4) * 64 + (c % 4) * 16 + row : v * kWave + lane] = r[v];
+    }
     if (kt_scales && lane == 0) kt_scales[h] = host_scales[2 * h];
   }
 }
@@ -488,16 +498,33 @@ __device__ inline void decode_word(const u32x4& w, float* f) {
   }
 }
 
-// sum over the LPT lanes of a token row (xor butterfly within 32 lanes)
-template <int LPT>
-__device__ inline float row_sum(float v) {
-  if constexpr (LPT >= 32) v += swz_xor<16>(v);
-  if constexpr (LPT >= 16) v += swz_xor<8>(v);
-  if constexpr (LPT >= 8) v += swz_xor<4>(v);
-  v += swz_xor<2>(v);
-  v += swz_xor<1>(v);
-  return v;
+// Sum of a lane's N partial dot products over the lanes of a token row (xor
+// X, X/2, ..., 1): while a lane holds more than one partial the level is
+// transposed (each lane keeps half and adds its partner's half of the same
+// sums), after that it is the plain butterfly.  With N = V partials and
+// X = LPT/2, lane p of the row ends with max(1, V/LPT) sums: sum k + NF p
+// (V >= LPT) or sum p >> log2(LPT/V) (V < LPT).
+template <int X, int N>
+__device__ inline void reduce_rows(float* a, int p) {
+  if constexpr (X >= 1) {
+    if constexpr (N > 1) {
+      transpose_level<X, N>(a, p);
+      reduce_rows<X / 2, N / 2>(a, p);
+    } else {
+      a[0] += swz_xor<X>(a[0]);
+      reduce_rows<X / 2, 1>(a, p);
+    }
+  }
 }
+
+__device__ inline float row16_max(float v) {
+  v = fmaxf(v, swz_xor<8>(v));
+  v = fmaxf(v, swz_xor<4>(v));
+  v = fmaxf(v, swz_xor<2>(v));
+  return fmaxf(v, swz_xor<1>(v));
+}
+
+constexpr int ilog2c(int x) { return x <= 1 ? 0 : 1 + ilog2c(x / 2); }
 
 // (m, s) of a softmax in the exp2 domain merged with another
 __device__ inline void lse_merge(float& m, float& s, float om, float os) {
@@ -508,52 +535,70 @@ __device__ inline void lse_merge(float& m, float& s, float om, float os) {
 
 }  // namespace
 
-// One workgroup (W wavefronts) per (request, layer).  For each kv head:
-// pass 1 computes every query head's softmax maximum and normaliser over all
-// the context's tokens (online, exp2 domain, merged over lanes and
-// wavefronts); pass 2 recomputes the logits and adds each block's mass (its
-// tokens' probabilities, summed over the query heads) to its LDS score.  The
-// lanes of a wavefront cover one block: lane (t, p) holds 16 bytes of row
-// t + TPI i of K for i < NI, the dims of its 16-byte word, and the query dims
-// to match; a row's dot product is summed over its LPT lanes.  The scores
-// then go through the same radix top-k as the Quest method, and the layer's
-// list is written to every kv head's row.  Dynamic LDS: max_n floats.
+// Persistent workgroups of W wavefronts over the (request, layer) items, one
+// pass over the K table per kv head:
+//  * each wavefront takes U blocks at a time; lane (t, p) holds 16 bytes of
+//    K rows t + TPI i (i < NI) and the matching query dims of the G query
+//    heads, forms the V = NI G partial dot products and sums them over the
+//    row's LPT lanes (transposed reduction);
+//  * the logits go through a small LDS tile, one 16-lane row per (block,
+//    query head), where a 16-lane butterfly gives the block's softmax maximum
+//    m_b and sum s_b = sum_t exp2(x_t - m_b) (exp2 domain: q is pre-scaled by
+//    log2(e) / sqrt(128)); (m_b, s_b) go to the workgroup's workspace slice
+//    and are merged into the query head's running (M, S);
+//  * once (M, S) is merged over the workgroup, block b's mass is
+//    sum over query heads of exp2(m_b - M) s_b / S, added to its LDS score.
+// The scores then go through the same radix top-k as the Quest method and the
+// layer's list is written to every kv head's row.  Dynamic LDS: max_n floats;
+// workspace: max_n * G * 2 floats per workgroup.
 template <int DT, int G, int W>
 __global__ __launch_bounds__(W * 64) void k_select_mass(Geo g, const float* __restrict__ q,
                                                         const int32_t* __restrict__ ctx_blocks,
                                                         const uint8_t* __restrict__ kt,
                                                         const float* __restrict__ kt_scales,
-                                                        uint64_t kt_mod, uint32_t* __restrict__ sel,
-                                                        int l0, int nl, int max_n,
-                                                        int* __restrict__ err) {
+                                                        uint64_t kt_mod, float* __restrict__ ws_all,
+                                                        uint32_t* __restrict__ sel, int l0, int nl,
+                                                        int max_n, int* __restrict__ err) {
   constexpr int ES = DT == FERRY_F32 ? 4 : (DT == FERRY_FP8_E4M3 ? 1 : 2);
   constexpr int D = 128, T = 16, NT = W * 64;
   constexpr int EPL = 16 / ES, LPT = D / EPL, TPI = 64 / LPT, NI = T / TPI;
+  constexpr int V = NI * G, NF = V >= LPT ? V / LPT : 1, SH = V >= LPT ? 0 : ilog2c(LPT / V);
   constexpr uint32_t KT = T * D * ES;
-  constexpr int U = 2;  // blocks in flight per wavefront
+  constexpr int U = G >= 4 ? 2 : 4;             // blocks in flight per wavefront
+  constexpr int XW = 16 * G * U;                // logits of one wavefront's U blocks
+  constexpr int R = (XW + 63) / 64;             // LDS tile rows per lane
+  constexpr int NE = W * 4 * R;                 // running (M, S) entries per workgroup
   extern __shared__ uint32_t lds[];
   float* score = reinterpret_cast<float*>(lds);
   __shared__ uint32_t hist[256];
   __shared__ uint32_t wtot[2 * W];
   __shared__ uint32_t sh[2];
-  __shared__ float red_m[W][G], red_s[W][G], lse_m[G], lse_zi[G];
+  __shared__ float xl[W][XW];
+  __shared__ float red_m[NE], red_s[NE], lse_m[G], lse_zi[G];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int p = lane % LPT;
-  const int r = blockIdx.x / nl, l = l0 + blockIdx.x % nl;
-  const int rl = r * g.L + l;
-  int n = ctx_blocks[r];
-  if (n < 0) n = 0;
-  if (n > max_n || n > g.max_blocks) {
-    if (tid == 0) set_error(err, FERRY_ERANGE);
-    n = 0;
-  }
-  const int k = g.k;
-  const int kk = n < k ? n : k;
-  uint32_t* out0 = sel + (size_t)rl * g.Hkv * (size_t)k;
+  const int p = lane % LPT, t = lane / LPT;
+  float* ws = ws_all + (size_t)blockIdx.x * max_n * G * 2;
+  const int n_items = g.n_req * nl;
+  const float qmul = 1.4426950408889634f / sqrtf((float)D);  // log2(e) / sqrt(D)
 
-  if (n > k) {
-    for (int b = tid; b < n; b += NT) score[b] = 0.0f;
-    const float qmul = 1.4426950408889634f / sqrtf((float)D);  // log2(e) / sqrt(D)
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    __syncthreads();  // the previous item's top-k is done with the LDS
+    const int r = item / nl, l = l0 + item % nl;
+    const int rl = r * g.L + l;
+    int n = ctx_blocks[r];
+    if (n < 0) n = 0;
+    if (n > max_n || n > g.max_blocks) {
+      if (tid == 0) set_error(err, FERRY_ERANGE);
+      n = 0;
+    }
+    const int k = g.k;
+    const int kk = n < k ? n : k;
+    uint32_t* out0 = sel + (size_t)rl * g.Hkv * (size_t)k;
+    if (n <= k) {
+      for (int j = tid; j < k; j += NT)
+        for (int hh = 0; hh < g.Hkv; ++hh) out0[(size_t)hh * k + j] = j < kk ? (uint32_t)j : kNone;
+      continue;
+    }
     for (int h = 0; h < g.Hkv; ++h) {
       const uint64_t set = (uint64_t)rl * g.Hkv + h;
       float qr[G][EPL];
@@ -562,61 +607,267 @@ __global__ __launch_bounds__(W * 64) void k_select_mass(Geo g, const float* __re
 #pragma unroll
         for (int e = 0; e < EPL; ++e)
           qr[gq][e] = q[((size_t)rl * g.Hq + (size_t)(h * G + gq)) * D + p * EPL + e] * qmul;
-      // the U blocks b0 + W u of this wavefront: records, K words, K scales
-      auto load = [&](int b0, u32x4 (&w)[U][NI], float (&ks)[U]) {
+      float run_m[R], run_s[R];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int b = b0 + W * u;
-          const uint64_t rec = host_index(set, b < n ? (uint32_t)b : 0u, (uint64_t)g.max_blocks, kt_mod);
-          const u32x4* base = reinterpret_cast<const u32x4*>(kt + rec * KT);
-#pragma unroll
-          for (int i = 0; i < NI; ++i) w[u][i] = __builtin_nontemporal_load(base + i * 64 + lane);
-          ks[u] = kt_scales ? kt_scales[rec] : 1.0f;
-        }
-      };
-      // logits of the token rows this lane's group holds, for every query head
-      auto logits = [&](const u32x4& word, float ksc, float (&x)[G]) {
-        float kf[EPL];
-        decode_word<DT, EPL>(word, kf);
-#pragma unroll
-        for (int gq = 0; gq < G; ++gq) {
-          float a = 0.0f;
-#pragma unroll
-          for (int e = 0; e < EPL; ++e) a = __fmaf_rn(qr[gq][e], kf[e], a);
-          x[gq] = row_sum<LPT>(a) * ksc;
-        }
-      };
-      // ---- pass 1: softmax maximum and normaliser of every query head
-      float m[G], s[G];
-#pragma unroll
-      for (int gq = 0; gq < G; ++gq) m[gq] = -INFINITY, s[gq] = 0.0f;
+      for (int rr = 0; rr < R; ++rr) run_m[rr] = -INFINITY, run_s[rr] = 0.0f;
       for (int b0 = wave; b0 < n; b0 += W * U) {
         u32x4 w[U][NI];
         float ks[U];
-        load(b0, w, ks);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          if (b0 + W * u >= n) break;  // wavefront-uniform
+          const int b = b0 + W * u;
+          if (b < n) {  // wavefront-uniform
+            const uint64_t rec = host_index(set, (uint32_t)b, (uint64_t)g.max_blocks, kt_mod);
+            const u32x4* base = reinterpret_cast<const u32x4*>(kt + rec * KT);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) w[u][i] = __builtin_nontemporal_load(base + i * 64 + lane);
+            ks[u] = kt_scales ? kt_scales[rec] : 1.0f;
+          } else {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) w[u][i] = u32x4{0u, 0u, 0u, 0u};
+            ks[u] = 0.0f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float a[V];
 #pragma unroll
           for (int i = 0; i < NI; ++i) {
-            float x[G];
-            logits(w[u][i], ks[u], x);
-            if (p == 0) {
+            float kf[EPL];
+            decode_word<DT, EPL>(w[u][i], kf);
 #pragma unroll
-              for (int gq = 0; gq < G; ++gq) lse_merge(m[gq], s[gq], x[gq], 1.0f);
+            for (int gq = 0; gq < G; ++gq) {
+              float acc = 0.0f;
+#pragma unroll
+              for (int e = 0; e < EPL; ++e) acc = __fmaf_rn(qr[gq][e], kf[e], acc);
+              a[gq * NI + i] = acc;
+            }
+          }
+          reduce_rows<LPT / 2, V>(a, p);
+          if (V >= LPT || (p & ((LPT >> ilog2c(V)) - 1)) == 0) {
+#pragma unroll
+            for (int kq = 0; kq < NF; ++kq) {
+              const int v = V >= LPT ? kq + NF * p : (p >> SH);
+              const int gq = v / NI, i = v % NI;
+              xl[wave][u * 16 * G + gq * 16 + t + TPI * i] = a[kq] * ks[u];
+            }
+          }
+        }
+        wave_fence();
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+          const int idx = lane + 64 * rr;
+          if (XW % 64 == 0 || idx < XW) {
+            const float x = xl[wave][idx];
+            const float m = row16_max(x);
+            const float sm = row16_sum(exp2f(x - m));
+            const int b = b0 + W * (idx / (16 * G));
+            if ((lane & 15) == 0 && b < n) {
+              const int gq = (idx >> 4) % G;
+              ws[((size_t)b * G + gq) * 2] = m;
+              ws[((size_t)b * G + gq) * 2 + 1] = sm;
+              lse_merge(run_m[rr], run_s[rr], m, sm);
+            }
+          }
+        }
+        wave_fence();
+      }
+      // the workgroup's (M, S) of every query head
+      if ((lane & 15) == 0) {
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+          red_m[(wave * 4 + (lane >> 4)) * R + rr] = run_m[rr];
+          red_s[(wave * 4 + (lane >> 4)) * R + rr] = run_s[rr];
+        }
+      }
+      __syncthreads();
+      if (tid < G) {
+        float mm = -INFINITY, ss = 0.0f;
+        for (int e = 0; e < NE; ++e) {
+          const int c = e / R, rr = e % R;  // entry of lane 16 (c % 4) of wave c / 4, tile row rr
+          const int idx = (c % 4) * 16 + 64 * rr;
+          if (idx < XW && (idx >> 4) % G == tid) lse_merge(mm, ss, red_m[e], red_s[e]);
+        }
+        lse_m[tid] = mm;
+        lse_zi[tid] = 1.0f / ss;
+      }
+      __syncthreads();
+      for (int b = tid; b < n; b += NT) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int gq = 0; gq < G; ++gq)
+          acc += exp2f(ws[((size_t)b * G + gq) * 2] - lse_m[gq]) * ws[((size_t)b * G + gq) * 2 + 1] *
+                 lse_zi[gq];
+        score[b] = h == 0 ? acc : score[b] + acc;
+      }
+      __syncthreads();
+    }
+    for (int b = tid; b < n; b += NT) lds[b] = fkey(score[b]);
+    __syncthreads();
+    topk_ascending<W>(lds, n, kk, hist, wtot, sh, out0, g.Hkv, (size_t)k);
+    for (int j = kk + tid; j < k; j += NT)
+      for (int hh = 0; hh < g.Hkv; ++hh) out0[(size_t)hh * k + j] = kNone;
+  }
+}
+
+// Matrix-core variant for 16-bit and fp8 K (the same contract and workspace
+// as k_select_mass).  Per block the scores of the G query heads are one
+// 16 x 16 tile on the matrix cores,
+//   S^T[16 tok][16 hd] = K[16 tok][128] . Q^T[128][16 hd]   (4 k-steps of 32),
+// with the heads padded to 16 columns, in the operand layout of k_attn_mfma:
+// lane l (n = l % 16, grp = l / 16) holds the 16-byte words 4 w + grp of
+// token n's K row (one contiguous 1 KiB load per w from the lane-transposed
+// record), the matching query dims of head n, and receives the
+// scores of tokens 4 grp + i (i < 4) of head n.  A block's (m_b, s_b) of head
+// n is then a 4-element max/sum in the lane and two cross-lane steps (xor 16,
+// 32).  The query, pre-scaled by log2(e) / sqrt(128), is split into NQ
+// operand-precision terms (fp16 hi + lo for fp16 and fp8 K, bf16 hi + mid +
+// lo for bf16 K) so the fp32 accumulation sees ~22-24 bits of it; fp8 K is
+// widened to fp16 exactly and its block scale multiplies the scores.
+template <int DT, int G, int W>
+__global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
+    Geo g, const float* __restrict__ q, const int32_t* __restrict__ ctx_blocks,
+    const uint8_t* __restrict__ kt, const float* __restrict__ kt_scales, uint64_t kt_mod,
+    float* __restrict__ ws_all, uint32_t* __restrict__ sel, int l0, int nl, int max_n,
+    int* __restrict__ err) {
+  static_assert(G >= 1 && G <= 16, "the score tile holds up to 16 query heads");
+  static_assert(DT == FERRY_F16 || DT == FERRY_BF16 || DT == FERRY_FP8_E4M3, "16/8-bit K");
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  constexpr bool F8 = DT == FERRY_FP8_E4M3, BF = DT == FERRY_BF16;
+  constexpr int D = 128, T = 16, NT = W * 64;
+  constexpr int ES = F8 ? 1 : 2;
+  constexpr uint32_t ROW = D * ES, KT = T * ROW;
+  constexpr int NKW = F8 ? 2 : 4;  // 16-byte K words per lane per block
+  constexpr int EPW = 16 / ES, SUB = EPW / 8;
+  constexpr int NQ = BF ? 3 : 2;   // query terms
+  constexpr int U = 4;             // blocks in flight per wavefront
+  extern __shared__ uint32_t lds[];
+  float* score = reinterpret_cast<float*>(lds);
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wtot[2 * W];
+  __shared__ uint32_t sh[2];
+  __shared__ float red_m[W][G], red_s[W][G], lse_m[G], lse_zi[G];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, grp = lane >> 4;
+  const bool head_lane = grp == 0 && n < G;
+  float* ws = ws_all + (size_t)blockIdx.x * max_n * G * 2;
+  const int n_items = g.n_req * nl;
+  const float qmul = 1.4426950408889634f / sqrtf((float)D);  // log2(e) / sqrt(D)
+
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    __syncthreads();  // the previous item's top-k is done with the LDS
+    const int r = item / nl, l = l0 + item % nl;
+    const int rl = r * g.L + l;
+    int nb = ctx_blocks[r];
+    if (nb < 0) nb = 0;
+    if (nb > max_n || nb > g.max_blocks) {
+      if (tid == 0) set_error(err, FERRY_ERANGE);
+      nb = 0;
+    }
+    const int k = g.k;
+    const int kk = nb < k ? nb : k;
+    uint32_t* out0 = sel + (size_t)rl * g.Hkv * (size_t)k;
+    if (nb <= k) {
+      for (int j = tid; j < k; j += NT)
+        for (int hh = 0; hh < g.Hkv; ++hh) out0[(size_t)hh * k + j] = j < kk ? (uint32_t)j : kNone;
+      continue;
+    }
+    for (int h = 0; h < g.Hkv; ++h) {
+      const uint64_t set = (uint64_t)rl * g.Hkv + h;
+      // ---- Q^T operand: k-step ks, this lane's 8 dims, head n (0 for pad heads)
+      uint32_t qb[NQ][4][4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int d0 = EPW * (4 * (ks / SUB) + grp) + 8 * (ks % SUB);
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          x[e] = n < G ? q[((size_t)rl * g.Hq + (size_t)(h * G + n)) * D + d0 + e] * qmul : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          float a = x[e], b = x[e + 1];
+#pragma unroll
+          for (int t = 0; t < NQ; ++t) {
+            if constexpr (BF) {
+              const uint16_t ah = bf16_rne(a), bh = bf16_rne(b);
+              qb[t][ks][e / 2] = (uint32_t)ah | ((uint32_t)bh << 16);
+              a -= __builtin_bit_cast(float, (uint32_t)ah << 16);
+              b -= __builtin_bit_cast(float, (uint32_t)bh << 16);
+            } else {
+              const _Float16 ah = (_Float16)a, bh = (_Float16)b;
+              qb[t][ks][e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, ah) |
+                                 ((uint32_t)__builtin_bit_cast(uint16_t, bh) << 16);
+              a -= (float)ah;
+              b -= (float)bh;
             }
           }
         }
       }
+      float run_m = -INFINITY, run_s = 0.0f;
+      for (int b0 = wave; b0 < nb; b0 += W * U) {
+        u32x4 kw[U][NKW];
+        float ksc[U];
 #pragma unroll
-      for (int gq = 0; gq < G; ++gq) {
-        float mm = m[gq], ss = s[gq];
+        for (int u = 0; u < U; ++u) {
+          const int b = b0 + W * u;
+          if (b < nb) {  // wavefront-uniform
+            const uint64_t rec = host_index(set, (uint32_t)b, (uint64_t)g.max_blocks, kt_mod);
+            // lane-transposed record: this lane's word w is word 64 w + lane
+            const u32x4* base = reinterpret_cast<const u32x4*>(kt + rec * KT) + lane;
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) lse_merge(mm, ss, __shfl_xor(mm, off), __shfl_xor(ss, off));
-        if (lane == 0) {
-          red_m[wave][gq] = mm;
-          red_s[wave][gq] = ss;
+            for (int w = 0; w < NKW; ++w) kw[u][w] = __builtin_nontemporal_load(base + 64 * w);
+            ksc[u] = F8 ? kt_scales[rec] : 1.0f;
+          }
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int b = b0 + W * u;
+          if (b >= nb) break;  // wavefront-uniform
+          f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const int w = ks / SUB, sub = ks % SUB;
+            u32x4 a;
+            if constexpr (F8) {
+              const mx_u32x2 lo = e4m3x4_to_f16(kw[u][w][2 * sub]);
+              const mx_u32x2 hi = e4m3x4_to_f16(kw[u][w][2 * sub + 1]);
+              a = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            } else {
+              a = kw[u][w];
+            }
+#pragma unroll
+            for (int t = 0; t < NQ; ++t) {
+              const u32x4 bq = {qb[t][ks][0], qb[t][ks][1], qb[t][ks][2], qb[t][ks][3]};
+              if constexpr (BF)
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                            __builtin_bit_cast(bf16x8, bq), s, 0, 0, 0);
+              else
+                s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                           __builtin_bit_cast(f16x8, bq), s, 0, 0, 0);
+            }
+          }
+          float x[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = s[i] * ksc[u];
+          float m = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+          m = fmaxf(m, __shfl_xor(m, 16));
+          m = fmaxf(m, __shfl_xor(m, 32));
+          float e = (exp2f(x[0] - m) + exp2f(x[1] - m)) + (exp2f(x[2] - m) + exp2f(x[3] - m));
+          e += __shfl_xor(e, 16);
+          e += __shfl_xor(e, 32);
+          if (head_lane) {
+            ws[((size_t)b * G + n) * 2] = m;
+            ws[((size_t)b * G + n) * 2 + 1] = e;
+            lse_merge(run_m, run_s, m, e);
+          }
+        }
+      }
+      // the workgroup's (M, S) of every query head
+      if (head_lane) {
+        red_m[wave][n] = run_m;
+        red_s[wave][n] = run_s;
       }
       __syncthreads();
       if (tid < G) {
@@ -626,61 +877,47 @@ __global__ __launch_bounds__(W * 64) void k_select_mass(Geo g, const float* __re
         lse_zi[tid] = 1.0f / ss;
       }
       __syncthreads();
-      float M[G], Zi[G];
+      for (int b = tid; b < nb; b += NT) {
+        float acc = 0.0f;
 #pragma unroll
-      for (int gq = 0; gq < G; ++gq) M[gq] = lse_m[gq], Zi[gq] = lse_zi[gq];
-      // ---- pass 2: each block's probability mass, summed over the heads
-      for (int b0 = wave; b0 < n; b0 += W * U) {
-        u32x4 w[U][NI];
-        float ks[U];
-        load(b0, w, ks);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          if (b0 + W * u >= n) break;
-          float bm = 0.0f;
-#pragma unroll
-          for (int i = 0; i < NI; ++i) {
-            float x[G];
-            logits(w[u][i], ks[u], x);
-            if (p == 0) {
-#pragma unroll
-              for (int gq = 0; gq < G; ++gq) bm += exp2f(x[gq] - M[gq]) * Zi[gq];
-            }
-          }
-#pragma unroll
-          for (int off = 32; off > 0; off >>= 1) bm += __shfl_xor(bm, off);
-          if (lane == 0) score[b0 + W * u] += bm;
-        }
+        for (int gq = 0; gq < G; ++gq)
+          acc += exp2f(ws[((size_t)b * G + gq) * 2] - lse_m[gq]) * ws[((size_t)b * G + gq) * 2 + 1] *
+                 lse_zi[gq];
+        score[b] = h == 0 ? acc : score[b] + acc;
       }
       __syncthreads();
     }
-    for (int b = tid; b < n; b += NT) lds[b] = fkey(score[b]);
+    for (int b = tid; b < nb; b += NT) lds[b] = fkey(score[b]);
     __syncthreads();
-    topk_ascending<W>(lds, n, kk, hist, wtot, sh, out0, g.Hkv, (size_t)k);
-  } else {
-    for (int j = tid; j < kk; j += NT)
-      for (int hh = 0; hh < g.Hkv; ++hh) out0[(size_t)hh * k + j] = (uint32_t)j;
+    topk_ascending<W>(lds, nb, kk, hist, wtot, sh, out0, g.Hkv, (size_t)k);
+    for (int j = kk + tid; j < k; j += NT)
+      for (int hh = 0; hh < g.Hkv; ++hh) out0[(size_t)hh * k + j] = kNone;
   }
-  for (int j = kk + tid; j < k; j += NT)
-    for (int hh = 0; hh < g.Hkv; ++hh) out0[(size_t)hh * k + j] = kNone;
 }
 
-#define FERRY_MASS_INST(DT, G)                                                                  \
-  template __global__ void k_select_mass<DT, G, 4>(Geo, const float*, const int32_t*,           \
-                                                   const uint8_t*, const float*, uint64_t,      \
+#define FERRY_MASS_INST(DT, G)                                                                   \
+  template __global__ void k_select_mass<DT, G, 4>(Geo, const float*, const int32_t*,              \
+                                                   const uint8_t*, const float*, uint64_t, float*, \
                                                    uint32_t*, int, int, int, int*);
-#define FERRY_MASS_INST_G(DT) \
-  FERRY_MASS_INST(DT, 1)      \
-  FERRY_MASS_INST(DT, 2)      \
-  FERRY_MASS_INST(DT, 4)      \
-  FERRY_MASS_INST(DT, 8)
-FERRY_MASS_INST_G(FERRY_F32)
-FERRY_MASS_INST_G(FERRY_F16)
-FERRY_MASS_INST_G(FERRY_BF16)
-FERRY_MASS_INST_G(FERRY_FP8_E4M3)
-template __global__ void k_ktiles_build<2>(Geo, const uint8_t*, const float*, uint8_t*, float*);
-template __global__ void k_ktiles_build<4>(Geo, const uint8_t*, const float*, uint8_t*, float*);
-template __global__ void k_ktiles_build<8>(Geo, const uint8_t*, const float*, uint8_t*, float*);
+#define FERRY_MASS_MFMA_INST(DT, G)                                                               \
+  template __global__ void k_select_mass_mfma<DT, G, 8>(Geo, const float*, const int32_t*,         \
+                                                        const uint8_t*, const float*, uint64_t,    \
+                                                        float*, uint32_t*, int, int, int, int*);
+#define FERRY_MASS_MFMA_INST_G(DT) \
+  FERRY_MASS_MFMA_INST(DT, 1)      \
+  FERRY_MASS_MFMA_INST(DT, 2)      \
+  FERRY_MASS_MFMA_INST(DT, 4)      \
+  FERRY_MASS_MFMA_INST(DT, 8)
+FERRY_MASS_INST(FERRY_F32, 1)
+FERRY_MASS_INST(FERRY_F32, 2)
+FERRY_MASS_INST(FERRY_F32, 4)
+FERRY_MASS_INST(FERRY_F32, 8)
+FERRY_MASS_MFMA_INST_G(FERRY_F16)
+FERRY_MASS_MFMA_INST_G(FERRY_BF16)
+FERRY_MASS_MFMA_INST_G(FERRY_FP8_E4M3)
+template __global__ void k_ktiles_build<2>(Geo, const uint8_t*, const float*, uint8_t*, float*, int);
+template __global__ void k_ktiles_build<4>(Geo, const uint8_t*, const float*, uint8_t*, float*, int);
+template __global__ void k_ktiles_build<8>(Geo, const uint8_t*, const float*, uint8_t*, float*, int);
 
 #define FERRY_SUMS_INST(DT)                                                                 \
   template __global__ void k_summaries_build<DT>(Geo, const uint8_t*, const float*, uint8_t*, \

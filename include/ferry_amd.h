@@ -300,6 +300,9 @@ int ferry_select_topk_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float
  * n_records records (a multiple of host_blocks; 0 = one per host block; block
  * (set, b) reads record (set * max_blocks + b) mod n_records, as the
  * summaries), device-direct from the pinned tier, fp8 K scales included.
+ * fp32 records keep the block's row-major order; 16-bit and fp8 records are
+ * lane-transposed for the matrix-core kernel (16-byte word c of token row t
+ * at word 64 (c / 4) + 16 (c % 4) + t), as ferry_ktiles_view shows them.
  * q [B][L][Hq][128] fp32 and ctx_blocks [B] int32 on the device; group 1
  * only; max_blocks <= 15360 (one score per block in LDS).  A context longer
  * than max_blocks latches FERRY_ERANGE and leaves that row EMPTY. */

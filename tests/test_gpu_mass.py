@@ -2,9 +2,10 @@
 method): the dense K table bit-exact against the host tier, and each
 (request, layer)'s page list against the oracle's float64 scores.
 
-The device scores in float32 (exp2 of log2-scaled logits, an online softmax
-merged over lanes and wavefronts), so near-ties may order differently from the
-float64 oracle.  The bar: every row holds min(k, ctx) distinct ascending ids in
+The device scores in float32 (logits on the matrix cores from a 2-3 term
+split of the query for 16-bit and fp8 K, on the vector ALUs for fp32 K; each
+block's softmax maximum and sum merged over wavefronts in the exp2 domain), so
+near-ties may order differently from the float64 oracle.  The bar: every row holds min(k, ctx) distinct ascending ids in
 range, the same list in every kv head's row, EMPTY after; a block that the
 device takes and the oracle does not (or the reverse) scores within
 TOL_MASS x (the row's largest score) of the oracle's k-th score; and at least
@@ -69,6 +70,21 @@ def _check_rows(p, got, q, ctx, rows=None):
     return exact / max(total, 1)
 
 
+def _table_layout(dtype, hk):
+    """Host-tier K halves [n, bytes] in the table's record layout: fp32
+    row-major; 16-bit and fp8 lane-transposed, 16-byte word c of token row t
+    at word 64 (c // 4) + 16 (c % 4) + t."""
+    if dtype == F.F32:
+        return hk
+    n = hk.shape[0]
+    words = hk.reshape(n, 16, -1, 16)  # [record][row][word][16 bytes]
+    out = np.empty((n, words.shape[1] * words.shape[2], 16), np.uint8)
+    for t in range(16):
+        for c in range(words.shape[2]):
+            out[:, 64 * (c // 4) + 16 * (c % 4) + t] = words[:, t, c]
+    return out.reshape(n, -1)
+
+
 @pytest.mark.parametrize("dtype", [F.F32, F.F16, F.BF16, F.FP8])
 def test_ktiles_bit_exact(dtype):
     hb = 1031
@@ -78,7 +94,7 @@ def test_ktiles_bit_exact(dtype):
     kt, scales = p.ex.ktiles_array()
     half = p.bb // 2
     assert kt.shape == (3 * hb, half)
-    hk = p.host.reshape(hb, p.bb)[:, :half]
+    hk = _table_layout(dtype, p.host.reshape(hb, p.bb)[:, :half])
     for c in range(3):
         assert np.array_equal(kt[c * hb:(c + 1) * hb], hk)
     if dtype == F.FP8:
