@@ -365,7 +365,7 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     # top-k selection (Quest bound) over every request's whole context, the
     # step upstream of the miss queue: one launch reads the K summary of every
     # context block of every (request, layer, kv head)
-    select = None
+    select = mass = None
     if w["group"] == 1:
         # one summary record per (set, block): no two blocks share one, so no
         # summary read is served by another block's cache line
@@ -387,6 +387,7 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
                   "ms": round(t_sel, 4), "context_blocks_per_launch": int(ctx.sum()) * L * H,
                   "achieved": round(sel_bytes / (t_sel * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
                   "unit": "GB/s", "frac": round(sel_bytes / (t_sel * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        mass = run_mass(a, ex, F, torch, stream, dtype, w, ctx, dctx, qs, sels[0], sg.max_blocks)
     # ceilings: plain reads of the same bytes (attention slots; host-tier blocks)
     _, _, gather_gbs = ex.bw_probe(F.PROBE_HBM_GATHER, B * L * H, slots=bufs["slots"],
                                    iters=max(3, a.steps // 2), stream=stream)
@@ -430,6 +431,7 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
                            "plain_read_gbs": round(hread_gbs, 2), "dma_copy_gbs": round(hdma_gbs, 2),
                            "frac_of_plain_read": round(link_gbs / hread_gbs, 4)},
         "roofline_select": select,
+        "roofline_select_mass": mass,
         "roofline_handoff": handoff,
         "steals_per_step": round((st2["steals"] - s0) / a.steps, 1),
         "selection_gen_s": round(gen_s, 2),
@@ -446,6 +448,42 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
                                            a.cpu_reqs, a.cpu_steps, reuse_r)
     ex.close()
     return res
+
+
+def run_mass(a, ex, F, torch, stream, dtype, w, ctx, dctx, qs, sel0, max_blocks):
+    """The capture tool's mass selection over every request's whole context:
+    one launch reads the K half of every context block of every (request,
+    layer, kv head) from a dense K table in HBM.  The table gets one record per
+    (set, block), so no two blocks share a record and no read is served by
+    another block's cache line; when that table does not fit in free HBM the
+    measurement is skipped and says why."""
+    B, L, H, Hq, k = w["B"], w["L"], w["Hkv"], w["Hq"], w["k"]
+    hb = a.host_blocks
+    rec = 16 * 128 * F.ESIZE[dtype]
+    n_rec = -(-ex.n_sets * max_blocks // hb) * hb
+    free = torch.cuda.mem_get_info()[0]
+    if n_rec * rec > 0.85 * free:
+        return {"skipped": f"a K table with a record per (set, block) needs {n_rec * rec / 1e9:.0f} GB,"
+                           f" {free / 1e9:.0f} GB of HBM free"}
+    ex.ktiles_build(n_rec, stream)
+    msel = torch.empty_like(sel0)
+    ex.select_mass(qs[0], dctx, msel, stream=stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(a.steps):
+        ex.select_mass(qs[i & 1], dctx, msel, stream=stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    assert ex.stats()["device_error"] == 0
+    t = e0.elapsed_time(e1) / a.steps
+    nb = int(ctx.sum()) * L * H
+    nbytes = nb * (rec + (4 if dtype == F.FP8 else 0)) + B * L * Hq * 128 * 4 + B * L * H * k * 4
+    kern = "k_select_mass" if dtype == F.F32 else "k_select_mass_mfma"
+    gbs = nbytes / (t * 1e-3) / 1e9
+    return {"bound": "hbm", "kernel": f"{kern}<{w['dtype']},{Hq // H}>", "ms": round(t, 4),
+            "context_blocks_per_launch": nb, "k_table_gb": round(n_rec * rec / 1e9, 1),
+            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def run_handoff(a, ex, F, torch, stream, dtype):
@@ -681,6 +719,10 @@ def main():
         with open(tpath) as f:
             r["roofline_select"]["traffic"] = json.load(f).get(a.workload + "_select", {}).get(
                 "bytes_per_launch")
+    if (r.get("roofline_select_mass") or {}).get("ms") and os.path.exists(tpath):
+        with open(tpath) as f:
+            r["roofline_select_mass"]["traffic"] = json.load(f).get(a.workload + "_mass", {}).get(
+                "bytes_per_launch")
     if os.path.exists(tpath):
         with open(tpath) as f:
             fo = json.load(f).get(a.workload + "_fetch")
@@ -715,7 +757,8 @@ def main():
     }
     for key in ("miss_rate", "miss_blocks_per_s", "miss_blocks_per_s_fetch_kernel",
                 "attention_tok_per_s", "kernel_ms", "roofline", "roofline_fetch",
-                "roofline_select", "roofline_handoff", "steals_per_step", "selection_gen_s",
+                "roofline_select", "roofline_select_mass", "roofline_handoff", "steals_per_step",
+                "selection_gen_s",
                 "cpu_baseline"):
         if key in r:
             res[key] = r[key]
