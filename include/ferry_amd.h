@@ -305,7 +305,11 @@ int ferry_select_topk_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float
  * at word 64 (c / 4) + 16 (c % 4) + t), as ferry_ktiles_view shows them.
  * q [B][L][Hq][128] fp32 and ctx_blocks [B] int32 on the device; group 1
  * only; max_blocks <= 15360 (one score per block in LDS).  A context longer
- * than max_blocks latches FERRY_ERANGE and leaves that row EMPTY. */
+ * than max_blocks latches FERRY_ERANGE and leaves that row EMPTY.
+ * The table is a snapshot of the host tier: rebuild it after the tier's
+ * content changes.  The selection keeps each block's softmax max and sum in a
+ * workspace of the context (allocated by ferry_ktiles_build), so two
+ * ferry_select_mass calls on one context must not run concurrently. */
 int ferry_ktiles_build(ferry_ctx* ctx, uint64_t n_records, void* stream);
 int ferry_ktiles_view(ferry_ctx* ctx, void** ktiles, float** scales, uint64_t* n_records);
 int ferry_select_mass(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks, uint32_t* sel,

@@ -206,3 +206,52 @@ def test_refusals():
     torch.cuda.synchronize()
     assert p.ex.stats()["device_error"] == -3
     assert np.all(sel[0].cpu().numpy().view(np.uint32) == O.NONE)
+
+
+def test_mass_selection_feeds_the_executor():
+    """q -> mass selection -> bookkeeping/fetch -> attention over four decode
+    steps: the selection under the near-tie bar, everything downstream of it
+    (slots, misses, state, fetched bytes, attention) against the oracle fed
+    with the device's selection."""
+    n_req, L, Hkv, Hq, k, cap, mb = 4, 2, 2, 8, 24, 96, 400
+    p = Pair(n_req, L, Hkv, Hq, k, cap, mb, F.BF16)
+    p.ex.ktiles_build()
+    rng = np.random.default_rng(12)
+    ctx = np.array([400, 120, 20, 333], np.int32)
+    dctx = torch.from_numpy(ctx).cuda()
+    base = rng.standard_normal((n_req, L, Hq, 128)).astype(np.float32)
+    for t in range(4):
+        q = (base + 0.3 * rng.standard_normal(base.shape)).astype(np.float32)
+        got = _run(p, q, ctx)
+        _check_rows(p, got, q, ctx)
+        p.check_fetched_bytes(p.step(got.reshape(-1)))
+        p.check_state()
+    p.check_attention(got.reshape(-1), seed=3)
+
+
+def _mass_geometry(seed):
+    rng = np.random.default_rng(2000 + seed)
+    dtype = int(rng.choice([F.F32, F.F16, F.BF16, F.FP8]))
+    Hkv = int(rng.choice([1, 2, 4]))
+    G = int(rng.choice([1, 2, 4, 8]))
+    n_req = int(rng.integers(1, 5))
+    L = int(rng.integers(1, 4))
+    k = int(rng.integers(1, 49))
+    mb = int(rng.integers(k + 1, 700))
+    hb = int(rng.choice([7, 1031, 4099]))  # 7: records repeat, identical blocks tie exactly
+    ctx = rng.integers(0, mb + 1, n_req).astype(np.int32)
+    ctx[0] = mb
+    return dict(dtype=dtype, Hkv=Hkv, G=G, n_req=n_req, L=L, k=k, mb=mb, hb=hb), ctx
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_geometry_mass(seed):
+    c, ctx = _mass_geometry(seed)
+    print("[mass geometry]", c, ctx.tolist(), flush=True)
+    p = Pair(c["n_req"], c["L"], c["Hkv"], c["Hkv"] * c["G"], c["k"], c["k"], c["mb"],
+             c["dtype"], host_blocks=c["hb"])
+    p.ex.ktiles_build()
+    q = np.random.default_rng(seed).standard_normal(
+        (c["n_req"], c["L"], c["Hkv"] * c["G"], 128)).astype(np.float32)
+    _check_rows(p, _run(p, q, ctx), q, ctx)
+    assert p.ex.stats()["device_error"] == 0
