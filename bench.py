@@ -95,6 +95,9 @@ def parse():
                     help="mean inter-arrival gap in ticks (0: 0.9 of the lanes' service rate)")
     ap.add_argument("--mmpp-period", type=float, default=1.0,
                     help="mean sojourn of each MMPP state, in ticks (rates 1x and 10x)")
+    ap.add_argument("--queue", action="store_true",
+                    help="the device MPMC ring's push+pop throughput (bench_queue's test) against "
+                         "the ticket rate of one shared word")
     ap.add_argument("--rocprof-summary", metavar="DB",
                     help="summarise a rocprofv3 results database instead of benchmarking")
     ap.add_argument("--last", type=int, default=0,
@@ -654,6 +657,42 @@ def run_arrivals(a, w, F, torch, zipf=None, workers=None, steal=None):
     }
 
 
+def run_queue(F, iters=3):
+    """bench_queue's throughput test (src/benches/bench_queue.cu:127-146): P
+    producer and C consumer threads move n unique tasks through the ring (1 M
+    cells) in one kernel, per-thread and wave-batched reservation, each run
+    checked exactly-once.  Every pop takes one compare-and-swap ticket from the
+    ring's head word, one compare-and-swap per wavefront for its lanes, so the
+    ceiling is the ticket rate of one shared word taken that way by C threads
+    (per-thread mode's pushes take one compare-and-swap per thread; fetch-add
+    for reference).  Under a per-thread compare-and-swap each success costs
+    about one attempt per contending thread, so the runs are sized to ~1-4 M
+    tickets."""
+    rows = []
+    for P, Cn, n, reps in ((512, 512, 1 << 22, iters), (2048, 2048, 1 << 20, 1)):
+        ceil = {}
+        for kind, name in ((2, "wave_cas"), (1, "thread_cas"), (0, "fetch_add")):
+            F.queue_ticket_probe(Cn, 16, kind)  # warm-up
+            t, ms = F.queue_ticket_probe(Cn, (1 << 20) // Cn, kind)
+            ceil[name] = round(t / (ms * 1e-3) / 1e6, 1)
+        print(json.dumps({"threads": Cn, "ticket_ceiling_mops": ceil}), file=sys.stderr, flush=True)
+        for mode, mname in ((0, "per-thread"), (1, "wave")):
+            tot = 0.0
+            for _ in range(reps):
+                popped, dups, ms = F.queue_selftest(1 << 20, n, P, Cn, mode)
+                assert popped == n and dups == 0
+                tot += ms
+            mops = n / (tot / reps * 1e-3) / 1e6
+            # per-thread mode: pushes take per-thread tickets, pops per-wavefront ones
+            bound = ceil["wave_cas"] if mode == 1 else min(ceil["wave_cas"], ceil["thread_cas"])
+            rows.append({"producers": P, "consumers": Cn, "tasks": n, "mode": mname,
+                         "ms": round(tot / reps, 3), "mops": round(mops, 2),
+                         "ticket_ceiling_mops": ceil, "frac_of_ticket_ceiling": round(mops / bound, 4)})
+            print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+    return {"metric": "device MPMC ring push+pop Mops/s (exactly once)", "unit": "Mops/s",
+            "capacity": 1 << 20, "higher_is_better": True, "rows": rows}
+
+
 def main():
     a = parse()
     if a.rocprof_summary:
@@ -677,6 +716,9 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if a.queue:
+        print(json.dumps(run_queue(F)), flush=True)
+        return
     w = WORKLOADS[a.workload]
     if a.arrivals != "none":
         if a.workload == "skew":  # the stealing sweep of config 3 under MMPP arrivals

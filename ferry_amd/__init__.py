@@ -154,6 +154,8 @@ _PROTOS = {
     "ferry_bw_probe": (C.c_int, [_vp, C.c_int, _vp, C.c_uint64, C.c_int,
                                  C.POINTER(C.c_uint64), C.POINTER(C.c_float), _vp]),
     "ferry_stats_reset": (C.c_int, [_vp]),
+    "ferry_queue_ticket_probe": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_uint64),
+                                          C.POINTER(C.c_float)]),
     "ferry_queue_selftest": (C.c_int, [C.c_int, C.c_uint64, C.c_uint64, C.c_int, C.c_int,
                                        C.c_int, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
                                        C.POINTER(C.c_float)]),
@@ -604,3 +606,14 @@ def queue_selftest(capacity=1 << 20, n_tasks=1 << 22, producers=512, consumers=5
     _check(lib.ferry_queue_selftest(device, capacity, n_tasks, producers, consumers, mode,
                                     C.byref(p), C.byref(d), C.byref(ms)), "ferry_queue_selftest")
     return p.value, d.value, ms.value
+
+
+def queue_ticket_probe(threads=512, iters=4096, kind=1, device=0):
+    """Tickets taken from one shared word by `threads` threads, `iters` each:
+    kind 0 fetch-add per thread, kind 1 a load + compare-and-swap retry per
+    thread, kind 2 that retry once per wavefront for its 64 lanes.
+    Returns (tickets, ms)."""
+    t, ms = C.c_uint64(), C.c_float()
+    _check(lib.ferry_queue_ticket_probe(device, threads, iters, kind, C.byref(t), C.byref(ms)),
+           "ferry_queue_ticket_probe")
+    return t.value, ms.value

@@ -146,4 +146,7 @@ __global__ void k_select_mass_mfma(Geo g, const float* q, const int32_t* ctx_blo
 // persistent workgroups of k_select_mass; each holds max_blocks * G * 2 floats of workspace
 constexpr int kMassWgs = 2048;
 
+// queue.hip: the ceiling of the ring's tickets (one shared 64-bit word)
+__global__ void k_ticket_probe(unsigned long long* word, int iters, int kind, int* failed);
+
 }  // namespace ferry_amd

@@ -58,4 +58,40 @@ __global__ __launch_bounds__(256) void k_queue_pc(ferry::DeviceQueue* q, uint64_
   }
 }
 
+// The ceiling of the ring's tickets: every thread takes `iters` tickets from
+// one shared 64-bit word, by
+//  * kind 0: fetch-add per thread (the rate one address accepts returning
+//    atomics);
+//  * kind 1: a relaxed load + compare-and-swap retry per thread, as
+//    kPerThread's push reservation does;
+//  * kind 2: the same retry by the first lane of each wavefront for all 64
+//    lanes, as the wave-batched push and every pop do.
+// A thread whose retries on one ticket pass the queue's spin bound stops and
+// latches `failed`, so every wavefront ends.
+__global__ __launch_bounds__(256) void k_ticket_probe(unsigned long long* word, int iters, int kind,
+                                                      int* failed) {
+  unsigned long long acc = 0;
+  const int lane = threadIdx.x & 63;
+  for (int i = 0; i < iters; ++i) {
+    if (kind == 0) {
+      acc += atomicAdd(word, 1ull);
+      continue;
+    }
+    if (kind == 2 && lane != 0) continue;
+    const unsigned long long n = kind == 2 ? 64 : 1;
+    for (long spin = 0;; ++spin) {
+      const unsigned long long v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (atomicCAS(word, v, v + n) == v) {
+        acc += v;
+        break;
+      }
+      if (spin > ferry::kQueueSpinLimit) {
+        atomicExch(failed, 1);
+        return;
+      }
+    }
+  }
+  if (acc == ~0ull) atomicExch(failed, 2);  // keeps the returned tickets live
+}
+
 }  // namespace ferry_amd

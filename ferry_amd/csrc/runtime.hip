@@ -1256,4 +1256,37 @@ int ferry_queue_selftest(int device, uint64_t capacity, uint64_t n_tasks, int pr
   return FERRY_OK;
 }
 
+int ferry_queue_ticket_probe(int device, int threads, int iters, int kind, uint64_t* tickets,
+                             float* ms) {
+  if (threads < 256 || threads % 256 || threads > 8192)
+    return fail(FERRY_EINVAL, "threads must be a multiple of 256, at most 8192");
+  if (iters < 1 || iters > (1 << 20)) return fail(FERRY_EINVAL, "iters must be in [1, 2^20]");
+  if (kind < 0 || kind > 2) return fail(FERRY_EINVAL, "bad kind");
+  HIPC(hipSetDevice(device));
+  unsigned long long* word = nullptr;
+  HIPC(hipMalloc(&word, 16));
+  HIPC(hipMemset(word, 0, 16));
+  int* failed = reinterpret_cast<int*>(word + 1);
+  hipEvent_t e0, e1;
+  HIPC(hipEventCreate(&e0));
+  HIPC(hipEventCreate(&e1));
+  HIPC(hipEventRecord(e0, 0));
+  hipLaunchKernelGGL(k_ticket_probe, dim3(threads / 256), dim3(256), 0, 0, word, iters, kind, failed);
+  HIPC(hipGetLastError());
+  HIPC(hipEventRecord(e1, 0));
+  HIPC(hipEventSynchronize(e1));
+  float t = 0.0f;
+  HIPC(hipEventElapsedTime(&t, e0, e1));
+  unsigned long long h[2];
+  HIPC(hipMemcpy(h, word, 16, hipMemcpyDeviceToHost));
+  (void)hipFree(word);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (tickets) *tickets = h[0];
+  if (ms) *ms = t;
+  if ((int)h[1] == 1) return fail(FERRY_ESPIN, "ticket retries exceeded the spin bound");
+  if (h[0] != (uint64_t)threads * iters) return fail(FERRY_ESTATE, "ticket count mismatch");
+  return FERRY_OK;
+}
+
 }  // extern "C"

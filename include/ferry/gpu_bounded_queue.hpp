@@ -12,6 +12,12 @@
 //  * kWaveBatched reserves one ticket per active lane of the 64-wide
 //    wavefront with a single CAS by the first active lane (the reference
 //    reserves a fixed 32 per warp) and broadcasts with readfirstlane;
+//  * dq_pop reserves for the wavefront in the same way, in both modes: the
+//    first active lane takes up to one ticket per active lane (fewer when
+//    fewer are queued) with one CAS on head.  A per-lane CAS loop, as in the
+//    reference, makes the 64 lanes of a wavefront race each other for the
+//    same word, one winner per round; on MI355X that holds a ring to ~0.1 M
+//    pops/s under 512 consumers;
 //  * every wait is bounded; a wait that runs out sets `status` and the call
 //    returns false, so a broken protocol ends the kernel instead of hanging.
 #pragma once
@@ -23,13 +29,16 @@ namespace ferry {
 
 enum class ReservationMode { kPerThread = 0, kWaveBatched = 1 };
 
+// head and tail each own a 128-byte line: producers' CAS on tail and
+// consumers' CAS on head then never contend for one L2 line, nor with the
+// read-mostly fields.
 struct DeviceQueue {
   uint64_t* slots = nullptr;  // [capacity] payloads
   uint64_t* seq = nullptr;    // [capacity] cell sequence words
-  uint64_t head = 0;          // next ticket to pop
-  uint64_t tail = 0;          // next ticket to push
   uint64_t capacity = 0;
   int status = 0;             // nonzero once a bounded wait ran out
+  alignas(128) uint64_t head = 0;  // next ticket to pop
+  alignas(128) uint64_t tail = 0;  // next ticket to push
 };
 
 constexpr long kQueueSpinLimit = 1L << 22;
@@ -102,25 +111,52 @@ __device__ inline bool dq_push(DeviceQueue* q, uint64_t task, ReservationMode mo
   return q_publish(q, base + (uint64_t)below, task);
 }
 
-// Pop one task into *out.  false when empty (or a bounded wait ran out).
-__device__ inline bool dq_pop(DeviceQueue* q, uint64_t* out) {
+// Take up to `n` consecutive tickets of pushed tasks; returns how many (0
+// when the ring is empty).  Tickets past the tail are never taken; a taken
+// ticket's task may still be in the producer's hands (reserved, not yet
+// published), and its consumer waits for it.
+__device__ inline uint64_t q_take(DeviceQueue* q, uint64_t n, uint64_t* base) {
   for (long spin = 0; spin < kQueueSpinLimit; ++spin) {
     const uint64_t h = q_load(&q->head);
     const uint64_t t = q_load(&q->tail);
-    if (h >= t) return false;
-    const uint64_t cell = h % q->capacity;
-    if (q_load(q->seq + cell) != h + 1) {  // reserved, not yet published
-      __builtin_amdgcn_s_sleep(2);
-      continue;
+    if (h >= t) return 0;
+    const uint64_t m = t - h < n ? t - h : n;
+    if (atomicCAS((unsigned long long*)&q->head, h, h + m) == h) {
+      *base = h;
+      return m;
     }
-    if (atomicCAS((unsigned long long*)&q->head, h, h + 1) == h) {
-      *out = q->slots[cell];
-      q_store(q->seq + cell, h + q->capacity);
-      return true;
-    }
+    __builtin_amdgcn_s_sleep(1);
   }
   q_fail(q);
-  return false;
+  return 0;
+}
+
+// Pop one task into *out.  false when empty (or a bounded wait ran out).
+// Call it from whole or partial wavefronts alike: the active lanes share one
+// reservation, and a lane left without a ticket sees an empty ring.
+__device__ inline bool dq_pop(DeviceQueue* q, uint64_t* out) {
+  const uint64_t active = __ballot(true);
+  const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(active >> 32),
+                                              __builtin_amdgcn_mbcnt_lo((uint32_t)active, 0));
+  uint64_t base = 0;
+  int got = 0;
+  if (below == 0) got = (int)q_take(q, (uint64_t)__builtin_popcountll(active), &base);
+  got = __builtin_amdgcn_readfirstlane(got);
+  if (below >= got) return false;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32));
+  const uint64_t h = (((uint64_t)hi << 32) | lo) + (uint64_t)below;
+  const uint64_t cell = h % q->capacity;
+  for (long spin = 0; q_load(q->seq + cell) != h + 1; ++spin) {  // reserved, not yet published
+    if (spin >= kQueueSpinLimit) {
+      q_fail(q);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  *out = q->slots[cell];
+  q_store(q->seq + cell, h + q->capacity);
+  return true;
 }
 #endif
 

@@ -370,6 +370,19 @@ int ferry_queue_selftest(int device, uint64_t capacity, uint64_t n_tasks,
                          int producers, int consumers, int mode,
                          uint64_t* popped, uint64_t* duplicates, float* ms);
 
+/* The ceiling of the ring's throughput: `threads` threads take `iters` tickets
+ * each from one shared 64-bit word, by fetch-add per thread (kind 0), by the
+ * relaxed load + compare-and-swap retry per thread that kPerThread's push
+ * reservation uses (kind 1), or by that retry once per wavefront for its 64
+ * lanes (kind 2), as the wave-batched push and every pop reserve.  Every pop
+ * takes its ticket from the head word that way, so tickets/s of kind 2 bound
+ * the pops/s of ferry_queue_selftest.  Returns the tickets taken
+ * (threads * iters) and the kernel time.  No counterpart in the
+ * reference: it is the ceiling bench_queue's Mops/s
+ * (src/benches/bench_queue.cu:127-146) is compared against. */
+int ferry_queue_ticket_probe(int device, int threads, int iters, int kind, uint64_t* tickets,
+                             float* ms);
+
 /* ---- synthetic workload generator (host) ----
  * Stateful per-(request, layer, kv head) top-k selection: keep each previous
  * block with probability `reuse`, complete to k distinct blocks by Zipf(s)
