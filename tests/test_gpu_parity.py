@@ -201,6 +201,26 @@ def test_queue_exactly_once(mode):
     assert popped == 1 << 20 and dups == 0
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+def test_queue_small_ring_partial_pops(mode):
+    # 1000 cells (not a multiple of 64) under 256 producers and 1024 consumers:
+    # the consumers outnumber what is queued, so wavefront pops often get fewer
+    # tickets than lanes asked, and every cell wraps 65 times.  (With fewer
+    # cells than producers, per-thread reservation has no fairness: a lane can
+    # lose the race for a freed cell past the harness's retry bound.)
+    popped, dups, ms = F.queue_selftest(capacity=1000, n_tasks=1 << 16, producers=256,
+                                        consumers=1024, mode=mode)
+    assert popped == 1 << 16 and dups == 0
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_ticket_probe_counts_every_ticket(kind):
+    tickets, ms = F.queue_ticket_probe(threads=512, iters=8, kind=kind)
+    assert tickets == 512 * 8 and ms > 0
+    with pytest.raises(F.FerryError, match="kind"):
+        F.queue_ticket_probe(threads=256, iters=1, kind=3)
+
+
 def test_steal_and_assignment_do_not_change_results():
     n_req, L, H, k, cap = 6, 2, 4, 16, 48
     mb, sels = _zipf_stream(n_req, L, H, k, 100, 400, 4, seed=11)
