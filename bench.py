@@ -527,6 +527,8 @@ def run_handoff(a, ex, F, torch, stream, dtype):
     torch.cuda.synchronize()
     copy_gbs = moved / (ev[0].elapsed_time(ev[1]) / it * 1e-3) / 1e9
     del img, src, dst
+    # and the streaming copy of as many pool blocks (non-temporal loads and stores)
+    _, _, nt_copy_gbs = ex.bw_probe(F.PROBE_HBM_COPY, resident, iters=it, stream=stream)
     bb = ex.block_bytes // 1024
     return {"bound": "hbm", "kernel": f"k_owner_export_data<{bb}> + k_owner_import_data<{bb}>",
             "resident_blocks": resident, "image_gb": round(resident * per / 1e9, 3),
@@ -535,7 +537,9 @@ def run_handoff(a, ex, F, torch, stream, dtype):
             "import_gbs": round(moved / (t_imp * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac_export": round(moved / (t_exp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "frac_import": round(moved / (t_imp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "plain_copy_gbs": round(copy_gbs, 1)}
+            "plain_copy_gbs": round(copy_gbs, 1), "nt_copy_gbs": round(nt_copy_gbs, 1),
+            "frac_of_nt_copy": [round(moved / (t_exp * 1e-3) / 1e9 / nt_copy_gbs, 4),
+                                round(moved / (t_imp * 1e-3) / 1e9 / nt_copy_gbs, 4)]}
 
 
 def arrival_plan(a, w, F, n_ticks, zipf):

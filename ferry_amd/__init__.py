@@ -42,7 +42,7 @@ F32, F16, BF16, FP8 = 0, 1, 2, 3
 LRU_STEP, LRU_SERIAL = 0, 1
 ASSIGN_SPREAD, ASSIGN_AFFINITY = 0, 1
 ATTN_AUTO, ATTN_VALU, ATTN_MFMA = 0, 1, 2
-PROBE_HBM_GATHER, PROBE_HOST_READ, PROBE_HOST_DMA = 0, 1, 2
+PROBE_HBM_GATHER, PROBE_HOST_READ, PROBE_HOST_DMA, PROBE_HBM_COPY = 0, 1, 2, 3
 ARRIVAL_STEADY, ARRIVAL_BURSTY, ARRIVAL_POISSON, ARRIVAL_MMPP = 0, 1, 2, 3
 EMPTY = 0xFFFFFFFF  # selection id of an empty position (and its slot)
 SCHED_FIFO, SCHED_PINNED = 0, 1

@@ -85,6 +85,8 @@ template <int NLD>
 __global__ void k_probe_gather(const uint8_t* pool, uint64_t bb, const uint32_t* slots, int k,
                                uint64_t pool_slots, uint32_t* sink);
 template <int NV>
+__global__ void k_probe_copy(const uint8_t* src, uint8_t* dst, uint64_t bb, uint64_t n_blocks);
+template <int NV>
 __global__ void k_probe_host(const uint8_t* host, uint64_t bb, uint64_t n_blocks, uint32_t* sink);
 
 __global__ void k_hosttier_fill(Geo g, uint8_t* host, float* scales, uint64_t seed, float mult,

@@ -9,7 +9,10 @@
 //    replaced by an XOR;
 //  * k_probe_host: device-direct 16-byte reads of consecutive host-tier
 //    blocks over the host link, as the fetch kernel issues them, without the
-//    ring bookkeeping or the pool writes.
+//    ring bookkeeping or the pool writes;
+//  * k_probe_copy: a streaming device copy of consecutive pool blocks
+//    (non-temporal 16-byte loads and stores), the ceiling of the owner
+//    hand-off, which reads and writes every resident block once.
 // They play the role of the reference's host-staged bandwidth sweep
 // (probe_host_staged_bandwidth, src/topo/topo.cpp:68-129), measured here for
 // the one-hop device-direct path instead of the two-hop pinned ring.
@@ -91,6 +94,24 @@ __global__ __launch_bounds__(256) void k_probe_host(const uint8_t* __restrict__ 
   if (lane == 0) sink[wave] = x;
 }
 
+template <int NV>
+__global__ __launch_bounds__(256) void k_probe_copy(const uint8_t* __restrict__ src,
+                                                    uint8_t* __restrict__ dst, uint64_t bb,
+                                                    uint64_t n_blocks) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const uint64_t n_waves = (uint64_t)gridDim.x * (blockDim.x >> 6);
+  for (uint64_t b = wave; b < n_blocks; b += n_waves) {
+    const u32x4* s = reinterpret_cast<const u32x4*>(src + b * bb);
+    u32x4* d = reinterpret_cast<u32x4*>(dst + b * bb);
+    u32x4 r[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) r[i] = __builtin_nontemporal_load(s + i * kWave + lane);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) __builtin_nontemporal_store(r[i], d + i * kWave + lane);
+  }
+}
+
 template __global__ void k_probe_gather<4>(const uint8_t*, uint64_t, const uint32_t*, int, uint64_t,
                                            uint32_t*);
 template __global__ void k_probe_gather<8>(const uint8_t*, uint64_t, const uint32_t*, int, uint64_t,
@@ -100,5 +121,8 @@ template __global__ void k_probe_gather<16>(const uint8_t*, uint64_t, const uint
 template __global__ void k_probe_host<4>(const uint8_t*, uint64_t, uint64_t, uint32_t*);
 template __global__ void k_probe_host<8>(const uint8_t*, uint64_t, uint64_t, uint32_t*);
 template __global__ void k_probe_host<16>(const uint8_t*, uint64_t, uint64_t, uint32_t*);
+template __global__ void k_probe_copy<4>(const uint8_t*, uint8_t*, uint64_t, uint64_t);
+template __global__ void k_probe_copy<8>(const uint8_t*, uint8_t*, uint64_t, uint64_t);
+template __global__ void k_probe_copy<16>(const uint8_t*, uint8_t*, uint64_t, uint64_t);
 
 }  // namespace ferry_amd

@@ -1095,12 +1095,14 @@ int ferry_owner_import(ferry_ctx* ctx, uint32_t owner, const void* image, uint64
 int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, int iters,
                    uint64_t* bytes, float* ms, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
-  if (kind < FERRY_PROBE_HBM_GATHER || kind > FERRY_PROBE_HOST_DMA) return fail(FERRY_EINVAL, "bad kind");
+  if (kind < FERRY_PROBE_HBM_GATHER || kind > FERRY_PROBE_HBM_COPY) return fail(FERRY_EINVAL, "bad kind");
   if (n < 1 || iters < 1) return fail(FERRY_EINVAL, "n and iters must be positive");
   if (kind == FERRY_PROBE_HBM_GATHER && (!slots || n > 0x7FFFFFFFull))
     return fail(FERRY_EINVAL, "gather needs a slot table of at most 2^31 rows");
-  if (kind != FERRY_PROBE_HBM_GATHER && n > ctx->g.host_blocks)
+  if ((kind == FERRY_PROBE_HOST_READ || kind == FERRY_PROBE_HOST_DMA) && n > ctx->g.host_blocks)
     return fail(FERRY_EINVAL, "more blocks than the host tier holds");
+  if (kind == FERRY_PROBE_HBM_COPY && n > ctx->g.pool_slots)
+    return fail(FERRY_EINVAL, "more blocks than the pool holds");
   const Geo& g = ctx->g;
   HIPC(hipSetDevice(ctx->device));
   hipStream_t s = (hipStream_t)stream;
@@ -1113,13 +1115,17 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
     HIPC(hipMalloc(&ctx->probe_sink, words * 4));
     ctx->probe_sink_words = words;
   }
-  const uint64_t moved = kind == FERRY_PROBE_HBM_GATHER ? n * (uint64_t)g.k * g.bb : n * g.bb;
-  if (kind == FERRY_PROBE_HOST_DMA && ctx->probe_dst_bytes < moved) {
+  // bytes per launch: read, plus written for the device copy
+  const uint64_t moved = kind == FERRY_PROBE_HBM_GATHER ? n * (uint64_t)g.k * g.bb
+                         : kind == FERRY_PROBE_HBM_COPY ? 2 * n * g.bb
+                                                        : n * g.bb;
+  const uint64_t dst_bytes = n * g.bb;
+  if ((kind == FERRY_PROBE_HOST_DMA || kind == FERRY_PROBE_HBM_COPY) && ctx->probe_dst_bytes < dst_bytes) {
     if (ctx->probe_dst) HIPC(hipFree(ctx->probe_dst));
     ctx->probe_dst = nullptr;
     ctx->probe_dst_bytes = 0;
-    HIPC(hipMalloc(&ctx->probe_dst, moved));
-    ctx->probe_dst_bytes = moved;
+    HIPC(hipMalloc(&ctx->probe_dst, dst_bytes));
+    ctx->probe_dst_bytes = dst_bytes;
   }
   const int nld = (int)(g.bb / 1024);
   if (nld != 4 && nld != 8 && nld != 16) return fail(FERRY_EINVAL, "unsupported block size");
@@ -1144,7 +1150,17 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
         hipLaunchKernelGGL(k_probe_host<16>, grid, block, 0, s, ctx->host_dev, g.bb, n, ctx->probe_sink);
       return hipGetLastError();
     }
-    return hipMemcpyAsync(ctx->probe_dst, ctx->host, moved, hipMemcpyHostToDevice, s);
+    if (kind == FERRY_PROBE_HBM_COPY) {
+      const dim3 grid((unsigned)std::min<uint64_t>((n + 3) / 4, 8192)), block(256);
+      if (nld == 4)
+        hipLaunchKernelGGL(k_probe_copy<4>, grid, block, 0, s, ctx->pool, ctx->probe_dst, g.bb, n);
+      else if (nld == 8)
+        hipLaunchKernelGGL(k_probe_copy<8>, grid, block, 0, s, ctx->pool, ctx->probe_dst, g.bb, n);
+      else
+        hipLaunchKernelGGL(k_probe_copy<16>, grid, block, 0, s, ctx->pool, ctx->probe_dst, g.bb, n);
+      return hipGetLastError();
+    }
+    return hipMemcpyAsync(ctx->probe_dst, ctx->host, dst_bytes, hipMemcpyHostToDevice, s);
   };
   HIPC(launch());  // warm-up
   hipEvent_t e0, e1;

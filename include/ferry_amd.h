@@ -348,12 +348,16 @@ int ferry_owner_import(ferry_ctx* ctx, uint32_t owner, const void* image, uint64
  *                           [0, n) by the fetch workgroups, no pool writes
  *   FERRY_PROBE_HOST_DMA    hipMemcpyAsync of host-tier blocks [0, n) into
  *                           device memory (the copy engines)
+ *   FERRY_PROBE_HBM_COPY    a streaming copy of pool slots [0, n) into device
+ *                           memory (non-temporal loads and stores, the owner
+ *                           hand-off's ceiling); bytes = 2*n*block_bytes
  * `bytes` gets the bytes moved per launch, `ms` the mean launch time.  The
  * reference sweeps its host-staged channel the same way
  * (probe_host_staged_bandwidth, src/topo/topo.cpp:68-129). */
 #define FERRY_PROBE_HBM_GATHER 0
 #define FERRY_PROBE_HOST_READ 1
 #define FERRY_PROBE_HOST_DMA 2
+#define FERRY_PROBE_HBM_COPY 3
 int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, int iters,
                    uint64_t* bytes, float* ms, void* stream);
 

@@ -445,6 +445,11 @@ def test_bandwidth_probes_move_the_stated_bytes():
     for kind in (F.PROBE_HOST_READ, F.PROBE_HOST_DMA):
         b, ms, gbs = p.ex.bw_probe(kind, 512, iters=2)
         assert b == 512 * p.bb and ms > 0 and gbs > 0
+    pool = n_req * L * H * 32
+    b, ms, gbs = p.ex.bw_probe(F.PROBE_HBM_COPY, pool, iters=2)  # every pool slot, read + written
+    assert b == 2 * pool * p.bb and ms > 0 and gbs > 0
     with pytest.raises(F.FerryError):
         p.ex.bw_probe(F.PROBE_HOST_READ, 1 << 40)  # more than the host tier holds
+    with pytest.raises(F.FerryError, match="pool"):
+        p.ex.bw_probe(F.PROBE_HBM_COPY, pool + 1)
     assert p.ex.stats()["device_error"] == 0
