@@ -286,6 +286,29 @@ int drain_ring(ferry_ctx* ctx, void* stream, int which);
 
 }  // namespace
 
+namespace {
+// A record table and its fp8 scales, allocated together or not at all: on a
+// failure nothing stays allocated and the caller keeps no table (a table whose
+// record count is 0 would send the selection's record index through mod 0).
+int alloc_table(uint64_t bytes, uint64_t scale_count, uint8_t** table, float** scales) {
+  *table = nullptr;
+  *scales = nullptr;
+  if (hipMalloc(table, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    *table = nullptr;
+    return fail(FERRY_ENOMEM, "record table allocation failed (" + std::to_string(bytes) + " B)");
+  }
+  if (scale_count && hipMalloc(scales, scale_count * 4) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFree(*table);
+    *table = nullptr;
+    *scales = nullptr;
+    return fail(FERRY_ENOMEM, "record scale allocation failed");
+  }
+  return FERRY_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char* ferry_last_error(void) { return g_err.c_str(); }
@@ -803,8 +826,8 @@ int ferry_summaries_build(ferry_ctx* ctx, uint64_t n_records, void* stream) {
     ctx->sum_blocks = 0;
   }
   if (!ctx->sums) {
-    HIPC(hipMalloc(&ctx->sums, S * rec));
-    if (g.dtype == FERRY_FP8_E4M3) HIPC(hipMalloc(&ctx->sum_scales, S * 4ull));
+    if (int rc = alloc_table(S * rec, g.dtype == FERRY_FP8_E4M3 ? S : 0, &ctx->sums, &ctx->sum_scales))
+      return rc;
     ctx->sum_blocks = S;
   }
   const unsigned blocks = (unsigned)std::min<uint64_t>((g.host_blocks + 3) / 4, 16384);
@@ -897,7 +920,8 @@ int ferry_select_topk_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float
   if (g.group != 1)
     return fail(FERRY_EINVAL, "top-k selection needs private sets (group 1): a group's members select "
                               "from their own contexts");
-  if (!ctx->sums) return fail(FERRY_EINVAL, "block summaries not built (ferry_summaries_build)");
+  if (!ctx->sums || !ctx->sum_blocks)
+    return fail(FERRY_EINVAL, "block summaries not built (ferry_summaries_build)");
   const bool layer = mode == FERRY_TOPK_LAYER_MAX;
   const int G = g.Hq / g.Hkv;
   const int Gq = layer ? g.Hq : G;
@@ -943,8 +967,8 @@ int ferry_ktiles_build(ferry_ctx* ctx, uint64_t n_records, void* stream) {
     ctx->kt_records = 0;
   }
   if (!ctx->ktab) {
-    HIPC(hipMalloc(&ctx->ktab, S * KT));
-    if (g.dtype == FERRY_FP8_E4M3) HIPC(hipMalloc(&ctx->ktab_scales, S * 4ull));
+    if (int rc = alloc_table(S * KT, g.dtype == FERRY_FP8_E4M3 ? S : 0, &ctx->ktab, &ctx->ktab_scales))
+      return rc;
     ctx->kt_records = S;
   }
   if (!ctx->mass_ws && (uint64_t)g.max_blocks * 4 <= kMassLds) {
@@ -988,9 +1012,10 @@ int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float
   if (g.group != 1)
     return fail(FERRY_EINVAL, "top-k selection needs private sets (group 1): a group's members select "
                               "from their own contexts");
-  if (!ctx->ktab) return fail(FERRY_EINVAL, "K table not built (ferry_ktiles_build)");
+  if (!ctx->ktab || !ctx->kt_records) return fail(FERRY_EINVAL, "K table not built (ferry_ktiles_build)");
   const size_t lds = (size_t)g.max_blocks * 4;
   if (lds > kMassLds) return fail(FERRY_EINVAL, "max_blocks exceed the mass selection's 60 KiB of LDS");
+  if (!ctx->mass_ws) return fail(FERRY_EINVAL, "no mass-selection workspace (ferry_ktiles_build failed)");
   HIPC(hipSetDevice(ctx->device));
   const dim3 grid((unsigned)std::min<size_t>((size_t)g.n_req * nl, kMassWgs));
   hipStream_t s = (hipStream_t)stream;
