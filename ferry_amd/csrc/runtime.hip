@@ -307,6 +307,20 @@ int alloc_table(uint64_t bytes, uint64_t scale_count, uint8_t** table, float** s
   }
   return FERRY_OK;
 }
+
+// Device buffers and events of a one-off measurement, released on every
+// return path (hipFree waits for the device first).
+struct Scratch {
+  std::vector<void*> bufs;
+  std::vector<hipEvent_t> events;
+  Scratch() = default;
+  Scratch(const Scratch&) = delete;
+  Scratch& operator=(const Scratch&) = delete;
+  ~Scratch() {
+    for (void* p : bufs) (void)hipFree(p);
+    for (hipEvent_t e : events) (void)hipEventDestroy(e);
+  }
+};
 }  // namespace
 
 extern "C" {
@@ -1188,18 +1202,18 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
     return hipMemcpyAsync(ctx->probe_dst, ctx->host, dst_bytes, hipMemcpyHostToDevice, s);
   };
   HIPC(launch());  // warm-up
+  Scratch sc;
   hipEvent_t e0, e1;
   HIPC(hipEventCreate(&e0));
+  sc.events.push_back(e0);
   HIPC(hipEventCreate(&e1));
-  hipError_t err = hipEventRecord(e0, s);
-  for (int i = 0; i < iters && err == hipSuccess; ++i) err = launch();
-  if (err == hipSuccess) err = hipEventRecord(e1, s);
-  if (err == hipSuccess) err = hipEventSynchronize(e1);
+  sc.events.push_back(e1);
+  HIPC(hipEventRecord(e0, s));
+  for (int i = 0; i < iters; ++i) HIPC(launch());
+  HIPC(hipEventRecord(e1, s));
+  HIPC(hipEventSynchronize(e1));
   float t = 0.0f;
-  if (err == hipSuccess) err = hipEventElapsedTime(&t, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  HIPC(err);
+  HIPC(hipEventElapsedTime(&t, e0, e1));
   if (bytes) *bytes = moved;
   if (ms) *ms = t / (float)iters;
   return FERRY_OK;
@@ -1254,18 +1268,24 @@ int ferry_queue_selftest(int device, uint64_t capacity, uint64_t n_tasks, int pr
   ferry::GPUBoundedQueue q(capacity, mode ? ferry::ReservationMode::kWaveBatched
                                           : ferry::ReservationMode::kPerThread);
   if (!q.ok()) return fail(FERRY_ENOMEM, "queue allocation failed");
+  Scratch sc;
   uint32_t* seen = nullptr;
   unsigned long long* counters = nullptr;
   int* flags = nullptr;
   HIPC(hipMalloc(&seen, n_tasks * 4));
+  sc.bufs.push_back(seen);
   HIPC(hipMalloc(&counters, 16));
+  sc.bufs.push_back(counters);
   HIPC(hipMalloc(&flags, 8));
+  sc.bufs.push_back(flags);
   HIPC(hipMemset(seen, 0, n_tasks * 4));
   HIPC(hipMemset(counters, 0, 16));
   HIPC(hipMemset(flags, 0, 8));
   hipEvent_t e0, e1;
   HIPC(hipEventCreate(&e0));
+  sc.events.push_back(e0);
   HIPC(hipEventCreate(&e1));
+  sc.events.push_back(e1);
   const uint32_t pb = producers / 256, cb = consumers / 256;
   HIPC(hipEventRecord(e0, 0));
   hipLaunchKernelGGL(k_queue_pc, dim3(pb + cb), dim3(256), 0, 0, q.device_ptr(),
@@ -1284,11 +1304,6 @@ int ferry_queue_selftest(int device, uint64_t capacity, uint64_t n_tasks, int pr
   uint64_t missing = 0;
   for (uint32_t v : h) missing += v == 0;
   const auto snap = q.snapshot();
-  (void)hipFree(seen);
-  (void)hipFree(counters);
-  (void)hipFree(flags);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
   if (popped) *popped = c[0];
   if (duplicates) *duplicates = c[1];
   if (ms) *ms = t;
@@ -1304,13 +1319,17 @@ int ferry_queue_ticket_probe(int device, int threads, int iters, int kind, uint6
   if (iters < 1 || iters > (1 << 20)) return fail(FERRY_EINVAL, "iters must be in [1, 2^20]");
   if (kind < 0 || kind > 2) return fail(FERRY_EINVAL, "bad kind");
   HIPC(hipSetDevice(device));
+  Scratch sc;
   unsigned long long* word = nullptr;
   HIPC(hipMalloc(&word, 16));
+  sc.bufs.push_back(word);
   HIPC(hipMemset(word, 0, 16));
   int* failed = reinterpret_cast<int*>(word + 1);
   hipEvent_t e0, e1;
   HIPC(hipEventCreate(&e0));
+  sc.events.push_back(e0);
   HIPC(hipEventCreate(&e1));
+  sc.events.push_back(e1);
   HIPC(hipEventRecord(e0, 0));
   hipLaunchKernelGGL(k_ticket_probe, dim3(threads / 256), dim3(256), 0, 0, word, iters, kind, failed);
   HIPC(hipGetLastError());
@@ -1320,9 +1339,6 @@ int ferry_queue_ticket_probe(int device, int threads, int iters, int kind, uint6
   HIPC(hipEventElapsedTime(&t, e0, e1));
   unsigned long long h[2];
   HIPC(hipMemcpy(h, word, 16, hipMemcpyDeviceToHost));
-  (void)hipFree(word);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
   if (tickets) *tickets = h[0];
   if (ms) *ms = t;
   if ((int)h[1] == 1) return fail(FERRY_ESPIN, "ticket retries exceeded the spin bound");
