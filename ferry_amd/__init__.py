@@ -186,6 +186,30 @@ def _ptr(t):
     return t.ctypes.data
 
 
+def _dev(t, name, numel, dtypes, device):
+    """Pointer of a contiguous tensor on CUDA device `device` holding at least
+    `numel` elements of one of `dtypes`: the kernels read and write exactly
+    that many through the raw pointer, so anything else is refused here
+    instead of reaching the device."""
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name}: expected a CUDA tensor, got {type(t).__name__}"
+                         f"{'' if not isinstance(t, torch.Tensor) else ' on ' + str(t.device)}")
+    if t.device.index != device:
+        raise ValueError(f"{name}: on {t.device}, the executor is on cuda:{device}")
+    if t.dtype not in dtypes:
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {' or '.join(map(str, dtypes))}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if t.numel() < numel:
+        raise ValueError(f"{name}: {t.numel()} elements, the geometry needs {numel}")
+    return t.data_ptr()
+
+
+_I32 = (torch.int32,)
+_F32 = (torch.float32,)
+_U8 = (torch.uint8,)
+
+
 def _stream(stream):
     if stream is None:
         return torch.cuda.current_stream().cuda_stream
@@ -226,6 +250,24 @@ class Executor:
         self.close()
 
     # ---- buffers --------------------------------------------------------
+    # ---- argument checks (shapes the kernels index) ---------------------------
+    def _sel(self, t, name="sel"):
+        return _dev(t, name, int(np.prod(self.sel_shape)), _I32, self.device)
+
+    def _q(self, t, name="q"):
+        B, L = self.sel_shape[0], self.sel_shape[1]
+        return _dev(t, name, B * L * self.cfg.q_heads * self.cfg.head_dim, _F32, self.device)
+
+    def _ctx(self, t):
+        return _dev(t, "ctx_blocks", self.sel_shape[0], _I32, self.device)
+
+    def _bufs(self, bufs, flags=True):
+        n = int(np.prod(self.sel_shape))
+        return (_dev(bufs["slots"], "slots", n, _I32, self.device),
+                _dev(bufs["miss_count"], "miss_count", self.n_sets, _I32, self.device),
+                _dev(bufs["misses"], "misses", self.n_sets * self.max_sel * 4, _I32, self.device),
+                _dev(bufs["miss_flag"], "miss_flag", n, _U8, self.device) if flags else None)
+
     def alloc_step_buffers(self):
         dev = torch.device("cuda", self.device)
         return dict(
@@ -240,26 +282,21 @@ class Executor:
         _check(lib.ferry_hosttier_fill(self._h, _stream(stream)), "ferry_hosttier_fill")
 
     def fetch_step(self, sel, bufs, stream=None, flags=True):
-        _check(lib.ferry_fetch_step(self._h, _ptr(sel), _ptr(bufs["slots"]),
-                                    _ptr(bufs["miss_count"]), _ptr(bufs["misses"]),
-                                    _ptr(bufs["miss_flag"]) if flags else None,
+        _check(lib.ferry_fetch_step(self._h, self._sel(sel), *self._bufs(bufs, flags),
                                     _stream(stream)), "ferry_fetch_step")
 
     def bookkeep_step(self, sel, bufs, stream=None, flags=True):
-        _check(lib.ferry_bookkeep_step(self._h, _ptr(sel), _ptr(bufs["slots"]),
-                                       _ptr(bufs["miss_count"]), _ptr(bufs["misses"]),
-                                       _ptr(bufs["miss_flag"]) if flags else None,
+        _check(lib.ferry_bookkeep_step(self._h, self._sel(sel), *self._bufs(bufs, flags),
                                        _stream(stream)), "ferry_bookkeep_step")
 
     def bookkeep_layers(self, l0, nl, sel, bufs, stream=None, flags=True):
-        _check(lib.ferry_bookkeep_layers(self._h, l0, nl, _ptr(sel), _ptr(bufs["slots"]),
-                                         _ptr(bufs["miss_count"]), _ptr(bufs["misses"]),
-                                         _ptr(bufs["miss_flag"]) if flags else None,
+        _check(lib.ferry_bookkeep_layers(self._h, l0, nl, self._sel(sel), *self._bufs(bufs, flags),
                                          _stream(stream)), "ferry_bookkeep_layers")
 
     def sparse_decode_layers(self, l0, nl, q, slots, out, stream=None):
-        _check(lib.ferry_sparse_decode_layers(self._h, l0, nl, _ptr(q), _ptr(slots), _ptr(out),
-                                              _stream(stream)), "ferry_sparse_decode_layers")
+        _check(lib.ferry_sparse_decode_layers(self._h, l0, nl, self._q(q), self._sel(slots, "slots"),
+                                              self._q(out, "out"), _stream(stream)),
+               "ferry_sparse_decode_layers")
 
     def owner_image_bytes(self):
         n = C.c_uint64()
@@ -272,12 +309,12 @@ class Executor:
                            device=torch.device("cuda", self.device))
 
     def owner_export(self, owner, image, stream=None):
-        _check(lib.ferry_owner_export(self._h, owner, _ptr(image), image.numel(), _stream(stream)),
-               "ferry_owner_export")
+        _check(lib.ferry_owner_export(self._h, owner, _dev(image, "image", 0, _U8, self.device),
+                                      image.numel(), _stream(stream)), "ferry_owner_export")
 
     def owner_import(self, owner, image, stream=None):
-        _check(lib.ferry_owner_import(self._h, owner, _ptr(image), image.numel(), _stream(stream)),
-               "ferry_owner_import")
+        _check(lib.ferry_owner_import(self._h, owner, _dev(image, "image", 0, _U8, self.device),
+                                      image.numel(), _stream(stream)), "ferry_owner_import")
 
     def set_batch_policy(self, min_mb=32.0, max_mb=512.0, target_batches=8.0):
         _check(lib.ferry_set_batch_policy(self._h, min_mb, max_mb, target_batches),
@@ -293,21 +330,23 @@ class Executor:
         """Whole step; fetch of layer chunk c+1 (side stream) overlaps attention
         of chunk c (stream).  side_stream None runs everything on one stream.
         chunks 0 = adaptive (from the last step's fetched bytes)."""
-        _check(lib.ferry_decode_step(self._h, _ptr(sel), _ptr(q), _ptr(bufs["slots"]), _ptr(out),
-                                     _ptr(bufs["miss_count"]), _ptr(bufs["misses"]), chunks,
+        slots, miss_count, misses, _ = self._bufs(bufs, flags=False)
+        _check(lib.ferry_decode_step(self._h, self._sel(sel), self._q(q), slots, self._q(out, "out"),
+                                     miss_count, misses, chunks,
                                      _stream(stream),
                                      None if side_stream is None else _stream(side_stream)),
                "ferry_decode_step")
 
     def missq_push(self, misses, n, stream=None):
-        _check(lib.ferry_missq_push(self._h, _ptr(misses), n, _stream(stream)), "ferry_missq_push")
+        _check(lib.ferry_missq_push(self._h, _dev(misses, "misses", 4 * n, _I32, self.device), n,
+                                    _stream(stream)), "ferry_missq_push")
 
     def missq_drain(self, stream=None):
         _check(lib.ferry_missq_drain(self._h, _stream(stream)), "ferry_missq_drain")
 
     def sparse_decode(self, q, slots, out, stream=None):
-        _check(lib.ferry_sparse_decode(self._h, _ptr(q), _ptr(slots), _ptr(out), _stream(stream)),
-               "ferry_sparse_decode")
+        _check(lib.ferry_sparse_decode(self._h, self._q(q), self._sel(slots, "slots"),
+                                       self._q(out, "out"), _stream(stream)), "ferry_sparse_decode")
 
     def summaries_build(self, n_records=0, stream=None):
         """K min/max summaries for select_topk: n_records records (a multiple of
@@ -333,12 +372,12 @@ class Executor:
         """Top-k blocks of every (request, layer, kv head) from q (device
         tensors: q [B,L,Hq,128] fp32, ctx_blocks [B] int32, sel out [B,L,Hkv,k])."""
         if layers is None:
-            _check(lib.ferry_select_topk(self._h, _ptr(q), _ptr(ctx_blocks), mode, _ptr(sel),
-                                         _stream(stream)), "ferry_select_topk")
+            _check(lib.ferry_select_topk(self._h, self._q(q), self._ctx(ctx_blocks), mode,
+                                         self._sel(sel), _stream(stream)), "ferry_select_topk")
         else:
             l0, nl = layers
-            _check(lib.ferry_select_topk_layers(self._h, l0, nl, _ptr(q), _ptr(ctx_blocks), mode,
-                                                _ptr(sel), _stream(stream)),
+            _check(lib.ferry_select_topk_layers(self._h, l0, nl, self._q(q), self._ctx(ctx_blocks),
+                                                mode, self._sel(sel), _stream(stream)),
                    "ferry_select_topk_layers")
 
     def ktiles_build(self, n_records=0, stream=None):
@@ -365,12 +404,12 @@ class Executor:
         """The softmax-mass top-k of every (request, layer), written to every kv
         head's row of sel [B,L,Hkv,k] (device tensors as for select_topk)."""
         if layers is None:
-            _check(lib.ferry_select_mass(self._h, _ptr(q), _ptr(ctx_blocks), _ptr(sel),
+            _check(lib.ferry_select_mass(self._h, self._q(q), self._ctx(ctx_blocks), self._sel(sel),
                                          _stream(stream)), "ferry_select_mass")
         else:
             l0, nl = layers
-            _check(lib.ferry_select_mass_layers(self._h, l0, nl, _ptr(q), _ptr(ctx_blocks),
-                                                _ptr(sel), _stream(stream)),
+            _check(lib.ferry_select_mass_layers(self._h, l0, nl, self._q(q), self._ctx(ctx_blocks),
+                                                self._sel(sel), _stream(stream)),
                    "ferry_select_mass_layers")
 
     def sets_reset(self, stream=None):
@@ -378,8 +417,9 @@ class Executor:
 
     def reset_owners(self, owners, stream=None):
         """Empty the sets of the owners in `owners` (int32 device tensor)."""
-        _check(lib.ferry_sets_reset_owners(self._h, _ptr(owners), int(owners.numel()),
-                                           _stream(stream)), "ferry_sets_reset_owners")
+        _check(lib.ferry_sets_reset_owners(self._h, _dev(owners, "owners", 0, _I32, self.device),
+                                           int(owners.numel()), _stream(stream)),
+               "ferry_sets_reset_owners")
 
     # ---- inspection (synchronous) ---------------------------------------
     def stats(self):
@@ -391,7 +431,11 @@ class Executor:
         """Plain-read bandwidth ceiling (ferry_bw_probe): returns (bytes per
         launch, mean ms per launch, GB/s)."""
         b, ms = C.c_uint64(), C.c_float()
-        _check(lib.ferry_bw_probe(self._h, kind, _ptr(slots), n, iters, C.byref(b), C.byref(ms),
+        if kind == PROBE_HBM_GATHER:  # n rows of the slot table
+            slots_p = _dev(slots, "slots", n * self.cfg.k, _I32, self.device)
+        else:
+            slots_p = None
+        _check(lib.ferry_bw_probe(self._h, kind, slots_p, n, iters, C.byref(b), C.byref(ms),
                                   _stream(stream)), "ferry_bw_probe")
         return b.value, ms.value, b.value / (ms.value * 1e-3) / 1e9
 

@@ -93,3 +93,14 @@ def test_selgen_per_request_reuse_matches_oracle():
         if prev is not None:  # reuse 1.0 keeps the whole selection, 0.0 redraws all of it
             assert np.array_equal(a[4], prev[4])
         prev = a
+
+
+
+def test_host_buffers_are_refused_before_the_call():
+    """The Python mirror refuses buffers that are not CUDA tensors before any
+    pointer reaches the library (the device-side refusals are GPU tests)."""
+    import torch
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        F._dev(torch.zeros(8, dtype=torch.int32), "sel", 8, F._I32, 0)
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        F._dev(np.zeros(8, np.int32), "sel", 8, F._I32, 0)

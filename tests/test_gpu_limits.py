@@ -94,3 +94,31 @@ def test_selection_at_its_largest_context(mode, Hkv, Hq):
         big.ex.select_topk(torch.zeros((1, 1, Hq, 128), device="cuda"),
                            torch.tensor([8], dtype=torch.int32, device="cuda"),
                            torch.empty((1, 1, Hkv, 8), dtype=torch.int32, device="cuda"), mode)
+
+
+def test_wrong_buffers_are_refused_before_the_call():
+    """Host tensors, wrong dtypes, non-contiguous views and buffers smaller
+    than the geometry are refused by the Python mirror before a pointer
+    reaches a kernel; the executor works normally afterwards."""
+    mb, sels = _zipf_stream(2, 2, 2, 8, 30, 60, 1, seed=4)
+    p = Pair(2, 2, 2, 4, 8, 16, mb, F.F16, host_blocks=257)
+    sel = torch.from_numpy(np.ascontiguousarray(sels[0], np.uint32).view(np.int32)).cuda()
+    q = torch.zeros((2, 2, 4, 128), device="cuda")
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        p.ex.fetch_step(sel.cpu(), p.bufs)
+    with pytest.raises(ValueError, match="dtype"):
+        p.ex.fetch_step(sel.float(), p.bufs)
+    with pytest.raises(ValueError, match="contiguous"):
+        p.ex.fetch_step(sel.view(2, 2, 2, 8).transpose(0, 1), p.bufs)
+    with pytest.raises(ValueError, match="elements"):
+        p.ex.fetch_step(sel[: sel.numel() // 2].contiguous(), p.bufs)
+    bad = dict(p.bufs, misses=p.bufs["misses"][:1].contiguous())
+    with pytest.raises(ValueError, match="misses"):
+        p.ex.fetch_step(sel, bad)
+    with pytest.raises(ValueError, match="elements"):
+        p.ex.sparse_decode(q[:1].contiguous(), p.bufs["slots"], torch.empty_like(q))
+    with pytest.raises(ValueError, match="ctx_blocks"):
+        p.ex.summaries_build()
+        p.ex.select_topk(q, torch.zeros(1, dtype=torch.int32, device="cuda"), sel)
+    p.check_fetched_bytes(p.step(sels[0]))
+    assert p.ex.stats()["device_error"] == 0
