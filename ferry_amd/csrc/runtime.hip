@@ -12,6 +12,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <initializer_list>
+#include <utility>
 #include <vector>
 
 #include "common.hpp"
@@ -287,6 +289,28 @@ int drain_ring(ferry_ctx* ctx, void* stream, int which);
 }  // namespace
 
 namespace {
+// A buffer a kernel reads or writes must be memory HIP knows: device, managed
+// or pinned host memory.  Pageable host memory would fault the kernel, so it
+// is refused here.  Sizes cannot be checked (the entry points take bare
+// pointers); the Python mirror checks them.
+int check_buf(const void* p, const char* name) {
+  if (!p) return fail(FERRY_EINVAL, std::string("null ") + name);
+  hipPointerAttribute_t a{};
+  if (hipPointerGetAttributes(&a, p) != hipSuccess || a.type == hipMemoryTypeUnregistered) {
+    (void)hipGetLastError();
+    return fail(FERRY_EINVAL, std::string(name) +
+                                  " is not device-accessible memory (device, managed or pinned host)");
+  }
+  return FERRY_OK;
+}
+
+// check_buf over several buffers, in order
+int check_bufs(std::initializer_list<std::pair<const void*, const char*>> bufs) {
+  for (const auto& b : bufs)
+    if (int rc = check_buf(b.first, b.second)) return rc;
+  return FERRY_OK;
+}
+
 // A record table and its fp8 scales, allocated together or not at all: on a
 // failure nothing stays allocated and the caller keeps no table (a table whose
 // record count is 0 would send the selection's record index through mod 0).
@@ -578,7 +602,7 @@ int ferry_sets_reset(ferry_ctx* ctx, void* stream) {
 int ferry_sets_reset_owners(ferry_ctx* ctx, const uint32_t* owners, uint32_t n, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
   if (n == 0) return FERRY_OK;
-  if (!owners) return fail(FERRY_EINVAL, "null owners");
+  if (int rc = check_buf(owners, "owners")) return rc;
   if (n > (uint32_t)ctx->g.n_owners) return fail(FERRY_EINVAL, "more owners than the executor has");
   HIPC(hipSetDevice(ctx->device));
   const uint64_t waves = (uint64_t)n * ctx->g.L * ctx->g.Hkv;
@@ -603,6 +627,10 @@ int ferry_bookkeep_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const uint32_t
                           uint32_t* slots, uint32_t* miss_count, ferry_miss* misses,
                           uint8_t* miss_flag, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_bufs({{sel, "sel"}, {slots, "slots"}, {miss_count, "miss_count"}, {misses, "misses"}}))
+    return rc;
+  if (miss_flag)
+    if (int rc = check_buf(miss_flag, "miss_flag")) return rc;
   return bookkeep_ring(ctx, l0, nl, sel, slots, miss_count, misses, miss_flag, stream, 0);
 }
 
@@ -678,7 +706,7 @@ int ferry_bookkeep_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots,
 int ferry_missq_push(ferry_ctx* ctx, const ferry_miss* misses, uint32_t n, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
   if (n == 0) return FERRY_OK;
-  if (!misses) return fail(FERRY_EINVAL, "null misses");
+  if (int rc = check_buf(misses, "misses")) return rc;
   HIPC(hipSetDevice(ctx->device));
   hipLaunchKernelGGL(k_missq_push, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, ctx->g,
                      ctx->ring(), misses, n, ctx->err);
@@ -697,7 +725,7 @@ int ferry_fetch_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots, uint3
 int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
                                const uint32_t* slots, float* out, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
-  if (!q || !slots || !out) return fail(FERRY_EINVAL, "null buffer");
+  if (int rc = check_bufs({{q, "q"}, {slots, "slots"}, {out, "out"}})) return rc;
   const Geo& g = ctx->g;
   if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
   HIPC(hipSetDevice(ctx->device));
@@ -741,6 +769,9 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
                       float* out, uint32_t* miss_count, ferry_miss* misses, int32_t chunks,
                       void* stream, void* side_stream) {
   if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_bufs({{sel, "sel"}, {q, "q"}, {slots, "slots"}, {out, "out"},
+                           {miss_count, "miss_count"}, {misses, "misses"}}))
+    return rc;
   const int L = ctx->g.L;
   if (chunks < 0) return fail(FERRY_EINVAL, "chunks < 0");
   const bool adaptive = chunks == 0;
@@ -927,7 +958,7 @@ extern "C" {
 int ferry_select_topk_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
                              const int32_t* ctx_blocks, int mode, uint32_t* sel, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
-  if (!q || !ctx_blocks || !sel) return fail(FERRY_EINVAL, "null buffer");
+  if (int rc = check_bufs({{q, "q"}, {ctx_blocks, "ctx_blocks"}, {sel, "sel"}})) return rc;
   const Geo& g = ctx->g;
   if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
   if (mode != FERRY_TOPK_PER_HEAD && mode != FERRY_TOPK_LAYER_MAX) return fail(FERRY_EINVAL, "bad mode");
@@ -1020,7 +1051,7 @@ int ferry_ktiles_view(ferry_ctx* ctx, void** ktiles, float** scales, uint64_t* n
 int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
                              const int32_t* ctx_blocks, uint32_t* sel, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
-  if (!q || !ctx_blocks || !sel) return fail(FERRY_EINVAL, "null buffer");
+  if (int rc = check_bufs({{q, "q"}, {ctx_blocks, "ctx_blocks"}, {sel, "sel"}})) return rc;
   const Geo& g = ctx->g;
   if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
   if (g.group != 1)
@@ -1076,7 +1107,7 @@ int ferry_owner_image_bytes(const ferry_ctx* ctx, uint64_t* bytes) {
 namespace {
 
 int owner_check(ferry_ctx* ctx, uint32_t owner, const void* image, uint64_t image_bytes) {
-  if (!image) return fail(FERRY_EINVAL, "null image");
+  if (int rc = check_buf(image, "image")) return rc;
   if (owner >= (uint32_t)ctx->g.n_owners) return fail(FERRY_EINVAL, "owner out of range");
   if (image_bytes < make_image_layout(ctx->g).bytes)
     return fail(FERRY_EINVAL, "image buffer smaller than ferry_owner_image_bytes");
@@ -1136,8 +1167,8 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
   if (int rc = check_ctx(ctx)) return rc;
   if (kind < FERRY_PROBE_HBM_GATHER || kind > FERRY_PROBE_HBM_COPY) return fail(FERRY_EINVAL, "bad kind");
   if (n < 1 || iters < 1) return fail(FERRY_EINVAL, "n and iters must be positive");
-  if (kind == FERRY_PROBE_HBM_GATHER && (!slots || n > 0x7FFFFFFFull))
-    return fail(FERRY_EINVAL, "gather needs a slot table of at most 2^31 rows");
+  if (kind == FERRY_PROBE_HBM_GATHER && (check_buf(slots, "slots") || n > 0x7FFFFFFFull))
+    return fail(FERRY_EINVAL, "gather needs a device slot table of at most 2^31 rows");
   if ((kind == FERRY_PROBE_HOST_READ || kind == FERRY_PROBE_HOST_DMA) && n > ctx->g.host_blocks)
     return fail(FERRY_EINVAL, "more blocks than the host tier holds");
   if (kind == FERRY_PROBE_HBM_COPY && n > ctx->g.pool_slots)

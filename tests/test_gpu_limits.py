@@ -122,3 +122,24 @@ def test_wrong_buffers_are_refused_before_the_call():
         p.ex.select_topk(q, torch.zeros(1, dtype=torch.int32, device="cuda"), sel)
     p.check_fetched_bytes(p.step(sels[0]))
     assert p.ex.stats()["device_error"] == 0
+
+
+def test_pageable_memory_is_refused_at_the_c_boundary():
+    """The C entry points take bare pointers; one into pageable host memory
+    (here numpy's) returns FERRY_EINVAL instead of reaching a kernel."""
+    import ctypes as C
+    mb, sels = _zipf_stream(2, 1, 1, 8, 20, 40, 1, seed=6)
+    p = Pair(2, 1, 1, 2, 8, 16, mb, F.F16, host_blocks=257)
+    q_host = np.zeros((2, 1, 2, 128), np.float32)
+    out = torch.empty((2, 1, 2, 128), device="cuda")
+    rc = F.lib.ferry_sparse_decode(p.ex._h, C.c_void_p(q_host.ctypes.data),
+                                   C.c_void_p(p.bufs["slots"].data_ptr()),
+                                   C.c_void_p(out.data_ptr()), None)
+    assert rc == -1 and b"not device-accessible" in F.lib.ferry_last_error()
+    sel_host = np.ascontiguousarray(sels[0], np.uint32)
+    rc = F.lib.ferry_fetch_step(p.ex._h, C.c_void_p(sel_host.ctypes.data),
+                                *[C.c_void_p(p.bufs[k].data_ptr()) for k in
+                                  ("slots", "miss_count", "misses", "miss_flag")], None)
+    assert rc == -1 and b"sel" in F.lib.ferry_last_error()
+    p.check_fetched_bytes(p.step(sels[0]))  # nothing was launched; the executor works
+    assert p.ex.stats()["device_error"] == 0
