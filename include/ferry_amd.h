@@ -7,6 +7,10 @@
  * Every function returns an int status (FERRY_OK == 0, negative on error) and
  * never exits the process; the reference aborted instead
  * (src/common/cuda_check.cuh:9-28, src/workloads/miss_trace.cuh:64-71).
+ * Buffers a kernel reads or writes must be device, managed or pinned host
+ * memory: a null pointer or one into pageable host memory returns
+ * FERRY_EINVAL before anything is launched.  Their sizes follow from the
+ * context's geometry and are the caller's to get right.
  *
  * The reference exposes this path as header-only C++ (namespace ferry) with
  * no FFI; each entry point below names the reference interface it replaces.
