@@ -148,3 +148,35 @@ def test_selection_errors():
     torch.cuda.synchronize()
     assert p.ex.stats()["device_error"] == -3  # FERRY_ERANGE: context longer than max_blocks
     assert np.all(sel.cpu().numpy()[0] == -1)  # that row is left empty
+
+
+def _topk_geometry(seed):
+    rng = np.random.default_rng(3000 + seed)
+    dtype = int(rng.choice([F.F32, F.F16, F.BF16, F.FP8]))
+    Hkv = int(rng.choice([1, 2, 4]))
+    G = int(rng.choice([1, 2, 4, 8]))
+    mode = int(rng.choice([F.TOPK_PER_HEAD, F.TOPK_LAYER_MAX]))
+    n_req = int(rng.integers(1, 5))
+    L = int(rng.integers(1, 4))
+    k = int(rng.integers(1, 49))
+    mb = int(rng.integers(k + 1, 900))
+    hb = int(rng.choice([7, 1031, 4099]))  # 7: records repeat, identical blocks tie exactly
+    ctx = rng.integers(0, mb + 1, n_req).astype(np.int32)
+    ctx[0] = mb
+    return dict(dtype=dtype, Hkv=Hkv, G=G, mode=mode, n_req=n_req, L=L, k=k, mb=mb, hb=hb), ctx
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_geometry_topk_bit_exact(seed):
+    c, ctx = _topk_geometry(seed)
+    print("[topk geometry]", c, ctx.tolist(), flush=True)
+    Hq = c["Hkv"] * c["G"]
+    p = Pair(c["n_req"], c["L"], c["Hkv"], Hq, c["k"], c["k"], c["mb"], c["dtype"],
+             host_blocks=c["hb"])
+    p.ex.summaries_build()
+    q = np.random.default_rng(seed).standard_normal((c["n_req"], c["L"], Hq, 128)).astype(np.float32)
+    sel = torch.full((c["n_req"], c["L"], c["Hkv"], c["k"]), -7, dtype=torch.int32, device="cuda")
+    p.ex.select_topk(torch.from_numpy(q).cuda(), torch.from_numpy(ctx).cuda(), sel, c["mode"])
+    torch.cuda.synchronize()
+    assert np.array_equal(sel.cpu().numpy().view(np.uint32), O.select_topk(p.g, q, ctx, c["mode"]))
+    assert p.ex.stats()["device_error"] == 0
