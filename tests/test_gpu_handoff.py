@@ -20,13 +20,14 @@ def _owner_rows(arr, owner, L, H):
     return arr.reshape(-1, L * H, *arr.shape[1:])[owner]
 
 
-@pytest.mark.parametrize("dtype,Hkv,Hq", [(F.F16, 2, 2), (F.FP8, 2, 8), (F.F32, 1, 2)])
-def test_owner_moves_between_executors(dtype, Hkv, Hq):
-    n_req, L, k, cap = 4, 3, 16, 40
-    mb, sels = _zipf_stream(n_req, L, Hkv, k, 60, 300, 9, seed=4)
-    X = Pair(n_req, L, Hkv, Hq, k, cap, mb, dtype)
-    Y = Pair(n_req, L, Hkv, Hq, k, cap, mb, dtype)
-    src, dst = 1, 2
+def _move_and_check(dtype, Hkv, Hq, n_req=4, L=3, k=16, cap=40, lo=60, hi=300, seed=4,
+                    src=1, dst=2, host_blocks=4099):
+    """Four steps in X, two unrelated steps in Y, owner src of X exported into
+    lane dst of Y: state, resident bytes, attention and four further steps of
+    the moved request compared between the two executors and the oracle."""
+    mb, sels = _zipf_stream(n_req, L, Hkv, k, lo, hi, 9, seed=seed)
+    X = Pair(n_req, L, Hkv, Hq, k, cap, mb, dtype, host_blocks=host_blocks)
+    Y = Pair(n_req, L, Hkv, Hq, k, cap, mb, dtype, host_blocks=host_blocks)
     for t in range(4):
         X.step(sels[t])
     for t in range(2):  # Y's lane 2 holds someone else's blocks before the move
@@ -83,6 +84,30 @@ def test_owner_moves_between_executors(dtype, Hkv, Hq):
         assert np.array_equal(xm[:, :3], ym[:, :3])  # same blocks, slots, evictions
         Y.check_fetched_bytes(y_fetched)
         Y.check_state()
+
+
+@pytest.mark.parametrize("dtype,Hkv,Hq", [(F.F16, 2, 2), (F.FP8, 2, 8), (F.F32, 1, 2)])
+def test_owner_moves_between_executors(dtype, Hkv, Hq):
+    _move_and_check(dtype, Hkv, Hq)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_owner_moves_random_geometry(seed):
+    rng = np.random.default_rng(4000 + seed)
+    dtype = int(rng.choice([F.F32, F.F16, F.BF16, F.FP8]))
+    Hkv = int(rng.choice([1, 2, 4]))
+    G = int(rng.choice([1, 2, 4, 8]))
+    n_req = int(rng.integers(2, 6))
+    L = int(rng.integers(1, 4))
+    k = int(rng.integers(4, 33))
+    cap = k + int(rng.integers(0, 2 * k + 1))
+    lo = int(rng.integers(k, 3 * k + 2))
+    src, dst = (int(x) for x in rng.choice(n_req, 2, replace=False))
+    print("[handoff geometry]", dict(dtype=dtype, Hkv=Hkv, G=G, n_req=n_req, L=L, k=k, cap=cap,
+                                     lo=lo, src=src, dst=dst), flush=True)
+    _move_and_check(dtype, Hkv, Hkv * G, n_req=n_req, L=L, k=k, cap=cap, lo=lo,
+                    hi=lo + int(rng.integers(0, 300)), seed=seed + 11, src=src, dst=dst,
+                    host_blocks=1031)
 
 
 def test_owner_round_trip_and_refusals():
