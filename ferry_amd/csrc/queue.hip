@@ -4,6 +4,8 @@
 // (src/benches/bench_queue.cu:26-59): producer blocks push unique task ids,
 // consumer blocks pop them and count arrivals per id in seen[].  The grid is
 // small enough to be co-resident, and every wait in the queue is bounded.
+// Consumers count each id's arrivals in seen[]; the host then finds ids that
+// arrived twice or never.
 #include "common.hpp"
 #include "../../include/ferry/gpu_bounded_queue.hpp"
 
@@ -34,12 +36,16 @@ __global__ __launch_bounds__(256) void k_queue_pc(ferry::DeviceQueue* q, uint64_
       if (atomicAdd(prod_blocks_done, 1) + 1 == (int)n_prod_blocks) atomicExch(done, 1);
     }
   } else {
+    const uint64_t n_tasks = per_thread * n_prod_blocks * (uint64_t)blockDim.x;
     long idle = 0;
     unsigned long long mine = 0;
     while (true) {
       uint64_t task;
       if (ferry::dq_pop(q, &task)) {
-        if (atomicAdd(seen + task, 1u) != 0u) atomicAdd(dups, 1ull);
+        // the count's old value is not read back (a non-returning atomic, no
+        // round trip per pop); the host finds ids seen twice or never
+        if (task < n_tasks) atomicAdd(seen + task, 1u);
+        else atomicAdd(dups, 1ull);  // an id no producer pushed
         ++mine;
         idle = 0;
       } else {

@@ -1332,8 +1332,12 @@ int ferry_queue_selftest(int device, uint64_t capacity, uint64_t n_tasks, int pr
   // every id must have arrived exactly once
   std::vector<uint32_t> h(n_tasks);
   HIPC(hipMemcpy(h.data(), seen, n_tasks * 4, hipMemcpyDeviceToHost));
-  uint64_t missing = 0;
-  for (uint32_t v : h) missing += v == 0;
+  uint64_t missing = 0, twice = 0;
+  for (uint32_t v : h) {
+    missing += v == 0;
+    twice += v > 1;
+  }
+  c[1] += twice;
   const auto snap = q.snapshot();
   if (popped) *popped = c[0];
   if (duplicates) *duplicates = c[1];
