@@ -23,8 +23,13 @@ Prints ONE JSON line.  `value` is whole-step decode tokens/s (B / step time).
 Kernel rates come from HIP events around separate launches of each kernel:
   roofline        attention kernel vs 8 TB/s HBM (algorithmic bytes/launch)
   roofline_fetch  fetch kernel vs the PCIe Gen5 x16 host link (63.0 GB/s)
-  roofline_select top-k selection over every context block vs HBM
-  roofline_handoff export / import of one owner's resident KV vs HBM
+  roofline_select top-k selection over every context block vs HBM (Quest
+                  bound over block summaries)
+  roofline_select_mass  the softmax-mass selection over every context token's
+                  key vs HBM, where a K table with a record per (set, block)
+                  fits in free HBM (gqa128k), else the reason it was skipped
+  roofline_handoff export / import of one owner's resident KV vs HBM, with
+                  torch's copy and a streaming copy of as many bytes as ceilings
 cpu_baseline times the oracle's C restatement of the same step (1 thread) on
 2 of the requests (a whole prefix group for grouped workloads), and again on
 every usable host core (at most 16) with one replica of those requests per
@@ -34,6 +39,11 @@ Other workloads (--workload): gqa128k (long-context GQA, bf16, ~30% misses),
 prefix_fp8 (shared-prefix groups, fp8 + scales, cross-request dedup), skew
 (lognormal per-request miss counts; prints a stealing on/off sweep over Zipf
 skew with 304 persistent fetch workgroups), small.
+
+Other modes: --arrivals poisson|mmpp (request arrivals and lane turnover
+through the tick loop), --queue (the device MPMC ring's push+pop rate, the
+reference's bench_queue test, against the ticket rate of one shared word),
+--rocprof-summary / --pmc-summary (profile tables).
 """
 import argparse
 import json
