@@ -74,7 +74,7 @@ WORKLOADS = {
                        zipf=1.1, reuse=0.66, group=16, prefix=512),
     # skewed per-request miss counts (lognormal(2, 1.2) fresh blocks per step), 7B shape
     "skew": dict(B=64, L=32, Hq=32, Hkv=32, k=64, ctx=(256, 2048), C=320, dtype="f16", zipf=1.0,
-                 reuse=0.66, group=1, prefix=0),
+                 reuse=0.66, group=1, prefix=0, lognormal=True),
     "small": dict(B=8, L=4, Hq=8, Hkv=8, k=64, ctx=(256, 2048), C=320, dtype="f16", zipf=1.1,
                   reuse=0.66, group=1, prefix=0),
 }
@@ -87,7 +87,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--workload", default="7b", choices=sorted(WORKLOADS))
     ap.add_argument("--host-blocks", type=int, default=1 << 20)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the cpu_baseline leg (the CPU timing and the oracle gate)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="7b only: leave out the gqa128k and prefix_fp8 sub-objects")
     ap.add_argument("--cpu-reqs", type=int, default=2)
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--steal", type=int, default=1)
@@ -291,13 +294,53 @@ def cpu_baseline_threads(g, sg_args, host_bytes, host_scales, steps, q):
     if any(r["rc"] for r in reps):
         raise RuntimeError("ora_cpu_step failed in a worker thread")
     return {"value": round(T * n_req * steps / wall, 3), "unit": "tok/s", "cores": T,
+            "host_cores": os.cpu_count(), "usable_cores": len(os.sched_getaffinity(0)),
+            "why_not_all": "one GPU's share of the host is 16 cores; the other cores of a "
+                           "multi-GPU host belong to the other GPUs' processes"
+            if T < (os.cpu_count() or T) else None,
             "sample": f"{T} threads, each an independent replica of the same {n_req} requests, "
                       f"{steps} concurrent steps after one untimed cold step; "
                       f"{wall / steps * 1e3:.0f} ms per concurrent step",
             "ms_per_step": round(wall / steps * 1e3, 1)}
 
 
-def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_cpu=True):
+PREROLL_WINDOW = 5      # steps per window of the settling test
+PREROLL_MIN = 20        # at least this many untimed steps from the cold pool
+PREROLL_MAX = 200       # and at most this many
+PREROLL_TOL = 0.01      # settled: two consecutive windows' miss rates within 1%
+
+
+def preroll(a, ex, sg, torch, dev, step_fn, gate, q, bufs):
+    """Untimed steps from the cold pool until the per-step miss rate settles:
+    the mean miss rate of the last window of PREROLL_WINDOW steps is within
+    PREROLL_TOL (relative) of the window before it, after at least
+    PREROLL_MIN steps.  Selections are drawn one step at a time.  With a gate
+    (the oracle replaying the first owners) every step is checked against it.
+    Returns the steps run and their miss rates."""
+    rates = []
+    W = PREROLL_WINDOW
+    for t in range(PREROLL_MAX):
+        sel = sg.step(t)
+        dsel = torch.from_numpy(sel.view(np.int32)).to(dev)
+        s0 = ex.stats()
+        step_fn(dsel, q)
+        torch.cuda.synchronize()
+        s1 = ex.stats()
+        if s1["device_error"]:
+            raise RuntimeError(f"device error {s1['device_error']} in pre-roll step {t}")
+        rates.append((s1["misses"] - s0["misses"]) / max(1, s1["selections"] - s0["selections"]))
+        if gate is not None:
+            gate.step(sel, bufs)
+        n = len(rates)
+        if n >= max(PREROLL_MIN, 2 * W):
+            last, prev = np.mean(rates[-W:]), np.mean(rates[-2 * W:-W])
+            if abs(last - prev) <= PREROLL_TOL * max(last, 1e-9):
+                break
+    return len(rates), rates
+
+
+def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_cpu=True,
+        extras=True, steps=None):
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream()
     side = torch.cuda.Stream()  # default priority
@@ -306,21 +349,18 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     steal = a.steal if steal is None else steal
     workers = a.workers if workers is None else workers
     zipf = w["zipf"] if zipf is None else zipf
+    n_timed = a.steps if steps is None else steps
     ctx = contexts(F, w)
     sg = F.SelGen(B, L, H, k, ctx, dist=1, zipf_s=zipf, reuse=w["reuse"], group=w["group"],
                   prefix_blocks=w["prefix"], seed=3)
     reuse_r = None
-    if a.workload == "skew":
+    if w.get("lognormal"):
         reuse_r = lognormal_reuse(B, k)
         sg.set_reuse(reuse_r)
-    n_steps = a.warmup + 2 * a.steps
-    t0 = time.perf_counter()
-    sels = [torch.from_numpy(sg.step(t).view(np.int32)).to(dev) for t in range(n_steps)]
-    gen_s = time.perf_counter() - t0
     qs = [torch.randn((B, L, Hq, 128), device=dev, dtype=torch.float32) for _ in range(2)]
     out = torch.empty_like(qs[0])
     if assign is None:
-        assign = F.ASSIGN_AFFINITY if a.workload == "skew" else F.ASSIGN_SPREAD
+        assign = F.ASSIGN_AFFINITY if w.get("lognormal") else F.ASSIGN_SPREAD
     attn = {"auto": F.ATTN_AUTO, "valu": F.ATTN_VALU, "mfma": F.ATTN_MFMA}[a.attn]
     ex = F.Executor(B, L, H, k, C, sg.max_blocks, q_heads=Hq, group=w["group"], dtype=dtype,
                     host_blocks=a.host_blocks, fetch_workers=workers, steal=steal, assign=assign,
@@ -329,12 +369,33 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     bufs = ex.alloc_step_buffers()
     torch.cuda.synchronize()
 
-    def step(t):
+    def step_q(sel, q):
         if a.chunks != 1:
-            ex.decode_step(sels[t], qs[t & 1], bufs, out, chunks=a.chunks, stream=stream,
-                           side_stream=side)
+            ex.decode_step(sel, q, bufs, out, chunks=a.chunks, stream=stream, side_stream=side)
         else:
-            ex.decode_step(sels[t], qs[t & 1], bufs, out, chunks=1, stream=stream)
+            ex.decode_step(sel, q, bufs, out, chunks=1, stream=stream)
+
+    # untimed pre-roll to the steady state; the oracle (the cpu_baseline leg's
+    # checker) replays the first owners of the same stream and gates the run
+    gate = None
+    if not a.no_cpu:
+        from oracle.gate import OwnerReplay
+
+        gate = OwnerReplay(n_req=B, group=w["group"], n_layers=L, kv_heads=H, q_heads=Hq, k=k,
+                           slots_per_set=C, max_blocks=sg.max_blocks, dtype=dtype,
+                           host_blocks=a.host_blocks)
+    t0 = time.perf_counter()
+    n_pre, pre_rates = preroll(a, ex, sg, torch, dev, step_q, gate, qs[0], bufs)
+    gate_res = gate.final(ex, qs[0], out) if gate is not None else None
+    pre_s = time.perf_counter() - t0
+    n_steps = a.warmup + 2 * n_timed
+    t0 = time.perf_counter()
+    sels = [torch.from_numpy(sg.step(n_pre + t).view(np.int32)).to(dev) for t in range(n_steps)]
+    gen_s = time.perf_counter() - t0
+    torch.cuda.synchronize()
+
+    def step(t):
+        step_q(sels[t], qs[t & 1])
 
     for t in range(a.warmup):
         step(t)
@@ -343,7 +404,7 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     # timed region: K whole steps, synchronised on both sides
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for t in range(a.warmup, a.warmup + a.steps):
+    for t in range(a.warmup, a.warmup + n_timed):
         step(t)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
@@ -351,12 +412,13 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     if st1["device_error"]:
         raise RuntimeError(f"device error {st1['device_error']}")
     timed_misses = st1["misses"] - st0["misses"]
+    timed_sel = st1["selections"] - st0["selections"]
 
     # per-kernel durations: K further steps, each kernel bracketed by HIP events
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_timed)]
     m0, s0 = ex.stats()["misses"], ex.stats()["steals"]
-    for i in range(a.steps):
-        t = a.warmup + a.steps + i
+    for i in range(n_timed):
+        t = a.warmup + n_timed + i
         e = evs[i]
         e[0].record(stream)
         ex.bookkeep_step(sels[t], bufs, flags=False)
@@ -370,16 +432,16 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     # attention alone, back to back over the last step's slot table
     r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     r0.record(stream)
-    for i in range(a.steps):
+    for i in range(n_timed):
         ex.sparse_decode(qs[i & 1], bufs["slots"], out)
     r1.record(stream)
     torch.cuda.synchronize()
-    t_attn_rep = r0.elapsed_time(r1) / a.steps
+    t_attn_rep = r0.elapsed_time(r1) / n_timed
     # top-k selection (Quest bound) over every request's whole context, the
     # step upstream of the miss queue: one launch reads the K summary of every
     # context block of every (request, layer, kv head)
-    select = mass = None
-    if w["group"] == 1:
+    select = mass = handoff = None
+    if extras and w["group"] == 1:
         # one summary record per (set, block): no two blocks share one, so no
         # summary read is served by another block's cache line
         hb = a.host_blocks
@@ -389,25 +451,27 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
         ex.select_topk(qs[0], dctx, tsel, stream=stream)
         es0, es1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         es0.record(stream)
-        for i in range(a.steps):
+        for i in range(n_timed):
             ex.select_topk(qs[i & 1], dctx, tsel, stream=stream)
         es1.record(stream)
         torch.cuda.synchronize()
-        t_sel = es0.elapsed_time(es1) / a.steps
+        t_sel = es0.elapsed_time(es1) / n_timed
         rec = 2 * 128 * F.ESIZE[dtype] + (4 if dtype == F.FP8 else 0)
         sel_bytes = int(ctx.sum()) * L * H * rec + B * L * Hq * 128 * 4 + B * L * H * k * 4
         select = {"bound": "hbm", "kernel": f"k_select_topk<{w['dtype']},{Hq // H}>",
                   "ms": round(t_sel, 4), "context_blocks_per_launch": int(ctx.sum()) * L * H,
                   "achieved": round(sel_bytes / (t_sel * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
                   "unit": "GB/s", "frac": round(sel_bytes / (t_sel * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-        mass = run_mass(a, ex, F, torch, stream, dtype, w, ctx, dctx, qs, sels[0], sg.max_blocks)
+        mass = run_mass(a, ex, F, torch, stream, dtype, w, ctx, dctx, qs, sels[0], sg.max_blocks,
+                        n_timed)
     # ceilings: plain reads of the same bytes (attention slots; host-tier blocks)
     _, _, gather_gbs = ex.bw_probe(F.PROBE_HBM_GATHER, B * L * H, slots=bufs["slots"],
-                                   iters=max(3, a.steps // 2), stream=stream)
-    n_host = int(min(a.host_blocks, max(1, (st2["misses"] - m0) // a.steps)))
+                                   iters=max(3, n_timed // 2), stream=stream)
+    n_host = int(min(a.host_blocks, max(1, (st2["misses"] - m0) // n_timed)))
     _, _, hread_gbs = ex.bw_probe(F.PROBE_HOST_READ, n_host, iters=3, stream=stream)
     _, _, hdma_gbs = ex.bw_probe(F.PROBE_HOST_DMA, n_host, iters=3, stream=stream)
-    handoff = run_handoff(a, ex, F, torch, stream, dtype)
+    if extras:
+        handoff = run_handoff(a, ex, F, torch, stream, dtype, n_timed)
     ev_misses = st2["misses"] - m0
     t_book = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
     t_fetch = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
@@ -417,8 +481,8 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     bb = ex.block_bytes
     scale_bytes = 8 if dtype == F.FP8 else 0
     attn_bytes = sel_per_step * (bb + scale_bytes) + 2 * B * L * Hq * 128 * 4 + sel_per_step * 4
-    fetch_bytes = ev_misses / a.steps * (bb + scale_bytes)
-    ms_step = elapsed / a.steps * 1e3
+    fetch_bytes = ev_misses / n_timed * (bb + scale_bytes)
+    ms_step = elapsed / n_timed * 1e3
     attn_gbs = attn_bytes / (t_attn * 1e-3) / 1e9
     link_gbs = fetch_bytes / (t_fetch * 1e-3) / 1e9
     G = Hq // H
@@ -427,9 +491,15 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     res = {
         "ms_per_step": round(ms_step, 3),
         "value": round(B / (ms_step * 1e-3), 2),
-        "miss_rate": round(timed_misses / (a.steps * sel_per_step), 4),
+        "miss_rate": round(timed_misses / max(1, timed_sel), 4),
+        "preroll": {"steps": n_pre, "seconds": round(pre_s, 1),
+                    "miss_rate_first_window": round(float(np.mean(pre_rates[:PREROLL_WINDOW])), 4),
+                    "miss_rate_last_window": round(float(np.mean(pre_rates[-PREROLL_WINDOW:])), 4),
+                    "rule": f"untimed steps from the cold pool until two consecutive "
+                            f"{PREROLL_WINDOW}-step windows' miss rates agree within "
+                            f"{PREROLL_TOL:.0%} (at least {PREROLL_MIN}), then --warmup"},
         "miss_blocks_per_s": round(timed_misses / elapsed, 1),
-        "miss_blocks_per_s_fetch_kernel": round(ev_misses / a.steps / (t_fetch * 1e-3), 1),
+        "miss_blocks_per_s_fetch_kernel": round(ev_misses / n_timed / (t_fetch * 1e-3), 1),
         "attention_tok_per_s": round(B / (t_attn * 1e-3), 1),
         "kernel_ms": {"bookkeep": round(t_book, 4), "fetch": round(t_fetch, 4),
                       "attention": round(t_attn, 4), "attention_back_to_back": round(t_attn_rep, 4)},
@@ -446,13 +516,15 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
         "roofline_select": select,
         "roofline_select_mass": mass,
         "roofline_handoff": handoff,
-        "steals_per_step": round((st2["steals"] - s0) / a.steps, 1),
+        "steals_per_step": round((st2["steals"] - s0) / n_timed, 1),
+        "gate": "pass" if gate_res is not None else "skipped (--no-cpu: no oracle leg)",
+        "gate_detail": gate_res,
         "selection_gen_s": round(gen_s, 2),
         "config_extra": {"slots_per_set": C, "host_tier_blocks": a.host_blocks,
                          "fetch_workers": ex.cfg.fetch_workers, "steal": steal,
                          "assign": "affinity" if assign == F.ASSIGN_AFFINITY else "spread",
                          "chunks": a.chunks if a.chunks else
-                         f"adaptive ({ex.decode_chunks(int(timed_misses / a.steps))})",
+                         f"adaptive ({ex.decode_chunks(int(timed_misses / n_timed))})",
                          "zipf": zipf},
     }
     if want_cpu and not a.no_cpu:
@@ -463,7 +535,7 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     return res
 
 
-def run_mass(a, ex, F, torch, stream, dtype, w, ctx, dctx, qs, sel0, max_blocks):
+def run_mass(a, ex, F, torch, stream, dtype, w, ctx, dctx, qs, sel0, max_blocks, n_timed):
     """The capture tool's mass selection over every request's whole context:
     one launch reads the K half of every context block of every (request,
     layer, kv head) from a dense K table in HBM.  The table gets one record per
@@ -483,12 +555,12 @@ def run_mass(a, ex, F, torch, stream, dtype, w, ctx, dctx, qs, sel0, max_blocks)
     ex.select_mass(qs[0], dctx, msel, stream=stream)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for i in range(a.steps):
+    for i in range(n_timed):
         ex.select_mass(qs[i & 1], dctx, msel, stream=stream)
     e1.record(stream)
     torch.cuda.synchronize()
     assert ex.stats()["device_error"] == 0
-    t = e0.elapsed_time(e1) / a.steps
+    t = e0.elapsed_time(e1) / n_timed
     nb = int(ctx.sum()) * L * H
     nbytes = nb * (rec + (4 if dtype == F.FP8 else 0)) + B * L * Hq * 128 * 4 + B * L * H * k * 4
     kern = "k_select_mass" if dtype == F.F32 else "k_select_mass_mfma"
@@ -499,7 +571,7 @@ def run_mass(a, ex, F, torch, stream, dtype, w, ctx, dctx, qs, sel0, max_blocks)
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def run_handoff(a, ex, F, torch, stream, dtype):
+def run_handoff(a, ex, F, torch, stream, dtype, n_timed):
     """Owner hand-off in steady state: export of owner 0's resident KV and LRU
     state into an image, and import of that image into owner 1 (the per-GPU
     halves of moving a request; the image crossing the link is not timed).
@@ -510,7 +582,7 @@ def run_handoff(a, ex, F, torch, stream, dtype):
     ex.owner_export(0, img, stream)
     torch.cuda.synchronize()
     resident = int(img[24:32].cpu().numpy().view(np.uint64)[0])
-    it = max(3, a.steps // 2)
+    it = max(3, n_timed // 2)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     ev[0].record(stream)
     for _ in range(it):
@@ -756,15 +828,37 @@ def main():
         rows = []
         for s in (0.6, 1.0, 1.4):
             for steal in (0, 1):
-                r = run(a, w, F, torch, steal=steal, workers=304, zipf=s, want_cpu=False)
+                r = run(a, w, F, torch, steal=steal, workers=304, zipf=s, want_cpu=False,
+                        extras=False)
                 rows.append({"zipf": s, "steal": steal, "fetch_ms": r["kernel_ms"]["fetch"],
+                             "attention_ms": r["kernel_ms"]["attention"],
                              "ms_per_step": r["ms_per_step"], "miss_rate": r["miss_rate"],
                              "link_gbs": r["roofline_fetch"]["achieved"],
-                             "steals_per_step": r["steals_per_step"]})
+                             "steals_per_step": r["steals_per_step"],
+                             "preroll_steps": r["preroll"]["steps"], "gate": r["gate"]})
                 print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
         print(json.dumps({"workload": "skew", "rows": rows}), flush=True)
         return
     r = run(a, w, F, torch)
+    # the long-context GQA and shared-prefix configurations, compact, in the same line
+    others = {}
+    if a.workload == "7b" and not a.no_configs:
+        for name in ("gqa128k", "prefix_fp8"):
+            torch.cuda.empty_cache()
+            o = run(a, WORKLOADS[name], F, torch, want_cpu=False, extras=False,
+                    steps=min(a.steps, 10))
+            others[name] = {k2: o[k2] for k2 in ("ms_per_step", "value", "miss_rate",
+                                                  "miss_blocks_per_s", "kernel_ms", "gate")}
+            others[name]["unit"] = "tok/s"
+            others[name]["steps"] = min(a.steps, 10)
+            others[name]["preroll_steps"] = o["preroll"]["steps"]
+            others[name]["roofline"] = {k2: o["roofline"][k2] for k2 in
+                                        ("kernel", "achieved", "peak", "unit", "frac",
+                                         "plain_gather_gbs", "frac_of_plain_gather")}
+            others[name]["roofline_fetch"] = {k2: o["roofline_fetch"][k2] for k2 in
+                                              ("kernel", "achieved", "peak", "unit", "frac",
+                                               "plain_read_gbs", "frac_of_plain_read")}
+            print(json.dumps({name: others[name]}), file=sys.stderr, flush=True)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
@@ -811,13 +905,14 @@ def main():
                         "layers": w["L"], "q_heads": w["Hq"], "kv_heads": w["Hkv"],
                         "top_k": w["k"]}, **r.pop("config_extra")),
     }
-    for key in ("miss_rate", "miss_blocks_per_s", "miss_blocks_per_s_fetch_kernel",
-                "attention_tok_per_s", "kernel_ms", "roofline", "roofline_fetch",
-                "roofline_select", "roofline_select_mass", "roofline_handoff", "steals_per_step",
-                "selection_gen_s",
-                "cpu_baseline"):
+    for key in ("miss_rate", "preroll", "gate", "gate_detail", "miss_blocks_per_s",
+                "miss_blocks_per_s_fetch_kernel", "attention_tok_per_s", "kernel_ms", "roofline",
+                "roofline_fetch", "roofline_select", "roofline_select_mass", "roofline_handoff",
+                "steals_per_step", "selection_gen_s", "cpu_baseline"):
         if key in r:
             res[key] = r[key]
+    if others:
+        res["configs"] = others
     print(json.dumps(res), flush=True)
 
 

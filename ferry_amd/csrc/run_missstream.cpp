@@ -1,8 +1,9 @@
 // run_missstream -- the reference's single-GPU Workload-A driver
 // (src/benches/run_missstream.cu:33-112) over include/ferry/ferry.hpp.
 // Same flags (--hot 1|2|4, --steps, --requests, --layers, --sel, --arrival,
-// --all; --attn is accepted and ignored) and the same output rows.  Unknown
-// flags are an error (exit 2) instead of being ignored.
+// --all; --attn is accepted and ignored) and the same output rows, each with
+// a status field and the blocks the GPU fetched appended.  Unknown flags are
+// an error (exit 2) instead of being ignored.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -12,9 +13,11 @@
 namespace {
 
 void print_wla(const char* name, const ferry::WlAStats& st) {
-  std::printf("  %-10s makespan=%9.2fms steps/s=%8.1f p50=%7.3f p99=%8.3f refill=%8llu bytes=%9.2fMB status=%d\n",
+  std::printf("  %-10s makespan=%9.2fms steps/s=%8.1f p50=%7.3f p99=%8.3f refill=%8llu bytes=%9.2fMB status=%d "
+              "fetched=%llu\n",
               name, st.makespan_ms, st.throughput_steps, st.p50_step_ms, st.p99_step_ms,
-              (unsigned long long)st.refill_events, st.refill_bytes / 1048576.0, st.status);
+              (unsigned long long)st.refill_events, st.refill_bytes / 1048576.0, st.status,
+              (unsigned long long)st.fetched_blocks);
   std::fflush(stdout);
 }
 
@@ -26,9 +29,12 @@ int run_scenario(const ferry::MissSpec& sp, const ferry::AdaptiveBatchPolicy& po
     std::printf("  trace failed: %d %s\n", tr.status, ferry_last_error());
     return 1;
   }
-  std::printf("  trace: selects=%llu miss=%llu hit_rate=%.3f miss_bytes=%.2fMB\n",
+  // miss bytes per selected token: a selection is one 4-token c4 block
+  const double b_per_token =
+      tr.total_selects ? (double)tr.miss_bytes / ((double)tr.total_selects * 4.0) : 0.0;
+  std::printf("  trace: selects=%llu miss=%llu hit_rate=%.3f miss_bytes=%.2fMB miss_B/token=%.1f\n",
               (unsigned long long)tr.total_selects, (unsigned long long)tr.total_misses, tr.hit_rate,
-              tr.miss_bytes / 1048576.0);
+              tr.miss_bytes / 1048576.0, b_per_token);
   std::fflush(stdout);
   const ferry::WlAStats a = ferry::run_miss_workload(0, 0, sp, tr, 0, pol);
   print_wla("baseline-A", a);
@@ -37,7 +43,9 @@ int run_scenario(const ferry::MissSpec& sp, const ferry::AdaptiveBatchPolicy& po
   const ferry::WlAStats c = ferry::run_miss_workload(0, 0, sp, tr, 2, pol);
   print_wla("ferry-C", c);
   if (a.status || b.status || c.status) return 1;
-  std::printf("  => C/A %.2fx  C/B %.2fx\n\n", a.makespan_ms / c.makespan_ms, b.makespan_ms / c.makespan_ms);
+  const double refill_ratio = b.refill_events ? (double)c.refill_events / (double)b.refill_events : 1.0;
+  std::printf("  => C/A %.2fx  C/B %.2fx  refill C/B %.3f\n\n", a.makespan_ms / c.makespan_ms,
+              b.makespan_ms / c.makespan_ms, refill_ratio);
   return 0;
 }
 

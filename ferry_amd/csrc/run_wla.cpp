@@ -18,10 +18,10 @@ namespace {
 
 void print_row(const char* name, const ferry::WlaMultiStats& st) {
   std::printf("  %-9s makespan=%9.2fms steps/s=%7.1f p50=%7.3f p99=%8.3f refill=%8llu seg %9.2fMB "
-              "hit=%.3f ticks=%llu status=%d\n",
+              "hit=%.3f ticks=%llu status=%d fetched=%llu\n",
               name, st.makespan_ms, st.throughput_steps, st.p50_step_ms, st.p99_step_ms,
               (unsigned long long)st.refill_events, st.refill_bytes / 1048576.0, st.hit_rate,
-              (unsigned long long)st.ticks, st.status);
+              (unsigned long long)st.ticks, st.status, (unsigned long long)st.fetched_blocks);
   std::fflush(stdout);
 }
 

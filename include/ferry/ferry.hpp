@@ -20,8 +20,14 @@
 //  * run_miss_workload moves each (request, layer, block) miss as one block of
 //    the HBM pool (fp32 blocks of 16 tokens x 128 dims = 16 KiB, the
 //    reference's c4 at its defaults) and runs real attention over the
-//    selected blocks instead of the FMA proxy; refill_events counts fetched
-//    blocks (there are no host submits to coalesce).
+//    selected blocks instead of the FMA proxy (attn_iters, the proxy's FMA
+//    count, has nothing to set).  refill_events / refill_bytes keep the
+//    reference's meaning per mode -- A: one per selected block, hits
+//    included; B: one per miss; C: one per submit of the coalesced,
+//    policy-batched step misses -- although the GPU moves every missing
+//    block with device-direct reads and has no submits; the blocks it
+//    actually moved are WlAStats::fetched_blocks / WlaMultiStats::
+//    fetched_blocks.
 //  * errors are reported through WlAStats::status / MissTrace::status /
 //    WlaMultiStats::status (a FERRY_E* code) instead of exiting the process.
 //  * run_wla_multigpu accepts exactly one device: it is the per-GPU executor
@@ -100,9 +106,10 @@ struct AdaptiveBatchPolicy {
 struct WlAStats {
   double makespan_ms = 0.0;
   double p50_step_ms = 0.0, p99_step_ms = 0.0;
-  uint64_t refill_events = 0;
-  uint64_t refill_bytes = 0;
+  uint64_t refill_events = 0;  // the reference's transfer count of the mode
+  uint64_t refill_bytes = 0;   // ... and its bytes
   double throughput_steps = 0.0;
+  uint64_t fetched_blocks = 0;  // blocks the GPU fetch moved into the pool
   int status = FERRY_OK;
 };
 
@@ -169,6 +176,57 @@ struct Exec {
   }
 };
 
+// Submits of one request-step under the reference's C engine
+// (src/workloads/kv_exec.cuh:200-268, src/runtime/wla_multigpu.cuh:2529-2601):
+// the step's misses over every layer, sorted by (layer, block) and
+// deduplicated, are cut into batches of pol.choose_mb(pending) MB; inside a
+// batch each run of consecutive blocks of one layer counts as one refill
+// event (a run that would wrap the reference's direct-mapped slot range is
+// sent block by block there, but is still counted once, kv_exec.cuh:250-266).
+// `ml` holds (layer, block) and is reordered.  Returns the events and adds
+// their bytes to *bytes.
+inline uint64_t cmode_submits(std::vector<std::pair<int, uint64_t>>& ml, size_t c4,
+                              const AdaptiveBatchPolicy& pol, uint64_t* bytes) {
+  std::sort(ml.begin(), ml.end());
+  ml.erase(std::unique(ml.begin(), ml.end()), ml.end());
+  uint64_t submits = 0;
+  const size_t n = ml.size();
+  for (size_t i0 = 0; i0 < n;) {
+    const double gmb = pol.choose_mb((double)(n - i0) * (double)c4 / 1048576.0);
+    const size_t take = std::min(std::max<size_t>((size_t)(gmb * 1048576.0 / (double)c4), 1), n - i0);
+    for (size_t k = 0; k < take;) {
+      size_t run = 1;
+      while (k + run < take && ml[i0 + k + run].first == ml[i0 + k].first &&
+             ml[i0 + k + run].second == ml[i0 + k].second + run)
+        ++run;
+      ++submits;
+      *bytes += run * c4;
+      k += run;
+    }
+    i0 += take;
+  }
+  return submits;
+}
+
+// The (layer, block) misses of one owner in the last bookkeeping step, read
+// back from the executor's per-set miss lists (kv_heads 1: set = owner * L +
+// layer).
+inline int owner_misses(const Exec& ex, int owner, int L, std::vector<uint32_t>& mc,
+                        std::vector<ferry_miss>& ms, bool download,
+                        std::vector<std::pair<int, uint64_t>>* out) {
+  if (download) {
+    if (hipMemcpy(mc.data(), ex.mc, mc.size() * 4, hipMemcpyDeviceToHost) ||
+        hipMemcpy(ms.data(), ex.misses, ms.size() * sizeof(ferry_miss), hipMemcpyDeviceToHost))
+      return FERRY_EHIP;
+  }
+  out->clear();
+  for (int l = 0; l < L; ++l) {
+    const size_t set = (size_t)owner * L + l;
+    for (uint32_t i = 0; i < mc[set]; ++i) out->push_back({l, (uint64_t)ms[set * ex.max_sel + i].block});
+  }
+  return FERRY_OK;
+}
+
 }  // namespace detail
 
 // Selections of the reference generator (missstream.cuh:104-133), hit/miss
@@ -226,15 +284,18 @@ inline MissTrace replay_miss_stream(const MissSpec& spec, int device = 0) {
 // selection of a step is fetched; modes 1 (B) and 2 (C): per-selection LRU of
 // hot_blocks slots, one fetch launch per step (B's per-miss submits modelled
 // the host-staged channel, which this build does not have).  Each step then
-// runs sparse attention over the selected blocks (attn_iters is ignored).
+// runs sparse attention over the selected blocks.  The refill counters are
+// the reference's (src/workloads/kv_exec.cuh:108-145, 148-185, 188-292): A
+// counts every selected block, B every miss, C the submits of each
+// request-step's coalesced misses under `pol` (cmode_submits, computed from
+// the executor's own miss lists after each step, outside its timing).
 inline WlAStats run_miss_workload(int src_dev, int dst_dev, const MissSpec& sp, const MissTrace& tr,
                                   int mode, const AdaptiveBatchPolicy& pol, int attn_iters = 8) {
   (void)src_dev;
-  (void)pol;
   (void)attn_iters;
   WlAStats st;
   const int R = sp.num_requests, L = sp.num_layers, S = sp.steps, G = sp.sel_blocks;
-  if (tr.events.size() != (size_t)R * S * L * G) {
+  if (tr.events.size() != (size_t)R * S * L * G || mode < 0 || mode > 2) {
     st.status = FERRY_EINVAL;
     return st;
   }
@@ -242,7 +303,11 @@ inline WlAStats run_miss_workload(int src_dev, int dst_dev, const MissSpec& sp, 
   detail::Exec ex(sp, dst_dev, FERRY_LRU_SERIAL, hot);
   if ((st.status = ex.status)) return st;
   std::vector<uint32_t> step((size_t)R * L * G);
+  std::vector<uint32_t> mc(ex.n_sets);
+  std::vector<ferry_miss> ms((size_t)ex.n_sets * ex.max_sel);
+  std::vector<std::pair<int, uint64_t>> ml;
   std::vector<double> step_ms;
+  uint64_t c_events = 0, c_bytes = 0;
   const auto t0 = std::chrono::steady_clock::now();
   for (int s = 0; s < S; ++s) {
     const auto ts = std::chrono::steady_clock::now();
@@ -263,13 +328,27 @@ inline WlAStats run_miss_workload(int src_dev, int dst_dev, const MissSpec& sp, 
       return st;
     }
     step_ms.push_back(std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - ts).count());
+    if (mode == 2)
+      for (int r = 0; r < R; ++r) {
+        if ((st.status = detail::owner_misses(ex, r, L, mc, ms, r == 0, &ml))) return st;
+        c_events += detail::cmode_submits(ml, sp.c4_bytes(), pol, &c_bytes);
+      }
   }
   st.makespan_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
   ferry_stats fs{};
   ferry_stats_get(ex.ctx, &fs);
   if (fs.device_error) st.status = fs.device_error;
-  st.refill_events = fs.misses;
-  st.refill_bytes = fs.fetched_bytes;
+  st.fetched_blocks = fs.misses;
+  if (mode == 0) {  // one synchronous copy per selected block, hits included
+    st.refill_events = (uint64_t)tr.events.size();
+    st.refill_bytes = st.refill_events * sp.c4_bytes();
+  } else if (mode == 1) {  // one channel submit per miss
+    st.refill_events = fs.misses;
+    st.refill_bytes = fs.misses * sp.c4_bytes();
+  } else {
+    st.refill_events = c_events;
+    st.refill_bytes = c_bytes;
+  }
   st.throughput_steps = st.makespan_ms > 0 ? (double)(R * S) / (st.makespan_ms / 1000.0) : 0.0;
   std::sort(step_ms.begin(), step_ms.end());
   if (!step_ms.empty()) {
@@ -431,12 +510,13 @@ struct WlaMultiStats {
   size_t migrated_bytes = 0;
   uint64_t steals = 0;
   uint64_t migrated_reqs = 0;
-  uint64_t refill_events = 0;  // fetched blocks
-  size_t refill_bytes = 0;
+  uint64_t refill_events = 0;  // the reference's transfer count of the mode
+  size_t refill_bytes = 0;     // ... and its bytes
   double imbalance = 0.0;
   double hit_rate = 0.0;
   int n_gpus = 0;
   uint64_t ticks = 0;
+  uint64_t fetched_blocks = 0;  // blocks the GPU fetch moved into the pool
   int status = FERRY_OK;
 };
 
@@ -474,7 +554,7 @@ inline WlaMultiStats run_wla_multigpu(const std::vector<int>& devices, MissSpec 
                                       const std::string& skew, const std::string& arrival, double gap_ms,
                                       int steal_batch, int attn_iters, WlaKvMode kvmode = WlaKvMode::Full,
                                       double rebal_interval_ms = 50.0, double rebal_thr = 0.25) {
-  (void)pol, (void)spol, (void)skew, (void)steal_batch, (void)attn_iters, (void)kvmode;
+  (void)spol, (void)skew, (void)steal_batch, (void)attn_iters, (void)kvmode;
   (void)rebal_interval_ms, (void)rebal_thr;
   WlaMultiStats st;
   st.n_gpus = (int)devices.size();
@@ -525,6 +605,10 @@ inline WlaMultiStats run_wla_multigpu(const std::vector<int>& devices, MissSpec 
   std::vector<uint32_t> step_ids((size_t)R * L * G);
   std::vector<uint32_t> own;
   std::vector<double> tick_ms;
+  std::vector<uint32_t> mc(ex.n_sets);
+  std::vector<ferry_miss> ms((size_t)ex.n_sets * ex.max_sel);
+  std::vector<std::pair<int, uint64_t>> ml;
+  uint64_t a_events = 0, c_events = 0, c_bytes = 0;
   const auto t0 = std::chrono::steady_clock::now();
   auto elapsed = [&]() { return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count(); };
   for (uint64_t t = 0;; ++t) {
@@ -579,6 +663,18 @@ inline WlaMultiStats run_wla_multigpu(const std::vector<int>& devices, MissSpec 
       }
       if ((st.status = ferry_fetch_step(ex.ctx, ex.sel, ex.slots, ex.mc, ex.misses, nullptr, nullptr))) break;
       if ((st.status = ferry_sparse_decode(ex.ctx, ex.q, ex.slots, ex.out, nullptr))) break;
+      // the reference's refill count of this sub-tick's requests
+      bool first = true;
+      for (int r = 0; r < R && !st.status; ++r) {
+        if (lane_req[r] < 0 || r % group != j) continue;
+        if (mode == 0) {
+          a_events += (uint64_t)L * G;
+        } else if (mode >= 2) {
+          st.status = detail::owner_misses(ex, r / group, L, mc, ms, first, &ml);
+          first = false;
+          c_events += detail::cmode_submits(ml, sp.c4_bytes(), pol, &c_bytes);
+        }
+      }
     }
     if (st.status) break;
     if (hipDeviceSynchronize()) {
@@ -594,8 +690,17 @@ inline WlaMultiStats run_wla_multigpu(const std::vector<int>& devices, MissSpec 
   ferry_stats fs{};
   ferry_stats_get(ex.ctx, &fs);
   if (!st.status && fs.device_error) st.status = fs.device_error;
-  st.refill_events = fs.misses;
-  st.refill_bytes = (size_t)fs.misses * sp.c4_bytes();
+  st.fetched_blocks = fs.misses;
+  if (mode == 0) {  // every selected block of every resident request, hits included (:2489-2504)
+    st.refill_events = a_events;
+    st.refill_bytes = (size_t)a_events * sp.c4_bytes();
+  } else if (mode == 1) {  // one submit per miss (:2505-2526)
+    st.refill_events = fs.misses;
+    st.refill_bytes = (size_t)fs.misses * sp.c4_bytes();
+  } else {  // coalesced, policy-batched submits per request-step (:2527-2604)
+    st.refill_events = c_events;
+    st.refill_bytes = (size_t)c_bytes;
+  }
   st.hit_rate = fs.selections ? 1.0 - (double)fs.misses / (double)fs.selections : 0.0;
   st.throughput_steps = st.makespan_ms > 0 ? (double)R / (st.makespan_ms / 1000.0) : 0.0;
   std::sort(tick_ms.begin(), tick_ms.end());

@@ -25,23 +25,53 @@ def _run(args):
     return res.stdout
 
 
+def _ms_rows(out):
+    """run_missstream rows: name -> (refill, MB, status, fetched)."""
+    rows = {}
+    for m in re.finditer(r"^\s+(baseline-A|baseline-B|ferry-C)\s+makespan=.*refill=\s*(\d+) "
+                         r"bytes=\s*([\d.]+)MB status=(-?\d+) fetched=(\d+)", out, re.M):
+        rows[m.group(1)] = (int(m.group(2)), m.group(3), int(m.group(4)), int(m.group(5)))
+    return rows
+
+
 @pytest.mark.gpu
 def test_driver_golden_default_stream():
-    # results/wla_7rep_20260930/*.log: selects 589,824, misses 79,550, hit 0.865,
-    # refill 1242.97 MB in modes B and C.
+    # results/wla_7rep_20260930/*.log: selects 589,824, misses 79,550, hit 0.865.
+    # The reference's counts per mode (kv_exec.cuh:108-145, 148-185, 188-292):
+    # A copies every selected block (589,824 = 9216.00 MB), B submits every miss
+    # (79,550 = 1242.97 MB), C one submit per coalesced run of a request-step's
+    # misses under run_missstream's policy (target 8 batches,
+    # run_missstream.cu:101), which the oracle's restated planner counts.
+    from oracle import pyoracle as O
+
     out = _run(["--requests", "48", "--layers", "12", "--steps", "16", "--sel", "64", "--hot", "1"])
     assert "selects=589824 miss=79550 hit_rate=0.865 miss_bytes=1242.97MB" in out
-    for mode in ("baseline-B", "ferry-C"):
-        row = re.search(mode + r".*refill=\s*(\d+) bytes=\s*([\d.]+)MB status=(-?\d+)", out)
-        assert row and row.group(1) == "79550" and row.group(2) == "1242.97" and row.group(3) == "0"
+    rows = _ms_rows(out)
+    blocks, miss, _, nm = O.ref_replay(48, 12, 16, 64, 128)
+    assert nm == 79550
+    c_runs, c_bytes = O.ref_cmode_runs(48, 12, 16, 64, 128, 16384, blocks, miss, target=8.0)
+    assert rows["baseline-A"][:3] == (589824, "9216.00", 0)
+    assert rows["baseline-B"][:3] == (79550, "1242.97", 0)
+    assert rows["ferry-C"][:3] == (c_runs, "1242.97", 0) and c_bytes == 79550 * 16384
+    # the GPU moved each miss once in B and C (A: every distinct block per step)
+    assert rows["baseline-B"][3] == rows["ferry-C"][3] == 79550
+    assert 79550 < rows["baseline-A"][3] <= 589824
+    ratio = re.search(r"refill C/B ([\d.]+)", out).group(1)
+    assert ratio == f"{c_runs / 79550:.3f}"
 
 
 @pytest.mark.gpu
 def test_driver_golden_single_gpu_run():
-    # 实验设计.txt:494-495: 4 req x 12 layers x 4 steps, sel 128, hot 1024 -> 57.66 MB.
+    # 实验设计.txt:494-495: 4 req x 12 layers x 4 steps, sel 128, hot 1024 ->
+    # 57.66 MB of misses; the C engine's submits drop from 3690 to 1227.
     out = _run(["--requests", "4", "--layers", "12", "--steps", "4", "--sel", "128", "--hot", "4"])
     assert "miss=3690" in out and "miss_bytes=57.66MB" in out
-    assert re.search(r"ferry-C .*refill=\s*3690 bytes=\s*57.66MB status=0", out)
+    rows = _ms_rows(out)
+    assert rows["baseline-A"][:3] == (24576, "384.00", 0)
+    assert rows["baseline-B"][:3] == (3690, "57.66", 0)
+    assert rows["ferry-C"][:3] == (1227, "57.66", 0)
+    assert rows["baseline-B"][3] == rows["ferry-C"][3] == 3690
+    assert "refill C/B 0.333" in out
 
 
 WLA = os.path.join(ROOT, "ferry_amd", "run_wla")
@@ -57,11 +87,12 @@ def test_wla_driver_rejects_bad_flags():
 
 
 def _rows(out):
+    """run_wla rows: mode -> (refill, MB, hit, ticks, status, fetched)."""
     rows = {}
     for m in re.finditer(r"^\s+([ABC])\s+makespan=.*refill=\s*(\d+) seg\s+([\d.]+)MB hit=([\d.]+) "
-                         r"ticks=(\d+) status=(-?\d+)", out, re.M):
+                         r"ticks=(\d+) status=(-?\d+) fetched=(\d+)", out, re.M):
         rows[m.group(1)] = (int(m.group(2)), m.group(3), float(m.group(4)), int(m.group(5)),
-                            int(m.group(6)))
+                            int(m.group(6)), int(m.group(7)))
     return rows
 
 
@@ -78,14 +109,18 @@ def _run_wla(args, env=None):
 def test_wla_slice_default_stream_with_bursty_arrivals():
     # The reference's default stream through the per-GPU tick loop: requests
     # arrive in bursts and run interleaved, but each has its own hot cache, so
-    # modes B and C refill exactly the replay's 79,550 misses (1242.97 MB).
+    # the refill counts are the reference's golden rows (results/
+    # wla_7rep_20260930/*.log l.2-4, default policy target 4): A 589,824
+    # selected blocks, B 79,550 misses, C 59,863 coalesced submits, the last
+    # two 1242.97 MB; the GPU fetched the 79,550 misses once in B and C.
     out = _run_wla(["--requests", "48", "--layers", "12", "--steps", "16", "--sel", "64",
                     "--hot", "128", "--arrival", "bursty", "--gap", "0.2"])
     rows = _rows(out)
+    assert rows["A"][0] == 589824 and rows["A"][1] == "9216.00" and rows["A"][4] == 0
+    assert rows["B"][0] == 79550 and rows["C"][0] == 59863
     for mode in "BC":
-        assert rows[mode][0] == 79550 and rows[mode][1] == "1242.97" and rows[mode][4] == 0
+        assert rows[mode][1] == "1242.97" and rows[mode][4] == 0 and rows[mode][5] == 79550
         assert round(rows[mode][2], 3) == 0.865
-    assert rows["A"][4] == 0 and rows["A"][0] > rows["C"][0]
 
 
 @pytest.mark.gpu
@@ -116,7 +151,7 @@ def test_wla_slice_prefix_groups_match_oracle():
                     max_blocks=64 + 8 * S, dtype=O.F32, granularity=1)
     ex = O.Executor(g)
     step = np.zeros(R, int)
-    misses = ticks = 0
+    misses = ticks = runs = 0
     for t in range(len(clock)):
         live = table[t] >= 0
         if not live.any():
@@ -132,11 +167,17 @@ def test_wla_slice_prefix_groups_match_oracle():
                 continue
             _, _, _, c = ex.step(sel)
             misses += int(c[1])
+            flags = ex.last_flags.reshape(R, L, SEL)
+            for ln in np.nonzero(live)[0]:
+                if ln % GRP == j:  # this request-step's coalesced submits (target 4)
+                    runs += O.ref_cmode_runs(1, L, 1, SEL, HOT, 16384,
+                                             sel[ln, :, 0].astype(np.uint64), flags[ln], target=4.0)[0]
         for ln in np.nonzero(live)[0]:
             step[table[t, ln]] += 1
         ticks += 1
+    assert rows["B"][0] == misses and rows["C"][0] == runs < misses
     for mode in "BC":
-        assert rows[mode][0] == misses and rows[mode][3] == ticks and rows[mode][4] == 0
+        assert rows[mode][3] == ticks and rows[mode][4] == 0 and rows[mode][5] == misses
 
 
 def _fnv1a64(data):
@@ -166,12 +207,18 @@ def test_wla_slice_runs_a_trace(tmp_path):
     assert f"fnv1a64={_fnv1a64(path.read_bytes()):016x}" in out
     _, ids, _, _ = O.trace_load(str(path))
     want = 0
+    miss = np.zeros(ids.shape, np.uint8)  # (r, s, l, k)
     for r in range(R):
         for l in range(L):
             stream = np.ascontiguousarray(ids[r, :, l].reshape(-1), np.uint32)
             flags = np.zeros(stream.size, np.uint8)
             assert O.lib.ora_deque_lru_run(HOT, stream, stream.size, flags) == 0
+            miss[r, :, l] = flags.reshape(S, -1)
             want += int(flags.sum())
+    # C: the coalesced submits of every request-step (default policy, target 4)
+    runs, _ = O.ref_cmode_runs(R, L, S, SP * 4, HOT, 4 * 2 * 4 * 128 * 2,
+                               ids.reshape(-1).astype(np.uint64), miss.reshape(-1), target=4.0)
     rows = _rows(out)
+    assert rows["B"][0] == want and rows["C"][0] == runs
     for mode in "BC":
-        assert rows[mode][0] == want and rows[mode][4] == 0
+        assert rows[mode][4] == 0 and rows[mode][5] == want
