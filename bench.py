@@ -108,6 +108,9 @@ def parse():
                     help="mean inter-arrival gap in ticks (0: 0.9 of the lanes' service rate)")
     ap.add_argument("--mmpp-period", type=float, default=1.0,
                     help="mean sojourn of each MMPP state, in ticks (rates 1x and 10x)")
+    ap.add_argument("--zipf-list", default="0.6,1.0,1.4",
+                    help="skew workload: the Zipf exponents swept")
+    ap.add_argument("--steal-list", default="0,1", help="skew workload: stealing off/on swept")
     ap.add_argument("--queue", action="store_true",
                     help="the device MPMC ring's push+pop throughput (bench_queue's test) against "
                          "the ticket rate of one shared word")
@@ -826,8 +829,8 @@ def main():
         # stealing on vs off over the Zipf skew sweep, 304 persistent workgroups,
         # request-affinity assignment of misses to workgroups
         rows = []
-        for s in (0.6, 1.0, 1.4):
-            for steal in (0, 1):
+        for s in map(float, a.zipf_list.split(",")):
+            for steal in map(int, a.steal_list.split(",")):
                 r = run(a, w, F, torch, steal=steal, workers=304, zipf=s, want_cpu=False,
                         extras=False)
                 rows.append({"zipf": s, "steal": steal, "fetch_ms": r["kernel_ms"]["fetch"],

@@ -87,12 +87,14 @@ template <int NV>
 __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
   // the fetch shares CUs with the attention it overlaps: its few wavefronts
   // issue first so the host link never waits on them
-  __builtin_amdgcn_s_setprio(3);
+  if (a.prio) __builtin_amdgcn_s_setprio(3);
   const int lane = threadIdx.x & 63;
   const int W = gridDim.x;
   const int me = blockIdx.x;
   uint64_t* state = a.ring.state;
   uint64_t steals = 0, stolen = 0, copied = 0;
+  uint32_t fair = 0;  // a thief's fair share from its last full pass (0: none yet)
+  int backoff = 0;    // lost compare-and-swaps in a row
   // Every iteration either copies at least one miss or observes a CAS lost to
   // a peer that made progress; the guard only bounds a broken protocol.
   for (long guard = 0;; ++guard) {
@@ -126,54 +128,70 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
       ++copied;
       continue;
     }
-    if (!a.steal) break;
-    // Fair share = ceil(remaining / deques), from one pass over every deque.
-    // The victim is the fullest deque of the first 64-deque window, visited
-    // from this wavefront's own starting point, that holds more than its fair
-    // share: thieves spread over the victims instead of racing for one.  No
-    // deque above its share (a balanced drain's end): the wavefront leaves the
-    // rest to the deques' own wavefronts.
+    // Thieves.  Only the first thief_waves wavefronts of a workgroup steal;
+    // the others leave once their own deque is empty.  A thief keeps the
+    // fair share ceil(remaining / deques) of its last full pass over the
+    // deques and looks for a victim 64 deques at a time (one per lane), from a
+    // window that differs per thief, taking the fullest deque of the
+    // first window holding at least twice its share: thieves spread over the
+    // victims instead of racing for one.  When no window has a victim it
+    // makes a fresh pass and searches again, and leaves if there is still
+    // none (a balanced drain's end: the rest stays with the deques' own
+    // wavefronts).  A lost compare-and-swap backs off, longer each time in a
+    // row.  Every deque state word is read coherently across the chip's
+    // L2s, so each pass is fabric traffic shared with the overlapped
+    // attention's loads: passes are made only when a search fails.
+    if (!a.steal || (int)(threadIdx.x >> 6) >= a.thief_waves) break;
     const int nwin = (W + kWave - 1) / kWave;
-    const int wave_id = me * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
+    const int first_win = me * a.thief_waves + (int)(threadIdx.x >> 6);
     auto rem_of = [&](int w) -> uint32_t {
       if (w >= W) return 0u;
       const uint64_t st = aload64(state + (size_t)w * kStateStride);
       const uint32_t h = (uint32_t)st, t = min((uint32_t)(st >> 32), a.ring.cap[w]);
       return t > h ? t - h : 0u;
     };
-    uint64_t total = 0;
-    for (int i = 0; i < nwin; ++i) total += rem_of(i * kWave + lane);
+    auto search = [&](uint32_t floor_rem, uint32_t& best, int& bw) {
+      best = 0;
+      bw = W;
+      for (int i = 0; i < nwin && best == 0; ++i) {
+        const int w = ((first_win + i) % nwin) * kWave + lane;
+        const uint32_t rem = rem_of(w);
+        best = rem > floor_rem ? rem : 0u;
+        bw = best ? w : W;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
-    total = first_lane_u64(total);
-    if (total == 0) break;  // every deque is drained
-    const uint32_t fair = (uint32_t)((total + (uint64_t)W - 1) / (uint64_t)W);
+        for (int off = 32; off > 0; off >>= 1) {
+          const uint32_t ob = __shfl_xor(best, off);
+          const int ow = __shfl_xor(bw, off);
+          if (ob > best || (ob == best && ow < bw)) {
+            best = ob;
+            bw = ow;
+          }
+        }
+        best = first_lane_u(best);
+        bw = first_lane_i(bw);
+      }
+    };
     // A victim must hold at least twice its share, and two entries per
     // wavefront of a workgroup above it.  The link, not the wavefronts, bounds
     // a drain: a deque a few entries or percent above the others finishes with
     // them, and robbing it only adds atomics and a late copy; a deque holding
     // several shares (skewed, request-affine misses) would end the drain late.
-    const uint32_t floor_rem = max(2u * fair, fair + 2u * (blockDim.x >> 6));
+    auto floor_of = [&](uint32_t f) { return max(2u * f, f + 2u * (blockDim.x >> 6)); };
     uint32_t best = 0;
     int bw = W;
-    for (int i = 0; i < nwin && best == 0; ++i) {
-      const int w = ((wave_id + i) % nwin) * kWave + lane;
-      const uint32_t rem = rem_of(w);
-      best = rem > floor_rem ? rem : 0u;
-      bw = best ? w : W;
+    if (fair) search(floor_of(fair), best, bw);
+    if (best == 0) {  // fresh pass over every deque
+      uint64_t total = 0;
+      for (int i = 0; i < nwin; ++i) total += rem_of(i * kWave + lane);
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t ob = __shfl_xor(best, off);
-        const int ow = __shfl_xor(bw, off);
-        if (ob > best || (ob == best && ow < bw)) {
-          best = ob;
-          bw = ow;
-        }
-      }
-      best = first_lane_u(best);
-      bw = first_lane_i(bw);
+      for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
+      total = first_lane_u64(total);
+      if (total == 0) break;  // every deque is drained
+      fair = (uint32_t)((total + (uint64_t)W - 1) / (uint64_t)W);
+      search(floor_of(fair), best, bw);
+      if (best == 0) break;  // no deque far enough above its fair share
     }
-    if (best == 0) break;  // no deque far enough above its fair share
+    const uint32_t floor_rem = floor_of(fair);
     int ok = 0;
     uint32_t s0 = 0, s1 = 0;
     if (lane == 0) {
@@ -193,15 +211,19 @@ __global__ __launch_bounds__(256) void k_fetch(FetchArgs a) {
     }
     ok = first_lane_i(ok);
     if (!ok) {  // a peer took it first: back off before looking again
-      __builtin_amdgcn_s_sleep(2);
+      backoff = min(backoff + 1, 6);
+      for (int i = 0; i < (1 << backoff); ++i) __builtin_amdgcn_s_sleep(2);
       continue;
     }
+    backoff = 0;
     s0 = first_lane_u(s0);
     s1 = first_lane_u(s1);
     const ferry_miss* seg = a.ring.entries + a.ring.seg[bw];
-    constexpr int KS = NV <= 8 ? 4 : 2;  // stolen blocks in flight (registers: KS * NV * 4)
     uint32_t i = s0;
-    for (; i + KS <= s1; i += KS) copy_blocks<NV, KS>(a, seg + i, lane);
+    if (a.steal_inflight >= 4 && NV <= 8)
+      for (; i + 4 <= s1; i += 4) copy_blocks<NV, 4>(a, seg + i, lane);
+    if (a.steal_inflight >= 2)
+      for (; i + 2 <= s1; i += 2) copy_blocks<NV, 2>(a, seg + i, lane);
     for (; i < s1; ++i) copy_block<NV>(a, load_entry(seg + i), lane);
     ++steals;
     stolen += s1 - s0;

@@ -47,6 +47,9 @@ struct FetchArgs {
   float* pool_scales;
   int steal;
   uint32_t steal_chunk;
+  int prio;              // raise the fetch wavefronts' issue priority
+  int thief_waves;       // wavefronts per workgroup that steal once their deque is empty
+  int steal_inflight;    // stolen blocks a thief keeps in flight (1, 2 or 4)
   unsigned long long* stats;
   unsigned long long* step_acc;  // blocks fetched since the last k_step_close
   uint32_t* done;

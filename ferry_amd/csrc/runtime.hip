@@ -92,6 +92,11 @@ struct ferry_ctx {
   std::vector<hipEvent_t> booked;   // ... and bookkeeping done
   hipStream_t book = nullptr;       // ... whose bookkeeping runs on this stream
   int attn_waves = 0;              // wavefronts per attention workgroup (FERRY_ATTN_WAVES), 0 = default
+  int fetch_waves = 0;             // wavefronts per fetch workgroup (FERRY_FETCH_WAVES: 1, 2, 4; 0 = by rule)
+  int fetch_prio = 1;              // fetch wavefronts issue first (FERRY_FETCH_PRIO=0: not)
+  uint32_t steal_chunk = 8;        // most entries one steal takes (FERRY_STEAL_CHUNK)
+  int thief_waves = 1;             // wavefronts per fetch workgroup that steal (FERRY_THIEF_WAVES)
+  int steal_inflight = 2;          // stolen blocks in flight per thief (FERRY_STEAL_INFLIGHT)
   int attn_loads = 0;              // K/V loads (FERRY_ATTN_LOADS): 0 = by plan, 1 = nt, 2 = temporal
   uint32_t* probe_sink = nullptr;  // bandwidth probes: one word per row / wavefront
   size_t probe_sink_words = 0;
@@ -361,6 +366,14 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   ferry_ctx* c = new ferry_ctx();
   c->cfg = *cfg;
   if (const char* e = std::getenv("FERRY_ATTN_WAVES")) c->attn_waves = std::atoi(e);
+  if (const char* e = std::getenv("FERRY_FETCH_WAVES")) {
+    const int v = std::atoi(e);
+    c->fetch_waves = v == 1 || v == 2 ? v : 4;
+  }
+  if (const char* e = std::getenv("FERRY_FETCH_PRIO")) c->fetch_prio = std::atoi(e) != 0;
+  if (const char* e = std::getenv("FERRY_STEAL_CHUNK")) c->steal_chunk = (uint32_t)std::max(1, std::atoi(e));
+  if (const char* e = std::getenv("FERRY_THIEF_WAVES")) c->thief_waves = std::max(1, std::atoi(e));
+  if (const char* e = std::getenv("FERRY_STEAL_INFLIGHT")) c->steal_inflight = std::max(1, std::atoi(e));
   if (const char* e = std::getenv("FERRY_ATTN_LOADS"))
     c->attn_loads = std::string(e) == "nt" ? 1 : (std::string(e) == "temporal" ? 2 : 0);
   c->device = device;
@@ -392,6 +405,19 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   // with 2 per CU), and the CUs they leave idle run the attention that
   // overlaps the fetch (the 7B step: 64.2 ms, against 67-68 ms).
   g.workers = cfg->fetch_workers > 0 ? cfg->fetch_workers : std::max(1, cus / 4);
+  // Wavefronts per fetch workgroup.  About 256 copying wavefronts with one
+  // block in flight each fill the link; more only hold host reads in the
+  // memory system's queues, ahead of the loads of the kernels the fetch
+  // overlaps (measured with 304 workgroups of 4: the attention and the
+  // bookkeeping running beside a stealing drain took 4-8 times their time
+  // alone).  With stealing every wavefront can reach any deque, so the count
+  // follows the link: 256 / workgroups, 1 to 4.  Without stealing a deque's
+  // own wavefronts are all that copy it: 4.
+  if (c->fetch_waves == 0) {
+    c->fetch_waves = 4;
+    if (cfg->steal)
+      while (c->fetch_waves > 1 && g.workers * c->fetch_waves > 256) c->fetch_waves >>= 1;
+  }
   if ((uint64_t)g.n_sets * (uint64_t)g.C >= 0xFFFFFFFFull ||
       (uint64_t)g.n_sets * (uint64_t)g.max_sel >= 0xFFFFFFFFull) {
     delete c;
@@ -676,12 +702,15 @@ int drain_ring(ferry_ctx* ctx, void* stream, int which) {
   a.pool = ctx->pool;
   a.pool_scales = ctx->pool_scales;
   a.steal = ctx->cfg.steal;
-  a.steal_chunk = 8;
+  a.steal_chunk = ctx->steal_chunk;
+  a.prio = ctx->fetch_prio;
+  a.thief_waves = ctx->thief_waves;
+  a.steal_inflight = ctx->steal_inflight;
   a.stats = ctx->stats;
   a.step_acc = ctx->step_acc;
   a.done = ctx->done;
   a.err = ctx->err;
-  const dim3 grid(ctx->g.workers), block(256);
+  const dim3 grid(ctx->g.workers), block(64 * ctx->fetch_waves);
   switch (ctx->g.bb / 1024) {
     case 4: hipLaunchKernelGGL(k_fetch<4>, grid, block, 0, (hipStream_t)stream, a); break;
     case 8: hipLaunchKernelGGL(k_fetch<8>, grid, block, 0, (hipStream_t)stream, a); break;
