@@ -136,6 +136,7 @@ _PROTOS = {
     "ferry_ktiles_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(C.c_uint64)]),
     "ferry_select_mass": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "ferry_select_mass_layers": (C.c_int, [_vp, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "ferry_select_mass_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "ferry_sched_destroy": (C.c_int, [_vp]),
     "ferry_sched_tick": (C.c_int, [_vp, C.c_double, _vp, _vp, _vp, C.POINTER(_i32), _vp,
                                    C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32)]),
@@ -411,6 +412,14 @@ class Executor:
             _check(lib.ferry_select_mass_layers(self._h, l0, nl, self._q(q), self._ctx(ctx_blocks),
                                                 self._sel(sel), _stream(stream)),
                    "ferry_select_mass_layers")
+
+    def select_mass_noalloc(self, q, ctx_blocks, sel, stream=None):
+        """select_mass over every layer with the library's static per-GPU
+        workspace instead of the context's: allocates nothing.  Calls that
+        overlap on one GPU race for that workspace."""
+        _check(lib.ferry_select_mass_noalloc(self._h, self._q(q), self._ctx(ctx_blocks),
+                                             self._sel(sel), _stream(stream)),
+               "ferry_select_mass_noalloc")
 
     def sets_reset(self, stream=None):
         _check(lib.ferry_sets_reset(self._h, _stream(stream)), "ferry_sets_reset")

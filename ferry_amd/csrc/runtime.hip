@@ -13,6 +13,8 @@
 #include <cstring>
 #include <string>
 #include <initializer_list>
+#include <map>
+#include <mutex>
 #include <utility>
 #include <vector>
 
@@ -57,6 +59,35 @@ int esize_of(int dtype) { return dtype == FERRY_F32 ? 4 : (dtype == FERRY_FP8_E4
 
 float value_mult(double std_) { return (float)(std_ / (65536.0 / std::sqrt(3.0))); }
 
+}  // namespace
+
+// Workspace of ferry_select_mass_noalloc: one array per GPU, part of the
+// library's code object, so that entry point allocates nothing.  Each GPU the
+// library runs on holds it until the process ends.  Host code never passes
+// the array's name to a kernel (on the host it is a stand-in, not a device
+// address): ferry_ctx_create resolves each device's own address once, with
+// that device current, and the entry point uses that address.
+static constexpr size_t kNoAllocScratchBytes = 64ull << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, float*> g_scratch_ptr;  // device -> address of its `scratch`
+
+// The calling thread's current device must be `device`.
+int resolve_scratch(int device, float** out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch_ptr.find(device);
+  if (it == g_scratch_ptr.end()) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(FERRY_EHIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    it = g_scratch_ptr.emplace(device, static_cast<float*>(p)).first;
+  }
+  *out = it->second;
+  return FERRY_OK;
+}
 }  // namespace
 
 struct ferry_ctx {
@@ -110,6 +141,7 @@ struct ferry_ctx {
   uint64_t kt_records = 0;         // records, addressed like the summaries
   float* mass_ws = nullptr;        // per-workgroup (max, sum) of every block and query head
   int kt_perm = 0;                 // K table words lane-transposed for the matrix-core loads
+  float* scratch_dev = nullptr;    // this device's address of the static `scratch` array
 
   Ring ring(int which = 0) const {
     Ring r;
@@ -377,6 +409,10 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   if (const char* e = std::getenv("FERRY_ATTN_LOADS"))
     c->attn_loads = std::string(e) == "nt" ? 1 : (std::string(e) == "temporal" ? 2 : 0);
   c->device = device;
+  if ((rc = resolve_scratch(device, &c->scratch_dev))) {
+    delete c;
+    return rc;
+  }
   Geo& g = c->g;
   g.n_req = cfg->n_req;
   g.group = cfg->group;
@@ -1077,21 +1113,20 @@ int ferry_ktiles_view(ferry_ctx* ctx, void** ktiles, float** scales, uint64_t* n
   return FERRY_OK;
 }
 
-int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
-                             const int32_t* ctx_blocks, uint32_t* sel, void* stream) {
-  if (int rc = check_ctx(ctx)) return rc;
-  if (int rc = check_bufs({{q, "q"}, {ctx_blocks, "ctx_blocks"}, {sel, "sel"}})) return rc;
+}  // extern "C"
+
+namespace {
+
+// The mass selection of layers [l0, l0 + nl) with workspace `ws`, which holds
+// max_wgs slices of max_blocks * G (max, sum) pairs.
+int launch_select_mass(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
+                       const int32_t* ctx_blocks, uint32_t* sel, void* stream, float* ws,
+                       uint64_t max_wgs) {
   const Geo& g = ctx->g;
-  if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
-  if (g.group != 1)
-    return fail(FERRY_EINVAL, "top-k selection needs private sets (group 1): a group's members select "
-                              "from their own contexts");
-  if (!ctx->ktab || !ctx->kt_records) return fail(FERRY_EINVAL, "K table not built (ferry_ktiles_build)");
-  const size_t lds = (size_t)g.max_blocks * 4;
-  if (lds > kMassLds) return fail(FERRY_EINVAL, "max_blocks exceed the mass selection's 60 KiB of LDS");
-  if (!ctx->mass_ws) return fail(FERRY_EINVAL, "no mass-selection workspace (ferry_ktiles_build failed)");
   HIPC(hipSetDevice(ctx->device));
-  const dim3 grid((unsigned)std::min<size_t>((size_t)g.n_req * nl, kMassWgs));
+  const dim3 grid((unsigned)std::min<uint64_t>(std::min<uint64_t>((uint64_t)g.n_req * nl, kMassWgs),
+                                               max_wgs));
+  const size_t lds = (size_t)g.max_blocks * 4;
   hipStream_t s = (hipStream_t)stream;
   const int G = g.Hq / g.Hkv;
   // vector ALUs (4 wavefronts) for fp32 K, matrix cores (8 wavefronts) for
@@ -1099,7 +1134,7 @@ int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float
   // there are few (request, layer) items
 #define FERRY_MASS_LAUNCH(KERN, DT, GG, WW)                                                      \
   hipLaunchKernelGGL((KERN<DT, GG, WW>), grid, dim3(64 * WW), lds, s, g, q, ctx_blocks,         \
-                     ctx->ktab, ctx->ktab_scales, ctx->kt_records, ctx->mass_ws, sel, l0, nl,   \
+                     ctx->ktab, ctx->ktab_scales, ctx->kt_records, ws, sel, l0, nl,             \
                      g.max_blocks, ctx->err)
 #define FERRY_MASS_G(KERN, DT, WW)                       \
   switch (G) {                                           \
@@ -1120,10 +1155,53 @@ int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float
   return FERRY_OK;
 }
 
+// Arguments every mass selection needs, checked before anything launches.
+int check_select_mass(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
+                      const int32_t* ctx_blocks, uint32_t* sel) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_bufs({{q, "q"}, {ctx_blocks, "ctx_blocks"}, {sel, "sel"}})) return rc;
+  const Geo& g = ctx->g;
+  if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
+  if (g.group != 1)
+    return fail(FERRY_EINVAL, "top-k selection needs private sets (group 1): a group's members select "
+                              "from their own contexts");
+  if (!ctx->ktab || !ctx->kt_records) return fail(FERRY_EINVAL, "K table not built (ferry_ktiles_build)");
+  if ((size_t)g.max_blocks * 4 > kMassLds)
+    return fail(FERRY_EINVAL, "max_blocks exceed the mass selection's 60 KiB of LDS");
+  return FERRY_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
+                             const int32_t* ctx_blocks, uint32_t* sel, void* stream) {
+  if (int rc = check_select_mass(ctx, l0, nl, q, ctx_blocks, sel)) return rc;
+  if (!ctx->mass_ws) return fail(FERRY_EINVAL, "no mass-selection workspace (ferry_ktiles_build failed)");
+  return launch_select_mass(ctx, l0, nl, q, ctx_blocks, sel, stream, ctx->mass_ws, kMassWgs);
+}
+
 int ferry_select_mass(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks, uint32_t* sel,
                       void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
   return ferry_select_mass_layers(ctx, 0, ctx->g.L, q, ctx_blocks, sel, stream);
+}
+
+int ferry_select_mass_noalloc(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks,
+                              uint32_t* sel, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_select_mass(ctx, 0, ctx->g.L, q, ctx_blocks, sel)) return rc;
+  const Geo& g = ctx->g;
+  // one workgroup's slice: a (max, sum) pair per context block and query head
+  const uint64_t slice = (uint64_t)g.max_blocks * (uint64_t)(g.Hq / g.Hkv) * 2 * sizeof(float);
+  if (slice > kNoAllocScratchBytes)
+    return fail(FERRY_EINVAL, "ferry_select_mass_noalloc: one workgroup's workspace (" +
+                                  std::to_string(slice) + " B) exceeds the static scratch of " +
+                                  std::to_string(kNoAllocScratchBytes) + " B");
+  if (!ctx->scratch_dev) return fail(FERRY_EHIP, "static scratch not resolved for this device");
+  return launch_select_mass(ctx, 0, g.L, q, ctx_blocks, sel, stream, ctx->scratch_dev,
+                            kNoAllocScratchBytes / slice);
 }
 
 int ferry_owner_image_bytes(const ferry_ctx* ctx, uint64_t* bytes) {

@@ -320,6 +320,22 @@ int ferry_select_mass(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks,
                       void* stream);
 int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
                              const int32_t* ctx_blocks, uint32_t* sel, void* stream);
+/* ferry_select_mass over every layer, allocating nothing: the per-workgroup
+ * softmax (max, sum) workspace lives in a static 64 MiB array of the library
+ * (one per GPU, held until the process ends) instead of the context's.  No
+ * counterpart in the reference; it is for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  It calls no hipMalloc/hipFree.  Needs the K table
+ * (ferry_ktiles_build, which the caller runs beforehand) and one workgroup's
+ * workspace, max_blocks * (q_heads / kv_heads) * 8 bytes, within the 64 MiB
+ * (FERRY_EINVAL otherwise; max_blocks <= 15360 always fits); fewer
+ * workgroups share the (request, layer) items when the array holds fewer
+ * slices than ferry_select_mass would launch.  Output equals
+ * ferry_select_mass's bit for bit.  Every call on one GPU uses the same array:
+ * calls that overlap on one GPU (other streams, other contexts, other host
+ * threads) race and must be serialised by the caller. */
+int ferry_select_mass_noalloc(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks,
+                              uint32_t* sel, void* stream);
 
 /* ---- owner hand-off (the per-GPU halves of moving a request) ----
  * ferry_owner_export writes an image of one owner's sets: per (layer, kv
