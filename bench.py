@@ -148,30 +148,67 @@ def pmc_summary(csv_path, last):
 
 
 def rocprof_summary(db_path, last):
-    """Per-kernel dispatch statistics from a rocprofv3 database (markdown)."""
+    """Per-kernel dispatch statistics from a rocprofv3 kernel trace (markdown).
+
+    Two tables: every dispatch of each kernel, and the whole-step dispatches
+    only -- those issued after the last k_step_close, i.e. bench.py's
+    event-timed steps (bookkeeping, fetch drain and attention of the whole
+    batch launched one after the other) and its back-to-back attention
+    launches, which are what the bench line's kernel_ms and rooflines are
+    computed from.  The pipelined steps before them launch the same kernels
+    per layer range."""
     import sqlite3
 
     if db_path.endswith(".csv"):  # rocprofv3 --output-format csv kernel_trace.csv
         import csv
 
         with open(db_path) as f:
-            rows = sorted(((r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+            rows = sorted(((r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
+                            int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])))
                            for r in csv.DictReader(f)), key=lambda x: x[1])
     else:
         cur = sqlite3.connect(db_path).cursor()
-        rows = cur.execute("select name, start, end from kernels order by start").fetchall()
-    per = {}
-    for name, t0, t1 in rows:
-        per.setdefault(name.split("(")[0].replace("void ", ""), []).append((t1 - t0) / 1e3)
-    lines = ["| kernel | calls | avg us (all) | min us | max us |"
-             + (f" avg us (last {last}) |" if last else ""),
-             "|---|---|---|---|---|" + ("---|" if last else "")]
-    for name, d in sorted(per.items(), key=lambda kv: -sum(kv[1])):
-        row = f"| `{name}` | {len(d)} | {np.mean(d):.1f} | {min(d):.1f} | {max(d):.1f} |"
-        if last:
-            row += f" {np.mean(d[-last:]):.1f} |"
-        lines.append(row)
-    return "\n".join(lines)
+        rows = [(n, a, b, 0) for n, a, b in
+                cur.execute("select name, start, end from kernels order by start").fetchall()]
+
+    def short(name):
+        return name.split("(")[0].replace("void ", "")
+
+    def table(sel, title, with_last):
+        per = {}
+        for name, t0, t1, wg in sel:
+            per.setdefault((short(name), wg), []).append((t1 - t0) / 1e3)
+        lines = [title, "",
+                 "| kernel | workgroups | calls | avg us | min us | max us |"
+                 + (f" avg us (last {last}) |" if with_last else ""),
+                 "|---|---|---|---|---|---|" + ("---|" if with_last else "")]
+        for (name, wg), d in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+            row = (f"| `{name}` | {wg} | {len(d)} | {np.mean(d):.1f} | {min(d):.1f} | "
+                   f"{max(d):.1f} |")
+            if with_last:
+                row += f" {np.mean(d[-last:]):.1f} |"
+            lines.append(row)
+        return lines
+
+    out = table(rows, "### Every dispatch", bool(last))
+    closes = [i for i, r in enumerate(rows) if short(r[0]).endswith("k_step_close")]
+    if closes:
+        tail = [r for r in rows[closes[-1] + 1:]
+                if any(k in short(r[0]) for k in ("k_lru_step", "k_fetch", "k_attn"))]
+        # an attention launch right after a fetch drain belongs to an event-timed
+        # step; the ones after another attention launch are the back-to-back runs
+        timed, b2b = [], []
+        for i, r in enumerate(tail):
+            if "k_attn" in short(r[0]) and i and "k_attn" in short(tail[i - 1][0]):
+                b2b.append(r)
+            else:
+                timed.append(r)
+        out += ["", *table(timed, "### Whole-step dispatches of the event-timed steps (after the "
+                                  "last pipelined step; the bench line's kernel_ms)", False)]
+        if b2b:
+            out += ["", *table(b2b, "### Back-to-back attention launches (kernel_ms."
+                                    "attention_back_to_back)", False)]
+    return "\n".join(out)
 
 
 def contexts(F, w):
@@ -503,6 +540,7 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
                             f"{PREROLL_TOL:.0%} (at least {PREROLL_MIN}), then --warmup"},
         "miss_blocks_per_s": round(timed_misses / elapsed, 1),
         "miss_blocks_per_s_fetch_kernel": round(ev_misses / n_timed / (t_fetch * 1e-3), 1),
+        "fetched_blocks_per_event_step": round(ev_misses / n_timed, 1),
         "attention_tok_per_s": round(B / (t_attn * 1e-3), 1),
         "kernel_ms": {"bookkeep": round(t_book, 4), "fetch": round(t_fetch, 4),
                       "attention": round(t_attn, 4), "attention_back_to_back": round(t_attn_rep, 4)},
@@ -862,30 +900,33 @@ def main():
                                               ("kernel", "achieved", "peak", "unit", "frac",
                                                "plain_read_gbs", "frac_of_plain_read")}
             print(json.dumps({name: others[name]}), file=sys.stderr, flush=True)
-    traffic = None
+    # HBM traffic per launch is not measured in this run: it comes from two
+    # rocprofv3 counter runs of the same workload (FETCH_SIZE, WRITE_SIZE),
+    # stored in profiles/traffic.json with the commit they were measured at
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get(a.workload, {}).get("bytes_per_launch")
-    r["roofline"]["traffic"] = traffic
-    if r.get("roofline_select") and os.path.exists(tpath):
-        with open(tpath) as f:
-            r["roofline_select"]["traffic"] = json.load(f).get(a.workload + "_select", {}).get(
-                "bytes_per_launch")
-    if (r.get("roofline_select_mass") or {}).get("ms") and os.path.exists(tpath):
-        with open(tpath) as f:
-            r["roofline_select_mass"]["traffic"] = json.load(f).get(a.workload + "_mass", {}).get(
-                "bytes_per_launch")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            fo = json.load(f).get(a.workload + "_fetch")
-        r["roofline_fetch"]["traffic"] = (
-            {"read": fo["read_bytes"], "write": fo["write_bytes"]} if fo else None)
-    if r.get("roofline_handoff") and os.path.exists(tpath):
-        with open(tpath) as f:
-            ho = json.load(f).get(a.workload + "_handoff")
-        r["roofline_handoff"]["traffic"] = (
-            {"export": ho["export_bytes"], "import": ho["import_bytes"]} if ho else None)
+    tj = json.load(open(tpath)) if os.path.exists(tpath) else {}
+    src = tj.get("measured_at", {})
+    label = (f"stored counters: profiles/traffic.json, measured at commit {src.get('commit')} "
+             f"({src.get('source')})" if src else None)
+
+    def stored(key, fields):
+        e = tj.get(a.workload + key)
+        return ({f: e[f] for f in fields} if e else None)
+
+    def put(obj, value):
+        if obj is not None and not obj.get("skipped"):
+            obj["traffic"] = value
+            obj["traffic_source"] = label if value is not None else None
+
+    put(r["roofline"], (tj.get(a.workload) or {}).get("bytes_per_launch"))
+    put(r["roofline_fetch"], stored("_fetch", ("read_bytes", "write_bytes")))
+    put(r.get("roofline_select"), (tj.get(a.workload + "_select") or {}).get("bytes_per_launch"))
+    put(r.get("roofline_select_mass"), (tj.get(a.workload + "_mass") or {}).get("bytes_per_launch"))
+    put(r.get("roofline_handoff"), stored("_handoff", ("export_bytes", "import_bytes")))
+    for name, o in others.items():
+        put(o["roofline"], (tj.get(name) or {}).get("bytes_per_launch"))
+        e = tj.get(name + "_fetch")
+        put(o["roofline_fetch"], {f: e[f] for f in ("read_bytes", "write_bytes")} if e else None)
     lo, hi = w["ctx"]
     desc = (f"B={w['B']}, L={w['L']}, Hq={w['Hq']}, Hkv={w['Hkv']}, D=128, {w['dtype']} KV, "
             f"16-token blocks, ctx {'U[%d,%d]' % (lo * 16, hi * 16) if lo != hi else lo * 16} "

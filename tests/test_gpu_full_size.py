@@ -7,10 +7,17 @@ decode step exactly as the benchmark runs them:
   * shared-prefix groups: 8 groups of 16 requests x 32 layers x 8 kv heads of 4
     query heads, a 512-block shared prefix + 32-256 private blocks, top-k 64,
     1536 slots per group set, fp8 E4M3 with per-block K and V scales;
-all with Zipf 1.1 popularity, reuse 0.66 and a 1 M-block host tier.  A replay
-of millions of selections per step through the oracle does not fit a test, so
-the checks are the size-independent properties every step must keep, plus
-spot checks of fetched bytes and attention against the host tier:
+all with Zipf 1.1 popularity, reuse 0.66 and a 1 M-block host tier.  Sets
+belong to one owner and draws are keyed per request, so the first owners (two
+requests, or one prefix group of 16) evolve exactly as a batch of only them
+would: the oracle replays those owners from the same cold start, and every
+step their slots and per-set miss lists (block, slot, evicted block) must be
+bit-equal; after the last step their LRU state too, the blocks fetched in it
+and every resident slot of the first and last layer memcmp-equal to the host
+tier, and their attention in three layers within 2e-3 (fp8: 1e-2) of the
+float64 oracle (oracle/gate.py).  For the whole batch, whose replay does not
+fit a test, the checks are the size-independent properties every step must
+keep, plus spot checks of fetched bytes and attention against the host tier:
   * every selection's slot lies in its owner's set and holds its block;
   * each set's LRU order is a permutation of its resident slots;
   * the per-step miss counts add up to the executor's counters, and the
@@ -25,6 +32,7 @@ import torch
 
 import ferry_amd as F
 from oracle import pyoracle as O
+from oracle.gate import OwnerReplay
 
 pytestmark = pytest.mark.gpu
 
@@ -83,6 +91,8 @@ def test_benchmark_shapes_at_full_size(name):
             np.arange(Hkv)[None, None, :])
     total_misses = 0
     tol = 1e-2 if dtype == F.FP8 else 2e-3
+    replay = OwnerReplay(n_req=B, group=c["group"], n_layers=L, kv_heads=Hkv, q_heads=Hq, k=k,
+                         slots_per_set=C, max_blocks=mb, dtype=dtype, host_blocks=HB)
     for t in range(6):
         sel = sg.step(t)
         q = torch.randn((B, L, Hq, 128), device="cuda")
@@ -92,6 +102,7 @@ def test_benchmark_shapes_at_full_size(name):
         torch.cuda.synchronize()
         st = ex.stats()
         assert st["device_error"] == 0, st
+        replay.step(sel, bufs)  # the first owners, bit-exact against the oracle
         mc = _u32(bufs["miss_count"])
         total_misses += int(mc.sum())
         assert st["misses"] == total_misses
@@ -133,3 +144,6 @@ def test_benchmark_shapes_at_full_size(name):
                 assert err < tol, (name, t, r, l, h, gq, err)
     # after a few steps a minority of the step's selections miss
     assert 0.005 < int(mc.sum()) / (B * L * Hkv * k) < 0.6
+    res = replay.final(ex, q, out)
+    print(f"[full size] {name} owner replay: {res}", flush=True)
+    assert res["steps"] == 6 and res["misses_compared"] > 0
