@@ -29,7 +29,8 @@ __all__ = [
     "ctx_uniform", "arrivals", "lib", "LIB_PATH", "F32", "F16", "BF16", "FP8", "LRU_STEP",
     "LRU_SERIAL", "ASSIGN_SPREAD", "ASSIGN_AFFINITY", "ATTN_AUTO", "ATTN_VALU", "ATTN_MFMA",
     "MISS_DTYPE", "EMPTY", "ARRIVAL_STEADY", "ARRIVAL_BURSTY", "ARRIVAL_POISSON", "ARRIVAL_MMPP",
-    "SCHED_FIFO", "SCHED_PINNED", "trace_load", "TOPK_PER_HEAD", "TOPK_LAYER_MAX",
+    "SCHED_FIFO", "SCHED_PINNED", "trace_load", "TOPK_PER_HEAD", "TOPK_LAYER_MAX", "CAP_GROUP",
+    "CAP_PER_MEMBER",
 ]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libferry_amd.so")
@@ -42,6 +43,7 @@ F32, F16, BF16, FP8 = 0, 1, 2, 3
 LRU_STEP, LRU_SERIAL = 0, 1
 ASSIGN_SPREAD, ASSIGN_AFFINITY = 0, 1
 ATTN_AUTO, ATTN_VALU, ATTN_MFMA = 0, 1, 2
+CAP_GROUP, CAP_PER_MEMBER = 0, 1
 PROBE_HBM_GATHER, PROBE_HOST_READ, PROBE_HOST_DMA, PROBE_HBM_COPY = 0, 1, 2, 3
 ARRIVAL_STEADY, ARRIVAL_BURSTY, ARRIVAL_POISSON, ARRIVAL_MMPP = 0, 1, 2, 3
 EMPTY = 0xFFFFFFFF  # selection id of an empty position (and its slot)
@@ -69,7 +71,7 @@ class Config(C.Structure):
         ("max_blocks", C.c_int32), ("dtype", C.c_int32), ("lru_mode", C.c_int32),
         ("host_blocks", C.c_uint64), ("host_seed", C.c_uint64), ("value_std", C.c_float),
         ("fetch_workers", C.c_int32), ("steal", C.c_int32), ("assign", C.c_int32),
-        ("attn", C.c_int32),
+        ("attn", C.c_int32), ("cap_mode", C.c_int32),
     ]
 
 
@@ -117,6 +119,9 @@ _PROTOS = {
     "ferry_sets_reset": (C.c_int, [_vp, _vp]),
     "ferry_sets_state": (C.c_int, [_vp, _vp, _vp, _vp]),
     "ferry_sets_reset_owners": (C.c_int, [_vp, _vp, C.c_uint32, _vp]),
+    "ferry_members_leave": (C.c_int, [_vp, _vp, C.c_uint32, _vp]),
+    "ferry_members_join": (C.c_int, [_vp, _vp, C.c_uint32, _vp]),
+    "ferry_members_get": (C.c_int, [_vp, _vp]),
     "ferry_selgen_admit": (C.c_int, [_vp, _i32, _i32, _i32, _i32]),
     "ferry_selgen_retire": (C.c_int, [_vp, _i32]),
     "ferry_arrivals": (C.c_int, [C.c_int, C.c_uint32, C.c_double, C.c_double, C.c_double,
@@ -163,6 +168,8 @@ _PROTOS = {
     "ferry_selgen_create": (C.c_int, [C.POINTER(SelGenConfig), _vp, C.POINTER(_vp)]),
     "ferry_selgen_destroy": (C.c_int, [_vp]),
     "ferry_selgen_max_blocks": (C.c_int, [_vp, C.POINTER(_i32)]),
+    "ferry_selgen_set_private_ranges": (C.c_int, [_vp, _i32]),
+    "ferry_selgen_admit_member": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _i32]),
     "ferry_selgen_step": (C.c_int, [_vp, _i32, _vp]),
     "ferry_ctx_uniform": (C.c_int, [C.c_uint64, _i32, _i32, _i32, _vp]),
     "ferry_refgen_selections": (C.c_int, [_i32, _i32, _i32, _i32, C.c_uint64, _vp]),
@@ -223,10 +230,12 @@ class Executor:
     def __init__(self, n_req, n_layers, kv_heads, k, slots_per_set, max_blocks,
                  q_heads=None, group=1, head_dim=128, block_tokens=16, dtype=F16,
                  lru_mode=LRU_STEP, host_blocks=1 << 16, host_seed=7, value_std=0.5,
-                 fetch_workers=0, steal=1, assign=ASSIGN_SPREAD, attn=ATTN_AUTO, device=0):
+                 fetch_workers=0, steal=1, assign=ASSIGN_SPREAD, attn=ATTN_AUTO, device=0,
+                 cap_mode=CAP_GROUP):
         cfg = Config(n_req, group, n_layers, kv_heads, q_heads or kv_heads, head_dim,
                      block_tokens, k, slots_per_set, max_blocks, dtype, lru_mode,
-                     host_blocks, host_seed, value_std, fetch_workers, steal, assign, attn)
+                     host_blocks, host_seed, value_std, fetch_workers, steal, assign, attn,
+                     cap_mode)
         self.device = device
         torch.cuda.set_device(device)
         h = _vp()
@@ -431,6 +440,25 @@ class Executor:
                "ferry_sets_reset_owners")
 
     # ---- inspection (synchronous) ---------------------------------------
+    def members_leave(self, lanes, stream=None):
+        """The requests of these lanes (int32 device tensor) leave their owners;
+        under CAP_PER_MEMBER the owners' sets are trimmed to the new capacity."""
+        n = int(lanes.numel())
+        _check(lib.ferry_members_leave(self._h, _dev(lanes, "lanes", n, _I32, self.device), n,
+                                       _stream(stream)), "ferry_members_leave")
+
+    def members_join(self, lanes, stream=None):
+        """New requests of the owners' groups take these lanes (resident again)."""
+        n = int(lanes.numel())
+        _check(lib.ferry_members_join(self._h, _dev(lanes, "lanes", n, _I32, self.device), n,
+                                      _stream(stream)), "ferry_members_join")
+
+    def members(self):
+        """Resident members of every owner (synchronises)."""
+        out = np.zeros((self.sel_shape[0] + self.cfg.group - 1) // self.cfg.group, np.uint32)
+        _check(lib.ferry_members_get(self._h, out.ctypes.data), "ferry_members_get")
+        return out
+
     def stats(self):
         s = Stats()
         _check(lib.ferry_stats_get(self._h, C.byref(s)), "ferry_stats_get")
@@ -565,6 +593,21 @@ class SelGen:
     def retire(self, lane):
         """`lane` produces empty rows until its next admission."""
         _check(lib.ferry_selgen_retire(self._h, lane), "ferry_selgen_retire")
+
+    def set_private_ranges(self, ranges):
+        """`ranges` (>= group) private id ranges per prefix-group owner, for
+        members that turn over; updates max_blocks."""
+        _check(lib.ferry_selgen_set_private_ranges(self._h, ranges),
+               "ferry_selgen_set_private_ranges")
+        mb = _i32()
+        _check(lib.ferry_selgen_max_blocks(self._h, C.byref(mb)), "ferry_selgen_max_blocks")
+        self.max_blocks = mb.value
+
+    def admit_member(self, lane, request_id, ctx_blocks, step, private_range):
+        """A request of the lane's prefix group takes `lane` from `step` on,
+        its private blocks in id range `private_range`."""
+        _check(lib.ferry_selgen_admit_member(self._h, lane, request_id, ctx_blocks, step,
+                                             private_range), "ferry_selgen_admit_member")
 
     def __del__(self):
         h, self._h = getattr(self, "_h", None), None

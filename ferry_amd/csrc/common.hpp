@@ -23,6 +23,8 @@ constexpr int kMaxTopK = 1024;
 struct Geo {
   int n_req, group, L, Hkv, Hq, D, T, k, C, max_blocks;
   int n_owners, n_sets, max_sel, dtype, esize, workers;
+  int cap_mode;      // FERRY_CAP_GROUP or FERRY_CAP_PER_MEMBER
+  int member_slots;  // C / group: one resident member's share under FERRY_CAP_PER_MEMBER
   uint64_t bb;           // K+V bytes of one block
   uint64_t host_blocks;  // host tier capacity (blocks)
   uint64_t pool_slots;   // n_sets * C

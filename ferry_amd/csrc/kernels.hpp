@@ -7,11 +7,22 @@ namespace ferry_amd {
 
 // Per-set LRU state in HBM (see lru.hip for the rule it implements).
 struct SetState {
-  uint32_t* fill;  // [n_sets] slots in use; free slots are [fill, C)
-  uint32_t* ord;   // [n_sets][C] local slots, least recent first
-  uint32_t* tag;   // [n_sets][C] block held by each slot (kNone if free)
-  uint32_t* map;   // [n_sets][max_blocks] slot holding each block (kNone)
+  uint32_t* fill;     // [n_sets] slots in use; free slots are [fill, C)
+  uint32_t* ord;      // [n_sets][C] local slots, least recent first
+  uint32_t* tag;      // [n_sets][C] block held by each slot (kNone if free)
+  uint32_t* map;      // [n_sets][max_blocks] slot holding each block (kNone)
+  uint32_t* members;  // [n_owners] resident member lanes of each owner
 };
+
+// Blocks an owner's sets may hold: C, or under FERRY_CAP_PER_MEMBER one
+// member's share per resident member, at least one share (wla_group_cap,
+// src/workloads/missstream.cuh:91-94).
+__host__ __device__ inline uint32_t set_capacity(const Geo& g, uint32_t members) {
+  if (g.cap_mode != FERRY_CAP_PER_MEMBER) return (uint32_t)g.C;
+  const uint32_t m = members > 0 ? members : 1u;
+  const uint64_t c = (uint64_t)g.member_slots * m;
+  return c < (uint64_t)g.C ? (uint32_t)c : (uint32_t)g.C;
+}
 
 // Device miss ring: one deque per fetch worker, each a fixed segment of
 // `entries`.  state[w] packs (tail << 32 | head) relative to the segment, so
@@ -62,6 +73,15 @@ __global__ void k_lru_step(Geo g, const uint32_t* sel, uint32_t* slots_out, uint
                            int nl, unsigned long long* sel_counts, int* err);
 __global__ void k_sets_reset(Geo g, SetState st);
 __global__ void k_sets_reset_owners(Geo g, SetState st, const uint32_t* owners, uint32_t n, int* err);
+// Resident members: lanes leave (delta -1) or join (+1); owners that lost a
+// member are marked with trim generation `gen` for k_sets_trim.
+__global__ void k_members_update(Geo g, uint32_t* lane_live, uint32_t* members, uint32_t* trim_gen,
+                                 const uint32_t* lanes, uint32_t n, int delta, uint32_t gen, int* err);
+// Trim the sets of owners marked with `gen` to their capacity (one wavefront
+// per set, C words of LDS); NV 16-byte words per lane per block moved.
+template <int NV>
+__global__ void k_sets_trim(Geo g, SetState st, const uint32_t* trim_gen, uint32_t gen, uint8_t* pool,
+                            float* pool_scales);
 
 template <int NV>
 __global__ void k_fetch(FetchArgs a);

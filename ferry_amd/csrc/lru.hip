@@ -40,7 +40,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
                        uint8_t* __restrict__ miss_flag, uint32_t* __restrict__ map,
                        int* lastpos, uint32_t* sord, uint32_t* stag, uint32_t* smblk,
                        uint32_t* svict, uint32_t& fill, ferry_miss* __restrict__ mo,
-                       const Ring& ring, uint32_t worker) {
+                       const Ring& ring, uint32_t worker, uint32_t cap) {
   const int lane = lane_id();
   const int C = g.C;
   const int pend = p0 + cnt;
@@ -72,8 +72,9 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
     if (is_miss) smblk[M + lanes_below(mask)] = x;
     M += __builtin_popcountll(mask);
   }
-  // phase 3: victims = least recent untouched residents, oldest first
-  const int freeslots = C - (int)fill;
+  // phase 3: victims = least recent untouched residents, oldest first; the
+  // set may use `cap` of its C slots (fewer under per-member capacity)
+  const int freeslots = (int)cap > (int)fill ? (int)cap - (int)fill : 0;
   const int need = M > freeslots ? M - freeslots : 0;
   int nv = 0;
   for (int c = 0; c < (int)fill && nv < need; c += kWave) {
@@ -249,15 +250,16 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
 
   ferry_miss* mo = misses + (size_t)set * g.max_sel;
   const uint32_t worker = ring.worker_of_set[set];
+  const uint32_t cap = set_capacity(g, st.members[sv.o]);
   int total = 0, rc = 0;
   if (!SERIAL) {
     rc = substep(g, sv, (uint32_t)set, 0, sv.n, sel, slots_out, miss_flag, map, lastpos, sord, stag,
-                 smblk, svict, fill, mo, ring, worker);
+                 smblk, svict, fill, mo, ring, worker, cap);
     if (rc >= 0) total = rc;
   } else {
     for (int p = 0; p < sv.n; ++p) {
       rc = substep(g, sv, (uint32_t)set, p, 1, sel, slots_out, miss_flag, map, lastpos, sord, stag,
-                   smblk, svict, fill, mo + total, ring, worker);
+                   smblk, svict, fill, mo + total, ring, worker, cap);
       if (rc < 0) break;
       total += rc;
     }
@@ -327,6 +329,122 @@ __global__ __launch_bounds__(256) void k_sets_reset_owners(Geo g, SetState st,
   }
   if (lane == 0) st.fill[set] = 0;
 }
+
+// Resident members.  One thread per listed lane: leaving (delta -1) needs
+// the lane resident and marks its owner for the trim of generation `gen`;
+// joining (+1) needs it not resident.  A lane out of range or in the wrong
+// state latches FERRY_EINVAL and changes nothing.
+__global__ void k_members_update(Geo g, uint32_t* lane_live, uint32_t* members, uint32_t* trim_gen,
+                                 const uint32_t* lanes, uint32_t n, int delta, uint32_t gen,
+                                 int* err) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t lane = lanes[i];
+  if (lane >= (uint32_t)g.n_req) {
+    set_error(err, FERRY_EINVAL);
+    return;
+  }
+  const uint32_t o = lane / (uint32_t)g.group;
+  const uint32_t want = delta < 0 ? 1u : 0u;  // the state the lane must be in
+  if (atomicCAS(lane_live + lane, want, 1u - want) != want) {
+    set_error(err, FERRY_EINVAL);
+    return;
+  }
+  if (delta < 0) {
+    atomicSub(members + o, 1u);
+    trim_gen[o] = gen;
+  } else {
+    atomicAdd(members + o, 1u);
+  }
+}
+
+// Trim one set to its capacity (grp_trim, src/runtime/wla_multigpu.cuh:
+// 1923-1936): the e = fill - cap least recently used blocks are evicted and the
+// survivors keep their order.  Resident slots stay [0, fill): the survivors in
+// slots >= cap ("movers", ascending) move into the evicted slots < cap
+// ("holes", ascending), the i-th mover into the i-th hole, data and fp8
+// scales included.  One wavefront per set; pos[C] (the LRU position of each
+// slot) and the movers' list live in LDS.
+template <int NV>
+__global__ __launch_bounds__(64) void k_sets_trim(Geo g, SetState st, const uint32_t* trim_gen,
+                                                  uint32_t gen, uint8_t* __restrict__ pool,
+                                                  float* __restrict__ pool_scales) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  extern __shared__ uint32_t lds[];
+  const int lane = threadIdx.x;
+  const uint32_t set = blockIdx.x;
+  const uint32_t o = set / (uint32_t)(g.L * g.Hkv);
+  if (trim_gen[o] != gen) return;
+  const uint32_t C = (uint32_t)g.C;
+  const uint32_t fill = st.fill[set];
+  const uint32_t cap = set_capacity(g, st.members[o]);
+  if (fill <= cap) return;
+  const uint32_t e = fill - cap;
+  uint32_t* pos = lds;         // [C]
+  uint32_t* movers = lds + C;  // [C - cap] at most
+  uint32_t* ord = st.ord + (size_t)set * C;
+  uint32_t* tag = st.tag + (size_t)set * C;
+  uint32_t* map = st.map + (size_t)set * (size_t)g.max_blocks;
+  for (uint32_t i = lane; i < fill; i += kWave) pos[ord[i]] = i;
+  // the evicted blocks leave the map
+  for (uint32_t i = lane; i < e; i += kWave) astore(map + tag[ord[i]], kNone);
+  wave_fence();
+  // movers: surviving slots >= cap, ascending
+  uint32_t nm = 0;
+  for (uint32_t c = cap; c < fill; c += kWave) {
+    const uint32_t v = c + lane;
+    const bool mv = v < fill && pos[v] >= e;
+    const uint64_t mask = ballot(mv);
+    if (mv) movers[nm + lanes_below(mask)] = v;
+    nm += (uint32_t)__builtin_popcountll(mask);
+  }
+  __builtin_amdgcn_wave_barrier();
+  // holes: evicted slots < cap, ascending; the r-th takes the r-th mover
+  uint32_t nh = 0;
+  for (uint32_t c = 0; c < cap && nh < nm; c += kWave) {
+    const uint32_t v = c + lane;
+    const bool hole = v < cap && pos[v] < e;
+    uint64_t mask = ballot(hole);
+    while (mask) {  // wavefront-uniform: one block at a time, all lanes copy
+      const int b = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      const uint32_t h = c + (uint32_t)b, m = movers[nh++];
+      const u32x4* src = reinterpret_cast<const u32x4*>(pool + ((size_t)set * C + m) * g.bb);
+      u32x4* dst = reinterpret_cast<u32x4*>(pool + ((size_t)set * C + h) * g.bb);
+      u32x4 r[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) r[i] = __builtin_nontemporal_load(src + i * kWave + lane);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) __builtin_nontemporal_store(r[i], dst + i * kWave + lane);
+      if (pool_scales && lane < 2)
+        pool_scales[((size_t)set * C + h) * 2 + lane] = pool_scales[((size_t)set * C + m) * 2 + lane];
+      if (lane == 0) {
+        const uint32_t blk = tag[m];
+        tag[h] = blk;
+        astore(map + blk, h);
+        ord[pos[m]] = h;
+      }
+    }
+  }
+  wave_fence();
+  // new order: the survivors, shifted to the front; slots >= cap are free
+  for (uint32_t c = 0; c < cap; c += kWave) {
+    const uint32_t i = c + lane;
+    const uint32_t v = i < cap ? ord[e + i] : 0u;
+    __builtin_amdgcn_wave_barrier();
+    if (i < cap) ord[i] = v;
+    __builtin_amdgcn_wave_barrier();
+  }
+  for (uint32_t i = cap + lane; i < C; i += kWave) {
+    ord[i] = kNone;
+    tag[i] = kNone;
+  }
+  if (lane == 0) st.fill[set] = cap;
+}
+
+template __global__ void k_sets_trim<4>(Geo, SetState, const uint32_t*, uint32_t, uint8_t*, float*);
+template __global__ void k_sets_trim<8>(Geo, SetState, const uint32_t*, uint32_t, uint8_t*, float*);
+template __global__ void k_sets_trim<16>(Geo, SetState, const uint32_t*, uint32_t, uint8_t*, float*);
 
 // Reset all sets: empty order, no tags, map cleared.
 __global__ void k_sets_reset(Geo g, SetState st) {

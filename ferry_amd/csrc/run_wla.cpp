@@ -5,8 +5,9 @@
 // driver runs modes A, B and C of the same tick loop and prints one row each.
 // Flags keep the reference's names: --gpus (one id), --requests, --steps,
 // --layers, --sel, --hot, --arrival steady|bursty, --gap, --prefix-group,
-// --prefix-steps, --miss-trace (sets FERRY_MISS_TRACE), --kv-heads,
-// --head-dim.  Unknown flags are an error (exit 2).
+// --prefix-steps, --cap-mode group|perreq, --miss-trace (sets
+// FERRY_MISS_TRACE), --kv-heads, --head-dim.  Unknown flags are an error
+// (exit 2).
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -61,6 +62,15 @@ int main(int argc, char** argv) {
     else if (!std::strcmp(argv[i], "--gap")) gap_ms = std::atof(next());
     else if (!std::strcmp(argv[i], "--prefix-group")) sp.prefix_group = std::atoi(next());
     else if (!std::strcmp(argv[i], "--prefix-steps")) sp.prefix_steps = std::atoi(next());
+    else if (!std::strcmp(argv[i], "--cap-mode")) {
+      const char* v = next();
+      if (!std::strcmp(v, "group")) sp.cap_mode = 0;
+      else if (!std::strcmp(v, "perreq")) sp.cap_mode = 1;
+      else {
+        std::fprintf(stderr, "--cap-mode group|perreq, got %s\n", v);
+        return 2;
+      }
+    }
     else if (!std::strcmp(argv[i], "--miss-trace")) trace = next();
     else if (!std::strcmp(argv[i], "--kv-heads")) sp.kv_heads = std::atoi(next());
     else if (!std::strcmp(argv[i], "--head-dim")) sp.head_dim = std::atoi(next());
@@ -76,9 +86,11 @@ int main(int argc, char** argv) {
     std::printf("[trace] %s fnv1a64=%016llx bytes=%llu\n", trace.c_str(), (unsigned long long)h,
                 (unsigned long long)bytes);
   }
-  std::printf("[wla] gpu=%d reqs=%d layers=%d steps=%d sel=%d hot=%d arrival=%s gap=%.3fms prefix_group=%d%s%s\n",
+  std::printf("[wla] gpu=%d reqs=%d layers=%d steps=%d sel=%d hot=%d arrival=%s gap=%.3fms prefix_group=%d "
+              "cap_mode=%s%s%s\n",
               device, sp.num_requests, sp.num_layers, sp.steps, sp.sel_blocks, sp.hot_blocks, arrival.c_str(),
-              gap_ms, sp.prefix_group, trace.empty() ? "" : " trace=", trace.c_str());
+              gap_ms, sp.prefix_group, sp.cap_mode ? "perreq" : "group", trace.empty() ? "" : " trace=",
+              trace.c_str());
   ferry::AdaptiveBatchPolicy pol;
   ferry::WlaStealPolicy spol;
   int rc = 0;

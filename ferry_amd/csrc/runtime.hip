@@ -142,6 +142,9 @@ struct ferry_ctx {
   float* mass_ws = nullptr;        // per-workgroup (max, sum) of every block and query head
   int kt_perm = 0;                 // K table words lane-transposed for the matrix-core loads
   float* scratch_dev = nullptr;    // this device's address of the static `scratch` array
+  uint32_t* lane_live = nullptr;   // [n_req] 1 while the lane's request is a resident member
+  uint32_t* trim_gen = nullptr;    // [n_owners] last ferry_members_leave that shrank the owner
+  uint32_t member_calls = 0;       // ferry_members_leave calls so far (trim generations)
 
   Ring ring(int which = 0) const {
     Ring r;
@@ -178,6 +181,10 @@ int validate(const ferry_config* c) {
   if (c->attn == FERRY_ATTN_MFMA && (grp < 2 || c->dtype == FERRY_F32))
     return fail(FERRY_EINVAL, "the MFMA attention kernel needs q_heads/kv_heads >= 2 and 16/8-bit KV");
   if (c->fetch_workers < 0) return fail(FERRY_EINVAL, "fetch_workers < 0");
+  if (c->cap_mode != FERRY_CAP_GROUP && c->cap_mode != FERRY_CAP_PER_MEMBER)
+    return fail(FERRY_EINVAL, "bad cap_mode");
+  if (c->cap_mode == FERRY_CAP_PER_MEMBER && c->slots_per_set % c->group)
+    return fail(FERRY_EINVAL, "per-member capacity needs slots_per_set to be a multiple of group");
   if ((uint64_t)c->max_blocks >= (uint64_t)kPend) return fail(FERRY_EINVAL, "max_blocks too large");
   return FERRY_OK;
 }
@@ -192,6 +199,7 @@ void release(ferry_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   void* dev[] = {c->pool, c->pool_scales, c->st.fill, c->st.ord, c->st.tag, c->st.map,
+                 c->st.members, c->lane_live, c->trim_gen,
                  c->ring_entries, c->ring_state, c->ring_entries2, c->ring_state2,
                  c->ring_seg, c->ring_cap, c->worker_of_set,
                  c->stats, c->sel_counts, c->step_acc, c->done, c->err, c->probe_sink,
@@ -433,6 +441,8 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   g.bb = 2ull * g.T * g.D * g.esize;
   g.host_blocks = cfg->host_blocks;
   g.pool_slots = (uint64_t)g.n_sets * (uint64_t)g.C;
+  g.cap_mode = cfg->cap_mode;
+  g.member_slots = g.C / g.group;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1)
     cus = 256;
@@ -484,6 +494,9 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   TRY(dalloc(&c->st.ord, nslots));
   TRY(dalloc(&c->st.tag, nslots));
   TRY(dalloc(&c->st.map, (size_t)g.n_sets * g.max_blocks));
+  TRY(dalloc(&c->st.members, g.n_owners));
+  TRY(dalloc(&c->lane_live, g.n_req));
+  TRY(dalloc(&c->trim_gen, g.n_owners));
   // ring: worker segments sized for every miss their sets can produce
   const int W = g.workers;
   std::vector<uint32_t> wos(g.n_sets), cnt(W, 0), seg(W, 0), cap(W, 0);
@@ -554,6 +567,13 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   }
   hipLaunchKernelGGL(k_sets_reset, dim3(1024), dim3(256), 0, 0, g, c->st);
   HIPT(hipGetLastError());
+  {  // every lane starts as a resident member of its owner
+    std::vector<uint32_t> mem(g.n_owners), live(g.n_req, 1u);
+    for (int o = 0; o < g.n_owners; ++o) mem[o] = (uint32_t)std::min(g.group, g.n_req - o * g.group);
+    HIPT(hipMemcpy(c->st.members, mem.data(), (size_t)g.n_owners * 4, hipMemcpyHostToDevice));
+    HIPT(hipMemcpy(c->lane_live, live.data(), (size_t)g.n_req * 4, hipMemcpyHostToDevice));
+    HIPT(hipMemset(c->trim_gen, 0, (size_t)g.n_owners * 4));
+  }
   c->events.resize((size_t)g.L + 1, nullptr);
   for (auto& e : c->events) HIPT(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   c->booked.resize((size_t)g.L, nullptr);
@@ -682,6 +702,55 @@ int ferry_sets_state(ferry_ctx* ctx, uint32_t* fill, uint32_t* ord, uint32_t* ta
   if (fill) HIPC(hipMemcpy(fill, ctx->st.fill, ns * 4, hipMemcpyDeviceToHost));
   if (ord) HIPC(hipMemcpy(ord, ctx->st.ord, nsl * 4, hipMemcpyDeviceToHost));
   if (tag) HIPC(hipMemcpy(tag, ctx->st.tag, nsl * 4, hipMemcpyDeviceToHost));
+  return FERRY_OK;
+}
+
+}  // extern "C"
+
+namespace {
+int members_update(ferry_ctx* ctx, const uint32_t* lanes, uint32_t n, int delta, void* stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (n == 0) return FERRY_OK;
+  if (int rc = check_buf(lanes, "lanes")) return rc;
+  const Geo& g = ctx->g;
+  if (n > (uint32_t)g.n_req) return fail(FERRY_EINVAL, "more lanes than the executor has");
+  HIPC(hipSetDevice(ctx->device));
+  hipStream_t s = (hipStream_t)stream;
+  const uint32_t gen = delta < 0 ? ++ctx->member_calls : 0u;
+  hipLaunchKernelGGL(k_members_update, dim3((n + 255) / 256), dim3(256), 0, s, g, ctx->lane_live,
+                     ctx->st.members, ctx->trim_gen, lanes, n, delta, gen, ctx->err);
+  HIPC(hipGetLastError());
+  if (delta < 0 && g.cap_mode == FERRY_CAP_PER_MEMBER) {
+    const size_t lds = (size_t)2 * g.C * 4;
+    const dim3 grid((unsigned)g.n_sets), block(64);
+    switch (g.bb / 1024) {
+      case 4: hipLaunchKernelGGL(k_sets_trim<4>, grid, block, lds, s, g, ctx->st, ctx->trim_gen, gen, ctx->pool, ctx->pool_scales); break;
+      case 8: hipLaunchKernelGGL(k_sets_trim<8>, grid, block, lds, s, g, ctx->st, ctx->trim_gen, gen, ctx->pool, ctx->pool_scales); break;
+      case 16: hipLaunchKernelGGL(k_sets_trim<16>, grid, block, lds, s, g, ctx->st, ctx->trim_gen, gen, ctx->pool, ctx->pool_scales); break;
+      default: return fail(FERRY_EINVAL, "unsupported block size");
+    }
+    HIPC(hipGetLastError());
+  }
+  return FERRY_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int ferry_members_leave(ferry_ctx* ctx, const uint32_t* lanes, uint32_t n, void* stream) {
+  return members_update(ctx, lanes, n, -1, stream);
+}
+
+int ferry_members_join(ferry_ctx* ctx, const uint32_t* lanes, uint32_t n, void* stream) {
+  return members_update(ctx, lanes, n, +1, stream);
+}
+
+int ferry_members_get(ferry_ctx* ctx, uint32_t* members) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!members) return fail(FERRY_EINVAL, "null out");
+  HIPC(hipSetDevice(ctx->device));
+  HIPC(hipDeviceSynchronize());
+  HIPC(hipMemcpy(members, ctx->st.members, (size_t)ctx->g.n_owners * 4, hipMemcpyDeviceToHost));
   return FERRY_OK;
 }
 
@@ -1211,6 +1280,8 @@ int ferry_owner_image_bytes(const ferry_ctx* ctx, uint64_t* bytes) {
   return FERRY_OK;
 }
 
+}  // extern "C"
+
 namespace {
 
 int owner_check(ferry_ctx* ctx, uint32_t owner, const void* image, uint64_t image_bytes) {
@@ -1223,6 +1294,8 @@ int owner_check(ferry_ctx* ctx, uint32_t owner, const void* image, uint64_t imag
 }
 
 }  // namespace
+
+extern "C" {
 
 int ferry_owner_export(ferry_ctx* ctx, uint32_t owner, void* image, uint64_t image_bytes, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;

@@ -18,6 +18,9 @@
 // (request id, steps since admission) and it starts without carry-over, as a
 // fresh decode does.  A retired lane produces rows of FERRY_EMPTY.  A context
 // shorter than k blocks selects all of them and pads the row with FERRY_EMPTY.
+// In a prefix group a new member keeps the owner's permutation and shared
+// prefix ids, and ferry_selgen_admit_member gives its private blocks their
+// own id range, so a lane's successive requests never share private ids.
 //
 // ferry_refgen_selections: the selection half of replay_miss_stream
 // (src/workloads/missstream.cuh:104-133) with std::mt19937_64.
@@ -59,9 +62,25 @@ struct ferry_selgen {
   std::vector<int32_t> rid;    // request id held by each lane
   std::vector<int32_t> start;  // step at which that request was admitted
   std::vector<uint8_t> active; // lane holds a request
+  std::vector<int32_t> prange; // private id range of the lane's request (prefix groups)
+  int ranges = 0;              // private id ranges per owner (>= group)
   int nmax = 0;
   int max_blocks = 0;
 };
+
+namespace {
+// Largest block id + 1 over owners: shared prefix, then `ranges` private
+// ranges of (np - prefix) ids each.
+int selgen_max_blocks(const ferry_selgen* g) {
+  int mx = 0;
+  for (size_t o = 0; o < g->nperm.size(); ++o) {
+    const int np = g->nperm[o];
+    const int pre = std::min(g->cfg.prefix_blocks, np);
+    mx = std::max(mx, pre + g->ranges * (np - pre));
+  }
+  return mx;
+}
+}  // namespace
 
 extern "C" {
 
@@ -90,11 +109,9 @@ int ferry_selgen_create(const ferry_selgen_config* cfg, const int32_t* ctx_block
   const int nown = (cfg->n_req + cfg->group - 1) / cfg->group;
   g->nperm.assign(nown, 0);
   for (int r = 0; r < cfg->n_req; ++r) g->nperm[r / cfg->group] = std::max(g->nperm[r / cfg->group], g->ctx[r]);
-  for (int o = 0; o < nown; ++o) {
-    const int np = g->nperm[o];
-    const int pre = std::min(cfg->prefix_blocks, np);
-    g->max_blocks = std::max(g->max_blocks, pre + cfg->group * (np - pre));
-  }
+  (void)nown;
+  g->ranges = cfg->group;
+  g->max_blocks = selgen_max_blocks(g);
   if (cfg->dist == 1) {
     g->cum.resize(g->nmax);
     double acc = 0.0;
@@ -108,6 +125,8 @@ int ferry_selgen_create(const ferry_selgen_config* cfg, const int32_t* ctx_block
   for (int r = 0; r < cfg->n_req; ++r) g->rid[r] = r;
   g->start.assign(cfg->n_req, 0);
   g->active.assign(cfg->n_req, 1);
+  g->prange.resize(cfg->n_req);
+  for (int r = 0; r < cfg->n_req; ++r) g->prange[r] = r % cfg->group;
   *out = g;
   return FERRY_OK;
 }
@@ -123,6 +142,30 @@ int ferry_selgen_admit(ferry_selgen* g, int32_t lane, int32_t request_id, int32_
   g->nperm[lane] = ctx_blocks;
   g->start[lane] = step;
   g->active[lane] = 1;
+  return FERRY_OK;
+}
+
+int ferry_selgen_set_private_ranges(ferry_selgen* g, int32_t ranges) {
+  if (!g || ranges < g->cfg.group || ranges > 65536) return FERRY_EINVAL;
+  g->ranges = ranges;
+  g->max_blocks = selgen_max_blocks(g);
+  return FERRY_OK;
+}
+
+int ferry_selgen_admit_member(ferry_selgen* g, int32_t lane, int32_t request_id, int32_t ctx_blocks,
+                              int32_t step, int32_t private_range) {
+  if (!g || lane < 0 || lane >= g->cfg.n_req) return FERRY_EINVAL;
+  if (g->cfg.group == 1)
+    return private_range == 0 ? ferry_selgen_admit(g, lane, request_id, ctx_blocks, step) : FERRY_EINVAL;
+  const int o = lane / g->cfg.group;
+  if (request_id < 0 || request_id >= 65536 || step < 0) return FERRY_EINVAL;
+  if (ctx_blocks < 1 || ctx_blocks > g->nperm[o]) return FERRY_EINVAL;
+  if (private_range < 0 || private_range >= g->ranges) return FERRY_EINVAL;
+  g->rid[lane] = request_id;
+  g->ctx[lane] = ctx_blocks;
+  g->start[lane] = step;
+  g->active[lane] = 1;
+  g->prange[lane] = private_range;
   return FERRY_OK;
 }
 
@@ -171,7 +214,7 @@ int ferry_selgen_step(ferry_selgen* g, int32_t step, uint32_t* out) {
         std::fill(out + (size_t)r * L * H * k, out + (size_t)(r + 1) * L * H * k, FERRY_EMPTY);
         continue;
       }
-      const int o = r / c.group, m = r % c.group;
+      const int o = r / c.group, m = g->prange[r];  // m: the lane's private id range
       const int nr = g->ctx[r];
       const int np = g->nperm[o];
       const int pre = std::min(c.prefix_blocks, np);

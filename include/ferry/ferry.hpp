@@ -134,10 +134,12 @@ struct Exec {
   int status = FERRY_OK;
   uint32_t n_sets = 0, max_sel = 0;
 
-  Exec(const MissSpec& sp, int device, int lru_mode, int hot, int max_blocks = 0, int group = 1) {
+  Exec(const MissSpec& sp, int device, int lru_mode, int hot, int max_blocks = 0, int group = 1,
+       int cap_mode = FERRY_CAP_GROUP) {
     ferry_config c{};
     c.n_req = sp.num_requests;
     c.group = group;
+    c.cap_mode = cap_mode;
     c.n_layers = sp.num_layers;
     c.kv_heads = 1;
     c.q_heads = 1;
@@ -547,8 +549,10 @@ inline void wla_apply_prefix_sharing(std::vector<uint32_t>& ids, const MissSpec&
 // replay_miss_stream's (+ the prefix transform), or the trace named by
 // FERRY_MISS_TRACE.  The clock is the wall clock from the start, as in the
 // reference; FERRY_VIRTUAL_TICK_MS=x makes tick t start at t*x ms, which
-// fixes the tick composition (tests).  cap_mode 1 (capacity following the
-// resident members) is not modelled: status FERRY_EINVAL.
+// fixes the tick composition (tests).  Requests join their prefix group when
+// admitted and leave it when finished (ferry_members_join / _leave); with
+// cap_mode 1 the group's capacity is hot_blocks per resident member and a
+// leave trims it (wla_group_cap, grp_trim, wla_multigpu.cuh:1923-1936).
 inline WlaMultiStats run_wla_multigpu(const std::vector<int>& devices, MissSpec sp, int mode,
                                       const AdaptiveBatchPolicy& pol, const WlaStealPolicy& spol,
                                       const std::string& skew, const std::string& arrival, double gap_ms,
@@ -558,7 +562,7 @@ inline WlaMultiStats run_wla_multigpu(const std::vector<int>& devices, MissSpec 
   (void)rebal_interval_ms, (void)rebal_thr;
   WlaMultiStats st;
   st.n_gpus = (int)devices.size();
-  if (devices.size() != 1 || mode < 0 || mode > 7 || (sp.cap_mode == 1 && sp.prefix_group > 1) ||
+  if (devices.size() != 1 || mode < 0 || mode > 7 || sp.cap_mode < 0 || sp.cap_mode > 1 ||
       !(gap_ms > 0.0)) {
     st.status = FERRY_EINVAL;
     return st;
@@ -587,17 +591,40 @@ inline WlaMultiStats run_wla_multigpu(const std::vector<int>& devices, MissSpec 
   ferry_sched* sched = nullptr;
   if ((st.status = ferry_sched_create(R, FERRY_SCHED_PINNED, (uint32_t)R, arrive.data(), len.data(), &sched)))
     return st;
-  const int hot = mode == 0 ? G * group : sp.hot_blocks;
-  detail::Exec ex(sp, dev, FERRY_LRU_SERIAL, hot, max_blocks, group);
+  // per-request capacity (cap_mode 1, wla_group_cap): the group's sets have a
+  // share of hot_blocks per member, and members arrive and leave
+  const bool per_member = sp.cap_mode == 1 && mode != 0;
+  const int hot = mode == 0 ? G * group : sp.hot_blocks * (per_member ? group : 1);
+  detail::Exec ex(sp, dev, FERRY_LRU_SERIAL, hot, max_blocks, group,
+                  per_member ? FERRY_CAP_PER_MEMBER : FERRY_CAP_GROUP);
   if ((st.status = ex.status)) {
     ferry_sched_destroy(sched);
     return st;
   }
-  uint32_t* owners = nullptr;
-  if (hipMalloc(&owners, (size_t)R * 4)) {
+  uint32_t *owners = nullptr, *lanes = nullptr;
+  if (hipMalloc(&owners, (size_t)R * 4) || hipMalloc(&lanes, (size_t)R * 4)) {
     ferry_sched_destroy(sched);
+    (void)hipFree(owners);
     st.status = FERRY_ENOMEM;
     return st;
+  }
+  // Members join at dispatch and leave at tick_end (grp_member_add,
+  // wla_multigpu.cuh:801, 846-862): every lane starts out of its group.
+  auto members = [&](const int32_t* ids, int n, bool join) -> int {
+    if (n == 0) return FERRY_OK;
+    if (hipMemcpy(lanes, ids, (size_t)n * 4, hipMemcpyHostToDevice)) return FERRY_EHIP;
+    return join ? ferry_members_join(ex.ctx, lanes, (uint32_t)n, nullptr)
+                : ferry_members_leave(ex.ctx, lanes, (uint32_t)n, nullptr);
+  };
+  {
+    std::vector<int32_t> all(R);
+    for (int r = 0; r < R; ++r) all[r] = r;
+    if ((st.status = members(all.data(), R, false))) {
+      ferry_sched_destroy(sched);
+      (void)hipFree(owners);
+      (void)hipFree(lanes);
+      return st;
+    }
   }
   double vtick = 0.0;
   if (const char* e = std::getenv("FERRY_VIRTUAL_TICK_MS")) vtick = std::atof(e);
@@ -617,6 +644,10 @@ inline WlaMultiStats run_wla_multigpu(const std::vector<int>& devices, MissSpec 
     if ((st.status = ferry_sched_tick(sched, now, lane_req.data(), lane_step.data(), admitted.data(), &na,
                                       retired.data(), &nr, &nres, &done)))
       break;
+    // finished requests leave their groups (trimmed under cap_mode 1), then
+    // the arrived ones join
+    if ((st.status = members(retired.data(), nr, false))) break;
+    if ((st.status = members(admitted.data(), na, true))) break;
     if (done) break;
     if (nres == 0) {  // nothing resident: wait for the next arrival (wait_arrival, :1535-1540)
       if (vtick <= 0.0) {
@@ -686,6 +717,7 @@ inline WlaMultiStats run_wla_multigpu(const std::vector<int>& devices, MissSpec 
   }
   st.makespan_ms = elapsed();
   (void)hipFree(owners);
+  (void)hipFree(lanes);
   ferry_sched_destroy(sched);
   ferry_stats fs{};
   ferry_stats_get(ex.ctx, &fs);

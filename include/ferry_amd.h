@@ -80,7 +80,13 @@ typedef struct ferry_config {
   int32_t steal;         /* 1 = fetch workers steal from each other */
   int32_t assign;        /* FERRY_ASSIGN_SPREAD or FERRY_ASSIGN_AFFINITY */
   int32_t attn;          /* FERRY_ATTN_AUTO, FERRY_ATTN_VALU or FERRY_ATTN_MFMA */
+  int32_t cap_mode;      /* FERRY_CAP_GROUP or FERRY_CAP_PER_MEMBER */
 } ferry_config;
+
+/* ---- capacity of an owner's sets (MissSpec::cap_mode, wla_group_cap,
+ * src/workloads/missstream.cuh:40-47, 91-94) ---- */
+#define FERRY_CAP_GROUP 0      /* every set holds slots_per_set blocks */
+#define FERRY_CAP_PER_MEMBER 1 /* (slots_per_set / group) x resident members, at least one share */
 
 /* One fetched block: written per set in miss order. */
 typedef struct ferry_miss {
@@ -161,6 +167,27 @@ int ferry_sets_reset_owners(ferry_ctx* ctx, const uint32_t* owners, uint32_t n, 
 /* Copy per-set LRU state to host arrays: fill[n_sets], ord[n_sets][slots]
  * (local slots, LRU first), tag[n_sets][slots] (block per slot). */
 int ferry_sets_state(ferry_ctx* ctx, uint32_t* fill, uint32_t* ord, uint32_t* tag);
+
+/* Resident members of prefix groups.  Every batch lane (request row) is a
+ * member of its owner (lane / group) and starts resident.  ferry_members_leave
+ * takes the requests of the listed lanes (device array of n lane ids) out:
+ * each owner loses one resident member per lane, and under
+ * FERRY_CAP_PER_MEMBER its sets are trimmed to the new capacity, least
+ * recently used blocks first; the surviving blocks keep their LRU order and
+ * are compacted into slots [0, capacity) (blocks in higher slots move into
+ * the freed lower ones, data and fp8 scales included), so a set's resident
+ * slots stay [0, fill).  ferry_members_join makes the listed lanes resident
+ * again (a new request of the group takes the lane): its owner gains a
+ * member, and with it capacity; nothing is evicted or reset.  Lanes must
+ * alternate leave / join: leaving a lane that is not resident, or joining one
+ * that is, latches FERRY_EINVAL in the device error word.  Replaces
+ * grp_member_add at dispatch and tick_end plus grp_trim
+ * (src/runtime/wla_multigpu.cuh:801, 846-862, 1923-1936).  ferry_members_get
+ * copies the resident members of every owner to members[n_owners]
+ * (synchronises). */
+int ferry_members_leave(ferry_ctx* ctx, const uint32_t* lanes, uint32_t n, void* stream);
+int ferry_members_join(ferry_ctx* ctx, const uint32_t* lanes, uint32_t n, void* stream);
+int ferry_members_get(ferry_ctx* ctx, uint32_t* members);
 
 /* Empty positions.  A selection id of FERRY_EMPTY (0xFFFFFFFF) selects
  * nothing: it is neither hit nor miss, its slot comes back as FERRY_EMPTY,
@@ -451,6 +478,19 @@ int ferry_ctx_uniform(uint64_t seed, int32_t n_req, int32_t lo, int32_t hi,
 int ferry_selgen_admit(ferry_selgen* g, int32_t lane, int32_t request_id, int32_t ctx_blocks,
                        int32_t step);
 int ferry_selgen_retire(ferry_selgen* g, int32_t lane);
+/* Prefix-group turnover.  A group's members share its prefix ids [0, prefix)
+ * and each has a private range of (np - prefix) ids after them, np = the
+ * owner's largest member context at creation.  ferry_selgen_set_private_ranges
+ * makes `ranges` (>= group) such ranges per owner (read max_blocks after it);
+ * ferry_selgen_admit_member puts request `request_id` (context <= np) into a
+ * lane of the group from step `step` on, its private blocks in range
+ * `private_range` (< ranges), so that successive requests of one lane select
+ * different private ids.  For group 1 it is ferry_selgen_admit (range 0).
+ * Replaces the group membership of the reference's C2 prefix affinity
+ * (src/workloads/missstream.cuh:33-38, src/runtime/wla_multigpu.cuh:355-369). */
+int ferry_selgen_set_private_ranges(ferry_selgen* g, int32_t ranges);
+int ferry_selgen_admit_member(ferry_selgen* g, int32_t lane, int32_t request_id, int32_t ctx_blocks,
+                              int32_t step, int32_t private_range);
 
 /* ---- request arrivals and the per-GPU tick scheduler ----
  * Arrival times in ms of n requests (out_ms[n], non-decreasing, first

@@ -342,6 +342,7 @@ uint64_t ora_ref_cmode_runs(int R, int L, int S, int sel, int hot,
 
 int ora_lru_init(ora_lru* s, int cap, int max_blocks) {
   s->cap = cap;
+  s->lim = cap;
   s->max_blocks = max_blocks;
   s->ord = (uint32_t*)malloc((size_t)cap * 4);
   s->tag = (uint32_t*)malloc((size_t)cap * 4);
@@ -405,8 +406,8 @@ int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
     if (flag_out) flag_out[p] = (uint8_t)first;
     if (first) mblk[M++] = x[p];
   }
-  /* phase 3: victims */
-  const int freeslots = cap - (int)s->fill;
+  /* phase 3: victims; the set may use lim of its cap slots */
+  const int freeslots = s->lim > (int)s->fill ? s->lim - (int)s->fill : 0;
   const int need = M > freeslots ? M - freeslots : 0;
   int nv = 0;
   for (uint32_t i = 0; i < s->fill && nv < need; ++i)
@@ -459,6 +460,39 @@ int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
   return w == s->fill ? 0 : -4;
 }
 
+int ora_lru_trim(ora_lru* s, int lim, uint32_t* moves) {
+  s->lim = lim;
+  if ((int)s->fill <= lim) return 0;
+  const uint32_t e = s->fill - (uint32_t)lim, f = s->fill;
+  uint32_t* pos = (uint32_t*)malloc((size_t)s->cap * 4);
+  for (uint32_t i = 0; i < f; ++i) pos[s->ord[i]] = i;
+  for (uint32_t i = 0; i < e; ++i) s->map[s->tag[s->ord[i]]] = ORA_NONE;
+  uint32_t hole = 0;  /* next candidate hole slot */
+  int nm = 0;
+  for (uint32_t m = (uint32_t)lim; m < f; ++m) {
+    if (pos[m] < e) continue; /* evicted, not a mover */
+    while (pos[hole] >= e) ++hole; /* next evicted slot below lim */
+    const uint32_t blk = s->tag[m];
+    s->tag[hole] = blk;
+    s->map[blk] = hole;
+    s->ord[pos[m]] = hole;
+    if (moves) {
+      moves[2 * nm] = m;
+      moves[2 * nm + 1] = hole;
+    }
+    ++nm;
+    ++hole;
+  }
+  memmove(s->ord, s->ord + e, (size_t)lim * 4);
+  for (int i = lim; i < s->cap; ++i) {
+    s->ord[i] = ORA_NONE;
+    s->tag[i] = ORA_NONE;
+  }
+  s->fill = (uint32_t)lim;
+  free(pos);
+  return nm;
+}
+
 /* Deque LRU, restating the replay's per-touch loop (missstream.cuh:137-161)
  * over a single (request, layer) stream. */
 int ora_deque_lru_run(int cap, const uint32_t* x, int n, uint8_t* miss_flag) {
@@ -485,6 +519,44 @@ int ora_deque_lru_run(int cap, const uint32_t* x, int n, uint8_t* miss_flag) {
   }
   free(d);
   return 0;
+}
+
+/* kv_touch with a capacity per touch and grp_trim at capacity drops
+ * (wla_multigpu.cuh:1923-1962), as a plain deque. */
+int ora_deque_lru_run_caps(const int* trim_at, const int* cap_at, const uint32_t* x, int n,
+                           uint8_t* miss_flag, uint32_t* final_blocks) {
+  int mx = 1;
+  for (int i = 0; i < n; ++i)
+    if (cap_at[i] > mx) mx = cap_at[i];
+  uint32_t* d = (uint32_t*)malloc((size_t)(mx + 1) * 4);
+  int dn = 0;
+  for (int i = 0; i < n; ++i) {
+    const int cap = cap_at[i];
+    if (dn > trim_at[i]) { /* grp_trim: drop from the front down to the capacity */
+      memmove(d, d + (dn - trim_at[i]), (size_t)trim_at[i] * 4);
+      dn = trim_at[i];
+    }
+    int pos = -1;
+    for (int j = 0; j < dn; ++j)
+      if (d[j] == x[i]) {
+        pos = j;
+        break;
+      }
+    miss_flag[i] = pos < 0;
+    if (pos >= 0) {
+      memmove(d + pos, d + pos + 1, (size_t)(dn - pos - 1) * 4);
+      d[dn - 1] = x[i];
+    } else {
+      while (dn >= cap) {
+        memmove(d, d + 1, (size_t)(dn - 1) * 4);
+        dn--;
+      }
+      d[dn++] = x[i];
+    }
+  }
+  if (final_blocks) memcpy(final_blocks, d, (size_t)dn * 4);
+  free(d);
+  return dn;
 }
 
 /* Timestamp LRU with step-batched semantics, written independently of the
@@ -591,7 +663,16 @@ struct ora_exec {
   uint32_t* x;
   uint32_t* slot;
   uint8_t* flag;
+  uint32_t* members;  /* [n_owners] resident member lanes */
+  uint8_t* live;      /* [n_req] lane resident */
 };
+
+int ora_capacity(const ora_geom* g, int members) {
+  if (g->cap_mode != 1) return g->cap;
+  const int share = g->cap / g->group;
+  const long c = (long)share * (members > 0 ? members : 1);
+  return c < g->cap ? (int)c : g->cap;
+}
 
 ora_exec* ora_exec_create(const ora_geom* g) {
   ora_exec* e = (ora_exec*)calloc(1, sizeof(ora_exec));
@@ -603,7 +684,45 @@ ora_exec* ora_exec_create(const ora_geom* g) {
   e->x = (uint32_t*)malloc((size_t)ora_max_sel_per_set(g) * 4);
   e->slot = (uint32_t*)malloc((size_t)ora_max_sel_per_set(g) * 4);
   e->flag = (uint8_t*)malloc((size_t)ora_max_sel_per_set(g));
+  e->members = (uint32_t*)malloc((size_t)ora_n_owners(g) * 4);
+  e->live = (uint8_t*)malloc((size_t)g->n_req);
+  for (int o = 0; o < ora_n_owners(g); ++o) e->members[o] = (uint32_t)ora_members(g, o);
+  memset(e->live, 1, (size_t)g->n_req);
   return e;
+}
+
+int ora_exec_members(ora_exec* e, const uint32_t* lanes, int n, int delta) {
+  const ora_geom* g = &e->g;
+  const int nown = ora_n_owners(g), per = g->n_layers * g->kv_heads;
+  uint8_t* shrunk = (uint8_t*)calloc((size_t)nown, 1);
+  int rc = 0;
+  for (int i = 0; i < n; ++i) {
+    const uint32_t ln = lanes[i];
+    const uint8_t want = delta < 0 ? 1 : 0;
+    if (ln >= (uint32_t)g->n_req || e->live[ln] != want) {
+      rc = -1;
+      continue;
+    }
+    e->live[ln] = (uint8_t)(1 - want);
+    const uint32_t o = ln / (uint32_t)g->group;
+    if (delta < 0) {
+      e->members[o]--;
+      shrunk[o] = 1;
+    } else {
+      e->members[o]++;
+    }
+  }
+  if (g->cap_mode == 1)
+    for (int o = 0; o < nown; ++o)
+      if (shrunk[o])
+        for (int i = 0; i < per; ++i)
+          ora_lru_trim(&e->sets[o * per + i], ora_capacity(g, (int)e->members[o]), NULL);
+  free(shrunk);
+  return rc;
+}
+
+void ora_exec_members_get(const ora_exec* e, uint32_t* members) {
+  memcpy(members, e->members, (size_t)ora_n_owners(&e->g) * 4);
 }
 
 void ora_exec_destroy(ora_exec* e) {
@@ -614,6 +733,8 @@ void ora_exec_destroy(ora_exec* e) {
   free(e->x);
   free(e->slot);
   free(e->flag);
+  free(e->members);
+  free(e->live);
   free(e);
 }
 
@@ -637,6 +758,7 @@ int ora_exec_step(ora_exec* e, const uint32_t* sel, uint32_t* slots_out,
         }
         ora_miss* mo = misses + (size_t)set * maxsel;
         int M = 0;
+        e->sets[set].lim = ora_capacity(g, (int)e->members[o]);
         if (g->granularity == 0) {
           const int rc = ora_lru_substep(&e->sets[set], set, e->x, n, e->slot, mo, &M, e->flag);
           if (rc) return rc;
@@ -741,11 +863,12 @@ static int owner_nperm(const ora_selgen* s, int o) {
 
 int ora_selgen_max_blocks(const ora_selgen* s) {
   const int nown = (s->n_req + s->group - 1) / s->group;
+  const int ranges = s->private_ranges > s->group ? s->private_ranges : s->group;
   int mx = 0;
   for (int o = 0; o < nown; ++o) {
-    const int np = owner_nperm(s, o);
+    const int np = s->nperm ? s->nperm[o] : owner_nperm(s, o);
     const int pre = s->prefix_blocks < np ? s->prefix_blocks : np;
-    const int b = pre + s->group * (np - pre);
+    const int b = pre + ranges * (np - pre);
     if (b > mx) mx = b;
   }
   return mx;
@@ -773,9 +896,12 @@ static int cmp_u32(const void* a, const void* b) {
 int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
                     uint32_t* out) {
   const int L = s->n_layers, H = s->kv_heads, k = s->k;
-  int nmax = 0;
+  int nmax = 0; /* the largest permutation domain (Zipf weights and draw marks) */
   for (int r = 0; r < s->n_req; ++r)
     if (s->ctx_blocks[r] > nmax) nmax = s->ctx_blocks[r];
+  if (s->nperm)
+    for (int o = 0; o < (s->n_req + s->group - 1) / s->group; ++o)
+      if (s->nperm[o] > nmax) nmax = s->nperm[o];
   double* cum = NULL;
   if (s->dist == 1) {
     cum = (double*)malloc((size_t)nmax * sizeof(double));
@@ -792,9 +918,10 @@ int ora_selgen_step(const ora_selgen* s, int step, uint32_t* state,
       for (size_t i = 0; i < rows; ++i) out[(size_t)r * rows + i] = ORA_NONE;
       continue;
     }
-    const int o = r / s->group, m = r % s->group;
+    const int o = r / s->group;
+    const int m = s->prange ? s->prange[r] : r % s->group; /* private id range */
     const int nr = s->ctx_blocks[r];
-    const int np = owner_nperm(s, o);
+    const int np = s->nperm ? s->nperm[o] : owner_nperm(s, o);
     const int pre = s->prefix_blocks < np ? s->prefix_blocks : np;
     const double reuse = s->reuse_r ? s->reuse_r[r] : s->reuse;
     const uint64_t keep_thr = (uint64_t)(reuse * 4294967296.0);

@@ -98,6 +98,7 @@ typedef struct {
 
 typedef struct {
   int cap;         /* slots per set */
+  int lim;         /* slots the set may use now (<= cap; fewer under per-member capacity) */
   int max_blocks;  /* block ids are < max_blocks */
   uint32_t fill;   /* slots in use; free slots are [fill, cap) */
   uint32_t* ord;   /* [cap] local slots, LRU first; first `fill` valid */
@@ -117,9 +118,25 @@ int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
                     uint32_t* slot_out, ora_miss* miss_out, int* n_miss,
                     uint8_t* flag_out);
 
+/* Trim a set to `lim` blocks (grp_trim, wla_multigpu.cuh:1923-1936): the
+ * fill - lim least recently used blocks are evicted, the survivors keep their
+ * order and are compacted into slots [0, lim): the i-th surviving slot >= lim
+ * (ascending) moves into the i-th evicted slot < lim (ascending).  Sets
+ * s->lim = lim.  moves (may be NULL) gets (from, to) pairs; returns their
+ * number. */
+int ora_lru_trim(ora_lru* s, int lim, uint32_t* moves);
+
 /* Independent restatements (cross-checks only). */
 /* Deque LRU with per-touch semantics (missstream.cuh:137-161). */
 int ora_deque_lru_run(int cap, const uint32_t* x, int n, uint8_t* miss_flag);
+/* The same with a capacity per touch, as kv_touch under per-member capacity
+ * (wla_multigpu.cuh:1923-1962): before touch i the deque is trimmed from the
+ * front to trim_at[i] (grp_trim: the smallest capacity members leaving left
+ * since the previous touch), and a miss pops the front while the deque holds
+ * cap_at[i] or more.  final_blocks (may be NULL) gets the deque at the end,
+ * least recent first; returns its length. */
+int ora_deque_lru_run_caps(const int* trim_at, const int* cap_at, const uint32_t* x, int n,
+                           uint8_t* miss_flag, uint32_t* final_blocks);
 /* Timestamp LRU with step-batched semantics (victim = least recent stamp
  * among slots not selected in the step). */
 typedef struct {
@@ -151,6 +168,7 @@ typedef struct {
   uint64_t host_blocks; /* host tier capacity in blocks */
   uint64_t seed;   /* host tier content seed */
   float value_std; /* std of K/V values */
+  int cap_mode;    /* 0: every set holds cap blocks; 1: (cap / group) per resident member */
 } ora_geom;
 
 int ora_n_owners(const ora_geom* g);
@@ -173,6 +191,15 @@ int ora_exec_step(ora_exec* e, const uint32_t* sel, uint32_t* slots_out,
                   uint8_t* flags);
 /* Empty the sets of one owner (a new request takes over its lane). */
 int ora_exec_reset_owner(ora_exec* e, int owner);
+/* Resident members (every lane starts resident): the requests of lanes[0..n)
+ * leave (delta -1) or join (+1) their owners; leaving owners are trimmed to
+ * their new capacity under cap_mode 1 (ora_lru_trim).  A lane out of range,
+ * leaving while not resident or joining while resident is skipped and makes
+ * the call return -1.  ora_exec_members_get copies the per-owner counts. */
+int ora_exec_members(ora_exec* e, const uint32_t* lanes, int n, int delta);
+void ora_exec_members_get(const ora_exec* e, uint32_t* members);
+/* Blocks the sets of an owner with `members` resident members may hold. */
+int ora_capacity(const ora_geom* g, int members);
 /* Copy owner src_owner's sets of src onto owner dst_owner of dst. */
 int ora_exec_copy_owner(const ora_exec* src, int src_owner, ora_exec* dst, int dst_owner);
 /* Per-set state export for parity: fill[n_sets], ord[n_sets][cap],
@@ -196,6 +223,13 @@ typedef struct {
   const int* rid;
   const int* start;
   const uint8_t* active;
+  /* Prefix-group turnover (NULL / 0 = none): the private id range of the
+   * request in each lane (default: its member index r % group), the number
+   * of such ranges per owner (0 = group), and each owner's permutation
+   * domain fixed at creation (NULL = the largest current member context). */
+  const int* prange;
+  int private_ranges;
+  const int* nperm;
 } ora_selgen;
 
 /* Per-request context lengths: uniform integer in [lo, hi]. */

@@ -49,6 +49,7 @@ class Geom(C.Structure):
         ("block_tokens", C.c_int), ("k", C.c_int), ("cap", C.c_int),
         ("max_blocks", C.c_int), ("dtype", C.c_int), ("granularity", C.c_int),
         ("host_blocks", C.c_uint64), ("seed", C.c_uint64), ("value_std", C.c_float),
+        ("cap_mode", C.c_int),
     ]
 
 
@@ -59,7 +60,8 @@ class SelGen(C.Structure):
         ("zipf_s", C.c_double), ("reuse", C.c_double), ("prefix_blocks", C.c_int), ("seed", C.c_uint64),
         ("ctx_blocks", C.POINTER(C.c_int)), ("reuse_r", C.POINTER(C.c_double)),
         ("rid", C.POINTER(C.c_int)), ("start", C.POINTER(C.c_int)),
-        ("active", C.POINTER(C.c_uint8)),
+        ("active", C.POINTER(C.c_uint8)), ("prange", C.POINTER(C.c_int)),
+        ("private_ranges", C.c_int), ("nperm", C.POINTER(C.c_int)),
     ]
 
 
@@ -68,7 +70,7 @@ class MT64(C.Structure):
 
 
 class LRU(C.Structure):
-    _fields_ = [("cap", C.c_int), ("max_blocks", C.c_int), ("fill", C.c_uint32),
+    _fields_ = [("cap", C.c_int), ("lim", C.c_int), ("max_blocks", C.c_int), ("fill", C.c_uint32),
                 ("ord", C.POINTER(C.c_uint32)), ("tag", C.POINTER(C.c_uint32)),
                 ("map", C.POINTER(C.c_uint32))]
 
@@ -104,6 +106,11 @@ _sig("ora_lru_free", None, C.POINTER(LRU))
 _sig("ora_lru_substep", C.c_int, C.POINTER(LRU), C.c_uint32, _u32p, C.c_int, _u32p, _missp,
      C.POINTER(C.c_int), C.c_void_p)
 _sig("ora_deque_lru_run", C.c_int, C.c_int, _u32p, C.c_int, _u8p)
+_sig("ora_deque_lru_run_caps", C.c_int, _i32p, _i32p, _u32p, C.c_int, _u8p, _u32p)
+_sig("ora_lru_trim", C.c_int, C.POINTER(LRU), C.c_int, C.c_void_p)
+_sig("ora_exec_members", C.c_int, C.c_void_p, _u32p, C.c_int, C.c_int)
+_sig("ora_exec_members_get", None, C.c_void_p, _u32p)
+_sig("ora_capacity", C.c_int, C.POINTER(Geom), C.c_int)
 _sig("ora_tslru_init", C.c_int, C.POINTER(TSLRU), C.c_int, C.c_int)
 _sig("ora_tslru_free", None, C.POINTER(TSLRU))
 _sig("ora_tslru_step", C.c_int, C.POINTER(TSLRU), _u32p, C.c_int, _u32p, _u32p, _u32p,
@@ -207,6 +214,21 @@ class Executor:
         if lib.ora_exec_reset_owner(self.ptr, owner):
             raise ValueError(f"owner {owner}")
 
+    def members_leave(self, lanes):
+        """Requests of these lanes leave (trim under cap_mode 1); False if a
+        lane was out of range or not resident (it is skipped)."""
+        return lib.ora_exec_members(self.ptr, np.ascontiguousarray(lanes, np.uint32),
+                                    len(lanes), -1) == 0
+
+    def members_join(self, lanes):
+        return lib.ora_exec_members(self.ptr, np.ascontiguousarray(lanes, np.uint32),
+                                    len(lanes), 1) == 0
+
+    def members(self):
+        out = np.zeros((self.g.n_req + self.g.group - 1) // self.g.group, np.uint32)
+        lib.ora_exec_members_get(self.ptr, out)
+        return out
+
     def state(self):
         cap = self.g.cap
         fill = np.zeros(self.n_sets, np.uint32)
@@ -219,7 +241,7 @@ class Executor:
 def make_geom(**kw):
     g = Geom()
     defaults = dict(group=1, q_heads=None, head_dim=128, block_tokens=16, dtype=F16,
-                    granularity=0, host_blocks=1 << 16, seed=7, value_std=0.5)
+                    granularity=0, host_blocks=1 << 16, seed=7, value_std=0.5, cap_mode=0)
     defaults.update(kw)
     if defaults["q_heads"] is None:
         defaults["q_heads"] = defaults["kv_heads"]
@@ -258,6 +280,26 @@ def selgen_admit(s: SelGen, lane, request_id, ctx_blocks, step):
 
 def selgen_retire(s: SelGen, lane):
     s._active[lane] = 0
+
+
+def selgen_group_turnover(s: SelGen, private_ranges):
+    """Let prefix-group lanes turn over: each owner's permutation domain is
+    fixed at its creation value, and `private_ranges` private id ranges per
+    owner are available to successive members (selgen_admit_member)."""
+    nown = (s.n_req + s.group - 1) // s.group
+    s._nperm = np.array([int(s._ctx[o * s.group:(o + 1) * s.group].max()) for o in range(nown)],
+                        np.int32)
+    s._prange = (np.arange(s.n_req) % s.group).astype(np.int32)
+    s.nperm = s._nperm.ctypes.data_as(C.POINTER(C.c_int))
+    s.prange = s._prange.ctypes.data_as(C.POINTER(C.c_int))
+    s.private_ranges = private_ranges
+
+
+def selgen_admit_member(s: SelGen, lane, request_id, ctx_blocks, step, private_range):
+    """A request of lane's prefix group takes the lane from `step`, with its
+    private blocks in id range `private_range`."""
+    selgen_admit(s, lane, request_id, ctx_blocks, step)
+    s._prange[lane] = private_range
 
 
 def selgen_step(s: SelGen, step):

@@ -65,12 +65,14 @@ def test_refgen_matches_reference_replay():
     dict(k=0), dict(slots_per_set=0), dict(assign=5), dict(max_blocks=0), dict(attn=3),
     dict(attn=2),  # MFMA kernel needs a GQA group (q_heads/kv_heads >= 2)
     dict(attn=2, q_heads=4, dtype=0),  # ... and 16/8-bit KV
+    dict(cap_mode=2),
+    dict(cap_mode=1, group=2, slots_per_set=7),  # per-member shares must divide the slots
 ])
 def test_invalid_config_rejected_before_any_device_call(bad):
     base = dict(n_req=2, group=1, n_layers=1, kv_heads=2, q_heads=2, head_dim=128,
                 block_tokens=16, k=4, slots_per_set=8, max_blocks=16, dtype=F.F16, lru_mode=0,
                 host_blocks=64, host_seed=1, value_std=0.5, fetch_workers=0, steal=1, assign=0,
-                attn=0)
+                attn=0, cap_mode=0)
     base.update(bad)
     cfg = F.Config(*[base[f] for f, _ in F.Config._fields_])
     h = C.c_void_p()

@@ -124,11 +124,15 @@ def test_wla_slice_default_stream_with_bursty_arrivals():
 
 
 @pytest.mark.gpu
-def test_wla_slice_prefix_groups_match_oracle():
+@pytest.mark.parametrize("cap_mode", ["group", "perreq"])
+def test_wla_slice_prefix_groups_match_oracle(cap_mode):
     # C2 prefix groups (wla_multigpu.cuh:355-369): members repeat their head's
     # selections for 8 steps and share the group's LRU, touched member after
     # member within a tick (:2643-2648).  With a virtual clock the tick
-    # composition is fixed, and the oracle replays the same ticks.
+    # composition is fixed, and the oracle replays the same ticks.  Under
+    # --cap-mode perreq the group's capacity is hot x resident members: a
+    # request joins at its arrival and leaves when it finishes, which trims the
+    # group (wla_group_cap, grp_trim, :846-862, 1923-1936).
     import numpy as np
 
     import ferry_amd as F
@@ -137,7 +141,7 @@ def test_wla_slice_prefix_groups_match_oracle():
     R, L, S, SEL, HOT, GRP, PS, GAP, TICK = 12, 3, 10, 16, 40, 4, 8, 0.7, 1.0
     out = _run_wla(["--requests", str(R), "--layers", str(L), "--steps", str(S), "--sel", str(SEL),
                     "--hot", str(HOT), "--arrival", "steady", "--gap", str(GAP),
-                    "--prefix-group", str(GRP), "--prefix-steps", str(PS)],
+                    "--prefix-group", str(GRP), "--prefix-steps", str(PS), "--cap-mode", cap_mode],
                    env={"FERRY_VIRTUAL_TICK_MS": str(TICK)})
     rows = _rows(out)
     ids = F.refgen_selections(R, L, S, SEL, 42)
@@ -147,13 +151,21 @@ def test_wla_slice_prefix_groups_match_oracle():
     arrive = O.arrivals(0, R, GAP)
     clock = np.arange(0.0, 200.0, TICK)
     table, _, _ = O.sched_run(R, arrive, np.full(R, S), clock, pinned=True)
-    g = O.make_geom(n_req=R, group=GRP, n_layers=L, kv_heads=1, k=SEL, cap=HOT,
-                    max_blocks=64 + 8 * S, dtype=O.F32, granularity=1)
+    per = cap_mode == "perreq"
+    g = O.make_geom(n_req=R, group=GRP, n_layers=L, kv_heads=1, k=SEL,
+                    cap=HOT * GRP if per else HOT, max_blocks=64 + 8 * S, dtype=O.F32,
+                    granularity=1, cap_mode=1 if per else 0)
     ex = O.Executor(g)
+    assert ex.members_leave(list(range(R)))  # members join when they arrive
     step = np.zeros(R, int)
     misses = ticks = runs = 0
+    was = np.zeros(R, bool)
     for t in range(len(clock)):
         live = table[t] >= 0
+        gone = [int(x) for x in np.nonzero(was & ~live)[0]]
+        came = [int(x) for x in np.nonzero(live & ~was)[0]]
+        assert (not gone or ex.members_leave(gone)) and (not came or ex.members_join(came))
+        was = live
         if not live.any():
             if t > 0 and (table[:t] >= 0).any() and not (table[t:] >= 0).any():
                 break
