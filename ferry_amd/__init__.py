@@ -133,6 +133,9 @@ _PROTOS = {
     "ferry_owner_image_bytes": (C.c_int, [_vp, C.POINTER(C.c_uint64)]),
     "ferry_owner_export": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint64, _vp]),
     "ferry_owner_import": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint64, _vp]),
+    "ferry_owner_export_member": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint64, _vp]),
+    "ferry_owner_import_member": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint64, _vp]),
+    "ferry_sets_own": (C.c_int, [_vp, _vp]),
     "ferry_decode_chunks": (C.c_int, [_vp, C.c_uint64, C.POINTER(_i32)]),
     "ferry_summaries_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(C.c_uint64)]),
     "ferry_select_topk": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp, _vp]),
@@ -326,6 +329,21 @@ class Executor:
         _check(lib.ferry_owner_import(self._h, owner, _dev(image, "image", 0, _U8, self.device),
                                       image.numel(), _stream(stream)), "ferry_owner_import")
 
+    def owner_export_member(self, lane, image, stream=None):
+        """Image of the blocks only `lane`'s member of its prefix group touched
+        (kv_handoff_owned's carry, src/runtime/wla_multigpu.cuh:1996-2016)."""
+        _check(lib.ferry_owner_export_member(self._h, lane,
+                                             _dev(image, "image", 0, _U8, self.device),
+                                             image.numel(), _stream(stream)),
+               "ferry_owner_export_member")
+
+    def owner_import_member(self, lane, image, stream=None):
+        """Merge a member image into `lane`'s owner (join the lane first)."""
+        _check(lib.ferry_owner_import_member(self._h, lane,
+                                             _dev(image, "image", 0, _U8, self.device),
+                                             image.numel(), _stream(stream)),
+               "ferry_owner_import_member")
+
     def set_batch_policy(self, min_mb=32.0, max_mb=512.0, target_batches=8.0):
         _check(lib.ferry_set_batch_policy(self._h, min_mb, max_mb, target_batches),
                "ferry_set_batch_policy")
@@ -487,6 +505,12 @@ class Executor:
         _check(lib.ferry_sets_state(self._h, fill.ctypes.data, ord_.ctypes.data, tag.ctypes.data),
                "ferry_sets_state")
         return fill, ord_, tag
+
+    def sets_own(self):
+        """Per-slot member masks [n_sets, slots] of prefix groups (synchronises)."""
+        own = np.zeros((self.n_sets, self.cfg.slots_per_set), np.uint32)
+        _check(lib.ferry_sets_own(self._h, own.ctypes.data), "ferry_sets_own")
+        return own
 
     def hosttier_register(self, host, scales=None):
         """Use the caller's pinned host memory (a pin_memory uint8 CPU tensor of

@@ -15,11 +15,12 @@
 //
 // Image layout (device memory, offsets in bytes from its start):
 //   [0, 64)          header: magic, sets, slots_per_set, block_bytes, dtype,
-//                    max_blocks, resident blocks (u64)
+//                    max_blocks, resident blocks (u64), member bit (0: the
+//                    whole owner)
 //   fill[sets], start[sets]                      u32 each
-//   ord[sets * C], tag[sets * C]                 u32, per set from start[s]:
-//                                                local slots in LRU order and
-//                                                their blocks
+//   ord[sets * C], tag[sets * C], own[sets * C]  u32, per set from start[s]:
+//                                                local slots in LRU order,
+//                                                their blocks and member masks
 //   scales[sets * C][2]                          fp32 (fp8 KV only)
 //   data[sets * C][block_bytes]                  from a 256-byte boundary:
 //                                                resident blocks, compacted
@@ -37,6 +38,7 @@ constexpr uint32_t kImageMagic = 0x4E574F46u;  // "FOWN"
 struct ImageHeader {
   uint32_t magic, sets, slots, bb, dtype, max_blocks;
   unsigned long long resident;
+  uint32_t member_bit;  // 0: the whole owner; else the member whose exclusive blocks it holds
 };
 
 __device__ inline ImageLayout image_layout(const Geo& g) { return make_image_layout(g); }
@@ -72,6 +74,7 @@ __device__ inline void clear_set(const Geo& g, SetState st, size_t set, int lane
   for (uint32_t i = lane; i < C; i += kWave) {
     tag[i] = kNone;
     ord[i] = kNone;
+    if (st.own) st.own[set * C + i] = 0u;
   }
   if (lane == 0) st.fill[set] = 0;
   wave_fence();
@@ -84,7 +87,9 @@ __device__ inline void clear_set(const Geo& g, SetState st, size_t set, int lane
 // consecutive sets; the runs' totals are scanned across the workgroup
 // (wavefront shuffles, then the 4 wavefront totals through LDS).
 __global__ __launch_bounds__(256) void k_owner_export_meta(Geo g, SetState st, uint32_t owner,
-                                                           uint8_t* __restrict__ image) {
+                                                           uint8_t* __restrict__ image,
+                                                           const uint32_t* counts,
+                                                           uint32_t member_bit) {
   const ImageLayout lay = image_layout(g);
   const uint32_t S = (uint32_t)(g.L * g.Hkv);
   uint32_t* fill = reinterpret_cast<uint32_t*>(image + lay.fill);
@@ -94,7 +99,7 @@ __global__ __launch_bounds__(256) void k_owner_export_meta(Geo g, SetState st, u
   const uint32_t per = (S + 255) / 256, s0 = min(S, t * per), s1 = min(S, s0 + per);
   unsigned long long run = 0;
   for (uint32_t s = s0; s < s1; ++s) {
-    const uint32_t f = st.fill[(size_t)owner * S + s];
+    const uint32_t f = counts ? counts[s] : st.fill[(size_t)owner * S + s];
     fill[s] = f;
     run += f;
   }
@@ -120,6 +125,7 @@ __global__ __launch_bounds__(256) void k_owner_export_meta(Geo g, SetState st, u
     h->dtype = (uint32_t)g.dtype;
     h->max_blocks = (uint32_t)g.max_blocks;
     h->resident = acc;
+    h->member_bit = member_bit;
   }
 }
 
@@ -147,6 +153,7 @@ __global__ __launch_bounds__(256) void k_owner_export_data(Geo g, SetState st, u
   if (lane == 0) {
     reinterpret_cast<uint32_t*>(image + lay.ord)[pos] = slot;
     reinterpret_cast<uint32_t*>(image + lay.tag)[pos] = st.tag[gslot];
+    reinterpret_cast<uint32_t*>(image + lay.own)[pos] = st.own ? st.own[gslot] : 0u;
     if (pool_scales) {
       reinterpret_cast<float*>(image + lay.scales)[2 * pos] = pool_scales[2 * gslot];
       reinterpret_cast<float*>(image + lay.scales)[2 * pos + 1] = pool_scales[2 * gslot + 1];
@@ -176,7 +183,8 @@ __global__ __launch_bounds__(256) void k_owner_import_meta(Geo g, SetState st, u
   clear_set(g, st, set, lane);
   const bool hdr_ok = h->magic == kImageMagic && h->sets == S && h->slots == C &&
                       h->bb == (uint32_t)g.bb && h->dtype == (uint32_t)g.dtype &&
-                      h->max_blocks == (uint32_t)g.max_blocks && h->resident <= (unsigned long long)S * C;
+                      h->max_blocks == (uint32_t)g.max_blocks && h->member_bit == 0u &&
+                      h->resident <= (unsigned long long)S * C;
   const uint32_t f = hdr_ok ? fill[s] : 0, p0 = hdr_ok ? start[s] : 0;
   bool bad = !hdr_ok || f > C || (unsigned long long)p0 + f > h->resident;
   for (uint32_t i = lane; i < f && !bad; i += kWave)
@@ -188,11 +196,13 @@ __global__ __launch_bounds__(256) void k_owner_import_meta(Geo g, SetState st, u
   uint32_t* map = st.map + set * (size_t)g.max_blocks;
   uint32_t* tag = st.tag + set * C;
   uint32_t* ord = st.ord + set * C;
+  const uint32_t* iown = reinterpret_cast<const uint32_t*>(image + lay.own);
   for (uint32_t i = lane; i < f; i += kWave) {
     const uint32_t slot = iord[p0 + i], b = itag[p0 + i];
     ord[i] = slot;
     astore(tag + slot, b);
     astore(map + b, slot);
+    if (st.own) st.own[set * C + slot] = iown[p0 + i];
   }
   wave_fence();
   // The order must be a permutation of [0, f) with distinct blocks: a repeated
@@ -238,6 +248,142 @@ __global__ __launch_bounds__(256) void k_owner_import_data(Geo g, SetState st, u
   copy_block<NV>(image + lay.data + pos * g.bb, pool + gslot * g.bb, lane);
 }
 
+// ---- member carry (kv_handoff_owned, src/runtime/wla_multigpu.cuh:1901-1921) ----
+// One wavefront per set of the owner: how many resident blocks only member
+// `bit` touched (own == bit) -> the image's fill[set].
+__global__ __launch_bounds__(256) void k_member_export_count(Geo g, SetState st, uint32_t owner,
+                                                             uint32_t bit, uint8_t* __restrict__ image) {
+  const ImageLayout lay = image_layout(g);
+  const uint32_t S = (uint32_t)(g.L * g.Hkv), C = (uint32_t)g.C;
+  const uint32_t s = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (s >= S) return;
+  const size_t set = (size_t)owner * S + s;
+  const uint32_t f = st.fill[set];
+  uint32_t n = 0;
+  for (uint32_t c = 0; c < f; c += kWave) {
+    const uint32_t i = c + lane;
+    n += (uint32_t)__builtin_popcountll(ballot(i < f && st.own[set * C + st.ord[set * C + i]] == bit));
+  }
+  if (lane == 0) reinterpret_cast<uint32_t*>(image + lay.fill)[s] = n;
+}
+
+// One wavefront per set: the member's exclusive blocks in LRU order, each
+// written at start[set] + its rank (slot, tag, mask, fp8 scales, data).
+template <int NV>
+__global__ __launch_bounds__(256) void k_member_export_data(Geo g, SetState st, uint32_t owner,
+                                                            uint32_t bit,
+                                                            const uint8_t* __restrict__ pool,
+                                                            const float* __restrict__ pool_scales,
+                                                            uint8_t* __restrict__ image) {
+  const ImageLayout lay = image_layout(g);
+  const uint32_t S = (uint32_t)(g.L * g.Hkv), C = (uint32_t)g.C;
+  const uint32_t s = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (s >= S) return;
+  const size_t set = (size_t)owner * S + s;
+  const uint32_t f = st.fill[set];
+  size_t pos = reinterpret_cast<const uint32_t*>(image + lay.start)[s];
+  for (uint32_t c = 0; c < f; c += kWave) {
+    const uint32_t i = c + lane;
+    const uint32_t slot = i < f ? st.ord[set * C + i] : 0u;
+    uint64_t mask = ballot(i < f && st.own[set * C + slot] == bit);
+    while (mask) {  // wavefront-uniform: one block at a time, all lanes copy
+      const int b = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      const uint32_t v = (uint32_t)__shfl((int)slot, b);
+      const size_t gslot = set * C + v;
+      if (lane == 0) {
+        reinterpret_cast<uint32_t*>(image + lay.ord)[pos] = v;
+        reinterpret_cast<uint32_t*>(image + lay.tag)[pos] = st.tag[gslot];
+        reinterpret_cast<uint32_t*>(image + lay.own)[pos] = bit;
+        if (pool_scales) {
+          reinterpret_cast<float*>(image + lay.scales)[2 * pos] = pool_scales[2 * gslot];
+          reinterpret_cast<float*>(image + lay.scales)[2 * pos + 1] = pool_scales[2 * gslot + 1];
+        }
+      }
+      copy_block<NV>(pool + gslot * g.bb, image + lay.data + pos * g.bb, lane);
+      ++pos;
+    }
+  }
+}
+
+// One wavefront per set of the importing owner merges the image's blocks in
+// their order: a block already resident gains the member's bit and keeps its
+// place; another becomes the most recent, taking the least recent block's
+// slot when the set holds its capacity, else slot fill (resident slots stay
+// [0, fill)).  The set's order is kept in LDS (2 C words: evictions advance
+// its head).  A mismatching image, a count above C, a block id out of range or
+// a set already above its capacity latch FERRY_EINVAL and stop that set.
+template <int NV>
+__global__ __launch_bounds__(64) void k_member_import(Geo g, SetState st, uint32_t owner, uint32_t bit,
+                                                      uint8_t* __restrict__ pool,
+                                                      float* __restrict__ pool_scales,
+                                                      const uint8_t* __restrict__ image,
+                                                      int* __restrict__ err) {
+  extern __shared__ uint32_t lds[];  // [2 C]
+  const ImageLayout lay = image_layout(g);
+  const uint32_t S = (uint32_t)(g.L * g.Hkv), C = (uint32_t)g.C;
+  const uint32_t s = blockIdx.x;
+  const int lane = threadIdx.x;
+  const ImageHeader* h = reinterpret_cast<const ImageHeader*>(image);
+  const size_t set = (size_t)owner * S + s;
+  const uint32_t cap = set_capacity(g, st.members[owner]);
+  uint32_t fill = st.fill[set];
+  const bool hdr_ok = h->magic == kImageMagic && h->sets == S && h->slots == C &&
+                      h->bb == (uint32_t)g.bb && h->dtype == (uint32_t)g.dtype &&
+                      h->max_blocks == (uint32_t)g.max_blocks && h->member_bit != 0u;
+  const uint32_t n = hdr_ok ? reinterpret_cast<const uint32_t*>(image + lay.fill)[s] : 0u;
+  const size_t p0 = hdr_ok ? reinterpret_cast<const uint32_t*>(image + lay.start)[s] : 0u;
+  if (!hdr_ok || n > C || fill > cap || p0 + n > h->resident) {
+    if (lane == 0) set_error(err, FERRY_EINVAL);
+    return;
+  }
+  const uint32_t* itag = reinterpret_cast<const uint32_t*>(image + lay.tag);
+  uint32_t* map = st.map + set * (size_t)g.max_blocks;
+  uint32_t* tag = st.tag + set * C;
+  uint32_t* ord = st.ord + set * C;
+  uint32_t* own = st.own + set * C;
+  for (uint32_t i = lane; i < fill; i += kWave) lds[i] = ord[i];
+  __builtin_amdgcn_wave_barrier();
+  uint32_t head = 0;
+  for (uint32_t j = 0; j < n; ++j) {  // wavefront-uniform
+    const uint32_t x = itag[p0 + j];
+    if (x >= (uint32_t)g.max_blocks) {
+      if (lane == 0) set_error(err, FERRY_EINVAL);
+      break;
+    }
+    const uint32_t r = aload(map + x);
+    if (r < C) {  // already resident: only the member's bit
+      if (lane == 0) own[r] |= bit;
+      continue;
+    }
+    uint32_t v = fill;
+    if (fill >= cap) {  // the least recent block leaves; its slot takes the new one
+      v = lds[head++];
+      if (lane == 0) astore(map + tag[v], kNone);
+      --fill;
+    }
+    if (lane == 0) {
+      tag[v] = x;
+      astore(map + x, v);
+      own[v] = bit;
+      lds[head + fill] = v;
+      if (pool_scales) {
+        pool_scales[2 * (set * C + v)] = reinterpret_cast<const float*>(image + lay.scales)[2 * (p0 + j)];
+        pool_scales[2 * (set * C + v) + 1] =
+            reinterpret_cast<const float*>(image + lay.scales)[2 * (p0 + j) + 1];
+      }
+    }
+    ++fill;
+    wave_fence();
+    copy_block<NV>(image + lay.data + (p0 + j) * g.bb, pool + (set * C + v) * g.bb, lane);
+  }
+  __builtin_amdgcn_wave_barrier();
+  for (uint32_t i = lane; i < C; i += kWave) ord[i] = i < fill ? lds[head + i] : kNone;
+  if (lane == 0) st.fill[set] = fill;
+}
+
 #define FERRY_HANDOFF_INST(NV)                                                                    \
   template __global__ void k_owner_export_data<NV>(Geo, SetState, uint32_t, const uint8_t*,       \
                                                    const float*, uint8_t*);                        \
@@ -246,5 +392,14 @@ __global__ __launch_bounds__(256) void k_owner_import_data(Geo g, SetState st, u
 FERRY_HANDOFF_INST(4)
 FERRY_HANDOFF_INST(8)
 FERRY_HANDOFF_INST(16)
+
+#define FERRY_MEMBER_INST(NV)                                                                      \
+  template __global__ void k_member_export_data<NV>(Geo, SetState, uint32_t, uint32_t,             \
+                                                    const uint8_t*, const float*, uint8_t*);        \
+  template __global__ void k_member_import<NV>(Geo, SetState, uint32_t, uint32_t, uint8_t*, float*, \
+                                               const uint8_t*, int*);
+FERRY_MEMBER_INST(4)
+FERRY_MEMBER_INST(8)
+FERRY_MEMBER_INST(16)
 
 }  // namespace ferry_amd

@@ -12,7 +12,15 @@ struct SetState {
   uint32_t* tag;      // [n_sets][C] block held by each slot (kNone if free)
   uint32_t* map;      // [n_sets][max_blocks] slot holding each block (kNone)
   uint32_t* members;  // [n_owners] resident member lanes of each owner
+  uint32_t* own;      // [n_sets][C] members that touched each slot's block since it
+                      // was loaded (bit m = member m); prefix groups only, else null
 };
+
+// LDS words of one bookkeeping wavefront: lastpos, order, tags, the step's
+// misses and victims, and the member masks when the owner is a group.
+__host__ __device__ inline size_t lru_lds_words(const Geo& g) {
+  return (size_t)(3 + (g.group > 1 ? 1 : 0)) * g.C + 2 * (size_t)g.max_sel;
+}
 
 // Blocks an owner's sets may hold: C, or under FERRY_CAP_PER_MEMBER one
 // member's share per resident member, at least one share (wla_group_cap,
@@ -80,8 +88,8 @@ __global__ void k_members_update(Geo g, uint32_t* lane_live, uint32_t* members, 
 // Trim the sets of owners marked with `gen` to their capacity (one wavefront
 // per set, C words of LDS); NV 16-byte words per lane per block moved.
 template <int NV>
-__global__ void k_sets_trim(Geo g, SetState st, const uint32_t* trim_gen, uint32_t gen, uint8_t* pool,
-                            float* pool_scales);
+__global__ void k_sets_trim(Geo g, SetState st, const uint32_t* lane_live, const uint32_t* trim_gen,
+                            uint32_t gen, uint8_t* pool, float* pool_scales);
 
 template <int NV>
 __global__ void k_fetch(FetchArgs a);
@@ -116,10 +124,10 @@ __global__ void k_hosttier_fill(Geo g, uint8_t* host, float* scales, uint64_t se
                                 float mult8, float scale_base);
 
 // Byte offsets of an owner image (handoff.hip): header, fill[S], start[S],
-// ord[S*C], tag[S*C], scales[S*C][2] (fp8 only), then the data from a
+// ord[S*C], tag[S*C], own[S*C], scales[S*C][2] (fp8 only), then the data from a
 // 256-byte boundary, S = L * Hkv sets of C slots.
 struct ImageLayout {
-  uint64_t fill, start, ord, tag, scales, data, bytes;
+  uint64_t fill, start, ord, tag, own, scales, data, bytes;
 };
 __host__ __device__ inline ImageLayout make_image_layout(const Geo& g) {
   const uint64_t S = (uint64_t)g.L * (uint64_t)g.Hkv, N = S * (uint64_t)g.C;
@@ -128,13 +136,26 @@ __host__ __device__ inline ImageLayout make_image_layout(const Geo& g) {
   l.start = l.fill + 4 * S;
   l.ord = l.start + 4 * S;
   l.tag = l.ord + 4 * N;
-  l.scales = l.tag + 4 * N;
+  l.own = l.tag + 4 * N;
+  l.scales = l.own + 4 * N;
   const uint64_t sc = g.dtype == FERRY_FP8_E4M3 ? 8 * N : 0;
   l.data = (l.scales + sc + 255) / 256 * 256;
   l.bytes = l.data + N * g.bb;
   return l;
 }
-__global__ void k_owner_export_meta(Geo g, SetState st, uint32_t owner, uint8_t* image);
+// counts: the blocks each set exports (null: its fill); member_bit 0 for a
+// whole-owner image, else the one member whose exclusive blocks it carries.
+__global__ void k_owner_export_meta(Geo g, SetState st, uint32_t owner, uint8_t* image,
+                                    const uint32_t* counts, uint32_t member_bit);
+// Member carry: per set, the resident blocks only that member touched.
+__global__ void k_member_export_count(Geo g, SetState st, uint32_t owner, uint32_t bit,
+                                      uint8_t* image);
+template <int NV>
+__global__ void k_member_export_data(Geo g, SetState st, uint32_t owner, uint32_t bit,
+                                     const uint8_t* pool, const float* pool_scales, uint8_t* image);
+template <int NV>
+__global__ void k_member_import(Geo g, SetState st, uint32_t owner, uint32_t bit, uint8_t* pool,
+                                float* pool_scales, const uint8_t* image, int* err);
 template <int NV>
 __global__ void k_owner_export_data(Geo g, SetState st, uint32_t owner, const uint8_t* pool,
                                     const float* pool_scales, uint8_t* image);

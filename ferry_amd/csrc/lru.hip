@@ -40,7 +40,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
                        uint8_t* __restrict__ miss_flag, uint32_t* __restrict__ map,
                        int* lastpos, uint32_t* sord, uint32_t* stag, uint32_t* smblk,
                        uint32_t* svict, uint32_t& fill, ferry_miss* __restrict__ mo,
-                       const Ring& ring, uint32_t worker, uint32_t cap) {
+                       const Ring& ring, uint32_t worker, uint32_t cap, uint32_t* sown) {
   const int lane = lane_id();
   const int C = g.C;
   const int pend = p0 + cnt;
@@ -123,6 +123,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
       if (ev < (uint32_t)g.max_blocks) astore(map + ev, kNone);
     }
     stag[v] = x;
+    if (sown) sown[v] = 0u;  // a new block: the slot's old members are dropped
     astore(map + x, v);
     ferry_miss m;
     m.block = x;
@@ -145,6 +146,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
         const uint32_t v = aload(map + x);
         slots_out[gi] = set * (uint32_t)C + v;
         atomicMax(lastpos + v, p);
+        if (sown) atomicOr(sown + v, 1u << (uint32_t)(p / g.k));  // member of position p
       }
     }
   }
@@ -208,12 +210,13 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   if (idx >= g.n_owners * nl * g.Hkv) return;  // no workgroup barriers follow
   const int set = ((idx / (nl * g.Hkv)) * g.L + l0 + (idx / g.Hkv) % nl) * g.Hkv + idx % g.Hkv;
   const int C = g.C;
-  uint32_t* base = lds + (size_t)wave * (3 * C + 2 * g.max_sel);
+  uint32_t* base = lds + (size_t)wave * lru_lds_words(g);
   int* lastpos = (int*)base;
   uint32_t* sord = base + C;
   uint32_t* stag = base + 2 * C;
   uint32_t* smblk = base + 3 * C;
   uint32_t* svict = smblk + g.max_sel;
+  uint32_t* sown = st.own ? svict + g.max_sel : nullptr;  // [C] member masks
 
   SetView sv;
   sv.h = set % g.Hkv;
@@ -225,11 +228,13 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   uint32_t* map = st.map + (size_t)set * (size_t)g.max_blocks;
   uint32_t* gord = st.ord + (size_t)set * C;
   uint32_t* gtag = st.tag + (size_t)set * C;
+  uint32_t* gown = st.own ? st.own + (size_t)set * C : nullptr;
   uint32_t fill = st.fill[set];
   for (int i = lane; i < C; i += kWave) {
     lastpos[i] = -1;
     sord[i] = gord[i];
     stag[i] = gtag[i];
+    if (sown) sown[i] = gown[i];
   }
   // range check of every selected id before touching the map
   bool bad = false;
@@ -254,12 +259,12 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   int total = 0, rc = 0;
   if (!SERIAL) {
     rc = substep(g, sv, (uint32_t)set, 0, sv.n, sel, slots_out, miss_flag, map, lastpos, sord, stag,
-                 smblk, svict, fill, mo, ring, worker, cap);
+                 smblk, svict, fill, mo, ring, worker, cap, sown);
     if (rc >= 0) total = rc;
   } else {
     for (int p = 0; p < sv.n; ++p) {
       rc = substep(g, sv, (uint32_t)set, p, 1, sel, slots_out, miss_flag, map, lastpos, sord, stag,
-                   smblk, svict, fill, mo + total, ring, worker, cap);
+                   smblk, svict, fill, mo + total, ring, worker, cap, sown);
       if (rc < 0) break;
       total += rc;
     }
@@ -285,6 +290,7 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   for (int i = lane; i < C; i += kWave) {
     gord[i] = i < (int)fill ? sord[i] : kNone;
     gtag[i] = stag[i];
+    if (sown) gown[i] = sown[i];
   }
   if (lane == 0) {
     st.fill[set] = fill;
@@ -326,6 +332,7 @@ __global__ __launch_bounds__(256) void k_sets_reset_owners(Geo g, SetState st,
     if (b < (uint32_t)g.max_blocks) map[b] = kNone;
     tag[i] = kNone;
     ord[i] = kNone;
+    if (st.own) st.own[set * (size_t)g.C + i] = 0u;
   }
   if (lane == 0) st.fill[set] = 0;
 }
@@ -366,8 +373,9 @@ __global__ void k_members_update(Geo g, uint32_t* lane_live, uint32_t* members, 
 // scales included.  One wavefront per set; pos[C] (the LRU position of each
 // slot) and the movers' list live in LDS.
 template <int NV>
-__global__ __launch_bounds__(64) void k_sets_trim(Geo g, SetState st, const uint32_t* trim_gen,
-                                                  uint32_t gen, uint8_t* __restrict__ pool,
+__global__ __launch_bounds__(64) void k_sets_trim(Geo g, SetState st, const uint32_t* lane_live,
+                                                  const uint32_t* trim_gen, uint32_t gen,
+                                                  uint8_t* __restrict__ pool,
                                                   float* __restrict__ pool_scales) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   extern __shared__ uint32_t lds[];
@@ -377,6 +385,14 @@ __global__ __launch_bounds__(64) void k_sets_trim(Geo g, SetState st, const uint
   if (trim_gen[o] != gen) return;
   const uint32_t C = (uint32_t)g.C;
   const uint32_t fill = st.fill[set];
+  uint32_t* own = st.own ? st.own + (size_t)set * C : nullptr;
+  if (own) {  // own_release: members that left drop out of every mask
+    uint32_t live = 0;
+    for (int m = 0; m < g.group && (int)o * g.group + m < g.n_req; ++m)
+      if (lane_live[o * g.group + m]) live |= 1u << m;
+    for (uint32_t i = lane; i < fill; i += kWave) own[i] &= live;
+    wave_fence();
+  }
   const uint32_t cap = set_capacity(g, st.members[o]);
   if (fill <= cap) return;
   const uint32_t e = fill - cap;
@@ -421,6 +437,7 @@ __global__ __launch_bounds__(64) void k_sets_trim(Geo g, SetState st, const uint
       if (lane == 0) {
         const uint32_t blk = tag[m];
         tag[h] = blk;
+        if (own) own[h] = own[m];
         astore(map + blk, h);
         ord[pos[m]] = h;
       }
@@ -438,13 +455,17 @@ __global__ __launch_bounds__(64) void k_sets_trim(Geo g, SetState st, const uint
   for (uint32_t i = cap + lane; i < C; i += kWave) {
     ord[i] = kNone;
     tag[i] = kNone;
+    if (own) own[i] = 0u;
   }
   if (lane == 0) st.fill[set] = cap;
 }
 
-template __global__ void k_sets_trim<4>(Geo, SetState, const uint32_t*, uint32_t, uint8_t*, float*);
-template __global__ void k_sets_trim<8>(Geo, SetState, const uint32_t*, uint32_t, uint8_t*, float*);
-template __global__ void k_sets_trim<16>(Geo, SetState, const uint32_t*, uint32_t, uint8_t*, float*);
+template __global__ void k_sets_trim<4>(Geo, SetState, const uint32_t*, const uint32_t*, uint32_t,
+                                        uint8_t*, float*);
+template __global__ void k_sets_trim<8>(Geo, SetState, const uint32_t*, const uint32_t*, uint32_t,
+                                        uint8_t*, float*);
+template __global__ void k_sets_trim<16>(Geo, SetState, const uint32_t*, const uint32_t*, uint32_t,
+                                         uint8_t*, float*);
 
 // Reset all sets: empty order, no tags, map cleared.
 __global__ void k_sets_reset(Geo g, SetState st) {
@@ -455,6 +476,7 @@ __global__ void k_sets_reset(Geo g, SetState st) {
   for (size_t i = tid; i < nslots; i += stride) {
     st.ord[i] = kNone;
     st.tag[i] = kNone;
+    if (st.own) st.own[i] = 0u;
   }
   for (size_t i = tid; i < nmap; i += stride) st.map[i] = kNone;
   for (size_t i = tid; i < (size_t)g.n_sets; i += stride) st.fill[i] = 0;

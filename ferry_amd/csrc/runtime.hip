@@ -185,6 +185,7 @@ int validate(const ferry_config* c) {
     return fail(FERRY_EINVAL, "bad cap_mode");
   if (c->cap_mode == FERRY_CAP_PER_MEMBER && c->slots_per_set % c->group)
     return fail(FERRY_EINVAL, "per-member capacity needs slots_per_set to be a multiple of group");
+  if (c->group > 32) return fail(FERRY_EINVAL, "group must be <= 32 (one mask bit per member)");
   if ((uint64_t)c->max_blocks >= (uint64_t)kPend) return fail(FERRY_EINVAL, "max_blocks too large");
   return FERRY_OK;
 }
@@ -199,7 +200,7 @@ void release(ferry_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   void* dev[] = {c->pool, c->pool_scales, c->st.fill, c->st.ord, c->st.tag, c->st.map,
-                 c->st.members, c->lane_live, c->trim_gen,
+                 c->st.members, c->st.own, c->lane_live, c->trim_gen,
                  c->ring_entries, c->ring_state, c->ring_entries2, c->ring_state2,
                  c->ring_seg, c->ring_cap, c->worker_of_set,
                  c->stats, c->sel_counts, c->step_acc, c->done, c->err, c->probe_sink,
@@ -470,7 +471,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
     return fail(FERRY_EINVAL, "too many slots or selections for 32-bit ids");
   }
   // bookkeeping launch shape: waves per workgroup bounded by 64 KiB of LDS
-  const size_t per_wave = (size_t)(3 * g.C + 2 * g.max_sel) * 4;
+  const size_t per_wave = lru_lds_words(g) * 4;
   if (per_wave > 65536) {
     delete c;
     return fail(FERRY_EINVAL, "slots_per_set/group*k too large for the bookkeeping LDS budget");
@@ -495,6 +496,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   TRY(dalloc(&c->st.tag, nslots));
   TRY(dalloc(&c->st.map, (size_t)g.n_sets * g.max_blocks));
   TRY(dalloc(&c->st.members, g.n_owners));
+  if (g.group > 1) TRY(dalloc(&c->st.own, nslots));
   TRY(dalloc(&c->lane_live, g.n_req));
   TRY(dalloc(&c->trim_gen, g.n_owners));
   // ring: worker segments sized for every miss their sets can produce
@@ -705,6 +707,16 @@ int ferry_sets_state(ferry_ctx* ctx, uint32_t* fill, uint32_t* ord, uint32_t* ta
   return FERRY_OK;
 }
 
+int ferry_sets_own(ferry_ctx* ctx, uint32_t* own) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!own) return fail(FERRY_EINVAL, "null out");
+  if (!ctx->st.own) return fail(FERRY_EINVAL, "member masks exist only for prefix groups (group > 1)");
+  HIPC(hipSetDevice(ctx->device));
+  HIPC(hipDeviceSynchronize());
+  HIPC(hipMemcpy(own, ctx->st.own, (size_t)ctx->g.n_sets * ctx->g.C * 4, hipMemcpyDeviceToHost));
+  return FERRY_OK;
+}
+
 }  // extern "C"
 
 namespace {
@@ -720,13 +732,13 @@ int members_update(ferry_ctx* ctx, const uint32_t* lanes, uint32_t n, int delta,
   hipLaunchKernelGGL(k_members_update, dim3((n + 255) / 256), dim3(256), 0, s, g, ctx->lane_live,
                      ctx->st.members, ctx->trim_gen, lanes, n, delta, gen, ctx->err);
   HIPC(hipGetLastError());
-  if (delta < 0 && g.cap_mode == FERRY_CAP_PER_MEMBER) {
+  if (delta < 0 && (g.cap_mode == FERRY_CAP_PER_MEMBER || g.group > 1)) {
     const size_t lds = (size_t)2 * g.C * 4;
     const dim3 grid((unsigned)g.n_sets), block(64);
     switch (g.bb / 1024) {
-      case 4: hipLaunchKernelGGL(k_sets_trim<4>, grid, block, lds, s, g, ctx->st, ctx->trim_gen, gen, ctx->pool, ctx->pool_scales); break;
-      case 8: hipLaunchKernelGGL(k_sets_trim<8>, grid, block, lds, s, g, ctx->st, ctx->trim_gen, gen, ctx->pool, ctx->pool_scales); break;
-      case 16: hipLaunchKernelGGL(k_sets_trim<16>, grid, block, lds, s, g, ctx->st, ctx->trim_gen, gen, ctx->pool, ctx->pool_scales); break;
+      case 4: hipLaunchKernelGGL(k_sets_trim<4>, grid, block, lds, s, g, ctx->st, ctx->lane_live, ctx->trim_gen, gen, ctx->pool, ctx->pool_scales); break;
+      case 8: hipLaunchKernelGGL(k_sets_trim<8>, grid, block, lds, s, g, ctx->st, ctx->lane_live, ctx->trim_gen, gen, ctx->pool, ctx->pool_scales); break;
+      case 16: hipLaunchKernelGGL(k_sets_trim<16>, grid, block, lds, s, g, ctx->st, ctx->lane_live, ctx->trim_gen, gen, ctx->pool, ctx->pool_scales); break;
       default: return fail(FERRY_EINVAL, "unsupported block size");
     }
     HIPC(hipGetLastError());
@@ -1304,7 +1316,8 @@ int ferry_owner_export(ferry_ctx* ctx, uint32_t owner, void* image, uint64_t ima
   HIPC(hipSetDevice(ctx->device));
   hipStream_t s = (hipStream_t)stream;
   uint8_t* im = (uint8_t*)image;
-  hipLaunchKernelGGL(k_owner_export_meta, dim3(1), dim3(256), 0, s, g, ctx->st, owner, im);
+  hipLaunchKernelGGL(k_owner_export_meta, dim3(1), dim3(256), 0, s, g, ctx->st, owner, im,
+                     (const uint32_t*)nullptr, 0u);
   HIPC(hipGetLastError());
   const uint64_t waves = (uint64_t)g.L * g.Hkv * g.C;
   const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
@@ -1336,6 +1349,66 @@ int ferry_owner_import(ferry_ctx* ctx, uint32_t owner, const void* image, uint64
     case 4: hipLaunchKernelGGL(k_owner_import_data<4>, grid, block, 0, s, g, ctx->st, owner, ctx->pool, ctx->pool_scales, im); break;
     case 8: hipLaunchKernelGGL(k_owner_import_data<8>, grid, block, 0, s, g, ctx->st, owner, ctx->pool, ctx->pool_scales, im); break;
     case 16: hipLaunchKernelGGL(k_owner_import_data<16>, grid, block, 0, s, g, ctx->st, owner, ctx->pool, ctx->pool_scales, im); break;
+    default: return fail(FERRY_EINVAL, "unsupported block size");
+  }
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+int member_check(ferry_ctx* ctx, uint32_t lane, const void* image, uint64_t image_bytes) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!ctx->st.own) return fail(FERRY_EINVAL, "member carry needs prefix groups (group > 1)");
+  if (lane >= (uint32_t)ctx->g.n_req) return fail(FERRY_EINVAL, "lane out of range");
+  return owner_check(ctx, lane / (uint32_t)ctx->g.group, image, image_bytes);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ferry_owner_export_member(ferry_ctx* ctx, uint32_t lane, void* image, uint64_t image_bytes,
+                              void* stream) {
+  if (int rc = member_check(ctx, lane, image, image_bytes)) return rc;
+  const Geo& g = ctx->g;
+  HIPC(hipSetDevice(ctx->device));
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* im = (uint8_t*)image;
+  const uint32_t owner = lane / (uint32_t)g.group, bit = 1u << (lane % (uint32_t)g.group);
+  const unsigned sets = (unsigned)(g.L * g.Hkv);
+  const dim3 grid((sets + 3) / 4), block(256);
+  hipLaunchKernelGGL(k_member_export_count, grid, block, 0, s, g, ctx->st, owner, bit, im);
+  HIPC(hipGetLastError());
+  const uint32_t* counts = (const uint32_t*)(im + make_image_layout(g).fill);
+  hipLaunchKernelGGL(k_owner_export_meta, dim3(1), dim3(256), 0, s, g, ctx->st, owner, im, counts, bit);
+  HIPC(hipGetLastError());
+  switch (g.bb / 1024) {
+    case 4: hipLaunchKernelGGL(k_member_export_data<4>, grid, block, 0, s, g, ctx->st, owner, bit, ctx->pool, ctx->pool_scales, im); break;
+    case 8: hipLaunchKernelGGL(k_member_export_data<8>, grid, block, 0, s, g, ctx->st, owner, bit, ctx->pool, ctx->pool_scales, im); break;
+    case 16: hipLaunchKernelGGL(k_member_export_data<16>, grid, block, 0, s, g, ctx->st, owner, bit, ctx->pool, ctx->pool_scales, im); break;
+    default: return fail(FERRY_EINVAL, "unsupported block size");
+  }
+  HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_owner_import_member(ferry_ctx* ctx, uint32_t lane, const void* image, uint64_t image_bytes,
+                              void* stream) {
+  if (int rc = member_check(ctx, lane, image, image_bytes)) return rc;
+  const Geo& g = ctx->g;
+  HIPC(hipSetDevice(ctx->device));
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t* im = (const uint8_t*)image;
+  const uint32_t owner = lane / (uint32_t)g.group, bit = 1u << (lane % (uint32_t)g.group);
+  const dim3 grid((unsigned)(g.L * g.Hkv)), block(64);
+  const size_t lds = 2 * (size_t)g.C * 4;
+  switch (g.bb / 1024) {
+    case 4: hipLaunchKernelGGL(k_member_import<4>, grid, block, lds, s, g, ctx->st, owner, bit, ctx->pool, ctx->pool_scales, im, ctx->err); break;
+    case 8: hipLaunchKernelGGL(k_member_import<8>, grid, block, lds, s, g, ctx->st, owner, bit, ctx->pool, ctx->pool_scales, im, ctx->err); break;
+    case 16: hipLaunchKernelGGL(k_member_import<16>, grid, block, lds, s, g, ctx->st, owner, bit, ctx->pool, ctx->pool_scales, im, ctx->err); break;
     default: return fail(FERRY_EINVAL, "unsupported block size");
   }
   HIPC(hipGetLastError());

@@ -167,6 +167,13 @@ int ferry_sets_reset_owners(ferry_ctx* ctx, const uint32_t* owners, uint32_t n, 
 /* Copy per-set LRU state to host arrays: fill[n_sets], ord[n_sets][slots]
  * (local slots, LRU first), tag[n_sets][slots] (block per slot). */
 int ferry_sets_state(ferry_ctx* ctx, uint32_t* fill, uint32_t* ord, uint32_t* tag);
+/* Per-slot member masks of prefix groups (group > 1): own[n_sets][slots],
+ * bit m set when member m (lane % group) of the set's owner touched the
+ * slot's block since it became resident and is still resident itself
+ * (cleared when the member leaves; 0 for a free slot).  Replaces the
+ * reference's own_mask table (src/runtime/wla_multigpu.cuh:1871-1912);
+ * synchronises. */
+int ferry_sets_own(ferry_ctx* ctx, uint32_t* own);
 
 /* Resident members of prefix groups.  Every batch lane (request row) is a
  * member of its owner (lane / group) and starts resident.  ferry_members_leave
@@ -384,6 +391,25 @@ int ferry_owner_image_bytes(const ferry_ctx* ctx, uint64_t* bytes);
 int ferry_owner_export(ferry_ctx* ctx, uint32_t owner, void* image, uint64_t image_bytes, void* stream);
 int ferry_owner_import(ferry_ctx* ctx, uint32_t owner, const void* image, uint64_t image_bytes,
                        void* stream);
+/* Member carry for prefix groups (group > 1): moving one request of a group
+ * carries only the blocks that request alone touched.  ferry_owner_export_member
+ * writes an image (same layout and size as above) of the blocks of `lane`'s
+ * owner whose member mask is exactly lane's bit, per set in LRU order, with
+ * their bytes and fp8 scales; blocks other members touched stay where they
+ * are.  ferry_owner_import_member merges such an image into `lane`'s owner of
+ * this (or another) executor: a block already resident gains lane's bit and
+ * keeps its place; another becomes the most recent, taking the least recent
+ * block's slot (which is evicted) when the set holds its capacity, else slot
+ * fill.  Call ferry_members_join for the lane first, so that the capacity
+ * counts it.  A whole-owner image, a geometry mismatch, a malformed image or
+ * a set above its capacity latches FERRY_EINVAL; sets before the failure keep
+ * their merged blocks.  Replaces kv_handoff(carry) with own_carry,
+ * kv_handoff_owned and kv_live_owned (src/runtime/wla_multigpu.cuh:
+ * 1901-1911, 1970-2016). */
+int ferry_owner_export_member(ferry_ctx* ctx, uint32_t lane, void* image, uint64_t image_bytes,
+                              void* stream);
+int ferry_owner_import_member(ferry_ctx* ctx, uint32_t lane, const void* image, uint64_t image_bytes,
+                              void* stream);
 
 /* ---- bandwidth ceilings ----
  * Plain reads of the bytes the executor's kernels move, timed with HIP events

@@ -347,7 +347,8 @@ int ora_lru_init(ora_lru* s, int cap, int max_blocks) {
   s->ord = (uint32_t*)malloc((size_t)cap * 4);
   s->tag = (uint32_t*)malloc((size_t)cap * 4);
   s->map = (uint32_t*)malloc((size_t)max_blocks * 4);
-  if (!s->ord || !s->tag || !s->map) return -1;
+  s->own = (uint32_t*)malloc((size_t)cap * 4);
+  if (!s->ord || !s->tag || !s->map || !s->own) return -1;
   ora_lru_reset(s);
   return 0;
 }
@@ -356,7 +357,8 @@ void ora_lru_free(ora_lru* s) {
   free(s->ord);
   free(s->tag);
   free(s->map);
-  s->ord = s->tag = s->map = NULL;
+  free(s->own);
+  s->ord = s->tag = s->map = s->own = NULL;
 }
 
 void ora_lru_reset(ora_lru* s) {
@@ -364,6 +366,7 @@ void ora_lru_reset(ora_lru* s) {
   for (int i = 0; i < s->cap; ++i) {
     s->ord[i] = ORA_NONE;
     s->tag[i] = ORA_NONE;
+    s->own[i] = 0;
   }
   for (int i = 0; i < s->max_blocks; ++i) s->map[i] = ORA_NONE;
 }
@@ -382,6 +385,11 @@ void ora_lru_reset(ora_lru* s) {
 int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
                     uint32_t* slot_out, ora_miss* miss_out, int* n_miss,
                     uint8_t* flag_out) {
+  return ora_lru_substep_m(s, set, x, NULL, n, slot_out, miss_out, n_miss, flag_out);
+}
+
+int ora_lru_substep_m(ora_lru* s, uint32_t set, const uint32_t* x, const uint8_t* member, int n,
+                      uint32_t* slot_out, ora_miss* miss_out, int* n_miss, uint8_t* flag_out) {
   const int cap = s->cap;
   for (int p = 0; p < n; ++p)
     if (x[p] != ORA_NONE && x[p] >= (uint32_t)s->max_blocks) return -1;
@@ -430,6 +438,7 @@ int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
     }
     s->tag[v] = mblk[q];
     s->map[mblk[q]] = v;
+    s->own[v] = 0; /* a new block: the slot's old members are dropped (own_drop) */
     miss_out[q].block = mblk[q];
     miss_out[q].slot = v;
     miss_out[q].evicted = ev;
@@ -443,6 +452,7 @@ int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
     const uint32_t v = s->map[x[p]];
     slot_out[p] = v;
     lastpos[v] = p;
+    if (member) s->own[v] |= 1u << member[p]; /* own_mask |= own_bit(r) */
   }
   /* phase 5: new LRU order */
   uint32_t w = 0;
@@ -474,6 +484,7 @@ int ora_lru_trim(ora_lru* s, int lim, uint32_t* moves) {
     while (pos[hole] >= e) ++hole; /* next evicted slot below lim */
     const uint32_t blk = s->tag[m];
     s->tag[hole] = blk;
+    s->own[hole] = s->own[m];
     s->map[blk] = hole;
     s->ord[pos[m]] = hole;
     if (moves) {
@@ -487,6 +498,7 @@ int ora_lru_trim(ora_lru* s, int lim, uint32_t* moves) {
   for (int i = lim; i < s->cap; ++i) {
     s->ord[i] = ORA_NONE;
     s->tag[i] = ORA_NONE;
+    s->own[i] = 0;
   }
   s->fill = (uint32_t)lim;
   free(pos);
@@ -665,6 +677,7 @@ struct ora_exec {
   uint8_t* flag;
   uint32_t* members;  /* [n_owners] resident member lanes */
   uint8_t* live;      /* [n_req] lane resident */
+  uint8_t* mem;       /* [max_sel] member index of each position of a set's step */
 };
 
 int ora_capacity(const ora_geom* g, int members) {
@@ -686,6 +699,8 @@ ora_exec* ora_exec_create(const ora_geom* g) {
   e->flag = (uint8_t*)malloc((size_t)ora_max_sel_per_set(g));
   e->members = (uint32_t*)malloc((size_t)ora_n_owners(g) * 4);
   e->live = (uint8_t*)malloc((size_t)g->n_req);
+  e->mem = (uint8_t*)malloc((size_t)ora_max_sel_per_set(g));
+  for (int p = 0; p < ora_max_sel_per_set(g); ++p) e->mem[p] = (uint8_t)(p / g->k);
   for (int o = 0; o < ora_n_owners(g); ++o) e->members[o] = (uint32_t)ora_members(g, o);
   memset(e->live, 1, (size_t)g->n_req);
   return e;
@@ -712,13 +727,74 @@ int ora_exec_members(ora_exec* e, const uint32_t* lanes, int n, int delta) {
       e->members[o]++;
     }
   }
-  if (g->cap_mode == 1)
-    for (int o = 0; o < nown; ++o)
-      if (shrunk[o])
-        for (int i = 0; i < per; ++i)
-          ora_lru_trim(&e->sets[o * per + i], ora_capacity(g, (int)e->members[o]), NULL);
+  for (int o = 0; o < nown; ++o) {
+    if (!shrunk[o]) continue;
+    /* own_release: the members that left drop out of every mask of the owner */
+    uint32_t live = 0;
+    for (int m = 0; m < g->group && o * g->group + m < g->n_req; ++m)
+      if (e->live[o * g->group + m]) live |= 1u << m;
+    for (int i = 0; i < per; ++i) {
+      ora_lru* s = &e->sets[o * per + i];
+      for (uint32_t v = 0; v < s->fill; ++v) s->own[v] &= live;
+      if (g->cap_mode == 1) ora_lru_trim(s, ora_capacity(g, (int)e->members[o]), NULL);
+    }
+  }
   free(shrunk);
   return rc;
+}
+
+void ora_exec_own(const ora_exec* e, uint32_t* own) {
+  const int ns = ora_n_sets(&e->g), cap = e->g.cap;
+  for (int i = 0; i < ns; ++i) memcpy(own + (size_t)i * cap, e->sets[i].own, (size_t)cap * 4);
+}
+
+int ora_exec_export_member(const ora_exec* e, int lane, uint32_t* counts, uint32_t* blocks) {
+  const ora_geom* g = &e->g;
+  if (lane < 0 || lane >= g->n_req) return -1;
+  const int o = lane / g->group, per = g->n_layers * g->kv_heads;
+  const uint32_t bit = 1u << (uint32_t)(lane % g->group);
+  for (int i = 0; i < per; ++i) {
+    const ora_lru* s = &e->sets[o * per + i];
+    uint32_t c = 0;
+    for (uint32_t j = 0; j < s->fill; ++j) {
+      const uint32_t v = s->ord[j];
+      if (s->own[v] == bit) blocks[(size_t)i * g->cap + c++] = s->tag[v];
+    }
+    counts[i] = c;
+  }
+  return 0;
+}
+
+int ora_exec_import_member(ora_exec* e, int lane, const uint32_t* counts, const uint32_t* blocks) {
+  const ora_geom* g = &e->g;
+  if (lane < 0 || lane >= g->n_req) return -1;
+  const int o = lane / g->group, per = g->n_layers * g->kv_heads;
+  const uint32_t bit = 1u << (uint32_t)(lane % g->group);
+  const uint32_t lim = (uint32_t)ora_capacity(g, (int)e->members[o]);
+  for (int i = 0; i < per; ++i) {
+    ora_lru* s = &e->sets[o * per + i];
+    if (counts[i] > (uint32_t)g->cap || s->fill > lim) return -1;
+    for (uint32_t j = 0; j < counts[i]; ++j) {
+      const uint32_t x = blocks[(size_t)i * g->cap + j];
+      if (x >= (uint32_t)g->max_blocks) return -1;
+      if (s->map[x] != ORA_NONE) { /* already here: only the member bit */
+        s->own[s->map[x]] |= bit;
+        continue;
+      }
+      uint32_t v = s->fill;
+      if (s->fill >= lim) { /* evict the least recent; the new block takes its slot */
+        v = s->ord[0];
+        s->map[s->tag[v]] = ORA_NONE;
+        memmove(s->ord, s->ord + 1, (size_t)(s->fill - 1) * 4);
+        s->fill--;
+      }
+      s->tag[v] = x;
+      s->map[x] = v;
+      s->own[v] = bit;
+      s->ord[s->fill++] = v;
+    }
+  }
+  return 0;
 }
 
 void ora_exec_members_get(const ora_exec* e, uint32_t* members) {
@@ -735,6 +811,7 @@ void ora_exec_destroy(ora_exec* e) {
   free(e->flag);
   free(e->members);
   free(e->live);
+  free(e->mem);
   free(e);
 }
 
@@ -759,14 +836,15 @@ int ora_exec_step(ora_exec* e, const uint32_t* sel, uint32_t* slots_out,
         ora_miss* mo = misses + (size_t)set * maxsel;
         int M = 0;
         e->sets[set].lim = ora_capacity(g, (int)e->members[o]);
+        const uint8_t* who = g->group > 1 ? e->mem : NULL; /* member masks for groups */
         if (g->granularity == 0) {
-          const int rc = ora_lru_substep(&e->sets[set], set, e->x, n, e->slot, mo, &M, e->flag);
+          const int rc = ora_lru_substep_m(&e->sets[set], set, e->x, who, n, e->slot, mo, &M, e->flag);
           if (rc) return rc;
         } else {
           for (int p = 0; p < n; ++p) {
             int m1 = 0;
-            const int rc = ora_lru_substep(&e->sets[set], set, e->x + p, 1,
-                                           e->slot + p, mo + M, &m1, e->flag + p);
+            const int rc = ora_lru_substep_m(&e->sets[set], set, e->x + p, who ? who + p : NULL, 1,
+                                             e->slot + p, mo + M, &m1, e->flag + p);
             if (rc) return rc;
             M += m1;
           }
@@ -820,6 +898,7 @@ int ora_exec_copy_owner(const ora_exec* src, int src_owner, ora_exec* dst, int d
     d->fill = s->fill;
     memcpy(d->ord, s->ord, (size_t)s->cap * 4);
     memcpy(d->tag, s->tag, (size_t)s->cap * 4);
+    memcpy(d->own, s->own, (size_t)s->cap * 4);
     memcpy(d->map, s->map, (size_t)s->max_blocks * 4);
   }
   return 0;

@@ -104,6 +104,8 @@ typedef struct {
   uint32_t* ord;   /* [cap] local slots, LRU first; first `fill` valid */
   uint32_t* tag;   /* [cap] block id per slot (ORA_NONE when free) */
   uint32_t* map;   /* [max_blocks] local slot per block (ORA_NONE) */
+  uint32_t* own;   /* [cap] members that touched each slot's block since it was loaded
+                      (bit m = member m of the owner); own_mask, wla_multigpu.cuh:1871-1921 */
 } ora_lru;
 
 int ora_lru_init(ora_lru* s, int cap, int max_blocks);
@@ -117,6 +119,11 @@ void ora_lru_reset(ora_lru* s);
 int ora_lru_substep(ora_lru* s, uint32_t set, const uint32_t* x, int n,
                     uint32_t* slot_out, ora_miss* miss_out, int* n_miss,
                     uint8_t* flag_out);
+/* The same, with member[p] the member (bit index) of position p: every
+ * selected slot's mask gains its members' bits, and a newly loaded slot's
+ * mask starts empty (NULL: masks untouched). */
+int ora_lru_substep_m(ora_lru* s, uint32_t set, const uint32_t* x, const uint8_t* member, int n,
+                      uint32_t* slot_out, ora_miss* miss_out, int* n_miss, uint8_t* flag_out);
 
 /* Trim a set to `lim` blocks (grp_trim, wla_multigpu.cuh:1923-1936): the
  * fill - lim least recently used blocks are evicted, the survivors keep their
@@ -191,9 +198,23 @@ int ora_exec_step(ora_exec* e, const uint32_t* sel, uint32_t* slots_out,
                   uint8_t* flags);
 /* Empty the sets of one owner (a new request takes over its lane). */
 int ora_exec_reset_owner(ora_exec* e, int owner);
+/* Per-slot member masks of every set: own[n_sets][cap]. */
+void ora_exec_own(const ora_exec* e, uint32_t* own);
+/* Per-request carry of a member (kv_handoff_owned, wla_multigpu.cuh:1901-1921):
+ * ora_exec_export_member lists, per set of lane's owner, the resident blocks
+ * only lane's member touched (own == its bit), least recently used first:
+ * counts[L*Hkv] and blocks[L*Hkv][cap].  ora_exec_import_member merges such a
+ * list into `lane`'s owner of `dst`: a block already resident gains the lane's
+ * member bit and keeps its place; another is appended as most recent after
+ * evicting the least recent block while the set holds its capacity or more,
+ * the new block taking the evicted slot (else slot fill).  Returns 0 or -1. */
+int ora_exec_export_member(const ora_exec* e, int lane, uint32_t* counts, uint32_t* blocks);
+int ora_exec_import_member(ora_exec* e, int lane, const uint32_t* counts, const uint32_t* blocks);
 /* Resident members (every lane starts resident): the requests of lanes[0..n)
- * leave (delta -1) or join (+1) their owners; leaving owners are trimmed to
- * their new capacity under cap_mode 1 (ora_lru_trim).  A lane out of range,
+ * leave (delta -1) or join (+1) their owners; a leaving member's bit is
+ * cleared from every slot of its owner (own_release, wla_multigpu.cuh:
+ * 1896-1909) and the owner is trimmed to its new capacity under cap_mode 1
+ * (ora_lru_trim).  A lane out of range,
  * leaving while not resident or joining while resident is skipped and makes
  * the call return -1.  ora_exec_members_get copies the per-owner counts. */
 int ora_exec_members(ora_exec* e, const uint32_t* lanes, int n, int delta);

@@ -72,7 +72,7 @@ class MT64(C.Structure):
 class LRU(C.Structure):
     _fields_ = [("cap", C.c_int), ("lim", C.c_int), ("max_blocks", C.c_int), ("fill", C.c_uint32),
                 ("ord", C.POINTER(C.c_uint32)), ("tag", C.POINTER(C.c_uint32)),
-                ("map", C.POINTER(C.c_uint32))]
+                ("map", C.POINTER(C.c_uint32)), ("own", C.POINTER(C.c_uint32))]
 
 
 class TSLRU(C.Structure):
@@ -110,6 +110,9 @@ _sig("ora_deque_lru_run_caps", C.c_int, _i32p, _i32p, _u32p, C.c_int, _u8p, _u32
 _sig("ora_lru_trim", C.c_int, C.POINTER(LRU), C.c_int, C.c_void_p)
 _sig("ora_exec_members", C.c_int, C.c_void_p, _u32p, C.c_int, C.c_int)
 _sig("ora_exec_members_get", None, C.c_void_p, _u32p)
+_sig("ora_exec_own", None, C.c_void_p, _u32p)
+_sig("ora_exec_export_member", C.c_int, C.c_void_p, C.c_int, _u32p, _u32p)
+_sig("ora_exec_import_member", C.c_int, C.c_void_p, C.c_int, _u32p, _u32p)
 _sig("ora_capacity", C.c_int, C.POINTER(Geom), C.c_int)
 _sig("ora_tslru_init", C.c_int, C.POINTER(TSLRU), C.c_int, C.c_int)
 _sig("ora_tslru_free", None, C.POINTER(TSLRU))
@@ -228,6 +231,27 @@ class Executor:
         out = np.zeros((self.g.n_req + self.g.group - 1) // self.g.group, np.uint32)
         lib.ora_exec_members_get(self.ptr, out)
         return out
+
+    def own(self):
+        """Member masks [n_sets, cap] (bit m: member m touched the slot's block)."""
+        out = np.zeros(self.n_sets * self.g.cap, np.uint32)
+        lib.ora_exec_own(self.ptr, out)
+        return out.reshape(self.n_sets, self.g.cap)
+
+    def export_member(self, lane):
+        """Blocks only lane's member touched, per set of its owner, LRU first:
+        (counts [L*Hkv], blocks [L*Hkv, cap])."""
+        per = self.g.n_layers * self.g.kv_heads
+        counts = np.zeros(per, np.uint32)
+        blocks = np.zeros(per * self.g.cap, np.uint32)
+        if lib.ora_exec_export_member(self.ptr, lane, counts, blocks):
+            raise ValueError(f"lane {lane}")
+        return counts, blocks.reshape(per, self.g.cap)
+
+    def import_member(self, lane, counts, blocks):
+        if lib.ora_exec_import_member(self.ptr, lane, np.ascontiguousarray(counts, np.uint32),
+                                      np.ascontiguousarray(blocks, np.uint32).reshape(-1)):
+            raise ValueError("import_member refused")
 
     def state(self):
         cap = self.g.cap

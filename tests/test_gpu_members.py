@@ -11,7 +11,9 @@ With per-member capacity (MissSpec::cap_mode 1, src/workloads/missstream.cuh:
 into lower slots.  Every tick the slots, miss lists and flags must equal the
 oracle's bit for bit, the LRU state and member counts after every change, the
 bytes (and fp8 scales) of every resident slot the host tier's, and attention
-within the dtype's tolerance of the float64 oracle."""
+within the dtype's tolerance of the float64 oracle.  The member masks (own_mask,
+src/runtime/wla_multigpu.cuh:1871-1912) must equal the oracle's too, and a
+request moved between executors carries only the blocks it alone touched."""
 import numpy as np
 import pytest
 import torch
@@ -81,6 +83,10 @@ class GroupPair:
         for s in range(len(fill)):
             assert np.array_equal(ord_[s, :fill[s]], oord[s, :fill[s]])
         assert np.array_equal(self.ex.members(), self.ox.members())
+        # member masks of the resident slots (own_mask after touches, releases and moves)
+        own, oown = self.ex.sets_own(), self.ox.own()
+        live = np.arange(self.C)[None, :] < fill[:, None]
+        assert np.array_equal(own[live], oown[live])
         # every resident slot holds its block's bytes (moved ones included)
         sets = np.repeat(np.arange(len(fill)), fill)
         loc = np.concatenate([np.arange(f) for f in fill]) if fill.sum() else np.zeros(0, int)
@@ -180,6 +186,140 @@ def test_prefix_groups_turn_over_under_arrivals(kind, dtype, cap_mode):
     if cap_mode == F.CAP_PER_MEMBER:
         assert trims > 0
     print(f"[members] {steps} steps, {joins} joins, {leaves} leaves, {trims} trims", flush=True)
+
+
+def _image_layout(S, C, dtype):
+    """Byte offsets of an owner image: header, fill[S], start[S], ord, tag and
+    own [S*C] u32, fp8 scales [S*C][2], data from a 256-byte boundary."""
+    N = S * C
+    lay = dict(fill=64)
+    lay["start"] = lay["fill"] + 4 * S
+    lay["ord"] = lay["start"] + 4 * S
+    lay["tag"] = lay["ord"] + 4 * N
+    lay["own"] = lay["tag"] + 4 * N
+    lay["scales"] = lay["own"] + 4 * N
+    lay["data"] = (lay["scales"] + (8 * N if dtype == F.FP8 else 0) + 255) // 256 * 256
+    return lay
+
+
+def _u32_at(im, off, n):
+    return im[off:off + 4 * n].view(np.uint32)
+
+
+@pytest.mark.parametrize("dtype,cap_mode", [(F.FP8, F.CAP_PER_MEMBER), (F.BF16, F.CAP_GROUP)])
+def test_member_carry_between_executors(dtype, cap_mode):
+    """One request of a prefix group moves from executor A to B, carrying only
+    the blocks it alone touched (kv_handoff_owned, src/runtime/wla_multigpu.cuh:
+    1996-2016): the image must list the oracle's exclusive blocks in LRU order
+    with the host tier's bytes; after leave on A and join + merge on B both
+    executors' sets, member masks and pool bytes equal the oracle's, and four
+    more steps (the request now in B) stay bit-exact."""
+    lanes, grp, L, Hkv, Hq, k, share, pre = 8, 4, 2, 2, 8, 16, 24, 48
+    mv = 1  # lane of owner 0, member bit 1 << 1
+    S = L * Hkv
+    print(f"[member carry] dtype={dtype} cap_mode={cap_mode} lane={mv}", flush=True)
+    ctx = np.full(lanes, 80 + pre, np.int32)
+    sga = F.SelGen(lanes, L, Hkv, k, ctx, group=grp, prefix_blocks=pre, seed=4)
+    sgb = F.SelGen(lanes, L, Hkv, k, ctx, group=grp, prefix_blocks=pre, seed=9)
+    assert sga.max_blocks == sgb.max_blocks
+    mb = sga.max_blocks
+    A = GroupPair(lanes, grp, L, Hkv, Hq, k, share, mb, dtype, cap_mode)
+    B = GroupPair(lanes, grp, L, Hkv, Hq, k, share, mb, dtype, cap_mode)
+    B.leave([mv])  # the lane is free on B until the request arrives
+    shape = (lanes, L, Hkv, k)
+    for t in range(6):
+        A.step(sga.step(t).reshape(-1))
+        sb = sgb.step(t).reshape(shape).copy()
+        sb[mv] = NONE
+        B.step(sb.reshape(-1))
+    A.check_state()
+    B.check_state()
+    img = A.ex.alloc_owner_image()
+    A.ex.owner_export_member(mv, img)
+    counts, blocks = A.ox.export_member(mv)
+    torch.cuda.synchronize()
+    assert A.ex.stats()["device_error"] == 0
+    im = img.cpu().numpy()
+    lay = _image_layout(S, A.C, dtype)
+    hdr = im[:64].view(np.uint32)
+    assert hdr[0] == 0x4E574F46 and hdr[1] == S and hdr[2] == A.C and hdr[8] == 1 << mv
+    assert int(im[24:32].view(np.uint64)[0]) == int(counts.sum())
+    assert 0 < counts.sum() < A.ox.state()[0][:S].sum()  # some blocks stay behind
+    assert np.array_equal(_u32_at(im, lay["fill"], S), counts)
+    start = _u32_at(im, lay["start"], S)
+    assert np.array_equal(start, np.concatenate([[0], np.cumsum(counts)[:-1]]))
+    afill, aord, atag = A.ex.sets_state()
+    n = int(counts.sum())
+    itag, iord = _u32_at(im, lay["tag"], n), _u32_at(im, lay["ord"], n)
+    assert np.all(_u32_at(im, lay["own"], n) == 1 << mv)
+    sets = np.repeat(np.arange(S), counts)
+    assert np.array_equal(itag, np.concatenate([blocks[s, :counts[s]] for s in range(S)]))
+    assert np.array_equal(atag[sets, iord], itag)  # each slot is where A holds the block
+    hidx = (sets.astype(np.int64) * mb + itag) % 4099
+    bb = A.ex.block_bytes
+    assert np.array_equal(im[lay["data"]:lay["data"] + n * bb].reshape(n, bb), A.hostb[hidx])
+    if dtype == F.FP8:
+        isc = im[lay["scales"]:lay["scales"] + 8 * n].view(np.float32).reshape(n, 2)
+        assert np.array_equal(isc, A.hsc[hidx])
+    # the request leaves A and joins B, whose group merges its blocks
+    A.leave([mv])
+    B.join([mv])
+    before = B.ox.state()[0][:S].copy()
+    resident = sum(int(np.isin(blocks[s, :counts[s]], B.ox.state()[2][s, :before[s]]).sum())
+                   for s in range(S))
+    B.ex.owner_import_member(mv, img)
+    B.ox.import_member(mv, counts, blocks)
+    B.check_state()
+    after = B.ox.state()[0][:S]
+    evicted = int(before.sum()) + n - resident - int(after.sum())
+    print(f"[member carry] {n} blocks carried, {resident} already resident on B, "
+          f"{evicted} evicted", flush=True)
+    assert resident > 0
+    if cap_mode == F.CAP_GROUP:
+        assert evicted > 0
+    for t in range(6, 10):
+        sa = sga.step(t).reshape(shape).copy()
+        sb = sgb.step(t).reshape(shape).copy()
+        sb[mv] = sa[mv]
+        sa[mv] = NONE
+        A.step(sa.reshape(-1))
+        B.step(sb.reshape(-1))
+    A.check_state()
+    B.check_state()
+    B.check_attention(sb.reshape(-1), seed=11)
+    # a whole-owner image carries the member masks too
+    whole = B.ex.alloc_owner_image()
+    B.ex.owner_export(0, whole)
+    C2 = GroupPair(lanes, grp, L, Hkv, Hq, k, share, mb, dtype, cap_mode)
+    C2.ex.owner_import(0, whole)
+    torch.cuda.synchronize()
+    assert C2.ex.stats()["device_error"] == 0
+    bf, bo, bt = B.ex.sets_state()
+    cf, co, ct = C2.ex.sets_state()
+    assert np.array_equal(cf[:S], bf[:S]) and np.array_equal(ct[:S], bt[:S])
+    live = np.arange(B.C)[None, :] < bf[:S, None]
+    assert np.array_equal(C2.ex.sets_own()[:S][live], B.ex.sets_own()[:S][live])
+
+
+def test_member_carry_refusals():
+    p = GroupPair(4, 2, 1, 1, 2, 8, 8, 40, F.F16, F.CAP_GROUP)
+    img = p.ex.alloc_owner_image()
+    p.ex.owner_export(1, img)  # a whole-owner image
+    p.ex.owner_import_member(0, img)
+    torch.cuda.synchronize()
+    assert p.ex.stats()["device_error"] == -1
+    q = GroupPair(4, 2, 1, 1, 2, 8, 8, 40, F.F16, F.CAP_GROUP)
+    q.ex.owner_export_member(3, img)  # a member image
+    q.ex.owner_import(1, img)
+    torch.cuda.synchronize()
+    assert q.ex.stats()["device_error"] == -1
+    with pytest.raises(F.FerryError):
+        q.ex.owner_export_member(4, img)  # no such lane
+    solo = F.Executor(2, 1, 1, 8, 8, 40, q_heads=1, dtype=F.F16, host_blocks=64)
+    with pytest.raises(F.FerryError):
+        solo.owner_export_member(0, solo.alloc_owner_image())  # no prefix groups
+    with pytest.raises(F.FerryError):
+        solo.sets_own()
 
 
 def test_members_refusals_latch_einval():

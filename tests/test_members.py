@@ -186,3 +186,122 @@ def test_group_turnover_selections_match_oracle():
         mine.admit_member(0, rid, pre + 1, 12, 16)
     with pytest.raises(F.FerryError):
         mine.admit_member(0, rid, nperm[0] + 1, 12, 3)
+
+
+class _RefGroupSet:
+    """The reference's state of one (gpu, group, layer) under own_carry,
+    restated from its rules with a list and a dict (wla_multigpu.cuh:
+    1871-1962): the LRU deque (front = least recent), and the mask of the
+    members that touched each resident block (own_mask)."""
+
+    def __init__(self):
+        self.dq, self.mask = [], {}
+
+    def touch(self, blk, bit, cap):  # kv_touch + own_mask |= own_bit(r)
+        if blk in self.mask:
+            self.dq.remove(blk)
+            self.dq.append(blk)
+        else:
+            while len(self.dq) >= cap:  # own_drop with the eviction
+                self.mask.pop(self.dq.pop(0))
+            self.dq.append(blk)
+            self.mask[blk] = 0
+        self.mask[blk] |= bit
+
+    def release(self, bit):  # own_release (a zero mask is a dead block, still resident)
+        for b in self.mask:
+            self.mask[b] &= ~bit
+
+    def trim(self, cap):  # grp_trim
+        while len(self.dq) > cap:
+            self.mask.pop(self.dq.pop(0))
+
+    def export(self, bit):  # the blocks kv_handoff_owned moves: mask == bit
+        return [b for b in self.dq if self.mask[b] == bit]
+
+    def merge(self, blocks, bit, cap):  # kv_handoff_owned at the consumer
+        for b in blocks:
+            if b in self.mask:
+                self.mask[b] |= bit
+                continue
+            while len(self.dq) >= cap:
+                self.mask.pop(self.dq.pop(0))
+            self.dq.append(b)
+            self.mask[b] = bit
+
+
+def _compare(ox, model, per):
+    fill, ord_, tag = ox.state()
+    own = ox.own()
+    for s in range(per):
+        blocks = tag[s, ord_[s, :fill[s]]]
+        assert list(blocks) == model[s].dq, s
+        assert [int(own[s, v]) for v in ord_[s, :fill[s]]] == [model[s].mask[b] for b in blocks], s
+
+
+@pytest.mark.parametrize("seed,cap_mode", [(s, m) for s in range(6) for m in (0, 1)])
+def test_member_carry_equals_reference_rules(seed, cap_mode):
+    """Serial (kv_touch) bookkeeping with member masks, members leaving and
+    joining, and a member's exclusive blocks carried from one executor's group
+    into another's: the oracle equals _RefGroupSet after every event."""
+    rng = np.random.default_rng(300 + seed)
+    grp, L, k = 4, 2, 3
+    share = int(rng.integers(k, 3 * k))
+    nb = int(rng.integers(2 * share, 8 * share))
+    cap_slots = share * grp
+    g = O.make_geom(n_req=grp, group=grp, n_layers=L, kv_heads=1, k=k, cap=cap_slots,
+                    max_blocks=nb, dtype=O.F32, granularity=1, cap_mode=cap_mode)
+    ex = {0: O.Executor(g), 1: O.Executor(g)}
+    model = {e: [_RefGroupSet() for _ in range(L)] for e in ex}
+    live = {e: np.ones(grp, bool) for e in ex}
+
+    def cap_of(e):
+        return share * max(1, int(live[e].sum())) if cap_mode else cap_slots
+
+    def step(e):
+        sel = np.full((grp, L, 1, k), NONE, np.uint32)
+        for ln in np.nonzero(live[e])[0]:
+            sel[ln, :, 0] = rng.integers(0, nb, (L, k))
+        ex[e].step(sel.reshape(-1))
+        for l in range(L):
+            for ln in range(grp):
+                for j in range(k):
+                    if sel[ln, l, 0, j] != NONE:
+                        model[e][l].touch(int(sel[ln, l, 0, j]), 1 << ln, cap_of(e))
+
+    def leave(e, ln):
+        assert ex[e].members_leave([ln])
+        live[e][ln] = False
+        for m in model[e]:
+            m.release(1 << ln)
+            if cap_mode:
+                m.trim(cap_of(e))
+
+    for t in range(40):
+        for e in ex:
+            for ln in range(grp):
+                if rng.random() < 0.1:
+                    if live[e][ln]:
+                        leave(e, ln)
+                    else:
+                        assert ex[e].members_join([ln])
+                        live[e][ln] = True
+            step(e)
+            _compare(ex[e], model[e], L)
+        if t % 5 == 4:  # a member of executor 0 moves to a free lane of executor 1
+            src = [ln for ln in range(grp) if live[0][ln]]
+            dst = [ln for ln in range(grp) if not live[1][ln]]
+            if not src or not dst:
+                continue
+            a, b = int(rng.choice(src)), int(rng.choice(dst))
+            counts, blocks = ex[0].export_member(a)
+            for l in range(L):
+                assert list(blocks[l, :counts[l]]) == model[0][l].export(1 << a)
+            leave(0, a)
+            assert ex[1].members_join([b])
+            live[1][b] = True
+            ex[1].import_member(b, counts, blocks)
+            for l in range(L):
+                model[1][l].merge(list(blocks[l, :counts[l]]), 1 << b, cap_of(1))
+            for e in ex:
+                _compare(ex[e], model[e], L)
