@@ -95,7 +95,7 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--steal", type=int, default=1)
     ap.add_argument("--workers", type=int, default=0)
-    ap.add_argument("--attn", default="auto", choices=["auto", "valu", "mfma"],
+    ap.add_argument("--attn", default="auto", choices=["auto", "valu", "mfma", "group"],
                     help="attention kernel: MFMA for GQA groups of 16/8-bit KV (auto), or forced")
     ap.add_argument("--chunks", type=int, default=0,
                     help="layer chunks of the fetch/attention overlap (1 = no side stream, "
@@ -379,6 +379,36 @@ def preroll(a, ex, sg, torch, dev, step_fn, gate, q, bufs):
     return len(rates), rates
 
 
+def distinct_per_set(sel, group):
+    """Distinct selected blocks of every (owner, layer, kv head) set of one step
+    (the blocks a group set's members select are read once by the group kernel)."""
+    B, L, H, k = sel.shape
+    n_own = -(-B // group)
+    pad = np.full((n_own * group - B, L, H, k), 0xFFFFFFFF, np.uint32)
+    s = np.concatenate([sel, pad]).reshape(n_own, group, L, H, k)
+    s = np.sort(s.transpose(0, 2, 3, 1, 4).reshape(n_own * L * H, group * k), axis=1)
+    new = np.ones(s.shape, bool)
+    new[:, 1:] = s[:, 1:] != s[:, :-1]
+    return (new & (s != 0xFFFFFFFF)).sum(axis=1)
+
+
+def distinct_slots(slots, group, k):
+    """The distinct pool slots of every group set of a slot table, set after set,
+    padded to whole rows of k by repeating the last one (a cache hit)."""
+    B, L, H = slots.shape[0], slots.shape[1], slots.shape[2]
+    n_own = -(-B // group)
+    out = []
+    for o in range(n_own):
+        rows = slots[o * group:(o + 1) * group]  # [members][L][H][k]
+        for l in range(L):
+            for h in range(H):
+                u = np.unique(rows[:, l, h].reshape(-1))
+                out.append(u[u != 0xFFFFFFFF])
+    flat = np.concatenate(out).astype(np.uint32)
+    pad = (-flat.size) % k
+    return np.concatenate([flat, np.full(pad, flat[-1], np.uint32)])
+
+
 def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_cpu=True,
         extras=True, steps=None):
     dev = torch.device("cuda", 0)
@@ -401,7 +431,8 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     out = torch.empty_like(qs[0])
     if assign is None:
         assign = F.ASSIGN_AFFINITY if w.get("lognormal") else F.ASSIGN_SPREAD
-    attn = {"auto": F.ATTN_AUTO, "valu": F.ATTN_VALU, "mfma": F.ATTN_MFMA}[a.attn]
+    attn = {"auto": F.ATTN_AUTO, "valu": F.ATTN_VALU, "mfma": F.ATTN_MFMA,
+            "group": F.ATTN_GROUP}[a.attn]
     ex = F.Executor(B, L, H, k, C, sg.max_blocks, q_heads=Hq, group=w["group"], dtype=dtype,
                     host_blocks=a.host_blocks, fetch_workers=workers, steal=steal, assign=assign,
                     attn=attn)
@@ -430,7 +461,12 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     pre_s = time.perf_counter() - t0
     n_steps = a.warmup + 2 * n_timed
     t0 = time.perf_counter()
-    sels = [torch.from_numpy(sg.step(n_pre + t).view(np.int32)).to(dev) for t in range(n_steps)]
+    sels, distinct = [], []
+    for t in range(n_steps):
+        sel = sg.step(n_pre + t)
+        if t >= a.warmup + n_timed:  # the steps whose kernels are timed one by one
+            distinct.append(distinct_per_set(sel, w["group"]))
+        sels.append(torch.from_numpy(sel.view(np.int32)).to(dev))
     gen_s = time.perf_counter() - t0
     torch.cuda.synchronize()
 
@@ -526,8 +562,29 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     attn_gbs = attn_bytes / (t_attn * 1e-3) / 1e9
     link_gbs = fetch_bytes / (t_fetch * 1e-3) / 1e9
     G = Hq // H
-    mfma = dtype != F.F32 and G >= 2 and attn != F.ATTN_VALU
-    attn_kernel = f"k_attn{'_mfma' if mfma else ''}<{w['dtype']},{G}>"
+    kind, waves = ex.attn_kernel()
+    attn_kernel = {F.ATTN_VALU: "k_attn", F.ATTN_MFMA: "k_attn_mfma",
+                   F.ATTN_GROUP: "k_attn_group"}[kind] + f"<{w['dtype']},{G}>"
+    grouped = None
+    if kind == F.ATTN_GROUP:
+        # algorithmic bytes of the group kernel: every distinct block of a group
+        # set once per launch, plus q in, out and the slot table; the ceiling is
+        # a plain gather of the same distinct blocks (last timed step's table)
+        n_distinct = float(np.mean([d.sum() for d in distinct]))
+        grp_bytes = (n_distinct * (bb + scale_bytes) + 2 * B * L * Hq * 128 * 4
+                     + sel_per_step * 4)
+        grp_gbs = grp_bytes / (t_attn * 1e-3) / 1e9
+        flat = distinct_slots(bufs["slots"].cpu().numpy().view(np.uint32), w["group"], k)
+        drows = torch.from_numpy(flat.view(np.int32)).to(dev)
+        dbytes, _, dgather_gbs = ex.bw_probe(F.PROBE_HBM_GATHER, flat.size // k, slots=drows,
+                                             iters=max(3, n_timed // 2), stream=stream)
+        grouped = {"achieved": round(grp_gbs, 1), "frac": round(grp_gbs / HBM_PEAK_GBS, 4),
+                   "waves": waves, "distinct_blocks_per_launch": round(n_distinct, 1),
+                   "bytes_per_launch": int(grp_bytes),
+                   "per_request_bytes_per_launch": int(attn_bytes),
+                   "effective_gbs": round(attn_gbs, 1),
+                   "plain_gather_distinct_gbs": round(dgather_gbs, 1),
+                   "frac_of_plain_gather": round(grp_gbs / dgather_gbs, 4)}
     res = {
         "ms_per_step": round(ms_step, 3),
         "value": round(B / (ms_step * 1e-3), 2),
@@ -544,11 +601,14 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
         "attention_tok_per_s": round(B / (t_attn * 1e-3), 1),
         "kernel_ms": {"bookkeep": round(t_book, 4), "fetch": round(t_fetch, 4),
                       "attention": round(t_attn, 4), "attention_back_to_back": round(t_attn_rep, 4)},
-        "roofline": {"bound": "hbm", "kernel": attn_kernel,
-                     "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "plain_gather_gbs": round(gather_gbs, 1),
-                     "frac_of_plain_gather": round(attn_gbs / gather_gbs, 4)},
+        "roofline": ({"bound": "hbm", "kernel": attn_kernel,
+                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                      "plain_gather_gbs": round(gather_gbs, 1),
+                      "frac_of_plain_gather": round(attn_gbs / gather_gbs, 4)}
+                     if grouped is None else
+                     {"bound": "hbm", "kernel": attn_kernel, "peak": HBM_PEAK_GBS,
+                      "unit": "GB/s", "traffic": None, **grouped}),
         "roofline_fetch": {"bound": "host-link", "kernel": f"k_fetch<{bb // 1024}>",
                            "achieved": round(link_gbs, 2), "peak": round(LINK_PEAK_GBS, 2),
                            "unit": "GB/s", "frac": round(link_gbs / LINK_PEAK_GBS, 4),

@@ -28,7 +28,7 @@ __all__ = [
     "FerryError", "Executor", "SelGen", "Sched", "queue_selftest", "refgen_selections",
     "ctx_uniform", "arrivals", "lib", "LIB_PATH", "F32", "F16", "BF16", "FP8", "LRU_STEP",
     "LRU_SERIAL", "ASSIGN_SPREAD", "ASSIGN_AFFINITY", "ATTN_AUTO", "ATTN_VALU", "ATTN_MFMA",
-    "MISS_DTYPE", "EMPTY", "ARRIVAL_STEADY", "ARRIVAL_BURSTY", "ARRIVAL_POISSON", "ARRIVAL_MMPP",
+    "ATTN_GROUP", "MISS_DTYPE", "EMPTY", "ARRIVAL_STEADY", "ARRIVAL_BURSTY", "ARRIVAL_POISSON", "ARRIVAL_MMPP",
     "SCHED_FIFO", "SCHED_PINNED", "trace_load", "TOPK_PER_HEAD", "TOPK_LAYER_MAX", "CAP_GROUP",
     "CAP_PER_MEMBER",
 ]
@@ -42,7 +42,7 @@ lib = C.CDLL(LIB_PATH)
 F32, F16, BF16, FP8 = 0, 1, 2, 3
 LRU_STEP, LRU_SERIAL = 0, 1
 ASSIGN_SPREAD, ASSIGN_AFFINITY = 0, 1
-ATTN_AUTO, ATTN_VALU, ATTN_MFMA = 0, 1, 2
+ATTN_AUTO, ATTN_VALU, ATTN_MFMA, ATTN_GROUP = 0, 1, 2, 3
 CAP_GROUP, CAP_PER_MEMBER = 0, 1
 PROBE_HBM_GATHER, PROBE_HOST_READ, PROBE_HOST_DMA, PROBE_HBM_COPY = 0, 1, 2, 3
 ARRIVAL_STEADY, ARRIVAL_BURSTY, ARRIVAL_POISSON, ARRIVAL_MMPP = 0, 1, 2, 3
@@ -137,6 +137,7 @@ _PROTOS = {
     "ferry_owner_import_member": (C.c_int, [_vp, C.c_uint32, _vp, C.c_uint64, _vp]),
     "ferry_sets_own": (C.c_int, [_vp, _vp]),
     "ferry_decode_chunks": (C.c_int, [_vp, C.c_uint64, C.POINTER(_i32)]),
+    "ferry_attn_kernel": (C.c_int, [_vp, C.POINTER(_i32), C.POINTER(_i32)]),
     "ferry_summaries_view": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(C.c_uint64)]),
     "ferry_select_topk": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp, _vp]),
     "ferry_select_topk_layers": (C.c_int, [_vp, _i32, _i32, _vp, _vp, C.c_int, _vp, _vp]),
@@ -371,6 +372,13 @@ class Executor:
 
     def missq_drain(self, stream=None):
         _check(lib.ferry_missq_drain(self._h, _stream(stream)), "ferry_missq_drain")
+
+    def attn_kernel(self):
+        """(kind, waves) of the attention kernel sparse_decode runs: kind is
+        ATTN_VALU, ATTN_MFMA (per request row) or ATTN_GROUP (per group set)."""
+        kind, waves = _i32(), _i32()
+        _check(lib.ferry_attn_kernel(self._h, C.byref(kind), C.byref(waves)), "ferry_attn_kernel")
+        return kind.value, waves.value
 
     def sparse_decode(self, q, slots, out, stream=None):
         _check(lib.ferry_sparse_decode(self._h, self._q(q), self._sel(slots, "slots"),

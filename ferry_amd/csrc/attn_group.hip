@@ -1,0 +1,402 @@
+// attn_group.hip -- block-sparse decode attention of a whole prefix group per
+// workgroup, reading every distinct selected block of the group's set once.
+//
+// Same result as k_attn_mfma (attn_mfma.hip) for every member row:
+// out[r,l,hq] = softmax(q K^T / sqrt(D)) V over the tokens of the k blocks
+// selected for (r, l, kv head of hq), a block selected twice in one row counted
+// twice, a row with nothing selected giving 0.  The reference has only an FMA
+// proxy (src/workloads/kv_exec.cuh:30-37); the semantics are the textbook
+// softmax attention of the top-k pages selected in
+// tools/capture_miss_trace.py:139-159.  Prefix groups share one LRU set per
+// (group, layer, kv head) (src/runtime/wla_multigpu.cuh:323-349, wla_gslot_off),
+// so the members' selections of the shared prefix land on the same slots.
+//
+// One workgroup of four wavefronts per (group, layer, kv head).  The group's
+// query columns (member x query head, NTILE tiles of 16, attn_mfma.hpp) are
+// held by every wavefront; the blocks are split between the wavefronts.
+//  1. List: every member row's slots are OR-ed into a per-slot member mask in
+//     LDS (one word per slot of the set).  A repeated selection in one row,
+//     or a slot outside the row's set, becomes an entry of its own with that
+//     member alone.  The masks are compacted in slot order, then the own
+//     entries ordered by (member, slot), so the list and the summation order
+//     do not depend on the order the atomics ran in.
+//  2. Blocks: entry j of the list goes to wavefront j mod 4, which streams its
+//     entries through its own ring of R blocks in LDS (three fp8 or two 16-bit
+//     blocks) with direct-to-LDS
+//     16-byte loads (global_load_lds_dwordx4, non-temporal: each block is read
+//     once), R - 1 blocks ahead, waiting only on its own load counter: no
+//     workgroup barrier in the loop.  Token rows keep their 16-byte chunks
+//     XOR-swizzled by (row mod 8), so the K and V reads of eight rows at one
+//     offset fall on eight different bank groups.
+//  3. Attention: a block's K and V operands are built once (block_operands)
+//     and every query tile with a member that selected the block attends to
+//     it (tile_block); the columns of members that did not are masked, so
+//     every member accumulates exactly its own blocks.  The tiles' Q^T
+//     operands wait in LDS (one conflict-free 16-byte read per lane and
+//     k-slice), so a wavefront's registers hold the accumulators of all its
+//     columns but only one tile's queries at a time.
+//  4. Merge: the four wavefronts' partial softmax states of each column are
+//     combined through LDS (max, rescaled sums and outputs), as k_attn_mfma
+//     merges its wavefronts.
+// HBM bytes per launch: the distinct blocks of each group set once (plus q in,
+// out and the slot table), against k blocks per member row for k_attn_mfma.
+#include "attn_mfma.hpp"
+#include "kernels.hpp"
+
+namespace ferry_amd {
+
+using namespace mx;
+
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
+
+// Wait until at most N vector-memory loads of this wavefront are outstanding.
+// The "memory" clobber keeps the LDS reads of the landed block below it.
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Wait until the oldest of this wavefront's outstanding block loads are done,
+// leaving `later` (<= K) younger blocks of NI loads each in flight.
+template <int NI, int K>
+__device__ inline void wait_blocks(int later) {
+  if constexpr (K == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (later >= K) wait_vmcnt<K * NI>();
+    else wait_blocks<NI, K - 1>(later);
+  }
+}
+
+// Exclusive prefix sum of v over the workgroup's threads (thread order);
+// *total = the sum over all.  `sh` is LDS scratch of W ints.  Barriers on
+// entry and exit, so `sh` can be reused right after.
+template <int W>
+__device__ inline int block_exclusive_scan(int v, int* sh, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  __syncthreads();
+  if (lane == 63) sh[wave] = x;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const int c = sh[w];
+    before += w < wave ? c : 0;
+    tot += c;
+  }
+  *total = tot;
+  __syncthreads();
+  return before + x - v;
+}
+
+}  // namespace
+
+template <int DT, int G, int NTILE>
+__global__ __launch_bounds__(kGroupWaves * 64) void k_attn_group(
+    Geo g, const float* __restrict__ q, const uint32_t* __restrict__ slots,
+    const uint8_t* __restrict__ pool, const float* __restrict__ pool_scales,
+    float* __restrict__ out, float qscale, int l0, int nl, int* __restrict__ err) {
+  static_assert(G == 2 || G == 4 || G == 8, "GQA group of 2, 4 or 8 query heads");
+  static_assert(NTILE >= 1 && NTILE <= kGroupMaxTiles, "query tiles per workgroup");
+  static_assert(DT == FERRY_F16 || DT == FERRY_BF16 || DT == FERRY_FP8_E4M3, "16/8-bit KV");
+  using S = Shape<DT>;
+  constexpr int D = S::D, T = S::T, NKW = S::NKW, VW = S::VW;
+  constexpr int ROW = (int)S::ROW;     // bytes of one token row
+  constexpr int RC = ROW / 16;         // 16-byte chunks of a row (8 or 16)
+  constexpr int BB = 2 * T * ROW;      // bytes of one block, K tile then V tile
+  constexpr int NI = BB / 1024;        // direct-to-LDS loads of one block per wavefront
+  constexpr int W = kGroupWaves;       // wavefronts
+  constexpr int NT = W * 64;           // threads
+  constexpr int MPT = 16 / G;          // members per query tile
+  constexpr int R = group_ring_blocks(DT);   // ring blocks per wavefront
+  constexpr int RB = group_ring_bytes(DT);    // ring bytes per wavefront
+  constexpr int NQ = S::BF ? 2 : 1;           // parts of the Q^T operands (bf16: hi, lo)
+  constexpr int COLS = 16 * NTILE;            // query columns
+  constexpr int TR = RB / (16 * D * 4);       // tiles merged per round
+  static_assert(RB == R * BB && R >= 2 && (R - 2) * NI < 64, "ring depth and load counter");
+  static_assert(TR >= 1, "a merge round fits the rings");
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int GK = g.group * g.k;
+  uint8_t* rings = smem;                                                  // [W][R][BB]
+  u32x4* qops = reinterpret_cast<u32x4*>(smem + W * RB);                  // [NQ][NTILE][4][64]
+  uint32_t* lslot = reinterpret_cast<uint32_t*>(qops + NQ * NTILE * 4 * 64);  // [GK] list
+  uint32_t* lmask = lslot + GK;                                           // [GK] members
+  float* red_ml = reinterpret_cast<float*>(lmask + GK);                   // [W][COLS][2]
+  int* sh = reinterpret_cast<int*>(red_ml + W * COLS * 2);                // [W] scan
+  uint32_t* msk = reinterpret_cast<uint32_t*>(rings);                     // [C] listing
+  uint32_t* own = msk + g.C;                                              // [GK] listing
+  float* red_o = reinterpret_cast<float*>(rings);                         // [W][TR*16][D] merge
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n = lane & 15, grp = lane >> 4;
+  const int h = blockIdx.x % g.Hkv;
+  const int l = l0 + (blockIdx.x / g.Hkv) % nl;
+  const int o = blockIdx.x / (nl * g.Hkv);
+  const int mem = min(g.group, g.n_req - o * g.group);  // member rows of this owner
+  const uint32_t base = (uint32_t)((o * g.L + l) * g.Hkv + h) * (uint32_t)g.C;
+
+  // ---- 1. the distinct list of the group's selections
+  for (int i = tid; i < g.C; i += NT) msk[i] = 0u;
+  __syncthreads();
+  bool bad = false;
+  for (int e = tid; e < GK; e += NT) {
+    const int mi = e / g.k;
+    uint32_t s = kNone, mine = kNone;
+    if (mi < mem)
+      s = slots[((size_t)((o * g.group + mi) * g.L + l) * g.Hkv + h) * g.k + (e - mi * g.k)];
+    if (s != kNone) {
+      if (s >= g.pool_slots) {  // read as slot 0 and reported, as k_attn_mfma does
+        bad = true;
+        s = 0;
+      }
+      const uint32_t loc = s - base;
+      if (loc < (uint32_t)g.C) {
+        const uint32_t bit = 1u << mi;
+        if (atomicOr(&msk[loc], bit) & bit) mine = s;  // a repeat in this row
+      } else {
+        mine = s;  // outside the set
+      }
+    }
+    own[e] = mine;
+  }
+  if (bad) set_error(err, FERRY_ERANGE);
+  __syncthreads();
+  // masks in slot order: each thread compacts a contiguous range of slots
+  const int per = (g.C + NT - 1) / NT;
+  const int c0 = min(g.C, tid * per), c1 = min(g.C, c0 + per);
+  int cnt = 0;
+  for (int i = c0; i < c1; ++i) cnt += msk[i] != 0u;
+  int n_in = 0;
+  int pos = block_exclusive_scan<W>(cnt, sh, &n_in);
+  for (int i = c0; i < c1; ++i) {
+    const uint32_t mm = msk[i];
+    if (mm) {
+      lslot[pos] = base + (uint32_t)i;
+      lmask[pos] = mm;
+      ++pos;
+    }
+  }
+  // own entries after them, ordered by (member, slot); equal keys are the same
+  // block for the same member, so their order among themselves does not matter
+  int cown = 0;
+  for (int e = tid; e < GK; e += NT) cown += own[e] != kNone;
+  int n_own = 0;
+  (void)block_exclusive_scan<W>(cown, sh, &n_own);
+  if (n_own > 0) {  // uniform
+    for (int e = tid; e < GK; e += NT) {
+      const uint32_t s = own[e];
+      if (s == kNone) continue;
+      const int mi = e / g.k;
+      int rank = 0;
+      for (int e2 = 0; e2 < GK; ++e2) {
+        const uint32_t s2 = own[e2];
+        if (s2 == kNone) continue;
+        const int m2 = e2 / g.k;
+        rank += m2 < mi || (m2 == mi && (s2 < s || (s2 == s && e2 < e)));
+      }
+      lslot[n_in + rank] = s;
+      lmask[n_in + rank] = 1u << mi;
+    }
+  }
+  const int nlist = n_in + n_own;
+  __syncthreads();  // the rings may now overwrite msk / own
+
+  // ---- Q^T operands of every tile, staged in LDS lane by lane (wavefront w
+  // builds tile w, w + W, ...): column n of tile t is member t*MPT + n/G,
+  // query head h*G + n%G (zeros past the group's members)
+  for (int t = wave; t < NTILE; t += W) {
+    const int mi = t * MPT + n / G;
+    const size_t qrow = (size_t)((o * g.group + mi) * g.L + l) * g.Hq + (size_t)h * G + n % G;
+    uint32_t qh[4][4], ql[4][4];
+    q_operand<DT>(mi < mem ? q + qrow * D : nullptr, grp, qscale, qh, ql);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      qops[(t * 4 + kk) * 64 + lane] = u32x4{qh[kk][0], qh[kk][1], qh[kk][2], qh[kk][3]};
+      if constexpr (NQ == 2)
+        qops[((NTILE + t) * 4 + kk) * 64 + lane] = u32x4{ql[kk][0], ql[kk][1], ql[kk][2], ql[kk][3]};
+    }
+  }
+  uint32_t tile_bits[NTILE], col_bit[NTILE];
+  Acc acc[NTILE];
+  const uint32_t mem_bits = (uint32_t)((1ull << mem) - 1ull);
+#pragma unroll
+  for (int t = 0; t < NTILE; ++t) {
+    const int mi = t * MPT + n / G;
+    tile_bits[t] = (((1u << MPT) - 1u) << (t * MPT)) & mem_bits;
+    col_bit[t] = mi < mem ? 1u << mi : 0u;
+    acc[t].init();
+  }
+  __syncthreads();  // Q^T operands staged
+
+  // ---- 2./3. this wavefront's entries wave, wave + W, ... through its ring
+  const int nb = nlist > wave ? (nlist - wave + W - 1) / W : 0;
+  uint8_t* ring = rings + wave * RB;
+  // block j of this wavefront into ring slot b: lane loads chunk p = i*64 +
+  // lane of the block, which holds logical chunk (p mod RC) ^ (row mod 8)
+  auto issue = [&](int j, int b) {
+    const uint32_t slot = (uint32_t)__builtin_amdgcn_readfirstlane((int)lslot[wave + W * j]);
+    const uint8_t* src = pool + (uint64_t)slot * BB;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int p = i * 64 + lane;
+      const int t = (p / RC) % T;  // token row within its tile
+      const int off = (p / RC) * ROW + ((p % RC) ^ (t & 7)) * 16;
+      __builtin_amdgcn_global_load_lds((glb_void*)(src + off),
+                                       (lds_void*)(ring + b * BB + i * 1024), 16, 0, 2 /* nt */);
+    }
+  };
+  // K word w of lane (n, grp): token n, logical chunk 4w + grp.  V of token i:
+  // row 4*grp + i of the V tile, elements 8n..8n+7 (logical chunk n/2, half n%2
+  // for fp8; chunk n for 16-bit).
+  auto read_block = [&](const uint8_t* blk, u32x4 (&kw)[NKW], uint32_t (&vw)[4][VW]) {
+#pragma unroll
+    for (int w = 0; w < NKW; ++w)
+      kw[w] = *reinterpret_cast<const u32x4*>(blk + n * ROW + (((4 * w + grp) ^ (n & 7)) * 16));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 4 * grp + i;
+      const uint8_t* vrow = blk + T * ROW + t * ROW;
+      if constexpr (S::F8) {
+        const u32x2 v =
+            *reinterpret_cast<const u32x2*>(vrow + (((n >> 1) ^ (t & 7)) * 16) + (n & 1) * 8);
+        vw[i][0] = v[0], vw[i][1] = v[1];
+      } else {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(vrow + ((n ^ (t & 7)) * 16));
+        vw[i][0] = v[0], vw[i][1] = v[1], vw[i][2] = v[2], vw[i][3] = v[3];
+      }
+    }
+  };
+#pragma unroll
+  for (int b = 0; b < R - 1; ++b)
+    if (b < nb) issue(b, b);
+  for (int j0 = 0; j0 < nb; j0 += R) {
+#pragma unroll
+    for (int b = 0; b < R; ++b) {
+      const int j = j0 + b;
+      if (j < nb) {  // uniform
+        // block j landed once at most the later blocks issued are in flight
+        wait_blocks<NI, R - 2>(min(R - 2, nb - 1 - j));
+        if (j + R - 1 < nb) {
+          // ring slot (b - 1) mod R held block j - 1: its LDS reads have returned
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          issue(j + R - 1, (b + R - 1) % R);
+        }
+        const int li = wave + W * j;
+        const uint32_t mm = (uint32_t)__builtin_amdgcn_readfirstlane((int)lmask[li]);
+        float ks = 1.0f, vs = 1.0f;
+        if constexpr (S::F8) {
+          const uint32_t slot = (uint32_t)__builtin_amdgcn_readfirstlane((int)lslot[li]);
+          ks = pool_scales[2 * (uint64_t)slot];
+          vs = pool_scales[2 * (uint64_t)slot + 1];
+        }
+        u32x4 kw[NKW];
+        uint32_t vw[4][VW];
+        read_block(ring + b * BB, kw, vw);
+        Ops op;
+        block_operands<DT>(kw, vw, op);
+#pragma unroll
+        for (int t = 0; t < NTILE; ++t) {
+          if (mm & tile_bits[t]) {  // uniform: a member of tile t selected the block
+            uint32_t qh[4][4], ql[4][4];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+              const u32x4 a = qops[(t * 4 + kk) * 64 + lane];
+              qh[kk][0] = a[0], qh[kk][1] = a[1], qh[kk][2] = a[2], qh[kk][3] = a[3];
+              if constexpr (NQ == 2) {
+                const u32x4 b = qops[((NTILE + t) * 4 + kk) * 64 + lane];
+                ql[kk][0] = b[0], ql[kk][1] = b[1], ql[kk][2] = b[2], ql[kk][3] = b[3];
+              } else {
+                ql[kk][0] = ql[kk][1] = ql[kk][2] = ql[kk][3] = 0u;
+              }
+            }
+            tile_block<DT, true>(op, ks, vs, qh, ql, acc[t], (mm & col_bit[t]) != 0u);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- 4. merge the wavefronts' states: per round, TR tiles through LDS
+#pragma unroll
+  for (int t = 0; t < NTILE; ++t) {
+    float lsum = acc[t].lsum;
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (grp == 0) {
+      red_ml[(wave * COLS + 16 * t + n) * 2] = acc[t].m;
+      red_ml[(wave * COLS + 16 * t + n) * 2 + 1] = lsum;
+    }
+  }
+#pragma unroll
+  for (int t0 = 0; t0 < NTILE; t0 += TR) {
+    __syncthreads();  // the rings (first round) or the last round's red_o are free
+#pragma unroll
+    for (int t = t0; t < min(t0 + TR, NTILE); ++t) {
+      const float vref = S::F8 ? acc[t].vs_ref : 1.0f;
+      float* ro = red_o + ((size_t)wave * TR * 16 + (t - t0) * 16 + n) * D + 32 * grp;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float4* op = reinterpret_cast<float4*>(ro + 8 * i);
+        op[0] = float4{acc[t].o[0][i] * vref, acc[t].o[1][i] * vref, acc[t].o[2][i] * vref,
+                       acc[t].o[3][i] * vref};
+        op[1] = float4{acc[t].o[4][i] * vref, acc[t].o[5][i] * vref, acc[t].o[6][i] * vref,
+                       acc[t].o[7][i] * vref};
+      }
+    }
+    __syncthreads();
+    const int ncol = 16 * (min(t0 + TR, NTILE) - t0);
+    for (int x = tid; x < ncol * D; x += NT) {
+      const int c = x / D, d = x % D;  // column 16*t0 + c
+      const int col = 16 * t0 + c;
+      const int mi = (col / 16) * MPT + (col % 16) / G;
+      if (mi >= mem) continue;
+      float mx = kNeg;
+#pragma unroll
+      for (int w = 0; w < W; ++w) mx = fmaxf(mx, red_ml[(w * COLS + col) * 2]);
+      float lt = 0.0f, ot = 0.0f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float f = exp2_fast(red_ml[(w * COLS + col) * 2] - mx);
+        lt += red_ml[(w * COLS + col) * 2 + 1] * f;
+        ot += red_o[((size_t)w * TR * 16 + c) * D + d] * f;
+      }
+      const size_t qrow =
+          (size_t)((o * g.group + mi) * g.L + l) * g.Hq + (size_t)h * G + (col % 16) % G;
+      out[qrow * D + d] = lt > 0.0f ? ot / lt : 0.0f;  // nothing selected: 0
+    }
+  }
+}
+
+#define FERRY_ATTN_GROUP_INST(DT, G, NTILE)                                                    \
+  template __global__ void k_attn_group<DT, G, NTILE>(Geo, const float*, const uint32_t*,      \
+                                                      const uint8_t*, const float*, float*,    \
+                                                      float, int, int, int*);
+#define FERRY_ATTN_GROUP_INST_DT(DT) \
+  FERRY_ATTN_GROUP_INST(DT, 2, 1)    \
+  FERRY_ATTN_GROUP_INST(DT, 2, 2)    \
+  FERRY_ATTN_GROUP_INST(DT, 2, 3)    \
+  FERRY_ATTN_GROUP_INST(DT, 2, 4)    \
+  FERRY_ATTN_GROUP_INST(DT, 4, 1)    \
+  FERRY_ATTN_GROUP_INST(DT, 4, 2)    \
+  FERRY_ATTN_GROUP_INST(DT, 4, 3)    \
+  FERRY_ATTN_GROUP_INST(DT, 4, 4)    \
+  FERRY_ATTN_GROUP_INST(DT, 8, 1)    \
+  FERRY_ATTN_GROUP_INST(DT, 8, 2)    \
+  FERRY_ATTN_GROUP_INST(DT, 8, 3)    \
+  FERRY_ATTN_GROUP_INST(DT, 8, 4)
+FERRY_ATTN_GROUP_INST_DT(FERRY_F16)
+FERRY_ATTN_GROUP_INST_DT(FERRY_BF16)
+FERRY_ATTN_GROUP_INST_DT(FERRY_FP8_E4M3)
+
+}  // namespace ferry_amd

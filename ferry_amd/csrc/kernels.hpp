@@ -110,6 +110,32 @@ __global__ void k_attn_mfma(Geo g, const float* q, const uint32_t* slots, const 
                             const float* pool_scales, float* out, float qscale, int l0, int nl,
                             int* err);
 
+// Prefix-group attention (attn_group.hip): one workgroup of kGroupWaves
+// wavefronts per (group, layer, kv head) reads each distinct block of the
+// group's set once and attends every member row; NTILE tiles of 16 query
+// columns (group * G / 16 rounded up); dynamic LDS of attn_group_lds_bytes().
+constexpr int kGroupWaves = 4;     // wavefronts per workgroup; blocks are split between them
+constexpr int kGroupMaxTiles = 4;  // query tiles every wavefront attends with (64 columns)
+// blocks in one wavefront's LDS ring: three fp8 blocks (12 KiB), two 16-bit (16 KiB)
+constexpr int group_ring_blocks(int dtype) { return dtype == FERRY_FP8_E4M3 ? 3 : 2; }
+constexpr int group_ring_bytes(int dtype) {
+  return group_ring_blocks(dtype) * 2 * 16 * 128 * (dtype == FERRY_FP8_E4M3 ? 1 : 2);
+}
+template <int DT, int G, int NTILE>
+__global__ void k_attn_group(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
+                             const float* pool_scales, float* out, float qscale, int l0, int nl,
+                             int* err);
+// LDS of one k_attn_group workgroup: the wavefronts' rings, the Q^T operands
+// of every tile (fp16, or bf16 hi and lo parts: 4 KiB per part and tile), the
+// distinct list (slot and member mask per entry, at most group * k entries),
+// the merge's per-column max and sum of every wavefront, and the scan scratch.
+inline size_t attn_group_lds_bytes(const Geo& g, int ntile) {
+  const size_t parts = g.dtype == FERRY_BF16 ? 2 : 1;
+  return (size_t)kGroupWaves * group_ring_bytes(g.dtype) + parts * ntile * 4096 +
+         8 * (size_t)g.group * g.k + 8 * (size_t)kGroupWaves * 16 * ntile +
+         4 * (size_t)kGroupWaves;
+}
+
 // Bandwidth ceilings (probe.hip): the attention kernels' loads without their
 // math, and device-direct host-tier reads without the fetch bookkeeping.
 template <int NLD>

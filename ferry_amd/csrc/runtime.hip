@@ -129,6 +129,7 @@ struct ferry_ctx {
   int thief_waves = 1;             // wavefronts per fetch workgroup that steal (FERRY_THIEF_WAVES)
   int steal_inflight = 2;          // stolen blocks in flight per thief (FERRY_STEAL_INFLIGHT)
   int attn_loads = 0;              // K/V loads (FERRY_ATTN_LOADS): 0 = by plan, 1 = nt, 2 = temporal
+  bool attn_grouped = true;        // FERRY_ATTN_AUTO may pick the prefix-group kernel (FERRY_ATTN_GROUPED)
   uint32_t* probe_sink = nullptr;  // bandwidth probes: one word per row / wavefront
   size_t probe_sink_words = 0;
   uint8_t* probe_dst = nullptr;    // bandwidth probes: DMA destination
@@ -159,6 +160,19 @@ struct ferry_ctx {
 
 namespace {
 
+// Whether the prefix-group attention kernel (k_attn_group) can run this
+// geometry: every wavefront holds all group * G query columns (at most
+// kGroupMaxTiles tiles of 16), the distinct list has group * k entries, and
+// the per-slot member masks plus the list's scratch fit the block rings while
+// the list is built.
+bool group_attn_fits(const ferry_config* c) {
+  const int G = c->q_heads / c->kv_heads;
+  const long gk = (long)c->group * c->k;
+  return c->group > 1 && G >= 2 && c->dtype != FERRY_F32 && c->group * G <= 16 * kGroupMaxTiles &&
+         gk <= 2048 &&
+         4 * ((long)c->slots_per_set + gk) <= (long)kGroupWaves * group_ring_bytes(c->dtype);
+}
+
 int validate(const ferry_config* c) {
   if (!c) return fail(FERRY_EINVAL, "null config");
   if (c->n_req < 1 || c->group < 1 || c->n_layers < 1 || c->kv_heads < 1 || c->q_heads < 1 ||
@@ -176,10 +190,16 @@ int validate(const ferry_config* c) {
     return fail(FERRY_EINVAL, "bad lru_mode");
   if (c->assign != FERRY_ASSIGN_SPREAD && c->assign != FERRY_ASSIGN_AFFINITY)
     return fail(FERRY_EINVAL, "bad assign");
-  if (c->attn != FERRY_ATTN_AUTO && c->attn != FERRY_ATTN_VALU && c->attn != FERRY_ATTN_MFMA)
+  if (c->attn != FERRY_ATTN_AUTO && c->attn != FERRY_ATTN_VALU && c->attn != FERRY_ATTN_MFMA &&
+      c->attn != FERRY_ATTN_GROUP)
     return fail(FERRY_EINVAL, "bad attn");
-  if (c->attn == FERRY_ATTN_MFMA && (grp < 2 || c->dtype == FERRY_F32))
-    return fail(FERRY_EINVAL, "the MFMA attention kernel needs q_heads/kv_heads >= 2 and 16/8-bit KV");
+  if ((c->attn == FERRY_ATTN_MFMA || c->attn == FERRY_ATTN_GROUP) &&
+      (grp < 2 || c->dtype == FERRY_F32))
+    return fail(FERRY_EINVAL, "the MFMA attention kernels need q_heads/kv_heads >= 2 and 16/8-bit KV");
+  if (c->attn == FERRY_ATTN_GROUP && !group_attn_fits(c))
+    return fail(FERRY_EINVAL,
+                "the prefix-group attention kernel needs group > 1, group * q_heads/kv_heads <= 64, "
+                "group * k <= 2048 and slots_per_set + group * k <= 12288");
   if (c->fetch_workers < 0) return fail(FERRY_EINVAL, "fetch_workers < 0");
   if (c->cap_mode != FERRY_CAP_GROUP && c->cap_mode != FERRY_CAP_PER_MEMBER)
     return fail(FERRY_EINVAL, "bad cap_mode");
@@ -255,9 +275,12 @@ struct AttnArgs {
 // measured the same on MI355X.  K/V loads are non-temporal unless requests
 // share prefix-group sets (group > 1), whose blocks the member rows of one
 // launch re-read from cache; FERRY_ATTN_LOADS=nt|temporal overrides.
+// Prefix groups that fit it run the group kernel instead (one workgroup per
+// group set, each distinct block read once), unless the config asks for the
+// per-row MFMA kernel or FERRY_ATTN_GROUPED=0 is set.
 struct AttnPlan {
-  bool mfma, nt;
-  int dtype, G, waves;
+  bool mfma, nt, grouped;
+  int dtype, G, waves, tiles;
 };
 
 AttnPlan attn_plan(const ferry_ctx* ctx) {
@@ -266,8 +289,15 @@ AttnPlan attn_plan(const ferry_ctx* ctx) {
   p.dtype = g.dtype;
   p.G = g.Hq / g.Hkv;
   p.mfma = g.dtype != FERRY_F32 && p.G >= 2 && ctx->cfg.attn != FERRY_ATTN_VALU;
+  p.grouped = ctx->cfg.attn == FERRY_ATTN_GROUP ||
+              (ctx->cfg.attn == FERRY_ATTN_AUTO && ctx->attn_grouped && group_attn_fits(&ctx->cfg));
   p.waves = 4;
   if (ctx->attn_waves == 8) p.waves = 8;
+  p.tiles = 0;
+  if (p.grouped) {  // tiles of 16 query columns held by every wavefront
+    p.waves = kGroupWaves;
+    p.tiles = (g.group * p.G + 15) / 16;
+  }
   p.nt = ctx->attn_loads ? ctx->attn_loads == 1 : g.group == 1;
   return p;
 }
@@ -290,9 +320,29 @@ void launch_mfma(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnA
     hipLaunchKernelGGL((k_attn_mfma<DT, G, W, false>), grid, dim3(W * 64), 0, s, a.g, a.q,
                        a.slots, a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
 }
+template <int DT, int G, int NT>
+void launch_group(const dim3& grid, size_t lds, hipStream_t s, const AttnArgs& a) {
+  // more than the default 64 KiB of dynamic LDS: allowed once per instance
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&k_attn_group<DT, G, NT>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  (void)attr;
+  hipLaunchKernelGGL((k_attn_group<DT, G, NT>), grid, dim3(kGroupWaves * 64), lds, s, a.g, a.q,
+                     a.slots, a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
+}
 template <int DT, int G>
 void launch_g(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs& a) {
   if constexpr (DT != FERRY_F32 && G >= 2) {
+    if (p.grouped) {
+      const dim3 ggrid((unsigned)(a.g.n_owners * a.nl * a.g.Hkv));
+      const size_t lds = attn_group_lds_bytes(a.g, p.tiles);
+      switch (p.tiles) {
+        case 1: launch_group<DT, G, 1>(ggrid, lds, s, a); return;
+        case 2: launch_group<DT, G, 2>(ggrid, lds, s, a); return;
+        case 3: launch_group<DT, G, 3>(ggrid, lds, s, a); return;
+        default: launch_group<DT, G, 4>(ggrid, lds, s, a); return;
+      }
+    }
     if (p.mfma) {
       switch (p.waves) {
         case 8: launch_mfma<DT, G, 8>(p, grid, s, a); return;
@@ -415,6 +465,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   if (const char* e = std::getenv("FERRY_STEAL_CHUNK")) c->steal_chunk = (uint32_t)std::max(1, std::atoi(e));
   if (const char* e = std::getenv("FERRY_THIEF_WAVES")) c->thief_waves = std::max(1, std::atoi(e));
   if (const char* e = std::getenv("FERRY_STEAL_INFLIGHT")) c->steal_inflight = std::max(1, std::atoi(e));
+  if (const char* e = std::getenv("FERRY_ATTN_GROUPED")) c->attn_grouped = std::atoi(e) != 0;
   if (const char* e = std::getenv("FERRY_ATTN_LOADS"))
     c->attn_loads = std::string(e) == "nt" ? 1 : (std::string(e) == "temporal" ? 2 : 0);
   c->device = device;
@@ -881,6 +932,15 @@ int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const flo
   const AttnPlan p = attn_plan(ctx);
   launch_attn(p, grid, (hipStream_t)stream, a);
   HIPC(hipGetLastError());
+  return FERRY_OK;
+}
+
+int ferry_attn_kernel(const ferry_ctx* ctx, int32_t* kind, int32_t* waves) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!kind || !waves) return fail(FERRY_EINVAL, "null output");
+  const AttnPlan p = attn_plan(ctx);
+  *kind = p.grouped ? FERRY_ATTN_GROUP : p.mfma ? FERRY_ATTN_MFMA : FERRY_ATTN_VALU;
+  *waves = p.waves;
   return FERRY_OK;
 }
 

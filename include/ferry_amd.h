@@ -51,9 +51,16 @@ extern "C" {
 #define FERRY_ASSIGN_AFFINITY 1 /* request (owner) modulo workers */
 
 /* ---- attention kernel selection ---- */
-#define FERRY_ATTN_AUTO 0 /* MFMA for GQA groups (q_heads/kv_heads >= 2) of 16/8-bit KV, else VALU */
+#define FERRY_ATTN_AUTO 0 /* MFMA for GQA groups (q_heads/kv_heads >= 2) of 16/8-bit KV, else VALU;
+                            prefix groups (group > 1) that fit FERRY_ATTN_GROUP use it */
 #define FERRY_ATTN_VALU 1 /* vector-ALU kernel for every shape */
-#define FERRY_ATTN_MFMA 2 /* MFMA kernel; needs q_heads/kv_heads >= 2 and 16/8-bit KV */
+#define FERRY_ATTN_MFMA 2 /* MFMA kernel per (request, layer, kv head) row; needs
+                            q_heads/kv_heads >= 2 and 16/8-bit KV */
+#define FERRY_ATTN_GROUP 3 /* MFMA kernel per (prefix group, layer, kv head): every distinct
+                             block of the group's set is read from HBM once for all members.
+                             Needs group > 1, q_heads/kv_heads >= 2, 16/8-bit KV,
+                             group * q_heads/kv_heads <= 64, group * k <= 2048 and
+                             slots_per_set + group * k <= 12288 */
 
 /* Geometry and policy of one executor.  Sets are (owner, layer, kv head)
  * with owner = request / group; each set owns slots_per_set slots of the HBM
@@ -248,11 +255,23 @@ int ferry_missq_drain(ferry_ctx* ctx, void* stream);
  *   slots [B][L][Hkv][k] pool slots from ferry_fetch_step (device)
  *   out   [B][L][Hq][D] fp32 (device)
  * softmax(q K^T / sqrt(D)) V over every token of the k blocks, fp32
- * accumulation, online softmax.  Replaces the FMA proxy attn_kernel /
+ * accumulation, online softmax.  A slot selected twice in one row counts
+ * twice; a row with no slot (all FERRY_EMPTY) gives 0; a slot outside the pool
+ * is read as slot 0 and reported as FERRY_ERANGE.  With the prefix-group
+ * kernel (FERRY_ATTN_GROUP) a member row's slots are expected in its group's
+ * set (as ferry_fetch_step assigns them); other in-pool slots are attended
+ * correctly on a slower path.  Replaces the FMA proxy attn_kernel /
  * wla_attn_kernel (src/workloads/kv_exec.cuh:30-37,
  * src/runtime/wla_multigpu.cuh:96-103). */
 int ferry_sparse_decode(ferry_ctx* ctx, const float* q, const uint32_t* slots,
                         float* out, void* stream);
+
+/* Which attention kernel ferry_sparse_decode runs for this context:
+ * *kind = FERRY_ATTN_VALU, FERRY_ATTN_MFMA (one workgroup per request row) or
+ * FERRY_ATTN_GROUP (one per prefix-group set), *waves = wavefronts per
+ * workgroup.  No reference counterpart (the reference has one proxy kernel);
+ * for callers that report rooflines per kernel. */
+int ferry_attn_kernel(const ferry_ctx* ctx, int32_t* kind, int32_t* waves);
 
 /* Attention of layers [l0, l0 + nl) only. */
 int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,

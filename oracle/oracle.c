@@ -1450,27 +1450,33 @@ void ora_host_fill(const ora_geom* g, uint8_t* host, float* host_scales) {
  * p = softmax(s) over every token of every selected block, out = sum p_t V_t
  * (the semantics the reference's FMA proxy stands in for,
  * src/workloads/kv_exec.cuh:30-37; selection as in
- * tools/capture_miss_trace.py:146-159). */
-int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
-                      double* out) {
+ * tools/capture_miss_trace.py:146-159).  Rows name their blocks by host-tier
+ * index: hidx [B][L][Hkv][k], ORA_NONE64 for an empty position (skipped); a
+ * block named twice in a row is attended twice. */
+int ora_attention_hidx_f64(const ora_geom* g, const uint64_t* hidx, const float* q,
+                           double* out) {
   const int L = g->n_layers, Hq = g->q_heads, Hk = g->kv_heads, D = g->head_dim;
   const int T = g->block_tokens, k = g->k, grp = Hq / Hk;
   const int ntok_max = k * T;
   double* s = (double*)malloc((size_t)ntok_max * sizeof(double));
   double* V = (double*)malloc((size_t)ntok_max * D * sizeof(double));
   double* K = (double*)malloc((size_t)ntok_max * D * sizeof(double));
+  if (!s || !V || !K) {
+    free(s);
+    free(V);
+    free(K);
+    return -1;
+  }
   const double isd = 1.0 / sqrt((double)D);
   for (int r = 0; r < g->n_req; ++r) {
-    const int o = r / g->group;
     for (int l = 0; l < L; ++l)
       for (int h = 0; h < Hk; ++h) {
-        const uint32_t set = (uint32_t)((o * L + l) * Hk + h);
-        const uint32_t* bl = sel + ((size_t)(r * L + l) * Hk + h) * k;
+        const uint64_t* bl = hidx + ((size_t)(r * L + l) * Hk + h) * k;
         int nv = 0; /* selected blocks of the row, empty positions skipped */
         for (int jj = 0; jj < k; ++jj) {
-          if (bl[jj] == ORA_NONE) continue;
+          if (bl[jj] == ORA_NONE64) continue;
           const int j = nv++;
-          const uint64_t hi = ora_host_index(g, set, bl[jj]);
+          const uint64_t hi = bl[jj];
           const double sk = ora_host_scale(g, hi, 0), sv = ora_host_scale(g, hi, 1);
           for (int t = 0; t < T; ++t)
             for (int d = 0; d < D; ++d) {
@@ -1513,6 +1519,30 @@ int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
   free(V);
   free(K);
   return 0;
+}
+
+/* The same over block ids: row (r, l, h) selects blocks of its owner's set
+ * (r / group, l, h), host index ora_host_index(set, block). */
+int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
+                      double* out) {
+  const int L = g->n_layers, Hk = g->kv_heads, k = g->k;
+  const size_t n = (size_t)g->n_req * L * Hk * k;
+  uint64_t* hidx = (uint64_t*)malloc(n * sizeof(uint64_t));
+  if (!hidx) return -1;
+  for (int r = 0; r < g->n_req; ++r) {
+    const int o = r / g->group;
+    for (int l = 0; l < L; ++l)
+      for (int h = 0; h < Hk; ++h) {
+        const uint32_t set = (uint32_t)((o * L + l) * Hk + h);
+        const size_t row = ((size_t)(r * L + l) * Hk + h) * k;
+        for (int jj = 0; jj < k; ++jj)
+          hidx[row + jj] =
+              sel[row + jj] == ORA_NONE ? ORA_NONE64 : ora_host_index(g, set, sel[row + jj]);
+      }
+  }
+  const int rc = ora_attention_hidx_f64(g, hidx, q, out);
+  free(hidx);
+  return rc;
 }
 
 static float load_elem_f32(int dtype, const uint8_t* p, size_t i) {

@@ -50,6 +50,7 @@ extern "C" {
 #endif
 
 #define ORA_NONE 0xFFFFFFFFu
+#define ORA_NONE64 0xFFFFFFFFFFFFFFFFull
 
 /* dtype codes shared with include/ferry_amd.h */
 enum { ORA_F32 = 0, ORA_F16 = 1, ORA_BF16 = 2, ORA_FP8 = 3 };
@@ -309,6 +310,11 @@ int ora_select_mass(const ora_geom* g, const float* q, const int* ctx_blocks, ui
  * (set, block).  q, out: [B][L][Hq][D] (q fp32, out fp64). */
 int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
                       double* out);
+/* The same with every row's blocks named by host-tier index: hidx
+ * [B][L][Hkv][k], ORA_NONE64 for an empty position; a block named twice in
+ * one row is attended twice. */
+int ora_attention_hidx_f64(const ora_geom* g, const uint64_t* hidx, const float* q,
+                           double* out);
 /* Same attention, but K/V read from a host pool image laid out like the HBM
  * pool (slot-major, bb bytes per slot, scales[slot][2]) through the slot
  * table; fp32 accumulation.  Used by the CPU baseline. */

@@ -138,6 +138,7 @@ _sig("ora_host_scale", C.c_float, C.POINTER(Geom), C.c_uint64, C.c_int)
 _sig("ora_host_block", None, C.POINTER(Geom), C.c_uint64, C.c_void_p, C.c_void_p)
 _sig("ora_host_fill", None, C.POINTER(Geom), C.c_void_p, C.c_void_p)
 _sig("ora_attention_f64", C.c_int, C.POINTER(Geom), _u32p, _f32p, _f64p)
+_sig("ora_attention_hidx_f64", C.c_int, C.POINTER(Geom), _u64p, _f32p, _f64p)
 _sig("ora_attention_pool_f32", C.c_int, C.POINTER(Geom), _u32p, C.c_void_p, C.c_void_p,
      _f32p, _f32p)
 _sig("ora_summary", None, C.POINTER(Geom), C.c_uint64, _f32p, _f32p)
@@ -368,6 +369,20 @@ def attention_f64(g: Geom, sel, q):
     if rc:
         raise RuntimeError("ora_attention_f64")
     return out.reshape(q.shape)
+
+
+def attention_hidx_f64(g: Geom, hidx, q):
+    """Attention with each row's blocks given as host-tier indices
+    ([B][L][Hkv][k] uint64, NONE64 = empty position)."""
+    out = np.zeros(q.size, np.float64)
+    rc = lib.ora_attention_hidx_f64(C.byref(g), np.ascontiguousarray(hidx, np.uint64).reshape(-1),
+                                    np.ascontiguousarray(q, np.float32).reshape(-1), out)
+    if rc:
+        raise RuntimeError("ora_attention_hidx_f64")
+    return out.reshape(q.shape)
+
+
+NONE64 = np.uint64(0xFFFFFFFFFFFFFFFF)
 
 
 def host_index(g: Geom, set_id, block):

@@ -283,6 +283,57 @@ def test_attention_f64_against_numpy(dtype, hq, hk):
                 assert np.allclose(out[r, l, hh], ref, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("dtype", [O.F16, O.BF16, O.FP8])
+def test_attention_hidx_rows_against_numpy(dtype):
+    # rows that name host blocks directly: a repeated block counts twice, a
+    # block of another set is just another block, empty positions are skipped
+    B, L, hk, hq, k = 2, 1, 2, 4, 6
+    g = O.make_geom(n_req=B, n_layers=L, kv_heads=hk, q_heads=hq, k=k, cap=8, max_blocks=40,
+                    dtype=dtype, host_blocks=97)
+    rng = np.random.default_rng(11)
+    rows = [[(0, 3), (0, 3), (0, 9), (1, 22), None, (0, 9)],
+            [None] * k,
+            [(1, 5), None, (3, 5), (3, 5), (3, 5), (2, 39)],
+            [(2, 0), (0, 0), (1, 0), (3, 0), (2, 0), None]]
+    hidx = np.full((B * L * hk, k), O.NONE64, np.uint64)
+    for r, row in enumerate(rows):
+        for j, e in enumerate(row):
+            if e is not None:
+                hidx[r, j] = O.host_index(g, *e)
+    q = rng.standard_normal((B, L, hq, 128)).astype(np.float32)
+    out = O.attention_hidx_f64(g, hidx, q)
+    grp = hq // hk
+    for r in range(B):
+        for hh in range(hq):
+            row = rows[r * hk + hh // grp]
+            picked = [e for e in row if e is not None]
+            if not picked:
+                assert np.all(out[r, 0, hh] == 0.0)
+                continue
+            kv = [_gather_kv(g, s, [b]) for s, b in picked]
+            K = np.concatenate([a for a, _ in kv])
+            V = np.concatenate([b for _, b in kv])
+            s = K @ q[r, 0, hh].astype(np.float64) / np.sqrt(128)
+            p = np.exp(s - s.max())
+            assert np.allclose(out[r, 0, hh], (p / p.sum()) @ V, rtol=1e-12, atol=1e-12)
+    # named through the block ids of the rows' own sets, it is attention_f64
+    sel = np.stack([rng.choice(40, k, replace=False) for _ in range(B * L * hk)]).astype(np.uint32)
+    sel[1, 2] = O.NONE
+    own = np.full_like(hidx, O.NONE64)
+    for r in range(B * L * hk):
+        for j in range(k):
+            if sel[r, j] != O.NONE:
+                own[r, j] = O.host_index(g, r, int(sel[r, j]))
+    assert np.array_equal(O.attention_hidx_f64(g, own, q), O.attention_f64(g, sel, q))
+    # a row that names one block twice attends exactly as one naming it once
+    one = np.full_like(hidx, O.NONE64)
+    two = np.full_like(hidx, O.NONE64)
+    one[:, 0] = own[:, 0]
+    two[:, 0] = two[:, 3] = own[:, 0]
+    assert np.allclose(O.attention_hidx_f64(g, one, q), O.attention_hidx_f64(g, two, q),
+                       rtol=1e-13, atol=1e-13)
+
+
 def test_attention_special_cases():
     g = O.make_geom(n_req=1, n_layers=1, kv_heads=1, k=3, cap=4, max_blocks=8, dtype=O.F32,
                     host_blocks=16)
