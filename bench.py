@@ -48,6 +48,7 @@ reference's bench_queue test, against the ticket rate of one shared word),
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -955,38 +956,43 @@ def main():
             others[name]["preroll_steps"] = o["preroll"]["steps"]
             others[name]["roofline"] = {k2: o["roofline"][k2] for k2 in
                                         ("kernel", "achieved", "peak", "unit", "frac",
-                                         "plain_gather_gbs", "frac_of_plain_gather")}
+                                         "plain_gather_gbs", "plain_gather_distinct_gbs",
+                                         "frac_of_plain_gather", "distinct_blocks_per_launch",
+                                         "bytes_per_launch", "effective_gbs")
+                                        if k2 in o["roofline"]}
             others[name]["roofline_fetch"] = {k2: o["roofline_fetch"][k2] for k2 in
                                               ("kernel", "achieved", "peak", "unit", "frac",
                                                "plain_read_gbs", "frac_of_plain_read")}
             print(json.dumps({name: others[name]}), file=sys.stderr, flush=True)
     # HBM traffic per launch is not measured in this run: it comes from two
     # rocprofv3 counter runs of the same workload (FETCH_SIZE, WRITE_SIZE),
-    # stored in profiles/traffic.json with the commit they were measured at
+    # stored in profiles/traffic.json with the commit each entry was measured at
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     tj = json.load(open(tpath)) if os.path.exists(tpath) else {}
     src = tj.get("measured_at", {})
-    label = (f"stored counters: profiles/traffic.json, measured at commit {src.get('commit')} "
-             f"({src.get('source')})" if src else None)
 
-    def stored(key, fields):
-        e = tj.get(a.workload + key)
-        return ({f: e[f] for f in fields} if e else None)
+    def put(obj, key, fields):
+        """obj["traffic"] = the stored entry's fields (one field: its value)."""
+        if obj is None or obj.get("skipped"):
+            return
+        e = tj.get(key)
+        bare = lambda s: re.sub(r"<[^>]*>", "", s)  # noqa: E731  kernel names without templates
+        if e is None or bare(e.get("kernel", "")) != bare(obj.get("kernel", "")):
+            obj["traffic"], obj["traffic_source"] = None, None  # no entry for this kernel
+            return
+        obj["traffic"] = e[fields[0]] if len(fields) == 1 else {f: e[f] for f in fields}
+        obj["traffic_source"] = (f"stored counters: profiles/traffic.json[{key}], measured at "
+                                 f"commit {e.get('commit', src.get('commit'))} "
+                                 f"({src.get('source')})")
 
-    def put(obj, value):
-        if obj is not None and not obj.get("skipped"):
-            obj["traffic"] = value
-            obj["traffic_source"] = label if value is not None else None
-
-    put(r["roofline"], (tj.get(a.workload) or {}).get("bytes_per_launch"))
-    put(r["roofline_fetch"], stored("_fetch", ("read_bytes", "write_bytes")))
-    put(r.get("roofline_select"), (tj.get(a.workload + "_select") or {}).get("bytes_per_launch"))
-    put(r.get("roofline_select_mass"), (tj.get(a.workload + "_mass") or {}).get("bytes_per_launch"))
-    put(r.get("roofline_handoff"), stored("_handoff", ("export_bytes", "import_bytes")))
+    put(r["roofline"], a.workload, ("bytes_per_launch",))
+    put(r["roofline_fetch"], a.workload + "_fetch", ("read_bytes", "write_bytes"))
+    put(r.get("roofline_select"), a.workload + "_select", ("bytes_per_launch",))
+    put(r.get("roofline_select_mass"), a.workload + "_mass", ("bytes_per_launch",))
+    put(r.get("roofline_handoff"), a.workload + "_handoff", ("export_bytes", "import_bytes"))
     for name, o in others.items():
-        put(o["roofline"], (tj.get(name) or {}).get("bytes_per_launch"))
-        e = tj.get(name + "_fetch")
-        put(o["roofline_fetch"], {f: e[f] for f in ("read_bytes", "write_bytes")} if e else None)
+        put(o["roofline"], name, ("bytes_per_launch",))
+        put(o["roofline_fetch"], name + "_fetch", ("read_bytes", "write_bytes"))
     lo, hi = w["ctx"]
     desc = (f"B={w['B']}, L={w['L']}, Hq={w['Hq']}, Hkv={w['Hkv']}, D=128, {w['dtype']} KV, "
             f"16-token blocks, ctx {'U[%d,%d]' % (lo * 16, hi * 16) if lo != hi else lo * 16} "
@@ -1010,7 +1016,8 @@ def main():
                         "top_k": w["k"]}, **r.pop("config_extra")),
     }
     for key in ("miss_rate", "preroll", "gate", "gate_detail", "miss_blocks_per_s",
-                "miss_blocks_per_s_fetch_kernel", "attention_tok_per_s", "kernel_ms", "roofline",
+                "miss_blocks_per_s_fetch_kernel", "fetched_blocks_per_event_step",
+                "attention_tok_per_s", "kernel_ms", "roofline",
                 "roofline_fetch", "roofline_select", "roofline_select_mass", "roofline_handoff",
                 "steals_per_step", "selection_gen_s", "cpu_baseline"):
         if key in r:
