@@ -11,7 +11,8 @@
 // (group, layer, kv head) (src/runtime/wla_multigpu.cuh:323-349, wla_gslot_off),
 // so the members' selections of the shared prefix land on the same slots.
 //
-// One workgroup of four wavefronts per (group, layer, kv head).  The group's
+// One workgroup of W = 4 wavefronts per (group, layer, kv head), two per CU
+// (the LDS is mostly the wavefronts' block rings).  The group's
 // query columns (member x query head, NTILE tiles of 16, attn_mfma.hpp) are
 // held by every wavefront; the blocks are split between the wavefronts.
 //  1. List: every member row's slots are OR-ed into a per-slot member mask in
@@ -20,14 +21,15 @@
 //     member alone.  The masks are compacted in slot order, then the own
 //     entries ordered by (member, slot), so the list and the summation order
 //     do not depend on the order the atomics ran in.
-//  2. Blocks: entry j of the list goes to wavefront j mod 4, which streams its
+//  2. Blocks: entry j of the list goes to wavefront j mod W, which streams its
 //     entries through its own ring of R blocks in LDS (three fp8 or two 16-bit
 //     blocks) with direct-to-LDS
 //     16-byte loads (global_load_lds_dwordx4, non-temporal: each block is read
 //     once), R - 1 blocks ahead, waiting only on its own load counter: no
-//     workgroup barrier in the loop.  Token rows keep their 16-byte chunks
-//     XOR-swizzled by (row mod 8), so the K and V reads of eight rows at one
-//     offset fall on eight different bank groups.
+//     workgroup barrier in the loop.  The block's rows and 16-byte chunks are
+//     permuted (lds_row, lds_chunk) so that the K reads (one row per lane, one
+//     chunk offset) and the V reads (four rows across the wavefront) hit
+//     distinct banks whether the LDS serves 128 or 256 bytes per pass.
 //  3. Attention: a block's K and V operands are built once (block_operands)
 //     and every query tile with a member that selected the block attends to
 //     it (tile_block); the columns of members that did not are masked, so
@@ -35,7 +37,7 @@
 //     operands wait in LDS (one conflict-free 16-byte read per lane and
 //     k-slice), so a wavefront's registers hold the accumulators of all its
 //     columns but only one tile's queries at a time.
-//  4. Merge: the four wavefronts' partial softmax states of each column are
+//  4. Merge: the W wavefronts' partial softmax states of each column are
 //     combined through LDS (max, rescaled sums and outputs), as k_attn_mfma
 //     merges its wavefronts.
 // HBM bytes per launch: the distinct blocks of each group set once (plus q in,
@@ -54,6 +56,23 @@ typedef __attribute__((address_space(1))) void glb_void;
 
 // Wait until at most N vector-memory loads of this wavefront are outstanding.
 // The "memory" clobber keeps the LDS reads of the landed block below it.
+// Block layout in LDS.  Row t (0..15) of a K or V tile is stored as row
+// lds_row(t), and its logical 16-byte chunk c at chunk c ^ lds_chunk(row).
+// fp8 rows are 128 bytes, two to a 256-byte bank line: rows 4..7 and 12..15
+// swap within their pairs, so the V rows 4g+i read together (g = 0..3) fall
+// in different halves of a line, and the chunk key (p ^ p/8) mod 8 differs
+// between the eight rows of one half and between rows 0..7 (and 8..15), so
+// the K reads (rows 0..15, one chunk offset) are conflict-free.  16-bit rows
+// are 256 bytes: the chunk key is the row number.
+template <int ES>
+__device__ inline int lds_row(int t) {
+  return ES == 1 ? t ^ ((t >> 2) & 1) : t;  // an involution
+}
+template <int ES>
+__device__ inline int lds_chunk(int p) {
+  return ES == 1 ? (p ^ (p >> 3)) & 7 : p & 15;
+}
+
 template <int N>
 __device__ inline void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
@@ -102,7 +121,7 @@ __device__ inline int block_exclusive_scan(int v, int* sh, int* total) {
 }  // namespace
 
 template <int DT, int G, int NTILE>
-__global__ __launch_bounds__(kGroupWaves * 64) void k_attn_group(
+__global__ __launch_bounds__(group_waves(DT) * 64) void k_attn_group(
     Geo g, const float* __restrict__ q, const uint32_t* __restrict__ slots,
     const uint8_t* __restrict__ pool, const float* __restrict__ pool_scales,
     float* __restrict__ out, float qscale, int l0, int nl, int* __restrict__ err) {
@@ -110,19 +129,20 @@ __global__ __launch_bounds__(kGroupWaves * 64) void k_attn_group(
   static_assert(NTILE >= 1 && NTILE <= kGroupMaxTiles, "query tiles per workgroup");
   static_assert(DT == FERRY_F16 || DT == FERRY_BF16 || DT == FERRY_FP8_E4M3, "16/8-bit KV");
   using S = Shape<DT>;
-  constexpr int D = S::D, T = S::T, NKW = S::NKW, VW = S::VW;
+  constexpr int D = S::D, T = S::T, NKW = S::NKW, VW = S::VW, ES = S::ES;
   constexpr int ROW = (int)S::ROW;     // bytes of one token row
   constexpr int RC = ROW / 16;         // 16-byte chunks of a row (8 or 16)
   constexpr int BB = 2 * T * ROW;      // bytes of one block, K tile then V tile
   constexpr int NI = BB / 1024;        // direct-to-LDS loads of one block per wavefront
-  constexpr int W = kGroupWaves;       // wavefronts
+  constexpr int W = group_waves(DT);   // wavefronts
   constexpr int NT = W * 64;           // threads
   constexpr int MPT = 16 / G;          // members per query tile
   constexpr int R = group_ring_blocks(DT);   // ring blocks per wavefront
   constexpr int RB = group_ring_bytes(DT);    // ring bytes per wavefront
   constexpr int NQ = S::BF ? 2 : 1;           // parts of the Q^T operands (bf16: hi, lo)
   constexpr int COLS = 16 * NTILE;            // query columns
-  constexpr int TR = RB / (16 * D * 4);       // tiles merged per round
+  constexpr int DP = D + 4;                   // floats per merged column (bank offset)
+  constexpr int TR = RB / (16 * DP * 4);      // tiles merged per round
   static_assert(RB == R * BB && R >= 2 && (R - 2) * NI < 64, "ring depth and load counter");
   static_assert(TR >= 1, "a merge round fits the rings");
 
@@ -136,7 +156,7 @@ __global__ __launch_bounds__(kGroupWaves * 64) void k_attn_group(
   int* sh = reinterpret_cast<int*>(red_ml + W * COLS * 2);                // [W] scan
   uint32_t* msk = reinterpret_cast<uint32_t*>(rings);                     // [C] listing
   uint32_t* own = msk + g.C;                                              // [GK] listing
-  float* red_o = reinterpret_cast<float*>(rings);                         // [W][TR*16][D] merge
+  float* red_o = reinterpret_cast<float*>(rings);                         // [W][TR*16][DP] merge
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15, grp = lane >> 4;
@@ -242,16 +262,17 @@ __global__ __launch_bounds__(kGroupWaves * 64) void k_attn_group(
   // ---- 2./3. this wavefront's entries wave, wave + W, ... through its ring
   const int nb = nlist > wave ? (nlist - wave + W - 1) / W : 0;
   uint8_t* ring = rings + wave * RB;
-  // block j of this wavefront into ring slot b: lane loads chunk p = i*64 +
-  // lane of the block, which holds logical chunk (p mod RC) ^ (row mod 8)
+  // block j of this wavefront into ring slot b: lane fills chunk p = i*64 +
+  // lane of the block: LDS row pr of its tile holds token row lds_row(pr),
+  // whose logical chunk (p mod RC) ^ lds_chunk(pr) sits there
   auto issue = [&](int j, int b) {
     const uint32_t slot = (uint32_t)__builtin_amdgcn_readfirstlane((int)lslot[wave + W * j]);
     const uint8_t* src = pool + (uint64_t)slot * BB;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int p = i * 64 + lane;
-      const int t = (p / RC) % T;  // token row within its tile
-      const int off = (p / RC) * ROW + ((p % RC) ^ (t & 7)) * 16;
+      const int tile = p / (T * RC), pr = (p / RC) % T;
+      const int off = (tile * T + lds_row<ES>(pr)) * ROW + ((p % RC) ^ lds_chunk<ES>(pr)) * 16;
       __builtin_amdgcn_global_load_lds((glb_void*)(src + off),
                                        (lds_void*)(ring + b * BB + i * 1024), 16, 0, 2 /* nt */);
     }
@@ -259,20 +280,22 @@ __global__ __launch_bounds__(kGroupWaves * 64) void k_attn_group(
   // K word w of lane (n, grp): token n, logical chunk 4w + grp.  V of token i:
   // row 4*grp + i of the V tile, elements 8n..8n+7 (logical chunk n/2, half n%2
   // for fp8; chunk n for 16-bit).
+  const int kr = lds_row<ES>(n);
   auto read_block = [&](const uint8_t* blk, u32x4 (&kw)[NKW], uint32_t (&vw)[4][VW]) {
 #pragma unroll
     for (int w = 0; w < NKW; ++w)
-      kw[w] = *reinterpret_cast<const u32x4*>(blk + n * ROW + (((4 * w + grp) ^ (n & 7)) * 16));
+      kw[w] = *reinterpret_cast<const u32x4*>(blk + kr * ROW +
+                                              (((4 * w + grp) ^ lds_chunk<ES>(kr)) * 16));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t = 4 * grp + i;
-      const uint8_t* vrow = blk + T * ROW + t * ROW;
+      const int vr = lds_row<ES>(4 * grp + i);
+      const uint8_t* vrow = blk + (T + vr) * ROW;
       if constexpr (S::F8) {
-        const u32x2 v =
-            *reinterpret_cast<const u32x2*>(vrow + (((n >> 1) ^ (t & 7)) * 16) + (n & 1) * 8);
+        const u32x2 v = *reinterpret_cast<const u32x2*>(
+            vrow + (((n >> 1) ^ lds_chunk<ES>(vr)) * 16) + (n & 1) * 8);
         vw[i][0] = v[0], vw[i][1] = v[1];
       } else {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(vrow + ((n ^ (t & 7)) * 16));
+        const u32x4 v = *reinterpret_cast<const u32x4*>(vrow + ((n ^ lds_chunk<ES>(vr)) * 16));
         vw[i][0] = v[0], vw[i][1] = v[1], vw[i][2] = v[2], vw[i][3] = v[3];
       }
     }
@@ -344,7 +367,7 @@ __global__ __launch_bounds__(kGroupWaves * 64) void k_attn_group(
 #pragma unroll
     for (int t = t0; t < min(t0 + TR, NTILE); ++t) {
       const float vref = S::F8 ? acc[t].vs_ref : 1.0f;
-      float* ro = red_o + ((size_t)wave * TR * 16 + (t - t0) * 16 + n) * D + 32 * grp;
+      float* ro = red_o + ((size_t)wave * TR * 16 + (t - t0) * 16 + n) * DP + 32 * grp;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float4* op = reinterpret_cast<float4*>(ro + 8 * i);
@@ -369,7 +392,7 @@ __global__ __launch_bounds__(kGroupWaves * 64) void k_attn_group(
       for (int w = 0; w < W; ++w) {
         const float f = exp2_fast(red_ml[(w * COLS + col) * 2] - mx);
         lt += red_ml[(w * COLS + col) * 2 + 1] * f;
-        ot += red_o[((size_t)w * TR * 16 + c) * D + d] * f;
+        ot += red_o[((size_t)w * TR * 16 + c) * DP + d] * f;
       }
       const size_t qrow =
           (size_t)((o * g.group + mi) * g.L + l) * g.Hq + (size_t)h * G + (col % 16) % G;

@@ -37,7 +37,7 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
   constexpr uint32_t ROW = S::ROW, KTILE = S::KTILE;
   constexpr int NPF = 3;  // prefetch ring depth
 
-  __shared__ float red_o[W][G][D];
+  __shared__ float red_o[W][G][D + 4];  // +4: the 16 columns' rows start on different banks
   __shared__ float red_ml[W][G][2];
   __shared__ uint32_t ids[kMaxTopK];
   __shared__ int id_cnt[kMaxTopK / 64];

@@ -162,15 +162,18 @@ namespace {
 
 // Whether the prefix-group attention kernel (k_attn_group) can run this
 // geometry: every wavefront holds all group * G query columns (at most
-// kGroupMaxTiles tiles of 16), the distinct list has group * k entries, and
-// the per-slot member masks plus the list's scratch fit the block rings while
-// the list is built.
+// kGroupMaxTiles tiles of 16), the workgroup's LDS fits one CU, and the
+// per-slot member masks plus the list's scratch fit the block rings while the
+// list is built.
 bool group_attn_fits(const ferry_config* c) {
   const int G = c->q_heads / c->kv_heads;
+  if (c->group < 2 || G < 2 || c->dtype == FERRY_F32 || c->group * G > 16 * kGroupMaxTiles)
+    return false;
   const long gk = (long)c->group * c->k;
-  return c->group > 1 && G >= 2 && c->dtype != FERRY_F32 && c->group * G <= 16 * kGroupMaxTiles &&
-         gk <= 2048 &&
-         4 * ((long)c->slots_per_set + gk) <= (long)kGroupWaves * group_ring_bytes(c->dtype);
+  const int ntile = (c->group * G + 15) / 16;
+  return attn_group_lds_bytes(c->dtype, ntile, gk) <= (size_t)kGroupMaxLds &&
+         4 * ((long)c->slots_per_set + gk) <=
+             (long)group_waves(c->dtype) * group_ring_bytes(c->dtype);
 }
 
 int validate(const ferry_config* c) {
@@ -199,7 +202,8 @@ int validate(const ferry_config* c) {
   if (c->attn == FERRY_ATTN_GROUP && !group_attn_fits(c))
     return fail(FERRY_EINVAL,
                 "the prefix-group attention kernel needs group > 1, group * q_heads/kv_heads <= 64, "
-                "group * k <= 2048 and slots_per_set + group * k <= 12288");
+                "its LDS (rings, queries, group * k list entries) within 160 KiB and "
+                "slots_per_set + group * k within its rings");
   if (c->fetch_workers < 0) return fail(FERRY_EINVAL, "fetch_workers < 0");
   if (c->cap_mode != FERRY_CAP_GROUP && c->cap_mode != FERRY_CAP_PER_MEMBER)
     return fail(FERRY_EINVAL, "bad cap_mode");
@@ -295,7 +299,7 @@ AttnPlan attn_plan(const ferry_ctx* ctx) {
   if (ctx->attn_waves == 8) p.waves = 8;
   p.tiles = 0;
   if (p.grouped) {  // tiles of 16 query columns held by every wavefront
-    p.waves = kGroupWaves;
+    p.waves = group_waves(g.dtype);
     p.tiles = (g.group * p.G + 15) / 16;
   }
   p.nt = ctx->attn_loads ? ctx->attn_loads == 1 : g.group == 1;
@@ -325,9 +329,9 @@ void launch_group(const dim3& grid, size_t lds, hipStream_t s, const AttnArgs& a
   // more than the default 64 KiB of dynamic LDS: allowed once per instance
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&k_attn_group<DT, G, NT>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      hipFuncAttributeMaxDynamicSharedMemorySize, kGroupMaxLds);
   (void)attr;
-  hipLaunchKernelGGL((k_attn_group<DT, G, NT>), grid, dim3(kGroupWaves * 64), lds, s, a.g, a.q,
+  hipLaunchKernelGGL((k_attn_group<DT, G, NT>), grid, dim3(group_waves(DT) * 64), lds, s, a.g, a.q,
                      a.slots, a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
 }
 template <int DT, int G>
@@ -335,7 +339,7 @@ void launch_g(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs
   if constexpr (DT != FERRY_F32 && G >= 2) {
     if (p.grouped) {
       const dim3 ggrid((unsigned)(a.g.n_owners * a.nl * a.g.Hkv));
-      const size_t lds = attn_group_lds_bytes(a.g, p.tiles);
+      const size_t lds = attn_group_lds_bytes(a.g.dtype, p.tiles, (long)a.g.group * a.g.k);
       switch (p.tiles) {
         case 1: launch_group<DT, G, 1>(ggrid, lds, s, a); return;
         case 2: launch_group<DT, G, 2>(ggrid, lds, s, a); return;
