@@ -121,7 +121,6 @@ struct ferry_ctx {
   uint64_t steps = 0;
   std::vector<hipEvent_t> events;   // layer-chunk pipeline of ferry_decode_step: fetch done
   std::vector<hipEvent_t> booked;   // ... and bookkeeping done
-  hipStream_t book = nullptr;       // ... whose bookkeeping runs on this stream
   int attn_waves = 0;              // wavefronts per attention workgroup (FERRY_ATTN_WAVES), 0 = default
   int fetch_waves = 0;             // wavefronts per fetch workgroup (FERRY_FETCH_WAVES: 1, 2, 4; 0 = by rule)
   int fetch_prio = 1;              // fetch wavefronts issue first (FERRY_FETCH_PRIO=0: not)
@@ -238,7 +237,6 @@ void release(ferry_ctx* c) {
   }
   for (hipEvent_t e : c->events) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->booked) (void)hipEventDestroy(e);
-  if (c->book) (void)hipStreamDestroy(c->book);
   delete c;
 }
 
@@ -631,7 +629,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
     HIPT(hipMemcpy(c->lane_live, live.data(), (size_t)g.n_req * 4, hipMemcpyHostToDevice));
     HIPT(hipMemset(c->trim_gen, 0, (size_t)g.n_owners * 4));
   }
-  c->events.resize((size_t)g.L + 1, nullptr);
+  c->events.resize((size_t)g.L, nullptr);
   for (auto& e : c->events) HIPT(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   c->booked.resize((size_t)g.L, nullptr);
   for (auto& e : c->booked) HIPT(hipEventCreateWithFlags(&e, hipEventDisableTiming));
@@ -1030,31 +1028,39 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
       if (rc) return rc;
     }
   } else {
-    // Three streams.  Bookkeeping of range c (its own stream) pushes into ring
-    // c mod 2 and waits only for the fetch of range c - 2, the last user of
-    // that ring; the fetch of c (side stream) waits for its bookkeeping; the
-    // attention of c (main stream) for its fetch.  Ranges touch disjoint sets,
-    // slots and outputs, so the bookkeeping of c + 1 runs while c is fetched
-    // and the link does not wait for it.
-    if (!ctx->book) HIPC(hipStreamCreateWithFlags(&ctx->book, hipStreamNonBlocking));
-    HIPC(hipEventRecord(ctx->events[L], ms));  // slots the main stream still reads
-    HIPC(hipStreamWaitEvent(ss, ctx->events[L], 0));
-    HIPC(hipStreamWaitEvent(ctx->book, ctx->events[L], 0));
-    int prev[2] = {-1, -1};  // last range fetched from each ring
-    for (int c = 0; c < chunks; ++c) {
-      const int l0 = first[c], nl = first[c + 1] - first[c];
-      if (nl <= 0) continue;
-      const int r = c & 1;
-      if (prev[r] >= 0) HIPC(hipStreamWaitEvent(ctx->book, ctx->events[prev[r]], 0));
-      int rc = bookkeep_ring(ctx, l0, nl, sel, slots, miss_count, misses, nullptr, ctx->book, r);
+    // Two streams, the caller's.  The main stream books range c + 1 (into ring
+    // (c + 1) mod 2) before it waits for the fetch of range c and attends it;
+    // the side stream fetches range c + 1 once it is booked.  So range c + 1 is
+    // booked while range c is fetched, and the link waits for no bookkeeping
+    // as long as attending c - 1 and booking c + 1 take less than fetching c.
+    // Ring (c + 1) mod 2 was last drained by the fetch of c - 1, which the main
+    // stream waited for before attending c - 1.  Ranges touch disjoint sets,
+    // slots and outputs.  No stream of the context's own: a third stream can
+    // share a hardware queue with the side stream (HIP hands a process a few
+    // queues, shared among its streams) and then serialise with the fetch.
+    std::vector<int> live;  // ranges with layers
+    for (int c = 0; c < chunks; ++c)
+      if (first[c + 1] > first[c]) live.push_back(c);
+    auto book_fetch = [&](int i) -> int {
+      const int c = live[(size_t)i], l0 = first[c], nl = first[c + 1] - first[c];
+      int rc = bookkeep_ring(ctx, l0, nl, sel, slots, miss_count, misses, nullptr, ms, i & 1);
       if (rc) return rc;
-      HIPC(hipEventRecord(ctx->booked[c], ctx->book));
-      HIPC(hipStreamWaitEvent(ss, ctx->booked[c], 0));
-      if ((rc = drain_ring(ctx, ss, r))) return rc;
-      HIPC(hipEventRecord(ctx->events[c], ss));
-      prev[r] = c;
-      HIPC(hipStreamWaitEvent(ms, ctx->events[c], 0));
-      if ((rc = ferry_sparse_decode_layers(ctx, l0, nl, q, slots, out, ms))) return rc;
+      HIPC(hipEventRecord(ctx->booked[i], ms));
+      HIPC(hipStreamWaitEvent(ss, ctx->booked[i], 0));
+      if ((rc = drain_ring(ctx, ss, i & 1))) return rc;
+      HIPC(hipEventRecord(ctx->events[i], ss));
+      return FERRY_OK;
+    };
+    const int n = (int)live.size();
+    if (int rc = book_fetch(0)) return rc;
+    for (int i = 0; i < n; ++i) {
+      if (i + 1 < n)
+        if (int rc = book_fetch(i + 1)) return rc;
+      const int c = live[(size_t)i];
+      HIPC(hipStreamWaitEvent(ms, ctx->events[i], 0));
+      if (int rc = ferry_sparse_decode_layers(ctx, first[c], first[c + 1] - first[c], q, slots,
+                                              out, ms))
+        return rc;
     }
   }
   // the step's fetched blocks, for the next step's adaptive chunking
