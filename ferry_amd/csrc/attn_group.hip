@@ -54,8 +54,6 @@ namespace {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
 
-// Wait until at most N vector-memory loads of this wavefront are outstanding.
-// The "memory" clobber keeps the LDS reads of the landed block below it.
 // Block layout in LDS.  Row t (0..15) of a K or V tile is stored as row
 // lds_row(t), and its logical 16-byte chunk c at chunk c ^ lds_chunk(row).
 // fp8 rows are 128 bytes, two to a 256-byte bank line: rows 4..7 and 12..15
@@ -73,6 +71,8 @@ __device__ inline int lds_chunk(int p) {
   return ES == 1 ? (p ^ (p >> 3)) & 7 : p & 15;
 }
 
+// Wait until at most N vector-memory loads of this wavefront are outstanding.
+// The "memory" clobber keeps the LDS reads of the landed block below it.
 template <int N>
 __device__ inline void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
