@@ -55,6 +55,20 @@ __device__ inline uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) 
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Max over the four lanes n, n + 16, n + 32, n + 48 of column n, with the VALU
+// lane swaps of gfx950 instead of two LDS permutes.  With the same value in
+// both operands, v_permlane16_swap (v_permlane32_swap) hands every lane the
+// two values of its pair (l, l ^ 16) (resp. (l, l ^ 32)), the lower lane's
+// first (checked on MI355X), so both lanes of a pair get the same max.
+__device__ inline float max_over_groups(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+  const uint32_t v = __builtin_bit_cast(uint32_t, x);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+
 // Shapes of one block's operands for KV dtype DT.
 template <int DT>
 struct Shape {
@@ -197,8 +211,7 @@ __device__ __forceinline__ void tile_block(const Ops& op, float ks, float vs,
 #pragma unroll
   for (int t = 0; t < 4; ++t) sv[t] = s[t] * ks;
   float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-  bm = fmaxf(bm, __shfl_xor(bm, 16));
-  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  bm = max_over_groups(bm);
   const bool raise = (!MASK || live) && bm > a.m + kRescale;
   if (__builtin_amdgcn_ballot_w64(raise)) {  // uniform: some column's max moved up
     const float alpha = raise ? exp2_fast(a.m - bm) : 1.0f;
