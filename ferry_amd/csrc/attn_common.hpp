@@ -27,6 +27,39 @@ __device__ inline mx_u32x2 e4m3x4_to_f16(uint32_t w) {
   return mx_u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
 }
 
+// The two values of lane l's pair (l, l ^ 16) (X = 16) or (l, l ^ 32) (X = 32),
+// the lower lane's first, on both lanes of the pair: with the same value in
+// both operands, gfx950's v_permlane16_swap / v_permlane32_swap exchange
+// those lanes on the VALU (lane layout checked on MI355X), where __shfl_xor
+// takes an LDS permute and a wait.
+template <int X>
+__device__ inline mx_u32x2 pair_values(float x) {
+  static_assert(X == 16 || X == 32, "lane distance 16 or 32");
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  if constexpr (X == 16) return __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  else return __builtin_amdgcn_permlane32_swap(u, u, false, false);
+}
+
+// Max / sum over lanes n, n + 16, n + 32, n + 48 (the four 16-lane groups),
+// on every one of them.  The same bits as two __shfl_xor steps (16, then 32):
+// max and a two-term sum do not depend on the operands' order.
+__device__ inline float max_over_groups(float x) {
+#pragma unroll
+  for (int X = 16; X <= 32; X *= 2) {
+    const mx_u32x2 p = X == 16 ? pair_values<16>(x) : pair_values<32>(x);
+    x = fmaxf(__builtin_bit_cast(float, (uint32_t)p[0]), __builtin_bit_cast(float, (uint32_t)p[1]));
+  }
+  return x;
+}
+__device__ inline float sum_over_groups(float x) {
+#pragma unroll
+  for (int X = 16; X <= 32; X *= 2) {
+    const mx_u32x2 p = X == 16 ? pair_values<16>(x) : pair_values<32>(x);
+    x = __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+  }
+  return x;
+}
+
 // fp32 -> bf16 bits, round to nearest even (finite inputs)
 __device__ inline uint16_t bf16_rne(float x) {
   uint32_t u = __builtin_bit_cast(uint32_t, x);

@@ -55,19 +55,6 @@ __device__ inline uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) 
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Max over the four lanes n, n + 16, n + 32, n + 48 of column n, with the VALU
-// lane swaps of gfx950 instead of two LDS permutes.  With the same value in
-// both operands, v_permlane16_swap (v_permlane32_swap) hands every lane the
-// two values of its pair (l, l ^ 16) (resp. (l, l ^ 32)), the lower lane's
-// first (checked on MI355X), so both lanes of a pair get the same max.
-__device__ inline float max_over_groups(float x) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  x = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
-  const uint32_t v = __builtin_bit_cast(uint32_t, x);
-  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
-}
 
 // Shapes of one block's operands for KV dtype DT.
 template <int DT>

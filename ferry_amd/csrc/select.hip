@@ -852,11 +852,9 @@ __global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
 #pragma unroll
           for (int i = 0; i < 4; ++i) x[i] = s[i] * ksc[u];
           float m = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-          m = fmaxf(m, __shfl_xor(m, 16));
-          m = fmaxf(m, __shfl_xor(m, 32));
+          m = max_over_groups(m);
           float e = (exp2f(x[0] - m) + exp2f(x[1] - m)) + (exp2f(x[2] - m) + exp2f(x[3] - m));
-          e += __shfl_xor(e, 16);
-          e += __shfl_xor(e, 32);
+          e = sum_over_groups(e);
           if (head_lane) {
             ws[((size_t)b * G + n) * 2] = m;
             ws[((size_t)b * G + n) * 2 + 1] = e;
