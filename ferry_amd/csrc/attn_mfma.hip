@@ -105,8 +105,9 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
     const uint64_t slot = slot_at(j);
     load_block(slot, j < nblk ? 1 : 0, kb[b], vb[b]);
     if constexpr (F8) {
-      ksb[b] = pool_scales[2 * slot];
-      vsb[b] = pool_scales[2 * slot + 1];
+      const float2 sc = load_scales(pool_scales + 2 * slot);
+      ksb[b] = sc.x;
+      vsb[b] = sc.y;
     } else {
       ksb[b] = vsb[b] = 1.0f;
     }
