@@ -60,6 +60,18 @@ __device__ inline float sum_over_groups(float x) {
   return x;
 }
 
+// A slot's two fp8 scales (K, V) by a vector load, counted on vmcnt in order
+// with the block's own loads.  The address is wavefront-uniform, so the
+// compiler would make it a scalar load, whose counter (lgkmcnt) it shares with
+// the LDS reads and can only be waited for whole: the wait before the next
+// LDS read or block would then include the scales just issued for a block
+// further ahead.  An opaque zero in a VGPR keeps the address per lane.
+__device__ inline float2 load_scales(const float* p) {
+  int z;
+  asm("v_mov_b32 %0, 0" : "=v"(z));
+  return *reinterpret_cast<const float2*>(p + z);
+}
+
 // fp32 -> bf16 bits, round to nearest even (finite inputs)
 __device__ inline uint16_t bf16_rne(float x) {
   uint32_t u = __builtin_bit_cast(uint32_t, x);

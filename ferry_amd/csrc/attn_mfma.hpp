@@ -56,18 +56,6 @@ __device__ inline uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 
-// A slot's two fp8 scales (K, V) by a vector load, counted on vmcnt in order
-// with the block's own loads.  The address is wavefront-uniform, so the
-// compiler would make it a scalar load, whose counter (lgkmcnt) can only be
-// waited for whole: the wait before the next LDS read or block would then
-// include the scales just issued for a block further ahead.  An opaque zero
-// in a VGPR keeps the address per lane.
-__device__ inline float2 load_scales(const float* p) {
-  int z;
-  asm("v_mov_b32 %0, 0" : "=v"(z));
-  return *reinterpret_cast<const float2*>(p + z);
-}
-
 // Shapes of one block's operands for KV dtype DT.
 template <int DT>
 struct Shape {
