@@ -61,23 +61,24 @@ __device__ inline void copy_block(const uint8_t* src_b, uint8_t* dst_b, int lane
 }
 
 // Forget every block of one set (map entries of its tags, tags, order, fill).
-__device__ inline void clear_set(const Geo& g, SetState st, size_t set, int lane) {
+// Every thread of the workgroup (NT threads) calls it; ends with a barrier.
+// Thread t clears slots t, t + NT, ...: the map entry of its tag first, then
+// the tag itself, so no thread needs another's writes in between.
+template <int NT>
+__device__ inline void clear_set(const Geo& g, SetState st, size_t set) {
   const uint32_t C = (uint32_t)g.C;
   uint32_t* map = st.map + set * (size_t)g.max_blocks;
   uint32_t* tag = st.tag + set * C;
   uint32_t* ord = st.ord + set * C;
-  for (uint32_t i = lane; i < C; i += kWave) {
-    const uint32_t b = tag[i];
+  for (uint32_t i = threadIdx.x; i < C; i += NT) {
+    const uint32_t b = aload(tag + i);  // other threads may have written it (L2 atomics)
     if (b < (uint32_t)g.max_blocks) map[b] = kNone;
-  }
-  wave_fence();
-  for (uint32_t i = lane; i < C; i += kWave) {
     tag[i] = kNone;
     ord[i] = kNone;
     if (st.own) st.own[set * C + i] = 0u;
   }
-  if (lane == 0) st.fill[set] = 0;
-  wave_fence();
+  if (threadIdx.x == 0) st.fill[set] = 0;
+  __syncthreads();
 }
 
 }  // namespace
@@ -162,63 +163,67 @@ __global__ __launch_bounds__(256) void k_owner_export_data(Geo g, SetState st, u
   copy_block<NV>(pool + gslot * g.bb, image + lay.data + pos * g.bb, lane);
 }
 
-// One wavefront per set of the importing owner: forget the set's blocks, check
-// the image against this executor's geometry, then take the image's fill,
-// order, tags and map entries.  A mismatching or malformed image latches
-// FERRY_EINVAL and leaves the set empty (so the data kernel writes nothing).
+// One workgroup of 256 threads per set of the importing owner (one
+// wavefront per set left each CU a single wavefront walking up to C entries):
+// forget the set's blocks, check the image against this executor's geometry,
+// then take the image's fill, order, tags and map entries.  A mismatching or
+// malformed image latches FERRY_EINVAL and leaves the set empty (so the data
+// kernel writes nothing).  Words other threads wrote are read with L1-bypassing
+// atomics after a barrier.
 __global__ __launch_bounds__(256) void k_owner_import_meta(Geo g, SetState st, uint32_t owner,
                                                            const uint8_t* __restrict__ image,
                                                            int* __restrict__ err) {
+  constexpr int NT = 256;
   const ImageLayout lay = image_layout(g);
   const uint32_t S = (uint32_t)(g.L * g.Hkv), C = (uint32_t)g.C;
-  const uint32_t s = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (s >= S) return;
+  const uint32_t s = blockIdx.x;
+  const uint32_t tid = threadIdx.x;
+  if (s >= S) return;  // uniform
   const ImageHeader* h = reinterpret_cast<const ImageHeader*>(image);
   const uint32_t* fill = reinterpret_cast<const uint32_t*>(image + lay.fill);
   const uint32_t* start = reinterpret_cast<const uint32_t*>(image + lay.start);
   const uint32_t* iord = reinterpret_cast<const uint32_t*>(image + lay.ord);
   const uint32_t* itag = reinterpret_cast<const uint32_t*>(image + lay.tag);
   const size_t set = (size_t)owner * S + s;
-  clear_set(g, st, set, lane);
+  clear_set<NT>(g, st, set);
   const bool hdr_ok = h->magic == kImageMagic && h->sets == S && h->slots == C &&
                       h->bb == (uint32_t)g.bb && h->dtype == (uint32_t)g.dtype &&
                       h->max_blocks == (uint32_t)g.max_blocks && h->member_bit == 0u &&
                       h->resident <= (unsigned long long)S * C;
   const uint32_t f = hdr_ok ? fill[s] : 0, p0 = hdr_ok ? start[s] : 0;
   bool bad = !hdr_ok || f > C || (unsigned long long)p0 + f > h->resident;
-  for (uint32_t i = lane; i < f && !bad; i += kWave)
+  for (uint32_t i = tid; i < f && !bad; i += NT)
     bad |= iord[p0 + i] >= f || itag[p0 + i] >= (uint32_t)g.max_blocks;
-  if (ballot(bad)) {
-    if (lane == 0) set_error(err, FERRY_EINVAL);
+  if (__syncthreads_or(bad)) {  // uniform
+    if (tid == 0) set_error(err, FERRY_EINVAL);
     return;
   }
   uint32_t* map = st.map + set * (size_t)g.max_blocks;
   uint32_t* tag = st.tag + set * C;
   uint32_t* ord = st.ord + set * C;
   const uint32_t* iown = reinterpret_cast<const uint32_t*>(image + lay.own);
-  for (uint32_t i = lane; i < f; i += kWave) {
+  for (uint32_t i = tid; i < f; i += NT) {
     const uint32_t slot = iord[p0 + i], b = itag[p0 + i];
     ord[i] = slot;
     astore(tag + slot, b);
     astore(map + b, slot);
     if (st.own) st.own[set * C + slot] = iown[p0 + i];
   }
-  wave_fence();
+  __syncthreads();
   // The order must be a permutation of [0, f) with distinct blocks: a repeated
   // slot leaves some slot below f untagged, and a slot or block repeated with
   // another partner fails to read back through tag or map.
   bool dup = false;
-  for (uint32_t i = lane; i < f; i += kWave) {
+  for (uint32_t i = tid; i < f; i += NT) {
     const uint32_t slot = iord[p0 + i], b = itag[p0 + i];
     dup |= aload(tag + slot) != b || aload(map + b) != slot || aload(tag + i) == kNone;
   }
-  if (ballot(dup)) {
-    clear_set(g, st, set, lane);
-    if (lane == 0) set_error(err, FERRY_EINVAL);
+  if (__syncthreads_or(dup)) {  // uniform
+    clear_set<NT>(g, st, set);
+    if (tid == 0) set_error(err, FERRY_EINVAL);
     return;
   }
-  if (lane == 0) st.fill[set] = f;
+  if (tid == 0) st.fill[set] = f;
 }
 
 // One wavefront per (set, LRU position i < fill): the image block goes back to

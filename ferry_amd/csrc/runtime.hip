@@ -1410,7 +1410,7 @@ int ferry_owner_import(ferry_ctx* ctx, uint32_t owner, const void* image, uint64
   hipStream_t s = (hipStream_t)stream;
   const uint8_t* im = (const uint8_t*)image;
   const unsigned sets = (unsigned)(g.L * g.Hkv);
-  hipLaunchKernelGGL(k_owner_import_meta, dim3((sets + 3) / 4), dim3(256), 0, s, g, ctx->st, owner, im,
+  hipLaunchKernelGGL(k_owner_import_meta, dim3(sets), dim3(256), 0, s, g, ctx->st, owner, im,
                      ctx->err);
   HIPC(hipGetLastError());
   const uint64_t waves = (uint64_t)sets * g.C;
