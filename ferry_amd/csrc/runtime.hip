@@ -1028,13 +1028,13 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
       if (rc) return rc;
     }
   } else {
-    // Two streams, the caller's.  The main stream books range c + 1 (into ring
-    // (c + 1) mod 2) before it waits for the fetch of range c and attends it;
-    // the side stream fetches range c + 1 once it is booked.  So range c + 1 is
-    // booked while range c is fetched, and the link waits for no bookkeeping
-    // as long as attending c - 1 and booking c + 1 take less than fetching c.
-    // Ring (c + 1) mod 2 was last drained by the fetch of c - 1, which the main
-    // stream waited for before attending c - 1.  Ranges touch disjoint sets,
+    // Two streams, the caller's.  Ranges 0 and 1 are booked up front (rings 0
+    // and 1); then for each range c the main stream waits for its fetch, books
+    // range c + 2 into the ring that fetch has just drained (c mod 2), and
+    // attends c, while the side stream fetches each range once it is booked.
+    // Booking c + 2 runs beside the fetch of c + 1 and never waits for an
+    // attention, which beside a fetch can run several times slower than alone
+    // (the fetch's wavefronts share the CUs).  Ranges touch disjoint sets,
     // slots and outputs.  No stream of the context's own: a third stream can
     // share a hardware queue with the side stream (HIP hands a process a few
     // queues, shared among its streams) and then serialise with the fetch.
@@ -1052,12 +1052,13 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
       return FERRY_OK;
     };
     const int n = (int)live.size();
-    if (int rc = book_fetch(0)) return rc;
+    for (int i = 0; i < std::min(n, 2); ++i)
+      if (int rc = book_fetch(i)) return rc;
     for (int i = 0; i < n; ++i) {
-      if (i + 1 < n)
-        if (int rc = book_fetch(i + 1)) return rc;
       const int c = live[(size_t)i];
       HIPC(hipStreamWaitEvent(ms, ctx->events[i], 0));
+      if (i + 2 < n)  // ring i mod 2 is drained
+        if (int rc = book_fetch(i + 2)) return rc;
       if (int rc = ferry_sparse_decode_layers(ctx, first[c], first[c + 1] - first[c], q, slots,
                                               out, ms))
         return rc;

@@ -280,10 +280,10 @@ int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const flo
 /* One whole decode step with the fetch overlapped with attention: layers are
  * cut into `chunks` ranges; the fetch of each range runs on side_stream, and
  * attention of a range starts on `stream` as soon as its fetch is done, while
- * the next range is fetched.  Bookkeeping runs on `stream`, one range ahead
- * (range c + 1 is booked before range c is attended), into one of two miss
- * rings, so the fetch of a range does not wait for its bookkeeping while
- * attention keeps up with the link.  The overlap needs the two streams on
+ * the next range is fetched.  Bookkeeping runs on `stream`, two ranges ahead
+ * (range c + 2 is booked, into the miss ring the fetch of range c has just
+ * drained, before range c is attended), so the fetch of a range waits for
+ * neither its bookkeeping nor any attention.  The overlap needs the two streams on
  * different hardware queues: HIP shares a few queues (4 by default) among a
  * process's streams, and two streams on one queue run in turn.  The context
  * creates no stream of its own.  side_stream NULL (or
