@@ -29,7 +29,7 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
                                                    const float* __restrict__ pool_scales,
                                                    float* __restrict__ out, float qscale, int l0,
                                                    int nl, int* __restrict__ err) {
-  static_assert(G >= 2 && G <= 16, "MFMA tile holds up to 16 query heads");
+  static_assert(G >= 1 && G <= 16, "MFMA tile holds up to 16 query heads");
   static_assert(DT == FERRY_F16 || DT == FERRY_BF16 || DT == FERRY_FP8_E4M3, "16/8-bit KV");
   using S = Shape<DT>;
   constexpr bool F8 = S::F8;
@@ -174,10 +174,14 @@ __global__ __launch_bounds__(W * 64) void k_attn_mfma(Geo g, const float* __rest
   FERRY_ATTN_MFMA_INST(DT, 2, W)      \
   FERRY_ATTN_MFMA_INST(DT, 4, W)      \
   FERRY_ATTN_MFMA_INST(DT, 8, W)
-#define FERRY_ATTN_MFMA_INST_ALL(W)        \
-  FERRY_ATTN_MFMA_INST_G(FERRY_F16, W)     \
-  FERRY_ATTN_MFMA_INST_G(FERRY_BF16, W)    \
-  FERRY_ATTN_MFMA_INST_G(FERRY_FP8_E4M3, W)
+// fp8 MHA (G = 1) too: widening fp8 and the dot products on the vector ALUs
+// cost about twice as many instructions per byte as 16-bit KV, so one live
+// column of the 16-column tile beats the VALU kernel there.
+#define FERRY_ATTN_MFMA_INST_ALL(W)           \
+  FERRY_ATTN_MFMA_INST_G(FERRY_F16, W)        \
+  FERRY_ATTN_MFMA_INST_G(FERRY_BF16, W)       \
+  FERRY_ATTN_MFMA_INST_G(FERRY_FP8_E4M3, W)   \
+  FERRY_ATTN_MFMA_INST(FERRY_FP8_E4M3, 1, W)
 FERRY_ATTN_MFMA_INST_ALL(4)
 FERRY_ATTN_MFMA_INST_ALL(8)
 

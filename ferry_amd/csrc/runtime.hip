@@ -195,9 +195,12 @@ int validate(const ferry_config* c) {
   if (c->attn != FERRY_ATTN_AUTO && c->attn != FERRY_ATTN_VALU && c->attn != FERRY_ATTN_MFMA &&
       c->attn != FERRY_ATTN_GROUP)
     return fail(FERRY_EINVAL, "bad attn");
-  if ((c->attn == FERRY_ATTN_MFMA || c->attn == FERRY_ATTN_GROUP) &&
-      (grp < 2 || c->dtype == FERRY_F32))
-    return fail(FERRY_EINVAL, "the MFMA attention kernels need q_heads/kv_heads >= 2 and 16/8-bit KV");
+  if (c->attn == FERRY_ATTN_MFMA &&
+      (c->dtype == FERRY_F32 || (grp < 2 && c->dtype != FERRY_FP8_E4M3)))
+    return fail(FERRY_EINVAL,
+                "the MFMA attention kernel needs 16/8-bit KV and q_heads/kv_heads >= 2 (any for fp8)");
+  if (c->attn == FERRY_ATTN_GROUP && (grp < 2 || c->dtype == FERRY_F32))
+    return fail(FERRY_EINVAL, "the prefix-group attention kernel needs q_heads/kv_heads >= 2 and 16/8-bit KV");
   if (c->attn == FERRY_ATTN_GROUP && !group_attn_fits(c))
     return fail(FERRY_EINVAL,
                 "the prefix-group attention kernel needs group > 1, group * q_heads/kv_heads <= 64, "
@@ -290,7 +293,8 @@ AttnPlan attn_plan(const ferry_ctx* ctx) {
   AttnPlan p;
   p.dtype = g.dtype;
   p.G = g.Hq / g.Hkv;
-  p.mfma = g.dtype != FERRY_F32 && p.G >= 2 && ctx->cfg.attn != FERRY_ATTN_VALU;
+  p.mfma = g.dtype != FERRY_F32 && (p.G >= 2 || g.dtype == FERRY_FP8_E4M3) &&
+           ctx->cfg.attn != FERRY_ATTN_VALU;
   p.grouped = ctx->cfg.attn == FERRY_ATTN_GROUP ||
               (ctx->cfg.attn == FERRY_ATTN_AUTO && ctx->attn_grouped && group_attn_fits(&ctx->cfg));
   p.waves = 4;
@@ -345,6 +349,8 @@ void launch_g(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs
         default: launch_group<DT, G, 4>(ggrid, lds, s, a); return;
       }
     }
+  }
+  if constexpr (DT != FERRY_F32 && (G >= 2 || DT == FERRY_FP8_E4M3)) {
     if (p.mfma) {
       switch (p.waves) {
         case 8: launch_mfma<DT, G, 8>(p, grid, s, a); return;

@@ -51,11 +51,12 @@ extern "C" {
 #define FERRY_ASSIGN_AFFINITY 1 /* request (owner) modulo workers */
 
 /* ---- attention kernel selection ---- */
-#define FERRY_ATTN_AUTO 0 /* MFMA for GQA groups (q_heads/kv_heads >= 2) of 16/8-bit KV, else VALU;
-                            prefix groups (group > 1) that fit FERRY_ATTN_GROUP use it */
+#define FERRY_ATTN_AUTO 0 /* MFMA for GQA groups (q_heads/kv_heads >= 2) of 16/8-bit KV and for
+                            fp8 MHA, else VALU; prefix groups (group > 1) that fit
+                            FERRY_ATTN_GROUP use it */
 #define FERRY_ATTN_VALU 1 /* vector-ALU kernel for every shape */
-#define FERRY_ATTN_MFMA 2 /* MFMA kernel per (request, layer, kv head) row; needs
-                            q_heads/kv_heads >= 2 and 16/8-bit KV */
+#define FERRY_ATTN_MFMA 2 /* MFMA kernel per (request, layer, kv head) row; needs 16/8-bit KV
+                            and q_heads/kv_heads >= 2, or fp8 KV */
 #define FERRY_ATTN_GROUP 3 /* MFMA kernel per (prefix group, layer, kv head): every distinct
                              block of the group's set is read from HBM once for all members.
                              Needs group > 1, q_heads/kv_heads >= 2, 16/8-bit KV,

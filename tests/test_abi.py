@@ -63,7 +63,8 @@ def test_refgen_matches_reference_replay():
 @pytest.mark.parametrize("bad", [
     dict(q_heads=3), dict(head_dim=64), dict(block_tokens=8), dict(dtype=7), dict(lru_mode=3),
     dict(k=0), dict(slots_per_set=0), dict(assign=5), dict(max_blocks=0), dict(attn=3),
-    dict(attn=2),  # MFMA kernel needs a GQA group (q_heads/kv_heads >= 2)
+    dict(attn=2),  # MFMA kernel needs a GQA group (q_heads/kv_heads >= 2) for 16-bit KV
+    dict(attn=3, dtype=3),  # the group kernel needs a GQA group even for fp8
     dict(attn=2, q_heads=4, dtype=0),  # ... and 16/8-bit KV
     dict(cap_mode=2),
     dict(cap_mode=1, group=2, slots_per_set=7),  # per-member shares must divide the slots

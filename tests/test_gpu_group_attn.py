@@ -149,7 +149,7 @@ def test_group_kernel_limits():
         F.Executor(4, 1, 2, 16, 64, 64, q_heads=8, group=1, dtype=F.FP8, attn=F.ATTN_GROUP)
     with pytest.raises(F.FerryError, match="prefix-group"):  # 16 members x 8 heads > 64 columns
         F.Executor(16, 1, 1, 16, 64, 64, q_heads=8, group=16, dtype=F.F16, attn=F.ATTN_GROUP)
-    with pytest.raises(F.FerryError, match="MFMA"):
+    with pytest.raises(F.FerryError, match="16/8-bit KV"):
         F.Executor(4, 1, 2, 16, 64, 64, q_heads=8, group=4, dtype=F.F32, attn=F.ATTN_GROUP)
 
 
@@ -162,3 +162,5 @@ def test_auto_picks_the_group_kernel_where_it_fits():
     assert wide.attn_kernel() == (F.ATTN_MFMA, 4)
     mha = F.Executor(8, 1, 2, 16, 96, 96, q_heads=2, group=4, dtype=F.F16)  # G 1: vector ALUs
     assert mha.attn_kernel() == (F.ATTN_VALU, 4)
+    mha8 = F.Executor(8, 1, 2, 16, 96, 96, q_heads=2, group=4, dtype=F.FP8)  # fp8 G 1: MFMA
+    assert mha8.attn_kernel() == (F.ATTN_MFMA, 4)

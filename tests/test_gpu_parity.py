@@ -401,7 +401,8 @@ def test_mfma_attention_matches_oracle_and_valu(dtype, G):
 
 @pytest.mark.parametrize("dtype,G,attn", [(F.F32, 1, F.ATTN_AUTO), (F.F16, 1, F.ATTN_AUTO),
                                            (F.BF16, 4, F.ATTN_VALU), (F.BF16, 4, F.ATTN_MFMA),
-                                           (F.FP8, 4, F.ATTN_MFMA), (F.FP8, 2, F.ATTN_VALU)])
+                                           (F.FP8, 4, F.ATTN_MFMA), (F.FP8, 2, F.ATTN_VALU),
+                                           (F.FP8, 1, F.ATTN_AUTO)])
 def test_attention_load_flavours_are_bit_identical(dtype, G, attn, monkeypatch):
     # Non-temporal and temporal K/V loads differ only in cache policy: the
     # outputs must be bit-identical, and both within tolerance of the oracle.
@@ -422,6 +423,31 @@ def test_attention_load_flavours_are_bit_identical(dtype, G, attn, monkeypatch):
         outs.append(out.cpu())
         p.ex.close()
     assert torch.equal(outs[0], outs[1])
+
+
+def test_fp8_mha_runs_on_the_matrix_cores():
+    # fp8 MHA (one query head per kv head): AUTO picks the MFMA kernel with one
+    # live column of its 16; it matches the fp64 oracle and the VALU kernel.
+    n_req, L, H, k = 3, 2, 4, 13
+    mb, sels = _zipf_stream(n_req, L, H, k, 40, 200, 2, seed=11)
+    pm = Pair(n_req, L, H, H, k, 32, mb, F.FP8)
+    pv = Pair(n_req, L, H, H, k, 32, mb, F.FP8, attn=F.ATTN_VALU)
+    assert pm.ex.attn_kernel()[0] == F.ATTN_MFMA and pv.ex.attn_kernel()[0] == F.ATTN_VALU
+    for sel in sels:
+        pm.step(sel)
+        pv.step(sel)
+    for q_std in (1.0, 4.0):
+        pm.check_attention(sels[-1], seed=3, q_std=q_std)
+        pv.check_attention(sels[-1], seed=3, q_std=q_std)
+    q = torch.from_numpy(np.random.default_rng(3).standard_normal(
+        (n_req, L, H, 128)).astype(np.float32)).cuda()
+    om, ov = torch.empty_like(q), torch.empty_like(q)
+    pm.ex.sparse_decode(q, pm.bufs["slots"], om)
+    pv.ex.sparse_decode(q, pv.bufs["slots"], ov)
+    torch.cuda.synchronize()
+    rel = ((om - ov).abs().amax(dim=-1) / ov.abs().amax(dim=-1)).max().item()
+    assert rel < 5e-3, rel
+    assert pm.ex.stats()["device_error"] == 0
 
 
 def test_mfma_attention_long_selection():
