@@ -33,10 +33,18 @@ __device__ inline size_t sel_index(const Geo& g, const SetView& s, int p) {
   return ((size_t)((s.o * g.group + m) * g.L + s.l) * g.Hkv + s.h) * (size_t)g.k + j;
 }
 
+// Selection at position p of the set: from its LDS copy when the kernel staged
+// one (ssel, wave-uniform), else from the step's selection table.
+__device__ inline uint32_t sel_at(const Geo& g, const SetView& s, const uint32_t* __restrict__ sel,
+                                  const uint32_t* ssel, int p) {
+  return ssel ? ssel[p] : sel[sel_index(g, s, p)];
+}
+
 // One batched sub-step over positions [p0, p0 + cnt).  Returns the number of
 // misses appended at mo[0..), or a negative FERRY_E* code.
 __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, int cnt,
-                       const uint32_t* __restrict__ sel, uint32_t* __restrict__ slots_out,
+                       const uint32_t* __restrict__ sel, const uint32_t* ssel,
+                       uint32_t* __restrict__ slots_out,
                        uint8_t* __restrict__ miss_flag, uint32_t* __restrict__ map,
                        int* lastpos, uint32_t* sord, uint32_t* stag, uint32_t* smblk,
                        uint32_t* svict, uint32_t& fill, ferry_miss* __restrict__ mo,
@@ -47,7 +55,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
   // phase 1: classify (hits mark their slot; misses race for first occurrence)
   for (int c = p0; c < pend; c += kWave) {
     const int p = c + lane;
-    const uint32_t x = p < pend ? sel[sel_index(g, sv, p)] : kNone;
+    const uint32_t x = p < pend ? sel_at(g, sv, sel, ssel, p) : kNone;
     if (x != kNone) {
       const uint32_t v = aload(map + x);
       if (v < (uint32_t)C)
@@ -64,7 +72,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
     bool is_miss = false;
     uint32_t x = kNone;
     if (p < pend) {
-      x = sel[sel_index(g, sv, p)];
+      x = sel_at(g, sv, sel, ssel, p);
       is_miss = x != kNone && aload(map + x) == (kPend | (uint32_t)p);
       if (miss_flag) miss_flag[sel_index(g, sv, p)] = is_miss ? 1 : 0;
     }
@@ -139,7 +147,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
     const int p = c + lane;
     if (p < pend) {
       const size_t gi = sel_index(g, sv, p);
-      const uint32_t x = sel[gi];
+      const uint32_t x = sel_at(g, sv, sel, ssel, p);
       if (x == kNone) {
         slots_out[gi] = kNone;
       } else {
@@ -170,7 +178,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
     const int p = c + lane;
     bool emit = false;
     uint32_t v = 0;
-    const uint32_t x = p < pend ? sel[sel_index(g, sv, p)] : kNone;
+    const uint32_t x = p < pend ? sel_at(g, sv, sel, ssel, p) : kNone;
     if (x != kNone) {
       v = aload(map + x);
       emit = lastpos[v] == p;
@@ -184,7 +192,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
   // phase 6: clear the marks of this sub-step
   for (int c = p0; c < pend; c += kWave) {
     const int p = c + lane;
-    const uint32_t x = p < pend ? sel[sel_index(g, sv, p)] : kNone;
+    const uint32_t x = p < pend ? sel_at(g, sv, sel, ssel, p) : kNone;
     if (x != kNone) lastpos[aload(map + x)] = -1;
   }
   __builtin_amdgcn_wave_barrier();
@@ -210,13 +218,14 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   if (idx >= g.n_owners * nl * g.Hkv) return;  // no workgroup barriers follow
   const int set = ((idx / (nl * g.Hkv)) * g.L + l0 + (idx / g.Hkv) % nl) * g.Hkv + idx % g.Hkv;
   const int C = g.C;
-  uint32_t* base = lds + (size_t)wave * lru_lds_words(g);
+  uint32_t* base = lds + (size_t)wave * lru_lds_wave_words(g);
   int* lastpos = (int*)base;
   uint32_t* sord = base + C;
   uint32_t* stag = base + 2 * C;
   uint32_t* smblk = base + 3 * C;
   uint32_t* svict = smblk + g.max_sel;
   uint32_t* sown = st.own ? svict + g.max_sel : nullptr;  // [C] member masks
+  uint32_t* ssel = lru_stages_sel(g) ? base + lru_lds_words(g) : nullptr;  // [max_sel]
 
   SetView sv;
   sv.h = set % g.Hkv;
@@ -241,6 +250,7 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   int nsel = 0;  // non-empty positions
   for (int p = lane; p < sv.n; p += kWave) {
     const uint32_t x = sel[sel_index(g, sv, p)];
+    if (ssel) ssel[p] = x;
     bad |= x != kNone && x >= (uint32_t)g.max_blocks;
     nsel += __builtin_popcountll(ballot(x != kNone));
   }
@@ -258,13 +268,13 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   const uint32_t cap = set_capacity(g, st.members[sv.o]);
   int total = 0, rc = 0;
   if (!SERIAL) {
-    rc = substep(g, sv, (uint32_t)set, 0, sv.n, sel, slots_out, miss_flag, map, lastpos, sord, stag,
-                 smblk, svict, fill, mo, ring, worker, cap, sown);
+    rc = substep(g, sv, (uint32_t)set, 0, sv.n, sel, ssel, slots_out, miss_flag, map, lastpos, sord,
+                 stag, smblk, svict, fill, mo, ring, worker, cap, sown);
     if (rc >= 0) total = rc;
   } else {
     for (int p = 0; p < sv.n; ++p) {
-      rc = substep(g, sv, (uint32_t)set, p, 1, sel, slots_out, miss_flag, map, lastpos, sord, stag,
-                   smblk, svict, fill, mo + total, ring, worker, cap, sown);
+      rc = substep(g, sv, (uint32_t)set, p, 1, sel, ssel, slots_out, miss_flag, map, lastpos, sord,
+                   stag, smblk, svict, fill, mo + total, ring, worker, cap, sown);
       if (rc < 0) break;
       total += rc;
     }

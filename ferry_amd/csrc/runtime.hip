@@ -535,9 +535,10 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
     delete c;
     return fail(FERRY_EINVAL, "slots_per_set/group*k too large for the bookkeeping LDS budget");
   }
+  const size_t wave_lds = lru_lds_wave_words(g) * 4;  // with the staged selections
   c->lru_wpb = 4;
-  while (c->lru_wpb > 1 && per_wave * c->lru_wpb > 65536) c->lru_wpb >>= 1;
-  c->lru_lds = per_wave * c->lru_wpb;
+  while (c->lru_wpb > 1 && wave_lds * c->lru_wpb > 65536) c->lru_wpb >>= 1;
+  c->lru_lds = wave_lds * c->lru_wpb;
 
   const size_t nslots = (size_t)g.n_sets * g.C;
 #define TRY(x)        \
