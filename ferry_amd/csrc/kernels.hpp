@@ -21,13 +21,14 @@ struct SetState {
 __host__ __device__ inline size_t lru_lds_words(const Geo& g) {
   return (size_t)(3 + (g.group > 1 ? 1 : 0)) * g.C + 2 * (size_t)g.max_sel;
 }
-// The bookkeeping also stages a set's selections in LDS (one read of each from
-// HBM instead of one per pass) where they fit beside that state in 64 KiB.
+// The bookkeeping also stages a set's selections and, once assigned, their
+// slots in LDS (one HBM read of each instead of one per pass) where they fit
+// beside that state in 64 KiB.
 __host__ __device__ inline bool lru_stages_sel(const Geo& g) {
-  return (lru_lds_words(g) + (size_t)g.max_sel) * 4 <= 65536;
+  return (lru_lds_words(g) + 2 * (size_t)g.max_sel) * 4 <= 65536;
 }
 __host__ __device__ inline size_t lru_lds_wave_words(const Geo& g) {
-  return lru_lds_words(g) + (lru_stages_sel(g) ? (size_t)g.max_sel : 0);
+  return lru_lds_words(g) + (lru_stages_sel(g) ? 2 * (size_t)g.max_sel : 0);
 }
 
 // Blocks an owner's sets may hold: C, or under FERRY_CAP_PER_MEMBER one

@@ -34,7 +34,9 @@ __device__ inline size_t sel_index(const Geo& g, const SetView& s, int p) {
 }
 
 // Selection at position p of the set: from its LDS copy when the kernel staged
-// one (ssel, wave-uniform), else from the step's selection table.
+// one (ssel, wave-uniform), else from the step's selection table.  With the
+// copy, ssel[max_sel + p] keeps the slot position p resolved to (pass 4b) for
+// the passes after it.
 __device__ inline uint32_t sel_at(const Geo& g, const SetView& s, const uint32_t* __restrict__ sel,
                                   const uint32_t* ssel, int p) {
   return ssel ? ssel[p] : sel[sel_index(g, s, p)];
@@ -43,7 +45,7 @@ __device__ inline uint32_t sel_at(const Geo& g, const SetView& s, const uint32_t
 // One batched sub-step over positions [p0, p0 + cnt).  Returns the number of
 // misses appended at mo[0..), or a negative FERRY_E* code.
 __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, int cnt,
-                       const uint32_t* __restrict__ sel, const uint32_t* ssel,
+                       const uint32_t* __restrict__ sel, uint32_t* ssel,
                        uint32_t* __restrict__ slots_out,
                        uint8_t* __restrict__ miss_flag, uint32_t* __restrict__ map,
                        int* lastpos, uint32_t* sord, uint32_t* stag, uint32_t* smblk,
@@ -152,6 +154,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
         slots_out[gi] = kNone;
       } else {
         const uint32_t v = aload(map + x);
+        if (ssel) ssel[g.max_sel + p] = v;
         slots_out[gi] = set * (uint32_t)C + v;
         atomicMax(lastpos + v, p);
         if (sown) atomicOr(sown + v, 1u << (uint32_t)(p / g.k));  // member of position p
@@ -180,7 +183,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
     uint32_t v = 0;
     const uint32_t x = p < pend ? sel_at(g, sv, sel, ssel, p) : kNone;
     if (x != kNone) {
-      v = aload(map + x);
+      v = ssel ? ssel[g.max_sel + p] : aload(map + x);
       emit = lastpos[v] == p;
     }
     const uint64_t mask = ballot(emit);
@@ -193,7 +196,7 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
   for (int c = p0; c < pend; c += kWave) {
     const int p = c + lane;
     const uint32_t x = p < pend ? sel_at(g, sv, sel, ssel, p) : kNone;
-    if (x != kNone) lastpos[aload(map + x)] = -1;
+    if (x != kNone) lastpos[ssel ? ssel[g.max_sel + p] : aload(map + x)] = -1;
   }
   __builtin_amdgcn_wave_barrier();
   return M;
@@ -225,7 +228,7 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   uint32_t* smblk = base + 3 * C;
   uint32_t* svict = smblk + g.max_sel;
   uint32_t* sown = st.own ? svict + g.max_sel : nullptr;  // [C] member masks
-  uint32_t* ssel = lru_stages_sel(g) ? base + lru_lds_words(g) : nullptr;  // [max_sel]
+  uint32_t* ssel = lru_stages_sel(g) ? base + lru_lds_words(g) : nullptr;  // [2 max_sel]
 
   SetView sv;
   sv.h = set % g.Hkv;
