@@ -1,6 +1,7 @@
 """GPU parity at the library's size limits: the largest top-k (1024), the
 largest slot count the bookkeeping's 64 KiB LDS budget allows with it (4778
-per set: (3 C + 2 k) * 4 bytes per wavefront), block ids at the top of the
+per set: (3 C + 2 k) * 4 bytes per wavefront), prefix-group sets too large for
+the bookkeeping to stage their selections in LDS, block ids at the top of the
 31-bit range, and the refusals one past each limit."""
 import numpy as np
 import pytest
@@ -40,6 +41,28 @@ def test_one_past_the_limits_is_refused():
         F.Executor(1, 1, 1, K_MAX, C_MAX + 1, 8192)
     with pytest.raises(F.FerryError, match="1024"):
         F.Executor(1, 1, 1, K_MAX + 1, 64, 8192)
+
+
+def test_group_sets_past_the_staging_budget():
+    # 16-member prefix groups with k 64 (1,024 selections per set) and 3,200
+    # slots: the set's state fits the bookkeeping's 64 KiB of LDS, but not with
+    # its staged selections and slots beside it, so the passes read those from
+    # HBM.  Bit-exact against the oracle in both LRU granularities, filling the
+    # sets and then evicting.
+    n_req, group, L, Hkv, k, C = 16, 16, 1, 1, 64, 3200
+    assert (4 * C + 2 * group * k) * 4 <= 65536 < (4 * C + 4 * group * k) * 4
+    mb, sels = _zipf_stream(n_req, L, Hkv, k, 300, 600, 8, group=group, prefix=64, seed=5,
+                            reuse=0.3, dist=0)
+    for lru in (0, 1):
+        p = Pair(n_req, L, Hkv, Hkv, k, C, mb, F.F16, group=group, lru=lru)
+        evicted = 0
+        for sel in sels:
+            fetched = p.step(sel)
+            p.check_fetched_bytes(fetched)
+            evicted += int(np.sum(fetched[:, 2] != O.NONE))
+        p.check_state()
+        assert evicted > 0
+        p.ex.close()
 
 
 def test_block_ids_at_the_top_of_the_range():
