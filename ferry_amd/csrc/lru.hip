@@ -43,7 +43,14 @@ __device__ inline uint32_t sel_at(const Geo& g, const SetView& s, const uint32_t
 }
 
 // One batched sub-step over positions [p0, p0 + cnt).  Returns the number of
-// misses appended at mo[0..), or a negative FERRY_E* code.
+// misses appended at mo[0..), or a negative FERRY_E* code.  The passes that
+// look positions up in the block->slot map load the entries of B rounds of 64
+// positions before using any: a wavefront keeps B round trips in flight
+// instead of one.  That is safe within each pass: classify only turns a
+// non-resident entry into another non-resident one (the first occurrence's
+// mark), which sends a position down the same path whichever it reads, and
+// the later passes only read.
+template <int B>
 __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, int cnt,
                        const uint32_t* __restrict__ sel, uint32_t* ssel,
                        uint32_t* __restrict__ slots_out,
@@ -54,33 +61,45 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
   const int lane = lane_id();
   const int C = g.C;
   const int pend = p0 + cnt;
+  uint32_t xs[B], vs[B];
+  // positions c0 + 64 u + lane of a batch; kNone past the sub-step
+  auto gather = [&](int c0) {
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int p = c0 + u * kWave + lane;
+      xs[u] = p < pend ? sel_at(g, sv, sel, ssel, p) : kNone;
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) vs[u] = xs[u] != kNone ? aload(map + xs[u]) : kNone;
+  };
   // phase 1: classify (hits mark their slot; misses race for first occurrence)
-  for (int c = p0; c < pend; c += kWave) {
-    const int p = c + lane;
-    const uint32_t x = p < pend ? sel_at(g, sv, sel, ssel, p) : kNone;
-    if (x != kNone) {
-      const uint32_t v = aload(map + x);
-      if (v < (uint32_t)C)
-        atomicMax(lastpos + v, p);
-      else
-        atomicMin(map + x, kPend | (uint32_t)p);
+  for (int c0 = p0; c0 < pend; c0 += B * kWave) {
+    gather(c0);
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int p = c0 + u * kWave + lane;
+      if (xs[u] != kNone) {
+        if (vs[u] < (uint32_t)C)
+          atomicMax(lastpos + vs[u], p);
+        else
+          atomicMin(map + xs[u], kPend | (uint32_t)p);
+      }
     }
   }
   wave_fence();
   // phase 2: rank misses by first occurrence
   int M = 0;
-  for (int c = p0; c < pend; c += kWave) {
-    const int p = c + lane;
-    bool is_miss = false;
-    uint32_t x = kNone;
-    if (p < pend) {
-      x = sel_at(g, sv, sel, ssel, p);
-      is_miss = x != kNone && aload(map + x) == (kPend | (uint32_t)p);
-      if (miss_flag) miss_flag[sel_index(g, sv, p)] = is_miss ? 1 : 0;
+  for (int c0 = p0; c0 < pend; c0 += B * kWave) {
+    gather(c0);
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int p = c0 + u * kWave + lane;
+      const bool is_miss = xs[u] != kNone && vs[u] == (kPend | (uint32_t)p);
+      if (p < pend && miss_flag) miss_flag[sel_index(g, sv, p)] = is_miss ? 1 : 0;
+      const uint64_t mask = ballot(is_miss);
+      if (is_miss) smblk[M + lanes_below(mask)] = xs[u];
+      M += __builtin_popcountll(mask);
     }
-    const uint64_t mask = ballot(is_miss);
-    if (is_miss) smblk[M + lanes_below(mask)] = x;
-    M += __builtin_popcountll(mask);
   }
   // phase 3: victims = least recent untouched residents, oldest first; the
   // set may use `cap` of its C slots (fewer under per-member capacity)
@@ -145,19 +164,22 @@ __device__ int substep(const Geo& g, const SetView& sv, uint32_t set, int p0, in
   }
   wave_fence();
   // phase 4b: slot of every position; last occurrence per touched slot
-  for (int c = p0; c < pend; c += kWave) {
-    const int p = c + lane;
-    if (p < pend) {
-      const size_t gi = sel_index(g, sv, p);
-      const uint32_t x = sel_at(g, sv, sel, ssel, p);
-      if (x == kNone) {
-        slots_out[gi] = kNone;
-      } else {
-        const uint32_t v = aload(map + x);
-        if (ssel) ssel[g.max_sel + p] = v;
-        slots_out[gi] = set * (uint32_t)C + v;
-        atomicMax(lastpos + v, p);
-        if (sown) atomicOr(sown + v, 1u << (uint32_t)(p / g.k));  // member of position p
+  for (int c0 = p0; c0 < pend; c0 += B * kWave) {
+    gather(c0);
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int p = c0 + u * kWave + lane;
+      if (p < pend) {
+        const size_t gi = sel_index(g, sv, p);
+        if (xs[u] == kNone) {
+          slots_out[gi] = kNone;
+        } else {
+          const uint32_t v = vs[u];
+          if (ssel) ssel[g.max_sel + p] = v;
+          slots_out[gi] = set * (uint32_t)C + v;
+          atomicMax(lastpos + v, p);
+          if (sown) atomicOr(sown + v, 1u << (uint32_t)(p / g.k));  // member of position p
+        }
       }
     }
   }
@@ -271,13 +293,19 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   const uint32_t cap = set_capacity(g, st.members[sv.o]);
   int total = 0, rc = 0;
   if (!SERIAL) {
-    rc = substep(g, sv, (uint32_t)set, 0, sv.n, sel, ssel, slots_out, miss_flag, map, lastpos, sord,
-                 stag, smblk, svict, fill, mo, ring, worker, cap, sown);
+    // four rounds per map batch where a set has that many positions (prefix
+    // groups: group * k), one otherwise
+    if (g.max_sel >= 4 * kWave)
+      rc = substep<4>(g, sv, (uint32_t)set, 0, sv.n, sel, ssel, slots_out, miss_flag, map, lastpos,
+                      sord, stag, smblk, svict, fill, mo, ring, worker, cap, sown);
+    else
+      rc = substep<1>(g, sv, (uint32_t)set, 0, sv.n, sel, ssel, slots_out, miss_flag, map, lastpos,
+                      sord, stag, smblk, svict, fill, mo, ring, worker, cap, sown);
     if (rc >= 0) total = rc;
   } else {
     for (int p = 0; p < sv.n; ++p) {
-      rc = substep(g, sv, (uint32_t)set, p, 1, sel, ssel, slots_out, miss_flag, map, lastpos, sord,
-                   stag, smblk, svict, fill, mo + total, ring, worker, cap, sown);
+      rc = substep<1>(g, sv, (uint32_t)set, p, 1, sel, ssel, slots_out, miss_flag, map, lastpos,
+                      sord, stag, smblk, svict, fill, mo + total, ring, worker, cap, sown);
       if (rc < 0) break;
       total += rc;
     }
