@@ -264,20 +264,46 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   uint32_t* gtag = st.tag + (size_t)set * C;
   uint32_t* gown = st.own ? st.own + (size_t)set * C : nullptr;
   uint32_t fill = st.fill[set];
-  for (int i = lane; i < C; i += kWave) {
-    lastpos[i] = -1;
-    sord[i] = gord[i];
-    stag[i] = gtag[i];
-    if (sown) sown[i] = gown[i];
+  // the set's state into LDS, four rounds of loads in flight at a time
+  for (int i0 = 0; i0 < C; i0 += 4 * kWave) {
+    uint32_t o4[4], t4[4], w4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * kWave + lane;
+      if (i < C) {
+        o4[u] = gord[i];
+        t4[u] = gtag[i];
+        w4[u] = sown ? gown[i] : 0u;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * kWave + lane;
+      if (i < C) {
+        lastpos[i] = -1;
+        sord[i] = o4[u];
+        stag[i] = t4[u];
+        if (sown) sown[i] = w4[u];
+      }
+    }
   }
   // range check of every selected id before touching the map
   bool bad = false;
   int nsel = 0;  // non-empty positions
-  for (int p = lane; p < sv.n; p += kWave) {
-    const uint32_t x = sel[sel_index(g, sv, p)];
-    if (ssel) ssel[p] = x;
-    bad |= x != kNone && x >= (uint32_t)g.max_blocks;
-    nsel += __builtin_popcountll(ballot(x != kNone));
+  for (int p0 = 0; p0 < sv.n; p0 += 4 * kWave) {  // four rounds of loads in flight
+    uint32_t x4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = p0 + u * kWave + lane;
+      x4[u] = p < sv.n ? sel[sel_index(g, sv, p)] : kNone;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = p0 + u * kWave + lane;
+      if (ssel && p < sv.n) ssel[p] = x4[u];
+      bad |= x4[u] != kNone && x4[u] >= (uint32_t)g.max_blocks;
+      nsel += __builtin_popcountll(ballot(x4[u] != kNone));
+    }
   }
   if (ballot(bad)) {
     if (lane == 0) {
@@ -293,9 +319,12 @@ __global__ __launch_bounds__(256) void k_lru_step(Geo g, const uint32_t* __restr
   const uint32_t cap = set_capacity(g, st.members[sv.o]);
   int total = 0, rc = 0;
   if (!SERIAL) {
-    // four rounds per map batch where a set has that many positions (prefix
-    // groups: group * k), one otherwise
-    if (g.max_sel >= 4 * kWave)
+    // eight or four rounds per map batch where a set has that many positions
+    // (prefix groups: group * k), one otherwise
+    if (g.max_sel >= 8 * kWave)
+      rc = substep<8>(g, sv, (uint32_t)set, 0, sv.n, sel, ssel, slots_out, miss_flag, map, lastpos,
+                      sord, stag, smblk, svict, fill, mo, ring, worker, cap, sown);
+    else if (g.max_sel >= 4 * kWave)
       rc = substep<4>(g, sv, (uint32_t)set, 0, sv.n, sel, ssel, slots_out, miss_flag, map, lastpos,
                       sord, stag, smblk, svict, fill, mo, ring, worker, cap, sown);
     else
