@@ -124,7 +124,8 @@ template <int DT, int G, int NTILE>
 __global__ __launch_bounds__(group_waves(DT) * 64) void k_attn_group(
     Geo g, const float* __restrict__ q, const uint32_t* __restrict__ slots,
     const uint8_t* __restrict__ pool, const float* __restrict__ pool_scales,
-    float* __restrict__ out, float qscale, int l0, int nl, int* __restrict__ err) {
+    float* __restrict__ out, float qscale, int l0, int nl, int* __restrict__ err,
+    unsigned long long* __restrict__ attn_blocks) {
   static_assert(G == 2 || G == 4 || G == 8, "GQA group of 2, 4 or 8 query heads");
   static_assert(NTILE >= 1 && NTILE <= kGroupMaxTiles, "query tiles per workgroup");
   static_assert(DT == FERRY_F16 || DT == FERRY_BF16 || DT == FERRY_FP8_E4M3, "16/8-bit KV");
@@ -230,6 +231,7 @@ __global__ __launch_bounds__(group_waves(DT) * 64) void k_attn_group(
     }
   }
   const int nlist = n_in + n_own;
+  if (attn_blocks && tid == 0) atomicAdd(attn_blocks, (unsigned long long)nlist);
   __syncthreads();  // the rings may now overwrite msk / own
 
   // ---- Q^T operands of every tile, staged in LDS lane by lane (wavefront w
@@ -404,7 +406,8 @@ __global__ __launch_bounds__(group_waves(DT) * 64) void k_attn_group(
 #define FERRY_ATTN_GROUP_INST(DT, G, NTILE)                                                    \
   template __global__ void k_attn_group<DT, G, NTILE>(Geo, const float*, const uint32_t*,      \
                                                       const uint8_t*, const float*, float*,    \
-                                                      float, int, int, int*);
+                                                      float, int, int, int*,                   \
+                                                      unsigned long long*);
 #define FERRY_ATTN_GROUP_INST_DT(DT) \
   FERRY_ATTN_GROUP_INST(DT, 2, 1)    \
   FERRY_ATTN_GROUP_INST(DT, 2, 2)    \

@@ -258,10 +258,11 @@ template __global__ void k_fetch<4>(FetchArgs);
 template __global__ void k_fetch<8>(FetchArgs);
 template __global__ void k_fetch<16>(FetchArgs);
 
-__global__ void k_step_close(unsigned long long* step_acc, unsigned long long* last) {
+__global__ void k_step_close(unsigned long long* acc) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
-    *last = *step_acc;
-    *step_acc = 0ull;
+    acc[2] = acc[0];
+    acc[3] = acc[1];
+    acc[0] = acc[1] = 0ull;
   }
 }
 

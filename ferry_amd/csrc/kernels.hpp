@@ -103,8 +103,9 @@ __global__ void k_sets_trim(Geo g, SetState st, const uint32_t* lane_live, const
 template <int NV>
 __global__ void k_fetch(FetchArgs a);
 __global__ void k_missq_push(Geo g, Ring ring, const ferry_miss* m, uint32_t n, int* err);
-// End of a decode step: last = blocks fetched in the step, then step_acc = 0.
-__global__ void k_step_close(unsigned long long* step_acc, unsigned long long* last);
+// End of a decode step: acc[2..3] = the step's fetched and attended blocks
+// (acc[0..1]), then acc[0..1] = 0.
+__global__ void k_step_close(unsigned long long* acc);
 
 // Vector-ALU attention (attn.hip); W wavefronts per workgroup; NT selects
 // non-temporal K/V loads.
@@ -138,7 +139,7 @@ constexpr int group_ring_bytes(int dtype) {
 template <int DT, int G, int NTILE>
 __global__ void k_attn_group(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
                              const float* pool_scales, float* out, float qscale, int l0, int nl,
-                             int* err);
+                             int* err, unsigned long long* attn_blocks);
 // LDS of one k_attn_group workgroup: the wavefronts' rings, the Q^T operands
 // of every tile (fp16, or bf16 hi and lo parts: 4 KiB per part and tile), the
 // distinct list (slot and member mask per entry, at most group * k entries),

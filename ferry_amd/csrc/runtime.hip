@@ -106,8 +106,10 @@ struct ferry_ctx {
   uint32_t* worker_of_set = nullptr;
   unsigned long long* stats = nullptr;
   unsigned long long* sel_counts = nullptr;  // [kSelCounters * kSelStride]
-  unsigned long long* step_acc = nullptr;    // [2]: blocks fetched in this step, in the last one
-  unsigned long long* pend_host = nullptr;   // pinned: the last step's count, copied at step end
+  // [4]: blocks fetched and blocks the prefix-group attention read in this
+  // step, then the same two of the last finished step (k_step_close)
+  unsigned long long* step_acc = nullptr;
+  unsigned long long* pend_host = nullptr;   // pinned [2]: the last step's two, copied at step end
   double pol_min_mb = 32.0, pol_max_mb = 512.0, pol_target = 8.0;  // adaptive layer chunking
   uint32_t* done = nullptr;
   int* err = nullptr;
@@ -272,6 +274,7 @@ struct AttnArgs {
   float qscale;
   int l0, nl;
   int* err;
+  unsigned long long* attn_blocks;  // the group kernel adds the blocks it read (or null)
 };
 
 // Which attention kernel runs and how many wavefronts share one (request,
@@ -334,7 +337,8 @@ void launch_group(const dim3& grid, size_t lds, hipStream_t s, const AttnArgs& a
       hipFuncAttributeMaxDynamicSharedMemorySize, kGroupMaxLds);
   (void)attr;
   hipLaunchKernelGGL((k_attn_group<DT, G, NT>), grid, dim3(group_waves(DT) * 64), lds, s, a.g, a.q,
-                     a.slots, a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
+                     a.slots, a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err,
+                     a.attn_blocks);
 }
 template <int DT, int G>
 void launch_g(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs& a) {
@@ -412,6 +416,25 @@ int check_buf(const void* p, const char* name) {
 int check_bufs(std::initializer_list<std::pair<const void*, const char*>> bufs) {
   for (const auto& b : bufs)
     if (int rc = check_buf(b.first, b.second)) return rc;
+  return FERRY_OK;
+}
+
+// Attention of layers [l0, l0 + nl).  attn_blocks (decode steps only): the
+// prefix-group kernel adds the distinct blocks it reads there, which the next
+// step's layer chunking takes as the attention's bytes.
+int decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q, const uint32_t* slots,
+                  float* out, void* stream, unsigned long long* attn_blocks) {
+  if (int rc = check_bufs({{q, "q"}, {slots, "slots"}, {out, "out"}})) return rc;
+  const Geo& g = ctx->g;
+  if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
+  HIPC(hipSetDevice(ctx->device));
+  const dim3 grid((unsigned)(g.n_req * nl * g.Hkv));
+  const float qscale = (float)(1.4426950408889634 / std::sqrt((double)g.D));
+  const AttnArgs a{g, q, slots, ctx->pool, ctx->pool_scales, out, qscale, l0, nl, ctx->err,
+                   attn_blocks};
+  const AttnPlan p = attn_plan(ctx);
+  launch_attn(p, grid, (hipStream_t)stream, a);
+  HIPC(hipGetLastError());
   return FERRY_OK;
 }
 
@@ -583,7 +606,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   TRY(dalloc(&c->worker_of_set, g.n_sets));
   TRY(dalloc(&c->stats, kStatCount));
   TRY(dalloc(&c->sel_counts, (size_t)kSelCounters * kSelStride));
-  TRY(dalloc(&c->step_acc, 2));
+  TRY(dalloc(&c->step_acc, 4));
   TRY(dalloc(&c->done, 1));
   TRY(dalloc(&c->err, 1));
 #define HIPT(x)                                                                        \
@@ -601,13 +624,13 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   HIPT(hipMemset(c->ring_state2, 0, (size_t)W * kStateStride * 8));
   HIPT(hipMemset(c->stats, 0, kStatCount * 8));
   HIPT(hipMemset(c->sel_counts, 0, (size_t)kSelCounters * kSelStride * 8));
-  HIPT(hipMemset(c->step_acc, 0, 16));
-  if (hipHostMalloc((void**)&c->pend_host, 8, hipHostMallocDefault) != hipSuccess) {
+  HIPT(hipMemset(c->step_acc, 0, 32));
+  if (hipHostMalloc((void**)&c->pend_host, 16, hipHostMallocDefault) != hipSuccess) {
     c->pend_host = nullptr;
     release(c);
     return fail(FERRY_ENOMEM, "hipHostMalloc of the step counter failed");
   }
-  *c->pend_host = 0;
+  c->pend_host[0] = c->pend_host[1] = 0;
   HIPT(hipMemset(c->done, 0, 4));
   HIPT(hipMemset(c->err, 0, 4));
   HIPT(hipMemset(c->pool, 0, nslots * g.bb));
@@ -931,17 +954,7 @@ int ferry_fetch_step(ferry_ctx* ctx, const uint32_t* sel, uint32_t* slots, uint3
 int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
                                const uint32_t* slots, float* out, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
-  if (int rc = check_bufs({{q, "q"}, {slots, "slots"}, {out, "out"}})) return rc;
-  const Geo& g = ctx->g;
-  if (l0 < 0 || nl < 1 || l0 + nl > g.L) return fail(FERRY_EINVAL, "bad layer range");
-  HIPC(hipSetDevice(ctx->device));
-  const dim3 grid((unsigned)(g.n_req * nl * g.Hkv));
-  const float qscale = (float)(1.4426950408889634 / std::sqrt((double)g.D));
-  const AttnArgs a{g, q, slots, ctx->pool, ctx->pool_scales, out, qscale, l0, nl, ctx->err};
-  const AttnPlan p = attn_plan(ctx);
-  launch_attn(p, grid, (hipStream_t)stream, a);
-  HIPC(hipGetLastError());
-  return FERRY_OK;
+  return decode_layers(ctx, l0, nl, q, slots, out, stream, nullptr);
 }
 
 int ferry_attn_kernel(const ferry_ctx* ctx, int32_t* kind, int32_t* waves) {
@@ -990,9 +1003,11 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
   const int L = ctx->g.L;
   if (chunks < 0) return fail(FERRY_EINVAL, "chunks < 0");
   const bool adaptive = chunks == 0;
-  uint64_t last = 0;
-  if (adaptive) {  // from the blocks the last finished step fetched
-    last = *reinterpret_cast<volatile unsigned long long*>(ctx->pend_host);
+  uint64_t last = 0, last_attn = 0;
+  if (adaptive) {  // from the blocks the last finished step fetched (and attended)
+    const volatile unsigned long long* pend = ctx->pend_host;
+    last = pend[0];
+    last_attn = pend[1];
     if (int rc = ferry_decode_chunks(ctx, last, &chunks)) return rc;
   }
   chunks = std::min(chunks, L);
@@ -1009,7 +1024,10 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
     if (adaptive && chunks >= 2 && last > 0) {
       const Geo& g = ctx->g;
       const double kv = (double)g.bb + (g.dtype == FERRY_FP8_E4M3 ? 8.0 : 0.0);
-      const double attn_s = (double)g.n_req * g.L * g.Hkv * g.k * kv / 6.5e12;
+      // the blocks attention reads: k per row, or the distinct blocks the
+      // prefix-group kernel counted in the last step
+      const double blocks = last_attn ? (double)last_attn : (double)g.n_req * g.L * g.Hkv * g.k;
+      const double attn_s = blocks * kv / 6.5e12;
       const double fetch_s = (double)last * (double)g.bb / 55e9;
       const int rest = (L - 1 + chunks - 2) / (chunks - 1);  // layers of the other ranges
       const double want = std::ceil(2.0 * attn_s / fetch_s * rest);
@@ -1031,7 +1049,7 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
       if (nl <= 0) continue;
       int rc = bookkeep_ring(ctx, l0, nl, sel, slots, miss_count, misses, nullptr, ms, 0);
       if (!rc) rc = drain_ring(ctx, ms, 0);
-      if (!rc) rc = ferry_sparse_decode_layers(ctx, l0, nl, q, slots, out, ms);
+      if (!rc) rc = decode_layers(ctx, l0, nl, q, slots, out, ms, ctx->step_acc + 1);
       if (rc) return rc;
     }
   } else {
@@ -1066,15 +1084,15 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
       HIPC(hipStreamWaitEvent(ms, ctx->events[i], 0));
       if (i + 2 < n)  // ring i mod 2 is drained
         if (int rc = book_fetch(i + 2)) return rc;
-      if (int rc = ferry_sparse_decode_layers(ctx, first[c], first[c + 1] - first[c], q, slots,
-                                              out, ms))
+      if (int rc = decode_layers(ctx, first[c], first[c + 1] - first[c], q, slots, out, ms,
+                                 ctx->step_acc + 1))
         return rc;
     }
   }
   // the step's fetched blocks, for the next step's adaptive chunking
-  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(64), 0, ms, ctx->step_acc, ctx->step_acc + 1);
+  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(64), 0, ms, ctx->step_acc);
   HIPC(hipGetLastError());
-  HIPC(hipMemcpyAsync(ctx->pend_host, ctx->step_acc + 1, 8, hipMemcpyDeviceToHost, ms));
+  HIPC(hipMemcpyAsync(ctx->pend_host, ctx->step_acc + 2, 16, hipMemcpyDeviceToHost, ms));
   return FERRY_OK;
 }
 
