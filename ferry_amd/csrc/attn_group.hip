@@ -120,8 +120,8 @@ __device__ inline int block_exclusive_scan(int v, int* sh, int* total) {
 
 }  // namespace
 
-template <int DT, int G, int NTILE>
-__global__ __launch_bounds__(group_waves(DT) * 64) void k_attn_group(
+template <int DT, int G, int NTILE, int W>
+__global__ __launch_bounds__(W * 64) void k_attn_group(
     Geo g, const float* __restrict__ q, const uint32_t* __restrict__ slots,
     const uint8_t* __restrict__ pool, const float* __restrict__ pool_scales,
     float* __restrict__ out, float qscale, int l0, int nl, int* __restrict__ err,
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(group_waves(DT) * 64) void k_attn_group(
   constexpr int RC = ROW / 16;         // 16-byte chunks of a row (8 or 16)
   constexpr int BB = 2 * T * ROW;      // bytes of one block, K tile then V tile
   constexpr int NI = BB / 1024;        // direct-to-LDS loads of one block per wavefront
-  constexpr int W = group_waves(DT);   // wavefronts
+  static_assert(W == group_waves(DT) || W == kGroupWideWaves, "wavefronts per workgroup");
   constexpr int NT = W * 64;           // threads
   constexpr int MPT = 16 / G;          // members per query tile
   constexpr int R = group_ring_blocks(DT);   // ring blocks per wavefront
@@ -403,11 +403,14 @@ __global__ __launch_bounds__(group_waves(DT) * 64) void k_attn_group(
   }
 }
 
-#define FERRY_ATTN_GROUP_INST(DT, G, NTILE)                                                    \
-  template __global__ void k_attn_group<DT, G, NTILE>(Geo, const float*, const uint32_t*,      \
-                                                      const uint8_t*, const float*, float*,    \
-                                                      float, int, int, int*,                   \
-                                                      unsigned long long*);
+#define FERRY_ATTN_GROUP_INST_W(DT, G, NTILE, W)                                          \
+  template __global__ void k_attn_group<DT, G, NTILE, W>(Geo, const float*, const uint32_t*, \
+                                                         const uint8_t*, const float*, float*, \
+                                                         float, int, int, int*,              \
+                                                         unsigned long long*);
+#define FERRY_ATTN_GROUP_INST(DT, G, NTILE)                       \
+  FERRY_ATTN_GROUP_INST_W(DT, G, NTILE, group_waves(DT))          \
+  FERRY_ATTN_GROUP_INST_W(DT, G, NTILE, kGroupWideWaves)
 #define FERRY_ATTN_GROUP_INST_DT(DT) \
   FERRY_ATTN_GROUP_INST(DT, 2, 1)    \
   FERRY_ATTN_GROUP_INST(DT, 2, 2)    \

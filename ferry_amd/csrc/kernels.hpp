@@ -120,23 +120,27 @@ __global__ void k_attn_mfma(Geo g, const float* q, const uint32_t* slots, const 
                             const float* pool_scales, float* out, float qscale, int l0, int nl,
                             int* err);
 
-// Prefix-group attention (attn_group.hip): one workgroup of group_waves()
-// wavefronts per (group, layer, kv head) reads each distinct block of the
-// group's set once and attends every member row; NTILE tiles of 16 query
-// columns (group * G / 16 rounded up); dynamic LDS of attn_group_lds_bytes().
-// The LDS holds each wavefront's ring of blocks in flight: four wavefronts
-// with three fp8 blocks (or two 16-bit blocks) each let two workgroups share a
-// CU.  Eight wavefronts with four fp8 blocks each (one workgroup per CU, 96 KiB
-// in flight instead of 64) measured 5% slower alone and kept the overlapped
-// fetch off the CUs: the shared-prefix step took 4.23 ms against 3.80.
+// Prefix-group attention (attn_group.hip): one workgroup of W wavefronts per
+// (group, layer, kv head) reads each distinct block of the group's set once
+// and attends every member row; NTILE tiles of 16 query columns (group * G /
+// 16 rounded up); dynamic LDS of attn_group_lds_bytes().  The LDS holds each
+// wavefront's ring of blocks in flight: group_waves() = four wavefronts with
+// three fp8 blocks (or two 16-bit blocks) each let two workgroups share a CU.
+// Eight wavefronts with four fp8 blocks each (one workgroup per CU, 96 KiB in
+// flight instead of 64) measured 5% slower for a whole launch and kept the
+// overlapped fetch off the CUs: the shared-prefix step took 4.23 ms against
+// 3.80.  A launch with no more group sets than CUs, which leaves CUs idle
+// with four, runs kGroupWideWaves wavefronts per workgroup: each workgroup's
+// time is then bound by its own loads in flight, not by the CU's share.
 constexpr int kGroupMaxTiles = 4;         // query tiles every wavefront attends with (64 columns)
 constexpr int kGroupMaxLds = 160 * 1024;  // LDS of one CU
 constexpr int group_waves(int dtype) { return dtype == FERRY_F32 ? 0 : 4; }
+constexpr int kGroupWideWaves = 8;
 constexpr int group_ring_blocks(int dtype) { return dtype == FERRY_FP8_E4M3 ? 3 : 2; }
 constexpr int group_ring_bytes(int dtype) {
   return group_ring_blocks(dtype) * 2 * 16 * 128 * (dtype == FERRY_FP8_E4M3 ? 1 : 2);
 }
-template <int DT, int G, int NTILE>
+template <int DT, int G, int NTILE, int W>
 __global__ void k_attn_group(Geo g, const float* q, const uint32_t* slots, const uint8_t* pool,
                              const float* pool_scales, float* out, float qscale, int l0, int nl,
                              int* err, unsigned long long* attn_blocks);
@@ -144,8 +148,8 @@ __global__ void k_attn_group(Geo g, const float* q, const uint32_t* slots, const
 // of every tile (fp16, or bf16 hi and lo parts: 4 KiB per part and tile), the
 // distinct list (slot and member mask per entry, at most group * k entries),
 // the merge's per-column max and sum of every wavefront, and the scan scratch.
-inline size_t attn_group_lds_bytes(int dtype, int ntile, long group_k) {
-  const size_t w = group_waves(dtype), parts = dtype == FERRY_BF16 ? 2 : 1;
+inline size_t attn_group_lds_bytes(int dtype, int ntile, long group_k, int waves) {
+  const size_t w = (size_t)waves, parts = dtype == FERRY_BF16 ? 2 : 1;
   return w * group_ring_bytes(dtype) + parts * ntile * 4096 + 8 * (size_t)group_k +
          8 * w * 16 * ntile + 4 * w;
 }

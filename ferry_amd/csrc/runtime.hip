@@ -124,6 +124,8 @@ struct ferry_ctx {
   std::vector<hipEvent_t> events;   // layer-chunk pipeline of ferry_decode_step: fetch done
   std::vector<hipEvent_t> booked;   // ... and bookkeeping done
   int attn_waves = 0;              // wavefronts per attention workgroup (FERRY_ATTN_WAVES), 0 = default
+  int cus = 256;                   // compute units of the device
+  int group_waves_env = 0;         // prefix-group kernel wavefronts (FERRY_GROUP_WAVES=4|8), 0 = by launch
   int fetch_waves = 0;             // wavefronts per fetch workgroup (FERRY_FETCH_WAVES: 1, 2, 4; 0 = by rule)
   int fetch_prio = 1;              // fetch wavefronts issue first (FERRY_FETCH_PRIO=0: not)
   uint32_t steal_chunk = 8;        // most entries one steal takes (FERRY_STEAL_CHUNK)
@@ -172,7 +174,7 @@ bool group_attn_fits(const ferry_config* c) {
     return false;
   const long gk = (long)c->group * c->k;
   const int ntile = (c->group * G + 15) / 16;
-  return attn_group_lds_bytes(c->dtype, ntile, gk) <= (size_t)kGroupMaxLds &&
+  return attn_group_lds_bytes(c->dtype, ntile, gk, group_waves(c->dtype)) <= (size_t)kGroupMaxLds &&
          4 * ((long)c->slots_per_set + gk) <=
              (long)group_waves(c->dtype) * group_ring_bytes(c->dtype);
 }
@@ -288,7 +290,8 @@ struct AttnArgs {
 // per-row MFMA kernel or FERRY_ATTN_GROUPED=0 is set.
 struct AttnPlan {
   bool mfma, nt, grouped;
-  int dtype, G, waves, tiles;
+  int dtype, G, waves, tiles, cus;
+  int group_w;  // FERRY_GROUP_WAVES: 4 or 8 forced, else by launch size
 };
 
 AttnPlan attn_plan(const ferry_ctx* ctx) {
@@ -308,6 +311,8 @@ AttnPlan attn_plan(const ferry_ctx* ctx) {
     p.tiles = (g.group * p.G + 15) / 16;
   }
   p.nt = ctx->attn_loads ? ctx->attn_loads == 1 : g.group == 1;
+  p.cus = ctx->cus;
+  p.group_w = ctx->group_waves_env;
   return p;
 }
 
@@ -329,28 +334,39 @@ void launch_mfma(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnA
     hipLaunchKernelGGL((k_attn_mfma<DT, G, W, false>), grid, dim3(W * 64), 0, s, a.g, a.q,
                        a.slots, a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err);
 }
-template <int DT, int G, int NT>
-void launch_group(const dim3& grid, size_t lds, hipStream_t s, const AttnArgs& a) {
+template <int DT, int G, int NT, int W>
+void launch_group_w(const dim3& grid, size_t lds, hipStream_t s, const AttnArgs& a) {
   // more than the default 64 KiB of dynamic LDS: allowed once per instance
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_attn_group<DT, G, NT>),
+      reinterpret_cast<const void*>(&k_attn_group<DT, G, NT, W>),
       hipFuncAttributeMaxDynamicSharedMemorySize, kGroupMaxLds);
   (void)attr;
-  hipLaunchKernelGGL((k_attn_group<DT, G, NT>), grid, dim3(group_waves(DT) * 64), lds, s, a.g, a.q,
-                     a.slots, a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err,
-                     a.attn_blocks);
+  hipLaunchKernelGGL((k_attn_group<DT, G, NT, W>), grid, dim3(W * 64), lds, s, a.g, a.q, a.slots,
+                     a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err, a.attn_blocks);
+}
+// Eight wavefronts per workgroup for a launch with no more group sets than
+// CUs (where they fit the LDS), four otherwise; `force` (4 or 8) overrides.
+template <int DT, int G, int NT>
+void launch_group(const dim3& grid, int cus, int force, hipStream_t s, const AttnArgs& a) {
+  const long gk = (long)a.g.group * a.g.k;
+  const size_t wide = attn_group_lds_bytes(DT, NT, gk, kGroupWideWaves);
+  const bool want = force ? force == kGroupWideWaves : grid.x <= (unsigned)cus;
+  if (want && wide <= (size_t)kGroupMaxLds)
+    launch_group_w<DT, G, NT, kGroupWideWaves>(grid, wide, s, a);
+  else
+    launch_group_w<DT, G, NT, group_waves(DT)>(
+        grid, attn_group_lds_bytes(DT, NT, gk, group_waves(DT)), s, a);
 }
 template <int DT, int G>
 void launch_g(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnArgs& a) {
   if constexpr (DT != FERRY_F32 && G >= 2) {
     if (p.grouped) {
       const dim3 ggrid((unsigned)(a.g.n_owners * a.nl * a.g.Hkv));
-      const size_t lds = attn_group_lds_bytes(a.g.dtype, p.tiles, (long)a.g.group * a.g.k);
       switch (p.tiles) {
-        case 1: launch_group<DT, G, 1>(ggrid, lds, s, a); return;
-        case 2: launch_group<DT, G, 2>(ggrid, lds, s, a); return;
-        case 3: launch_group<DT, G, 3>(ggrid, lds, s, a); return;
-        default: launch_group<DT, G, 4>(ggrid, lds, s, a); return;
+        case 1: launch_group<DT, G, 1>(ggrid, p.cus, p.group_w, s, a); return;
+        case 2: launch_group<DT, G, 2>(ggrid, p.cus, p.group_w, s, a); return;
+        case 3: launch_group<DT, G, 3>(ggrid, p.cus, p.group_w, s, a); return;
+        default: launch_group<DT, G, 4>(ggrid, p.cus, p.group_w, s, a); return;
       }
     }
   }
@@ -488,6 +504,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   ferry_ctx* c = new ferry_ctx();
   c->cfg = *cfg;
   if (const char* e = std::getenv("FERRY_ATTN_WAVES")) c->attn_waves = std::atoi(e);
+  if (const char* e = std::getenv("FERRY_GROUP_WAVES")) c->group_waves_env = std::atoi(e);
   if (const char* e = std::getenv("FERRY_FETCH_WAVES")) {
     const int v = std::atoi(e);
     c->fetch_waves = v == 1 || v == 2 ? v : 4;
@@ -529,6 +546,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1)
     cus = 256;
+  c->cus = cus;
   // One fetch workgroup per 4 CUs by default: 256 wavefronts with a block each
   // in flight fill the host link (57.5 GB/s at the 7B shape, against 55 GB/s
   // with 2 per CU), and the CUs they leave idle run the attention that

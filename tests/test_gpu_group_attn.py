@@ -2,7 +2,9 @@
 reads each distinct block of the group's set once and attends every member row
 (FERRY_ATTN_GROUP).  Checked against the fp64 oracle (2e-3 relative, 1e-2 for
 fp8) and against the per-row MFMA kernel (FERRY_ATTN_MFMA) of a twin executor
-that went through the same fetch steps, so its pool holds the same bytes.
+that went through the same fetch steps, so its pool holds the same bytes, with
+four and with eight wavefronts per workgroup (FERRY_GROUP_WAVES; by default a
+launch with no more group sets than CUs runs eight).
 
 Slot tables are also edited by hand: a slot repeated in a row (attended twice),
 slots of another group's set, empty positions, rows with nothing selected.
@@ -65,8 +67,11 @@ def _rel(a, b):
     return np.abs(a - b).max(axis=1) / den
 
 
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("dtype,Hkv,Hq,group,n_req", CASES)
-def test_group_kernel_matches_oracle_and_row_kernel(dtype, Hkv, Hq, group, n_req):
+def test_group_kernel_matches_oracle_and_row_kernel(dtype, Hkv, Hq, group, n_req, waves,
+                                                    monkeypatch):
+    monkeypatch.setenv("FERRY_GROUP_WAVES", str(waves))
     gp, rp, sel = _twins(dtype, Hkv, Hq, group, n_req)
     g = gp.g
     rng = np.random.default_rng(group)
@@ -96,8 +101,10 @@ def _hidx_of_slots(p, slots):
     return out.reshape(slots.shape)
 
 
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("dtype,Hkv,Hq,group,n_req", [CASES[0], CASES[4], CASES[5]])
-def test_group_kernel_edited_slot_tables(dtype, Hkv, Hq, group, n_req):
+def test_group_kernel_edited_slot_tables(dtype, Hkv, Hq, group, n_req, waves, monkeypatch):
+    monkeypatch.setenv("FERRY_GROUP_WAVES", str(waves))
     gp, rp, _ = _twins(dtype, Hkv, Hq, group, n_req)
     g = gp.g
     k, L = g.k, g.n_layers
