@@ -258,11 +258,14 @@ template __global__ void k_fetch<4>(FetchArgs);
 template __global__ void k_fetch<8>(FetchArgs);
 template __global__ void k_fetch<16>(FetchArgs);
 
-__global__ void k_step_close(unsigned long long* acc) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) {
-    acc[2] = acc[0];
-    acc[3] = acc[1];
-    acc[0] = acc[1] = 0ull;
+__global__ void k_step_close(unsigned long long* acc, unsigned long long* host) {
+  // lanes 0 and 1 move the step's two counters into the mapped pinned words
+  // (system-scope stores over the host link: no copy launch on the stream
+  // ahead of the next step) and restart them from zero
+  const int t = threadIdx.x;
+  if (blockIdx.x == 0 && t < 2) {
+    __hip_atomic_store(host + t, acc[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    acc[t] = 0ull;
   }
 }
 

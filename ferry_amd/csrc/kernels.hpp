@@ -103,9 +103,9 @@ __global__ void k_sets_trim(Geo g, SetState st, const uint32_t* lane_live, const
 template <int NV>
 __global__ void k_fetch(FetchArgs a);
 __global__ void k_missq_push(Geo g, Ring ring, const ferry_miss* m, uint32_t n, int* err);
-// End of a decode step: acc[2..3] = the step's fetched and attended blocks
-// (acc[0..1]), then acc[0..1] = 0.
-__global__ void k_step_close(unsigned long long* acc);
+// End of a decode step: host[0..1] (mapped pinned memory) = the step's
+// fetched and attended blocks (acc[0..1]), then acc[0..1] = 0.
+__global__ void k_step_close(unsigned long long* acc, unsigned long long* host);
 
 // Vector-ALU attention (attn.hip); W wavefronts per workgroup; NT selects
 // non-temporal K/V loads.

@@ -106,10 +106,11 @@ struct ferry_ctx {
   uint32_t* worker_of_set = nullptr;
   unsigned long long* stats = nullptr;
   unsigned long long* sel_counts = nullptr;  // [kSelCounters * kSelStride]
-  // [4]: blocks fetched and blocks the prefix-group attention read in this
-  // step, then the same two of the last finished step (k_step_close)
+  // [2]: blocks fetched and blocks the prefix-group attention read in this
+  // step (moved to pend_host and cleared by k_step_close)
   unsigned long long* step_acc = nullptr;
-  unsigned long long* pend_host = nullptr;   // pinned [2]: the last step's two, copied at step end
+  unsigned long long* pend_host = nullptr;   // mapped pinned [2]: the last finished step's two
+  unsigned long long* pend_dev = nullptr;    // ... its device address
   double pol_min_mb = 32.0, pol_max_mb = 512.0, pol_target = 8.0;  // adaptive layer chunking
   uint32_t* done = nullptr;
   int* err = nullptr;
@@ -624,7 +625,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   TRY(dalloc(&c->worker_of_set, g.n_sets));
   TRY(dalloc(&c->stats, kStatCount));
   TRY(dalloc(&c->sel_counts, (size_t)kSelCounters * kSelStride));
-  TRY(dalloc(&c->step_acc, 4));
+  TRY(dalloc(&c->step_acc, 2));
   TRY(dalloc(&c->done, 1));
   TRY(dalloc(&c->err, 1));
 #define HIPT(x)                                                                        \
@@ -642,13 +643,14 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   HIPT(hipMemset(c->ring_state2, 0, (size_t)W * kStateStride * 8));
   HIPT(hipMemset(c->stats, 0, kStatCount * 8));
   HIPT(hipMemset(c->sel_counts, 0, (size_t)kSelCounters * kSelStride * 8));
-  HIPT(hipMemset(c->step_acc, 0, 32));
-  if (hipHostMalloc((void**)&c->pend_host, 16, hipHostMallocDefault) != hipSuccess) {
+  HIPT(hipMemset(c->step_acc, 0, 16));
+  if (hipHostMalloc((void**)&c->pend_host, 16, hipHostMallocMapped) != hipSuccess) {
     c->pend_host = nullptr;
     release(c);
     return fail(FERRY_ENOMEM, "hipHostMalloc of the step counter failed");
   }
   c->pend_host[0] = c->pend_host[1] = 0;
+  HIPT(hipHostGetDevicePointer((void**)&c->pend_dev, c->pend_host, 0));
   HIPT(hipMemset(c->done, 0, 4));
   HIPT(hipMemset(c->err, 0, 4));
   HIPT(hipMemset(c->pool, 0, nslots * g.bb));
@@ -1108,9 +1110,8 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
     }
   }
   // the step's fetched blocks, for the next step's adaptive chunking
-  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(64), 0, ms, ctx->step_acc);
+  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(64), 0, ms, ctx->step_acc, ctx->pend_dev);
   HIPC(hipGetLastError());
-  HIPC(hipMemcpyAsync(ctx->pend_host, ctx->step_acc + 2, 16, hipMemcpyDeviceToHost, ms));
   return FERRY_OK;
 }
 
