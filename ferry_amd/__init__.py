@@ -375,7 +375,9 @@ class Executor:
 
     def attn_kernel(self):
         """(kind, waves) of the attention kernel sparse_decode runs: kind is
-        ATTN_VALU, ATTN_MFMA (per request row) or ATTN_GROUP (per group set)."""
+        ATTN_VALU, ATTN_MFMA (per request row) or ATTN_GROUP (per group set);
+        waves per workgroup of that launch (the group kernel runs 8 on a launch
+        of no more group sets than CUs where its LDS allows, else 4)."""
         kind, waves = _i32(), _i32()
         _check(lib.ferry_attn_kernel(self._h, C.byref(kind), C.byref(waves)), "ferry_attn_kernel")
         return kind.value, waves.value

@@ -345,15 +345,21 @@ void launch_group_w(const dim3& grid, size_t lds, hipStream_t s, const AttnArgs&
   hipLaunchKernelGGL((k_attn_group<DT, G, NT, W>), grid, dim3(W * 64), lds, s, a.g, a.q, a.slots,
                      a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err, a.attn_blocks);
 }
-// Eight wavefronts per workgroup for a launch with no more group sets than
-// CUs (where they fit the LDS), four otherwise; `force` (4 or 8) overrides.
+// Wavefronts per workgroup of a prefix-group launch over `sets` group sets:
+// eight where the launch has no more sets than the GPU has CUs and the wider
+// LDS fits one CU, four otherwise; `force` (4 or 8) overrides the launch rule.
+int group_launch_waves(int dtype, int ntile, long gk, long sets, int cus, int force) {
+  const bool want = force ? force == kGroupWideWaves : sets <= (long)cus;
+  return want && attn_group_lds_bytes(dtype, ntile, gk, kGroupWideWaves) <= (size_t)kGroupMaxLds
+             ? kGroupWideWaves
+             : group_waves(dtype);
+}
 template <int DT, int G, int NT>
 void launch_group(const dim3& grid, int cus, int force, hipStream_t s, const AttnArgs& a) {
   const long gk = (long)a.g.group * a.g.k;
-  const size_t wide = attn_group_lds_bytes(DT, NT, gk, kGroupWideWaves);
-  const bool want = force ? force == kGroupWideWaves : grid.x <= (unsigned)cus;
-  if (want && wide <= (size_t)kGroupMaxLds)
-    launch_group_w<DT, G, NT, kGroupWideWaves>(grid, wide, s, a);
+  if (group_launch_waves(DT, NT, gk, grid.x, cus, force) == kGroupWideWaves)
+    launch_group_w<DT, G, NT, kGroupWideWaves>(
+        grid, attn_group_lds_bytes(DT, NT, gk, kGroupWideWaves), s, a);
   else
     launch_group_w<DT, G, NT, group_waves(DT)>(
         grid, attn_group_lds_bytes(DT, NT, gk, group_waves(DT)), s, a);
@@ -983,6 +989,9 @@ int ferry_attn_kernel(const ferry_ctx* ctx, int32_t* kind, int32_t* waves) {
   const AttnPlan p = attn_plan(ctx);
   *kind = p.grouped ? FERRY_ATTN_GROUP : p.mfma ? FERRY_ATTN_MFMA : FERRY_ATTN_VALU;
   *waves = p.waves;
+  if (p.grouped)  // ferry_sparse_decode's launch: every layer's group sets
+    *waves = group_launch_waves(p.dtype, p.tiles, (long)ctx->g.group * ctx->g.k,
+                                (long)ctx->g.n_owners * ctx->g.L * ctx->g.Hkv, p.cus, p.group_w);
   return FERRY_OK;
 }
 

@@ -270,7 +270,9 @@ int ferry_sparse_decode(ferry_ctx* ctx, const float* q, const uint32_t* slots,
 /* Which attention kernel ferry_sparse_decode runs for this context:
  * *kind = FERRY_ATTN_VALU, FERRY_ATTN_MFMA (one workgroup per request row) or
  * FERRY_ATTN_GROUP (one per prefix-group set), *waves = wavefronts per
- * workgroup.  No reference counterpart (the reference has one proxy kernel);
+ * workgroup of its launch (the prefix-group kernel runs eight on a launch of
+ * no more group sets than the GPU has CUs where its LDS allows, else four,
+ * so a layer range of ferry_sparse_decode_layers can differ).  No reference counterpart (the reference has one proxy kernel);
  * for callers that report rooflines per kernel. */
 int ferry_attn_kernel(const ferry_ctx* ctx, int32_t* kind, int32_t* waves);
 

@@ -38,7 +38,9 @@ CASES = [
 ROW_TOL = {F.F16: 1e-3, F.BF16: 1e-3, F.FP8: 5e-3}
 
 
-def _twins(dtype, Hkv, Hq, group, n_req, L=2, k=16, prefix=24, steps=3):
+def _twins(dtype, Hkv, Hq, group, n_req, L=2, k=16, prefix=24, steps=3, waves=8):
+    # waves: what the group launch runs; every case here fits the wider LDS
+    # and launches fewer group sets than the GPU has CUs, so 8 unless forced
     # a set holds every block its members select in one step (at most group * k)
     cap = max(96, group * k + 32)
     print(f"[group-attn] dtype={dtype} Hkv={Hkv} Hq={Hq} group={group} B={n_req} C={cap}",
@@ -46,7 +48,7 @@ def _twins(dtype, Hkv, Hq, group, n_req, L=2, k=16, prefix=24, steps=3):
     mb, sels = _zipf_stream(n_req, L, Hkv, k, 40, 120, steps, group=group, prefix=prefix)
     grp_pair = Pair(n_req, L, Hkv, Hq, k, cap, mb, dtype, group=group, attn=F.ATTN_GROUP)
     row_pair = Pair(n_req, L, Hkv, Hq, k, cap, mb, dtype, group=group, attn=F.ATTN_MFMA)
-    assert grp_pair.ex.attn_kernel() == (F.ATTN_GROUP, 4)
+    assert grp_pair.ex.attn_kernel() == (F.ATTN_GROUP, waves)
     assert row_pair.ex.attn_kernel() == (F.ATTN_MFMA, 4)
     for sel in sels:
         grp_pair.check_fetched_bytes(grp_pair.step(sel))
@@ -72,7 +74,7 @@ def _rel(a, b):
 def test_group_kernel_matches_oracle_and_row_kernel(dtype, Hkv, Hq, group, n_req, waves,
                                                     monkeypatch):
     monkeypatch.setenv("FERRY_GROUP_WAVES", str(waves))
-    gp, rp, sel = _twins(dtype, Hkv, Hq, group, n_req)
+    gp, rp, sel = _twins(dtype, Hkv, Hq, group, n_req, waves=waves)
     g = gp.g
     rng = np.random.default_rng(group)
     q = torch.from_numpy(rng.standard_normal((n_req, g.n_layers, Hq, 128)).astype(np.float32)).cuda()
@@ -105,7 +107,7 @@ def _hidx_of_slots(p, slots):
 @pytest.mark.parametrize("dtype,Hkv,Hq,group,n_req", [CASES[0], CASES[4], CASES[5]])
 def test_group_kernel_edited_slot_tables(dtype, Hkv, Hq, group, n_req, waves, monkeypatch):
     monkeypatch.setenv("FERRY_GROUP_WAVES", str(waves))
-    gp, rp, _ = _twins(dtype, Hkv, Hq, group, n_req)
+    gp, rp, _ = _twins(dtype, Hkv, Hq, group, n_req, waves=waves)
     g = gp.g
     k, L = g.k, g.n_layers
     slots = gp.bufs["slots"].cpu().numpy().view(np.uint32).reshape(n_req, L, Hkv, k).copy()
@@ -162,7 +164,10 @@ def test_group_kernel_limits():
 
 def test_auto_picks_the_group_kernel_where_it_fits():
     auto = F.Executor(8, 1, 2, 16, 96, 96, q_heads=8, group=4, dtype=F.FP8)
-    assert auto.attn_kernel() == (F.ATTN_GROUP, 4)
+    assert auto.attn_kernel() == (F.ATTN_GROUP, 8)  # 4 group sets: eight wavefronts
+    # 2 groups x 32 layers x 8 kv heads = 512 group sets, more than the CUs: four
+    many = F.Executor(8, 32, 8, 16, 96, 96, q_heads=32, group=4, dtype=F.FP8)
+    assert many.attn_kernel() == (F.ATTN_GROUP, 4)
     solo = F.Executor(8, 1, 2, 16, 96, 96, q_heads=8, group=1, dtype=F.FP8)
     assert solo.attn_kernel() == (F.ATTN_MFMA, 4)
     wide = F.Executor(16, 1, 1, 16, 96, 96, q_heads=8, group=16, dtype=F.FP8)  # 128 columns
