@@ -157,6 +157,7 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
   int* sh = reinterpret_cast<int*>(red_ml + W * COLS * 2);                // [W] scan
   uint32_t* msk = reinterpret_cast<uint32_t*>(rings);                     // [C] listing
   uint32_t* own = msk + g.C;                                              // [GK] listing
+  uint32_t* mcnt = own + GK;                                              // [group] listing
   float* red_o = reinterpret_cast<float*>(rings);                         // [W][TR*16][DP] merge
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -169,6 +170,7 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
 
   // ---- 1. the distinct list of the group's selections
   for (int i = tid; i < g.C; i += NT) msk[i] = 0u;
+  for (int i = tid; i < g.group; i += NT) mcnt[i] = 0u;
   __syncthreads();
   bool bad = false;
   for (int e = tid; e < GK; e += NT) {
@@ -190,6 +192,7 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
       }
     }
     own[e] = mine;
+    if (mine != kNone) atomicAdd(&mcnt[mi], 1u);
   }
   if (bad) set_error(err, FERRY_ERANGE);
   __syncthreads();
@@ -209,7 +212,9 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
     }
   }
   // own entries after them, ordered by (member, slot); equal keys are the same
-  // block for the same member, so their order among themselves does not matter
+  // block for the same member, so their order among themselves does not matter.
+  // An entry's rank: the own entries of earlier members (their counts) and
+  // those of its own member's row before it, k positions instead of group * k
   int cown = 0;
   for (int e = tid; e < GK; e += NT) cown += own[e] != kNone;
   int n_own = 0;
@@ -220,11 +225,10 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
       if (s == kNone) continue;
       const int mi = e / g.k;
       int rank = 0;
-      for (int e2 = 0; e2 < GK; ++e2) {
+      for (int m = 0; m < mi; ++m) rank += (int)mcnt[m];
+      for (int e2 = mi * g.k; e2 < (mi + 1) * g.k; ++e2) {
         const uint32_t s2 = own[e2];
-        if (s2 == kNone) continue;
-        const int m2 = e2 / g.k;
-        rank += m2 < mi || (m2 == mi && (s2 < s || (s2 == s && e2 < e)));
+        rank += s2 != kNone && (s2 < s || (s2 == s && e2 < e));
       }
       lslot[n_in + rank] = s;
       lmask[n_in + rank] = 1u << mi;

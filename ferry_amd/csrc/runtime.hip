@@ -167,8 +167,8 @@ namespace {
 // Whether the prefix-group attention kernel (k_attn_group) can run this
 // geometry: every wavefront holds all group * G query columns (at most
 // kGroupMaxTiles tiles of 16), the workgroup's LDS fits one CU, and the
-// per-slot member masks plus the list's scratch fit the block rings while the
-// list is built.
+// per-slot member masks plus the list's scratch (a slot per selection and a
+// count per member) fit the block rings while the list is built.
 bool group_attn_fits(const ferry_config* c) {
   const int G = c->q_heads / c->kv_heads;
   if (c->group < 2 || G < 2 || c->dtype == FERRY_F32 || c->group * G > 16 * kGroupMaxTiles)
@@ -176,7 +176,7 @@ bool group_attn_fits(const ferry_config* c) {
   const long gk = (long)c->group * c->k;
   const int ntile = (c->group * G + 15) / 16;
   return attn_group_lds_bytes(c->dtype, ntile, gk, group_waves(c->dtype)) <= (size_t)kGroupMaxLds &&
-         4 * ((long)c->slots_per_set + gk) <=
+         4 * ((long)c->slots_per_set + gk + c->group) <=
              (long)group_waves(c->dtype) * group_ring_bytes(c->dtype);
 }
 
