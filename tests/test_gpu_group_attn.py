@@ -75,8 +75,12 @@ def test_group_kernel_matches_oracle_and_row_kernel(dtype, Hkv, Hq, group, n_req
                                                     monkeypatch):
     monkeypatch.setenv("FERRY_GROUP_WAVES", str(waves))
     gp, rp, sel = _twins(dtype, Hkv, Hq, group, n_req, waves=waves)
+    _check_twins(gp, rp, sel, dtype, Hq, n_req, seed=group)
+
+
+def _check_twins(gp, rp, sel, dtype, Hq, n_req, seed):
     g = gp.g
-    rng = np.random.default_rng(group)
+    rng = np.random.default_rng(seed)
     q = torch.from_numpy(rng.standard_normal((n_req, g.n_layers, Hq, 128)).astype(np.float32)).cuda()
     got = _decode(gp, q, gp.bufs["slots"])
     row = _decode(rp, q, rp.bufs["slots"])
@@ -86,6 +90,19 @@ def test_group_kernel_matches_oracle_and_row_kernel(dtype, Hkv, Hq, group, n_req
     assert _rel(got, row).max() < ROW_TOL[dtype]
     # the list and its order do not depend on the order the atomics ran in
     assert np.array_equal(got, _decode(gp, q, gp.bufs["slots"]))
+
+
+@pytest.mark.parametrize("waves", [4, 8])
+def test_group_kernel_many_repeats_at_large_k(waves, monkeypatch):
+    # 256 selections per row drawn with replacement from contexts of 40-120
+    # blocks: most of a row repeats, and every repeat is an entry of its own,
+    # placed after the earlier members' entries by its member's row alone
+    monkeypatch.setenv("FERRY_GROUP_WAVES", str(waves))
+    gp, rp, sel = _twins(F.FP8, 2, 8, 4, 8, L=1, k=256, waves=waves)
+    rows = sel.reshape(-1, 256)
+    repeats = sum(256 - np.unique(r).size for r in rows)
+    assert repeats > 100 * rows.shape[0], repeats
+    _check_twins(gp, rp, sel, F.FP8, 8, 8, seed=11)
 
 
 def _hidx_of_slots(p, slots):
