@@ -130,8 +130,9 @@ __global__ void k_attn_mfma(Geo g, const float* q, const uint32_t* slots, const 
 // flight instead of 64) measured 5% slower for a whole launch and kept the
 // overlapped fetch off the CUs: the shared-prefix step took 4.23 ms against
 // 3.80.  A launch with no more group sets than CUs, which leaves CUs idle
-// with four, runs kGroupWideWaves wavefronts per workgroup: each workgroup's
-// time is then bound by its own loads in flight, not by the CU's share.
+// with four, runs kGroupWideWaves wavefronts per workgroup (the same rings):
+// a workgroup that has its CU alone then keeps twice the blocks in flight and
+// spreads its arithmetic over twice the wavefronts.
 constexpr int kGroupMaxTiles = 4;         // query tiles every wavefront attends with (64 columns)
 constexpr int kGroupMaxLds = 160 * 1024;  // LDS of one CU
 constexpr int group_waves(int dtype) { return dtype == FERRY_F32 ? 0 : 4; }
