@@ -227,100 +227,107 @@ def lognormal_reuse(B, k, mu=2.0, sigma=1.2, seed=17):
     return np.clip(1.0 - fresh / k, 0.0, 1.0)
 
 
-def cpu_baseline(w, ctx, max_blocks, host_bytes, host_scales, host_blocks, n_req, steps, reuse_r):
-    """Oracle C path (bookkeeping + memcpy gather + fp32 attention), 1 thread,
-    on the first n_req requests of the same workload and the same host tier."""
+def cpu_plan(w, ctx, n_req, steps, reuse_r):
+    """The sampled requests' selections for a steady cpu_baseline: steps + 1
+    steps of the same generator (draws are keyed per request, so requests
+    0..n_req-1 draw exactly what they draw in the full batch), no resets."""
+    from oracle import pyoracle as O
+
+    sg = O.selgen(n_req, w["L"], w["Hkv"], w["k"], ctx[:n_req], dist=1, zipf_s=w["zipf"],
+                  reuse=w["reuse"], group=w["group"], prefix_blocks=w["prefix"], seed=3,
+                  reuse_r=None if reuse_r is None else reuse_r[:n_req])
+    return [(O.selgen_step(sg, t), ()) for t in range(steps + 1)]
+
+
+class _CpuRun:
+    """One oracle executor with its host pool image, stepping a plan of
+    (selections, lanes reset before the step) with ora_cpu_step."""
+
+    def __init__(self, g, host_bytes, host_scales, q):
+        from oracle import pyoracle as O
+
+        self.O, self.g, self.q = O, g, q
+        self.ex = O.Executor(g)
+        bb = O.lib.ora_block_bytes(O.C.byref(g))
+        self.host, self.hsc = host_bytes, host_scales
+        self.pool = np.zeros(self.ex.n_sets * g.cap * bb, np.uint8)
+        self.pscale = (np.zeros(self.ex.n_sets * g.cap * 2, np.float32)
+                       if host_scales is not None else None)
+        self.out = np.zeros(q.size, np.float32)
+        self.slots = np.zeros(g.n_req * g.n_layers * g.kv_heads * g.k, np.uint32)
+        self.mc = np.zeros(self.ex.n_sets, np.uint32)
+        self.ms = np.zeros(self.ex.n_sets * self.ex.max_sel, O.MISS_DTYPE)
+        self.cnt = np.zeros(3, np.uint64)
+        self.rc = 0
+
+    def step(self, sel, resets=()):
+        for ln in resets:
+            self.ex.reset_owner(int(ln))
+        rc = self.O.lib.ora_cpu_step(
+            self.ex.ptr, sel, self.host.ctypes.data,
+            None if self.hsc is None else self.hsc.ctypes.data, self.pool.ctypes.data,
+            None if self.pscale is None else self.pscale.ctypes.data, self.q.reshape(-1),
+            self.out, self.slots, self.mc, self.ms, self.cnt)
+        self.rc = self.rc or rc
+        return rc
+
+
+def cpu_baseline(w, max_blocks, host_bytes, host_scales, host_blocks, n_req, plan, what):
+    """The oracle's C step (bookkeeping + memcpy gather + fp32 attention,
+    oracle/cpu_step.c) on the first n_req requests of the same workload and
+    the same host tier, 1 thread: plan[0] is an untimed cold step, the rest
+    are timed.  Then the same on every usable host core (cpu_baseline_threads).
+    `what` says what the plan's steps are."""
     from oracle import pyoracle as O
 
     dt = {"f16": O.F16, "bf16": O.BF16, "fp8": O.FP8, "f32": O.F32}[w["dtype"]]
     L, H, Hq, k, C = w["L"], w["Hkv"], w["Hq"], w["k"], w["C"]
-    n_req = max(n_req, w["group"])
     g = O.make_geom(n_req=n_req, group=w["group"], n_layers=L, kv_heads=H, q_heads=Hq, k=k, cap=C,
                     max_blocks=max_blocks, dtype=dt, host_blocks=host_blocks, seed=7,
                     value_std=0.5)
-    ex = O.Executor(g)
-    sg = O.selgen(n_req, L, H, k, ctx[:n_req], dist=1, zipf_s=w["zipf"], reuse=w["reuse"],
-                  group=w["group"], prefix_blocks=w["prefix"], seed=3,
-                  reuse_r=None if reuse_r is None else reuse_r[:n_req])
-    bb = O.lib.ora_block_bytes(O.C.byref(g))
-    pool = np.zeros(ex.n_sets * C * bb, np.uint8)
-    pscale = np.zeros(ex.n_sets * C * 2, np.float32) if host_scales is not None else None
-    rng = np.random.default_rng(1)
-    q = rng.standard_normal((n_req, L, Hq, 128)).astype(np.float32)
-    out = np.zeros(q.size, np.float32)
-    slots = np.zeros(n_req * L * H * k, np.uint32)
-    mc = np.zeros(ex.n_sets, np.uint32)
-    ms = np.zeros(ex.n_sets * ex.max_sel, O.MISS_DTYPE)
-    cnt = np.zeros(3, np.uint64)
+    q = np.random.default_rng(1).standard_normal((n_req, L, Hq, 128)).astype(np.float32)
+    cr = _CpuRun(g, host_bytes, host_scales, q)
     times, misses = [], []
-    for t in range(steps + 1):  # step 0 is the cold fill, not timed
-        sel = O.selgen_step(sg, t)
+    for t, (sel, resets) in enumerate(plan):  # step 0 is the cold fill, not timed
         t0 = time.perf_counter()
-        rc = O.lib.ora_cpu_step(ex.ptr, sel, host_bytes.ctypes.data,
-                                None if host_scales is None else host_scales.ctypes.data,
-                                pool.ctypes.data, None if pscale is None else pscale.ctypes.data,
-                                q.reshape(-1), out, slots, mc, ms, cnt)
+        rc = cr.step(sel, resets)
         dt_s = time.perf_counter() - t0
         if rc:
             raise RuntimeError(f"ora_cpu_step rc={rc}")
         if t:
             times.append(dt_s)
-            misses.append(int(cnt[1]))
+            misses.append(int(cr.cnt[1]))
+    steps = len(plan) - 1
     t_step = float(np.mean(times))
-    res = {"value": round(n_req / t_step, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+    toks = float(np.mean([np.count_nonzero(sel.reshape(n_req, -1)[:, 0] != O.NONE)
+                          for sel, _ in plan[1:]]))
+    res = {"value": round(toks / t_step, 3), "unit": "tok/s", "cores": 1, "kind": "port",
            "sample": f"oracle C step (bookkeeping + memcpy gather + fp32 attention) on "
-                     f"{n_req} of {w['B']} requests x {L} layers x {H} kv heads, {steps} steps "
-                     f"after one untimed cold step; {t_step * 1e3:.0f} ms/step",
+                     f"{n_req} of {w['B']} requests x {L} layers x {H} kv heads, {steps} {what} "
+                     f"after one untimed one; {t_step * 1e3:.0f} ms/step",
            "miss_blocks_per_s": round(float(np.mean(misses)) / t_step, 1),
            "ms_per_step": round(t_step * 1e3, 1)}
-    del pool, pscale, ex
-    res["all_cores"] = cpu_baseline_threads(g, sg_args=(n_req, L, H, k, ctx[:n_req], w, reuse_r),
-                                            host_bytes=host_bytes, host_scales=host_scales,
-                                            steps=steps, q=q)
+    del cr
+    res["all_cores"] = cpu_baseline_threads(g, host_bytes, host_scales, plan, q, toks, what)
     return res
 
 
-def cpu_baseline_threads(g, sg_args, host_bytes, host_scales, steps, q):
+def cpu_baseline_threads(g, host_bytes, host_scales, plan, q, toks, what):
     """The same oracle step on every host core the process may use (at most 16,
     the host share of one GPU): one independent replica of the sampled requests
     per thread, all stepping concurrently (the C calls release the GIL)."""
     import threading
 
-    from oracle import pyoracle as O
-
-    n_req, L, H, k, ctx, w, reuse_r = sg_args
     T = max(1, min(16, len(os.sched_getaffinity(0))))
-    sg = O.selgen(n_req, L, H, k, ctx, dist=1, zipf_s=w["zipf"], reuse=w["reuse"],
-                  group=w["group"], prefix_blocks=w["prefix"], seed=3,
-                  reuse_r=None if reuse_r is None else reuse_r)
-    sels = [O.selgen_step(sg, t) for t in range(steps + 1)]
-    bb = O.lib.ora_block_bytes(O.C.byref(g))
-    reps = []
-    for _ in range(T):
-        ex = O.Executor(g)
-        reps.append(dict(ex=ex, pool=np.zeros(ex.n_sets * g.cap * bb, np.uint8),
-                         pscale=(np.zeros(ex.n_sets * g.cap * 2, np.float32)
-                                 if host_scales is not None else None),
-                         out=np.zeros(q.size, np.float32),
-                         slots=np.zeros(n_req * L * H * k, np.uint32),
-                         mc=np.zeros(ex.n_sets, np.uint32),
-                         ms=np.zeros(ex.n_sets * ex.max_sel, O.MISS_DTYPE),
-                         cnt=np.zeros(3, np.uint64), rc=0))
+    reps = [_CpuRun(g, host_bytes, host_scales, q) for _ in range(T)]
     start = threading.Barrier(T + 1)
     done = threading.Barrier(T + 1)
 
     def worker(r):
-        def one(t):
-            rc = O.lib.ora_cpu_step(r["ex"].ptr, sels[t], host_bytes.ctypes.data,
-                                    None if host_scales is None else host_scales.ctypes.data,
-                                    r["pool"].ctypes.data,
-                                    None if r["pscale"] is None else r["pscale"].ctypes.data,
-                                    q.reshape(-1), r["out"], r["slots"], r["mc"], r["ms"], r["cnt"])
-            r["rc"] = r["rc"] or rc
-        one(0)  # cold fill, untimed
+        r.step(*plan[0])  # cold fill, untimed
         start.wait()
-        for t in range(1, steps + 1):
-            one(t)
+        for sel, resets in plan[1:]:
+            r.step(sel, resets)
         done.wait()
 
     th = [threading.Thread(target=worker, args=(r,)) for r in reps]
@@ -332,15 +339,16 @@ def cpu_baseline_threads(g, sg_args, host_bytes, host_scales, steps, q):
     wall = time.perf_counter() - t0
     for t in th:
         t.join()
-    if any(r["rc"] for r in reps):
+    if any(r.rc for r in reps):
         raise RuntimeError("ora_cpu_step failed in a worker thread")
-    return {"value": round(T * n_req * steps / wall, 3), "unit": "tok/s", "cores": T,
+    steps = len(plan) - 1
+    return {"value": round(T * toks * steps / wall, 3), "unit": "tok/s", "cores": T,
             "host_cores": os.cpu_count(), "usable_cores": len(os.sched_getaffinity(0)),
             "why_not_all": "one GPU's share of the host is 16 cores; the other cores of a "
                            "multi-GPU host belong to the other GPUs' processes"
             if T < (os.cpu_count() or T) else None,
-            "sample": f"{T} threads, each an independent replica of the same {n_req} requests, "
-                      f"{steps} concurrent steps after one untimed cold step; "
+            "sample": f"{T} threads, each an independent replica of the same {g.n_req} requests, "
+                      f"{steps} concurrent {what} after one untimed one; "
                       f"{wall / steps * 1e3:.0f} ms per concurrent step",
             "ms_per_step": round(wall / steps * 1e3, 1)}
 
@@ -411,7 +419,7 @@ def distinct_slots(slots, group, k):
 
 
 def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_cpu=True,
-        extras=True, steps=None):
+        extras=True, steps=None, cpu_steps=None):
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream()
     side = torch.cuda.Stream()  # default priority
@@ -478,13 +486,18 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
         step(t)
     torch.cuda.synchronize()
     st0 = ex.stats()
-    # timed region: K whole steps, synchronised on both sides
+    # timed region: K whole steps, synchronised on both sides; an event on the
+    # main stream between steps (a step ends on it) gives each step's duration
+    step_ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_timed + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for t in range(a.warmup, a.warmup + n_timed):
+    for i, t in enumerate(range(a.warmup, a.warmup + n_timed)):
+        step_ev[i].record(stream)
         step(t)
+    step_ev[n_timed].record(stream)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    step_ms = [step_ev[i].elapsed_time(step_ev[i + 1]) for i in range(n_timed)]
     st1 = ex.stats()
     if st1["device_error"]:
         raise RuntimeError(f"device error {st1['device_error']}")
@@ -588,6 +601,8 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
                    "frac_of_plain_gather": round(grp_gbs / dgather_gbs, 4)}
     res = {
         "ms_per_step": round(ms_step, 3),
+        "step_ms_p50": round(float(np.percentile(step_ms, 50)), 3),
+        "step_ms_p99": round(float(np.percentile(step_ms, 99)), 3),
         "value": round(B / (ms_step * 1e-3), 2),
         "miss_rate": round(timed_misses / max(1, timed_sel), 4),
         "preroll": {"steps": n_pre, "seconds": round(pre_s, 1),
@@ -631,8 +646,10 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
     }
     if want_cpu and not a.no_cpu:
         host, hsc = ex.hosttier_array()
-        res["cpu_baseline"] = cpu_baseline(w, ctx, sg.max_blocks, host, hsc, a.host_blocks,
-                                           a.cpu_reqs, a.cpu_steps, reuse_r)
+        n_req = max(a.cpu_reqs, w["group"])  # a whole prefix group
+        plan = cpu_plan(w, ctx, n_req, cpu_steps or a.cpu_steps, reuse_r)
+        res["cpu_baseline"] = cpu_baseline(w, sg.max_blocks, host, hsc, a.host_blocks, n_req,
+                                           plan, "steps")
     ex.close()
     return res
 
@@ -726,24 +743,25 @@ def run_handoff(a, ex, F, torch, stream, dtype, n_timed):
                                 round(moved / (t_imp * 1e-3) / 1e9 / nt_copy_gbs, 4)]}
 
 
-def arrival_plan(a, w, F, n_ticks, zipf):
+def arrival_plan(a, w, F, n_ticks, zipf, process, period_ticks, skew):
     """Virtual-clock schedule of an arrival run (one time unit = one tick).
     The first B requests are queued at t=0 with residual lengths so that the
     lanes start full; further requests arrive as a Poisson or Markov-modulated
-    Poisson process at 0.9 of the lanes' service rate.  Returns per tick the
-    selections, the lanes admitted (their sets are reset) and the resident
-    count, plus the per-request arrival/admission ticks."""
+    Poisson process at 0.9 of the lanes' service rate (the MMPP switches
+    between rates 1x and 10x, with exponential sojourns of mean period_ticks).
+    Returns per tick the selections, the lanes admitted (their sets are reset)
+    and the resident count, plus the per-request arrival/admission ticks."""
     B, L, H, k = w["B"], w["L"], w["Hkv"], w["k"]
     if w["group"] != 1:
         raise SystemExit("arrivals need private sets (group 1): a prefix group's lanes share sets")
     lo_len, hi_len = map(int, a.len.split(","))
     gap = a.gap_ticks or (lo_len + hi_len) / 2.0 / B / 0.9  # mean gap over the run
     n_req = min(65535, B + int(n_ticks / gap * 2) + 16)
-    kind = F.ARRIVAL_MMPP if a.arrivals == "mmpp" else F.ARRIVAL_POISSON
+    kind = F.ARRIVAL_MMPP if process == "mmpp" else F.ARRIVAL_POISSON
     # the MMPP spends half its time at each rate (equal mean sojourns): its
     # slow-state gap is (1 + ratio) / 2 times the mean gap
     slow_gap = gap * (1 + MMPP_RATIO) / 2 if kind == F.ARRIVAL_MMPP else gap
-    arrive = np.concatenate([np.zeros(B), F.arrivals(kind, n_req - B, slow_gap, a.mmpp_period,
+    arrive = np.concatenate([np.zeros(B), F.arrivals(kind, n_req - B, slow_gap, period_ticks,
                                                      MMPP_RATIO, seed=5)])
     lens = F.ctx_uniform(6, n_req, lo_len, hi_len)
     lens[:B] = F.ctx_uniform(8, B, 1, hi_len)  # residual lengths of the initial batch
@@ -751,7 +769,7 @@ def arrival_plan(a, w, F, n_ticks, zipf):
     ctxs = F.ctx_uniform(7, n_req, lo, hi)
     sg = F.SelGen(B, L, H, k, np.full(B, hi, np.int32), dist=1, zipf_s=zipf, reuse=w["reuse"],
                   seed=3)
-    reuse_req = lognormal_reuse(n_req, k) if a.workload == "skew" else None
+    reuse_req = lognormal_reuse(n_req, k) if skew else None
     lane_reuse = np.full(B, w["reuse"])
     for ln in range(B):
         sg.retire(ln)
@@ -773,20 +791,27 @@ def arrival_plan(a, w, F, n_ticks, zipf):
     return plan, arrive, admit, sg.max_blocks, gap
 
 
-def run_arrivals(a, w, F, torch, zipf=None, workers=None, steal=None):
+def run_arrivals(a, w, F, torch, process, zipf=None, workers=None, steal=None, skew=False,
+                 period_ticks=None, want_cpu=False, cpu_steps=3):
     """Arrival-driven run: warmup ticks (lanes turn over), then --steps timed
     ticks.  Each tick resets the sets of newly admitted lanes on the stream and
-    runs one decode step over the resident lanes (idle lanes are empty rows)."""
+    runs one decode step over the resident lanes (idle lanes are empty rows).
+    The warmup ticks are gated: the oracle replays the first two lanes (their
+    resets included) and every tick their slots and miss lists must be
+    bit-equal, then their LRU state, pool bytes and attention (oracle/gate.py).
+    An event between timed ticks on the main stream gives each tick's time."""
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream()
     side = torch.cuda.Stream()  # default priority
     B, L, H, Hq, k, C = w["B"], w["L"], w["Hkv"], w["Hq"], w["k"], w["C"]
     zipf = w["zipf"] if zipf is None else zipf
+    period_ticks = a.mmpp_period if period_ticks is None else period_ticks
     lo_len, hi_len = map(int, a.len.split(","))
     warm = max(a.warmup, (lo_len + hi_len) // 2 + 8)
     n_ticks = warm + a.steps
     t0 = time.perf_counter()
-    plan, arrive, admit, max_blocks, gap = arrival_plan(a, w, F, n_ticks, zipf)
+    plan, arrive, admit, max_blocks, gap = arrival_plan(a, w, F, n_ticks, zipf, process,
+                                                        period_ticks, skew)
     gen_s = time.perf_counter() - t0
     sels = [torch.from_numpy(p[0].view(np.int32)).to(dev) for p in plan]
     adm = [torch.from_numpy(p[1]).to(dev) if len(p[1]) else None for p in plan]
@@ -794,12 +819,19 @@ def run_arrivals(a, w, F, torch, zipf=None, workers=None, steal=None):
     ex = F.Executor(B, L, H, k, C, max_blocks, q_heads=Hq, dtype=dtype, host_blocks=a.host_blocks,
                     fetch_workers=a.workers if workers is None else workers,
                     steal=a.steal if steal is None else steal,
-                    assign=F.ASSIGN_AFFINITY if a.workload == "skew" else F.ASSIGN_SPREAD)
+                    assign=F.ASSIGN_AFFINITY if skew else F.ASSIGN_SPREAD)
     ex.hosttier_fill()
     bufs = ex.alloc_step_buffers()
     qs = [torch.randn((B, L, Hq, 128), device=dev, dtype=torch.float32) for _ in range(2)]
     out = torch.empty_like(qs[0])
     torch.cuda.synchronize()
+    gate = None
+    if not a.no_cpu:
+        from oracle.gate import OwnerReplay
+
+        gate = OwnerReplay(n_req=B, group=1, n_layers=L, kv_heads=H, q_heads=Hq, k=k,
+                           slots_per_set=C, max_blocks=max_blocks, dtype=dtype,
+                           host_blocks=a.host_blocks)
 
     def tick(t):
         if adm[t] is not None:
@@ -809,16 +841,35 @@ def run_arrivals(a, w, F, torch, zipf=None, workers=None, steal=None):
 
     for t in range(warm):
         tick(t)
+        if gate is not None:
+            torch.cuda.synchronize()
+            gate.reset(plan[t][1])
+            gate.step(plan[t][0], bufs)
+    gate_res = gate.final(ex, qs[(warm - 1) & 1], out) if gate is not None else None
     torch.cuda.synchronize()
     st0 = ex.stats()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(a.steps + 1)]
     t0 = time.perf_counter()
-    for t in range(warm, n_ticks):
+    for i, t in enumerate(range(warm, n_ticks)):
+        ev[i].record(stream)
         tick(t)
+    ev[a.steps].record(stream)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    tick_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(a.steps)]
     st1 = ex.stats()
     if st1["device_error"]:
         raise RuntimeError(f"device error {st1['device_error']}")
+    cpu = None
+    if want_cpu and not a.no_cpu:
+        # the CPU path over the first two lanes of the same plan from its first
+        # tick (their own resets included): a cold tick, then cpu_steps ticks
+        host, hsc = ex.hosttier_array()
+        nr = 2
+        cplan = [(np.ascontiguousarray(p[0].reshape(B, -1)[:nr]).reshape(-1),
+                  tuple(int(x) for x in p[1] if x < nr)) for p in plan[:cpu_steps + 1]]
+        cpu = cpu_baseline(w, max_blocks, host, hsc, a.host_blocks, nr, cplan,
+                           "ticks of the plan (ticks 0..%d, resident lanes counted)" % cpu_steps)
     ex.close()
     tokens = sum(p[2] for p in plan[warm:])
     ms_tick = elapsed / a.steps * 1e3
@@ -826,23 +877,34 @@ def run_arrivals(a, w, F, torch, zipf=None, workers=None, steal=None):
                        if warm <= admit[r] < n_ticks and arrive[r] > 0])
     misses = st1["misses"] - st0["misses"]
     sel = st1["selections"] - st0["selections"]
-    return {
+    res = {
         "ms_per_step": round(ms_tick, 3),
+        "tick_ms_p50": round(float(np.percentile(tick_ms, 50)), 3),
+        "tick_ms_p99": round(float(np.percentile(tick_ms, 99)), 3),
         "value": round(tokens / elapsed, 2),
+        "unit": "tok/s",
         "miss_rate": round(misses / max(sel, 1), 4),
         "miss_blocks_per_s": round(misses / elapsed, 1),
-        "arrivals": {"process": a.arrivals, "mean_gap_ticks": round(gap, 4),
+        "steals_per_tick": round((st1["steals"] - st0["steals"]) / a.steps, 1),
+        "arrivals": {"process": process, "mean_gap_ticks": round(gap, 4),
                      "mean_rate_req_per_s": round(1e3 / (gap * ms_tick), 2),
-                     "mmpp_period_ms": round(a.mmpp_period * ms_tick, 1) if a.arrivals == "mmpp"
-                     else None,
-                     "len_steps": [lo_len, hi_len], "warmup_ticks": warm,
+                     "mmpp_sojourn_ticks": round(period_ticks, 3) if process == "mmpp" else None,
+                     "mmpp_sojourn_ms_at_measured_tick": round(period_ticks * ms_tick, 1)
+                     if process == "mmpp" else None,
+                     "decode_len_steps": [lo_len, hi_len], "warmup_ticks": warm,
+                     "timed_ticks": a.steps,
                      "mean_resident_lanes": round(tokens / a.steps, 2), "lanes": B,
                      "admitted_in_timed_ticks": int(sum(len(p[1]) for p in plan[warm:])),
                      "queue_wait_ticks_mean": round(float(waited.mean()), 3) if waited.size else 0.0,
                      "queue_wait_ticks_p99": round(float(np.percentile(waited, 99)), 3)
                      if waited.size else 0.0},
+        "gate": "pass (warmup ticks)" if gate_res is not None else "skipped (--no-cpu: no oracle leg)",
+        "gate_detail": gate_res,
         "selection_gen_s": round(gen_s, 2),
     }
+    if cpu is not None:
+        res["cpu_baseline"] = cpu
+    return res
 
 
 def run_queue(F, iters=3):
@@ -881,6 +943,158 @@ def run_queue(F, iters=3):
             "capacity": 1 << 20, "higher_is_better": True, "rows": rows}
 
 
+def skew_rows(a, F, torch, zipfs, steals, steps, cpu_zipf=None):
+    """Config 3 steady: stealing on vs off over the Zipf sweep, 304 persistent
+    fetch workgroups with request-affinity assignment, lognormal(2, 1.2)
+    fresh blocks per request-step; each row pre-rolled and gated like the
+    headline.  With cpu_zipf, the row of that skew also carries the CPU leg
+    (the CPU path has no workgroups: one CPU figure serves both steal rows)."""
+    w = WORKLOADS["skew"]
+    rows, cpu = [], None
+    for s in zipfs:
+        for steal in steals:
+            want = cpu_zipf is not None and s == cpu_zipf and cpu is None
+            r = run(a, w, F, torch, steal=steal, workers=304, zipf=s, want_cpu=want,
+                    extras=False, steps=steps)
+            if want:
+                cpu = r.get("cpu_baseline")
+            rows.append({"zipf": s, "steal": steal, "ms_per_step": r["ms_per_step"],
+                         "step_ms_p50": r["step_ms_p50"], "step_ms_p99": r["step_ms_p99"],
+                         "value": r["value"], "unit": "tok/s",
+                         "fetch_ms": r["kernel_ms"]["fetch"],
+                         "attention_ms": r["kernel_ms"]["attention"],
+                         "miss_rate": r["miss_rate"],
+                         "link_gbs": r["roofline_fetch"]["achieved"],
+                         "link_frac": r["roofline_fetch"]["frac"],
+                         "steals_per_step": r["steals_per_step"],
+                         "preroll_steps": r["preroll"]["steps"], "gate": r["gate"],
+                         "gate_selections_compared": (r["gate_detail"] or {}).get(
+                             "selections_compared")})
+            print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+    return rows, cpu
+
+
+def run_config1(a, F, torch, ticks=1000, rate_per_s=200.0):
+    """Config 1 as stated, in full on the GPU and on the CPU: 1 layer, 8 kv
+    heads MHA, fp32 KV, 4 request lanes of 2048-token contexts (128 blocks),
+    32 blocks per (request, head) uniform without replacement, 96 slots per
+    set (the LRU's steady state misses 25% of selections), a host tier of
+    all 4096 blocks, requests arriving by a Poisson process at 200/s on a
+    virtual 1 ms tick for 1000 ticks, each decoding U[8, 24] steps.  Every
+    tick resets newly admitted lanes and runs bookkeeping, fetch and
+    attention for the resident lanes.  The GPU ticks are timed as a whole;
+    the same ticks then run through the oracle's C step on one core.  The two
+    must agree bit for bit in every tick's slot table and miss counts and in
+    the final LRU state, and in the last tick's attention within 2e-3."""
+    from oracle import pyoracle as O
+
+    LANES, L, H, K, CTX, C, HB = 4, 1, 8, 32, 128, 96, 4096
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream()
+    gap_ms = 1000.0 / rate_per_s
+    arrive = F.arrivals(F.ARRIVAL_POISSON, int(ticks / gap_ms * 1.2), gap_ms, seed=11)
+    arrive = arrive[arrive < ticks]
+    lens = F.ctx_uniform(12, arrive.size, 8, 24)
+    sched = F.Sched(LANES, arrive, lens)
+    sg = F.SelGen(LANES, L, H, K, np.full(LANES, CTX, np.int32), dist=0, reuse=0.0, seed=13)
+    for ln in range(LANES):
+        sg.retire(ln)
+    plan = []
+    for t in range(ticks):
+        r = sched.tick(float(t))
+        for ln in r["retired"]:
+            sg.retire(int(ln))
+        for ln in r["admitted"]:
+            sg.admit(int(ln), int(r["lane_req"][ln]), CTX, t)
+        if r["resident"]:
+            plan.append((sg.step(t), np.array(r["admitted"], np.int32), r["resident"]))
+        elif len(r["admitted"]):
+            raise RuntimeError("a lane was admitted on a tick with no resident request")
+    n = len(plan)
+    ex = F.Executor(LANES, L, H, K, C, sg.max_blocks, q_heads=H, dtype=F.F32, host_blocks=HB,
+                    value_std=1.0)
+    ex.hosttier_fill()
+    sels = [torch.from_numpy(p[0].view(np.int32)).to(dev) for p in plan]
+    adm = [torch.from_numpy(p[1]).to(dev) if len(p[1]) else None for p in plan]
+    hist = torch.empty((n,) + tuple(ex.sel_shape), dtype=torch.int32, device=dev)
+    hist_mc = torch.empty((n, ex.n_sets), dtype=torch.int32, device=dev)
+    bufs = ex.alloc_step_buffers()
+    qn = np.random.default_rng(1).standard_normal((LANES, L, H, 128)).astype(np.float32)
+    q = torch.from_numpy(qn).to(dev)
+    out = torch.empty_like(q)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(n):
+        ev[i].record(stream)
+        if adm[i] is not None:
+            ex.reset_owners(adm[i], stream=stream)
+        b = dict(bufs, slots=hist[i], miss_count=hist_mc[i])
+        ex.decode_step(sels[i], q, b, out, chunks=1, stream=stream)
+    ev[n].record(stream)
+    torch.cuda.synchronize()
+    gpu_s = time.perf_counter() - t0
+    st = ex.stats()
+    if st["device_error"]:
+        raise RuntimeError(f"device error {st['device_error']}")
+    tick_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(n)]
+    # the CPU path over the same ticks, from the same pinned host tier
+    host, _ = ex.hosttier_array()
+    g = O.make_geom(n_req=LANES, n_layers=L, kv_heads=H, q_heads=H, k=K, cap=C,
+                    max_blocks=sg.max_blocks, dtype=O.F32, host_blocks=HB, seed=7, value_std=1.0)
+    cr = _CpuRun(g, host, None, qn)
+    cpu_slots = np.empty((n, cr.slots.size), np.uint32)
+    cpu_mc = np.empty((n, cr.mc.size), np.uint32)
+    cpu_s = 0.0
+    for i, (sel, lanes, _) in enumerate(plan):
+        t1 = time.perf_counter()
+        rc = cr.step(sel, lanes)
+        cpu_s += time.perf_counter() - t1
+        if rc:
+            raise RuntimeError(f"ora_cpu_step rc={rc} at tick {i}")
+        cpu_slots[i] = cr.slots
+        cpu_mc[i] = cr.mc
+    gs = hist.cpu().numpy().view(np.uint32).reshape(n, -1)
+    gmc = hist_mc.cpu().numpy().view(np.uint32)
+    bad = [i for i in range(n) if not (np.array_equal(gs[i], cpu_slots[i]) and
+                                        np.array_equal(gmc[i], cpu_mc[i]))]
+    fill, ord_, tag = ex.sets_state()
+    ofill, oord, otag = cr.ex.state()
+    live = np.arange(C)[None, :] < ofill[:, None]
+    state_eq = (np.array_equal(fill, ofill) and np.array_equal(tag, otag)
+                and np.array_equal(ord_[live], oord[live]))
+    go = out.cpu().numpy().reshape(-1, 128).astype(np.float64)
+    co = cr.out.reshape(-1, 128).astype(np.float64)
+    den = np.abs(co).max(axis=1)
+    rows = den > 0
+    att = float((np.abs(go - co).max(axis=1)[rows] / den[rows]).max()) if rows.any() else 0.0
+    if bad or not state_eq or not att < 2e-3:
+        raise RuntimeError(f"config 1: GPU and CPU differ (ticks {bad[:5]}, state equal "
+                           f"{state_eq}, attention {att:.3g})")
+    ex.close()
+    tokens = sum(p[2] for p in plan)
+    sel_total = int(sum(np.count_nonzero(p[0] != O.NONE) for p in plan))
+    return {"workload": "config 1: L=1, Hq=Hkv=8, D=128, fp32 KV, 16-token blocks, 4 lanes of "
+                        "2048-token contexts, top-k 32 uniform without replacement, 96 slots/set, "
+                        f"host tier {HB} blocks, Poisson arrivals {rate_per_s:.0f}/s on a 1 ms "
+                        f"virtual tick, decode lengths U[8, 24]",
+            "ticks": ticks, "decode_ticks": n, "requests": int(arrive.size),
+            "miss_rate": round(int(st["misses"]) / max(1, sel_total), 4),
+            "value": round(tokens / gpu_s, 1), "unit": "tok/s",
+            "ms_per_tick": round(gpu_s / n * 1e3, 4),
+            "tick_ms_p50": round(float(np.percentile(tick_ms, 50)), 4),
+            "tick_ms_p99": round(float(np.percentile(tick_ms, 99)), 4),
+            "bit_exact": {"ticks_compared": n, "slot_tables_equal": True,
+                          "miss_counts_equal": True, "final_lru_state_equal": True,
+                          "last_tick_attention_max_rel_diff": float(f"{att:.3g}")},
+            "cpu_baseline": {"value": round(tokens / cpu_s, 1), "unit": "tok/s", "cores": 1,
+                             "kind": "port", "ms_per_tick": round(cpu_s / n * 1e3, 4),
+                             "sample": f"the same {n} decode ticks in full through the oracle's "
+                                       f"C step (bookkeeping + memcpy gather + fp32 attention), "
+                                       f"one thread: one stream of ticks, each depending on the "
+                                       f"last"}}
+
+
 def main():
     a = parse()
     if a.rocprof_summary:
@@ -911,48 +1125,39 @@ def main():
     if a.arrivals != "none":
         if a.workload == "skew":  # the stealing sweep of config 3 under MMPP arrivals
             rows = []
-            for zs in (0.6, 1.0, 1.4):
-                for steal in (0, 1):
-                    r = run_arrivals(a, w, F, torch, zipf=zs, workers=304, steal=steal)
+            for zs in map(float, a.zipf_list.split(",")):
+                for steal in map(int, a.steal_list.split(",")):
+                    r = run_arrivals(a, w, F, torch, a.arrivals, zipf=zs, workers=304,
+                                     steal=steal, skew=True)
                     rows.append(dict({"zipf": zs, "steal": steal}, **r))
                     print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
             print(json.dumps({"workload": f"skew+{a.arrivals}", "rows": rows}), flush=True)
             return
-        r = run_arrivals(a, w, F, torch)
+        r = run_arrivals(a, w, F, torch, a.arrivals, want_cpu=True)
         print(json.dumps({"metric": "decode tok/s under request arrivals (lane turnover)",
                           "workload": f"{a.workload}+{a.arrivals}", "n_gpus": 1,
                           "steps": a.steps, "dtype": w["dtype"], "data": "synthetic",
                           "higher_is_better": True, **r}), flush=True)
         return
     if a.workload == "skew":
-        # stealing on vs off over the Zipf skew sweep, 304 persistent workgroups,
-        # request-affinity assignment of misses to workgroups
-        rows = []
-        for s in map(float, a.zipf_list.split(",")):
-            for steal in map(int, a.steal_list.split(",")):
-                r = run(a, w, F, torch, steal=steal, workers=304, zipf=s, want_cpu=False,
-                        extras=False)
-                rows.append({"zipf": s, "steal": steal, "fetch_ms": r["kernel_ms"]["fetch"],
-                             "attention_ms": r["kernel_ms"]["attention"],
-                             "ms_per_step": r["ms_per_step"], "miss_rate": r["miss_rate"],
-                             "link_gbs": r["roofline_fetch"]["achieved"],
-                             "steals_per_step": r["steals_per_step"],
-                             "preroll_steps": r["preroll"]["steps"], "gate": r["gate"]})
-                print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        rows, cpu = skew_rows(a, F, torch, list(map(float, a.zipf_list.split(","))),
+                              list(map(int, a.steal_list.split(","))), a.steps)
         print(json.dumps({"workload": "skew", "rows": rows}), flush=True)
         return
     r = run(a, w, F, torch)
-    # the long-context GQA and shared-prefix configurations, compact, in the same line
+    # the other configurations, compact, in the same line
     others = {}
     if a.workload == "7b" and not a.no_configs:
-        for name in ("gqa128k", "prefix_fp8"):
+        small = min(a.steps, 10)
+        for name, extras, cpu_steps in (("gqa128k", True, None), ("prefix_fp8", False, 2)):
             torch.cuda.empty_cache()
-            o = run(a, WORKLOADS[name], F, torch, want_cpu=False, extras=False,
-                    steps=min(a.steps, 10))
-            others[name] = {k2: o[k2] for k2 in ("ms_per_step", "value", "miss_rate",
-                                                  "miss_blocks_per_s", "kernel_ms", "gate")}
+            o = run(a, WORKLOADS[name], F, torch, want_cpu=True, extras=extras, steps=small,
+                    cpu_steps=cpu_steps)
+            others[name] = {k2: o[k2] for k2 in ("ms_per_step", "step_ms_p50", "step_ms_p99",
+                                                  "value", "miss_rate", "miss_blocks_per_s",
+                                                  "kernel_ms", "gate")}
             others[name]["unit"] = "tok/s"
-            others[name]["steps"] = min(a.steps, 10)
+            others[name]["steps"] = small
             others[name]["preroll_steps"] = o["preroll"]["steps"]
             others[name]["roofline"] = {k2: o["roofline"][k2] for k2 in
                                         ("kernel", "achieved", "peak", "unit", "frac",
@@ -963,7 +1168,43 @@ def main():
             others[name]["roofline_fetch"] = {k2: o["roofline_fetch"][k2] for k2 in
                                               ("kernel", "achieved", "peak", "unit", "frac",
                                                "plain_read_gbs", "frac_of_plain_read")}
+            for k2 in ("roofline_select", "roofline_select_mass", "roofline_handoff",
+                       "cpu_baseline"):
+                if o.get(k2) is not None:
+                    others[name][k2] = o[k2]
             print(json.dumps({name: others[name]}), file=sys.stderr, flush=True)
+        # config 3: the stealing sweep, steady
+        torch.cuda.empty_cache()
+        rows, cpu = skew_rows(a, F, torch, [0.6, 1.0, 1.4], [0, 1], small, cpu_zipf=1.0)
+        others["skew"] = {"workload": "config 3, steady: 7B shape, lognormal(2, 1.2) fresh "
+                                      "blocks per request-step, 304 persistent fetch workgroups "
+                                      "(request affinity), stealing off/on, Zipf swept",
+                          "steps": small, "rows": rows}
+        if cpu is not None:
+            others["skew"]["cpu_baseline"] = dict(cpu, note="the Zipf 1.0 stream; the CPU path "
+                                                  "has no fetch workgroups to steal between")
+        # config 3 under its arrivals: Markov-modulated (1x / 10x), sojourns of
+        # 50 ms of modelled time, a tick being the steady step of the same row
+        lo_zipf = {(row["zipf"], row["steal"]): row["ms_per_step"] for row in rows}
+        mm = []
+        for steal in (0, 1):
+            period = 50.0 / lo_zipf[(1.4, steal)]
+            o = run_arrivals(a, WORKLOADS["skew"], F, torch, "mmpp", zipf=1.4, workers=304,
+                             steal=steal, skew=True, period_ticks=period, want_cpu=steal == 0)
+            mm.append(dict({"zipf": 1.4, "steal": steal}, **o))
+            print(json.dumps(mm[-1]), file=sys.stderr, flush=True)
+        others["skew_mmpp"] = {"workload": "config 3 with Markov-modulated arrivals (rates 1x "
+                                           "and 10x, mean sojourn 50 ms of modelled time), Zipf "
+                                           "1.4, stealing off/on", "rows": mm}
+        if "cpu_baseline" in mm[0]:
+            others["skew_mmpp"]["cpu_baseline"] = mm[0].pop("cpu_baseline")
+        # config 2 under its Poisson arrivals (lane turnover)
+        others["7b_poisson"] = run_arrivals(a, WORKLOADS["7b"], F, torch, "poisson",
+                                            want_cpu=True)
+        print(json.dumps({"7b_poisson": others["7b_poisson"]}), file=sys.stderr, flush=True)
+        # config 1 in full, GPU and CPU
+        others["config1"] = run_config1(a, F, torch)
+        print(json.dumps({"config1": others["config1"]}), file=sys.stderr, flush=True)
     # HBM traffic per launch is not measured in this run: it comes from two
     # rocprofv3 counter runs of the same workload (FETCH_SIZE, WRITE_SIZE),
     # stored in profiles/traffic.json with the commit each entry was measured at
@@ -991,8 +1232,13 @@ def main():
     put(r.get("roofline_select_mass"), a.workload + "_mass", ("bytes_per_launch",))
     put(r.get("roofline_handoff"), a.workload + "_handoff", ("export_bytes", "import_bytes"))
     for name, o in others.items():
+        if "roofline" not in o:
+            continue
         put(o["roofline"], name, ("bytes_per_launch",))
         put(o["roofline_fetch"], name + "_fetch", ("read_bytes", "write_bytes"))
+        put(o.get("roofline_select"), name + "_select", ("bytes_per_launch",))
+        put(o.get("roofline_select_mass"), name + "_mass", ("bytes_per_launch",))
+        put(o.get("roofline_handoff"), name + "_handoff", ("export_bytes", "import_bytes"))
     lo, hi = w["ctx"]
     desc = (f"B={w['B']}, L={w['L']}, Hq={w['Hq']}, Hkv={w['Hkv']}, D=128, {w['dtype']} KV, "
             f"16-token blocks, ctx {'U[%d,%d]' % (lo * 16, hi * 16) if lo != hi else lo * 16} "
@@ -1015,7 +1261,8 @@ def main():
                         "layers": w["L"], "q_heads": w["Hq"], "kv_heads": w["Hkv"],
                         "top_k": w["k"]}, **r.pop("config_extra")),
     }
-    for key in ("miss_rate", "preroll", "gate", "gate_detail", "miss_blocks_per_s",
+    for key in ("step_ms_p50", "step_ms_p99", "miss_rate", "preroll", "gate", "gate_detail",
+                "miss_blocks_per_s",
                 "miss_blocks_per_s_fetch_kernel", "fetched_blocks_per_event_step",
                 "attention_tok_per_s", "kernel_ms", "roofline",
                 "roofline_fetch", "roofline_select", "roofline_select_mass", "roofline_handoff",

@@ -19,8 +19,9 @@
 // bf16 K splits q into bf16 hi + lo parts (two MFMAs) and so does P for bf16
 // V, keeping ~16 mantissa bits.  fp8 E4M3 is widened to fp16 exactly; the
 // per-block K scale multiplies the scores.  The accumulator is kept in units
-// of a reference V scale (the first block's): each block's weights are
-// multiplied by vs / vs_ref before the fp16 rounding of P.
+// of a reference V scale (the first nonzero one): each block's weights are
+// multiplied by vs / vs_ref before the fp16 rounding of P, and a block whose
+// ratio leaves [1/64, 16] moves the reference to its own scale first.
 // Lazy rescaling: the running max m of a column is raised only when a block's
 // max exceeds it by more than kRescale (log2 units); otherwise the weights
 // 2^(s - m) may grow up to 2^kRescale, which fp16 holds exactly as well (its
@@ -48,6 +49,8 @@ constexpr uint32_t kSelLo = 0x05040100u;  // perm: low halves of (lo_src, hi_src
 constexpr uint32_t kSelHi = 0x07060302u;  // perm: high halves
 constexpr float kNeg = -1.0e30f;
 constexpr float kRescale = 8.0f;  // log2 of the largest weight between raises of the max
+constexpr float kVsHi = 16.0f;        // largest V-scale ratio folded into the fp16 weights
+constexpr float kVsLo = 1.0f / 64.0f;  // smallest
 
 __device__ inline uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
   return __builtin_amdgcn_perm(hi_src, lo_src, sel);
@@ -110,7 +113,7 @@ __device__ inline void q_operand(const float* __restrict__ qp, int grp, float qs
 
 // Running state of one wavefront's columns: online-softmax max and sum (lane
 // partial over its 4 tokens of each block), the reference V scale the
-// accumulator is kept in (0 until the first block), and O^T.  The column's
+// accumulator is kept in (0 until the first nonzero one), and O^T.  The column's
 // output is o * vs_ref / (sum over the 4 lanes of lsum).
 struct Acc {
   float m, lsum, vs_ref;
@@ -212,8 +215,25 @@ __device__ __forceinline__ void tile_block(const Ops& op, float ks, float vs,
   for (int t = 0; t < 4; ++t) p[t] = (!MASK || live) ? exp2_fast(sv[t] - a.m) : 0.0f;
   a.lsum += (p[0] + p[1]) + (p[2] + p[3]);
   if constexpr (S::F8) {  // weights in units of the reference V scale
-    if (a.vs_ref == 0.0f) a.vs_ref = vs;  // uniform: vs is the same on every lane
-    const float r = vs * __builtin_amdgcn_rcpf(a.vs_ref);
+    // r = vs / vs_ref is held in [kVsLo, kVsHi]: p * r <= 2^kRescale * kVsHi
+    // stays far below fp16's 65504, and weights near the max stay normal.  A
+    // block outside the band first moves the reference to its own scale (the
+    // accumulator rescaled in fp32), in a branch the wavefront takes together:
+    // vs and vs_ref are the same on every lane.  A zero V scale (an all-zero
+    // block) adds nothing and sets no reference; while there is none, r is
+    // inf and the first nonzero scale becomes the reference (o is still 0).
+    float r = 0.0f;
+    if (vs != 0.0f) {
+      r = vs * __builtin_amdgcn_rcpf(a.vs_ref);
+      const bool rebase = !(r >= kVsLo && r <= kVsHi);
+      if (__builtin_amdgcn_ballot_w64(rebase)) {
+        const float f = a.vs_ref * __builtin_amdgcn_rcpf(vs);
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) a.o[nb] *= f;
+        a.vs_ref = vs;
+        r = 1.0f;
+      }
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) p[t] *= r;
   }

@@ -259,13 +259,22 @@ template __global__ void k_fetch<8>(FetchArgs);
 template __global__ void k_fetch<16>(FetchArgs);
 
 __global__ void k_step_close(unsigned long long* acc, unsigned long long* host) {
-  // lanes 0 and 1 move the step's two counters into the mapped pinned words
+  // one lane moves the step's two counters into the mapped pinned words
   // (system-scope stores over the host link: no copy launch on the stream
-  // ahead of the next step) and restart them from zero
-  const int t = threadIdx.x;
-  if (blockIdx.x == 0 && t < 2) {
-    __hip_atomic_store(host + t, acc[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    acc[t] = 0ull;
+  // ahead of the next step) and restarts them from zero.  host[2] is a
+  // sequence word, odd while the counters change, so a host reader can tell
+  // a torn pair (the host enqueues steps ahead and may read at any time)
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    const unsigned long long seq = acc[2];
+    const unsigned long long fetched = acc[0], attended = acc[1];
+    __hip_atomic_store(host + 2, seq + 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __threadfence_system();
+    __hip_atomic_store(host + 0, fetched, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(host + 1, attended, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(host + 2, seq + 2ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    acc[0] = 0ull;
+    acc[1] = 0ull;
+    acc[2] = seq + 2ull;
   }
 }
 

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -106,10 +107,13 @@ struct ferry_ctx {
   uint32_t* worker_of_set = nullptr;
   unsigned long long* stats = nullptr;
   unsigned long long* sel_counts = nullptr;  // [kSelCounters * kSelStride]
-  // [2]: blocks fetched and blocks the prefix-group attention read in this
-  // step (moved to pend_host and cleared by k_step_close)
+  // [3]: blocks fetched and blocks the prefix-group attention read in this
+  // step (moved to pend_host and cleared by k_step_close), and the count of
+  // closed steps
   unsigned long long* step_acc = nullptr;
-  unsigned long long* pend_host = nullptr;   // mapped pinned [2]: the last finished step's two
+  // mapped pinned [3]: the last closed step's two counts and a sequence word
+  // (odd while k_step_close rewrites them)
+  unsigned long long* pend_host = nullptr;
   unsigned long long* pend_dev = nullptr;    // ... its device address
   double pol_min_mb = 32.0, pol_max_mb = 512.0, pol_target = 8.0;  // adaptive layer chunking
   uint32_t* done = nullptr;
@@ -631,7 +635,7 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   TRY(dalloc(&c->worker_of_set, g.n_sets));
   TRY(dalloc(&c->stats, kStatCount));
   TRY(dalloc(&c->sel_counts, (size_t)kSelCounters * kSelStride));
-  TRY(dalloc(&c->step_acc, 2));
+  TRY(dalloc(&c->step_acc, 3));
   TRY(dalloc(&c->done, 1));
   TRY(dalloc(&c->err, 1));
 #define HIPT(x)                                                                        \
@@ -649,13 +653,13 @@ int ferry_ctx_create(const ferry_config* cfg, int device, ferry_ctx** out) {
   HIPT(hipMemset(c->ring_state2, 0, (size_t)W * kStateStride * 8));
   HIPT(hipMemset(c->stats, 0, kStatCount * 8));
   HIPT(hipMemset(c->sel_counts, 0, (size_t)kSelCounters * kSelStride * 8));
-  HIPT(hipMemset(c->step_acc, 0, 16));
-  if (hipHostMalloc((void**)&c->pend_host, 16, hipHostMallocMapped) != hipSuccess) {
+  HIPT(hipMemset(c->step_acc, 0, 24));
+  if (hipHostMalloc((void**)&c->pend_host, 24, hipHostMallocMapped) != hipSuccess) {
     c->pend_host = nullptr;
     release(c);
     return fail(FERRY_ENOMEM, "hipHostMalloc of the step counter failed");
   }
-  c->pend_host[0] = c->pend_host[1] = 0;
+  c->pend_host[0] = c->pend_host[1] = c->pend_host[2] = 0;
   HIPT(hipHostGetDevicePointer((void**)&c->pend_dev, c->pend_host, 0));
   HIPT(hipMemset(c->done, 0, 4));
   HIPT(hipMemset(c->err, 0, 4));
@@ -1033,10 +1037,19 @@ int ferry_decode_step(ferry_ctx* ctx, const uint32_t* sel, const float* q, uint3
   if (chunks < 0) return fail(FERRY_EINVAL, "chunks < 0");
   const bool adaptive = chunks == 0;
   uint64_t last = 0, last_attn = 0;
-  if (adaptive) {  // from the blocks the last finished step fetched (and attended)
+  if (adaptive) {
+    // from the blocks the last closed step fetched (and attended): the host
+    // enqueues ahead of the GPU, so that step may be one or more steps back;
+    // the sequence word makes the two counts come from the same step
     const volatile unsigned long long* pend = ctx->pend_host;
-    last = pend[0];
-    last_attn = pend[1];
+    for (int tries = 0; tries < 1000; ++tries) {
+      const unsigned long long s0 = pend[2];
+      std::atomic_thread_fence(std::memory_order_acquire);
+      last = pend[0];
+      last_attn = pend[1];
+      std::atomic_thread_fence(std::memory_order_acquire);
+      if (!(s0 & 1ull) && pend[2] == s0) break;
+    }
     if (int rc = ferry_decode_chunks(ctx, last, &chunks)) return rc;
   }
   chunks = std::min(chunks, L);

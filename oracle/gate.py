@@ -55,6 +55,13 @@ class OwnerReplay:
         self.last_sel = None
         self.last_misses = None
 
+    def reset(self, owners):
+        """Owners whose sets the executor reset before the next step (a new
+        request took the lane): the replayed ones start empty too."""
+        for o in owners:
+            if int(o) < self.n_owners:
+                self.ox.reset_owner(int(o))
+
     def step(self, sel, bufs):
         """sel: the step's [B, L, Hkv, k] block ids (numpy, uint32 view); bufs:
         the executor's step buffers after the step ran (synchronised)."""

@@ -801,6 +801,8 @@ void ora_exec_members_get(const ora_exec* e, uint32_t* members) {
   memcpy(members, e->members, (size_t)ora_n_owners(&e->g) * 4);
 }
 
+const ora_geom* ora_exec_geom(const ora_exec* e) { return &e->g; }
+
 void ora_exec_destroy(ora_exec* e) {
   if (!e) return;
   const int ns = ora_n_sets(&e->g);
@@ -1453,8 +1455,23 @@ void ora_host_fill(const ora_geom* g, uint8_t* host, float* host_scales) {
  * tools/capture_miss_trace.py:146-159).  Rows name their blocks by host-tier
  * index: hidx [B][L][Hkv][k], ORA_NONE64 for an empty position (skipped); a
  * block named twice in a row is attended twice. */
-int ora_attention_hidx_f64(const ora_geom* g, const uint64_t* hidx, const float* q,
-                           double* out) {
+static float load_elem_f32(int dtype, const uint8_t* p, size_t i);
+
+/* Element e of host block hi, decoded: from the caller's tier image `host`
+ * when given, else from the generator (the two agree where the image is
+ * ora_host_fill's). */
+static double tier_elem(const ora_geom* g, const uint8_t* host, uint64_t hi, uint32_t e) {
+  if (!host) return ora_decode(g->dtype, ora_host_elem(g, hi, e));
+  return (double)load_elem_f32(g->dtype, host + hi * ora_block_bytes(g), e);
+}
+
+static double tier_scale(const ora_geom* g, const float* host_scales, uint64_t hi, int kv) {
+  if (g->dtype != ORA_FP8) return 1.0;
+  return host_scales ? (double)host_scales[2 * hi + (uint64_t)kv] : (double)ora_host_scale(g, hi, kv);
+}
+
+static int attention_rows_f64(const ora_geom* g, const uint64_t* hidx, const uint8_t* host,
+                              const float* host_scales, const float* q, double* out) {
   const int L = g->n_layers, Hq = g->q_heads, Hk = g->kv_heads, D = g->head_dim;
   const int T = g->block_tokens, k = g->k, grp = Hq / Hk;
   const int ntok_max = k * T;
@@ -1477,13 +1494,13 @@ int ora_attention_hidx_f64(const ora_geom* g, const uint64_t* hidx, const float*
           if (bl[jj] == ORA_NONE64) continue;
           const int j = nv++;
           const uint64_t hi = bl[jj];
-          const double sk = ora_host_scale(g, hi, 0), sv = ora_host_scale(g, hi, 1);
+          const double sk = tier_scale(g, host_scales, hi, 0);
+          const double sv = tier_scale(g, host_scales, hi, 1);
           for (int t = 0; t < T; ++t)
             for (int d = 0; d < D; ++d) {
               const size_t row = (size_t)(j * T + t) * D + d;
-              K[row] = ora_decode(g->dtype, ora_host_elem(g, hi, (uint32_t)(t * D + d))) * sk;
-              V[row] = ora_decode(g->dtype,
-                                  ora_host_elem(g, hi, (uint32_t)((T + t) * D + d))) * sv;
+              K[row] = tier_elem(g, host, hi, (uint32_t)(t * D + d)) * sk;
+              V[row] = tier_elem(g, host, hi, (uint32_t)((T + t) * D + d)) * sv;
             }
         }
         const int ntok = nv * T;
@@ -1519,6 +1536,20 @@ int ora_attention_hidx_f64(const ora_geom* g, const uint64_t* hidx, const float*
   free(V);
   free(K);
   return 0;
+}
+
+int ora_attention_hidx_f64(const ora_geom* g, const uint64_t* hidx, const float* q,
+                           double* out) {
+  return attention_rows_f64(g, hidx, NULL, NULL, q, out);
+}
+
+/* The same over a caller's host tier image (bytes [host_blocks][bb], fp8
+ * scales [host_blocks][2]) instead of the generated content: the reference
+ * for a tier registered with ferry_hosttier_register. */
+int ora_attention_tier_f64(const ora_geom* g, const uint64_t* hidx, const uint8_t* host,
+                           const float* host_scales, const float* q, double* out) {
+  if (!host || (g->dtype == ORA_FP8 && !host_scales)) return -1;
+  return attention_rows_f64(g, hidx, host, host_scales, q, out);
 }
 
 /* The same over block ids: row (r, l, h) selects blocks of its owner's set
@@ -1566,78 +1597,3 @@ static float load_elem_f32(int dtype, const uint8_t* p, size_t i) {
   }
 }
 
-int ora_attention_pool_f32(const ora_geom* g, const uint32_t* slots,
-                           const uint8_t* pool, const float* pool_scales,
-                           const float* q, float* out) {
-  const int L = g->n_layers, Hq = g->q_heads, Hk = g->kv_heads, D = g->head_dim;
-  const int T = g->block_tokens, k = g->k, grp = Hq / Hk;
-  const uint64_t bb = ora_block_bytes(g);
-  const float isd = 1.0f / sqrtf((float)D);
-  float* acc = (float*)malloc((size_t)D * sizeof(float));
-  float* sc = (float*)malloc((size_t)T * sizeof(float));
-  for (int r = 0; r < g->n_req; ++r)
-    for (int l = 0; l < L; ++l)
-      for (int h = 0; h < Hk; ++h) {
-        const uint32_t* sl = slots + ((size_t)(r * L + l) * Hk + h) * k;
-        for (int gq = 0; gq < grp; ++gq) {
-          const int hq = h * grp + gq;
-          const float* qv = q + ((size_t)(r * L + l) * Hq + hq) * D;
-          float m = -INFINITY, den = 0.0f;
-          for (int d = 0; d < D; ++d) acc[d] = 0.0f;
-          for (int j = 0; j < k; ++j) {
-            if (sl[j] == ORA_NONE) continue; /* empty position */
-            const uint8_t* blk = pool + (size_t)sl[j] * bb;
-            const float sk = pool_scales ? pool_scales[2 * (size_t)sl[j]] : 1.0f;
-            const float sv = pool_scales ? pool_scales[2 * (size_t)sl[j] + 1] : 1.0f;
-            float bm = -INFINITY;
-            for (int t = 0; t < T; ++t) {
-              float a = 0.0f;
-              for (int d = 0; d < D; ++d)
-                a += qv[d] * load_elem_f32(g->dtype, blk, (size_t)t * D + d);
-              sc[t] = a * sk * isd;
-              if (sc[t] > bm) bm = sc[t];
-            }
-            const float mn = bm > m ? bm : m;
-            const float alpha = expf(m - mn);
-            den *= alpha;
-            for (int d = 0; d < D; ++d) acc[d] *= alpha;
-            for (int t = 0; t < T; ++t) {
-              const float p = expf(sc[t] - mn);
-              den += p;
-              const float pv = p * sv;
-              for (int d = 0; d < D; ++d)
-                acc[d] += pv * load_elem_f32(g->dtype, blk, (size_t)(T + t) * D + d);
-            }
-            m = mn;
-          }
-          float* ov = out + ((size_t)(r * L + l) * Hq + hq) * D;
-          for (int d = 0; d < D; ++d) ov[d] = den > 0.0f ? acc[d] / den : 0.0f;
-        }
-      }
-  free(acc);
-  free(sc);
-  return 0;
-}
-
-int ora_cpu_step(ora_exec* e, const uint32_t* sel, const uint8_t* host,
-                 const float* host_scales, uint8_t* pool, float* pool_scales,
-                 const float* q, float* out, uint32_t* slots_scratch,
-                 uint32_t* miss_count, ora_miss* misses, uint64_t* counts) {
-  const ora_geom* g = &e->g;
-  int rc = ora_exec_step(e, sel, slots_scratch, miss_count, misses, counts, NULL);
-  if (rc) return rc;
-  const uint64_t bb = ora_block_bytes(g);
-  const int ns = ora_n_sets(g), maxsel = ora_max_sel_per_set(g);
-  for (int s = 0; s < ns; ++s)
-    for (uint32_t i = 0; i < miss_count[s]; ++i) {
-      const ora_miss* m = misses + (size_t)s * maxsel + i;
-      const uint64_t hi = ora_host_index(g, m->set, m->block);
-      const uint64_t dst = (uint64_t)m->set * (uint64_t)g->cap + m->slot;
-      memcpy(pool + dst * bb, host + hi * bb, bb);
-      if (pool_scales && host_scales) {
-        pool_scales[2 * dst] = host_scales[2 * hi];
-        pool_scales[2 * dst + 1] = host_scales[2 * hi + 1];
-      }
-    }
-  return ora_attention_pool_f32(g, slots_scratch, pool, pool_scales, q, out);
-}

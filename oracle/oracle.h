@@ -190,6 +190,7 @@ uint64_t ora_host_index(const ora_geom* g, uint32_t set, uint32_t block);
 typedef struct ora_exec ora_exec;
 ora_exec* ora_exec_create(const ora_geom* g);
 void ora_exec_destroy(ora_exec* e);
+const ora_geom* ora_exec_geom(const ora_exec* e);
 /* One decode step of bookkeeping.  sel: [B][L][Hkv][k] set block ids.
  * slots_out: [B][L][Hkv][k] global slot ids (set * cap + local).
  * miss_count: [n_sets]; misses: [n_sets][max_sel_per_set].  counts[0..2] =
@@ -315,9 +316,14 @@ int ora_attention_f64(const ora_geom* g, const uint32_t* sel, const float* q,
  * one row is attended twice. */
 int ora_attention_hidx_f64(const ora_geom* g, const uint64_t* hidx, const float* q,
                            double* out);
+/* The same over a caller's host tier image instead of the generated content:
+ * host [host_blocks][bb] bytes, host_scales [host_blocks][2] (fp8 only; K
+ * scale, V scale).  -1 if an image the dtype needs is missing. */
+int ora_attention_tier_f64(const ora_geom* g, const uint64_t* hidx, const uint8_t* host,
+                           const float* host_scales, const float* q, double* out);
 /* Same attention, but K/V read from a host pool image laid out like the HBM
  * pool (slot-major, bb bytes per slot, scales[slot][2]) through the slot
- * table; fp32 accumulation.  Used by the CPU baseline. */
+ * table; fp32 accumulation.  The CPU path timed beside the GPU (cpu_step.c). */
 int ora_attention_pool_f32(const ora_geom* g, const uint32_t* slots,
                            const uint8_t* pool, const float* pool_scales,
                            const float* q, float* out);

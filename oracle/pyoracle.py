@@ -139,6 +139,8 @@ _sig("ora_host_block", None, C.POINTER(Geom), C.c_uint64, C.c_void_p, C.c_void_p
 _sig("ora_host_fill", None, C.POINTER(Geom), C.c_void_p, C.c_void_p)
 _sig("ora_attention_f64", C.c_int, C.POINTER(Geom), _u32p, _f32p, _f64p)
 _sig("ora_attention_hidx_f64", C.c_int, C.POINTER(Geom), _u64p, _f32p, _f64p)
+_sig("ora_attention_tier_f64", C.c_int, C.POINTER(Geom), _u64p, C.c_void_p, C.c_void_p, _f32p,
+     _f64p)
 _sig("ora_attention_pool_f32", C.c_int, C.POINTER(Geom), _u32p, C.c_void_p, C.c_void_p,
      _f32p, _f32p)
 _sig("ora_summary", None, C.POINTER(Geom), C.c_uint64, _f32p, _f32p)
@@ -379,6 +381,21 @@ def attention_hidx_f64(g: Geom, hidx, q):
                                     np.ascontiguousarray(q, np.float32).reshape(-1), out)
     if rc:
         raise RuntimeError("ora_attention_hidx_f64")
+    return out.reshape(q.shape)
+
+
+def attention_tier_f64(g: Geom, hidx, host, host_scales, q):
+    """attention_hidx_f64 over a caller's host tier image (uint8 bytes
+    [host_blocks * bb], fp8 scales float32 [host_blocks * 2]) instead of the
+    generated content."""
+    host = np.ascontiguousarray(host, np.uint8)
+    sc = None if host_scales is None else np.ascontiguousarray(host_scales, np.float32)
+    out = np.zeros(q.size, np.float64)
+    rc = lib.ora_attention_tier_f64(C.byref(g), np.ascontiguousarray(hidx, np.uint64).reshape(-1),
+                                    host.ctypes.data, None if sc is None else sc.ctypes.data,
+                                    np.ascontiguousarray(q, np.float32).reshape(-1), out)
+    if rc:
+        raise RuntimeError("ora_attention_tier_f64")
     return out.reshape(q.shape)
 
 

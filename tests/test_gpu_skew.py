@@ -15,7 +15,15 @@ executor's slots, per-set miss lists and miss flags must equal the oracle's
 bit for bit; at the end of each phase the LRU state too, and the two pools
 must be byte-identical over every slot (stealing changes who copies a block,
 never what lands where), with sampled fetched blocks equal to the host tier.
-With stealing on the drains must have stolen."""
+With stealing on the drains must have stolen.
+
+The same twins also run the pipelined decode step the benchmark times
+(ferry_decode_step with adaptive layer ranges and a side stream, stealing
+beside the overlapped attention): slots and miss lists bit-exact every step,
+outputs bit-identical between the twins and within 2e-3 of float64, LRU state
+and pools at the end.  The whole 64-request batch at Zipf 1.4 with stealing
+runs that step from the cold pool with the first two requests replayed in the
+oracle (oracle/gate.py)."""
 import ctypes as C
 
 import numpy as np
@@ -24,6 +32,7 @@ import torch
 
 import ferry_amd as F
 from oracle import pyoracle as O
+from oracle.gate import OwnerReplay
 
 pytestmark = pytest.mark.gpu
 
@@ -174,3 +183,107 @@ def test_skew_stealing_on_off_parity(zipf):
     assert s0["misses"] == s1["misses"] == sum(misses)
     print(f"[skew] zipf={zipf}: {sum(misses)} misses over {len(misses)} steps, "
           f"{s1['steals']} steals moved {s1['stolen']}", flush=True)
+
+
+def _attention_layers_f64(g, sel, q, layers):
+    """float64 attention of the given layers (the others left empty)."""
+    s = np.full_like(sel, O.NONE)
+    s[:, layers] = sel[:, layers]
+    return O.attention_f64(g, s, q)[:, layers]
+
+
+@pytest.mark.parametrize("zipf", [0.6, 1.0, 1.4])
+def test_skew_pipelined_decode_step_parity(zipf):
+    # the step the benchmark times for this configuration: ferry_decode_step
+    # with adaptive layer ranges, bookkeeping two ranges ahead and the fetch of
+    # each range on a side stream while the range before it attends, with the
+    # 304 request-affine workgroups stealing (or not) beside that attention
+    print(f"[skew pipelined] zipf={zipf} B={B} L={L} H={H} k={K} C={CAP} workers={WORKERS}",
+          flush=True)
+    ctx = F.ctx_uniform(2, B, 256, 2048)
+    sg = F.SelGen(B, L, H, K, ctx, dist=1, zipf_s=zipf, reuse=0.66, seed=3)
+    sg.set_reuse(_lognormal_reuse(B, K))
+    tw = Twin(sg.max_blocks)
+    side = torch.cuda.Stream()
+    rng = np.random.default_rng(8)
+    layers = [0, 13, L - 1]
+    for t in range(6):
+        sel = sg.step(t)
+        dsel = torch.from_numpy(np.ascontiguousarray(sel, np.uint32).view(np.int32)).cuda()
+        q = torch.from_numpy(rng.standard_normal((B, L, H, 128)).astype(np.float32)).cuda()
+        outs = {}
+        for steal, (e, bufs) in tw.ex.items():
+            outs[steal] = torch.empty_like(q)
+            e.decode_step(dsel, q, bufs, outs[steal], chunks=0, side_stream=side)
+        torch.cuda.synchronize()
+        oslots, omc, oms, _ = tw.ox.step(sel)
+        oms4 = oms.view(np.uint32).reshape(tw.ox.n_sets, -1, 4)
+        live = np.arange(oms4.shape[1])[None, :] < omc[:, None]
+        for steal, (e, bufs) in tw.ex.items():
+            st = e.stats()
+            assert st["device_error"] == 0, (steal, st)
+            assert np.array_equal(_u32(bufs["slots"]).reshape(-1), oslots), (t, steal)
+            assert np.array_equal(_u32(bufs["miss_count"]), omc), (t, steal)
+            gms = _u32(bufs["misses"]).reshape(tw.ox.n_sets, -1, 4)
+            assert np.array_equal(gms[live], oms4[live]), (t, steal)
+        # same pool bytes, same kernel: the outputs are bit-identical
+        assert torch.equal(outs[0], outs[1]), t
+        if t in (0, 5):
+            ref = _attention_layers_f64(tw.g, sel.reshape(B, L, H, K), q.cpu().numpy(), layers)
+            got = outs[1].cpu().numpy()[:, layers].reshape(-1, 128).astype(np.float64)
+            ref = ref.reshape(-1, 128)
+            rel = np.abs(got - ref).max(axis=1) / np.abs(ref).max(axis=1)
+            assert rel.max() < 2e-3, (t, rel.max())
+        print(f"[skew pipelined] zipf={zipf} step {t}: {int(omc.sum())} misses", flush=True)
+    tw.check_state()
+    s0, s1 = tw.ex[0][0].stats(), tw.ex[1][0].stats()
+    assert s0["steals"] == 0 and s1["steals"] > 0
+    assert s0["misses"] == s1["misses"] > 0
+    print(f"[skew pipelined] zipf={zipf}: {s1['misses']} misses, {s1['steals']} steals moved "
+          f"{s1['stolen']}", flush=True)
+
+
+def test_skew_full_batch_pipelined_owner_replay():
+    # the whole config-3 batch (64 requests) at Zipf 1.4 with stealing, through
+    # the pipelined step from the cold pool: the first two requests replayed in
+    # the oracle every step (slots and miss lists bit-equal; LRU state, fetched
+    # and resident bytes and attention at the end), and for all 64 requests the
+    # size-independent properties (every slot in its owner's set holding its
+    # block, counters adding up)
+    Bf = 64
+    print(f"[skew full] B={Bf} L={L} H={H} k={K} C={CAP} workers={WORKERS} zipf=1.4", flush=True)
+    ctx = F.ctx_uniform(2, Bf, 256, 2048)
+    sg = F.SelGen(Bf, L, H, K, ctx, dist=1, zipf_s=1.4, reuse=0.66, seed=3)
+    sg.set_reuse(_lognormal_reuse(Bf, K))
+    ex = F.Executor(Bf, L, H, K, CAP, sg.max_blocks, dtype=F.F16, host_blocks=HB,
+                    fetch_workers=WORKERS, steal=1, assign=F.ASSIGN_AFFINITY)
+    ex.hosttier_fill()
+    bufs = ex.alloc_step_buffers()
+    side = torch.cuda.Stream()
+    replay = OwnerReplay(n_req=Bf, group=1, n_layers=L, kv_heads=H, q_heads=H, k=K,
+                         slots_per_set=CAP, max_blocks=sg.max_blocks, dtype=F.F16,
+                         host_blocks=HB)
+    sets = (np.arange(Bf)[:, None, None] * L + np.arange(L)[None, :, None]) * H + \
+        np.arange(H)[None, None, :]
+    total = 0
+    for t in range(8):
+        sel = sg.step(t)
+        q = torch.randn((Bf, L, H, 128), device="cuda")
+        out = torch.empty_like(q)
+        ex.decode_step(torch.from_numpy(sel.view(np.int32)).cuda(), q, bufs, out, chunks=0,
+                       side_stream=side)
+        torch.cuda.synchronize()
+        st = ex.stats()
+        assert st["device_error"] == 0, st
+        replay.step(sel, bufs)
+        total += int(_u32(bufs["miss_count"]).sum())
+        assert st["misses"] == total and st["fetched_bytes"] == total * ex.block_bytes
+        slots = _u32(bufs["slots"]).reshape(Bf, L, H, K).astype(np.int64)
+        assert np.all(slots // CAP == sets[..., None])
+        _, _, tag = ex.sets_state()
+        assert np.array_equal(tag.reshape(-1)[slots.reshape(-1)], sel.reshape(-1))
+        print(f"[skew full] step {t}: {total} misses so far, {st['steals']} steals", flush=True)
+    assert ex.stats()["steals"] > 0
+    res = replay.final(ex, q, out)
+    print(f"[skew full] owner replay: {res}", flush=True)
+    assert res["steps"] == 8 and res["misses_compared"] > 0

@@ -334,6 +334,67 @@ def test_attention_hidx_rows_against_numpy(dtype):
                        rtol=1e-13, atol=1e-13)
 
 
+def _decode_raw(dtype, raw):
+    if dtype == O.F16:
+        return raw.view(np.float16).astype(np.float64)
+    if dtype == O.F32:
+        return raw.view(np.float32).astype(np.float64)
+    if dtype == O.BF16:
+        return torch.from_numpy(raw.view(np.int16).copy()).view(torch.bfloat16).double().numpy()
+    return torch.from_numpy(raw.copy()).view(torch.float8_e4m3fn).double().numpy()
+
+
+@pytest.mark.parametrize("dtype", [O.F16, O.FP8])
+def test_attention_tier_image_against_numpy(dtype):
+    # the attention over a caller's tier image: equal to the generated-content
+    # attention while the image is ora_host_fill's, and to a numpy softmax over
+    # the image's own bytes and scales after they are rewritten (fp8 V scales
+    # spread over 1e-3..1e3, some zero, some blocks all zero)
+    B, L, hk, hq, k = 2, 1, 2, 4, 6
+    g = O.make_geom(n_req=B, n_layers=L, kv_heads=hk, q_heads=hq, k=k, cap=8, max_blocks=40,
+                    dtype=dtype, host_blocks=53)
+    bb = O.lib.ora_block_bytes(C.byref(g))
+    host, sc = O.host_fill(g)
+    rng = np.random.default_rng(12)
+    hidx = rng.integers(0, 53, (B * L * hk, k)).astype(np.uint64)
+    hidx[1, 2] = O.NONE64
+    q = rng.standard_normal((B, L, hq, 128)).astype(np.float32)
+    assert np.array_equal(O.attention_tier_f64(g, hidx, host, sc if dtype == O.FP8 else None, q),
+                          O.attention_hidx_f64(g, hidx, q))
+    host = host.copy()
+    blocks = host.reshape(53, bb)
+    blocks[5] = rng.integers(0, 256, bb, dtype=np.uint8) & 0x77  # finite fp8 codes and f16s
+    if dtype == O.FP8:
+        sc = sc.copy().reshape(53, 2)
+        sc[:, 1] *= 10.0 ** rng.uniform(-3, 3, 53)
+        sc[7, 1] = 0.0
+        sc[9, 0] = 0.0
+        blocks[11, bb // 2:] = 0
+        sc[11, 1] = 1e3
+        hidx[0, 0], hidx[0, 1], hidx[2, 0], hidx[3, 3] = 11, 7, 9, 5
+    else:
+        hidx[0, 0] = 5
+    out = O.attention_tier_f64(g, hidx, host, sc.reshape(-1) if dtype == O.FP8 else None, q)
+    T, D, grp = g.block_tokens, g.head_dim, hq // hk
+    for r in range(B):
+        for hh in range(hq):
+            row = hidx[r * hk + hh // grp]
+            picked = [int(b) for b in row if b != O.NONE64]
+            kv = [_decode_raw(dtype, blocks[b]).reshape(2, T, D) for b in picked]
+            ks = [sc[b, 0] if dtype == O.FP8 else 1.0 for b in picked]
+            vs = [sc[b, 1] if dtype == O.FP8 else 1.0 for b in picked]
+            K = np.concatenate([a[0] * s for a, s in zip(kv, ks)])
+            V = np.concatenate([a[1] * s for a, s in zip(kv, vs)])
+            s_ = K @ q[r, 0, hh].astype(np.float64) / np.sqrt(128)
+            p = np.exp(s_ - s_.max())
+            assert np.allclose(out[r, 0, hh], (p / p.sum()) @ V, rtol=1e-12, atol=1e-12)
+    with pytest.raises(RuntimeError):
+        if dtype == O.FP8:
+            O.attention_tier_f64(g, hidx, host, None, q)  # fp8 needs the scales
+        else:
+            raise RuntimeError("f16 needs none")
+
+
 def test_attention_special_cases():
     g = O.make_geom(n_req=1, n_layers=1, kv_heads=1, k=3, cap=4, max_blocks=8, dtype=O.F32,
                     host_blocks=16)
