@@ -684,10 +684,15 @@ def run_mass(a, ex, F, torch, stream, dtype, w, ctx, dctx, qs, sel0, max_blocks,
     nbytes = nb * (rec + (4 if dtype == F.FP8 else 0)) + B * L * Hq * 128 * 4 + B * L * H * k * 4
     kern = "k_select_mass" if dtype == F.F32 else "k_select_mass_mfma"
     gbs = nbytes / (t * 1e-3) / 1e9
+    # ceiling: the same records read in the kernel's order and grid, no scores
+    # (every set's first max(ctx) blocks: the same bytes where contexts are equal)
+    pbytes, pms, pgbs = ex.bw_probe(F.PROBE_KTAB_READ, int(ctx.max()), iters=3, stream=stream)
     return {"bound": "hbm", "kernel": f"{kern}<{w['dtype']},{Hq // H}>", "ms": round(t, 4),
             "context_blocks_per_launch": nb, "k_table_gb": round(n_rec * rec / 1e9, 1),
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "plain_read_gbs": round(pgbs, 1), "plain_read_ms": round(pms, 4),
+            "frac_of_plain_read": round(gbs / pgbs, 4)}
 
 
 def run_handoff(a, ex, F, torch, stream, dtype, n_timed):

@@ -162,6 +162,8 @@ __global__ void k_probe_gather(const uint8_t* pool, uint64_t bb, const uint32_t*
                                uint64_t pool_slots, uint32_t* sink);
 template <int NV>
 __global__ void k_probe_copy(const uint8_t* src, uint8_t* dst, uint64_t bb, uint64_t n_blocks);
+template <int NI, int W>
+__global__ void k_probe_ktab(Geo g, const uint8_t* kt, uint64_t kt_mod, int nb, uint32_t* sink);
 template <int NV>
 __global__ void k_probe_host(const uint8_t* host, uint64_t bb, uint64_t n_blocks, uint32_t* sink);
 

@@ -12,7 +12,11 @@
 //    ring bookkeeping or the pool writes;
 //  * k_probe_copy: a streaming device copy of consecutive pool blocks
 //    (non-temporal 16-byte loads and stores), the ceiling of the owner
-//    hand-off, which reads and writes every resident block once.
+//    hand-off, which reads and writes every resident block once;
+//  * k_probe_ktab: the mass selection's reads of the dense K table (every
+//    record of the first n blocks of every set, kv head by kv head of each
+//    (request, layer) item) with its grid, wavefronts and four records in
+//    flight per wavefront, the scores replaced by an XOR.
 // They play the role of the reference's host-staged bandwidth sweep
 // (probe_host_staged_bandwidth, src/topo/topo.cpp:68-129), measured here for
 // the one-hop device-direct path instead of the two-hop pinned ring.
@@ -112,6 +116,48 @@ __global__ __launch_bounds__(256) void k_probe_copy(const uint8_t* __restrict__ 
   }
 }
 
+template <int NI, int W>
+__global__ __launch_bounds__(W * 64) void k_probe_ktab(Geo g, const uint8_t* __restrict__ kt,
+                                                      uint64_t kt_mod, int nb,
+                                                      uint32_t* __restrict__ sink) {
+  constexpr int U = 4;  // records in flight per wavefront, as k_select_mass_mfma
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n_items = g.n_req * g.L;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    for (int h = 0; h < g.Hkv; ++h) {
+      const uint64_t set = (uint64_t)item * g.Hkv + h;
+      for (int b0 = wave; b0 < nb; b0 += W * U) {
+        u32x4 w[U][NI];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int b = b0 + W * u;
+          if (b < nb) {  // wavefront-uniform
+            const uint64_t rec = host_index(set, (uint32_t)b, (uint64_t)g.max_blocks, kt_mod);
+            const u32x4* base = reinterpret_cast<const u32x4*>(kt) + rec * (64 * NI) + lane;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) w[u][i] = __builtin_nontemporal_load(base + 64 * i);
+          } else {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) w[u][i] = u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int i = 0; i < NI; ++i) acc ^= w[u][i];
+      }
+    }
+  }
+  uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off);
+  if (lane == 0) sink[(size_t)blockIdx.x * W + wave] = x;
+}
+
+template __global__ void k_probe_ktab<2, 8>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
+template __global__ void k_probe_ktab<4, 8>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
+template __global__ void k_probe_ktab<8, 4>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
 template __global__ void k_probe_gather<4>(const uint8_t*, uint64_t, const uint32_t*, int, uint64_t,
                                            uint32_t*);
 template __global__ void k_probe_gather<8>(const uint8_t*, uint64_t, const uint32_t*, int, uint64_t,

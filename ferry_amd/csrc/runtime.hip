@@ -1555,7 +1555,7 @@ int ferry_owner_import_member(ferry_ctx* ctx, uint32_t lane, const void* image, 
 int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, int iters,
                    uint64_t* bytes, float* ms, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
-  if (kind < FERRY_PROBE_HBM_GATHER || kind > FERRY_PROBE_HBM_COPY) return fail(FERRY_EINVAL, "bad kind");
+  if (kind < FERRY_PROBE_HBM_GATHER || kind > FERRY_PROBE_KTAB_READ) return fail(FERRY_EINVAL, "bad kind");
   if (n < 1 || iters < 1) return fail(FERRY_EINVAL, "n and iters must be positive");
   if (kind == FERRY_PROBE_HBM_GATHER && (check_buf(slots, "slots") || n > 0x7FFFFFFFull))
     return fail(FERRY_EINVAL, "gather needs a device slot table of at most 2^31 rows");
@@ -1563,11 +1563,19 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
     return fail(FERRY_EINVAL, "more blocks than the host tier holds");
   if (kind == FERRY_PROBE_HBM_COPY && n > ctx->g.pool_slots)
     return fail(FERRY_EINVAL, "more blocks than the pool holds");
+  if (kind == FERRY_PROBE_KTAB_READ && (!ctx->ktab || n > (uint64_t)ctx->g.max_blocks))
+    return fail(FERRY_EINVAL, "the K-table probe needs ferry_ktiles_build and n <= max_blocks");
   const Geo& g = ctx->g;
   HIPC(hipSetDevice(ctx->device));
   hipStream_t s = (hipStream_t)stream;
   const int host_waves = g.workers * 4;
-  const size_t words = kind == FERRY_PROBE_HBM_GATHER ? (size_t)n : (size_t)host_waves;
+  // the K-table probe: the mass selection's grid (at most kMassWgs workgroups
+  // of 8 wavefronts, 4 for fp32 records)
+  const int kt_w = g.dtype == FERRY_F32 ? 4 : 8;
+  const uint64_t kt_grid = std::min<uint64_t>((uint64_t)g.n_req * g.L, kMassWgs);
+  const size_t words = kind == FERRY_PROBE_HBM_GATHER ? (size_t)n
+                       : kind == FERRY_PROBE_KTAB_READ ? (size_t)(kt_grid * kt_w)
+                                                       : (size_t)host_waves;
   if (ctx->probe_sink_words < words) {
     if (ctx->probe_sink) HIPC(hipFree(ctx->probe_sink));
     ctx->probe_sink = nullptr;
@@ -1578,7 +1586,9 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
   // bytes per launch: read, plus written for the device copy
   const uint64_t moved = kind == FERRY_PROBE_HBM_GATHER ? n * (uint64_t)g.k * g.bb
                          : kind == FERRY_PROBE_HBM_COPY ? 2 * n * g.bb
-                                                        : n * g.bb;
+                         : kind == FERRY_PROBE_KTAB_READ
+                             ? (uint64_t)g.n_req * g.L * g.Hkv * n * (g.bb / 2)
+                             : n * g.bb;
   const uint64_t dst_bytes = n * g.bb;
   if ((kind == FERRY_PROBE_HOST_DMA || kind == FERRY_PROBE_HBM_COPY) && ctx->probe_dst_bytes < dst_bytes) {
     if (ctx->probe_dst) HIPC(hipFree(ctx->probe_dst));
@@ -1608,6 +1618,20 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
         hipLaunchKernelGGL(k_probe_host<8>, grid, block, 0, s, ctx->host_dev, g.bb, n, ctx->probe_sink);
       else
         hipLaunchKernelGGL(k_probe_host<16>, grid, block, 0, s, ctx->host_dev, g.bb, n, ctx->probe_sink);
+      return hipGetLastError();
+    }
+    if (kind == FERRY_PROBE_KTAB_READ) {
+      const dim3 grid((unsigned)kt_grid);
+      const int nb = (int)n;
+      if (g.dtype == FERRY_F32)
+        hipLaunchKernelGGL((k_probe_ktab<8, 4>), grid, dim3(256), 0, s, g, ctx->ktab,
+                           ctx->kt_records, nb, ctx->probe_sink);
+      else if (g.dtype == FERRY_FP8_E4M3)
+        hipLaunchKernelGGL((k_probe_ktab<2, 8>), grid, dim3(512), 0, s, g, ctx->ktab,
+                           ctx->kt_records, nb, ctx->probe_sink);
+      else
+        hipLaunchKernelGGL((k_probe_ktab<4, 8>), grid, dim3(512), 0, s, g, ctx->ktab,
+                           ctx->kt_records, nb, ctx->probe_sink);
       return hipGetLastError();
     }
     if (kind == FERRY_PROBE_HBM_COPY) {

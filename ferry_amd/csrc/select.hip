@@ -732,7 +732,6 @@ __global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
     int* __restrict__ err) {
   static_assert(G >= 1 && G <= 16, "the score tile holds up to 16 query heads");
   static_assert(DT == FERRY_F16 || DT == FERRY_BF16 || DT == FERRY_FP8_E4M3, "16/8-bit K");
-  static_assert(W >= 4, "four wavefronts build the four k-steps of the Q^T operands");
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -750,11 +749,6 @@ __global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
   __shared__ uint32_t wtot[2 * W];
   __shared__ uint32_t sh[2];
   __shared__ float red_m[W][G], red_s[W][G], lse_m[G], lse_zi[G];
-  // the kv head's Q^T operands (term t, k-step ks, lane), shared by the
-  // wavefronts: in registers they would hold 4 * NQ * 4 VGPRs per lane, and
-  // with them the kernel needs more than 128, which leaves one workgroup per
-  // CU whose barrier phases then idle the CU's stream
-  __shared__ u32x4 qsh[NQ * 4 * 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, grp = lane >> 4;
   const bool head_lane = grp == 0 && n < G;
@@ -782,17 +776,15 @@ __global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
     }
     for (int h = 0; h < g.Hkv; ++h) {
       const uint64_t set = (uint64_t)rl * g.Hkv + h;
-      // ---- Q^T operand: k-step ks, this lane's 8 dims, head n (0 for pad
-      // heads); wavefront ks < 4 builds k-step ks into LDS (the last kv head's
-      // readers passed the score pass's barriers)
-      if (wave < 4) {
-        const int ks = wave;
+      // ---- Q^T operand: k-step ks, this lane's 8 dims, head n (0 for pad heads)
+      uint32_t qb[NQ][4][4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
         const int d0 = EPW * (4 * (ks / SUB) + grp) + 8 * (ks % SUB);
         float x[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           x[e] = n < G ? q[((size_t)rl * g.Hq + (size_t)(h * G + n)) * D + d0 + e] * qmul : 0.0f;
-        uint32_t qb[NQ][4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
           float a = x[e], b = x[e + 1];
@@ -800,23 +792,19 @@ __global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
           for (int t = 0; t < NQ; ++t) {
             if constexpr (BF) {
               const uint16_t ah = bf16_rne(a), bh = bf16_rne(b);
-              qb[t][e / 2] = (uint32_t)ah | ((uint32_t)bh << 16);
+              qb[t][ks][e / 2] = (uint32_t)ah | ((uint32_t)bh << 16);
               a -= __builtin_bit_cast(float, (uint32_t)ah << 16);
               b -= __builtin_bit_cast(float, (uint32_t)bh << 16);
             } else {
               const _Float16 ah = (_Float16)a, bh = (_Float16)b;
-              qb[t][e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, ah) |
-                             ((uint32_t)__builtin_bit_cast(uint16_t, bh) << 16);
+              qb[t][ks][e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, ah) |
+                                 ((uint32_t)__builtin_bit_cast(uint16_t, bh) << 16);
               a -= (float)ah;
               b -= (float)bh;
             }
           }
         }
-#pragma unroll
-        for (int t = 0; t < NQ; ++t)
-          qsh[(t * 4 + ks) * 64 + lane] = u32x4{qb[t][0], qb[t][1], qb[t][2], qb[t][3]};
       }
-      __syncthreads();
       float run_m = -INFINITY, run_s = 0.0f;
       for (int b0 = wave; b0 < nb; b0 += W * U) {
         u32x4 kw[U][NKW];
@@ -837,9 +825,6 @@ __global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
         for (int u = 0; u < U; ++u) {
           const int b = b0 + W * u;
           if (b >= nb) break;  // wavefront-uniform
-          // the Q^T reads below stay in the loop (read per block, not held in
-          // registers across it): the compiler may not hoist them past this
-          asm volatile("" ::: "memory");
           f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) {
@@ -854,7 +839,7 @@ __global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
             }
 #pragma unroll
             for (int t = 0; t < NQ; ++t) {
-              const u32x4 bq = qsh[(t * 4 + ks) * 64 + lane];
+              const u32x4 bq = {qb[t][ks][0], qb[t][ks][1], qb[t][ks][2], qb[t][ks][3]};
               if constexpr (BF)
                 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                             __builtin_bit_cast(bf16x8, bq), s, 0, 0, 0);

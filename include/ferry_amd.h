@@ -450,6 +450,10 @@ int ferry_owner_import_member(ferry_ctx* ctx, uint32_t lane, const void* image, 
  *   FERRY_PROBE_HBM_COPY    a streaming copy of pool slots [0, n) into device
  *                           memory (non-temporal loads and stores, the owner
  *                           hand-off's ceiling); bytes = 2*n*block_bytes
+ *   FERRY_PROBE_KTAB_READ   the mass selection's reads of the K table built by
+ *                           ferry_ktiles_build: the records of blocks [0, n)
+ *                           of every set, in its order and grid, no scores;
+ *                           bytes = n_req*L*Hkv*n*(block_bytes/2)
  * `bytes` gets the bytes moved per launch, `ms` the mean launch time.  The
  * reference sweeps its host-staged channel the same way
  * (probe_host_staged_bandwidth, src/topo/topo.cpp:68-129). */
@@ -457,6 +461,7 @@ int ferry_owner_import_member(ferry_ctx* ctx, uint32_t lane, const void* image, 
 #define FERRY_PROBE_HOST_READ 1
 #define FERRY_PROBE_HOST_DMA 2
 #define FERRY_PROBE_HBM_COPY 3
+#define FERRY_PROBE_KTAB_READ 4
 int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, int iters,
                    uint64_t* bytes, float* ms, void* stream);
 

@@ -208,6 +208,23 @@ def test_refusals():
     assert np.all(sel[0].cpu().numpy().view(np.uint32) == O.NONE)
 
 
+@pytest.mark.parametrize("dtype", [F.F16, F.FP8, F.F32])
+def test_ktable_read_probe(dtype):
+    # FERRY_PROBE_KTAB_READ reads the K half of n blocks of every set from the
+    # table in the mass selection's order: its bytes, and its refusals
+    p = Pair(3, 2, 2, 4, 8, 16, 96, dtype, host_blocks=257)
+    with pytest.raises(F.FerryError, match="ktiles_build"):
+        p.ex.bw_probe(F.PROBE_KTAB_READ, 10)
+    p.ex.ktiles_build()
+    b, ms, gbs = p.ex.bw_probe(F.PROBE_KTAB_READ, 96, iters=2)
+    assert b == 3 * 2 * 2 * 96 * (p.bb // 2) and ms > 0 and gbs > 0
+    b, _, _ = p.ex.bw_probe(F.PROBE_KTAB_READ, 37, iters=1)
+    assert b == 3 * 2 * 2 * 37 * (p.bb // 2)
+    with pytest.raises(F.FerryError, match="max_blocks"):
+        p.ex.bw_probe(F.PROBE_KTAB_READ, 97)
+    assert p.ex.stats()["device_error"] == 0
+
+
 def test_mass_selection_feeds_the_executor():
     """q -> mass selection -> bookkeeping/fetch -> attention over four decode
     steps: the selection under the near-tie bar, everything downstream of it
