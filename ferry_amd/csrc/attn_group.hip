@@ -25,8 +25,9 @@
 //     entries through its own ring of R blocks in LDS (three fp8 or two 16-bit
 //     blocks) with direct-to-LDS
 //     16-byte loads (global_load_lds_dwordx4, non-temporal: each block is read
-//     once), R - 1 blocks ahead, waiting only on its own load counter: no
-//     workgroup barrier in the loop.  The block's rows and 16-byte chunks are
+//     once), R blocks ahead: a slot takes the next block as soon as the
+//     block it held is read into registers.  A wavefront waits only on its
+//     own load counter: no workgroup barrier in the loop.  The block's rows and 16-byte chunks are
 //     permuted (lds_row, lds_chunk) so that the K reads (one row per lane, one
 //     chunk offset) and the V reads (four rows across the wavefront) hit
 //     distinct banks whether the LDS serves 128 or 256 bytes per pass.
@@ -142,10 +143,13 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
   constexpr int RB = group_ring_bytes(DT);    // ring bytes per wavefront
   constexpr int NQ = S::BF ? 2 : 1;           // parts of the Q^T operands (bf16: hi, lo)
   constexpr int COLS = 16 * NTILE;            // query columns
-  constexpr int DP = D + 4;                   // floats per merged column (bank offset)
-  constexpr int TR = RB / (16 * DP * 4);      // tiles merged per round
-  static_assert(RB == R * BB && R >= 2 && (R - 2) * NI < 64, "ring depth and load counter");
-  static_assert(TR >= 1, "a merge round fits the rings");
+  // tiles merged per round: W/2 wavefronts stage TT tiles of 8 KiB each in
+  // the rings and the Q^T operands, free once the blocks are consumed
+  constexpr int TT_FIT = (W * RB + NQ * NTILE * 4 * 64 * 16) / ((W / 2) * 8192);
+  constexpr int TT = NTILE < TT_FIT ? NTILE : TT_FIT;
+  static_assert(RB == R * BB && R >= 2 && (R - 1) * NI < 64, "ring depth and load counter");
+  static_assert(TT >= 1, "a merge round fits the rings and the Q^T operands");
+  static_assert(NTILE <= W, "each wavefront stages at most one query tile");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int GK = g.group * g.k;
@@ -158,7 +162,6 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
   uint32_t* msk = reinterpret_cast<uint32_t*>(rings);                     // [C] listing
   uint32_t* own = msk + g.C;                                              // [GK] listing
   uint32_t* mcnt = own + GK;                                              // [group] listing
-  float* red_o = reinterpret_cast<float*>(rings);                         // [W][TR*16][DP] merge
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15, grp = lane >> 4;
@@ -168,31 +171,57 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
   const int mem = min(g.group, g.n_req - o * g.group);  // member rows of this owner
   const uint32_t base = (uint32_t)((o * g.L + l) * g.Hkv + h) * (uint32_t)g.C;
 
+  // The global reads of the prologue go out together, so the workgroup pays
+  // one round trip before its first block loads, not one per read: the query
+  // values of the tile this wavefront stages, then this thread's first SB
+  // selections (the other workgroups on the CU keep the memory busy meanwhile)
+  float qx[4][8];
+  if (wave < NTILE) {  // tile `wave`: column n is member wave*MPT + n/G
+    const int mi = wave * MPT + n / G;
+    const size_t qrow = (size_t)((o * g.group + mi) * g.L + l) * g.Hq + (size_t)h * G + n % G;
+    q_load<DT>(mi < mem ? q + qrow * D : nullptr, grp, qx);
+  }
+  constexpr int SB = 4;  // selections in flight per thread
+  auto load_sel = [&](int e0, uint32_t (&sv)[SB]) {
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const int e = e0 + u * NT, mi = e / g.k;
+      sv[u] = kNone;
+      if (e < GK && mi < mem)
+        sv[u] = slots[((size_t)((o * g.group + mi) * g.L + l) * g.Hkv + h) * g.k + (e - mi * g.k)];
+    }
+  };
+  uint32_t sv[SB];
+  load_sel(tid, sv);
+
   // ---- 1. the distinct list of the group's selections
   for (int i = tid; i < g.C; i += NT) msk[i] = 0u;
   for (int i = tid; i < g.group; i += NT) mcnt[i] = 0u;
   __syncthreads();
   bool bad = false;
-  for (int e = tid; e < GK; e += NT) {
-    const int mi = e / g.k;
-    uint32_t s = kNone, mine = kNone;
-    if (mi < mem)
-      s = slots[((size_t)((o * g.group + mi) * g.L + l) * g.Hkv + h) * g.k + (e - mi * g.k)];
-    if (s != kNone) {
-      if (s >= g.pool_slots) {  // read as slot 0 and reported, as k_attn_mfma does
-        bad = true;
-        s = 0;
+  for (int e0 = tid; e0 < GK; e0 += NT * SB) {
+    if (e0 != tid) load_sel(e0, sv);
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const int e = e0 + u * NT, mi = e / g.k;
+      if (e >= GK) break;
+      uint32_t s = sv[u], mine = kNone;
+      if (s != kNone) {
+        if (s >= g.pool_slots) {  // read as slot 0 and reported, as k_attn_mfma does
+          bad = true;
+          s = 0;
+        }
+        const uint32_t loc = s - base;
+        if (loc < (uint32_t)g.C) {
+          const uint32_t bit = 1u << mi;
+          if (atomicOr(&msk[loc], bit) & bit) mine = s;  // a repeat in this row
+        } else {
+          mine = s;  // outside the set
+        }
       }
-      const uint32_t loc = s - base;
-      if (loc < (uint32_t)g.C) {
-        const uint32_t bit = 1u << mi;
-        if (atomicOr(&msk[loc], bit) & bit) mine = s;  // a repeat in this row
-      } else {
-        mine = s;  // outside the set
-      }
+      own[e] = mine;
+      if (mine != kNone) atomicAdd(&mcnt[mi], 1u);
     }
-    own[e] = mine;
-    if (mine != kNone) atomicAdd(&mcnt[mi], 1u);
   }
   if (bad) set_error(err, FERRY_ERANGE);
   __syncthreads();
@@ -239,13 +268,12 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
   __syncthreads();  // the rings may now overwrite msk / own
 
   // ---- Q^T operands of every tile, staged in LDS lane by lane (wavefront w
-  // builds tile w, w + W, ...): column n of tile t is member t*MPT + n/G,
-  // query head h*G + n%G (zeros past the group's members)
-  for (int t = wave; t < NTILE; t += W) {
-    const int mi = t * MPT + n / G;
-    const size_t qrow = (size_t)((o * g.group + mi) * g.L + l) * g.Hq + (size_t)h * G + n % G;
+  // builds tile w from the values it read first): column n of tile t is
+  // member t*MPT + n/G, query head h*G + n%G (zeros past the group's members)
+  if (wave < NTILE) {
+    const int t = wave;
     uint32_t qh[4][4], ql[4][4];
-    q_operand<DT>(mi < mem ? q + qrow * D : nullptr, grp, qscale, qh, ql);
+    q_convert<DT>(qx, qscale, qh, ql);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       qops[(t * 4 + kk) * 64 + lane] = u32x4{qh[kk][0], qh[kk][1], qh[kk][2], qh[kk][3]};
@@ -307,7 +335,7 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
     }
   };
 #pragma unroll
-  for (int b = 0; b < R - 1; ++b)
+  for (int b = 0; b < R; ++b)
     if (b < nb) issue(b, b);
   for (int j0 = 0; j0 < nb; j0 += R) {
 #pragma unroll
@@ -315,12 +343,7 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
       const int j = j0 + b;
       if (j < nb) {  // uniform
         // block j landed once at most the later blocks issued are in flight
-        wait_blocks<NI, R - 2>(min(R - 2, nb - 1 - j));
-        if (j + R - 1 < nb) {
-          // ring slot (b - 1) mod R held block j - 1: its LDS reads have returned
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          issue(j + R - 1, (b + R - 1) % R);
-        }
+        wait_blocks<NI, R - 1>(min(R - 1, nb - 1 - j));
         const int li = wave + W * j;
         const uint32_t mm = (uint32_t)__builtin_amdgcn_readfirstlane((int)lmask[li]);
         float ks = 1.0f, vs = 1.0f;
@@ -332,6 +355,12 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
         u32x4 kw[NKW];
         uint32_t vw[4][VW];
         read_block(ring + b * BB, kw, vw);
+        if (j + R < nb) {
+          // the block's LDS reads have returned: its ring slot takes block
+          // j + R, so R blocks stay in flight while this one is attended
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          issue(j + R, b);
+        }
         Ops op;
         block_operands<DT>(kw, vw, op);
 #pragma unroll
@@ -356,7 +385,13 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
     }
   }
 
-  // ---- 4. merge the wavefronts' states: per round, TR tiles through LDS
+  // ---- 4. merge the wavefronts' states.  (a) Every wavefront's per-column
+  // max and sum go to LDS; (b) each wavefront scales its accumulators to the
+  // column's final weights, o_w * vs_ref_w * 2^(m_w - M) / L with M the max
+  // over the wavefronts and L = sum_w l_w 2^(m_w - M) (0 where the column
+  // attended nothing); (c) the scaled accumulators are summed through LDS in
+  // a tree (wavefronts [h, 2h) write, [0, h) add, h = W/2 .. 1), TT tiles at a
+  // time, in a fixed order; (d) wavefront 0 writes the outputs.
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) {
     float lsum = acc[t].lsum;
@@ -367,42 +402,61 @@ __global__ __launch_bounds__(W * 64) void k_attn_group(
       red_ml[(wave * COLS + 16 * t + n) * 2 + 1] = lsum;
     }
   }
+  __syncthreads();  // red_ml complete; the rings and the Q^T operands are free
 #pragma unroll
-  for (int t0 = 0; t0 < NTILE; t0 += TR) {
-    __syncthreads();  // the rings (first round) or the last round's red_o are free
+  for (int t = 0; t < NTILE; ++t) {
+    const int col = 16 * t + n;
+    float mx = kNeg;
 #pragma unroll
-    for (int t = t0; t < min(t0 + TR, NTILE); ++t) {
-      const float vref = S::F8 ? acc[t].vs_ref : 1.0f;
-      float* ro = red_o + ((size_t)wave * TR * 16 + (t - t0) * 16 + n) * DP + 32 * grp;
+    for (int w = 0; w < W; ++w) mx = fmaxf(mx, red_ml[(w * COLS + col) * 2]);
+    float lt = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float4* op = reinterpret_cast<float4*>(ro + 8 * i);
-        op[0] = float4{acc[t].o[0][i] * vref, acc[t].o[1][i] * vref, acc[t].o[2][i] * vref,
-                       acc[t].o[3][i] * vref};
-        op[1] = float4{acc[t].o[4][i] * vref, acc[t].o[5][i] * vref, acc[t].o[6][i] * vref,
-                       acc[t].o[7][i] * vref};
+    for (int w = 0; w < W; ++w)
+      lt += red_ml[(w * COLS + col) * 2 + 1] * exp2_fast(red_ml[(w * COLS + col) * 2] - mx);
+    const float vref = S::F8 ? acc[t].vs_ref : 1.0f;
+    const float f = lt > 0.0f ? exp2_fast(acc[t].m - mx) * vref / lt : 0.0f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) acc[t].o[v] *= f;
+  }
+  f32x4* stage = reinterpret_cast<f32x4*>(smem);  // [W/2][TT][8][64], lane-major
+#pragma unroll
+  for (int t0 = 0; t0 < NTILE; t0 += TT) {
+    if (t0 > 0) __syncthreads();  // wavefront 0 has read the last round
+#pragma unroll
+    for (int hw = W / 2; hw >= 1; hw /= 2) {
+      if (wave >= hw && wave < 2 * hw) {
+#pragma unroll
+        for (int t = t0; t < min(t0 + TT, NTILE); ++t)
+#pragma unroll
+          for (int v = 0; v < 8; ++v)
+            stage[(((wave - hw) * TT + (t - t0)) * 8 + v) * 64 + lane] = acc[t].o[v];
       }
+      __syncthreads();
+      if (wave < hw) {
+#pragma unroll
+        for (int t = t0; t < min(t0 + TT, NTILE); ++t)
+#pragma unroll
+          for (int v = 0; v < 8; ++v)
+            acc[t].o[v] += stage[((wave * TT + (t - t0)) * 8 + v) * 64 + lane];
+      }
+      if (hw > 1) __syncthreads();  // the adders have read before the next writers
     }
-    __syncthreads();
-    const int ncol = 16 * (min(t0 + TR, NTILE) - t0);
-    for (int x = tid; x < ncol * D; x += NT) {
-      const int c = x / D, d = x % D;  // column 16*t0 + c
-      const int col = 16 * t0 + c;
-      const int mi = (col / 16) * MPT + (col % 16) / G;
-      if (mi >= mem) continue;
-      float mx = kNeg;
+    if (wave == 0) {
+      // lane (n, grp) holds dims 32 grp + 8 i + v of column n in o[v][i]
 #pragma unroll
-      for (int w = 0; w < W; ++w) mx = fmaxf(mx, red_ml[(w * COLS + col) * 2]);
-      float lt = 0.0f, ot = 0.0f;
+      for (int t = t0; t < min(t0 + TT, NTILE); ++t) {
+        const int mi = t * MPT + n / G;
+        if (mi >= mem) continue;
+        const size_t qrow =
+            (size_t)((o * g.group + mi) * g.L + l) * g.Hq + (size_t)h * G + n % G;
+        float4* dst = reinterpret_cast<float4*>(out + qrow * D + 32 * grp);
 #pragma unroll
-      for (int w = 0; w < W; ++w) {
-        const float f = exp2_fast(red_ml[(w * COLS + col) * 2] - mx);
-        lt += red_ml[(w * COLS + col) * 2 + 1] * f;
-        ot += red_o[((size_t)w * TR * 16 + c) * DP + d] * f;
+        for (int i = 0; i < 4; ++i) {
+          const f32x4* a = acc[t].o;
+          dst[2 * i] = float4{a[0][i], a[1][i], a[2][i], a[3][i]};
+          dst[2 * i + 1] = float4{a[4][i], a[5][i], a[6][i], a[7][i]};
+        }
       }
-      const size_t qrow =
-          (size_t)((o * g.group + mi) * g.L + l) * g.Hq + (size_t)h * G + (col % 16) % G;
-      out[qrow * D + d] = lt > 0.0f ? ot / lt : 0.0f;  // nothing selected: 0
     }
   }
 }

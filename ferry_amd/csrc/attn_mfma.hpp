@@ -73,29 +73,38 @@ struct Shape {
   static constexpr int VW = F8 ? 2 : 4;       // dwords of V per token per lane
 };
 
-// Q^T operand of column n for this lane's group: `qp` points at the column's
-// 128 fp32 values (nullptr for a padding column: zeros), pre-scaled by qscale
-// (log2(e) / sqrt(D)).
+// The 32 fp32 query values of column n that this lane's group holds in the
+// Q^T operand (k-slice kk: x[kk][0..7]); `qp` points at the column's 128
+// values, nullptr for a padding column (zeros).
 template <int DT>
-__device__ inline void q_operand(const float* __restrict__ qp, int grp, float qscale,
-                                 uint32_t (&qhi)[4][4], uint32_t (&qlo)[4][4]) {
+__device__ inline void q_load(const float* __restrict__ qp, int grp, float (&x)[4][8]) {
   using S = Shape<DT>;
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
     const int d0 = S::EPW * (4 * (kk / S::SUB) + grp) + 8 * (kk % S::SUB);
-    float x[8];
     if (qp) {
       const float4* p = reinterpret_cast<const float4*>(qp + d0);
       const float4 a = p[0], b = p[1];
-      x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z,
-      x[7] = b.w;
+      x[kk][0] = a.x, x[kk][1] = a.y, x[kk][2] = a.z, x[kk][3] = a.w;
+      x[kk][4] = b.x, x[kk][5] = b.y, x[kk][6] = b.z, x[kk][7] = b.w;
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+      for (int e = 0; e < 8; ++e) x[kk][e] = 0.0f;
     }
+  }
+}
+
+// Q^T operand of column n for this lane's group from the values q_load read,
+// pre-scaled by qscale (log2(e) / sqrt(D)).
+template <int DT>
+__device__ inline void q_convert(const float (&x)[4][8], float qscale, uint32_t (&qhi)[4][4],
+                                 uint32_t (&qlo)[4][4]) {
+  using S = Shape<DT>;
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
-      const float a = x[e] * qscale, b = x[e + 1] * qscale;
+      const float a = x[kk][e] * qscale, b = x[kk][e + 1] * qscale;
       if constexpr (S::BF) {
         const uint16_t ah = bf16_rne(a), bh = bf16_rne(b);
         const float ar = a - __builtin_bit_cast(float, (uint32_t)ah << 16);
@@ -109,6 +118,16 @@ __device__ inline void q_operand(const float* __restrict__ qp, int grp, float qs
       }
     }
   }
+}
+
+// Q^T operand of column n for this lane's group: `qp` points at the column's
+// 128 fp32 values (nullptr for a padding column: zeros), pre-scaled by qscale.
+template <int DT>
+__device__ inline void q_operand(const float* __restrict__ qp, int grp, float qscale,
+                                 uint32_t (&qhi)[4][4], uint32_t (&qlo)[4][4]) {
+  float x[4][8];
+  q_load<DT>(qp, grp, x);
+  q_convert<DT>(x, qscale, qhi, qlo);
 }
 
 // Running state of one wavefront's columns: online-softmax max and sum (lane
