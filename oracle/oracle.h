@@ -22,8 +22,9 @@
  *     modulo capacity: src/runtime/wla_multigpu.cuh:323-332)
  *   - fp64 block-sparse decode attention (textbook softmax attention; the
  *     reference only has an FMA proxy at src/workloads/kv_exec.cuh:30-37 and
- *     the selection semantics of tools/capture_miss_trace.py:139-159)
- *   - a timed fp32 CPU executor step (cpu_baseline of bench.py)
+ *     the selection semantics of tools/capture_miss_trace.py:139-159), over the
+ *     generated host tier or over a caller's tier image
+ *   - a timed fp32 CPU executor step (cpu_baseline of bench.py; cpu_step.c)
  *   - lane turnover: owner reset, empty selection positions and request
  *     arrivals (steady and bursty: src/runtime/wla_multigpu.cuh:497-501;
  *     Poisson and Markov-modulated), the owner copy of a hand-off
