@@ -270,10 +270,12 @@ int ferry_sparse_decode(ferry_ctx* ctx, const float* q, const uint32_t* slots,
 /* Which attention kernel ferry_sparse_decode runs for this context:
  * *kind = FERRY_ATTN_VALU, FERRY_ATTN_MFMA (one workgroup per request row) or
  * FERRY_ATTN_GROUP (one per prefix-group set), *waves = wavefronts per
- * workgroup of its launch (the prefix-group kernel runs eight on a launch of
- * no more group sets than the GPU has CUs where its LDS allows, else four,
- * so a layer range of ferry_sparse_decode_layers can differ).  No reference counterpart (the reference has one proxy kernel);
- * for callers that report rooflines per kernel. */
+ * workgroup of ferry_sparse_decode's launch over all L layers.  The
+ * prefix-group kernel runs eight on a launch of no more group sets than the
+ * GPU has CUs where its LDS allows, else four, so the smaller launches of
+ * ferry_sparse_decode_layers and of ferry_decode_step's layer ranges may run
+ * eight where four is reported.  No reference counterpart (the reference has
+ * one proxy kernel); for callers that report rooflines per kernel. */
 int ferry_attn_kernel(const ferry_ctx* ctx, int32_t* kind, int32_t* waves);
 
 /* Attention of layers [l0, l0 + nl) only. */
@@ -288,7 +290,9 @@ int ferry_sparse_decode_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const flo
  * drained, before range c is attended), so the fetch of a range waits for
  * neither its bookkeeping nor any attention.  The overlap needs the two streams on
  * different hardware queues: HIP shares a few queues (4 by default) among a
- * process's streams, and two streams on one queue run in turn.  The context
+ * process's streams round-robin as they are created, and two streams on one
+ * queue run in turn, so a caller creates its side stream once and keeps it (a
+ * fresh stream per step can land on the main stream's queue).  The context
  * creates no stream of its own.  side_stream NULL (or
  * equal to stream) runs the same sequence on one stream.  When this returns,
  * work queued on `stream` after it observes the whole step.  Replaces the refill /
