@@ -696,12 +696,14 @@ def run_mass(a, ex, F, torch, stream, dtype, w, ctx, dctx, qs, sel0, max_blocks,
     t = e0.elapsed_time(e1) / n_timed
     nb = int(ctx.sum()) * L * H
     nbytes = nb * (rec + (4 if dtype == F.FP8 else 0)) + B * L * Hq * 128 * 4 + B * L * H * k * 4
-    kern = "k_select_mass" if dtype == F.F32 else "k_select_mass_mfma"
+    G = Hq // H
+    kern = (f"k_select_mass<{w['dtype']},{G}>" if dtype == F.F32 else  # 16-bit and fp8 K: two launches
+            f"k_mass_units<{w['dtype']},{G}> + k_mass_topk")
     gbs = nbytes / (t * 1e-3) / 1e9
     # ceiling: the same records read in the kernel's order and grid, no scores
     # (every set's first max(ctx) blocks: the same bytes where contexts are equal)
     pbytes, pms, pgbs = ex.bw_probe(F.PROBE_KTAB_READ, int(ctx.max()), iters=3, stream=stream)
-    return {"bound": "hbm", "kernel": f"{kern}<{w['dtype']},{Hq // H}>", "ms": round(t, 4),
+    return {"bound": "hbm", "kernel": kern, "ms": round(t, 4),
             "context_blocks_per_launch": nb, "k_table_gb": round(n_rec * rec / 1e9, 1),
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),

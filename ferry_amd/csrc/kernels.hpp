@@ -162,7 +162,7 @@ __global__ void k_probe_gather(const uint8_t* pool, uint64_t bb, const uint32_t*
                                uint64_t pool_slots, uint32_t* sink);
 template <int NV>
 __global__ void k_probe_copy(const uint8_t* src, uint8_t* dst, uint64_t bb, uint64_t n_blocks);
-template <int NI, int W>
+template <int NI, int W, int U, int UNITS>
 __global__ void k_probe_ktab(Geo g, const uint8_t* kt, uint64_t kt_mod, int nb, uint32_t* sink);
 template <int NV>
 __global__ void k_probe_host(const uint8_t* host, uint64_t bb, uint64_t n_blocks, uint32_t* sink);
@@ -223,8 +223,8 @@ __global__ void k_select_topk(Geo g, const float* q, const int32_t* ctx_blocks, 
                               const float* sum_scales, uint64_t sum_mod, uint32_t* sel, int l0, int nl,
                               int max_n, int* err);
 
-// Mass method of the top-k selection (select.hip): the dense K table and the
-// per-(request, layer) softmax-mass scoring + radix top-k.
+// Mass method of the top-k selection (select.hip): the dense K table, the
+// softmax-mass scoring and the radix top-k of each (request, layer).
 template <int NV>
 __global__ void k_ktiles_build(Geo g, const uint8_t* host, const float* host_scales, uint8_t* kt,
                                float* kt_scales, int perm);
@@ -232,12 +232,31 @@ template <int DT, int G, int W>
 __global__ void k_select_mass(Geo g, const float* q, const int32_t* ctx_blocks, const uint8_t* kt,
                               const float* kt_scales, uint64_t kt_mod, float* ws, uint32_t* sel, int l0,
                               int nl, int max_n, int* err);
-template <int DT, int G, int W>
-__global__ void k_select_mass_mfma(Geo g, const float* q, const int32_t* ctx_blocks, const uint8_t* kt,
-                                   const float* kt_scales, uint64_t kt_mod, float* ws, uint32_t* sel,
-                                   int l0, int nl, int max_n, int* err);
-// persistent workgroups of k_select_mass; each holds max_blocks * G * 2 floats of workspace
+// 16-bit and fp8 K: k_mass_units scores one (request, layer, kv head) unit
+// per workgroup pass into mass[unit][block], then k_mass_topk sums each
+// (request, layer) item's kv heads and takes its top k.
+template <int DT, int G, int W, int U>
+__global__ void k_mass_units(Geo g, const float* q, const int32_t* ctx_blocks, const uint8_t* kt,
+                             const float* kt_scales, uint64_t kt_mod, float* ws, float* mass,
+                             unsigned* counter, int l0, int nl, int max_n, int* err);
+__global__ void k_mass_reset(unsigned* counter);
+template <int W>
+__global__ void k_mass_topk(Geo g, const int32_t* ctx_blocks, const float* mass, uint32_t* sel, int l0,
+                            int nl, int max_n);
+// persistent workgroups of k_select_mass (fp32 K); each holds max_blocks * G * 2
+// floats of workspace
 constexpr int kMassWgs = 2048;
+// k_mass_units: wavefronts per workgroup, K records in flight per wavefront,
+// and at most this many workgroups (the GPU's resident ones below that), each
+// with a max_blocks * G * 2-float workspace slice.  At the long-context GQA
+// shape (bf16, 138 VGPRs: one workgroup per CU) eight wavefronts with three
+// records each measured 0.80-0.84 of HBM, four records 0.80-0.83, and four
+// wavefronts (three workgroups per CU) 0.77-0.80 with four records, 0.82
+// with six.
+constexpr int kMassUnitWaves = 8;
+constexpr int kMassUnitInflight = 3;
+constexpr int kMassUnitWgs = 2048;
+constexpr int kMassTopkWaves = 4;
 
 // queue.hip: the ceiling of the ring's tickets (one shared 64-bit word)
 __global__ void k_ticket_probe(unsigned long long* word, int iters, int kind, int* failed);

@@ -116,17 +116,22 @@ __global__ __launch_bounds__(256) void k_probe_copy(const uint8_t* __restrict__ 
   }
 }
 
-template <int NI, int W>
+// The mass selection's K-table reads without its scores: NI 1 KiB loads per
+// record, U records in flight per wavefront, blocks [0, nb) of every set.
+// UNITS = 1: one (request, layer, kv head) set per workgroup pass, as
+// k_mass_units; UNITS = 0: a (request, layer) item's kv heads one after the
+// other per workgroup, as k_select_mass.
+template <int NI, int W, int U, int UNITS>
 __global__ __launch_bounds__(W * 64) void k_probe_ktab(Geo g, const uint8_t* __restrict__ kt,
                                                       uint64_t kt_mod, int nb,
                                                       uint32_t* __restrict__ sink) {
-  constexpr int U = 4;  // records in flight per wavefront, as k_select_mass_mfma
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n_items = g.n_req * g.L;
+  const int n_work = UNITS ? g.n_req * g.L * g.Hkv : g.n_req * g.L;
+  const int hs = UNITS ? 1 : g.Hkv;  // sets per work item
   u32x4 acc = {0u, 0u, 0u, 0u};
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    for (int h = 0; h < g.Hkv; ++h) {
-      const uint64_t set = (uint64_t)item * g.Hkv + h;
+  for (int wi = blockIdx.x; wi < n_work; wi += gridDim.x) {
+    for (int h = 0; h < hs; ++h) {
+      const uint64_t set = (uint64_t)wi * hs + h;
       for (int b0 = wave; b0 < nb; b0 += W * U) {
         u32x4 w[U][NI];
 #pragma unroll
@@ -155,9 +160,11 @@ __global__ __launch_bounds__(W * 64) void k_probe_ktab(Geo g, const uint8_t* __r
   if (lane == 0) sink[(size_t)blockIdx.x * W + wave] = x;
 }
 
-template __global__ void k_probe_ktab<2, 8>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
-template __global__ void k_probe_ktab<4, 8>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
-template __global__ void k_probe_ktab<8, 4>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
+template __global__ void k_probe_ktab<2, kMassUnitWaves, kMassUnitInflight, 1>(Geo, const uint8_t*,
+                                                                              uint64_t, int, uint32_t*);
+template __global__ void k_probe_ktab<4, kMassUnitWaves, kMassUnitInflight, 1>(Geo, const uint8_t*,
+                                                                              uint64_t, int, uint32_t*);
+template __global__ void k_probe_ktab<8, 4, 4, 0>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
 template __global__ void k_probe_gather<4>(const uint8_t*, uint64_t, const uint32_t*, int, uint64_t,
                                            uint32_t*);
 template __global__ void k_probe_gather<8>(const uint8_t*, uint64_t, const uint32_t*, int, uint64_t,

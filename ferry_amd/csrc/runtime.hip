@@ -130,6 +130,7 @@ struct ferry_ctx {
   std::vector<hipEvent_t> booked;   // ... and bookkeeping done
   int attn_waves = 0;              // wavefronts per attention workgroup (FERRY_ATTN_WAVES), 0 = default
   int cus = 256;                   // compute units of the device
+  int mass_resident = 0;           // k_mass_units workgroups resident at once (0: not yet asked)
   int group_waves_env = 0;         // prefix-group kernel wavefronts (FERRY_GROUP_WAVES=4|8), 0 = by launch
   int fetch_waves = 0;             // wavefronts per fetch workgroup (FERRY_FETCH_WAVES: 1, 2, 4; 0 = by rule)
   int fetch_prio = 1;              // fetch wavefronts issue first (FERRY_FETCH_PRIO=0: not)
@@ -1278,6 +1279,70 @@ int ferry_select_topk(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks,
 // one float score per context block in LDS
 constexpr uint64_t kMassLds = 60 * 1024;
 
+}  // extern "C"
+
+namespace {
+
+// One workgroup's workspace slice of the mass selection: a (max, sum) pair per
+// context block and query head.
+uint64_t mass_slice_bytes(const Geo& g) {
+  return (uint64_t)g.max_blocks * (uint64_t)(g.Hq / g.Hkv) * 2 * sizeof(float);
+}
+
+// Workgroups of k_mass_units the device holds at once (occupancy x CUs),
+// computed once per context.
+int mass_units_resident(ferry_ctx* ctx) {
+  if (ctx->mass_resident > 0) return ctx->mass_resident;
+  const Geo& g = ctx->g;
+  const int G = g.Hq / g.Hkv;
+  const void* fn = nullptr;
+#define FERRY_MASS_FN(DT)                                                                           \
+  fn = G == 1   ? reinterpret_cast<const void*>(&k_mass_units<DT, 1, kMassUnitWaves, kMassUnitInflight>) \
+       : G == 2 ? reinterpret_cast<const void*>(&k_mass_units<DT, 2, kMassUnitWaves, kMassUnitInflight>) \
+       : G == 4 ? reinterpret_cast<const void*>(&k_mass_units<DT, 4, kMassUnitWaves, kMassUnitInflight>) \
+                : reinterpret_cast<const void*>(&k_mass_units<DT, 8, kMassUnitWaves, kMassUnitInflight>)
+  if (g.dtype == FERRY_F16) FERRY_MASS_FN(FERRY_F16);
+  else if (g.dtype == FERRY_BF16) FERRY_MASS_FN(FERRY_BF16);
+  else FERRY_MASS_FN(FERRY_FP8_E4M3);
+#undef FERRY_MASS_FN
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * kMassUnitWaves, 0) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  ctx->mass_resident = per_cu * ctx->cus;
+  return ctx->mass_resident;
+}
+
+// Workgroups of a mass selection over nl layers, at most cap: (request,
+// layer) items for fp32 K (k_select_mass, at most kMassWgs); for 16-bit and
+// fp8 K (k_mass_units) at most the (request, layer, kv head) units, the
+// resident workgroups and kMassUnitWgs.
+uint64_t mass_wgs(ferry_ctx* ctx, int nl, uint64_t cap) {
+  const Geo& g = ctx->g;
+  if (g.dtype == FERRY_F32)
+    return std::min<uint64_t>(std::min<uint64_t>((uint64_t)g.n_req * nl, kMassWgs), cap);
+  const uint64_t units = (uint64_t)g.n_req * nl * g.Hkv;
+  const uint64_t res = std::min<uint64_t>((uint64_t)mass_units_resident(ctx), kMassUnitWgs);
+  return std::min<uint64_t>(std::min<uint64_t>(units, res), cap);
+}
+
+// Workspace of a mass selection over nl layers with wgs workgroups: their
+// slices; for 16-bit and fp8 K first a 256-byte unit counter, and after the
+// slices a float mass per context block of every (request, layer, kv head)
+// unit, 256-byte aligned.
+constexpr uint64_t kMassCounterBytes = 256;
+uint64_t mass_mass_offset(const Geo& g, uint64_t wgs) {
+  return kMassCounterBytes + (wgs * mass_slice_bytes(g) + 255) / 256 * 256;
+}
+uint64_t mass_ws_bytes(const Geo& g, int nl, uint64_t wgs) {
+  if (g.dtype == FERRY_F32) return wgs * mass_slice_bytes(g);
+  return mass_mass_offset(g, wgs) + (uint64_t)g.n_req * nl * g.Hkv * g.max_blocks * sizeof(float);
+}
+
+}  // namespace
+
+extern "C" {
+
 int ferry_ktiles_build(ferry_ctx* ctx, uint64_t n_records, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
   const Geo& g = ctx->g;
@@ -1299,10 +1364,8 @@ int ferry_ktiles_build(ferry_ctx* ctx, uint64_t n_records, void* stream) {
       return rc;
     ctx->kt_records = S;
   }
-  if (!ctx->mass_ws && (uint64_t)g.max_blocks * 4 <= kMassLds) {
-    const uint64_t wgs = std::min<uint64_t>((uint64_t)g.n_req * g.L, kMassWgs);
-    HIPC(hipMalloc(&ctx->mass_ws, wgs * g.max_blocks * (uint64_t)(g.Hq / g.Hkv) * 8));
-  }
+  if (!ctx->mass_ws && (uint64_t)g.max_blocks * 4 <= kMassLds)
+    HIPC(hipMalloc(&ctx->mass_ws, mass_ws_bytes(g, g.L, mass_wgs(ctx, g.L, ~0ull))));
   ctx->kt_perm = g.dtype != FERRY_F32;
   const unsigned blocks = (unsigned)std::min<uint64_t>((g.host_blocks + 3) / 4, 16384);
   switch (KT / 1024) {
@@ -1335,40 +1398,59 @@ int ferry_ktiles_view(ferry_ctx* ctx, void** ktiles, float** scales, uint64_t* n
 
 namespace {
 
-// The mass selection of layers [l0, l0 + nl) with workspace `ws`, which holds
-// max_wgs slices of max_blocks * G (max, sum) pairs.
+// The mass selection of layers [l0, l0 + nl) with `wgs` workgroups
+// (mass_wgs) and workspace `ws` of mass_ws_bytes(g, nl, wgs).
 int launch_select_mass(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
                        const int32_t* ctx_blocks, uint32_t* sel, void* stream, float* ws,
-                       uint64_t max_wgs) {
+                       uint64_t wgs) {
   const Geo& g = ctx->g;
   HIPC(hipSetDevice(ctx->device));
-  const dim3 grid((unsigned)std::min<uint64_t>(std::min<uint64_t>((uint64_t)g.n_req * nl, kMassWgs),
-                                               max_wgs));
-  const size_t lds = (size_t)g.max_blocks * 4;
   hipStream_t s = (hipStream_t)stream;
   const int G = g.Hq / g.Hkv;
-  // vector ALUs (4 wavefronts) for fp32 K, matrix cores (8 wavefronts) for
-  // 16-bit and fp8 K; the wider workgroup keeps more blocks in flight when
-  // there are few (request, layer) items
-#define FERRY_MASS_LAUNCH(KERN, DT, GG, WW)                                                      \
-  hipLaunchKernelGGL((KERN<DT, GG, WW>), grid, dim3(64 * WW), lds, s, g, q, ctx_blocks,         \
-                     ctx->ktab, ctx->ktab_scales, ctx->kt_records, ws, sel, l0, nl,             \
+  const size_t lds = (size_t)g.max_blocks * 4;
+  if (g.dtype == FERRY_F32) {  // vector ALUs, one (request, layer) item per workgroup pass
+#define FERRY_MASS_LAUNCH(GG)                                                                  \
+  hipLaunchKernelGGL((k_select_mass<FERRY_F32, GG, 4>), dim3((unsigned)wgs), dim3(256), lds, s, g, \
+                     q, ctx_blocks, ctx->ktab, ctx->ktab_scales, ctx->kt_records, ws, sel, l0, nl, \
                      g.max_blocks, ctx->err)
-#define FERRY_MASS_G(KERN, DT, WW)                       \
-  switch (G) {                                           \
-    case 1: FERRY_MASS_LAUNCH(KERN, DT, 1, WW); break;   \
-    case 2: FERRY_MASS_LAUNCH(KERN, DT, 2, WW); break;   \
-    case 4: FERRY_MASS_LAUNCH(KERN, DT, 4, WW); break;   \
-    default: FERRY_MASS_LAUNCH(KERN, DT, 8, WW); break;  \
+    switch (G) {
+      case 1: FERRY_MASS_LAUNCH(1); break;
+      case 2: FERRY_MASS_LAUNCH(2); break;
+      case 4: FERRY_MASS_LAUNCH(4); break;
+      default: FERRY_MASS_LAUNCH(8); break;
+    }
+#undef FERRY_MASS_LAUNCH
+    HIPC(hipGetLastError());
+    return FERRY_OK;
+  }
+  // matrix cores: the units' masses, then each item's sum over kv heads and top k
+  unsigned* counter = reinterpret_cast<unsigned*>(ws);
+  float* slices = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + kMassCounterBytes);
+  float* mass = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + mass_mass_offset(g, wgs));
+  hipLaunchKernelGGL(k_mass_reset, dim3(1), dim3(64), 0, s, counter);
+  HIPC(hipGetLastError());
+#define FERRY_MASS_UNITS(DT, GG)                                                                 \
+  hipLaunchKernelGGL((k_mass_units<DT, GG, kMassUnitWaves, kMassUnitInflight>), dim3((unsigned)wgs), \
+                     dim3(64 * kMassUnitWaves), 0, s, g, q, ctx_blocks, ctx->ktab, ctx->ktab_scales,  \
+                     ctx->kt_records, slices, mass, counter, l0, nl, g.max_blocks, ctx->err)
+#define FERRY_MASS_UNITS_G(DT)                \
+  switch (G) {                                \
+    case 1: FERRY_MASS_UNITS(DT, 1); break;   \
+    case 2: FERRY_MASS_UNITS(DT, 2); break;   \
+    case 4: FERRY_MASS_UNITS(DT, 4); break;   \
+    default: FERRY_MASS_UNITS(DT, 8); break;  \
   }
   switch (g.dtype) {
-    case FERRY_F32: FERRY_MASS_G(k_select_mass, FERRY_F32, 4); break;
-    case FERRY_F16: FERRY_MASS_G(k_select_mass_mfma, FERRY_F16, 8); break;
-    case FERRY_BF16: FERRY_MASS_G(k_select_mass_mfma, FERRY_BF16, 8); break;
-    default: FERRY_MASS_G(k_select_mass_mfma, FERRY_FP8_E4M3, 8); break;
+    case FERRY_F16: FERRY_MASS_UNITS_G(FERRY_F16); break;
+    case FERRY_BF16: FERRY_MASS_UNITS_G(FERRY_BF16); break;
+    default: FERRY_MASS_UNITS_G(FERRY_FP8_E4M3); break;
   }
-#undef FERRY_MASS_G
-#undef FERRY_MASS_LAUNCH
+#undef FERRY_MASS_UNITS_G
+#undef FERRY_MASS_UNITS
+  HIPC(hipGetLastError());
+  const unsigned items = (unsigned)std::min<uint64_t>((uint64_t)g.n_req * nl, kMassWgs);
+  hipLaunchKernelGGL((k_mass_topk<kMassTopkWaves>), dim3(items), dim3(64 * kMassTopkWaves), lds, s, g,
+                     ctx_blocks, mass, sel, l0, nl, g.max_blocks);
   HIPC(hipGetLastError());
   return FERRY_OK;
 }
@@ -1397,7 +1479,8 @@ int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float
                              const int32_t* ctx_blocks, uint32_t* sel, void* stream) {
   if (int rc = check_select_mass(ctx, l0, nl, q, ctx_blocks, sel)) return rc;
   if (!ctx->mass_ws) return fail(FERRY_EINVAL, "no mass-selection workspace (ferry_ktiles_build failed)");
-  return launch_select_mass(ctx, l0, nl, q, ctx_blocks, sel, stream, ctx->mass_ws, kMassWgs);
+  return launch_select_mass(ctx, l0, nl, q, ctx_blocks, sel, stream, ctx->mass_ws,
+                            mass_wgs(ctx, nl, ~0ull));
 }
 
 int ferry_select_mass(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks, uint32_t* sel,
@@ -1411,15 +1494,29 @@ int ferry_select_mass_noalloc(ferry_ctx* ctx, const float* q, const int32_t* ctx
   if (int rc = check_ctx(ctx)) return rc;
   if (int rc = check_select_mass(ctx, 0, ctx->g.L, q, ctx_blocks, sel)) return rc;
   const Geo& g = ctx->g;
-  // one workgroup's slice: a (max, sum) pair per context block and query head
-  const uint64_t slice = (uint64_t)g.max_blocks * (uint64_t)(g.Hq / g.Hkv) * 2 * sizeof(float);
-  if (slice > kNoAllocScratchBytes)
-    return fail(FERRY_EINVAL, "ferry_select_mass_noalloc: one workgroup's workspace (" +
-                                  std::to_string(slice) + " B) exceeds the static scratch of " +
-                                  std::to_string(kNoAllocScratchBytes) + " B");
   if (!ctx->scratch_dev) return fail(FERRY_EHIP, "static scratch not resolved for this device");
-  return launch_select_mass(ctx, 0, g.L, q, ctx_blocks, sel, stream, ctx->scratch_dev,
-                            kNoAllocScratchBytes / slice);
+  // the largest layer range whose workspace (the masses of its units, 16-bit
+  // and fp8 K) leaves room in the static array for at least one workgroup
+  // slice; ranges run one after the other on the stream
+  const uint64_t slice = mass_slice_bytes(g);
+  auto wgs_cap = [&](int n) -> uint64_t {
+    const uint64_t fixed = mass_ws_bytes(g, n, 0) + 256;
+    return fixed + slice <= kNoAllocScratchBytes ? (kNoAllocScratchBytes - fixed) / slice : 0;
+  };
+  int nl = g.L;
+  while (nl > 0 && wgs_cap(nl) == 0) --nl;
+  if (nl == 0)
+    return fail(FERRY_EINVAL, "ferry_select_mass_noalloc: the workspace of one layer (" +
+                                  std::to_string(mass_ws_bytes(g, 1, 1)) +
+                                  " B) exceeds the static scratch of " +
+                                  std::to_string(kNoAllocScratchBytes) + " B");
+  for (int l0 = 0; l0 < g.L; l0 += nl) {
+    const int n = std::min(nl, g.L - l0);
+    if (int rc = launch_select_mass(ctx, l0, n, q, ctx_blocks, sel, stream, ctx->scratch_dev,
+                                    mass_wgs(ctx, n, wgs_cap(n))))
+      return rc;
+  }
+  return FERRY_OK;
 }
 
 int ferry_owner_image_bytes(const ferry_ctx* ctx, uint64_t* bytes) {
@@ -1569,10 +1666,19 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
   HIPC(hipSetDevice(ctx->device));
   hipStream_t s = (hipStream_t)stream;
   const int host_waves = g.workers * 4;
-  // the K-table probe: the mass selection's grid (at most kMassWgs workgroups
-  // of 8 wavefronts, 4 for fp32 records)
-  const int kt_w = g.dtype == FERRY_F32 ? 4 : 8;
-  const uint64_t kt_grid = std::min<uint64_t>((uint64_t)g.n_req * g.L, kMassWgs);
+  // the K-table probe: the mass selection's order and wavefronts; for 16-bit
+  // and fp8 records one workgroup per (request, layer, kv head) unit, which
+  // the GPU dispatches in unit order as k_mass_units takes them
+  const int kt_w = g.dtype == FERRY_F32 ? 4 : kMassUnitWaves;
+  const uint64_t kt_grid = g.dtype == FERRY_F32 ? mass_wgs(ctx, g.L, ~0ull)
+                                                : (uint64_t)g.n_req * g.L * g.Hkv;
+  // and as many of its workgroups per CU as of k_mass_units (unused LDS
+  // reserved for the purpose: the probe needs fewer registers)
+  size_t kt_lds = 0;
+  if (kind == FERRY_PROBE_KTAB_READ && g.dtype != FERRY_F32) {
+    const int per_cu = std::max(1, mass_units_resident(ctx) / std::max(1, ctx->cus));
+    kt_lds = (size_t)kGroupMaxLds / (size_t)per_cu / 256 * 256;
+  }
   const size_t words = kind == FERRY_PROBE_HBM_GATHER ? (size_t)n
                        : kind == FERRY_PROBE_KTAB_READ ? (size_t)(kt_grid * kt_w)
                                                        : (size_t)host_waves;
@@ -1624,14 +1730,16 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
       const dim3 grid((unsigned)kt_grid);
       const int nb = (int)n;
       if (g.dtype == FERRY_F32)
-        hipLaunchKernelGGL((k_probe_ktab<8, 4>), grid, dim3(256), 0, s, g, ctx->ktab,
+        hipLaunchKernelGGL((k_probe_ktab<8, 4, 4, 0>), grid, dim3(256), 0, s, g, ctx->ktab,
                            ctx->kt_records, nb, ctx->probe_sink);
       else if (g.dtype == FERRY_FP8_E4M3)
-        hipLaunchKernelGGL((k_probe_ktab<2, 8>), grid, dim3(512), 0, s, g, ctx->ktab,
-                           ctx->kt_records, nb, ctx->probe_sink);
+        hipLaunchKernelGGL((k_probe_ktab<2, kMassUnitWaves, kMassUnitInflight, 1>), grid,
+                           dim3(64 * kMassUnitWaves), kt_lds, s, g, ctx->ktab, ctx->kt_records, nb,
+                           ctx->probe_sink);
       else
-        hipLaunchKernelGGL((k_probe_ktab<4, 8>), grid, dim3(512), 0, s, g, ctx->ktab,
-                           ctx->kt_records, nb, ctx->probe_sink);
+        hipLaunchKernelGGL((k_probe_ktab<4, kMassUnitWaves, kMassUnitInflight, 1>), grid,
+                           dim3(64 * kMassUnitWaves), kt_lds, s, g, ctx->ktab, ctx->kt_records, nb,
+                           ctx->probe_sink);
       return hipGetLastError();
     }
     if (kind == FERRY_PROBE_HBM_COPY) {

@@ -710,9 +710,14 @@ __global__ __launch_bounds__(W * 64) void k_select_mass(Geo g, const float* __re
   }
 }
 
-// Matrix-core variant for 16-bit and fp8 K (the same contract and workspace
-// as k_select_mass).  Per block the scores of the G query heads are one
-// 16 x 16 tile on the matrix cores,
+// Matrix-core mass selection for 16-bit and fp8 K, in two launches.
+//
+// k_mass_units: one (request, layer, kv head) unit per workgroup pass, each
+// workgroup taking the next unit from a counter (k_mass_reset zeroes it before
+// the launch), so a grid of the workgroups the GPU holds at once drains the
+// units in order and evenly; the result does not depend on which workgroup
+// scores a unit.  Per block the scores of the G query heads are
+// one 16 x 16 tile on the matrix cores,
 //   S^T[16 tok][16 hd] = K[16 tok][128] . Q^T[128][16 hd]   (4 k-steps of 32),
 // with the heads padded to 16 columns, in the operand layout of k_attn_mfma:
 // lane l (n = l % 16, grp = l / 16) holds the 16-byte words 4 w + grp of
@@ -720,16 +725,26 @@ __global__ __launch_bounds__(W * 64) void k_select_mass(Geo g, const float* __re
 // record), the matching query dims of head n, and receives the
 // scores of tokens 4 grp + i (i < 4) of head n.  A block's (m_b, s_b) of head
 // n is then a 4-element max/sum in the lane and two cross-lane steps (xor 16,
-// 32).  The query, pre-scaled by log2(e) / sqrt(128), is split into NQ
-// operand-precision terms (fp16 hi + lo for fp16 and fp8 K, bf16 hi + mid +
-// lo for bf16 K) so the fp32 accumulation sees ~22-24 bits of it; fp8 K is
-// widened to fp16 exactly and its block scale multiplies the scores.
-template <int DT, int G, int W>
-__global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
+// 32); it goes to the workgroup's workspace slice and into the wavefront's
+// running (M, S).  Once (M, S) is merged over the workgroup (wavefront order),
+// block b's mass for this kv head, sum over its query heads of
+// exp2(m_b - M) s_b / S, goes to mass[unit][b].  The query, pre-scaled by
+// log2(e) / sqrt(128), is split into NQ operand-precision terms (fp16 hi + lo
+// for fp16 and fp8 K, bf16 hi + mid + lo for bf16 K) so the fp32 accumulation
+// sees ~22-24 bits of it; fp8 K is widened to fp16 exactly and its block scale
+// multiplies the scores.
+//
+// One kv head per workgroup streams one contiguous run of the K table (32 MiB
+// at 8192 blocks of 16-bit K): at the long-context GQA shape that measured
+// 0.80-0.84 of HBM (by where the 137 GB table landed) against 0.79 for a
+// whole (request, layer) item per workgroup, whose kv heads stream one after
+// the other.
+template <int DT, int G, int W, int U>
+__global__ __launch_bounds__(W * 64) void k_mass_units(
     Geo g, const float* __restrict__ q, const int32_t* __restrict__ ctx_blocks,
     const uint8_t* __restrict__ kt, const float* __restrict__ kt_scales, uint64_t kt_mod,
-    float* __restrict__ ws_all, uint32_t* __restrict__ sel, int l0, int nl, int max_n,
-    int* __restrict__ err) {
+    float* __restrict__ ws_all, float* __restrict__ mass, unsigned* __restrict__ counter, int l0,
+    int nl, int max_n, int* __restrict__ err) {
   static_assert(G >= 1 && G <= 16, "the score tile holds up to 16 query heads");
   static_assert(DT == FERRY_F16 || DT == FERRY_BF16 || DT == FERRY_FP8_E4M3, "16/8-bit K");
   typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -742,30 +757,173 @@ __global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
   constexpr int NKW = F8 ? 2 : 4;  // 16-byte K words per lane per block
   constexpr int EPW = 16 / ES, SUB = EPW / 8;
   constexpr int NQ = BF ? 3 : 2;   // query terms
-  constexpr int U = 4;             // blocks in flight per wavefront
-  extern __shared__ uint32_t lds[];
-  float* score = reinterpret_cast<float*>(lds);
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t wtot[2 * W];
-  __shared__ uint32_t sh[2];
   __shared__ float red_m[W][G], red_s[W][G], lse_m[G], lse_zi[G];
+  __shared__ unsigned next_unit;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, grp = lane >> 4;
   const bool head_lane = grp == 0 && n < G;
   float* ws = ws_all + (size_t)blockIdx.x * max_n * G * 2;
-  const int n_items = g.n_req * nl;
+  const unsigned n_units = (unsigned)(g.n_req * nl * g.Hkv);
   const float qmul = 1.4426950408889634f / sqrtf((float)D);  // log2(e) / sqrt(D)
 
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    __syncthreads();  // the previous item's top-k is done with the LDS
+  for (;;) {
+    // the previous unit is done with the LDS and the workspace slice
+    if (tid == 0) next_unit = atomicAdd(counter, 1u);
+    __syncthreads();
+    const unsigned un = next_unit;
+    __syncthreads();  // every thread has read next_unit before it is rewritten
+    if (un >= n_units) break;  // workgroup-uniform; every unit is taken once
+    const int unit = (int)un;
+    const int item = unit / g.Hkv, h = unit % g.Hkv;
     const int r = item / nl, l = l0 + item % nl;
     const int rl = r * g.L + l;
     int nb = ctx_blocks[r];
     if (nb < 0) nb = 0;
     if (nb > max_n || nb > g.max_blocks) {
-      if (tid == 0) set_error(err, FERRY_ERANGE);
+      if (tid == 0 && h == 0) set_error(err, FERRY_ERANGE);
       nb = 0;
     }
+    if (nb <= g.k) continue;  // workgroup-uniform: k_mass_topk lists every block
+    const uint64_t set = (uint64_t)rl * g.Hkv + h;
+    // ---- Q^T operand: k-step ks, this lane's 8 dims, head n (0 for pad heads)
+    uint32_t qb[NQ][4][4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int d0 = EPW * (4 * (ks / SUB) + grp) + 8 * (ks % SUB);
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        x[e] = n < G ? q[((size_t)rl * g.Hq + (size_t)(h * G + n)) * D + d0 + e] * qmul : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float a = x[e], b = x[e + 1];
+#pragma unroll
+        for (int t = 0; t < NQ; ++t) {
+          if constexpr (BF) {
+            const uint16_t ah = bf16_rne(a), bh = bf16_rne(b);
+            qb[t][ks][e / 2] = (uint32_t)ah | ((uint32_t)bh << 16);
+            a -= __builtin_bit_cast(float, (uint32_t)ah << 16);
+            b -= __builtin_bit_cast(float, (uint32_t)bh << 16);
+          } else {
+            const _Float16 ah = (_Float16)a, bh = (_Float16)b;
+            qb[t][ks][e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, ah) |
+                               ((uint32_t)__builtin_bit_cast(uint16_t, bh) << 16);
+            a -= (float)ah;
+            b -= (float)bh;
+          }
+        }
+      }
+    }
+    float run_m = -INFINITY, run_s = 0.0f;
+    for (int b0 = wave; b0 < nb; b0 += W * U) {
+      u32x4 kw[U][NKW];
+      float ksc[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int b = b0 + W * u;
+        if (b < nb) {  // wavefront-uniform
+          const uint64_t rec = host_index(set, (uint32_t)b, (uint64_t)g.max_blocks, kt_mod);
+          // lane-transposed record: this lane's word w is word 64 w + lane
+          const u32x4* base = reinterpret_cast<const u32x4*>(kt + rec * KT) + lane;
+#pragma unroll
+          for (int w = 0; w < NKW; ++w) kw[u][w] = __builtin_nontemporal_load(base + 64 * w);
+          ksc[u] = F8 ? kt_scales[rec] : 1.0f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int b = b0 + W * u;
+        if (b >= nb) break;  // wavefront-uniform
+        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const int w = ks / SUB, sub = ks % SUB;
+          u32x4 a;
+          if constexpr (F8) {
+            const mx_u32x2 lo = e4m3x4_to_f16(kw[u][w][2 * sub]);
+            const mx_u32x2 hi = e4m3x4_to_f16(kw[u][w][2 * sub + 1]);
+            a = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          } else {
+            a = kw[u][w];
+          }
+#pragma unroll
+          for (int t = 0; t < NQ; ++t) {
+            const u32x4 bq = {qb[t][ks][0], qb[t][ks][1], qb[t][ks][2], qb[t][ks][3]};
+            if constexpr (BF)
+              s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                          __builtin_bit_cast(bf16x8, bq), s, 0, 0, 0);
+            else
+              s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                         __builtin_bit_cast(f16x8, bq), s, 0, 0, 0);
+          }
+        }
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = s[i] * ksc[u];
+        float m = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        m = max_over_groups(m);
+        float e = (exp2f(x[0] - m) + exp2f(x[1] - m)) + (exp2f(x[2] - m) + exp2f(x[3] - m));
+        e = sum_over_groups(e);
+        if (head_lane) {
+          ws[((size_t)b * G + n) * 2] = m;
+          ws[((size_t)b * G + n) * 2 + 1] = e;
+          lse_merge(run_m, run_s, m, e);
+        }
+      }
+    }
+    // the workgroup's (M, S) of every query head
+    if (head_lane) {
+      red_m[wave][n] = run_m;
+      red_s[wave][n] = run_s;
+    }
+    __syncthreads();
+    if (tid < G) {
+      float mm = -INFINITY, ss = 0.0f;
+      for (int w = 0; w < W; ++w) lse_merge(mm, ss, red_m[w][tid], red_s[w][tid]);
+      lse_m[tid] = mm;
+      lse_zi[tid] = 1.0f / ss;
+    }
+    __syncthreads();
+    float* mrow = mass + (size_t)unit * max_n;
+    for (int b = tid; b < nb; b += NT) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int gq = 0; gq < G; ++gq)
+        acc += exp2f(ws[((size_t)b * G + gq) * 2] - lse_m[gq]) * ws[((size_t)b * G + gq) * 2 + 1] *
+               lse_zi[gq];
+      mrow[b] = acc;
+    }
+  }
+}
+
+__global__ void k_mass_reset(unsigned* counter) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *counter = 0u;
+}
+
+// k_mass_topk: one (request, layer) item per workgroup pass.  A block's score
+// is its mass summed over the kv heads in head order (mass[unit][b] of the
+// item's Hkv units, written by k_mass_units in the same stream); the scores go
+// through the same radix top-k as the Quest method and the item's list is
+// written to every kv head's row.  A context of at most k blocks lists every
+// block in order.  Dynamic LDS: max_n keys.
+template <int W>
+__global__ __launch_bounds__(W * 64) void k_mass_topk(Geo g, const int32_t* __restrict__ ctx_blocks,
+                                                      const float* __restrict__ mass,
+                                                      uint32_t* __restrict__ sel, int l0, int nl,
+                                                      int max_n) {
+  constexpr int NT = W * 64;
+  extern __shared__ uint32_t lds[];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wtot[2 * W];
+  __shared__ uint32_t sh[2];
+  const int tid = threadIdx.x;
+  const int n_items = g.n_req * nl;
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    __syncthreads();  // the previous item's top-k is done with the LDS
+    const int r = item / nl, l = l0 + item % nl;
+    const int rl = r * g.L + l;
+    int nb = ctx_blocks[r];
+    if (nb < 0 || nb > max_n || nb > g.max_blocks) nb = 0;  // k_mass_units latched the error
     const int k = g.k;
     const int kk = nb < k ? nb : k;
     uint32_t* out0 = sel + (size_t)rl * g.Hkv * (size_t)k;
@@ -774,118 +932,12 @@ __global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
         for (int hh = 0; hh < g.Hkv; ++hh) out0[(size_t)hh * k + j] = j < kk ? (uint32_t)j : kNone;
       continue;
     }
-    for (int h = 0; h < g.Hkv; ++h) {
-      const uint64_t set = (uint64_t)rl * g.Hkv + h;
-      // ---- Q^T operand: k-step ks, this lane's 8 dims, head n (0 for pad heads)
-      uint32_t qb[NQ][4][4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int d0 = EPW * (4 * (ks / SUB) + grp) + 8 * (ks % SUB);
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          x[e] = n < G ? q[((size_t)rl * g.Hq + (size_t)(h * G + n)) * D + d0 + e] * qmul : 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          float a = x[e], b = x[e + 1];
-#pragma unroll
-          for (int t = 0; t < NQ; ++t) {
-            if constexpr (BF) {
-              const uint16_t ah = bf16_rne(a), bh = bf16_rne(b);
-              qb[t][ks][e / 2] = (uint32_t)ah | ((uint32_t)bh << 16);
-              a -= __builtin_bit_cast(float, (uint32_t)ah << 16);
-              b -= __builtin_bit_cast(float, (uint32_t)bh << 16);
-            } else {
-              const _Float16 ah = (_Float16)a, bh = (_Float16)b;
-              qb[t][ks][e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, ah) |
-                                 ((uint32_t)__builtin_bit_cast(uint16_t, bh) << 16);
-              a -= (float)ah;
-              b -= (float)bh;
-            }
-          }
-        }
-      }
-      float run_m = -INFINITY, run_s = 0.0f;
-      for (int b0 = wave; b0 < nb; b0 += W * U) {
-        u32x4 kw[U][NKW];
-        float ksc[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int b = b0 + W * u;
-          if (b < nb) {  // wavefront-uniform
-            const uint64_t rec = host_index(set, (uint32_t)b, (uint64_t)g.max_blocks, kt_mod);
-            // lane-transposed record: this lane's word w is word 64 w + lane
-            const u32x4* base = reinterpret_cast<const u32x4*>(kt + rec * KT) + lane;
-#pragma unroll
-            for (int w = 0; w < NKW; ++w) kw[u][w] = __builtin_nontemporal_load(base + 64 * w);
-            ksc[u] = F8 ? kt_scales[rec] : 1.0f;
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int b = b0 + W * u;
-          if (b >= nb) break;  // wavefront-uniform
-          f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) {
-            const int w = ks / SUB, sub = ks % SUB;
-            u32x4 a;
-            if constexpr (F8) {
-              const mx_u32x2 lo = e4m3x4_to_f16(kw[u][w][2 * sub]);
-              const mx_u32x2 hi = e4m3x4_to_f16(kw[u][w][2 * sub + 1]);
-              a = u32x4{lo[0], lo[1], hi[0], hi[1]};
-            } else {
-              a = kw[u][w];
-            }
-#pragma unroll
-            for (int t = 0; t < NQ; ++t) {
-              const u32x4 bq = {qb[t][ks][0], qb[t][ks][1], qb[t][ks][2], qb[t][ks][3]};
-              if constexpr (BF)
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                            __builtin_bit_cast(bf16x8, bq), s, 0, 0, 0);
-              else
-                s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                           __builtin_bit_cast(f16x8, bq), s, 0, 0, 0);
-            }
-          }
-          float x[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] = s[i] * ksc[u];
-          float m = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-          m = max_over_groups(m);
-          float e = (exp2f(x[0] - m) + exp2f(x[1] - m)) + (exp2f(x[2] - m) + exp2f(x[3] - m));
-          e = sum_over_groups(e);
-          if (head_lane) {
-            ws[((size_t)b * G + n) * 2] = m;
-            ws[((size_t)b * G + n) * 2 + 1] = e;
-            lse_merge(run_m, run_s, m, e);
-          }
-        }
-      }
-      // the workgroup's (M, S) of every query head
-      if (head_lane) {
-        red_m[wave][n] = run_m;
-        red_s[wave][n] = run_s;
-      }
-      __syncthreads();
-      if (tid < G) {
-        float mm = -INFINITY, ss = 0.0f;
-        for (int w = 0; w < W; ++w) lse_merge(mm, ss, red_m[w][tid], red_s[w][tid]);
-        lse_m[tid] = mm;
-        lse_zi[tid] = 1.0f / ss;
-      }
-      __syncthreads();
-      for (int b = tid; b < nb; b += NT) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int gq = 0; gq < G; ++gq)
-          acc += exp2f(ws[((size_t)b * G + gq) * 2] - lse_m[gq]) * ws[((size_t)b * G + gq) * 2 + 1] *
-                 lse_zi[gq];
-        score[b] = h == 0 ? acc : score[b] + acc;
-      }
-      __syncthreads();
+    const float* m0 = mass + (size_t)item * g.Hkv * max_n;
+    for (int b = tid; b < nb; b += NT) {
+      float s = m0[b];
+      for (int hh = 1; hh < g.Hkv; ++hh) s += m0[(size_t)hh * max_n + b];
+      lds[b] = fkey(s);
     }
-    for (int b = tid; b < nb; b += NT) lds[b] = fkey(score[b]);
     __syncthreads();
     topk_ascending<W>(lds, nb, kk, hist, wtot, sh, out0, g.Hkv, (size_t)k);
     for (int j = kk + tid; j < k; j += NT)
@@ -897,22 +949,24 @@ __global__ __launch_bounds__(W * 64) void k_select_mass_mfma(
   template __global__ void k_select_mass<DT, G, 4>(Geo, const float*, const int32_t*,              \
                                                    const uint8_t*, const float*, uint64_t, float*, \
                                                    uint32_t*, int, int, int, int*);
-#define FERRY_MASS_MFMA_INST(DT, G)                                                               \
-  template __global__ void k_select_mass_mfma<DT, G, 8>(Geo, const float*, const int32_t*,         \
-                                                        const uint8_t*, const float*, uint64_t,    \
-                                                        float*, uint32_t*, int, int, int, int*);
-#define FERRY_MASS_MFMA_INST_G(DT) \
-  FERRY_MASS_MFMA_INST(DT, 1)      \
-  FERRY_MASS_MFMA_INST(DT, 2)      \
-  FERRY_MASS_MFMA_INST(DT, 4)      \
-  FERRY_MASS_MFMA_INST(DT, 8)
+#define FERRY_MASS_UNITS_INST(DT, G)                                                          \
+  template __global__ void k_mass_units<DT, G, kMassUnitWaves, kMassUnitInflight>(            \
+      Geo, const float*, const int32_t*, const uint8_t*, const float*, uint64_t, float*, float*, \
+      unsigned*, int, int, int, int*);
+#define FERRY_MASS_UNITS_INST_G(DT) \
+  FERRY_MASS_UNITS_INST(DT, 1)      \
+  FERRY_MASS_UNITS_INST(DT, 2)      \
+  FERRY_MASS_UNITS_INST(DT, 4)      \
+  FERRY_MASS_UNITS_INST(DT, 8)
 FERRY_MASS_INST(FERRY_F32, 1)
 FERRY_MASS_INST(FERRY_F32, 2)
 FERRY_MASS_INST(FERRY_F32, 4)
 FERRY_MASS_INST(FERRY_F32, 8)
-FERRY_MASS_MFMA_INST_G(FERRY_F16)
-FERRY_MASS_MFMA_INST_G(FERRY_BF16)
-FERRY_MASS_MFMA_INST_G(FERRY_FP8_E4M3)
+FERRY_MASS_UNITS_INST_G(FERRY_F16)
+FERRY_MASS_UNITS_INST_G(FERRY_BF16)
+FERRY_MASS_UNITS_INST_G(FERRY_FP8_E4M3)
+template __global__ void k_mass_topk<kMassTopkWaves>(Geo, const int32_t*, const float*, uint32_t*, int,
+                                                     int, int);
 template __global__ void k_ktiles_build<2>(Geo, const uint8_t*, const float*, uint8_t*, float*, int);
 template __global__ void k_ktiles_build<4>(Geo, const uint8_t*, const float*, uint8_t*, float*, int);
 template __global__ void k_ktiles_build<8>(Geo, const uint8_t*, const float*, uint8_t*, float*, int);

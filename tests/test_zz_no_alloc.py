@@ -1,8 +1,11 @@
 """ferry_select_mass_noalloc, the entry point that allocates nothing: the mass
-selection with its per-workgroup (max, sum) workspace in the library's static
-per-GPU array instead of the context's, through the C-ABI.  Its page lists
-must equal ferry_select_mass's bit for bit (same kernels, same arithmetic per
-(request, layer) item, only fewer workgroups sharing the items) on two calls
+selection with its workspace (per-workgroup (max, sum) slices and, for 16-bit
+and fp8 K, the per-kv-head block masses) in the library's static per-GPU array
+instead of the context's, through the C-ABI.  Its page lists must equal
+ferry_select_mass's bit for bit (same kernels, same arithmetic per (request,
+layer, kv head) unit and (request, layer) item, only fewer workgroups sharing
+the work and, where the masses of every layer do not fit, layer ranges run one
+after the other) on two calls
 in a row, the second with smaller inputs, which finds the first call's data
 still in the shared array, and on a second, smaller executor on the same
 GPU.  It is collected last: it must pass alone in a fresh process and after
@@ -62,6 +65,24 @@ def test_noalloc_select_mass_equals_select_mass(dtype, Hkv, Hq):
     a3, b3 = _both(ex2, q3, ctx3, (2, 2, Hkv, 16))
     assert np.array_equal(a3, b3)
     ex2.close()
+
+
+def test_noalloc_select_mass_layer_ranges():
+    # the per-kv-head masses of all 12 layers (16 x 12 x 8 x 15360 floats, 94 MB)
+    # exceed the 64 MiB array: the call runs layer ranges one after the other
+    B, L, Hkv, Hq, k, mb = 16, 12, 8, 16, 32, 15360
+    print(f"[noalloc] layer ranges: bf16 B={B} L={L} Hkv={Hkv} Hq={Hq} k={k} max_blocks={mb}",
+          flush=True)
+    assert B * L * Hkv * mb * 4 > 64 << 20 and B * Hkv * mb * 4 < 64 << 20
+    ex = _exec(B, L, Hkv, Hq, k, mb, F.BF16)
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((B, L, Hq, 128)).astype(np.float32)
+    ctx = rng.integers(k + 1, 1500, B).astype(np.int32)
+    ctx[0], ctx[1] = mb, k - 3
+    a, b = _both(ex, q, ctx, (B, L, Hkv, k))
+    assert np.array_equal(a, b)
+    assert np.all(a[2:, ..., :k] >= 0) and np.all(a[1, ..., k - 3:] == -1)
+    ex.close()
 
 
 def test_noalloc_select_mass_refusals():
