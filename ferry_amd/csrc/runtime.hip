@@ -1306,9 +1306,12 @@ int mass_units_resident(ferry_ctx* ctx) {
   else FERRY_MASS_FN(FERRY_FP8_E4M3);
 #undef FERRY_MASS_FN
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * kMassUnitWaves, 0) != hipSuccess ||
-      per_cu < 1)
-    per_cu = 1;
+  if (hipSetDevice(ctx->device) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * kMassUnitWaves, 0) != hipSuccess ||
+      per_cu < 1) {
+    (void)hipGetLastError();
+    per_cu = 1;  // still correct: the workgroups take the units from the counter
+  }
   ctx->mass_resident = per_cu * ctx->cus;
   return ctx->mass_resident;
 }
