@@ -131,6 +131,7 @@ struct ferry_ctx {
   int attn_waves = 0;              // wavefronts per attention workgroup (FERRY_ATTN_WAVES), 0 = default
   int cus = 256;                   // compute units of the device
   int mass_resident = 0;           // k_mass_units workgroups resident at once (0: not yet asked)
+  int mass_lds = -1;               // k_mass_units keeps block log-sums in LDS (-1: not yet decided)
   int group_waves_env = 0;         // prefix-group kernel wavefronts (FERRY_GROUP_WAVES=4|8), 0 = by launch
   int fetch_waves = 0;             // wavefronts per fetch workgroup (FERRY_FETCH_WAVES: 1, 2, 4; 0 = by rule)
   int fetch_prio = 1;              // fetch wavefronts issue first (FERRY_FETCH_PRIO=0: not)
@@ -1283,9 +1284,31 @@ constexpr uint64_t kMassLds = 60 * 1024;
 
 namespace {
 
-// One workgroup's workspace slice of the mass selection: a (max, sum) pair per
-// context block and query head.
-uint64_t mass_slice_bytes(const Geo& g) {
+// Whether k_mass_units keeps its per-block log-sums in LDS: 16-bit K whose
+// max_blocks * G floats fit kMassLdsWs (FERRY_MASS_WS=hbm keeps the HBM
+// workspace).  At the long-context GQA shape the LDS copy measured 0.86-0.88
+// of HBM against 0.80-0.84 for bf16 and 0.86 against 0.80 for fp16; fp8 K
+// (2 KiB records, twice the arithmetic per byte) measured 0.69 against 0.77,
+// the LDS leaving one workgroup per CU instead of two, so it keeps HBM.
+constexpr uint64_t kMassLdsWs = 144 * 1024;
+bool mass_in_lds(ferry_ctx* ctx) {
+  if (ctx->mass_lds < 0) {
+    const Geo& g = ctx->g;
+    const char* e = std::getenv("FERRY_MASS_WS");
+    ctx->mass_lds = (g.dtype == FERRY_F16 || g.dtype == FERRY_BF16) && !(e && std::string(e) == "hbm") &&
+                    (uint64_t)g.max_blocks * (uint64_t)(g.Hq / g.Hkv) * 4 <= kMassLdsWs;
+  }
+  return ctx->mass_lds != 0;
+}
+size_t mass_lds_bytes(ferry_ctx* ctx) {
+  return mass_in_lds(ctx) ? (size_t)ctx->g.max_blocks * (size_t)(ctx->g.Hq / ctx->g.Hkv) * 4 : 0;
+}
+
+// One workgroup's workspace slice of the mass selection in HBM: a (max, sum)
+// pair per context block and query head (none when the log-sums stay in LDS).
+uint64_t mass_slice_bytes(ferry_ctx* ctx) {
+  const Geo& g = ctx->g;
+  if (g.dtype != FERRY_F32 && mass_in_lds(ctx)) return 0;
   return (uint64_t)g.max_blocks * (uint64_t)(g.Hq / g.Hkv) * 2 * sizeof(float);
 }
 
@@ -1306,8 +1329,10 @@ int mass_units_resident(ferry_ctx* ctx) {
   else FERRY_MASS_FN(FERRY_FP8_E4M3);
 #undef FERRY_MASS_FN
   int per_cu = 0;
+  const size_t lds = mass_lds_bytes(ctx);
+  if (lds > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMassLdsWs);
   if (hipSetDevice(ctx->device) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * kMassUnitWaves, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * kMassUnitWaves, lds) != hipSuccess ||
       per_cu < 1) {
     (void)hipGetLastError();
     per_cu = 1;  // still correct: the workgroups take the units from the counter
@@ -1334,12 +1359,13 @@ uint64_t mass_wgs(ferry_ctx* ctx, int nl, uint64_t cap) {
 // slices a float mass per context block of every (request, layer, kv head)
 // unit, 256-byte aligned.
 constexpr uint64_t kMassCounterBytes = 256;
-uint64_t mass_mass_offset(const Geo& g, uint64_t wgs) {
-  return kMassCounterBytes + (wgs * mass_slice_bytes(g) + 255) / 256 * 256;
+uint64_t mass_mass_offset(ferry_ctx* ctx, uint64_t wgs) {
+  return kMassCounterBytes + (wgs * mass_slice_bytes(ctx) + 255) / 256 * 256;
 }
-uint64_t mass_ws_bytes(const Geo& g, int nl, uint64_t wgs) {
-  if (g.dtype == FERRY_F32) return wgs * mass_slice_bytes(g);
-  return mass_mass_offset(g, wgs) + (uint64_t)g.n_req * nl * g.Hkv * g.max_blocks * sizeof(float);
+uint64_t mass_ws_bytes(ferry_ctx* ctx, int nl, uint64_t wgs) {
+  const Geo& g = ctx->g;
+  if (g.dtype == FERRY_F32) return wgs * mass_slice_bytes(ctx);
+  return mass_mass_offset(ctx, wgs) + (uint64_t)g.n_req * nl * g.Hkv * g.max_blocks * sizeof(float);
 }
 
 }  // namespace
@@ -1368,7 +1394,7 @@ int ferry_ktiles_build(ferry_ctx* ctx, uint64_t n_records, void* stream) {
     ctx->kt_records = S;
   }
   if (!ctx->mass_ws && (uint64_t)g.max_blocks * 4 <= kMassLds)
-    HIPC(hipMalloc(&ctx->mass_ws, mass_ws_bytes(g, g.L, mass_wgs(ctx, g.L, ~0ull))));
+    HIPC(hipMalloc(&ctx->mass_ws, mass_ws_bytes(ctx, g.L, mass_wgs(ctx, g.L, ~0ull))));
   ctx->kt_perm = g.dtype != FERRY_F32;
   const unsigned blocks = (unsigned)std::min<uint64_t>((g.host_blocks + 3) / 4, 16384);
   switch (KT / 1024) {
@@ -1402,7 +1428,7 @@ int ferry_ktiles_view(ferry_ctx* ctx, void** ktiles, float** scales, uint64_t* n
 namespace {
 
 // The mass selection of layers [l0, l0 + nl) with `wgs` workgroups
-// (mass_wgs) and workspace `ws` of mass_ws_bytes(g, nl, wgs).
+// (mass_wgs) and workspace `ws` of mass_ws_bytes(ctx, nl, wgs).
 int launch_select_mass(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
                        const int32_t* ctx_blocks, uint32_t* sel, void* stream, float* ws,
                        uint64_t wgs) {
@@ -1428,13 +1454,14 @@ int launch_select_mass(ferry_ctx* ctx, int32_t l0, int32_t nl, const float* q,
   }
   // matrix cores: the units' masses, then each item's sum over kv heads and top k
   unsigned* counter = reinterpret_cast<unsigned*>(ws);
-  float* slices = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + kMassCounterBytes);
-  float* mass = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + mass_mass_offset(g, wgs));
+  const size_t ulds = mass_lds_bytes(ctx);  // block log-sums in LDS, else HBM slices
+  float* slices = ulds ? nullptr : reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + kMassCounterBytes);
+  float* mass = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + mass_mass_offset(ctx, wgs));
   hipLaunchKernelGGL(k_mass_reset, dim3(1), dim3(64), 0, s, counter);
   HIPC(hipGetLastError());
 #define FERRY_MASS_UNITS(DT, GG)                                                                 \
   hipLaunchKernelGGL((k_mass_units<DT, GG, kMassUnitWaves, kMassUnitInflight>), dim3((unsigned)wgs), \
-                     dim3(64 * kMassUnitWaves), 0, s, g, q, ctx_blocks, ctx->ktab, ctx->ktab_scales,  \
+                     dim3(64 * kMassUnitWaves), ulds, s, g, q, ctx_blocks, ctx->ktab, ctx->ktab_scales, \
                      ctx->kt_records, slices, mass, counter, l0, nl, g.max_blocks, ctx->err)
 #define FERRY_MASS_UNITS_G(DT)                \
   switch (G) {                                \
@@ -1501,16 +1528,17 @@ int ferry_select_mass_noalloc(ferry_ctx* ctx, const float* q, const int32_t* ctx
   // the largest layer range whose workspace (the masses of its units, 16-bit
   // and fp8 K) leaves room in the static array for at least one workgroup
   // slice; ranges run one after the other on the stream
-  const uint64_t slice = mass_slice_bytes(g);
+  const uint64_t slice = mass_slice_bytes(ctx);
   auto wgs_cap = [&](int n) -> uint64_t {
-    const uint64_t fixed = mass_ws_bytes(g, n, 0) + 256;
-    return fixed + slice <= kNoAllocScratchBytes ? (kNoAllocScratchBytes - fixed) / slice : 0;
+    const uint64_t fixed = mass_ws_bytes(ctx, n, 0) + 256;
+    if (fixed + slice > kNoAllocScratchBytes) return 0;
+    return slice ? (kNoAllocScratchBytes - fixed) / slice : ~0ull;
   };
   int nl = g.L;
   while (nl > 0 && wgs_cap(nl) == 0) --nl;
   if (nl == 0)
     return fail(FERRY_EINVAL, "ferry_select_mass_noalloc: the workspace of one layer (" +
-                                  std::to_string(mass_ws_bytes(g, 1, 1)) +
+                                  std::to_string(mass_ws_bytes(ctx, 1, 1)) +
                                   " B) exceeds the static scratch of " +
                                   std::to_string(kNoAllocScratchBytes) + " B");
   for (int l0 = 0; l0 < g.L; l0 += nl) {

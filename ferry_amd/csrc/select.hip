@@ -725,10 +725,14 @@ __global__ __launch_bounds__(W * 64) void k_select_mass(Geo g, const float* __re
 // record), the matching query dims of head n, and receives the
 // scores of tokens 4 grp + i (i < 4) of head n.  A block's (m_b, s_b) of head
 // n is then a 4-element max/sum in the lane and two cross-lane steps (xor 16,
-// 32); it goes to the workgroup's workspace slice and into the wavefront's
-// running (M, S).  Once (M, S) is merged over the workgroup (wavefront order),
-// block b's mass for this kv head, sum over its query heads of
-// exp2(m_b - M) s_b / S, goes to mass[unit][b].  The query, pre-scaled by
+// 32); it goes into the wavefront's running (M, S) and is kept for the last
+// pass: as l_b = m_b + log2(s_b) in LDS when max_n * G floats fit there
+// (ws_all null), else as (m_b, s_b) in the workgroup's workspace slice in
+// HBM.  Once (M, S) is merged over the workgroup (wavefront order), block b's
+// mass for this kv head, sum over its query heads of exp2(l_b - M - log2 S)
+// (or exp2(m_b - M) s_b / S), goes to mass[unit][b].  At the long-context GQA
+// shape the round trip through HBM made the launch 0.80 or 0.84 of HBM by
+// where the K table landed, and dropping it 0.85-0.86 wherever it did.  The query, pre-scaled by
 // log2(e) / sqrt(128), is split into NQ operand-precision terms (fp16 hi + lo
 // for fp16 and fp8 K, bf16 hi + mid + lo for bf16 K) so the fp32 accumulation
 // sees ~22-24 bits of it; fp8 K is widened to fp16 exactly and its block scale
@@ -757,12 +761,14 @@ __global__ __launch_bounds__(W * 64) void k_mass_units(
   constexpr int NKW = F8 ? 2 : 4;  // 16-byte K words per lane per block
   constexpr int EPW = 16 / ES, SUB = EPW / 8;
   constexpr int NQ = BF ? 3 : 2;   // query terms
-  __shared__ float red_m[W][G], red_s[W][G], lse_m[G], lse_zi[G];
+  __shared__ float red_m[W][G], red_s[W][G], lse_m[G], lse_zi[G], lse_l[G];
   __shared__ unsigned next_unit;
+  extern __shared__ float lws[];  // [max_n][G] block log-sums when ws_all is null
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, grp = lane >> 4;
   const bool head_lane = grp == 0 && n < G;
-  float* ws = ws_all + (size_t)blockIdx.x * max_n * G * 2;
+  const bool in_lds = ws_all == nullptr;  // workgroup-uniform
+  float* ws = in_lds ? nullptr : ws_all + (size_t)blockIdx.x * max_n * G * 2;
   const unsigned n_units = (unsigned)(g.n_req * nl * g.Hkv);
   const float qmul = 1.4426950408889634f / sqrtf((float)D);  // log2(e) / sqrt(D)
 
@@ -865,8 +871,12 @@ __global__ __launch_bounds__(W * 64) void k_mass_units(
         float e = (exp2f(x[0] - m) + exp2f(x[1] - m)) + (exp2f(x[2] - m) + exp2f(x[3] - m));
         e = sum_over_groups(e);
         if (head_lane) {
-          ws[((size_t)b * G + n) * 2] = m;
-          ws[((size_t)b * G + n) * 2 + 1] = e;
+          if (in_lds) {
+            lws[b * G + n] = m + log2f(e);  // the block's log2-sum-exp2
+          } else {
+            ws[((size_t)b * G + n) * 2] = m;
+            ws[((size_t)b * G + n) * 2 + 1] = e;
+          }
           lse_merge(run_m, run_s, m, e);
         }
       }
@@ -882,15 +892,21 @@ __global__ __launch_bounds__(W * 64) void k_mass_units(
       for (int w = 0; w < W; ++w) lse_merge(mm, ss, red_m[w][tid], red_s[w][tid]);
       lse_m[tid] = mm;
       lse_zi[tid] = 1.0f / ss;
+      lse_l[tid] = mm + log2f(ss);  // the unit's log2-sum-exp2
     }
     __syncthreads();
     float* mrow = mass + (size_t)unit * max_n;
     for (int b = tid; b < nb; b += NT) {
       float acc = 0.0f;
+      if (in_lds) {
 #pragma unroll
-      for (int gq = 0; gq < G; ++gq)
-        acc += exp2f(ws[((size_t)b * G + gq) * 2] - lse_m[gq]) * ws[((size_t)b * G + gq) * 2 + 1] *
-               lse_zi[gq];
+        for (int gq = 0; gq < G; ++gq) acc += exp2f(lws[b * G + gq] - lse_l[gq]);
+      } else {
+#pragma unroll
+        for (int gq = 0; gq < G; ++gq)
+          acc += exp2f(ws[((size_t)b * G + gq) * 2] - lse_m[gq]) * ws[((size_t)b * G + gq) * 2 + 1] *
+                 lse_zi[gq];
+      }
       mrow[b] = acc;
     }
   }

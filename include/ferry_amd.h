@@ -375,11 +375,12 @@ int ferry_select_topk_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float
  * only; max_blocks <= 15360 (one score per block in LDS).  A context longer
  * than max_blocks latches FERRY_ERANGE and leaves that row EMPTY.
  * The table is a snapshot of the host tier: rebuild it after the tier's
- * content changes.  The selection keeps each block's softmax max and sum, and
- * (16-bit and fp8 K) each block's mass per kv head, in a workspace of the
- * context allocated by ferry_ktiles_build (for 16-bit and fp8 K about
- * n_req * L * kv_heads * max_blocks * 4 bytes), so two ferry_select_mass calls
- * on one context must not run concurrently. */
+ * content changes.  The selection keeps each block's mass per kv head (16-bit
+ * and fp8 K, about n_req * L * kv_heads * max_blocks * 4 bytes) and, for fp32
+ * and fp8 K or where max_blocks * q_heads / kv_heads floats exceed 144 KiB of
+ * LDS, each block's softmax max and sum in a workspace of the context
+ * allocated by ferry_ktiles_build, so two ferry_select_mass calls on one
+ * context must not run concurrently. */
 int ferry_ktiles_build(ferry_ctx* ctx, uint64_t n_records, void* stream);
 int ferry_ktiles_view(ferry_ctx* ctx, void** ktiles, float** scales, uint64_t* n_records);
 int ferry_select_mass(ferry_ctx* ctx, const float* q, const int32_t* ctx_blocks, uint32_t* sel,
@@ -393,8 +394,9 @@ int ferry_select_mass_layers(ferry_ctx* ctx, int32_t l0, int32_t nl, const float
  * memory -- code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc.  It calls no hipMalloc/hipFree.  Needs the K table
  * (ferry_ktiles_build, which the caller runs beforehand) and, within the
- * 64 MiB, one workgroup's workspace slice, max_blocks * (q_heads / kv_heads)
- * * 8 bytes, plus for 16-bit and fp8 K the masses of one layer,
+ * 64 MiB, one workgroup's workspace slice where the softmax max and sum stay
+ * in HBM (see ferry_select_mass), max_blocks * (q_heads / kv_heads) * 8
+ * bytes, plus for 16-bit and fp8 K the masses of one layer,
  * n_req * kv_heads * max_blocks * 4 bytes, and 512 bytes (FERRY_EINVAL
  * otherwise).  The layers run in ranges one after the other when the masses
  * of all of them do not fit, and fewer workgroups share the work when the
