@@ -126,6 +126,24 @@ def test_select_mass_parity(dtype, Hkv, Hq):
     assert p.ex.stats()["device_error"] == 0
 
 
+@pytest.mark.parametrize("dtype,Hkv,Hq", [(F.F16, 2, 2), (F.BF16, 2, 8)])
+def test_select_mass_hbm_workspace_parity(dtype, Hkv, Hq, monkeypatch):
+    # 16-bit K keeps each block's log-sum in LDS; FERRY_MASS_WS=hbm (read when the
+    # K table is built) keeps the (max, sum) pairs in the context's HBM workspace
+    monkeypatch.setenv("FERRY_MASS_WS", "hbm")
+    n_req, L, k, mb = 6, 2, 16, 300
+    print(f"[mass] HBM workspace dtype={dtype} Hkv={Hkv} Hq={Hq}", flush=True)
+    p = Pair(n_req, L, Hkv, Hq, k, 64, mb, dtype, host_blocks=4099)
+    p.ex.ktiles_build()
+    rng = np.random.default_rng(dtype * 11 + Hq)
+    ctx = np.array([300, 9, 0, 16, 17, 211], np.int32)
+    q = rng.standard_normal((n_req, L, Hq, 128)).astype(np.float32)
+    frac = _check_rows(p, _run(p, q, ctx), q, ctx)
+    print("[mass] exact rows", frac, flush=True)
+    assert frac >= 0.9
+    assert p.ex.stats()["device_error"] == 0
+
+
 @pytest.mark.parametrize("dtype", [F.F16, F.FP8])
 def test_zero_query_takes_the_lowest_ids(dtype):
     """q = 0: every token gets probability 1/(16 ctx), every block the same
