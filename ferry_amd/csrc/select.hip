@@ -243,18 +243,23 @@ __global__ __launch_bounds__(256) void k_summaries_tile(uint8_t* __restrict__ su
 // LDS read is a contiguous 64-key row (one key per lane, no bank conflicts).
 // (Per-thread chunks of n / 256 keys read 64 words one chunk apart per
 // instruction, all in one bank; the Quest launch at 128K-token contexts is
-// 2.51-2.55 ms with these two steps against 2.53-2.56 ms.)  hist: 256 LDS
-// words, wtot: 2 W, sh: 2.  Every thread must call it.
-template <int W>
+// 2.51-2.55 ms with these two steps against 2.53-2.56 ms.)  With HIST1 the
+// caller has counted the top bytes into hist while writing the keys.  A pass
+// whose bin holds exactly the keys still needed ends the search: every key
+// with that prefix is taken, so phase 2 compares the masked keys.  hist: 256
+// LDS words, wtot: 2 W, sh: 3.  Every thread must call it.
+template <int W, bool HIST1 = false>
 __device__ void topk_ascending(const uint32_t* keys, int n, int kk, uint32_t* hist, uint32_t* wtot,
                                uint32_t* sh, uint32_t* out, int nrows, size_t row_stride) {
   constexpr int NT = W * 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint32_t prefix = 0, mask = 0, need = (uint32_t)kk;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = tid; i < 256; i += NT) hist[i] = 0;
-    __syncthreads();
-    for (int i0 = 64 * wave; i0 < n; i0 += NT) {
+    if (!HIST1 || shift != 24) {
+      for (int i = tid; i < 256; i += NT) hist[i] = 0;
+      __syncthreads();
+    }
+    for (int i0 = 64 * wave; (!HIST1 || shift != 24) && i0 < n; i0 += NT) {
       const int i = i0 + lane;
       const uint32_t key = i < n ? keys[i] : 0u;
       const bool valid = i < n && (key & mask) == prefix;
@@ -289,6 +294,7 @@ __device__ void topk_ascending(const uint32_t* keys, int n, int kk, uint32_t* hi
           if (acc + c[e] >= need && acc < need) {
             sh[0] = prefix | ((uint32_t)(255 - 4 * lane - e) << shift);
             sh[1] = need - acc;
+            sh[2] = acc + c[e] == need;
           }
           acc += c[e];
         }
@@ -298,6 +304,7 @@ __device__ void topk_ascending(const uint32_t* keys, int n, int kk, uint32_t* hi
     prefix = sh[0];
     need = sh[1];
     mask |= 0xFFu << shift;
+    if (sh[2]) break;
   }
   const uint32_t T = prefix;
   const int span = ((n + NT - 1) / NT) * 64;
@@ -305,7 +312,7 @@ __device__ void topk_ascending(const uint32_t* keys, int n, int kk, uint32_t* hi
   uint32_t gt = 0, eq = 0;
   for (int i0 = w0; i0 < w1; i0 += 64) {
     const int i = i0 + lane;
-    const uint32_t key = i < w1 ? keys[i] : 0u;
+    const uint32_t key = i < w1 ? keys[i] & mask : 0u;
     gt += (uint32_t)__builtin_popcountll(ballot(i < w1 && key > T));
     eq += (uint32_t)__builtin_popcountll(ballot(i < w1 && key == T));
   }
@@ -322,7 +329,7 @@ __device__ void topk_ascending(const uint32_t* keys, int n, int kk, uint32_t* hi
   uint32_t pos = gt_before + min(ties, need);
   for (int i0 = w0; i0 < w1; i0 += 64) {
     const int i = i0 + lane;
-    const uint32_t key = i < w1 ? keys[i] : 0u;
+    const uint32_t key = i < w1 ? keys[i] & mask : 0u;
     const bool is_eq = i < w1 && key == T;
     const uint64_t eqm = ballot(is_eq);
     const bool take = (i < w1 && key > T) || (is_eq && ties + (uint32_t)lanes_below(eqm) < need);
@@ -356,7 +363,7 @@ __global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __re
   extern __shared__ uint32_t lds[];
   __shared__ uint32_t hist[256];
   __shared__ uint32_t wtot[2 * W];
-  __shared__ uint32_t sh[2];
+  __shared__ uint32_t sh[3];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nkv = LAYER ? g.Hkv : 1;  // kv heads scored per row
   const int Gq = G * nkv;             // query heads per row
@@ -378,8 +385,10 @@ __global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __re
   auto out_row = [&](int hh) { return sel + ((size_t)rl * g.Hkv + hh) * (size_t)k; };
 
   if (n > k) {
-    // ---- phase 1: scores
+    // ---- phase 1: scores, and the top-k's first radix pass (the keys' top
+    // bytes counted as they are written, while the loads stream)
     const int grp = lane >> 4, p = lane & 15;
+    for (int i = tid; i < 256; i += NT) hist[i] = 0;
     // the row's query dims of this lane (8 per head), and whether each uses kmax
     float qr[G][8];
     if (!LAYER) {
@@ -388,6 +397,7 @@ __global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __re
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           qr[gq][e] = q[((size_t)rl * g.Hq + (size_t)(hrow * G + gq)) * D + 8 * p + e];
+      __syncthreads();
     } else {
       for (int i = tid; i < Gq * D; i += NT) qs[i] = q[(size_t)rl * g.Hq * D + i];
       __syncthreads();
@@ -435,12 +445,16 @@ __global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __re
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int b = b0 + 4 * W * u + grp;
-        if (b < n && p == 0) keys[b] = fkey(score[u]);
+        if (b < n && p == 0) {
+          const uint32_t key = fkey(score[u]);
+          keys[b] = key;
+          atomicAdd(&hist[key >> 24], 1u);
+        }
       }
     }
     __syncthreads();
-    topk_ascending<W>(keys, n, kk, hist, wtot, sh, out_row(LAYER ? 0 : hrow), LAYER ? g.Hkv : 1,
-                      (size_t)k);
+    topk_ascending<W, true>(keys, n, kk, hist, wtot, sh, out_row(LAYER ? 0 : hrow),
+                            LAYER ? g.Hkv : 1, (size_t)k);
   } else {
     // a context of at most k blocks: every block, in order
     for (int j = tid; j < kk; j += NT)
@@ -576,7 +590,7 @@ __global__ __launch_bounds__(W * 64) void k_select_mass(Geo g, const float* __re
   float* score = reinterpret_cast<float*>(lds);
   __shared__ uint32_t hist[256];
   __shared__ uint32_t wtot[2 * W];
-  __shared__ uint32_t sh[2];
+  __shared__ uint32_t sh[3];
   __shared__ float xl[W][XW];
   __shared__ float red_m[NE], red_s[NE], lse_m[G], lse_zi[G];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -935,7 +949,7 @@ __global__ __launch_bounds__(W * 64) void k_mass_topk(Geo g, const int32_t* __re
   extern __shared__ uint32_t lds[];
   __shared__ uint32_t hist[256];
   __shared__ uint32_t wtot[2 * W];
-  __shared__ uint32_t sh[2];
+  __shared__ uint32_t sh[3];
   const int tid = threadIdx.x;
   const int n_items = g.n_req * nl;
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
