@@ -45,6 +45,7 @@ ASSIGN_SPREAD, ASSIGN_AFFINITY = 0, 1
 ATTN_AUTO, ATTN_VALU, ATTN_MFMA, ATTN_GROUP = 0, 1, 2, 3
 CAP_GROUP, CAP_PER_MEMBER = 0, 1
 PROBE_HBM_GATHER, PROBE_HOST_READ, PROBE_HOST_DMA, PROBE_HBM_COPY, PROBE_KTAB_READ = 0, 1, 2, 3, 4
+PROBE_SUMS_READ = 5
 ARRIVAL_STEADY, ARRIVAL_BURSTY, ARRIVAL_POISSON, ARRIVAL_MMPP = 0, 1, 2, 3
 EMPTY = 0xFFFFFFFF  # selection id of an empty position (and its slot)
 SCHED_FIFO, SCHED_PINNED = 0, 1

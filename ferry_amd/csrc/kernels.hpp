@@ -164,6 +164,8 @@ template <int NV>
 __global__ void k_probe_copy(const uint8_t* src, uint8_t* dst, uint64_t bb, uint64_t n_blocks);
 template <int NI, int W, int U, int UNITS>
 __global__ void k_probe_ktab(Geo g, const uint8_t* kt, uint64_t kt_mod, int nb, uint32_t* sink);
+template <int ES, int U>
+__global__ void k_probe_sums(Geo g, const uint8_t* sums, uint64_t sum_mod, int nb, uint32_t* sink);
 template <int NV>
 __global__ void k_probe_host(const uint8_t* host, uint64_t bb, uint64_t n_blocks, uint32_t* sink);
 

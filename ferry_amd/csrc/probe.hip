@@ -160,6 +160,57 @@ __global__ __launch_bounds__(W * 64) void k_probe_ktab(Geo g, const uint8_t* __r
   if (lane == 0) sink[(size_t)blockIdx.x * W + wave] = x;
 }
 
+// The Quest selection's summary reads without the scores: one workgroup of
+// four wavefronts per (request, layer, kv head) set, blocks [0, nb) of it,
+// sixteen lanes per record, each lane the same bytes of the record's min and
+// max halves as k_select_topk's loads (16-bit: 16 B of each, fp8: 8 B, fp32:
+// 32 B), U passes of four records per wavefront in flight.
+template <int ES, int U>
+__global__ __launch_bounds__(256) void k_probe_sums(Geo g, const uint8_t* __restrict__ sums,
+                                                   uint64_t sum_mod, int nb,
+                                                   uint32_t* __restrict__ sink) {
+  constexpr int D = 128, W = 4, REC = 2 * D * ES, LB = 8 * ES;  // bytes per lane and half
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane >> 4, p = lane & 15;
+  const uint64_t set = blockIdx.x;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int b0 = 4 * wave; b0 < nb; b0 += 4 * W * U) {
+    u32x4 lo[U][LB / 16 > 0 ? LB / 16 : 1], hi[U][LB / 16 > 0 ? LB / 16 : 1];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int b = b0 + 4 * W * u + grp;
+      const uint64_t rec = host_index(set, b < nb ? (uint32_t)b : 0u, (uint64_t)g.max_blocks, sum_mod);
+      const uint8_t* r = sums + rec * REC;
+      if constexpr (LB == 8) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 a = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(r + LB * p));
+        const u32x2 c = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(r + D * ES + LB * p));
+        lo[u][0] = u32x4{a[0], a[1], 0u, 0u};
+        hi[u][0] = u32x4{c[0], c[1], 0u, 0u};
+      } else {
+#pragma unroll
+        for (int i = 0; i < LB / 16; ++i) {
+          lo[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(r + LB * p) + i);
+          hi[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(r + D * ES + LB * p) + i);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < (LB / 16 > 0 ? LB / 16 : 1); ++i) acc ^= lo[u][i] ^ hi[u][i];
+  }
+  uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off);
+  if (lane == 0) sink[(size_t)blockIdx.x * W + wave] = x;
+}
+
+template __global__ void k_probe_sums<1, 2>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
+template __global__ void k_probe_sums<1, 4>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
+template __global__ void k_probe_sums<2, 2>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
+template __global__ void k_probe_sums<2, 4>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
+template __global__ void k_probe_sums<4, 2>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
+template __global__ void k_probe_sums<4, 4>(Geo, const uint8_t*, uint64_t, int, uint32_t*);
 template __global__ void k_probe_ktab<2, kMassUnitWaves, kMassUnitInflight, 1>(Geo, const uint8_t*,
                                                                               uint64_t, int, uint32_t*);
 template __global__ void k_probe_ktab<4, kMassUnitWaves, kMassUnitInflight, 1>(Geo, const uint8_t*,

@@ -1683,7 +1683,7 @@ int ferry_owner_import_member(ferry_ctx* ctx, uint32_t lane, const void* image, 
 int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, int iters,
                    uint64_t* bytes, float* ms, void* stream) {
   if (int rc = check_ctx(ctx)) return rc;
-  if (kind < FERRY_PROBE_HBM_GATHER || kind > FERRY_PROBE_KTAB_READ) return fail(FERRY_EINVAL, "bad kind");
+  if (kind < FERRY_PROBE_HBM_GATHER || kind > FERRY_PROBE_SUMS_READ) return fail(FERRY_EINVAL, "bad kind");
   if (n < 1 || iters < 1) return fail(FERRY_EINVAL, "n and iters must be positive");
   if (kind == FERRY_PROBE_HBM_GATHER && (check_buf(slots, "slots") || n > 0x7FFFFFFFull))
     return fail(FERRY_EINVAL, "gather needs a device slot table of at most 2^31 rows");
@@ -1693,6 +1693,8 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
     return fail(FERRY_EINVAL, "more blocks than the pool holds");
   if (kind == FERRY_PROBE_KTAB_READ && (!ctx->ktab || n > (uint64_t)ctx->g.max_blocks))
     return fail(FERRY_EINVAL, "the K-table probe needs ferry_ktiles_build and n <= max_blocks");
+  if (kind == FERRY_PROBE_SUMS_READ && (!ctx->sums || !ctx->sum_blocks || n > (uint64_t)ctx->g.max_blocks))
+    return fail(FERRY_EINVAL, "the summary probe needs ferry_summaries_build and n <= max_blocks");
   const Geo& g = ctx->g;
   HIPC(hipSetDevice(ctx->device));
   hipStream_t s = (hipStream_t)stream;
@@ -1710,8 +1712,15 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
     const int per_cu = std::max(1, mass_units_resident(ctx) / std::max(1, ctx->cus));
     kt_lds = (size_t)kGroupMaxLds / (size_t)per_cu / 256 * 256;
   }
+  // the summary probe: k_select_topk's grid (one workgroup per set) with its
+  // LDS, so as many of its workgroups share a CU
+  const uint64_t sum_grid = (uint64_t)g.n_req * g.L * g.Hkv;
+  const size_t sum_lds = ((size_t)(g.Hq / g.Hkv) * g.D + (size_t)g.max_blocks) * 4;
+  if (kind == FERRY_PROBE_SUMS_READ && sum_lds > 65536)
+    return fail(FERRY_EINVAL, "max_blocks exceeds the selection's 64 KiB of LDS");
   const size_t words = kind == FERRY_PROBE_HBM_GATHER ? (size_t)n
                        : kind == FERRY_PROBE_KTAB_READ ? (size_t)(kt_grid * kt_w)
+                       : kind == FERRY_PROBE_SUMS_READ ? (size_t)(sum_grid * 4)
                                                        : (size_t)host_waves;
   if (ctx->probe_sink_words < words) {
     if (ctx->probe_sink) HIPC(hipFree(ctx->probe_sink));
@@ -1725,6 +1734,8 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
                          : kind == FERRY_PROBE_HBM_COPY ? 2 * n * g.bb
                          : kind == FERRY_PROBE_KTAB_READ
                              ? (uint64_t)g.n_req * g.L * g.Hkv * n * (g.bb / 2)
+                         : kind == FERRY_PROBE_SUMS_READ
+                             ? sum_grid * n * (uint64_t)(2 * g.D * g.esize)
                              : n * g.bb;
   const uint64_t dst_bytes = n * g.bb;
   if ((kind == FERRY_PROBE_HOST_DMA || kind == FERRY_PROBE_HBM_COPY) && ctx->probe_dst_bytes < dst_bytes) {
@@ -1771,6 +1782,19 @@ int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, 
         hipLaunchKernelGGL((k_probe_ktab<4, kMassUnitWaves, kMassUnitInflight, 1>), grid,
                            dim3(64 * kMassUnitWaves), kt_lds, s, g, ctx->ktab, ctx->kt_records, nb,
                            ctx->probe_sink);
+      return hipGetLastError();
+    }
+    if (kind == FERRY_PROBE_SUMS_READ) {
+      const dim3 grid((unsigned)sum_grid), block(256);
+      const int nb = (int)n, es = g.esize;
+      const bool u2 = g.Hq / g.Hkv >= 8;  // k_select_topk's passes in flight
+      auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, block, sum_lds, s, g, ctx->sums, ctx->sum_blocks, nb,
+                           ctx->probe_sink);
+      };
+      if (es == 1) u2 ? go(k_probe_sums<1, 2>) : go(k_probe_sums<1, 4>);
+      else if (es == 2) u2 ? go(k_probe_sums<2, 2>) : go(k_probe_sums<2, 4>);
+      else u2 ? go(k_probe_sums<4, 2>) : go(k_probe_sums<4, 4>);
       return hipGetLastError();
     }
     if (kind == FERRY_PROBE_HBM_COPY) {

@@ -464,6 +464,11 @@ int ferry_owner_import_member(ferry_ctx* ctx, uint32_t lane, const void* image, 
  *                           ferry_ktiles_build: the records of blocks [0, n)
  *                           of every set, in its order and grid, no scores;
  *                           bytes = n_req*L*Hkv*n*(block_bytes/2)
+ *   FERRY_PROBE_SUMS_READ   the Quest selection's reads of the summary table
+ *                           built by ferry_summaries_build: the records of
+ *                           blocks [0, n) of every set, in its lane pattern,
+ *                           grid and LDS, no scores; bytes =
+ *                           n_req*L*Hkv*n*2*128*element_size
  * `bytes` gets the bytes moved per launch, `ms` the mean launch time.  The
  * reference sweeps its host-staged channel the same way
  * (probe_host_staged_bandwidth, src/topo/topo.cpp:68-129). */
@@ -472,6 +477,7 @@ int ferry_owner_import_member(ferry_ctx* ctx, uint32_t lane, const void* image, 
 #define FERRY_PROBE_HOST_DMA 2
 #define FERRY_PROBE_HBM_COPY 3
 #define FERRY_PROBE_KTAB_READ 4
+#define FERRY_PROBE_SUMS_READ 5
 int ferry_bw_probe(ferry_ctx* ctx, int kind, const uint32_t* slots, uint64_t n, int iters,
                    uint64_t* bytes, float* ms, void* stream);
 

@@ -150,6 +150,25 @@ def test_selection_errors():
     assert np.all(sel.cpu().numpy()[0] == -1)  # that row is left empty
 
 
+@pytest.mark.parametrize("dtype,Hkv,Hq", [(F.F16, 2, 4), (F.BF16, 1, 8), (F.FP8, 2, 8), (F.F32, 2, 2)])
+def test_summary_read_probe(dtype, Hkv, Hq):
+    # FERRY_PROBE_SUMS_READ reads the min/max record of n blocks of every set
+    # from the summary table in the Quest selection's pattern: its bytes, and
+    # its refusals
+    p = Pair(3, 2, Hkv, Hq, 8, 16, 96, dtype, host_blocks=257)
+    rec = 2 * 128 * {F.F32: 4, F.F16: 2, F.BF16: 2, F.FP8: 1}[dtype]
+    with pytest.raises(F.FerryError, match="summaries_build"):
+        p.ex.bw_probe(F.PROBE_SUMS_READ, 10)
+    p.ex.summaries_build()
+    b, ms, gbs = p.ex.bw_probe(F.PROBE_SUMS_READ, 96, iters=2)
+    assert b == 3 * 2 * Hkv * 96 * rec and ms > 0 and gbs > 0
+    b, _, _ = p.ex.bw_probe(F.PROBE_SUMS_READ, 37, iters=1)
+    assert b == 3 * 2 * Hkv * 37 * rec
+    with pytest.raises(F.FerryError, match="max_blocks"):
+        p.ex.bw_probe(F.PROBE_SUMS_READ, 97)
+    assert p.ex.stats()["device_error"] == 0
+
+
 def _topk_geometry(seed):
     rng = np.random.default_rng(3000 + seed)
     dtype = int(rng.choice([F.F32, F.F16, F.BF16, F.FP8]))
