@@ -150,6 +150,52 @@ def test_selection_errors():
     assert np.all(sel.cpu().numpy()[0] == -1)  # that row is left empty
 
 
+def _const_k_tile(dtype, c):
+    """Bytes of a 16 x 128 K tile whose every element is c (exact in dtype)."""
+    v = np.full((16, 128), c, np.float32)
+    if dtype == F.F16:
+        return v.astype(np.float16).view(np.uint8).ravel()
+    if dtype == F.BF16:
+        return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).ravel()
+    return v.view(np.uint8).ravel()
+
+
+@pytest.mark.parametrize("mode", [F.TOPK_PER_HEAD, F.TOPK_LAYER_MAX])
+@pytest.mark.parametrize("k", [8, 9, 63])
+@pytest.mark.parametrize("dtype", [F.F16, F.BF16, F.F32])
+def test_select_topk_known_answer(dtype, k, mode):
+    """Crafted blocks with a known selection: every K element of block b is
+    c_b and q is all ones, so block b's bound is 128 c_b exactly.  Eight blocks
+    of each row carry c = 4^j (j = 0..7), the other 56 carry 0.  With k = 8
+    the k-th key is alone in its top-byte bin, so the radix search ends at its
+    first pass; with k = 9 and 63 the k-th key is one of the 56 equal zeros
+    and the ties go to the lower block ids."""
+    mb, hb = 64, 128
+    big = {0: [3, 10, 17, 24, 31, 38, 45, 52], 1: [60, 50, 40, 30, 20, 10, 5, 0]}
+    ex = F.Executor(2, 1, 1, k, 16, mb, q_heads=1, dtype=dtype, host_blocks=hb)
+    ex.hosttier_fill()
+    torch.cuda.synchronize()  # the fill has landed before the K tiles are rewritten
+    host, _ = ex.hosttier_array()
+    bb = ex.block_bytes
+    kt = 16 * 128 * {F.F16: 2, F.BF16: 2, F.F32: 4}[dtype]
+    for r in (0, 1):
+        for b in range(mb):
+            c = 4.0 ** big[r].index(b) if b in big[r] else 0.0
+            h = r * mb + b  # block (set r, b) reads host block r * max_blocks + b
+            host[h * bb:h * bb + kt] = _const_k_tile(dtype, c)
+    ex.summaries_build()
+    q = torch.ones((2, 1, 1, 128), device="cuda")
+    sel = torch.empty((2, 1, 1, k), dtype=torch.int32, device="cuda")
+    ex.select_topk(q, torch.tensor([mb, mb], dtype=torch.int32, device="cuda"), sel, mode=mode)
+    torch.cuda.synchronize()
+    got = sel.cpu().numpy().reshape(2, k)
+    for r in (0, 1):
+        zeros = [b for b in range(mb) if b not in big[r]]
+        want = sorted(big[r] + zeros[:k - 8])
+        assert got[r].tolist() == want, (r, got[r].tolist(), want)
+    assert ex.stats()["device_error"] == 0
+
+
 @pytest.mark.parametrize("dtype,Hkv,Hq", [(F.F16, 2, 4), (F.BF16, 1, 8), (F.FP8, 2, 8), (F.F32, 2, 2)])
 def test_summary_read_probe(dtype, Hkv, Hq):
     # FERRY_PROBE_SUMS_READ reads the min/max record of n blocks of every set
