@@ -1330,9 +1330,10 @@ int mass_units_resident(ferry_ctx* ctx) {
 #undef FERRY_MASS_FN
   int per_cu = 0;
   const size_t lds = mass_lds_bytes(ctx);
-  if (lds > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMassLdsWs);
-  if (hipSetDevice(ctx->device) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * kMassUnitWaves, lds) != hipSuccess ||
+  const bool on_dev = hipSetDevice(ctx->device) == hipSuccess;
+  if (on_dev && lds > 65536)
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMassLdsWs);
+  if (!on_dev || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * kMassUnitWaves, lds) != hipSuccess ||
       per_cu < 1) {
     (void)hipGetLastError();
     per_cu = 1;  // still correct: the workgroups take the units from the counter
