@@ -11,7 +11,11 @@
 //    published cell of lap i, so a consumer could read the older task;
 //  * kWaveBatched reserves one ticket per active lane of the 64-wide
 //    wavefront with a single CAS by the first active lane (the reference
-//    reserves a fixed 32 per warp) and broadcasts with readfirstlane;
+//    reserves a fixed 32 per warp) and broadcasts with readfirstlane; a ring
+//    with fewer cells than active lanes takes them one per lane;
+//  * a lane publishes (and a consumer takes its task) as soon as its own cell
+//    is ready, inside the wait: lanes of one wavefront may hold tickets a lap
+//    apart, and a lane that waited for its siblings could stall them all;
 //  * dq_pop reserves for the wavefront in the same way, in both modes: the
 //    first active lane takes up to one ticket per active lane (fewer when
 //    fewer are queued) with one CAS on head.  A per-lane CAS loop, as in the
@@ -74,30 +78,42 @@ __device__ inline bool q_reserve(DeviceQueue* q, uint64_t n, uint64_t* base) {
   return false;
 }
 
+// Publish every active lane's task once its cell has been released for its
+// ticket.  A lane publishes inside the wait, as soon as its own cell is ready:
+// lanes of one wavefront can hold tickets a lap apart (per-thread reservation
+// under more producers than cells), and the later one's cell is released only
+// after the earlier one's task is consumed, so a lane that waited for its
+// siblings before publishing would stall the wavefront for good.
 __device__ inline bool q_publish(DeviceQueue* q, uint64_t ticket, uint64_t task) {
   const uint64_t cell = ticket % q->capacity;
-  for (long spin = 0; q_load(q->seq + cell) != ticket; ++spin) {
+  bool done = false;
+  for (long spin = 0;; ++spin) {
+    if (!done && q_load(q->seq + cell) == ticket) {
+      q->slots[cell] = task;
+      q_store(q->seq + cell, ticket + 1);
+      done = true;
+    }
+    if (!__ballot(!done)) return true;
     if (spin >= kQueueSpinLimit) {
-      q_fail(q);
-      return false;
+      if (!done) q_fail(q);
+      return done;
     }
     __builtin_amdgcn_s_sleep(2);
   }
-  q->slots[cell] = task;
-  q_store(q->seq + cell, ticket + 1);
-  return true;
 }
 
 // Push one task.  true on success, false when the ring is full (backpressure
 // is the caller's decision) or a bounded wait ran out (status set).
 __device__ inline bool dq_push(DeviceQueue* q, uint64_t task, ReservationMode mode) {
-  if (mode == ReservationMode::kPerThread) {
+  const uint64_t active = __ballot(true);
+  const int n = __builtin_popcountll(active);
+  // a ring with fewer cells than the wavefront's active lanes could never
+  // hold the batch: its lanes reserve one ticket each instead
+  if (mode == ReservationMode::kPerThread || (uint64_t)n > q->capacity) {
     uint64_t t;
     if (!q_reserve(q, 1, &t)) return false;
     return q_publish(q, t, task);
   }
-  const uint64_t active = __ballot(true);
-  const int n = __builtin_popcountll(active);
   const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(active >> 32),
                                               __builtin_amdgcn_mbcnt_lo((uint32_t)active, 0));
   uint64_t base = 0;
@@ -147,16 +163,22 @@ __device__ inline bool dq_pop(DeviceQueue* q, uint64_t* out) {
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32));
   const uint64_t h = (((uint64_t)hi << 32) | lo) + (uint64_t)below;
   const uint64_t cell = h % q->capacity;
-  for (long spin = 0; q_load(q->seq + cell) != h + 1; ++spin) {  // reserved, not yet published
+  // a taken ticket may be reserved and not yet published: each lane consumes
+  // (and releases its cell) as soon as its own task is there, as q_publish does
+  bool done = false;
+  for (long spin = 0;; ++spin) {
+    if (!done && q_load(q->seq + cell) == h + 1) {
+      *out = q->slots[cell];
+      q_store(q->seq + cell, h + q->capacity);
+      done = true;
+    }
+    if (!__ballot(!done)) return true;
     if (spin >= kQueueSpinLimit) {
-      q_fail(q);
-      return false;
+      if (!done) q_fail(q);
+      return done;
     }
     __builtin_amdgcn_s_sleep(2);
   }
-  *out = q->slots[cell];
-  q_store(q->seq + cell, h + q->capacity);
-  return true;
 }
 #endif
 

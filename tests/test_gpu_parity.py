@@ -196,9 +196,7 @@ def test_serial_mode_reproduces_reference_golden():
 
 @pytest.mark.parametrize("mode", [0, 1])
 def test_queue_exactly_once(mode):
-    # The ring (65,536 cells) is larger than the producer count on purpose:
-    # per-thread reservation (mode 0) has no progress guarantee when more
-    # producers race than there are cells (a lane may lose every freed cell).
+    # a large ring (65,536 cells): throughput of both reservation modes
     popped, dups, ms = F.queue_selftest(capacity=1 << 16, n_tasks=1 << 20, producers=512,
                                         consumers=512, mode=mode)
     assert popped == 1 << 20 and dups == 0
@@ -208,13 +206,27 @@ def test_queue_exactly_once(mode):
 def test_queue_small_ring_partial_pops(mode):
     # 1000 cells (not a multiple of 64) under 256 producers and 1024 consumers:
     # the consumers outnumber what is queued, so wavefront pops often get fewer
-    # tickets than lanes asked, and every cell wraps 65 times.  The ring is
-    # larger than the producer count on purpose: with fewer cells than
-    # producers, per-thread reservation has no progress guarantee (a lane can
-    # lose the race for a freed cell past the harness's retry bound).
+    # tickets than lanes asked, and every cell wraps 65 times.
     popped, dups, ms = F.queue_selftest(capacity=1000, n_tasks=1 << 16, producers=256,
                                         consumers=1024, mode=mode)
     assert popped == 1 << 16 and dups == 0
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_queue_more_producers_than_cells(mode):
+    # 64 cells under 2048 producers and 512 consumers.  Per-thread
+    # reservation (mode 0) can hand lanes of one wavefront tickets a lap or
+    # more apart: the later lane's cell is released only after the earlier
+    # lane's task is consumed, so each lane must publish as soon as its own
+    # cell is free rather than after its siblings' waits.
+    popped, dups, ms = F.queue_selftest(capacity=64, n_tasks=1 << 16, producers=2048,
+                                        consumers=512, mode=mode)
+    assert popped == 1 << 16 and dups == 0
+    # fewer cells than a wavefront's lanes: a wave-batched push takes a ticket
+    # per lane instead of one batch the ring could never hold
+    popped, dups, ms = F.queue_selftest(capacity=16, n_tasks=1 << 14, producers=4096,
+                                        consumers=256, mode=mode)
+    assert popped == 1 << 14 and dups == 0
 
 
 @pytest.mark.parametrize("kind", [0, 1, 2])
