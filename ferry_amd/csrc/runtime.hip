@@ -343,11 +343,14 @@ void launch_mfma(const AttnPlan& p, const dim3& grid, hipStream_t s, const AttnA
 }
 template <int DT, int G, int NT, int W>
 void launch_group_w(const dim3& grid, size_t lds, hipStream_t s, const AttnArgs& a) {
-  // more than the default 64 KiB of dynamic LDS: allowed once per instance
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_attn_group<DT, G, NT, W>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, kGroupMaxLds);
-  (void)attr;
+  // more than the default 64 KiB of dynamic LDS: allowed once per instance and
+  // device (the caller has made the context's device current)
+  static std::atomic<uint64_t> allowed{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !((allowed.load() >> dev) & 1u) &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_group<DT, G, NT, W>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kGroupMaxLds) == hipSuccess)
+    allowed.fetch_or(1ull << dev);
   hipLaunchKernelGGL((k_attn_group<DT, G, NT, W>), grid, dim3(W * 64), lds, s, a.g, a.q, a.slots,
                      a.pool, a.pool_scales, a.out, a.qscale, a.l0, a.nl, a.err, a.attn_blocks);
 }
