@@ -353,6 +353,61 @@ def cpu_baseline_threads(g, host_bytes, host_scales, plan, q, toks, what):
             "ms_per_step": round(wall / steps * 1e3, 1)}
 
 
+def cpu_full_groups(w, max_blocks, host_bytes, host_scales, host_blocks, ctx, steps, reuse_r):
+    """The oracle's C step over the whole batch of a prefix-group workload:
+    every group of w["group"] requests in an executor of its own (a group's
+    sets, LRU state, misses and bytes depend on its members' selections only,
+    so the groups are independent), the groups spread over the usable host
+    cores (at most 16), all stepping the same steps + 1 steps of the full
+    batch's selections; step 0 (the cold fill) is untimed."""
+    import threading
+    from oracle import pyoracle as O
+
+    dt = {"f16": O.F16, "bf16": O.BF16, "fp8": O.FP8, "f32": O.F32}[w["dtype"]]
+    B, grp, L, H = w["B"], w["group"], w["L"], w["Hkv"]
+    n_groups = B // grp
+    sg = O.selgen(B, L, H, w["k"], ctx[:B], dist=1, zipf_s=w["zipf"], reuse=w["reuse"],
+                  group=grp, prefix_blocks=w["prefix"], seed=3, reuse_r=reuse_r)
+    sels = [O.selgen_step(sg, t).reshape(B, -1) for t in range(steps + 1)]
+    g = O.make_geom(n_req=grp, group=grp, n_layers=L, kv_heads=H, q_heads=w["Hq"], k=w["k"],
+                    cap=w["C"], max_blocks=max_blocks, dtype=dt, host_blocks=host_blocks, seed=7,
+                    value_std=0.5)
+    q = np.random.default_rng(1).standard_normal((grp, L, w["Hq"], 128)).astype(np.float32)
+    runs = [_CpuRun(g, host_bytes, host_scales, q) for _ in range(n_groups)]
+    plans = [[np.ascontiguousarray(sels[t][j * grp:(j + 1) * grp]).reshape(-1)
+              for t in range(steps + 1)] for j in range(n_groups)]
+    T = max(1, min(16, n_groups, len(os.sched_getaffinity(0))))
+    mine = [list(range(i, n_groups, T)) for i in range(T)]
+    start = threading.Barrier(T + 1)
+    done = threading.Barrier(T + 1)
+
+    def worker(js):
+        for j in js:
+            runs[j].step(plans[j][0])  # cold fill, untimed
+        start.wait()
+        for t in range(1, steps + 1):
+            for j in js:
+                runs[j].step(plans[j][t])
+        done.wait()
+
+    th = [threading.Thread(target=worker, args=(js,)) for js in mine]
+    for t in th:
+        t.start()
+    start.wait()
+    t0 = time.perf_counter()
+    done.wait()
+    wall = time.perf_counter() - t0
+    for t in th:
+        t.join()
+    if any(r.rc for r in runs):
+        raise RuntimeError("ora_cpu_step failed in a worker thread")
+    return {"value": round(B * steps / wall, 3), "unit": "tok/s", "cores": T, "kind": "port",
+            "sample": f"the whole batch: {B} requests ({n_groups} groups of {grp}) x {L} layers x "
+                      f"{H} kv heads, {steps} steps after one untimed one, each group in an "
+                      f"executor of its own, {T} threads; {wall / steps * 1e3:.0f} ms per step",
+            "ms_per_step": round(wall / steps * 1e3, 1)}
+
+
 PREROLL_WINDOW = 5      # steps per window of the settling test
 PREROLL_MIN = 20        # at least this many untimed steps from the cold pool
 PREROLL_MAX = 200       # and at most this many
@@ -672,6 +727,9 @@ def run(a, w, F, torch, steal=None, workers=None, zipf=None, assign=None, want_c
         plan = cpu_plan(w, ctx, n_req, cpu_steps or a.cpu_steps, reuse_r)
         res["cpu_baseline"] = cpu_baseline(w, sg.max_blocks, host, hsc, a.host_blocks, n_req,
                                            plan, "steps")
+        if w["group"] > 1:  # prefix groups: the whole batch, a group per thread
+            res["cpu_baseline"]["in_full"] = cpu_full_groups(
+                w, sg.max_blocks, host, hsc, a.host_blocks, ctx, cpu_steps or a.cpu_steps, reuse_r)
     ex.close()
     return res
 

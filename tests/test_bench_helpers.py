@@ -83,3 +83,25 @@ def test_cpu_baseline_leg_on_a_small_workload():
     res = bench.cpu_baseline(SMALL, 64, host, None, 257, 2,
                              [plan[0], (idle.reshape(-1), (0,)), plan[2]], "ticks")
     assert res["value"] > 0
+
+
+def test_cpu_full_groups_runs_the_whole_batch():
+    # a prefix-group workload of 3 groups: every group in an executor of its
+    # own; its first group's selections are the sampled leg's (draws are keyed
+    # per request), and the whole batch's tokens per step are all requests'
+    w = dict(B=48, L=2, Hq=8, Hkv=2, k=8, ctx=(4, 32), C=256, dtype="fp8", zipf=1.1,
+             reuse=0.66, group=16, prefix=16)
+    ctx = O.ctx_uniform(2, w["B"], *w["ctx"]) + w["prefix"]
+    sg = O.selgen(w["B"], w["L"], w["Hkv"], w["k"], ctx, dist=1, zipf_s=w["zipf"],
+                  reuse=w["reuse"], group=w["group"], prefix_blocks=w["prefix"], seed=3)
+    mb = O.selgen_max_blocks(sg)
+    full0 = O.selgen_step(sg, 0).reshape(w["B"], -1)
+    plan = bench.cpu_plan(w, ctx, w["group"], 2, None)
+    assert np.array_equal(plan[0][0], full0[:w["group"]].reshape(-1))
+    g = O.make_geom(n_req=1, n_layers=1, kv_heads=1, k=1, cap=1, max_blocks=1, dtype=O.FP8,
+                    host_blocks=4099)
+    host, hsc = O.host_fill(g)
+    res = bench.cpu_full_groups(w, mb, host, hsc, 4099, ctx, 2, None)
+    assert res["kind"] == "port" and res["unit"] == "tok/s" and res["value"] > 0
+    assert 1 <= res["cores"] <= 3 and res["ms_per_step"] > 0
+    assert "48 requests (3 groups of 16)" in res["sample"]
