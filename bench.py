@@ -1191,7 +1191,7 @@ def main():
         print(pmc_summary(a.pmc_summary, a.last))
         return
     if a.gpus != 1:
-        print(f"bench.py runs on exactly one GPU (this build has no multi-GPU path); "
+        print(f"bench.py runs on exactly one GPU (the executor has no multi-GPU path); "
               f"got --gpus {a.gpus}", file=sys.stderr)
         sys.exit(2)
     import torch

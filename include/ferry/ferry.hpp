@@ -113,7 +113,7 @@ struct WlAStats {
   int status = FERRY_OK;
 };
 
-// Host-tier and pool offsets of (request, layer, block) in this build's
+// Host-tier and pool offsets of (request, layer, block) in this library's
 // layout (one set per (request, layer), one pool slot per block).
 inline size_t slab_offset(const MissSpec& sp, int req, int layer, uint64_t block) {
   const uint64_t max_blocks = 64 + (uint64_t)sp.steps * 8;
@@ -285,7 +285,7 @@ inline MissTrace replay_miss_stream(const MissSpec& spec, int device = 0) {
 // memory visible to the device).  mode 0 (A): no reuse, every distinct
 // selection of a step is fetched; modes 1 (B) and 2 (C): per-selection LRU of
 // hot_blocks slots, one fetch launch per step (B's per-miss submits modelled
-// the host-staged channel, which this build does not have).  Each step then
+// the host-staged channel, which this library does not have).  Each step then
 // runs sparse attention over the selected blocks.  The refill counters are
 // the reference's (src/workloads/kv_exec.cuh:108-145, 148-185, 188-292): A
 // counts every selected block, B every miss, C the submits of each

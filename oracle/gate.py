@@ -2,7 +2,7 @@
 owners from the same cold start and every step is compared with the GPU's.
 
 TEST INFRASTRUCTURE ONLY: used by tests/ and by the cpu_baseline leg of
-bench.py, as the checker.  The product never imports it.
+bench.py, to check the GPU against.  The product never imports it.
 
 Sets belong to one owner (a request, or a prefix group of `group` requests)
 and selection draws are keyed per request, so owners [0, n) of a batch of B

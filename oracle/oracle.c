@@ -1,7 +1,7 @@
 /*
  * oracle.c -- CPU restatement of the per-GPU sparse KV miss-stream executor.
  *
- * TEST INFRASTRUCTURE ONLY (the checker).  Loaded by tests/, by
+ * TEST INFRASTRUCTURE ONLY (what the GPU is checked against).  Loaded by tests/, by
  * __graft_entry__.smoke() and by the cpu_baseline leg of bench.py; never by
  * the product.  See oracle.h for the map of functions to reference files.
  * Paths in citations are relative to the clearleo126/ferry source tree.

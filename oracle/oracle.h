@@ -1,7 +1,7 @@
 /*
  * oracle.h -- CPU restatement of the per-GPU sparse KV miss-stream executor.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/,
+ * TEST INFRASTRUCTURE ONLY.  The GPU is checked against this library: only tests/,
  * __graft_entry__.smoke() and the cpu_baseline leg of bench.py may load it.
  * The product (ferry_amd/) never links, loads or calls it.
  *

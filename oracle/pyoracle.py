@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (oracle/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and
-by the cpu_baseline leg of bench.py, as the checker.  The product never
+by the cpu_baseline leg of bench.py, to check the GPU against.  The product never
 imports it.
 """
 import ctypes as C
