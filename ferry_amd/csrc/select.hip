@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256) void k_summaries_tile(uint8_t* __restrict__ su
 
 // The kk largest of keys[0, n) (n > kk), ids written in ascending order to
 // `nrows` output rows `row_stride` apart, ties to the lower ids.  Phase 1 finds
-// the kk-th largest key by 4 radix passes of 8 bits over LDS histograms (a
+// the kk-th largest key by up to 4 radix passes of 8 bits over LDS histograms (a
 // wavefront-wide suffix scan over the bins).  Scores of one row mostly share
 // their top byte, so each 64-key step counts its first key's bin with one
 // atomic for every lane in it (ballot) and only the other lanes add their own:
@@ -345,9 +345,10 @@ __device__ void topk_ascending(const uint32_t* keys, int n, int kk, uint32_t* hi
 
 // One workgroup (W wavefronts) per (request, layer, kv head) row, or per
 // (request, layer) with LAYER.  Phase 1 scores every block of the request's
-// context into LDS keys (16 lanes per block, 4 blocks per wavefront pass);
-// phase 2 finds the k-th largest key by 4 radix passes of 8 bits; phase 3
-// writes the selected block ids in ascending order (ties to lower ids).
+// context into LDS keys (16 lanes per block, 4 blocks per wavefront pass),
+// counting their top bytes as the first radix pass; phase 2 finds the k-th
+// largest key by at most 4 radix passes of 8 bits; phase 3 writes the
+// selected block ids in ascending order (ties to lower ids).
 // Dynamic LDS: q[Gq][128] floats, then keys[max_n].
 template <int DT, int G, bool LAYER, int W>
 __global__ __launch_bounds__(W * 64) void k_select_topk(Geo g, const float* __restrict__ q,
