@@ -12,13 +12,26 @@
 
 namespace {
 
-void print_wla(const char* name, const ferry::WlAStats& st) {
+void print_wla(const char* name, const ferry::WlAStats& st, float gpu_ms) {
   std::printf("  %-10s makespan=%9.2fms steps/s=%8.1f p50=%7.3f p99=%8.3f refill=%8llu bytes=%9.2fMB status=%d "
-              "fetched=%llu\n",
+              "fetched=%llu gpu=%.2fms\n",
               name, st.makespan_ms, st.throughput_steps, st.p50_step_ms, st.p99_step_ms,
               (unsigned long long)st.refill_events, st.refill_bytes / 1048576.0, st.status,
-              (unsigned long long)st.fetched_blocks);
+              (unsigned long long)st.fetched_blocks, gpu_ms);
   std::fflush(stdout);
+}
+
+// One mode's run, its interval also taken on the GPU's clock (events on the
+// default stream around it).
+ferry::WlAStats run_mode(const char* name, const ferry::MissSpec& sp, const ferry::MissTrace& tr, int mode,
+                         const ferry::AdaptiveBatchPolicy& pol) {
+  ferry::HipTimer gt;
+  gt.tick();
+  const ferry::WlAStats st = ferry::run_miss_workload(0, 0, sp, tr, mode, pol);
+  gt.toc();
+  FERRY_HIP_CHECK(hipEventSynchronize(gt.end));
+  print_wla(name, st, gt.elapsed_ms());
+  return st;
 }
 
 int run_scenario(const ferry::MissSpec& sp, const ferry::AdaptiveBatchPolicy& pol) {
@@ -36,12 +49,9 @@ int run_scenario(const ferry::MissSpec& sp, const ferry::AdaptiveBatchPolicy& po
               (unsigned long long)tr.total_selects, (unsigned long long)tr.total_misses, tr.hit_rate,
               tr.miss_bytes / 1048576.0, b_per_token);
   std::fflush(stdout);
-  const ferry::WlAStats a = ferry::run_miss_workload(0, 0, sp, tr, 0, pol);
-  print_wla("baseline-A", a);
-  const ferry::WlAStats b = ferry::run_miss_workload(0, 0, sp, tr, 1, pol);
-  print_wla("baseline-B", b);
-  const ferry::WlAStats c = ferry::run_miss_workload(0, 0, sp, tr, 2, pol);
-  print_wla("ferry-C", c);
+  const ferry::WlAStats a = run_mode("baseline-A", sp, tr, 0, pol);
+  const ferry::WlAStats b = run_mode("baseline-B", sp, tr, 1, pol);
+  const ferry::WlAStats c = run_mode("ferry-C", sp, tr, 2, pol);
   if (a.status || b.status || c.status) return 1;
   const double refill_ratio = b.refill_events ? (double)c.refill_events / (double)b.refill_events : 1.0;
   std::printf("  => C/A %.2fx  C/B %.2fx  refill C/B %.3f\n\n", a.makespan_ms / c.makespan_ms,

@@ -47,6 +47,7 @@
 #include <vector>
 
 #include "../ferry_amd.h"
+#include "common.hpp"
 
 namespace ferry {
 
@@ -310,9 +311,9 @@ inline WlAStats run_miss_workload(int src_dev, int dst_dev, const MissSpec& sp, 
   std::vector<std::pair<int, uint64_t>> ml;
   std::vector<double> step_ms;
   uint64_t c_events = 0, c_bytes = 0;
-  const auto t0 = std::chrono::steady_clock::now();
+  HostTimer ht;  // the makespan and each step's interval, as the reference times them
   for (int s = 0; s < S; ++s) {
-    const auto ts = std::chrono::steady_clock::now();
+    const double ts = ht.toc_ms();
     for (int r = 0; r < R; ++r)
       for (int l = 0; l < L; ++l)
         for (int k = 0; k < G; ++k)
@@ -329,14 +330,14 @@ inline WlAStats run_miss_workload(int src_dev, int dst_dev, const MissSpec& sp, 
       st.status = FERRY_EHIP;
       return st;
     }
-    step_ms.push_back(std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - ts).count());
+    step_ms.push_back(ht.toc_ms() - ts);
     if (mode == 2)
       for (int r = 0; r < R; ++r) {
         if ((st.status = detail::owner_misses(ex, r, L, mc, ms, r == 0, &ml))) return st;
         c_events += detail::cmode_submits(ml, sp.c4_bytes(), pol, &c_bytes);
       }
   }
-  st.makespan_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  st.makespan_ms = ht.toc_ms();
   ferry_stats fs{};
   ferry_stats_get(ex.ctx, &fs);
   if (fs.device_error) st.status = fs.device_error;
@@ -636,8 +637,8 @@ inline WlaMultiStats run_wla_multigpu(const std::vector<int>& devices, MissSpec 
   std::vector<ferry_miss> ms((size_t)ex.n_sets * ex.max_sel);
   std::vector<std::pair<int, uint64_t>> ml;
   uint64_t a_events = 0, c_events = 0, c_bytes = 0;
-  const auto t0 = std::chrono::steady_clock::now();
-  auto elapsed = [&]() { return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count(); };
+  const HostTimer ht;
+  auto elapsed = [&]() { return ht.toc_ms(); };
   for (uint64_t t = 0;; ++t) {
     const double now = vtick > 0.0 ? (double)t * vtick : elapsed();
     int32_t na = 0, nr = 0, nres = 0, done = 0;

@@ -58,6 +58,12 @@ def test_driver_golden_default_stream():
     assert 79550 < rows["baseline-A"][3] <= 589824
     ratio = re.search(r"refill C/B ([\d.]+)", out).group(1)
     assert ratio == f"{c_runs / 79550:.3f}"
+    # each row's interval on the GPU's clock (ferry::HipTimer around the run,
+    # which also creates and destroys its executor) covers its host makespan
+    spans = re.findall(r"makespan=\s*([\d.]+)ms.* gpu=([\d.]+)ms", out)
+    assert len(spans) == 3
+    for host_ms, gpu_ms in spans:
+        assert 0.0 < float(host_ms) <= float(gpu_ms) * 1.05 + 1.0
 
 
 @pytest.mark.gpu
