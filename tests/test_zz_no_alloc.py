@@ -37,10 +37,20 @@ def _both(ex, q, ctx, shape):
     return a.cpu().numpy(), b.cpu().numpy()
 
 
-@pytest.mark.parametrize("dtype,Hkv,Hq", [(F.BF16, 4, 16), (F.F32, 2, 4)])
-def test_noalloc_select_mass_equals_select_mass(dtype, Hkv, Hq):
+@pytest.mark.parametrize("dtype,Hkv,Hq,ws", [(F.BF16, 4, 16, ""), (F.F16, 2, 4, ""), (F.FP8, 2, 8, ""),
+                                             (F.BF16, 2, 8, "hbm"), (F.F32, 2, 4, "")])
+def test_noalloc_select_mass_equals_select_mass(dtype, Hkv, Hq, ws, monkeypatch):
+    # 16-bit K keeps the blocks' log-sums in LDS (or, with FERRY_MASS_WS=hbm,
+    # their max and sum in workspace slices, as fp8 K does); fp32 K runs the
+    # one-launch kernel with slices.  The context reads the variable when it
+    # first plans a mass selection.
+    if ws:
+        monkeypatch.setenv("FERRY_MASS_WS", ws)
+    else:
+        monkeypatch.delenv("FERRY_MASS_WS", raising=False)
     B, L, k, mb = 6, 3, 32, 2000
-    print(f"[noalloc] dtype={dtype} B={B} L={L} Hkv={Hkv} Hq={Hq} k={k} max_blocks={mb}", flush=True)
+    print(f"[noalloc] dtype={dtype} B={B} L={L} Hkv={Hkv} Hq={Hq} k={k} max_blocks={mb} ws={ws or 'default'}",
+          flush=True)
     ex = _exec(B, L, Hkv, Hq, k, mb, dtype)
     rng = np.random.default_rng(dtype)
     shape = (B, L, Hkv, k)
